@@ -1,0 +1,406 @@
+/*
+ * cache.c -- the per-layer expert-id -> slot state machine, restated.
+ * TEST INFRASTRUCTURE ONLY (see oracle.h).
+ *
+ * Follows llama-moecache.cpp as patched by 0006, 0007 and 0008 (file:line are
+ * inside those .patch files):
+ *   observe   0006:295-400, 0007:247-321 (heat, miss window), 0008:504-518 (route trace)
+ *   issue     0006:241-293, 0007:230-246 (early path)
+ *   step      0006:765-953, 0007:655-771, 0008:607-660 (deterministic publication)
+ *   admission 0007:398-429 (lru_resident, admit_ok)
+ *   tables    0007:327-396 (set_table_entry, flush_tables)
+ *   map trace 0008:417-489
+ * The predictor/evictor, heat file, speculative probation and freeze are not
+ * restated (out of scope); slot_protect is kept at 0, which is what it is when
+ * no speculative upload exists.
+ *
+ * Upload completion: every job is published at the step after the one that
+ * scheduled (or, early path, issued) it.  With `deterministic` the order is
+ * (layer, slot), as LLAMA_MOE_DETERMINISTIC=1 sorts the done list
+ * (0008:613-627); without it the order is scheduling order, which is the order
+ * the single upload worker of a live run finishes them in (0006:654-723).  A
+ * live run differs from this only when a copy is still running at the next
+ * boundary; or_cache_hold_job() models that by holding one job back a step.
+ */
+#include "oracle.h"
+
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+#define U64MAX 0xffffffffffffffffull
+
+typedef struct {
+    int il, S, E;
+    int32_t *slot_expert, *expert_slot;
+    uint64_t *slot_last_use, *slot_protect;
+    uint8_t *slot_in_flight;
+    int32_t *free_slots;
+    int n_free;
+    int32_t *pending;
+    int n_pending;
+    float *heat;
+    uint64_t *miss_last, *miss_prev;
+    int32_t *tbl_mirror;
+    float *prior_mirror;
+    int tbl_dirty;
+    uint64_t n_hit, n_miss;
+} layer_t;
+
+typedef struct {
+    int li, expert, slot;
+    uint64_t sched_step;
+    int hold;
+} job_t;
+
+struct or_cache {
+    int n_layers, E;
+    or_knobs k;
+    layer_t *L;
+    uint64_t clock, n_steps, n_uploads, n_scheduled, n_published;
+    uint64_t n_admit_ok, n_admit_denied, n_table_flushes;
+    job_t *jobs;
+    int n_jobs, cap_jobs;
+    job_t *holds;
+    int n_holds;
+    FILE *route, *map;
+};
+
+static void push_job(or_cache *c, int li, int e, int slot) {
+    if (c->n_jobs == c->cap_jobs) {
+        c->cap_jobs = c->cap_jobs ? 2 * c->cap_jobs : 256;
+        c->jobs = (job_t *)realloc(c->jobs, sizeof(job_t) * (size_t)c->cap_jobs);
+    }
+    job_t j = {li, e, slot, c->n_steps, 0};
+    for (int h = 0; h < c->n_holds; ++h) {
+        const job_t *q = &c->holds[h];
+        if (q->li == li && q->expert == e && q->slot == slot && q->sched_step == c->n_steps) j.hold = 1;
+    }
+    c->jobs[c->n_jobs++] = j;
+}
+
+static void set_table_entry(or_cache *c, layer_t *ls, int expert, int v) {
+    ls->tbl_mirror[expert] = v;
+    if (ls->prior_mirror) ls->prior_mirror[expert] = v == ls->S ? 0.0f : c->k.cache_prior;
+    ls->tbl_dirty = 1;
+}
+
+static int32_t lru_resident(const layer_t *ls) {
+    int32_t victim = -1;
+    uint64_t best = U64MAX;
+    for (int s = 0; s < ls->S; ++s) {
+        if (ls->slot_in_flight[s] || ls->slot_expert[s] < 0) continue;
+        if (ls->slot_last_use[s] < best) {
+            best = ls->slot_last_use[s];
+            victim = ls->slot_expert[s];
+        }
+    }
+    return victim;
+}
+
+static int admit_ok(or_cache *c, const layer_t *ls, int id, int victim) {
+    if (c->k.admit_mode == 0 || victim < 0) return 1;
+    int ok = 1;
+    if (c->k.admit_mode == 1) {
+        ok = ls->heat[id] > ls->heat[victim] * 1.25f + c->k.admit_floor;
+    } else if (c->k.admit_mode == 2) {
+        ok = ls->miss_prev[id] != U64MAX &&
+             ls->miss_last[id] - ls->miss_prev[id] < (uint64_t)c->k.admit_window;
+    }
+    if (ok) c->n_admit_ok++; else c->n_admit_denied++;
+    return ok;
+}
+
+or_cache *or_cache_create(int n_layers, int n_experts, const int32_t *slots, const or_knobs *k) {
+    or_cache *c = (or_cache *)calloc(1, sizeof(or_cache));
+    c->n_layers = n_layers;
+    c->E = n_experts;
+    c->k = *k;
+    if (c->k.max_inserts <= 0) c->k.max_inserts = 2;
+    if (c->k.admit_window <= 0) c->k.admit_window = 8;
+    if (c->k.admit_half <= 0) c->k.admit_half = 64;
+    c->L = (layer_t *)calloc((size_t)n_layers, sizeof(layer_t));
+    for (int l = 0; l < n_layers; ++l) {
+        layer_t *ls = &c->L[l];
+        const int S = slots[l], E = n_experts;
+        ls->il = l;
+        ls->S = S;
+        ls->E = E;
+        ls->slot_expert = (int32_t *)malloc(sizeof(int32_t) * (size_t)S);
+        ls->expert_slot = (int32_t *)malloc(sizeof(int32_t) * (size_t)E);
+        ls->slot_last_use = (uint64_t *)calloc((size_t)S, sizeof(uint64_t));
+        ls->slot_protect = (uint64_t *)calloc((size_t)S, sizeof(uint64_t));
+        ls->slot_in_flight = (uint8_t *)calloc((size_t)S, 1);
+        ls->free_slots = (int32_t *)malloc(sizeof(int32_t) * (size_t)S);
+        ls->pending = (int32_t *)malloc(sizeof(int32_t) * (size_t)E);
+        ls->tbl_mirror = (int32_t *)malloc(sizeof(int32_t) * (size_t)E);
+        for (int s = 0; s < S; ++s) ls->slot_expert[s] = -1;
+        for (int e = 0; e < E; ++e) { ls->expert_slot[e] = -1; ls->tbl_mirror[e] = S; }
+        for (int s = 0; s < S; ++s) ls->free_slots[s] = S - 1 - s;   /* lowest slot on top */
+        ls->n_free = S;
+        if (c->k.cache_prior > 0.0f) ls->prior_mirror = (float *)calloc((size_t)E, sizeof(float));
+        if (c->k.admit_mode == 1) ls->heat = (float *)calloc((size_t)E, sizeof(float));
+        if (c->k.admit_mode == 2) {
+            ls->miss_last = (uint64_t *)malloc(sizeof(uint64_t) * (size_t)E);
+            ls->miss_prev = (uint64_t *)malloc(sizeof(uint64_t) * (size_t)E);
+            for (int e = 0; e < E; ++e) ls->miss_last[e] = ls->miss_prev[e] = U64MAX;
+        }
+    }
+    return c;
+}
+
+void or_cache_destroy(or_cache *c) {
+    if (!c) return;
+    for (int l = 0; l < c->n_layers; ++l) {
+        layer_t *ls = &c->L[l];
+        free(ls->slot_expert); free(ls->expert_slot); free(ls->slot_last_use);
+        free(ls->slot_protect); free(ls->slot_in_flight); free(ls->free_slots);
+        free(ls->pending); free(ls->tbl_mirror); free(ls->prior_mirror);
+        free(ls->heat); free(ls->miss_last); free(ls->miss_prev);
+    }
+    if (c->route) fclose(c->route);
+    if (c->map) fclose(c->map);
+    free(c->L);
+    free(c->jobs);
+    free(c->holds);
+    free(c);
+}
+
+static void map_frame(or_cache *c) {
+    if (!c->map) return;
+    fprintf(c->map, "step %llu\n", (unsigned long long)c->n_steps);
+    int32_t *pub = (int32_t *)malloc(sizeof(int32_t) * 1024);
+    for (int l = 0; l < c->n_layers; ++l) {
+        const layer_t *ls = &c->L[l];
+        or_cache_frame(c, l, pub);
+        fprintf(c->map, "map %d", ls->il);
+        for (int s = 0; s < ls->S; ++s) fprintf(c->map, " %d", pub[s]);
+        fputc('\n', c->map);
+    }
+    free(pub);
+    fflush(c->map);
+}
+
+int or_cache_trace_open(or_cache *c, const char *route_path, const char *map_path) {
+    if (route_path) {
+        c->route = fopen(route_path, "w");
+        if (!c->route) return -1;
+    }
+    if (map_path) {
+        c->map = fopen(map_path, "w");
+        if (!c->map) return -1;
+        fprintf(c->map, "moe-map 1 %d\n", c->n_layers);
+        for (int l = 0; l < c->n_layers; ++l)
+            fprintf(c->map, "layer %d %d %d\n", c->L[l].il, c->L[l].S, c->L[l].E);
+        map_frame(c);
+    }
+    return 0;
+}
+
+/* 0006:241-293: early issue out of pre-freed slots; caller-side admission */
+static int issue_uploads(or_cache *c, int li, const int32_t *ids, int n, int budget, int min_keep) {
+    layer_t *ls = &c->L[li];
+    int issued = 0;
+    for (int i = 0; i < n && issued < budget; ++i) {
+        const int id = ids[i];
+        if (id < 0 || id >= ls->E) continue;
+        if (ls->expert_slot[id] >= 0) continue;
+        if (ls->n_free <= min_keep) break;
+        int dup = 0;
+        for (int j = 0; j < c->n_jobs; ++j)
+            if (c->jobs[j].li == li && c->jobs[j].expert == id) { dup = 1; break; }
+        if (dup) continue;
+        const int slot = ls->free_slots[--ls->n_free];
+        ls->slot_in_flight[slot] = 1;
+        push_job(c, li, id, slot);
+        c->n_uploads++;
+        c->n_scheduled++;
+        issued++;
+    }
+    return issued;
+}
+
+void or_cache_observe(or_cache *c, int li, const int32_t *ids, int n_ids, int n_tok) {
+    layer_t *ls = &c->L[li];
+    if (c->route) {
+        fprintf(c->route, "route %llu %d %d %d", (unsigned long long)c->n_steps, ls->il, n_ids, n_tok);
+        for (int i = 0; i < n_ids * n_tok; ++i)
+            fprintf(c->route, " %d:%d", ids[i], (ids[i] >= 0 && ids[i] < ls->E) ? ls->expert_slot[ids[i]] : -1);
+        fputc('\n', c->route);
+    }
+    for (int t = 0; t < n_tok; ++t) {
+        for (int i = 0; i < n_ids; ++i) {
+            const int id = ids[t * n_ids + i];
+            if (id < 0 || id >= ls->E) continue;
+            if (ls->heat) ls->heat[id] += 1.0f;
+            const int slot = ls->expert_slot[id];
+            if (slot >= 0) {
+                ls->n_hit++;
+                ls->slot_last_use[slot] = ++c->clock;
+            } else {
+                ls->n_miss++;
+                if (ls->miss_last && ls->miss_last[id] != c->n_steps) {
+                    ls->miss_prev[id] = ls->miss_last[id];
+                    ls->miss_last[id] = c->n_steps;
+                }
+                int dup = 0;
+                for (int p = 0; p < ls->n_pending; ++p) if (ls->pending[p] == id) { dup = 1; break; }
+                if (!dup) ls->pending[ls->n_pending++] = id;
+            }
+        }
+    }
+    if (c->k.early_issue) {
+        const int pool_target = c->k.max_inserts;
+        const int next_victim = c->k.admit_mode == 0 ? -1 :
+            (ls->n_free > pool_target ? -1 : lru_resident(ls));
+        if (c->k.admit_mode == 0) {
+            issue_uploads(c, li, ls->pending, ls->n_pending, c->k.max_inserts, 0);
+        } else {
+            int32_t adm[1024];
+            int n = 0;
+            for (int p = 0; p < ls->n_pending; ++p) {
+                const int id = ls->pending[p];
+                if (ls->expert_slot[id] < 0 && admit_ok(c, ls, id, next_victim)) adm[n++] = id;
+            }
+            issue_uploads(c, li, adm, n, c->k.max_inserts, 0);
+        }
+    }
+}
+
+static int job_cmp(const void *a, const void *b) {
+    const job_t *x = (const job_t *)a, *y = (const job_t *)b;
+    if (x->li != y->li) return x->li < y->li ? -1 : 1;
+    return x->slot < y->slot ? -1 : x->slot > y->slot;
+}
+
+void or_cache_step(or_cache *c) {
+    /* 1) publish every job not held back (sorted when deterministic) */
+    job_t *done = (job_t *)malloc(sizeof(job_t) * (size_t)(c->n_jobs + 1));
+    int n_done = 0, n_keep = 0;
+    for (int j = 0; j < c->n_jobs; ++j) {
+        job_t jb = c->jobs[j];
+        if (jb.hold) { jb.hold = 0; c->jobs[n_keep++] = jb; }
+        else done[n_done++] = jb;
+    }
+    c->n_jobs = n_keep;
+    if (c->k.deterministic) qsort(done, (size_t)n_done, sizeof(job_t), job_cmp);
+    for (int j = 0; j < n_done; ++j) {
+        layer_t *ls = &c->L[done[j].li];
+        ls->slot_expert[done[j].slot] = done[j].expert;
+        ls->expert_slot[done[j].expert] = done[j].slot;
+        ls->slot_last_use[done[j].slot] = ++c->clock;
+        ls->slot_in_flight[done[j].slot] = 0;
+        set_table_entry(c, ls, done[j].expert, done[j].slot);
+        c->n_published++;
+    }
+    free(done);
+
+    c->n_steps++;
+
+    /* 2) per layer: schedule (non-early) or top the free pool up (early) */
+    for (int li = 0; li < c->n_layers; ++li) {
+        layer_t *ls = &c->L[li];
+        if (!c->k.early_issue) {
+            if (ls->n_pending == 0) continue;
+            int budget = c->k.max_inserts;
+            for (int p = ls->n_pending - 1; p >= 0 && budget > 0; --p) {
+                const int id = ls->pending[p];
+                if (ls->expert_slot[id] >= 0) { --budget; continue; }
+                int slot = -1;
+                uint64_t best = U64MAX;
+                for (int s = 0; s < ls->S; ++s) {
+                    if (ls->slot_in_flight[s]) continue;
+                    if (ls->slot_expert[s] < 0) { slot = s; break; }
+                    if (ls->slot_protect[s] >= c->n_steps) continue;
+                    if (ls->slot_last_use[s] < best) { best = ls->slot_last_use[s]; slot = s; }
+                }
+                if (slot < 0) break;
+                const int victim = ls->slot_expert[slot];
+                if (!admit_ok(c, ls, id, victim)) continue;
+                --budget;
+                if (victim >= 0) {
+                    ls->expert_slot[victim] = -1;
+                    ls->slot_expert[slot] = -1;
+                    set_table_entry(c, ls, victim, ls->S);
+                }
+                ls->slot_in_flight[slot] = 1;
+                push_job(c, li, id, slot);
+                c->n_scheduled++;
+            }
+            ls->n_pending = 0;
+            continue;
+        }
+        ls->n_pending = 0;
+        const int pool_target = c->k.max_inserts;
+        while (ls->n_free < pool_target) {
+            int slot = -1;
+            uint64_t best = U64MAX;
+            for (int s = 0; s < ls->S; ++s) {
+                if (ls->slot_in_flight[s] || ls->slot_expert[s] < 0) continue;
+                if (ls->slot_protect[s] >= c->n_steps) continue;
+                if (ls->slot_last_use[s] < best) { best = ls->slot_last_use[s]; slot = s; }
+            }
+            if (slot < 0) break;
+            const int victim = ls->slot_expert[slot];
+            ls->expert_slot[victim] = -1;
+            ls->slot_expert[slot] = -1;
+            set_table_entry(c, ls, victim, ls->S);
+            ls->free_slots[ls->n_free++] = slot;
+        }
+    }
+
+    /* 3) heat decay on a clock */
+    if (c->k.admit_mode == 1 && c->k.admit_half > 0 && c->n_steps % (uint64_t)c->k.admit_half == 0) {
+        for (int li = 0; li < c->n_layers; ++li)
+            for (int e = 0; e < c->E; ++e) c->L[li].heat[e] *= 0.5f;
+    }
+
+    /* 4) flush_tables: one batched write of every dirty layer */
+    if (c->k.batch_tables) {
+        int any = 0;
+        for (int li = 0; li < c->n_layers; ++li) {
+            if (c->L[li].tbl_dirty) { any = 1; c->L[li].tbl_dirty = 0; }
+        }
+        if (any) c->n_table_flushes++;
+    } else {
+        for (int li = 0; li < c->n_layers; ++li) c->L[li].tbl_dirty = 0;
+    }
+
+    map_frame(c);
+    if (c->route) fflush(c->route);
+}
+
+void or_cache_hold_job(or_cache *c, int layer, int expert, int slot, uint64_t sched_step) {
+    c->holds = (job_t *)realloc(c->holds, sizeof(job_t) * (size_t)(c->n_holds + 1));
+    job_t j = {layer, expert, slot, sched_step, 1};
+    c->holds[c->n_holds++] = j;
+}
+
+void or_cache_frame(const or_cache *c, int layer, int32_t *out) {
+    const layer_t *ls = &c->L[layer];
+    for (int s = 0; s < ls->S; ++s) out[s] = -1;
+    for (int e = 0; e < ls->E; ++e)
+        if (ls->expert_slot[e] >= 0) out[ls->expert_slot[e]] = e;
+}
+
+void or_cache_table(const or_cache *c, int layer, int32_t *tbl, float *prior) {
+    const layer_t *ls = &c->L[layer];
+    if (tbl) memcpy(tbl, ls->tbl_mirror, sizeof(int32_t) * (size_t)ls->E);
+    if (prior) {
+        if (ls->prior_mirror) memcpy(prior, ls->prior_mirror, sizeof(float) * (size_t)ls->E);
+        else memset(prior, 0, sizeof(float) * (size_t)ls->E);
+    }
+}
+
+void or_cache_stats(const or_cache *c, or_stats *s) {
+    memset(s, 0, sizeof *s);
+    s->n_steps = c->n_steps;
+    s->clock = c->clock;
+    for (int l = 0; l < c->n_layers; ++l) { s->n_hit += c->L[l].n_hit; s->n_miss += c->L[l].n_miss; }
+    s->n_uploads = c->n_uploads;
+    s->n_scheduled = c->n_scheduled;
+    s->n_published = c->n_published;
+    s->n_admit_ok = c->n_admit_ok;
+    s->n_admit_denied = c->n_admit_denied;
+    s->n_table_flushes = c->n_table_flushes;
+}

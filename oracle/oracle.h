@@ -1,0 +1,160 @@
+/*
+ * oracle.h -- CPU restatement of the MoE decode hot path.
+ *
+ * TEST INFRASTRUCTURE ONLY.  Nothing in the product links, loads or calls this
+ * code.  Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg
+ * use it, and only as the checker (or, for the CPU baseline, as the thing timed
+ * beside the GPU).
+ *
+ * What each part restates, and what pins it:
+ *
+ *   block codecs (Q4_K, Q6_K, Q8_K), quantize_q8k, dot_q4k_q8k, dot_q6k_q8k
+ *       ggml at llama.cpp bccbacd (not vendored in the reference; the reference
+ *       uses them through mul_mat_id, patches/0008-fused-cpu-moe-rows.patch:186-251
+ *       and experiments/x2_cpu_expert_cost.cpp:115-156).  Restated from ggml's
+ *       published block layouts.  Pinned by closed forms in tests/test_oracle_quants.py
+ *       (integer exactness vs fp64 dequant-then-dot, all-zero / d=0 / dmin=0 /
+ *       constant-code blocks, one-hot probes of every element position).
+ *   or_expf, or_route
+ *       build_moe_ffn's softmax -> (+ cache prior, patches/0007-...patch:109-124)
+ *       -> argsort top-k -> get_rows -> renormalise.  Upstream reduction order and
+ *       tie order are unpinned; this file fixes a canonical order (below) that the
+ *       GPU router follows bit for bit.  Pinned by brute force against fp64
+ *       softmax/sort on random and tie-heavy inputs, and by the reference's own
+ *       integer-valued top-k case (cpp/test-moe-sidecar.cpp:155-217: lower id
+ *       wins a tie).
+ *   or_expert_chain, or_moe_layer
+ *       ggml CPU expert chain: quantize x to Q8_K once, one integer vec_dot per
+ *       gate/up row, SwiGLU in fp32, quantize h to Q8_K, one vec_dot per down
+ *       row (experiments/x2_cpu_expert_cost.cpp:115-156), weighted combine in k
+ *       order (patches/0009-moe-sidecar.patch:697-703).  Pinned by fp64
+ *       dequantise-then-dot on the same quantized operands.
+ *   or_dispatch
+ *       ggml mul_mat_id row mapping (per-expert counts + rows in (token, k)
+ *       order, patches/0008-...patch:157-167 context).  Pinned by brute force.
+ *   or_cache_*
+ *       the slot-table state machine of patches 0006+0007+0008
+ *       (observe: 0006:295-400, 0007:247-321, 0008:504-518; step: 0006:765-953,
+ *       0007:655-771, 0008:607-660; admission 0007:398-429; tables 0007:327-396;
+ *       map/route traces 0008:417-518).  Pinned by replaying the routes of the
+ *       reference's engine-recorded traces
+ *       (artifacts/x3_logits_1791160431756057451/{0..3}.routes-record.txt) and
+ *       requiring every placement frame of {0..3}.map.txt.
+ *
+ * Canonical router order (shared with the GPU kernel):
+ *   logit[e]  = 64 lane partials p_j, p_j accumulated with fmaf over
+ *               i = 0..H/256-1, c = 0..3 of W[e][256 i + 4 j + c] * x[...],
+ *               then a butterfly p_j += p_{j^o} for o = 32,16,8,4,2,1.
+ *   (+ bias[e], one fp32 add, when a steering bias is given)
+ *   m         = max_e logit[e]
+ *   ex[e]     = or_expf(logit[e] - m)
+ *   s         = per 64-expert chunk a butterfly sum, chunks added in order.
+ *   p[e]      = ex[e] / s
+ *   sel[e]    = p[e] + prior[e]           (only when a prior table is given)
+ *   ids       = k largest sel, descending, lower id first on equal values
+ *   wsum      = p[ids[0]] + p[ids[1]] + ... (left to right)
+ *   w[k]      = p[ids[k]] / wsum
+ */
+#ifndef MOE_ORACLE_H
+#define MOE_ORACLE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define OR_QK 256
+#define OR_Q4K_BYTES 144
+#define OR_Q6K_BYTES 210
+#define OR_Q8K_BYTES 292
+
+enum { OR_TYPE_Q4K = 12, OR_TYPE_Q6K = 14 };  /* ggml type ids */
+
+/* ---- fp16 ------------------------------------------------------------- */
+float    or_h2f(uint16_t h);
+uint16_t or_f2h(float f);
+
+/* ---- block codecs ------------------------------------------------------ */
+void  or_dequant_q4k(const void *blocks, float *y, int64_t n);
+void  or_dequant_q6k(const void *blocks, float *y, int64_t n);
+void  or_quant_q8k(const float *x, void *blocks, int64_t n);
+void  or_dequant_q8k(const void *blocks, float *y, int64_t n);
+/* one row of n weights against one Q8_K-quantized vector of n values */
+float or_dot_q4k_q8k(int n, const void *w, const void *q8);
+float or_dot_q6k_q8k(int n, const void *w, const void *q8);
+/* fp64 reference of the same two products: dequantize both, dot in double */
+double or_dot_deq_f64(int wtype, int n, const void *w, const void *q8);
+
+/* ---- router ------------------------------------------------------------ */
+float or_expf(float x);
+/* W [E][H] row-major f32, x [H].  bias/prior/table may be NULL.
+ * Writes ids[K], w[K]; slots[K] = table[ids[k]] when table and slots given;
+ * probs[E] when given.  H % 256 == 0, E % 64 == 0, K <= E. */
+void or_route(int E, int H, int K, const float *W, const float *x, const float *bias,
+              const float *prior, const int32_t *table, int32_t *ids, float *w,
+              int32_t *slots, float *probs);
+/* softmax/top-k part only, from given logits (batched prefill input) */
+void or_route_logits(int E, int K, const float *logits, const float *prior,
+                     int32_t *ids, float *w, float *probs);
+
+/* ---- expert chain ------------------------------------------------------ */
+/* One expert at batch 1.  up/gate: Q4_K [I rows][H/256 blocks];
+ * down: Q4_K or Q6_K [H rows][I/256 blocks].  y[H]. h_out[I] optional. */
+void or_expert_chain(int H, int I, int down_type, const void *up, const void *gate,
+                     const void *down, const float *x, float *y, float *h_out);
+/* K experts + weighted combine: out[H] = sum_k w[k] * y_k (k in order).
+ * experts[k] points at that expert's contiguous [up | gate | down] bytes.
+ * n_threads > 1 parallelises rows with OpenMP (the CPU baseline). */
+void or_moe_layer(int H, int I, int down_type, int K, const void *const *experts,
+                  const float *w, const float *x, float *out, int n_threads);
+size_t or_expert_bytes(int H, int I, int down_type);
+
+/* ---- dispatch ---------------------------------------------------------- */
+/* ids [T][K].  counts[E], offsets[E+1] (exclusive scan), perm[T*K]:
+ * perm[offsets[e] + j] = t*K + k of the j-th pair routed to e, (t, k) order. */
+void or_dispatch(int T, int K, int E, const int32_t *ids, int32_t *counts,
+                 int32_t *offsets, int32_t *perm);
+
+/* ---- slot-table state machine ------------------------------------------ */
+typedef struct or_cache or_cache;
+
+typedef struct {
+    int32_t max_inserts;     /* default 2 */
+    int32_t admit_mode;      /* 0 off, 1 heat, 2 window */
+    int32_t admit_window;    /* default 8 */
+    int32_t admit_half;      /* default 64 */
+    float   admit_floor;     /* default 1.0 */
+    int32_t batch_tables;    /* 0/1 */
+    int32_t early_issue;     /* 0/1 */
+    float   cache_prior;     /* delta, 0 = off */
+    int32_t deterministic;   /* 1: publish in (layer, slot) order; 0: in scheduling order */
+} or_knobs;
+
+typedef struct {
+    uint64_t n_steps, clock, n_hit, n_miss, n_uploads, n_scheduled, n_published,
+             n_admit_ok, n_admit_denied, n_table_flushes;
+} or_stats;
+
+/* slots[l] = slot count of layer l (layer il = l). */
+or_cache *or_cache_create(int n_layers, int n_experts, const int32_t *slots, const or_knobs *k);
+void      or_cache_destroy(or_cache *c);
+/* open trace writers (either may be NULL); writes the map header and frame 0 */
+int       or_cache_trace_open(or_cache *c, const char *route_path, const char *map_path);
+/* ids token-major [n_tok][n_ids] */
+void      or_cache_observe(or_cache *c, int layer, const int32_t *ids, int n_ids, int n_tok);
+void      or_cache_step(or_cache *c);
+/* hold the job (layer, expert, slot) scheduled at step `sched_step` back for
+ * one extra step: models an upload still copying at a live-mode boundary */
+void      or_cache_hold_job(or_cache *c, int layer, int expert, int slot, uint64_t sched_step);
+/* published placement of a layer: out[slot] = expert or -1 */
+void      or_cache_frame(const or_cache *c, int layer, int32_t *out);
+/* table mirror (expert -> slot or dummy) and prior mirror of a layer */
+void      or_cache_table(const or_cache *c, int layer, int32_t *tbl, float *prior);
+void      or_cache_stats(const or_cache *c, or_stats *s);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,264 @@
+"""ctypes view of liboracle.so -- the CPU restatement of the MoE decode path.
+
+TEST INFRASTRUCTURE ONLY.  Imported by tests/, __graft_entry__.smoke() and the
+cpu_baseline leg of bench.py, always as the checker (or the CPU baseline timed
+beside the GPU), never as a product path.  See oracle.h for what each function
+restates and what pins it.
+"""
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "liboracle.so")
+
+Q4K, Q6K = 12, 14
+QK = 256
+Q4K_BYTES, Q6K_BYTES, Q8K_BYTES = 144, 210, 292
+
+
+def build():
+    subprocess.run(["make", "-s", "-C", HERE], check=True)
+
+
+_lib = None
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            build()
+        _lib = ctypes.CDLL(LIB_PATH)
+        _declare(_lib)
+    return _lib
+
+
+class Knobs(ctypes.Structure):
+    _fields_ = [("max_inserts", ctypes.c_int32), ("admit_mode", ctypes.c_int32),
+                ("admit_window", ctypes.c_int32), ("admit_half", ctypes.c_int32),
+                ("admit_floor", ctypes.c_float), ("batch_tables", ctypes.c_int32),
+                ("early_issue", ctypes.c_int32), ("cache_prior", ctypes.c_float),
+                ("deterministic", ctypes.c_int32)]
+
+
+class Stats(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_uint64) for n in (
+        "n_steps", "clock", "n_hit", "n_miss", "n_uploads", "n_scheduled", "n_published",
+        "n_admit_ok", "n_admit_denied", "n_table_flushes")]
+
+
+P = ctypes.c_void_p
+I32 = ctypes.c_int32
+I64 = ctypes.c_int64
+F32 = ctypes.c_float
+
+
+def _declare(L):
+    def d(name, res, *args):
+        f = getattr(L, name)
+        f.restype = res
+        f.argtypes = list(args)
+    d("or_h2f", F32, ctypes.c_uint16)
+    d("or_f2h", ctypes.c_uint16, F32)
+    d("or_dequant_q4k", None, P, P, I64)
+    d("or_dequant_q6k", None, P, P, I64)
+    d("or_quant_q8k", None, P, P, I64)
+    d("or_dequant_q8k", None, P, P, I64)
+    d("or_dot_q4k_q8k", F32, ctypes.c_int, P, P)
+    d("or_dot_q6k_q8k", F32, ctypes.c_int, P, P)
+    d("or_dot_deq_f64", ctypes.c_double, ctypes.c_int, ctypes.c_int, P, P)
+    d("or_expf", F32, F32)
+    d("or_route", None, ctypes.c_int, ctypes.c_int, ctypes.c_int, P, P, P, P, P, P, P, P, P)
+    d("or_route_logits", None, ctypes.c_int, ctypes.c_int, P, P, P, P, P)
+    d("or_expert_chain", None, ctypes.c_int, ctypes.c_int, ctypes.c_int, P, P, P, P, P, P)
+    d("or_moe_layer", None, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, P, P, P, P,
+      ctypes.c_int)
+    d("or_expert_bytes", ctypes.c_size_t, ctypes.c_int, ctypes.c_int, ctypes.c_int)
+    d("or_dispatch", None, ctypes.c_int, ctypes.c_int, ctypes.c_int, P, P, P, P)
+    d("or_cache_create", P, ctypes.c_int, ctypes.c_int, P, ctypes.POINTER(Knobs))
+    d("or_cache_destroy", None, P)
+    d("or_cache_trace_open", ctypes.c_int, P, ctypes.c_char_p, ctypes.c_char_p)
+    d("or_cache_observe", None, P, ctypes.c_int, P, ctypes.c_int, ctypes.c_int)
+    d("or_cache_step", None, P)
+    d("or_cache_hold_job", None, P, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_uint64)
+    d("or_cache_frame", None, P, ctypes.c_int, P)
+    d("or_cache_table", None, P, ctypes.c_int, P, P)
+    d("or_cache_stats", None, P, ctypes.POINTER(Stats))
+
+
+def _p(a):
+    return None if a is None else a.ctypes.data
+
+
+# ---- codecs ---------------------------------------------------------------
+def h2f(h):
+    return lib().or_h2f(int(h))
+
+
+def f2h(f):
+    return lib().or_f2h(float(f))
+
+
+def dequant(wtype, blocks, n):
+    y = np.empty(n, np.float32)
+    blocks = np.ascontiguousarray(blocks, dtype=np.uint8)
+    (lib().or_dequant_q4k if wtype == Q4K else lib().or_dequant_q6k)(_p(blocks), _p(y), n)
+    return y
+
+
+def quant_q8k(x):
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.empty(x.size // QK * Q8K_BYTES, np.uint8)
+    lib().or_quant_q8k(_p(x), _p(out), x.size)
+    return out
+
+
+def dequant_q8k(blocks, n):
+    y = np.empty(n, np.float32)
+    blocks = np.ascontiguousarray(blocks, dtype=np.uint8)
+    lib().or_dequant_q8k(_p(blocks), _p(y), n)
+    return y
+
+
+def dot(wtype, n, w_row, q8):
+    w_row = np.ascontiguousarray(w_row, dtype=np.uint8)
+    q8 = np.ascontiguousarray(q8, dtype=np.uint8)
+    f = lib().or_dot_q4k_q8k if wtype == Q4K else lib().or_dot_q6k_q8k
+    return f(n, _p(w_row), _p(q8))
+
+
+def dot_f64(wtype, n, w_row, q8):
+    w_row = np.ascontiguousarray(w_row, dtype=np.uint8)
+    q8 = np.ascontiguousarray(q8, dtype=np.uint8)
+    return lib().or_dot_deq_f64(wtype, n, _p(w_row), _p(q8))
+
+
+# ---- router ---------------------------------------------------------------
+def expf(x):
+    return lib().or_expf(float(x))
+
+
+def route(W, x, K, bias=None, prior=None, table=None):
+    """W [E, H] f32, x [H] f32 -> (ids[K] i32, w[K] f32, slots[K] or None, probs[E])."""
+    W = np.ascontiguousarray(W, np.float32)
+    x = np.ascontiguousarray(x, np.float32)
+    E, H = W.shape
+    ids = np.empty(K, np.int32)
+    w = np.empty(K, np.float32)
+    probs = np.empty(E, np.float32)
+    slots = np.empty(K, np.int32) if table is not None else None
+    bias = None if bias is None else np.ascontiguousarray(bias, np.float32)
+    prior = None if prior is None else np.ascontiguousarray(prior, np.float32)
+    table = None if table is None else np.ascontiguousarray(table, np.int32)
+    lib().or_route(E, H, K, _p(W), _p(x), _p(bias), _p(prior), _p(table), _p(ids), _p(w),
+                   _p(slots), _p(probs))
+    return ids, w, slots, probs
+
+
+def route_logits(logits, K, prior=None):
+    logits = np.ascontiguousarray(logits, np.float32)
+    E = logits.size
+    ids = np.empty(K, np.int32)
+    w = np.empty(K, np.float32)
+    probs = np.empty(E, np.float32)
+    prior = None if prior is None else np.ascontiguousarray(prior, np.float32)
+    lib().or_route_logits(E, K, _p(logits), _p(prior), _p(ids), _p(w), _p(probs))
+    return ids, w, probs
+
+
+# ---- expert chain -----------------------------------------------------------
+def expert_bytes(H, I, down_type):
+    return lib().or_expert_bytes(H, I, down_type)
+
+
+def expert_chain(H, I, down_type, expert, x):
+    """expert: uint8 array of one expert's [up | gate | down] bytes."""
+    expert = np.ascontiguousarray(expert, np.uint8)
+    x = np.ascontiguousarray(x, np.float32)
+    upb = I * (H // QK) * Q4K_BYTES
+    y = np.empty(H, np.float32)
+    h = np.empty(I, np.float32)
+    base = expert.ctypes.data
+    lib().or_expert_chain(H, I, down_type, base, base + upb, base + 2 * upb, _p(x), _p(y), _p(h))
+    return y, h
+
+
+def moe_layer(H, I, down_type, experts, w, x, n_threads=1):
+    """experts: list of K uint8 arrays (or raw addresses); out = sum_k w_k y_k."""
+    K = len(experts)
+    ptrs = (ctypes.c_void_p * K)(*[e if isinstance(e, int) else e.ctypes.data for e in experts])
+    w = np.ascontiguousarray(w, np.float32)
+    x = np.ascontiguousarray(x, np.float32)
+    out = np.empty(H, np.float32)
+    lib().or_moe_layer(H, I, down_type, K, ctypes.cast(ptrs, ctypes.c_void_p), _p(w), _p(x),
+                       _p(out), n_threads)
+    return out
+
+
+def dispatch(ids, E):
+    ids = np.ascontiguousarray(ids, np.int32)
+    T, K = ids.shape
+    counts = np.empty(E, np.int32)
+    offsets = np.empty(E + 1, np.int32)
+    perm = np.empty(T * K, np.int32)
+    lib().or_dispatch(T, K, E, _p(ids), _p(counts), _p(offsets), _p(perm))
+    return counts, offsets, perm
+
+
+# ---- state machine ----------------------------------------------------------
+ADMIT = {"off": 0, "heat": 1, "window": 2}
+
+
+class Cache:
+    def __init__(self, slots, n_experts=128, max_inserts=2, admit="off", admit_window=8,
+                 admit_half=64, admit_floor=1.0, batch_tables=False, early_issue=False,
+                 cache_prior=0.0, deterministic=False):
+        self.slots = np.ascontiguousarray(slots, np.int32)
+        self.n_layers = self.slots.size
+        self.n_experts = n_experts
+        k = Knobs(max_inserts, ADMIT[admit], admit_window, admit_half, admit_floor,
+                  int(batch_tables), int(early_issue), cache_prior, int(deterministic))
+        self.h = lib().or_cache_create(self.n_layers, n_experts, _p(self.slots), ctypes.byref(k))
+
+    def close(self):
+        if self.h:
+            lib().or_cache_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        self.close()
+
+    def trace_open(self, route_path=None, map_path=None):
+        r = lib().or_cache_trace_open(self.h, route_path.encode() if route_path else None,
+                                      map_path.encode() if map_path else None)
+        if r != 0:
+            raise OSError("trace open failed")
+
+    def observe(self, layer, ids, n_tok=1):
+        ids = np.ascontiguousarray(ids, np.int32)
+        lib().or_cache_observe(self.h, layer, _p(ids), ids.size // n_tok, n_tok)
+
+    def step(self):
+        lib().or_cache_step(self.h)
+
+    def hold_job(self, layer, expert, slot, sched_step):
+        lib().or_cache_hold_job(self.h, layer, expert, slot, sched_step)
+
+    def frame(self, layer):
+        out = np.empty(int(self.slots[layer]), np.int32)
+        lib().or_cache_frame(self.h, layer, _p(out))
+        return out
+
+    def table(self, layer):
+        t = np.empty(self.n_experts, np.int32)
+        p = np.empty(self.n_experts, np.float32)
+        lib().or_cache_table(self.h, layer, _p(t), _p(p))
+        return t, p
+
+    def stats(self):
+        s = Stats()
+        lib().or_cache_stats(self.h, ctypes.byref(s))
+        return {n: getattr(s, n) for n, _ in Stats._fields_}

@@ -1,0 +1,188 @@
+"""Pins for the oracle's router, expert chain and dispatch (CPU only).
+
+  * or_expf against libm's expf: within 2 ulp over the softmax input range;
+  * the router against an fp64 softmax / sort on random inputs (ids equal
+    whenever the fp64 ordering is not within fp32 noise), and exactly on
+    integer-valued inputs where every logit is exact in any order -- the same
+    construction as the reference's top-k check (cpp/test-moe-sidecar.cpp:
+    155-217), including its rule that the lower id wins a tie;
+  * the cache prior acts on the selection only: weights stay the unbiased
+    probabilities of the chosen ids (patches/0007-...:109-124);
+  * the expert chain against an fp64 chain on the same quantized operands, and
+    its distance from an fp32-activation chain (why the GPU emulates Q8_K);
+  * dispatch against a brute-force stable sort.
+"""
+import numpy as np
+import pytest
+
+from oracle import oracle as O
+
+rng = np.random.default_rng(11)
+
+
+def _ulps(a, b):
+    a = np.float32(a).view(np.int32).astype(np.int64)
+    b = np.float32(b).view(np.int32).astype(np.int64)
+    return abs(a - b)
+
+
+def test_expf_within_2ulp():
+    xs = np.concatenate([np.linspace(-87, 0, 20001, dtype=np.float32),
+                         -np.abs(rng.standard_normal(5000)).astype(np.float32) * 10])
+    worst = max(_ulps(O.expf(float(x)), np.exp(np.float32(x))) for x in xs)
+    assert worst <= 2
+    assert O.expf(0.0) == 1.0
+    assert O.expf(-100.0) == 0.0
+
+
+def _f64_route(W, x, K, prior=None):
+    lg = W.astype(np.float64) @ x.astype(np.float64)
+    p = np.exp(lg - lg.max())
+    p /= p.sum()
+    sel = p + (0 if prior is None else prior.astype(np.float64))
+    order = sorted(range(len(sel)), key=lambda e: (-sel[e], e))
+    ids = np.array(order[:K])
+    w = p[ids] / p[ids].sum()
+    return ids, w, sel
+
+
+@pytest.mark.parametrize("E", [128, 256])
+def test_route_vs_f64(E):
+    H, K = 2048, 8
+    agree = 0
+    for t in range(40):
+        W = (rng.standard_normal((E, H)) * 0.02).astype(np.float32)
+        x = rng.standard_normal(H).astype(np.float32)
+        ids, w, _, probs = O.route(W, x, K)
+        rids, rw, sel = _f64_route(W, x, K)
+        s = np.sort(sel)[::-1]
+        if s[K - 1] - s[K] > 1e-5:         # selection not within fp32 noise
+            assert set(ids) == set(rids)
+            assert np.array_equal(ids, rids)
+            assert np.allclose(w, rw, rtol=1e-5, atol=1e-7)
+            agree += 1
+        assert np.isclose(probs.sum(), 1.0, atol=1e-5)
+        assert np.isclose(w.sum(), 1.0, atol=1e-6)
+    assert agree >= 30
+
+
+def test_route_integer_inputs_exact_with_ties():
+    # integer-valued W and x: every logit is an exact small integer in any
+    # summation order, so ties are frequent and the lower id must win them
+    E, H, K = 128, 2048, 8
+    ties = 0
+    for t in range(50):
+        # sparse small integers keep |logit| <= ~10, so no exp underflows and
+        # softmax stays strictly monotone between distinct logits
+        W = (rng.integers(-2, 3, size=(E, H)) * (rng.random((E, H)) < 0.004)).astype(np.float32)
+        x = rng.integers(-2, 3, size=H).astype(np.float32)
+        W[5] = W[70]                       # force an exact tie
+        ids, w, _, probs = O.route(W, x, K)
+        lg = W.astype(np.int64) @ x.astype(np.int64)
+        assert np.abs(lg).max() < 60
+        order = sorted(range(E), key=lambda e: (-lg[e], e))
+        assert list(ids) == order[:K]
+        ties += len(set(lg[order[:K + 1]])) < K + 1
+    assert ties > 10
+
+
+def test_route_prior_changes_selection_not_weights():
+    E, H, K = 128, 2048, 8
+    W = (rng.standard_normal((E, H)) * 0.02).astype(np.float32)
+    x = rng.standard_normal(H).astype(np.float32)
+    ids0, w0, _, probs = O.route(W, x, K)
+    # make the 9th..16th experts resident with a large delta: they must be chosen
+    order = np.argsort(-probs, kind="stable")
+    prior = np.zeros(E, np.float32)
+    prior[order[8:16]] = 0.5
+    ids1, w1, _, probs1 = O.route(W, x, K, prior=prior)
+    assert set(ids1) == set(order[8:16].tolist())
+    assert np.array_equal(probs, probs1)
+    assert np.allclose(w1, probs[ids1] / probs[ids1].sum(), rtol=1e-6)
+    # slot lookup through a table
+    table = np.full(E, 56, np.int32)
+    table[order[8:16]] = np.arange(8)
+    _, _, slots, _ = O.route(W, x, K, prior=prior, table=table)
+    assert np.array_equal(slots, table[ids1])
+
+
+def test_route_bias_steers():
+    E, H, K = 128, 2048, 8
+    W = (rng.standard_normal((E, H)) * 0.02).astype(np.float32)
+    x = rng.standard_normal(H).astype(np.float32)
+    bias = np.zeros(E, np.float32)
+    want = [3, 17, 40, 41, 77, 90, 100, 127]
+    bias[want] = 20.0
+    ids, _, _, _ = O.route(W, x, K, bias=bias)
+    assert sorted(ids) == want
+
+
+def _rand_expert(H, I, down_type):
+    upb = I * (H // 256) * 144
+    nb_dn = H * (I // 256)
+    parts = []
+    for _ in range(2):
+        b = rng.integers(0, 256, size=(upb // 144, 144), dtype=np.uint8)
+        b[:, 0:2] = np.frombuffer(np.float16(0.0008).tobytes(), np.uint8)
+        b[:, 2:4] = np.frombuffer(np.float16(0.0012).tobytes(), np.uint8)
+        parts.append(b.reshape(-1))
+    if down_type == O.Q4K:
+        b = rng.integers(0, 256, size=(nb_dn, 144), dtype=np.uint8)
+        b[:, 0:2] = np.frombuffer(np.float16(0.0008).tobytes(), np.uint8)
+        b[:, 2:4] = np.frombuffer(np.float16(0.0012).tobytes(), np.uint8)
+    else:
+        b = rng.integers(0, 256, size=(nb_dn, 210), dtype=np.uint8)
+        b[:, 192:208] = rng.integers(-20, 20, size=(nb_dn, 16)).astype(np.int8).view(np.uint8)
+        b[:, 208:210] = np.frombuffer(np.float16(0.0002).tobytes(), np.uint8)
+    parts.append(b.reshape(-1))
+    e = np.concatenate(parts)
+    assert e.size == O.expert_bytes(H, I, down_type)
+    return e
+
+
+@pytest.mark.parametrize("down_type", [O.Q4K, O.Q6K])
+def test_expert_chain_vs_f64(down_type):
+    H, I = 2048, 768
+    upb = I * (H // 256) * 144
+    e = _rand_expert(H, I, down_type)
+    x = rng.standard_normal(H).astype(np.float32)
+    y, h = O.expert_chain(H, I, down_type, e, x)
+    Wu = O.dequant(O.Q4K, e[:upb], I * H).reshape(I, H).astype(np.float64)
+    Wg = O.dequant(O.Q4K, e[upb:2 * upb], I * H).reshape(I, H).astype(np.float64)
+    Wd = O.dequant(down_type, e[2 * upb:], H * I).reshape(H, I).astype(np.float64)
+    xq = O.dequant_q8k(O.quant_q8k(x), H).astype(np.float64)
+    u, g = Wu @ xq, Wg @ xq
+    h64 = g / (1 + np.exp(-g)) * u
+    assert np.linalg.norm(h - h64) <= 1e-5 * np.linalg.norm(h64)
+    hq = O.dequant_q8k(O.quant_q8k(h), I).astype(np.float64)   # same h quantization
+    y64 = Wd @ hq
+    assert np.linalg.norm(y - y64) <= 1e-5 * np.linalg.norm(y64)
+    # without activation quantization the result is ~1e-2 away: the Q8_K step
+    # dominates, which is why the GPU path quantizes exactly like this
+    u2, g2 = Wu @ x, Wg @ x
+    yf = Wd @ (g2 / (1 + np.exp(-g2)) * u2)
+    rel = np.linalg.norm(y - yf) / np.linalg.norm(yf)
+    assert 1e-3 < rel < 5e-2
+
+
+def test_moe_layer_combines_in_k_order():
+    H, I, K = 2048, 768, 3
+    es = [_rand_expert(H, I, O.Q4K) for _ in range(K)]
+    x = rng.standard_normal(H).astype(np.float32)
+    w = np.array([0.5, 0.3, 0.2], np.float32)
+    out = O.moe_layer(H, I, O.Q4K, es, w, x, n_threads=2)
+    ys = [O.expert_chain(H, I, O.Q4K, e, x)[0] for e in es]
+    want = w[0] * ys[0]
+    for k in range(1, K):
+        want = (want + w[k] * ys[k]).astype(np.float32)
+    assert np.array_equal(out, want)
+
+
+def test_dispatch_brute_force():
+    for T, K, E in ((1, 8, 128), (7, 8, 16), (512, 8, 128), (64, 8, 256)):
+        ids = rng.integers(0, E, size=(T, K)).astype(np.int32)
+        counts, offsets, perm = O.dispatch(ids, E)
+        flat = ids.reshape(-1)
+        assert np.array_equal(counts, np.bincount(flat, minlength=E))
+        assert offsets[0] == 0 and np.array_equal(np.diff(offsets), counts)
+        assert np.array_equal(perm, np.argsort(flat, kind="stable"))
