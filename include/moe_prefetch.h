@@ -1,0 +1,220 @@
+/*
+ * moe_prefetch.h -- C ABI of the MI355X MoE decode hot path (libmoeprefetch.so).
+ *
+ * Plain pointers, sizes and int status codes; no C++ or torch types.  Device
+ * pointers are HIP device (HBM) addresses, `stream` is a hipStream_t passed as
+ * void* (null = the default stream).  Every call is safe to make from one
+ * host thread at a time per handle; calls on different handles are
+ * independent.
+ *
+ * Reference interfaces each entry point replaces (paths relative to the
+ * reference repository; patch line numbers are inside the .patch files):
+ *   moe_memcpy_h2d_batch    ggml_backend_cuda_memcpy_h2d_batch, patches/0006-online-predictor-batched-uploads-slot-profile.patch:52-87
+ *   moe_cache_create        llama_moe_cache_init, patches/0006-...:482-763 (knobs 0006:501-539, 0007:492-506, 0008:536-569)
+ *   moe_cache_destroy       llama_moe_cache_shutdown (owner-scoped teardown), patches/0009-moe-sidecar.patch:1021-1056
+ *   moe_cache_lookup        llama_moe_cache_lookup, patches/0008-fused-cpu-moe-rows.patch:1310 context (llama-moecache.h:60-70)
+ *   moe_cache_observe       moe_obs_cb (ggml_set_moe_obs_callback), patches/0006-...:295-400, 0007:247-321, 0008:504-518
+ *   moe_cache_step          llama_moe_cache_step, patches/0006-...:765-953, 0007:655-771, 0008:607-660
+ *   moe_cache_requires_sync llama_moe_cache_requires_sync, patches/0008-...:362-369, 601-605
+ *   moe_cache_trace_open    LLAMA_MOE_ROUTE_TRACE / LLAMA_MOE_MAP_RECORD writers, patches/0008-...:417-518
+ *   moe_cache_stats         LLAMA_MOE_STATS counters, patches/0006-...:928-953, 0007:758-770
+ *   moe_route               build_moe_ffn router: mul_mat(ffn_gate_inp) -> soft_max -> (+ prior, 0007:109-124)
+ *                           -> argsort_top_k -> get_rows -> normalise (llama.cpp llama-graph.cpp, un-vendored)
+ *   moe_experts             build_moe_ffn expert chain: mul_mat_id(up/gate) -> swiglu -> mul_mat_id(down)
+ *                           -> mul(weights) -> sum over k (0008:372-390, 0009:684-704; CPU twin ggml_cpu_moe_rows 0008:186-251)
+ *   moe_decode_layer        one cached MoE layer of the decode graph (0009:659-705)
+ *   moe_decode_token        llama_context::decode for one token over every cached layer followed by
+ *                           llama_moe_cache_step (0008:362-369)
+ *   moe_pool_*              the slab/slot store behind src/prefetch_engine.py ExpertCache (:45-168)
+ * No counterpart in the reference: moe_host_alloc/free (the reference pins the model buffer
+ * through ggml's CUDA_Host buffer type), moe_synth_* (seeded synthetic weights and inputs).
+ */
+#ifndef MOE_PREFETCH_H
+#define MOE_PREFETCH_H
+
+#include <stdbool.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status ------------------------------------------------------------ */
+#define MOE_OK          0
+#define MOE_ERR_ARG    -1   /* bad argument or unsupported shape */
+#define MOE_ERR_HIP    -2   /* a HIP runtime call failed */
+#define MOE_ERR_NOMEM  -3   /* allocation failed */
+#define MOE_ERR_STATE  -4   /* call not valid in the current state */
+#define MOE_ERR_IO     -5   /* trace file could not be opened or written */
+#define MOE_ERR_TIMEOUT -6  /* an upload did not finish in time */
+
+#define MOE_TYPE_Q4K 12     /* ggml type ids */
+#define MOE_TYPE_Q6K 14
+
+const char *moe_last_error(void);   /* message of the last failure on this thread */
+int moe_abi_version(void);
+
+/* ---- host memory -------------------------------------------------------- */
+/* Pinned host memory, mapped for device access (the expert store). */
+void *moe_host_alloc(size_t bytes);
+int moe_host_free(void *p);
+/* Device address of pinned host memory from moe_host_alloc (NULL if it is not
+ * device-mapped).  Kernels read absent experts through this address. */
+void *moe_host_device_ptr(void *host);
+/* HBM allocations for callers without a device allocator of their own. */
+void *moe_device_alloc(size_t bytes);
+int moe_device_free(void *p);
+int moe_device_synchronize(void);
+/* Synchronous copy between any two addresses the HIP runtime knows. */
+int moe_memcpy(void *dst, const void *src, size_t bytes);
+
+/* ---- batched host->device copy ----------------------------------------- */
+/* n copies on this library's per-thread copy stream and ONE synchronise.
+ * Returns false on any error, after synchronising; the caller treats the
+ * whole batch as not done.  n <= 0 returns true. */
+bool moe_memcpy_h2d_batch(int device, void **dst, const void **src, const size_t *sizes, int n);
+
+/* ---- synthetic inputs (no counterpart in the reference) ------------------ */
+/* Experts e0 .. e0+n-1 of `layer`, [up|gate|down] layout, each at out + e*stride.
+ * Weights N(0, sigma) quantized to Q4_K (up, gate) and down_type (down). */
+int moe_synth_experts(uint64_t seed, int layer, int e0, int n, int H, int I, int down_type,
+                      float sigma, void *out_dev, size_t stride, void *stream);
+int moe_synth_experts_host(uint64_t seed, int layer, int e0, int n, int H, int I, int down_type,
+                           float sigma, void *out_host, size_t stride, int n_threads);
+/* out[(a - a0)][(b - b0)][i] = N(0, sigma) value (kind, a, b, i), n values per (a, b).
+ * kinds: 0 router rows (a = layer, b = expert), 1 activations (a = token, b = layer). */
+int moe_synth_vec(uint64_t seed, int kind, int a0, int na, int b0, int nb, int n, float sigma,
+                  float *out_dev, void *stream);
+int moe_synth_vec_host(uint64_t seed, int kind, int a0, int na, int b0, int nb, int n, float sigma,
+                       float *out_host);
+size_t moe_expert_bytes(int H, int I, int down_type);
+
+/* ---- kernels --------------------------------------------------------------- */
+typedef struct {
+    const float *W;        /* dev [E][H] router weights, f32 */
+    const float *x;        /* dev [n_tok][H] */
+    const float *bias;     /* dev [n_tok][E] or NULL: added to the logits */
+    const float *prior;    /* dev [E] or NULL: added to the probabilities for selection only */
+    const int32_t *table;  /* dev [E] or NULL: expert -> slot (n_slots = absent) */
+    int32_t dummy;         /* slot written when table is NULL */
+    int32_t E, H, K, n_tok;
+    int32_t *ids;          /* dev out [n_tok][K], descending selection, lower id first on ties */
+    float *w;              /* dev out [n_tok][K], probs[ids] / sum(probs[ids]) */
+    int32_t *slots;        /* dev out [n_tok][K] */
+    float *probs;          /* dev out [n_tok][E] or NULL */
+    uint8_t *q8x;          /* dev out [n_tok][H/256] Q8_K blocks of x (292 B each) */
+    void *workspace;       /* dev, moe_route_workspace_bytes(); zero before first use */
+} moe_route_desc;
+
+typedef struct {
+    const int32_t *ids;       /* dev [K] */
+    const int32_t *slots;     /* dev [K] */
+    const float *w;           /* dev [K] */
+    const uint8_t *slot_pool; /* dev [n_slots][slot_bytes] */
+    uint64_t slot_bytes;
+    int32_t n_slots;
+    const uint8_t *host_store;  /* device address (moe_host_device_ptr) of the pinned
+                                   [n_experts][expert_bytes] store; absent experts are read from it */
+    uint64_t expert_bytes;
+    int32_t n_experts;          /* experts in host_store; an id outside it contributes zero */
+    const uint8_t *q8x;       /* dev [H/256] Q8_K of x (from moe_route) */
+    float *out;               /* dev [H] */
+    int32_t accumulate;       /* 1: out += sum_k w_k y_k */
+    int32_t H, I, K, down_type;
+    void *workspace;          /* dev, moe_experts_workspace_bytes(); zero before first use */
+} moe_experts_desc;
+
+size_t moe_route_workspace_bytes(int E, int n_tok);
+size_t moe_experts_workspace_bytes(int I, int K);
+int moe_route(const moe_route_desc *d, void *stream);
+int moe_experts(const moe_experts_desc *d, void *stream);
+
+/* ---- cache runtime --------------------------------------------------------- */
+typedef struct moe_cache moe_cache;
+
+#define MOE_ADMIT_OFF    0
+#define MOE_ADMIT_HEAT   1
+#define MOE_ADMIT_WINDOW 2
+
+#define MOE_PUBLISH_FIFO    0  /* wait for the previous step's copies, publish in scheduling order */
+#define MOE_PUBLISH_SORTED  1  /* LLAMA_MOE_DETERMINISTIC=1: wait, publish in (layer, slot) order */
+#define MOE_PUBLISH_LIVE    2  /* publish only copies already finished, in finishing order */
+
+typedef struct {
+    int32_t n_layers, n_experts, n_expert_used;  /* L, E, K */
+    int32_t hidden, intermediate;                /* H (2048), I (multiple of 256, <= 1024) */
+    int32_t n_slots;                             /* default slots per layer (--moe-expert-cache) */
+    const int32_t *slot_profile;                 /* [n_layers] slots per layer or NULL (LLAMA_MOE_SLOT_PROFILE) */
+    const int32_t *down_type;                    /* [n_layers] MOE_TYPE_* or NULL = all Q4_K */
+    int32_t max_inserts;                         /* --moe-expert-cache-inserts, default 2 */
+    int32_t admit_mode;                          /* LLAMA_MOE_ADMIT */
+    int32_t admit_window;                        /* LLAMA_MOE_ADMIT_WINDOW, default 8 */
+    int32_t admit_half;                          /* LLAMA_MOE_ADMIT_HALF, default 64 */
+    float admit_floor;                           /* LLAMA_MOE_ADMIT_FLOOR, default 1 */
+    int32_t batch_tables;                        /* LLAMA_MOE_BATCH_TABLES */
+    int32_t early_issue;                         /* LLAMA_MOE_EARLY_ISSUE */
+    float cache_prior;                           /* LLAMA_MOE_CACHE_PRIOR (delta, probabilities) */
+    int32_t publish;                             /* MOE_PUBLISH_*; LLAMA_MOE_DETERMINISTIC=1 is SORTED */
+    int32_t device;                              /* HIP device; < 0: state machine only (no GPU, no
+                                                    weights: every upload completes at once) */
+} moe_cache_config;
+
+typedef struct {
+    uint64_t n_steps, clock, n_hit, n_miss, n_uploads, n_scheduled, n_copied, n_published;
+    uint64_t n_admit_ok, n_admit_denied, n_table_flushes;
+    uint64_t bytes_uploaded;
+    double publication_wait_us;                  /* time step() spent waiting for copies */
+} moe_cache_stats;
+
+typedef struct {
+    int32_t il, n_slots, n_experts, down_type;
+    uint64_t slot_bytes, expert_bytes;
+    uint8_t *slot_pool;         /* dev [n_slots][slot_bytes] */
+    int32_t *dev_table;         /* dev [E]: slot or n_slots */
+    float *prior;               /* dev [E] or NULL when cache_prior == 0 */
+    const uint8_t *host_store;  /* registered pinned store or NULL */
+    const float *router;        /* registered router weights or NULL */
+} moe_layer_view;
+
+int moe_cache_create(const moe_cache_config *cfg, moe_cache **out);
+int moe_cache_destroy(moe_cache *c);
+/* register caller-owned memory: pinned [E][expert_bytes] store, device [E][H] router */
+int moe_cache_set_host_store(moe_cache *c, int layer, const void *experts, size_t expert_bytes);
+int moe_cache_set_router(moe_cache *c, int layer, const float *W_dev);
+int moe_cache_lookup(moe_cache *c, int layer, moe_layer_view *out);
+int moe_cache_trace_open(moe_cache *c, const char *route_path, const char *map_path);
+/* host ids, token-major [n_tok][n_ids] */
+int moe_cache_observe(moe_cache *c, int layer, const int32_t *ids, int n_ids, int n_tok);
+/* between graph executions only: publish, schedule uploads, flush tables */
+int moe_cache_step(moe_cache *c);
+int moe_cache_requires_sync(const moe_cache *c);
+int moe_cache_frame(moe_cache *c, int layer, int32_t *out);   /* out[slot] = expert or -1 */
+int moe_cache_table(moe_cache *c, int layer, int32_t *tbl, float *prior);  /* host mirrors */
+int moe_cache_stats_get(moe_cache *c, moe_cache_stats *out);
+int moe_cache_sync(moe_cache *c);  /* wait for every upload in flight */
+
+/* One layer at batch 1: route x (+bias), run the K experts, out = sum_k w_k y_k.
+ * ids_dev/w_dev receive this layer's routing (dev [K]) when not NULL. */
+int moe_decode_layer(moe_cache *c, int layer, const float *x, const float *bias, float *out,
+                     int32_t *ids_dev, float *w_dev, void *stream);
+/* One decode token over every layer: x dev [L][H], bias dev [L][E] or NULL,
+ * out dev [L][H]; then the routed ids come back (one copy), are observed in
+ * layer order and the cache steps.  ids_host [L][K] receives them when not NULL. */
+int moe_decode_token(moe_cache *c, const float *x, const float *bias, float *out, int32_t *ids_host,
+                     void *stream);
+
+/* ---- slab pool behind the Python ExpertCache ------------------------------- */
+typedef struct moe_pool moe_pool;
+int moe_pool_create(int n_layers, int capacity, size_t bytes_per_expert, int device, moe_pool **out);
+int moe_pool_destroy(moe_pool *p);
+/* async copy host -> slot on the pool's copy stream; records the slot's event */
+int moe_pool_copy(moe_pool *p, int layer, int slot, const void *src_host, size_t bytes);
+int moe_pool_ready(moe_pool *p, int layer, int slot);   /* 1 done, 0 in flight, <0 error */
+int moe_pool_sync(moe_pool *p);
+void *moe_pool_slot_ptr(moe_pool *p, int layer, int slot);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

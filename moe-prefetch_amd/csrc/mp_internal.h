@@ -1,0 +1,53 @@
+// mp_internal.h -- kernel argument blocks and launchers shared by the kernels
+// (mp_kernels.hip) and the host runtime (mp_runtime.cpp).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace mp {
+
+struct RouteLaunch {
+    const float *W;        // [E][H] f32
+    const float *x;        // [n_tok][H] f32
+    const float *bias;     // [n_tok][E] or null (synthetic steering)
+    const float *prior;    // [E] or null (cache prior: delta on resident experts)
+    const int32_t *table;  // [E] or null (expert -> slot, n_slots = absent)
+    int32_t dummy;
+    int E, H, K, n_tok;
+    float *logits;         // scratch [n_tok][E]
+    uint32_t *counter;     // scratch [n_tok], zero
+    int32_t *ids;          // out [n_tok][K]
+    float *w;              // out [n_tok][K]
+    int32_t *slots;        // out [n_tok][K]
+    float *probs;          // out [n_tok][E] or null
+    uint8_t *q8x;          // out [n_tok][H/256][292]
+};
+
+struct ExpertArgs {
+    const int32_t *ids;       // [K]
+    const int32_t *slots;     // [K]
+    const float *w;           // [K]
+    const uint8_t *slot_pool; // [n_slots][slot_bytes] in HBM
+    uint64_t slot_bytes;
+    int n_slots;
+    const uint8_t *host_store;  // [n_experts][expert_bytes], device view of pinned host memory
+    uint64_t expert_bytes;
+    int n_experts;
+    const uint8_t *q8x;       // [H/256][292]
+    float *h;                 // scratch [K][I]
+    uint8_t *q8h;             // scratch [K][I/256][292]
+    uint32_t *counter;        // scratch [K], zero
+    float *out;               // [H]
+    int accumulate;           // 1: out += result
+    int H, I, K, down_type;
+};
+
+hipError_t launch_route(const RouteLaunch &l, hipStream_t st);
+hipError_t launch_experts(const ExpertArgs &a, hipStream_t st);
+hipError_t launch_synth_experts(uint64_t seed, int layer, int e0, int n_experts, int H, int I, int down_type,
+                                float sigma, uint8_t *out, uint64_t stride, hipStream_t st);
+hipError_t launch_synth_vec(uint64_t seed, int kind, int a0, int na, int b0, int nb, int n, float sigma,
+                            float *out, hipStream_t st);
+
+}  // namespace mp

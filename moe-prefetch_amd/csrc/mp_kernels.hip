@@ -1,0 +1,513 @@
+// mp_kernels.hip -- gfx950 kernels of the batch-1 MoE decode step.
+//
+//   route_kernel    router GEMV (W_r f32 [E][H]) -> softmax -> + cache prior ->
+//                   top-k -> renormalised gate weights -> slot lookup, and the
+//                   Q8_K quantization of x the expert kernels consume.  One
+//                   wavefront per expert row; the last workgroup to finish (a
+//                   device-scope ticket, no waiting) does the softmax/top-k.
+//   gateup_kernel   for K routed experts: up/gate Q4_K rows against Q8_K(x)
+//                   with v_dot4_i32_i8, h = silu(gate) * up.  Resident experts
+//                   are read from their HBM slot, absent ones straight from the
+//                   pinned host store.  The last workgroup of each expert
+//                   quantizes that expert's h to Q8_K.
+//   down_kernel     down rows (Q4_K or Q6_K) against Q8_K(h), staged through LDS
+//                   in 16-byte aligned chunks of 8 rows (Q6_K rows are only
+//                   2-byte aligned), and the weighted combine over k in order.
+//
+// Numerics: integer dots are exact; fp32 only at the per-super-block scale and
+// across super-blocks.  The router follows the canonical order documented with
+// the oracle bit for bit (explicit fmaf, fixed butterflies, -ffp-contract=off).
+#include <hip/hip_runtime.h>
+
+#include "mp_format.h"
+#include "mp_internal.h"
+#include "mp_synth.h"
+
+namespace mp {
+
+// ---------------------------------------------------------------------------
+// canonical exp (same polynomial and constants as the oracle's or_expf)
+__device__ inline float canon_expf(float x) {
+    if (x < -87.0f) return 0.0f;
+    if (x > 88.0f) x = 88.0f;
+    const float n = rintf(x * 1.44269504088896341f);
+    float r = fmaf(n, -0.693145751953125f, x);
+    r = fmaf(n, -1.428606765330187045e-06f, r);
+    float p = 1.9841269841269841e-04f;
+    p = fmaf(p, r, 1.3888888888888889e-03f);
+    p = fmaf(p, r, 8.3333333333333333e-03f);
+    p = fmaf(p, r, 4.1666666666666667e-02f);
+    p = fmaf(p, r, 1.6666666666666667e-01f);
+    p = fmaf(p, r, 0.5f);
+    p = fmaf(p, r, 1.0f);
+    p = fmaf(p, r, 1.0f);
+    const uint32_t e = (uint32_t)((int32_t)n + 127);
+    return p * bits_f32(e << 23);
+}
+
+__device__ inline float bfly_add(float v) {
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) v = v + __shfl_xor(v, o, 64);
+    return v;
+}
+
+__device__ inline int32_t sdot4(uint32_t a, uint32_t b, int32_t c) {
+    return __builtin_amdgcn_sdot4((int)a, (int)b, c, false);
+}
+
+// One wavefront quantizes 256 values (4 per lane, lane-major) to a Q8_K block:
+// largest magnitude (first index on a tie) -> -127, q = min(127, rint(x*iscale)).
+__device__ void q8k_wave(const float *x, uint8_t *out, int lane) {
+    const float4 v = *(const float4 *)(x + 4 * lane);
+    float xv[4] = {v.x, v.y, v.z, v.w};
+    float amax = 0.0f, mx = 0.0f;
+    int idx = 1 << 30;
+    for (int i = 0; i < 4; ++i) {
+        const float ax = fabsf(xv[i]);
+        if (ax > amax) { amax = ax; mx = xv[i]; idx = 4 * lane + i; }
+    }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) {
+        const float oa = __shfl_xor(amax, o, 64);
+        const float om = __shfl_xor(mx, o, 64);
+        const int oi = __shfl_xor(idx, o, 64);
+        if (oa > amax || (oa == amax && oi < idx)) { amax = oa; mx = om; idx = oi; }
+    }
+    int q[4] = {0, 0, 0, 0};
+    float d = 0.0f;
+    if (amax != 0.0f) {
+        const float iscale = -127.0f / mx;
+        for (int i = 0; i < 4; ++i) {
+            const int t = (int)rintf(iscale * xv[i]);
+            q[i] = t < 127 ? t : 127;
+        }
+        d = 1.0f / iscale;
+    }
+    int gs = q[0] + q[1] + q[2] + q[3];
+    gs += __shfl_xor(gs, 1, 64);
+    gs += __shfl_xor(gs, 2, 64);
+    const uint32_t packed = (uint32_t)(q[0] & 0xff) | ((uint32_t)(q[1] & 0xff) << 8) |
+                            ((uint32_t)(q[2] & 0xff) << 16) | ((uint32_t)(q[3] & 0xff) << 24);
+    *(uint32_t *)(out + 4 + 4 * lane) = packed;
+    if ((lane & 3) == 0) *(int16_t *)(out + 4 + QK + 2 * (lane >> 2)) = (int16_t)gs;
+    if (lane == 0) *(float *)out = d;
+}
+
+// ---------------------------------------------------------------------------
+// router
+struct RouteArgs {
+    const float *W;        // [E][H]
+    const float *x;        // [n_tok][H]
+    const float *bias;     // [n_tok][E] or null
+    const float *prior;    // [E] or null
+    const int32_t *table;  // [E] or null
+    int32_t dummy;         // slot value for "absent" when no table
+    int E, H, K;
+    float *logits;         // scratch [n_tok][E]
+    uint32_t *counter;     // scratch [n_tok], zero between launches
+    int32_t *ids;          // [n_tok][K]
+    float *w;              // [n_tok][K]
+    int32_t *slots;        // [n_tok][K]
+    float *probs;          // [n_tok][E] or null
+    uint8_t *q8x;          // [n_tok][H/256 * 292]
+};
+
+__global__ __launch_bounds__(256) void route_kernel(RouteArgs a) {
+    const int tok = blockIdx.y;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int e = blockIdx.x * 4 + wave;
+    const float *x = a.x + (size_t)tok * a.H;
+    __shared__ uint32_t s_ticket;
+    __shared__ float s_lg[256];
+    __shared__ float s_p[256];
+
+    if (e < a.E) {
+        const float *w = a.W + (size_t)e * a.H;
+        float acc = 0.0f;
+        for (int i = 0; i < a.H / 256; ++i) {
+            const float4 wv = *(const float4 *)(w + 256 * i + 4 * lane);
+            const float4 xv = *(const float4 *)(x + 256 * i + 4 * lane);
+            acc = fmaf(wv.x, xv.x, acc);
+            acc = fmaf(wv.y, xv.y, acc);
+            acc = fmaf(wv.z, xv.z, acc);
+            acc = fmaf(wv.w, xv.w, acc);
+        }
+        acc = bfly_add(acc);
+        if (a.bias) acc = acc + a.bias[(size_t)tok * a.E + e];
+        if (lane == 0) a.logits[(size_t)tok * a.E + e] = acc;
+    }
+    __threadfence();
+    __syncthreads();
+    if (threadIdx.x == 0) s_ticket = atomicAdd(&a.counter[tok], 1u);
+    __syncthreads();
+    if (s_ticket != gridDim.x - 1) return;
+    __threadfence();
+
+    // last workgroup of this token: softmax, prior, top-k, weights, slots
+    for (int i = threadIdx.x; i < a.E; i += 256)
+        s_lg[i] = __hip_atomic_load(a.logits + (size_t)tok * a.E + i, __ATOMIC_RELAXED,
+                                    __HIP_MEMORY_SCOPE_AGENT);
+    __syncthreads();
+    if (wave == 0) {
+        const int nc = a.E / 64;
+        float m = s_lg[lane];
+        for (int c = 1; c < nc; ++c) m = fmaxf(m, s_lg[64 * c + lane]);
+#pragma unroll
+        for (int o = 32; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+        float ex[4];
+        float s = 0.0f;
+        for (int c = 0; c < nc; ++c) {
+            ex[c] = canon_expf(s_lg[64 * c + lane] - m);
+            const float cs = bfly_add(ex[c]);
+            s = c == 0 ? cs : s + cs;
+        }
+        float sel[4];
+        int taken = 0;
+        for (int c = 0; c < nc; ++c) {
+            const int ee = 64 * c + lane;
+            const float p = ex[c] / s;
+            s_p[ee] = p;
+            if (a.probs) a.probs[(size_t)tok * a.E + ee] = p;
+            sel[c] = a.prior ? p + a.prior[ee] : p;
+        }
+        int ids[16];
+        for (int k = 0; k < a.K; ++k) {
+            float bv = -INFINITY;
+            int bi = 1 << 30;
+            for (int c = 0; c < nc; ++c) {
+                if (taken & (1 << c)) continue;
+                if (sel[c] > bv) { bv = sel[c]; bi = 64 * c + lane; }  // c ascending: lower id keeps a tie
+            }
+#pragma unroll
+            for (int o = 32; o >= 1; o >>= 1) {
+                const float ov = __shfl_xor(bv, o, 64);
+                const int oi = __shfl_xor(bi, o, 64);
+                if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
+            }
+            if (bi >= a.E) bi = 0;   // only if every candidate were NaN: keep the index in range
+            ids[k] = bi;
+            if ((bi & 63) == lane) taken |= 1 << (bi >> 6);
+        }
+        __builtin_amdgcn_wave_barrier();
+        if (lane == 0) {
+            float ws = 0.0f;
+            for (int k = 0; k < a.K; ++k) ws = ws + s_p[ids[k]];
+            for (int k = 0; k < a.K; ++k) {
+                a.ids[(size_t)tok * a.K + k] = ids[k];
+                a.w[(size_t)tok * a.K + k] = s_p[ids[k]] / ws;
+                a.slots[(size_t)tok * a.K + k] = a.table ? a.table[ids[k]] : a.dummy;
+            }
+        }
+    }
+    // Q8_K of x for the expert kernels (all four waves)
+    uint8_t *q8 = a.q8x + (size_t)tok * (a.H / QK) * Q8K_BYTES;
+    for (int b = wave; b < a.H / QK; b += 4) q8k_wave(x + QK * b, q8 + (size_t)b * Q8K_BYTES, lane);
+    if (threadIdx.x == 0) a.counter[tok] = 0;
+}
+
+// ---------------------------------------------------------------------------
+// expert pointers: resident -> HBM slot, absent -> pinned host store
+// (null for an id outside the store: that expert contributes zero)
+__device__ inline const uint8_t *expert_base(const ExpertArgs &a, int k) {
+    const int slot = a.slots[k];
+    if (a.slot_pool && slot >= 0 && slot < a.n_slots) return a.slot_pool + (size_t)slot * a.slot_bytes;
+    const int id = a.ids[k];
+    if (!a.host_store || id < 0 || id >= a.n_experts) return nullptr;
+    return a.host_store + (size_t)id * a.expert_bytes;
+}
+
+// byte i (0..11) of the Q4_K scale field held in three words
+__device__ inline int sc_byte(const uint4 &hdr, int i) {
+    const uint32_t w = i < 4 ? hdr.y : (i < 8 ? hdr.z : hdr.w);
+    return (int)((w >> (8 * (i & 3))) & 0xffu);
+}
+
+__device__ inline void q4k_sm(const uint4 &hdr, int j, int &sc, int &m) {
+    if (j < 4) {
+        sc = sc_byte(hdr, j) & 63;
+        m = sc_byte(hdr, j + 4) & 63;
+    } else {
+        sc = (sc_byte(hdr, j + 4) & 0xF) | ((sc_byte(hdr, j - 4) >> 6) << 4);
+        m = (sc_byte(hdr, j + 4) >> 4) | ((sc_byte(hdr, j) >> 6) << 4);
+    }
+}
+
+// Q4_K super-block partial of one lane: 16 qs bytes (chunk u) against the
+// matching 32 activation bytes; returns (scale-weighted int dot, min-weighted bsum)
+__device__ inline void q4k_lane(uint4 hdr, uint4 qs, int u, const uint32_t *xlo, const uint32_t *xhi,
+                                int bslo, int bshi, int32_t &si, int32_t &mi) {
+    const int j = u >> 1;  // 64-element group
+    int sl, ml, sh, mh;
+    q4k_sm(hdr, 2 * j, sl, ml);
+    q4k_sm(hdr, 2 * j + 1, sh, mh);
+    const uint32_t q[4] = {qs.x, qs.y, qs.z, qs.w};
+    int32_t dl = 0, dh = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        dl = sdot4(q[i] & 0x0F0F0F0Fu, xlo[i], dl);
+        dh = sdot4((q[i] >> 4) & 0x0F0F0F0Fu, xhi[i], dh);
+    }
+    si = sl * dl + sh * dh;
+    mi = ml * bslo + mh * bshi;
+}
+
+template <int R>
+__global__ __launch_bounds__(256) void gateup_kernel(ExpertArgs a) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int k = blockIdx.y;
+    const int b = lane >> 3, u = lane & 7;
+    const int j = u >> 1;
+    const uint8_t *base = expert_base(a, k);
+    const size_t rb = (size_t)(a.H / QK) * Q4K_BYTES;     // 1152 at H = 2048
+    const uint8_t *up = base, *gate = base + (size_t)a.I * rb;
+    const bool valid = base != nullptr;
+
+    // this lane's activation bytes, held for every row
+    const uint8_t *xq = a.q8x + (size_t)b * Q8K_BYTES;
+    const float dx = *(const float *)xq;
+    uint32_t xlo[4], xhi[4];
+    const uint32_t *plo = (const uint32_t *)(xq + 4 + 64 * j + 16 * (u & 1));
+    const uint32_t *phi = (const uint32_t *)(xq + 4 + 64 * j + 32 + 16 * (u & 1));
+#pragma unroll
+    for (int i = 0; i < 4; ++i) { xlo[i] = plo[i]; xhi[i] = phi[i]; }
+    const int16_t *bs = (const int16_t *)(xq + 4 + QK);
+    const int bslo = bs[4 * j + (u & 1)], bshi = bs[4 * j + 2 + (u & 1)];
+
+    const int row0 = (blockIdx.x * 4 + wave) * R;
+    uint4 hg[R], qg[R], hu[R], qu[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        const size_t off = (size_t)(row0 + r) * rb + (size_t)b * Q4K_BYTES;
+        const uint4 z = make_uint4(0, 0, 0, 0);
+        hg[r] = valid ? *(const uint4 *)(gate + off) : z;
+        qg[r] = valid ? *(const uint4 *)(gate + off + 16 + 16 * u) : z;
+        hu[r] = valid ? *(const uint4 *)(up + off) : z;
+        qu[r] = valid ? *(const uint4 *)(up + off + 16 + 16 * u) : z;
+    }
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        float res[2];
+#pragma unroll
+        for (int m = 0; m < 2; ++m) {
+            const uint4 hdr = m == 0 ? hg[r] : hu[r];
+            const uint4 qs = m == 0 ? qg[r] : qu[r];
+            int32_t si, mi;
+            q4k_lane(hdr, qs, u, xlo, xhi, bslo, bshi, si, mi);
+            si += __shfl_xor(si, 1, 64);
+            mi += __shfl_xor(mi, 1, 64);
+            si += __shfl_xor(si, 2, 64);
+            mi += __shfl_xor(mi, 2, 64);
+            si += __shfl_xor(si, 4, 64);
+            mi += __shfl_xor(mi, 4, 64);
+            const float d = h2f((uint16_t)(hdr.x & 0xffff)) * dx;
+            const float dm = h2f((uint16_t)(hdr.x >> 16)) * dx;
+            float v = d * (float)si - dm * (float)mi;
+            v = v + __shfl_xor(v, 8, 64);
+            v = v + __shfl_xor(v, 16, 64);
+            v = v + __shfl_xor(v, 32, 64);
+            res[m] = v;
+        }
+        if (lane == 0) {
+            const float g = res[0], uu = res[1];
+            a.h[(size_t)k * a.I + row0 + r] = g / (1.0f + expf(-g)) * uu;
+        }
+    }
+
+    // the last workgroup of expert k quantizes its h to Q8_K
+    __shared__ uint32_t s_ticket;
+    __threadfence();
+    __syncthreads();
+    if (threadIdx.x == 0) s_ticket = atomicAdd(&a.counter[k], 1u);
+    __syncthreads();
+    if (s_ticket != gridDim.x - 1) return;
+    __threadfence();
+    const float *hk = a.h + (size_t)k * a.I;
+    uint8_t *q8h = a.q8h + (size_t)k * (a.I / QK) * Q8K_BYTES;
+    __shared__ __attribute__((aligned(16))) float s_h[1024];
+    for (int i = threadIdx.x; i < a.I; i += 256)
+        s_h[i] = __hip_atomic_load(hk + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __syncthreads();
+    for (int bb = wave; bb < a.I / QK; bb += 4) q8k_wave(s_h + QK * bb, q8h + (size_t)bb * Q8K_BYTES, lane);
+    if (threadIdx.x == 0) a.counter[k] = 0;
+}
+
+// ---------------------------------------------------------------------------
+// down + combine.  Workgroup = 8 waves, 8 output rows; wave w owns expert
+// kb + w of each group of 8 experts.
+constexpr int DN_ROWS = 8;
+constexpr int DN_LDS_ROWS = 5040;           // 8 Q6_K rows at I = 768
+constexpr int DN_LDS_Q8 = 3 * Q8K_BYTES;    // I <= 768
+
+__device__ inline uint32_t lds_u32_at2(const uint8_t *p) {   // 2-byte aligned
+    const uint16_t *q = (const uint16_t *)p;
+    return (uint32_t)q[0] | ((uint32_t)q[1] << 16);
+}
+
+template <int DT>
+__global__ __launch_bounds__(512) void down_kernel(ExpertArgs a) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int r0 = blockIdx.x * DN_ROWS;
+    const int nb = a.I / QK;
+    const int rowb = nb * (DT == TYPE_Q6K ? Q6K_BYTES : Q4K_BYTES);
+    __shared__ __attribute__((aligned(16))) uint8_t s_w[8][DN_LDS_ROWS];
+    __shared__ __attribute__((aligned(16))) uint8_t s_q8[8][DN_LDS_Q8 + 4];
+    __shared__ float s_y[16][DN_ROWS];
+
+    const int g = lane >> 3, u = lane & 7;   // g: row within the tile, u: part of a super-block
+    for (int kb = 0; kb < a.K; kb += 8) {
+        const int k = kb + wave;
+        if (k < a.K) {
+            const uint8_t *eb = expert_base(a, k);
+            uint4 *dst = (uint4 *)s_w[wave];
+            const int nvec = DN_ROWS * rowb / 16;
+            if (eb) {
+                const uint4 *src = (const uint4 *)(eb + 2ull * a.I * (a.H / QK) * Q4K_BYTES + (size_t)r0 * rowb);
+                for (int i = lane; i < nvec; i += 64) dst[i] = src[i];
+            } else {
+                for (int i = lane; i < nvec; i += 64) dst[i] = make_uint4(0, 0, 0, 0);
+            }
+            const uint32_t *q8s = (const uint32_t *)(a.q8h + (size_t)k * nb * Q8K_BYTES);
+            uint32_t *q8d = (uint32_t *)s_q8[wave];
+            for (int i = lane; i < nb * Q8K_BYTES / 4; i += 64) q8d[i] = q8s[i];
+        }
+        __syncthreads();
+        if (k < a.K) {
+            float y = 0.0f;
+            for (int b = 0; b < nb; ++b) {
+                const uint8_t *xq = s_q8[wave] + b * Q8K_BYTES;
+                const float dx = *(const float *)xq;
+                int32_t si = 0, mi = 0;
+                float d, dm = 0.0f;
+                if (DT == TYPE_Q4K) {
+                    const uint8_t *blk = s_w[wave] + g * rowb + b * Q4K_BYTES;
+                    const uint4 hdr = *(const uint4 *)blk;
+                    const uint4 qs = *(const uint4 *)(blk + 16 + 16 * u);
+                    const int j = u >> 1;
+                    const uint32_t *plo = (const uint32_t *)(xq + 4 + 64 * j + 16 * (u & 1));
+                    const uint32_t *phi = (const uint32_t *)(xq + 4 + 64 * j + 32 + 16 * (u & 1));
+                    uint32_t xlo[4], xhi[4];
+                    for (int i = 0; i < 4; ++i) { xlo[i] = plo[i]; xhi[i] = phi[i]; }
+                    const int16_t *bs = (const int16_t *)(xq + 4 + QK);
+                    q4k_lane(hdr, qs, u, xlo, xhi, bs[4 * j + (u & 1)], bs[4 * j + 2 + (u & 1)], si, mi);
+                    d = h2f((uint16_t)(hdr.x & 0xffff)) * dx;
+                    dm = h2f((uint16_t)(hdr.x >> 16)) * dx;
+                } else {
+                    const uint8_t *blk = s_w[wave] + g * rowb + b * Q6K_BYTES;
+                    const int hh = u >> 2, up4 = u & 3;
+                    const uint8_t *pa = blk + 64 * hh + 8 * up4;
+                    const uint8_t *pb = pa + 32;
+                    const uint8_t *ph = blk + 128 + 32 * hh + 8 * up4;
+                    const uint32_t a0 = lds_u32_at2(pa), a1 = lds_u32_at2(pa + 4);
+                    const uint32_t b0 = lds_u32_at2(pb), b1 = lds_u32_at2(pb + 4);
+                    const uint32_t h0 = lds_u32_at2(ph), h1 = lds_u32_at2(ph + 4);
+                    const int8_t *sc = (const int8_t *)(blk + 192 + 8 * hh + (up4 >> 1));
+                    const uint32_t L = 0x0F0F0F0Fu, Hm = 0x30303030u;
+                    const uint32_t qv[4][2] = {
+                        {(a0 & L) | ((h0 << 4) & Hm), (a1 & L) | ((h1 << 4) & Hm)},
+                        {(b0 & L) | ((h0 << 2) & Hm), (b1 & L) | ((h1 << 2) & Hm)},
+                        {((a0 >> 4) & L) | (h0 & Hm), ((a1 >> 4) & L) | (h1 & Hm)},
+                        {((b0 >> 4) & L) | ((h0 >> 2) & Hm), ((b1 >> 4) & L) | ((h1 >> 2) & Hm)}};
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        const uint32_t *px = (const uint32_t *)(xq + 4 + 128 * hh + 32 * q + 8 * up4);
+                        const uint32_t x0 = px[0], x1 = px[1];
+                        int32_t dq = sdot4(qv[q][0], x0, sdot4(qv[q][1], x1, 0));
+                        const int32_t sx = sdot4(0x01010101u, x0, sdot4(0x01010101u, x1, 0));
+                        dq -= 32 * sx;
+                        si += (int32_t)sc[2 * q] * dq;
+                    }
+                    d = h2f(*(const uint16_t *)(blk + 208)) * dx;
+                }
+                si += __shfl_xor(si, 1, 64);
+                si += __shfl_xor(si, 2, 64);
+                si += __shfl_xor(si, 4, 64);
+                float v;
+                if (DT == TYPE_Q4K) {
+                    mi += __shfl_xor(mi, 1, 64);
+                    mi += __shfl_xor(mi, 2, 64);
+                    mi += __shfl_xor(mi, 4, 64);
+                    v = d * (float)si - dm * (float)mi;
+                } else {
+                    v = d * (float)si;
+                }
+                y = b == 0 ? v : y + v;
+            }
+            if (u == 0) s_y[k][g] = y;
+        }
+        __syncthreads();
+    }
+    if (threadIdx.x < DN_ROWS) {
+        const int t = threadIdx.x;
+        float acc = a.w[0] * s_y[0][t];
+        for (int k = 1; k < a.K; ++k) acc = acc + a.w[k] * s_y[k][t];
+        a.out[r0 + t] = a.accumulate ? a.out[r0 + t] + acc : acc;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// synthetic data on the device
+__global__ void synth_experts_kernel(uint64_t seed, int layer, int e0, int n_experts, int H, int I,
+                                     int down_type, float sigma, uint8_t *out, uint64_t stride) {
+    const synth::ExpertShape sh{H, I, down_type};
+    const uint64_t nblk = (uint64_t)sh.n_blocks();
+    const uint64_t t = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= nblk * (uint64_t)n_experts) return;
+    const int e = (int)(t / nblk), blk = (int)(t % nblk);
+    synth::expert_block(seed, layer, e0 + e, sh, blk, sigma, out + (uint64_t)e * stride + sh.block_offset(blk));
+}
+
+__global__ void synth_vec_kernel(uint64_t seed, int kind, int a0, int na, int b0, int nb, int n,
+                                 float sigma, float *out) {
+    const uint64_t t = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const uint64_t total = (uint64_t)na * nb * n;
+    if (t >= total) return;
+    const int i = (int)(t % n);
+    const int bb = (int)((t / n) % nb);
+    const int aa = (int)(t / ((uint64_t)n * nb));
+    out[t] = synth::vec_value(seed, kind, a0 + aa, b0 + bb, i, sigma);
+}
+
+// ---------------------------------------------------------------------------
+// launchers (shapes were checked by the caller)
+hipError_t launch_route(const RouteLaunch &l, hipStream_t st) {
+    RouteArgs a;
+    a.W = l.W; a.x = l.x; a.bias = l.bias; a.prior = l.prior; a.table = l.table; a.dummy = l.dummy;
+    a.E = l.E; a.H = l.H; a.K = l.K;
+    a.logits = l.logits; a.counter = l.counter; a.ids = l.ids; a.w = l.w; a.slots = l.slots;
+    a.probs = l.probs; a.q8x = l.q8x;
+    dim3 grid((unsigned)(l.E / 4), (unsigned)l.n_tok);
+    hipLaunchKernelGGL(route_kernel, grid, dim3(256), 0, st, a);
+    return hipGetLastError();
+}
+
+hipError_t launch_experts(const ExpertArgs &a, hipStream_t st) {
+    constexpr int R = 2;
+    hipLaunchKernelGGL(gateup_kernel<R>, dim3((unsigned)(a.I / (4 * R)), (unsigned)a.K), dim3(256), 0, st, a);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    if (a.down_type == TYPE_Q6K)
+        hipLaunchKernelGGL(down_kernel<TYPE_Q6K>, dim3((unsigned)(a.H / DN_ROWS)), dim3(512), 0, st, a);
+    else
+        hipLaunchKernelGGL(down_kernel<TYPE_Q4K>, dim3((unsigned)(a.H / DN_ROWS)), dim3(512), 0, st, a);
+    return hipGetLastError();
+}
+
+hipError_t launch_synth_experts(uint64_t seed, int layer, int e0, int n_experts, int H, int I, int down_type,
+                                float sigma, uint8_t *out, uint64_t stride, hipStream_t st) {
+    const synth::ExpertShape sh{H, I, down_type};
+    const uint64_t total = (uint64_t)sh.n_blocks() * (uint64_t)n_experts;
+    const unsigned blocks = (unsigned)((total + 127) / 128);
+    hipLaunchKernelGGL(synth_experts_kernel, dim3(blocks), dim3(128), 0, st, seed, layer, e0, n_experts, H, I,
+                       down_type, sigma, out, stride);
+    return hipGetLastError();
+}
+
+hipError_t launch_synth_vec(uint64_t seed, int kind, int a0, int na, int b0, int nb, int n, float sigma,
+                            float *out, hipStream_t st) {
+    const uint64_t total = (uint64_t)na * nb * n;
+    const unsigned blocks = (unsigned)((total + 255) / 256);
+    hipLaunchKernelGGL(synth_vec_kernel, dim3(blocks), dim3(256), 0, st, seed, kind, a0, na, b0, nb, n, sigma, out);
+    return hipGetLastError();
+}
+
+}  // namespace mp

@@ -1,0 +1,982 @@
+// mp_runtime.cpp -- host side of libmoeprefetch.so: the C ABI, the per-layer
+// expert-id -> slot state machine, uploads into the HBM slot pool on a side
+// HIP stream, table publication, traces, and the batch-1 decode driver.
+//
+// State machine semantics follow llama-moecache.cpp as patched by 0006-0008 of
+// the reference (file:line inside the .patch files):
+//   observe   0006:295-400 (hit/miss, LRU clock, pending), 0007:247-321 (heat,
+//             miss window), 0008:504-518 (route trace line)
+//   issue     0006:241-293 early path; 0007:395-415 admission on it
+//   step      0006:765-953, 0007:655-771: publish finished uploads, n_steps++,
+//             per layer either schedule <= max_inserts uploads from the
+//             pending misses (non-early) or top the free pool up (early),
+//             heat decay, one batched table write
+//   publish   0008:613-627 deterministic (sorted) variant
+//   admission 0007:398-429; tables 0007:327-396; map trace 0008:417-489
+// The data path is this build's own: one contiguous copy per expert
+// ([up|gate|down] in the store and in the slot) on a dedicated stream,
+// completion by hipEvent, tables in one pinned mirror flushed with one copy.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <chrono>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <deque>
+#include <string>
+#include <thread>
+#include <vector>
+
+#include "../../include/moe_prefetch.h"
+#include "mp_format.h"
+#include "mp_internal.h"
+#include "mp_synth.h"
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(int code, const char *fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    g_err = buf;
+    return code;
+}
+
+#define HIPCHK(expr)                                                                            \
+    do {                                                                                        \
+        hipError_t e_ = (expr);                                                                 \
+        if (e_ != hipSuccess) return fail(MOE_ERR_HIP, "%s: %s", #expr, hipGetErrorString(e_)); \
+    } while (0)
+
+constexpr uint64_t U64MAX = ~0ull;
+
+size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
+
+struct Layer {
+    int il = 0, S = 0, E = 0, down_type = mp::TYPE_Q4K;
+    uint64_t expert_bytes = 0, slot_bytes = 0;
+    uint8_t *pool = nullptr;                  // dev [S][slot_bytes]
+    const uint8_t *store_host = nullptr;      // host address of the pinned store
+    const uint8_t *store_dev = nullptr;       // device view of it
+    const float *router = nullptr;
+    std::vector<int32_t> slot_expert, expert_slot, free_slots, pending;
+    std::vector<uint64_t> slot_last_use, slot_protect, miss_last, miss_prev;
+    std::vector<uint8_t> slot_in_flight;
+    std::vector<float> heat;
+    bool tbl_dirty = false;
+    uint64_t n_hit = 0, n_miss = 0;
+};
+
+struct Job {
+    int li, expert, slot;
+    hipEvent_t ev;     // live mode only
+};
+
+}  // namespace
+
+struct moe_cache {
+    moe_cache_config cfg{};
+    bool host_only = false;            // device < 0: state machine only, no HIP calls
+    std::vector<Layer> L;
+    int H = 0, I = 0, E = 0, K = 0;
+    // tables: device copies and pinned host mirrors, [L][E]
+    int32_t *d_tbl = nullptr, *h_tbl = nullptr;
+    float *d_prior = nullptr, *h_prior = nullptr;
+    // kernel scratch
+    void *route_ws = nullptr, *exp_ws = nullptr;
+    int32_t *d_ids = nullptr, *d_slots = nullptr, *h_ids = nullptr;
+    float *d_w = nullptr;
+    uint8_t *d_q8x = nullptr;
+    uint8_t *pool_base = nullptr;
+    hipStream_t up_stream = nullptr, tbl_stream = nullptr;
+    hipEvent_t up_mark = nullptr;
+    std::deque<Job> jobs;              // issued, not yet published, in issue order
+    std::vector<hipEvent_t> free_events;
+    uint64_t clock = 0, n_steps = 0, n_uploads = 0, n_scheduled = 0, n_copied = 0, n_published = 0;
+    uint64_t n_admit_ok = 0, n_admit_denied = 0, n_table_flushes = 0, bytes_uploaded = 0;
+    double wait_us = 0.0;
+    FILE *route = nullptr, *map = nullptr;
+};
+
+struct moe_pool {
+    int n_layers = 0, capacity = 0, device = 0;
+    size_t bytes = 0;
+    uint8_t *base = nullptr;
+    hipStream_t stream = nullptr;
+    std::vector<hipEvent_t> ev;     // [n_layers * capacity]
+    std::vector<uint8_t> armed;
+};
+
+namespace {
+
+// ---------------------------------------------------------------------------
+// state machine pieces
+void set_table_entry(moe_cache *c, Layer &ls, int expert, int v) {
+    const size_t o = (size_t)ls.il * c->E + expert;
+    c->h_tbl[o] = v;
+    if (c->h_prior) c->h_prior[o] = v == ls.S ? 0.0f : c->cfg.cache_prior;
+    ls.tbl_dirty = true;
+}
+
+int32_t lru_resident(const Layer &ls) {
+    int32_t victim = -1;
+    uint64_t best = U64MAX;
+    for (int s = 0; s < ls.S; ++s) {
+        if (ls.slot_in_flight[s] || ls.slot_expert[s] < 0) continue;
+        if (ls.slot_last_use[s] < best) {
+            best = ls.slot_last_use[s];
+            victim = ls.slot_expert[s];
+        }
+    }
+    return victim;
+}
+
+bool admit_ok(moe_cache *c, const Layer &ls, int id, int victim) {
+    if (c->cfg.admit_mode == MOE_ADMIT_OFF || victim < 0) return true;
+    bool ok = true;
+    if (c->cfg.admit_mode == MOE_ADMIT_HEAT) {
+        ok = ls.heat[id] > ls.heat[victim] * 1.25f + c->cfg.admit_floor;
+    } else if (c->cfg.admit_mode == MOE_ADMIT_WINDOW) {
+        ok = ls.miss_prev[id] != U64MAX && ls.miss_last[id] - ls.miss_prev[id] < (uint64_t)c->cfg.admit_window;
+    }
+    if (ok) c->n_admit_ok++;
+    else c->n_admit_denied++;
+    return ok;
+}
+
+hipEvent_t take_event(moe_cache *c) {
+    if (!c->free_events.empty()) {
+        hipEvent_t e = c->free_events.back();
+        c->free_events.pop_back();
+        return e;
+    }
+    hipEvent_t e = nullptr;
+    if (hipEventCreateWithFlags(&e, hipEventDisableTiming) != hipSuccess) return nullptr;
+    return e;
+}
+
+// hand one expert copy to the upload stream
+int start_upload(moe_cache *c, int li, int expert, int slot) {
+    Layer &ls = c->L[li];
+    Job j{li, expert, slot, nullptr};
+    if (c->host_only) {
+        c->jobs.push_back(j);
+        c->bytes_uploaded += ls.expert_bytes;
+        return MOE_OK;
+    }
+    if (!ls.store_host) return fail(MOE_ERR_STATE, "layer %d has no host store registered", li);
+    HIPCHK(hipMemcpyAsync(ls.pool + (size_t)slot * ls.slot_bytes, ls.store_host + (size_t)expert * ls.expert_bytes,
+                          ls.expert_bytes, hipMemcpyHostToDevice, c->up_stream));
+    if (c->cfg.publish == MOE_PUBLISH_LIVE) {
+        j.ev = take_event(c);
+        if (!j.ev) return fail(MOE_ERR_HIP, "event creation failed");
+        HIPCHK(hipEventRecord(j.ev, c->up_stream));
+    }
+    c->jobs.push_back(j);
+    c->bytes_uploaded += ls.expert_bytes;
+    return MOE_OK;
+}
+
+int issue_uploads(moe_cache *c, int li, const int32_t *ids, int n, int budget, int min_keep) {
+    Layer &ls = c->L[li];
+    int issued = 0;
+    for (int i = 0; i < n && issued < budget; ++i) {
+        const int id = ids[i];
+        if (id < 0 || id >= ls.E) continue;
+        if (ls.expert_slot[id] >= 0) continue;
+        if ((int)ls.free_slots.size() <= min_keep) break;
+        bool dup = false;
+        for (const Job &j : c->jobs)
+            if (j.li == li && j.expert == id) { dup = true; break; }
+        if (dup) continue;
+        const int slot = ls.free_slots.back();
+        ls.free_slots.pop_back();
+        ls.slot_in_flight[slot] = 1;
+        int r = start_upload(c, li, id, slot);
+        if (r != MOE_OK) return r;
+        c->n_uploads++;
+        c->n_scheduled++;
+        issued++;
+    }
+    return issued;
+}
+
+void map_frame(moe_cache *c) {
+    if (!c->map) return;
+    fprintf(c->map, "step %llu\n", (unsigned long long)c->n_steps);
+    for (const Layer &ls : c->L) {
+        std::vector<int32_t> pub(ls.S, -1);
+        for (int e = 0; e < ls.E; ++e)
+            if (ls.expert_slot[e] >= 0) pub[ls.expert_slot[e]] = e;
+        fprintf(c->map, "map %d", ls.il);
+        for (int v : pub) fprintf(c->map, " %d", v);
+        fputc('\n', c->map);
+    }
+    fflush(c->map);
+}
+
+int flush_tables(moe_cache *c) {
+    bool any = false;
+    for (Layer &ls : c->L) any |= ls.tbl_dirty;
+    if (!any) return MOE_OK;
+    if (c->host_only) {
+        for (Layer &ls : c->L) ls.tbl_dirty = false;
+        if (c->cfg.batch_tables) c->n_table_flushes++;
+        return MOE_OK;
+    }
+    const size_t n = (size_t)c->cfg.n_layers * c->E;
+    HIPCHK(hipMemcpyAsync(c->d_tbl, c->h_tbl, n * sizeof(int32_t), hipMemcpyHostToDevice, c->tbl_stream));
+    if (c->d_prior)
+        HIPCHK(hipMemcpyAsync(c->d_prior, c->h_prior, n * sizeof(float), hipMemcpyHostToDevice, c->tbl_stream));
+    HIPCHK(hipStreamSynchronize(c->tbl_stream));
+    for (Layer &ls : c->L) ls.tbl_dirty = false;
+    if (c->cfg.batch_tables) c->n_table_flushes++;
+    return MOE_OK;
+}
+
+void publish(moe_cache *c, const Job &j) {
+    Layer &ls = c->L[j.li];
+    ls.slot_expert[j.slot] = j.expert;
+    ls.expert_slot[j.expert] = j.slot;
+    ls.slot_last_use[j.slot] = ++c->clock;
+    ls.slot_in_flight[j.slot] = 0;
+    set_table_entry(c, ls, j.expert, j.slot);
+    c->n_published++;
+}
+
+int cache_step(moe_cache *c) {
+    // 1) publish finished uploads (no kernel of the cache is running)
+    if (!c->jobs.empty()) {
+        std::vector<Job> done;
+        if (c->host_only) {
+            done.assign(c->jobs.begin(), c->jobs.end());
+            c->jobs.clear();
+            if (c->cfg.publish == MOE_PUBLISH_SORTED)
+                std::stable_sort(done.begin(), done.end(), [](const Job &a, const Job &b) {
+                    return a.li != b.li ? a.li < b.li : a.slot < b.slot;
+                });
+        } else if (c->cfg.publish == MOE_PUBLISH_LIVE) {
+            while (!c->jobs.empty()) {
+                const hipError_t q = hipEventQuery(c->jobs.front().ev);
+                if (q == hipErrorNotReady) break;
+                if (q != hipSuccess) return fail(MOE_ERR_HIP, "hipEventQuery: %s", hipGetErrorString(q));
+                done.push_back(c->jobs.front());
+                c->free_events.push_back(c->jobs.front().ev);
+                c->jobs.pop_front();
+            }
+        } else {
+            const auto t0 = std::chrono::steady_clock::now();
+            HIPCHK(hipEventRecord(c->up_mark, c->up_stream));
+            HIPCHK(hipEventSynchronize(c->up_mark));
+            c->wait_us += std::chrono::duration<double, std::micro>(std::chrono::steady_clock::now() - t0).count();
+            done.assign(c->jobs.begin(), c->jobs.end());
+            c->jobs.clear();
+            if (c->cfg.publish == MOE_PUBLISH_SORTED)
+                std::stable_sort(done.begin(), done.end(), [](const Job &a, const Job &b) {
+                    return a.li != b.li ? a.li < b.li : a.slot < b.slot;
+                });
+        }
+        c->n_copied += done.size();
+        for (const Job &j : done) publish(c, j);
+    }
+
+    c->n_steps++;
+
+    // 2) per layer
+    for (size_t li = 0; li < c->L.size(); ++li) {
+        Layer &ls = c->L[li];
+        if (!c->cfg.early_issue) {
+            if (ls.pending.empty()) continue;
+            int budget = c->cfg.max_inserts;
+            for (auto it = ls.pending.rbegin(); it != ls.pending.rend() && budget > 0; ++it) {
+                const int id = *it;
+                if (ls.expert_slot[id] >= 0) {
+                    --budget;
+                    continue;
+                }
+                int slot = -1;
+                uint64_t best = U64MAX;
+                for (int s = 0; s < ls.S; ++s) {
+                    if (ls.slot_in_flight[s]) continue;
+                    if (ls.slot_expert[s] < 0) { slot = s; break; }
+                    if (ls.slot_protect[s] >= c->n_steps) continue;
+                    if (ls.slot_last_use[s] < best) { best = ls.slot_last_use[s]; slot = s; }
+                }
+                if (slot < 0) break;
+                const int victim = ls.slot_expert[slot];
+                if (!admit_ok(c, ls, id, victim)) continue;
+                --budget;
+                if (victim >= 0) {
+                    ls.expert_slot[victim] = -1;
+                    ls.slot_expert[slot] = -1;
+                    set_table_entry(c, ls, victim, ls.S);
+                }
+                ls.slot_in_flight[slot] = 1;
+                const int r = start_upload(c, (int)li, id, slot);
+                if (r != MOE_OK) return r;
+                c->n_scheduled++;
+            }
+            ls.pending.clear();
+            continue;
+        }
+        ls.pending.clear();
+        const int pool_target = c->cfg.max_inserts;
+        while ((int)ls.free_slots.size() < pool_target) {
+            int slot = -1;
+            uint64_t best = U64MAX;
+            for (int s = 0; s < ls.S; ++s) {
+                if (ls.slot_in_flight[s] || ls.slot_expert[s] < 0) continue;
+                if (ls.slot_protect[s] >= c->n_steps) continue;
+                if (ls.slot_last_use[s] < best) { best = ls.slot_last_use[s]; slot = s; }
+            }
+            if (slot < 0) break;
+            const int victim = ls.slot_expert[slot];
+            ls.expert_slot[victim] = -1;
+            ls.slot_expert[slot] = -1;
+            set_table_entry(c, ls, victim, ls.S);
+            ls.free_slots.push_back(slot);
+        }
+    }
+
+    // 3) heat decays on a clock
+    if (c->cfg.admit_mode == MOE_ADMIT_HEAT && c->cfg.admit_half > 0 && c->n_steps % (uint64_t)c->cfg.admit_half == 0)
+        for (Layer &ls : c->L)
+            for (float &h : ls.heat) h *= 0.5f;
+
+    // 4) every table edit of this step reaches the device in one transfer
+    const int r = flush_tables(c);
+    if (r != MOE_OK) return r;
+
+    map_frame(c);
+    if (c->route) fflush(c->route);
+    return MOE_OK;
+}
+
+int cache_observe(moe_cache *c, int li, const int32_t *ids, int n_ids, int n_tok) {
+    Layer &ls = c->L[li];
+    if (c->route) {
+        fprintf(c->route, "route %llu %d %d %d", (unsigned long long)c->n_steps, ls.il, n_ids, n_tok);
+        for (int i = 0; i < n_ids * n_tok; ++i)
+            fprintf(c->route, " %d:%d", ids[i], (ids[i] >= 0 && ids[i] < ls.E) ? ls.expert_slot[ids[i]] : -1);
+        fputc('\n', c->route);
+    }
+    for (int t = 0; t < n_tok; ++t) {
+        for (int i = 0; i < n_ids; ++i) {
+            const int id = ids[t * n_ids + i];
+            if (id < 0 || id >= ls.E) continue;
+            if (!ls.heat.empty()) ls.heat[id] += 1.0f;
+            const int slot = ls.expert_slot[id];
+            if (slot >= 0) {
+                ls.n_hit++;
+                ls.slot_last_use[slot] = ++c->clock;
+            } else {
+                ls.n_miss++;
+                if (!ls.miss_last.empty() && ls.miss_last[id] != c->n_steps) {
+                    ls.miss_prev[id] = ls.miss_last[id];
+                    ls.miss_last[id] = c->n_steps;
+                }
+                if (std::find(ls.pending.begin(), ls.pending.end(), id) == ls.pending.end())
+                    ls.pending.push_back(id);
+            }
+        }
+    }
+    if (c->cfg.early_issue) {
+        const int pool_target = c->cfg.max_inserts;
+        const int next_victim = c->cfg.admit_mode == MOE_ADMIT_OFF ? -1
+                                : ((int)ls.free_slots.size() > pool_target ? -1 : lru_resident(ls));
+        int r;
+        if (c->cfg.admit_mode == MOE_ADMIT_OFF) {
+            r = issue_uploads(c, li, ls.pending.data(), (int)ls.pending.size(), c->cfg.max_inserts, 0);
+        } else {
+            std::vector<int32_t> adm;
+            for (int id : ls.pending)
+                if (ls.expert_slot[id] < 0 && admit_ok(c, ls, id, next_victim)) adm.push_back(id);
+            r = issue_uploads(c, li, adm.data(), (int)adm.size(), c->cfg.max_inserts, 0);
+        }
+        if (r < 0) return r;
+    }
+    return MOE_OK;
+}
+
+int check_shape(int E, int H, int I, int K) {
+    if (H != 2048) return fail(MOE_ERR_ARG, "hidden size %d unsupported (the kernels are built for 2048)", H);
+    if (E <= 0 || E % 64 != 0 || E > 256) return fail(MOE_ERR_ARG, "n_experts %d must be a multiple of 64 <= 256", E);
+    if (K <= 0 || K > 16 || K > E) return fail(MOE_ERR_ARG, "n_expert_used %d must be 1..16", K);
+    if (I != 0 && (I % 256 != 0 || I > 768))
+        return fail(MOE_ERR_ARG, "intermediate %d must be 256, 512 or 768", I);
+    return MOE_OK;
+}
+
+size_t route_ws_bytes(int E, int n_tok) { return align_up((size_t)n_tok * E * 4, 256) + align_up((size_t)n_tok * 4, 256); }
+size_t exp_ws_bytes(int I, int K) {
+    return align_up((size_t)K * I * 4, 256) + align_up((size_t)K * (I / 256) * mp::Q8K_BYTES, 256) +
+           align_up((size_t)K * 4, 256);
+}
+
+int run_route(const moe_route_desc *d, hipStream_t st) {
+    mp::RouteLaunch l{};
+    l.W = d->W; l.x = d->x; l.bias = d->bias; l.prior = d->prior; l.table = d->table; l.dummy = d->dummy;
+    l.E = d->E; l.H = d->H; l.K = d->K; l.n_tok = d->n_tok;
+    uint8_t *ws = (uint8_t *)d->workspace;
+    l.logits = (float *)ws;
+    l.counter = (uint32_t *)(ws + align_up((size_t)d->n_tok * d->E * 4, 256));
+    l.ids = d->ids; l.w = d->w; l.slots = d->slots; l.probs = d->probs; l.q8x = d->q8x;
+    HIPCHK(mp::launch_route(l, st));
+    return MOE_OK;
+}
+
+int run_experts(const moe_experts_desc *d, hipStream_t st) {
+    mp::ExpertArgs a{};
+    a.ids = d->ids; a.slots = d->slots; a.w = d->w;
+    a.slot_pool = d->slot_pool; a.slot_bytes = d->slot_bytes; a.n_slots = d->n_slots;
+    a.host_store = d->host_store; a.expert_bytes = d->expert_bytes; a.n_experts = d->n_experts;
+    a.q8x = d->q8x; a.out = d->out; a.accumulate = d->accumulate;
+    a.H = d->H; a.I = d->I; a.K = d->K; a.down_type = d->down_type;
+    uint8_t *ws = (uint8_t *)d->workspace;
+    a.h = (float *)ws;
+    size_t o = align_up((size_t)d->K * d->I * 4, 256);
+    a.q8h = ws + o;
+    o += align_up((size_t)d->K * (d->I / 256) * mp::Q8K_BYTES, 256);
+    a.counter = (uint32_t *)(ws + o);
+    HIPCHK(mp::launch_experts(a, st));
+    return MOE_OK;
+}
+
+void free_cache(moe_cache *c) {
+    if (!c) return;
+    if (c->host_only) {
+        free(c->h_tbl);
+        free(c->h_prior);
+        if (c->route) fclose(c->route);
+        if (c->map) fclose(c->map);
+        delete c;
+        return;
+    }
+    if (c->up_stream) hipStreamSynchronize(c->up_stream);
+    for (Job &j : c->jobs)
+        if (j.ev) hipEventDestroy(j.ev);
+    for (hipEvent_t e : c->free_events) hipEventDestroy(e);
+    if (c->up_mark) hipEventDestroy(c->up_mark);
+    if (c->up_stream) hipStreamDestroy(c->up_stream);
+    if (c->tbl_stream) hipStreamDestroy(c->tbl_stream);
+    hipFree(c->pool_base);
+    hipFree(c->d_tbl);
+    hipFree(c->d_prior);
+    hipFree(c->route_ws);
+    hipFree(c->exp_ws);
+    hipFree(c->d_ids);
+    hipFree(c->d_slots);
+    hipFree(c->d_w);
+    hipFree(c->d_q8x);
+    if (c->h_tbl) hipHostFree(c->h_tbl);
+    if (c->h_prior) hipHostFree(c->h_prior);
+    if (c->h_ids) hipHostFree(c->h_ids);
+    if (c->route) fclose(c->route);
+    if (c->map) fclose(c->map);
+    delete c;
+}
+
+}  // namespace
+
+// ===========================================================================
+// C ABI
+extern "C" {
+
+const char *moe_last_error(void) { return g_err.c_str(); }
+int moe_abi_version(void) { return 1; }
+
+void *moe_host_alloc(size_t bytes) {
+    void *p = nullptr;
+    if (hipHostMalloc(&p, bytes, hipHostMallocMapped | hipHostMallocPortable) != hipSuccess) {
+        fail(MOE_ERR_NOMEM, "hipHostMalloc(%zu) failed", bytes);
+        return nullptr;
+    }
+    return p;
+}
+
+int moe_host_free(void *p) {
+    if (p) HIPCHK(hipHostFree(p));
+    return MOE_OK;
+}
+
+void *moe_host_device_ptr(void *host) {
+    void *dev = nullptr;
+    if (!host || hipHostGetDevicePointer(&dev, host, 0) != hipSuccess) {
+        fail(MOE_ERR_ARG, "%p is not device-mapped pinned memory", host);
+        return nullptr;
+    }
+    return dev;
+}
+
+void *moe_device_alloc(size_t bytes) {
+    void *p = nullptr;
+    if (hipMalloc(&p, bytes) != hipSuccess) {
+        fail(MOE_ERR_NOMEM, "hipMalloc(%zu) failed", bytes);
+        return nullptr;
+    }
+    return p;
+}
+
+int moe_device_free(void *p) {
+    if (p) HIPCHK(hipFree(p));
+    return MOE_OK;
+}
+
+int moe_device_synchronize(void) {
+    HIPCHK(hipDeviceSynchronize());
+    return MOE_OK;
+}
+
+int moe_memcpy(void *dst, const void *src, size_t bytes) {
+    if (!dst || !src) return fail(MOE_ERR_ARG, "null pointer");
+    HIPCHK(hipMemcpy(dst, src, bytes, hipMemcpyDefault));
+    return MOE_OK;
+}
+
+bool moe_memcpy_h2d_batch(int device, void **dst, const void **src, const size_t *sizes, int n) {
+    if (n <= 0) return true;
+    if (hipSetDevice(device) != hipSuccess) return false;
+    for (int i = 0; i < n; ++i) {
+        if (hipMemcpyAsync(dst[i], src[i], sizes[i], hipMemcpyHostToDevice, hipStreamPerThread) != hipSuccess) {
+            hipStreamSynchronize(hipStreamPerThread);
+            fail(MOE_ERR_HIP, "batched copy %d of %d failed", i, n);
+            return false;
+        }
+    }
+    return hipStreamSynchronize(hipStreamPerThread) == hipSuccess;
+}
+
+size_t moe_expert_bytes(int H, int I, int down_type) { return (size_t)mp::expert_bytes(H, I, down_type); }
+
+int moe_synth_experts(uint64_t seed, int layer, int e0, int n, int H, int I, int down_type, float sigma,
+                      void *out_dev, size_t stride, void *stream) {
+    if (H % 256 || I % 256 || n <= 0 || !out_dev) return fail(MOE_ERR_ARG, "bad synth_experts arguments");
+    if (stride < mp::expert_bytes(H, I, down_type)) return fail(MOE_ERR_ARG, "stride below expert size");
+    HIPCHK(mp::launch_synth_experts(seed, layer, e0, n, H, I, down_type, sigma, (uint8_t *)out_dev, stride,
+                                    (hipStream_t)stream));
+    return MOE_OK;
+}
+
+int moe_synth_experts_host(uint64_t seed, int layer, int e0, int n, int H, int I, int down_type, float sigma,
+                           void *out_host, size_t stride, int n_threads) {
+    if (H % 256 || I % 256 || n <= 0 || !out_host) return fail(MOE_ERR_ARG, "bad synth_experts arguments");
+    if (stride < mp::expert_bytes(H, I, down_type)) return fail(MOE_ERR_ARG, "stride below expert size");
+    const mp::synth::ExpertShape sh{H, I, down_type};
+    const uint64_t nblk = (uint64_t)sh.n_blocks();
+    const uint64_t total = nblk * (uint64_t)n;
+    if (n_threads < 1) n_threads = 1;
+    std::vector<std::thread> th;
+    for (int t = 0; t < n_threads; ++t) {
+        th.emplace_back([=]() {
+            for (uint64_t i = (uint64_t)t; i < total; i += (uint64_t)n_threads) {
+                const int e = (int)(i / nblk), blk = (int)(i % nblk);
+                mp::synth::expert_block(seed, layer, e0 + e, sh, blk, sigma,
+                                        (uint8_t *)out_host + (uint64_t)e * stride + sh.block_offset(blk));
+            }
+        });
+    }
+    for (auto &x : th) x.join();
+    return MOE_OK;
+}
+
+int moe_synth_vec(uint64_t seed, int kind, int a0, int na, int b0, int nb, int n, float sigma, float *out_dev,
+                  void *stream) {
+    if (na <= 0 || nb <= 0 || n <= 0 || !out_dev) return fail(MOE_ERR_ARG, "bad synth_vec arguments");
+    HIPCHK(mp::launch_synth_vec(seed, kind, a0, na, b0, nb, n, sigma, out_dev, (hipStream_t)stream));
+    return MOE_OK;
+}
+
+int moe_synth_vec_host(uint64_t seed, int kind, int a0, int na, int b0, int nb, int n, float sigma, float *out) {
+    if (na <= 0 || nb <= 0 || n <= 0 || !out) return fail(MOE_ERR_ARG, "bad synth_vec arguments");
+    size_t t = 0;
+    for (int a = 0; a < na; ++a)
+        for (int b = 0; b < nb; ++b)
+            for (int i = 0; i < n; ++i) out[t++] = mp::synth::vec_value(seed, kind, a0 + a, b0 + b, i, sigma);
+    return MOE_OK;
+}
+
+size_t moe_route_workspace_bytes(int E, int n_tok) { return route_ws_bytes(E, n_tok); }
+size_t moe_experts_workspace_bytes(int I, int K) { return exp_ws_bytes(I, K); }
+
+int moe_route(const moe_route_desc *d, void *stream) {
+    if (!d || !d->W || !d->x || !d->ids || !d->w || !d->slots || !d->q8x || !d->workspace)
+        return fail(MOE_ERR_ARG, "moe_route: null argument");
+    int r = check_shape(d->E, d->H, 0, d->K);
+    if (r != MOE_OK) return r;
+    if (d->n_tok < 1 || d->n_tok > 65535) return fail(MOE_ERR_ARG, "n_tok %d out of range", d->n_tok);
+    return run_route(d, (hipStream_t)stream);
+}
+
+int moe_experts(const moe_experts_desc *d, void *stream) {
+    if (!d || !d->ids || !d->slots || !d->w || !d->q8x || !d->out || !d->workspace)
+        return fail(MOE_ERR_ARG, "moe_experts: null argument");
+    int r = check_shape(64, d->H, d->I, d->K);
+    if (r != MOE_OK) return r;
+    if (d->I == 0) return fail(MOE_ERR_ARG, "intermediate size 0");
+    if (d->down_type != MOE_TYPE_Q4K && d->down_type != MOE_TYPE_Q6K)
+        return fail(MOE_ERR_ARG, "down type %d unsupported", d->down_type);
+    if (!d->host_store && !d->slot_pool) return fail(MOE_ERR_ARG, "no weights");
+    if (d->expert_bytes != mp::expert_bytes(d->H, d->I, d->down_type))
+        return fail(MOE_ERR_ARG, "expert_bytes %llu does not match the shape", (unsigned long long)d->expert_bytes);
+    if (d->slot_pool && (d->slot_bytes < d->expert_bytes || d->slot_bytes % 16))
+        return fail(MOE_ERR_ARG, "slot_bytes must be >= expert_bytes and a multiple of 16");
+    if (((uintptr_t)d->slot_pool | (uintptr_t)d->host_store | (uintptr_t)d->q8x) % 16)
+        return fail(MOE_ERR_ARG, "weights and activations must be 16-byte aligned");
+    // a kernel read of unmapped memory faults the GPU: refuse anything the
+    // runtime does not know as device memory or device-mapped pinned memory
+    for (const void *p : {(const void *)d->slot_pool, (const void *)d->host_store}) {
+        if (!p) continue;
+        hipPointerAttribute_t at{};
+        if (hipPointerGetAttributes(&at, p) != hipSuccess || (at.type != hipMemoryTypeDevice &&
+                                                              at.type != hipMemoryTypeHost &&
+                                                              at.type != hipMemoryTypeUnified))
+            return fail(MOE_ERR_ARG, "moe_experts: %p is not device memory or mapped pinned memory", p);
+        if (at.type == hipMemoryTypeHost && at.devicePointer != p)
+            return fail(MOE_ERR_ARG, "moe_experts: pass the device address of pinned memory (moe_host_device_ptr)");
+    }
+    return run_experts(d, (hipStream_t)stream);
+}
+
+int moe_cache_create(const moe_cache_config *cfg, moe_cache **out) {
+    if (!cfg || !out) return fail(MOE_ERR_ARG, "null argument");
+    *out = nullptr;
+    int r = check_shape(cfg->n_experts, cfg->hidden, cfg->intermediate, cfg->n_expert_used);
+    if (r != MOE_OK) return r;
+    if (cfg->n_layers <= 0 || cfg->n_layers > 4096) return fail(MOE_ERR_ARG, "n_layers %d", cfg->n_layers);
+    if (cfg->intermediate == 0) return fail(MOE_ERR_ARG, "intermediate size 0");
+    moe_cache *c = new moe_cache();
+    c->cfg = *cfg;
+    if (c->cfg.max_inserts <= 0) c->cfg.max_inserts = 2;
+    if (c->cfg.admit_window <= 0) c->cfg.admit_window = 8;
+    if (c->cfg.admit_half <= 0) c->cfg.admit_half = 64;
+    if (c->cfg.cache_prior < 0) c->cfg.cache_prior = 0;
+    c->cfg.slot_profile = nullptr;
+    c->cfg.down_type = nullptr;
+    c->H = cfg->hidden;
+    c->I = cfg->intermediate;
+    c->E = cfg->n_experts;
+    c->K = cfg->n_expert_used;
+    const int NL = cfg->n_layers, E = c->E;
+    auto bail = [&](int code) { free_cache(c); return code; };
+    c->host_only = cfg->device < 0;
+    if (!c->host_only && hipSetDevice(cfg->device) != hipSuccess)
+        return bail(fail(MOE_ERR_HIP, "hipSetDevice(%d)", cfg->device));
+
+    c->L.resize(NL);
+    size_t pool_total = 0;
+    for (int l = 0; l < NL; ++l) {
+        Layer &ls = c->L[l];
+        ls.il = l;
+        ls.E = E;
+        ls.S = cfg->slot_profile ? cfg->slot_profile[l] : cfg->n_slots;
+        if (ls.S <= 0 || ls.S > 4096) return bail(fail(MOE_ERR_ARG, "layer %d: %d slots", l, ls.S));
+        ls.down_type = cfg->down_type ? cfg->down_type[l] : MOE_TYPE_Q4K;
+        if (ls.down_type != MOE_TYPE_Q4K && ls.down_type != MOE_TYPE_Q6K)
+            return bail(fail(MOE_ERR_ARG, "layer %d: down type %d", l, ls.down_type));
+        ls.expert_bytes = mp::expert_bytes(c->H, c->I, ls.down_type);
+        ls.slot_bytes = align_up(ls.expert_bytes, 256);
+        pool_total += (size_t)ls.S * ls.slot_bytes;
+        ls.slot_expert.assign(ls.S, -1);
+        ls.expert_slot.assign(E, -1);
+        ls.slot_last_use.assign(ls.S, 0);
+        ls.slot_protect.assign(ls.S, 0);
+        ls.slot_in_flight.assign(ls.S, 0);
+        ls.free_slots.resize(ls.S);
+        for (int s = 0; s < ls.S; ++s) ls.free_slots[s] = ls.S - 1 - s;
+        if (cfg->admit_mode == MOE_ADMIT_HEAT) ls.heat.assign(E, 0.0f);
+        if (cfg->admit_mode == MOE_ADMIT_WINDOW) {
+            ls.miss_last.assign(E, U64MAX);
+            ls.miss_prev.assign(E, U64MAX);
+        }
+    }
+    const size_t nt = (size_t)NL * E;
+    if (c->host_only) {
+        c->h_tbl = (int32_t *)malloc(nt * 4);
+        c->h_prior = c->cfg.cache_prior > 0 ? (float *)calloc(nt, 4) : nullptr;
+        if (!c->h_tbl || (c->cfg.cache_prior > 0 && !c->h_prior)) return bail(fail(MOE_ERR_NOMEM, "tables"));
+        for (int l = 0; l < NL; ++l)
+            for (int e = 0; e < E; ++e) c->h_tbl[(size_t)l * E + e] = c->L[l].S;
+        *out = c;
+        return MOE_OK;
+    }
+    if (hipMalloc(&c->pool_base, pool_total) != hipSuccess)
+        return bail(fail(MOE_ERR_NOMEM, "slot pool of %zu bytes", pool_total));
+    size_t off = 0;
+    for (Layer &ls : c->L) {
+        ls.pool = c->pool_base + off;
+        off += (size_t)ls.S * ls.slot_bytes;
+    }
+    if (hipMalloc(&c->d_tbl, nt * 4) != hipSuccess || hipHostMalloc(&c->h_tbl, nt * 4, 0) != hipSuccess)
+        return bail(fail(MOE_ERR_NOMEM, "tables"));
+    for (int l = 0; l < NL; ++l)
+        for (int e = 0; e < E; ++e) c->h_tbl[(size_t)l * E + e] = c->L[l].S;
+    if (c->cfg.cache_prior > 0) {
+        if (hipMalloc(&c->d_prior, nt * 4) != hipSuccess || hipHostMalloc(&c->h_prior, nt * 4, 0) != hipSuccess)
+            return bail(fail(MOE_ERR_NOMEM, "prior tables"));
+        memset(c->h_prior, 0, nt * 4);
+    }
+    if (hipMemcpy(c->d_tbl, c->h_tbl, nt * 4, hipMemcpyHostToDevice) != hipSuccess ||
+        (c->d_prior && hipMemcpy(c->d_prior, c->h_prior, nt * 4, hipMemcpyHostToDevice) != hipSuccess))
+        return bail(fail(MOE_ERR_HIP, "initial table write"));
+    const size_t rws = route_ws_bytes(E, 1), ews = exp_ws_bytes(c->I, c->K);
+    if (hipMalloc(&c->route_ws, rws) != hipSuccess || hipMalloc(&c->exp_ws, ews) != hipSuccess ||
+        hipMalloc(&c->d_ids, (size_t)NL * c->K * 4) != hipSuccess ||
+        hipMalloc(&c->d_slots, (size_t)NL * c->K * 4) != hipSuccess ||
+        hipMalloc(&c->d_w, (size_t)NL * c->K * 4) != hipSuccess ||
+        hipMalloc(&c->d_q8x, (size_t)(c->H / 256) * mp::Q8K_BYTES + 256) != hipSuccess ||
+        hipHostMalloc(&c->h_ids, (size_t)NL * c->K * 4, 0) != hipSuccess)
+        return bail(fail(MOE_ERR_NOMEM, "decode scratch"));
+    if (hipMemset(c->route_ws, 0, rws) != hipSuccess || hipMemset(c->exp_ws, 0, ews) != hipSuccess)
+        return bail(fail(MOE_ERR_HIP, "scratch clear"));
+    if (hipStreamCreateWithFlags(&c->up_stream, hipStreamNonBlocking) != hipSuccess ||
+        hipStreamCreateWithFlags(&c->tbl_stream, hipStreamNonBlocking) != hipSuccess ||
+        hipEventCreateWithFlags(&c->up_mark, hipEventDisableTiming) != hipSuccess)
+        return bail(fail(MOE_ERR_HIP, "streams"));
+    *out = c;
+    return MOE_OK;
+}
+
+int moe_cache_destroy(moe_cache *c) {
+    free_cache(c);
+    return MOE_OK;
+}
+
+int moe_cache_set_host_store(moe_cache *c, int layer, const void *experts, size_t expert_bytes) {
+    if (!c || layer < 0 || layer >= (int)c->L.size() || !experts) return fail(MOE_ERR_ARG, "bad arguments");
+    if (c->host_only) return fail(MOE_ERR_STATE, "host-only cache (device < 0) holds no weights");
+    Layer &ls = c->L[layer];
+    if (expert_bytes != ls.expert_bytes)
+        return fail(MOE_ERR_ARG, "layer %d expects %llu bytes per expert, got %zu", layer,
+                    (unsigned long long)ls.expert_bytes, expert_bytes);
+    void *dev = nullptr;
+    HIPCHK(hipHostGetDevicePointer(&dev, const_cast<void *>(experts), 0));
+    if (((uintptr_t)dev | (uintptr_t)experts) % 16) return fail(MOE_ERR_ARG, "host store must be 16-byte aligned");
+    ls.store_host = (const uint8_t *)experts;
+    ls.store_dev = (const uint8_t *)dev;
+    return MOE_OK;
+}
+
+int moe_cache_set_router(moe_cache *c, int layer, const float *W_dev) {
+    if (!c || layer < 0 || layer >= (int)c->L.size() || !W_dev) return fail(MOE_ERR_ARG, "bad arguments");
+    if ((uintptr_t)W_dev % 16) return fail(MOE_ERR_ARG, "router must be 16-byte aligned");
+    c->L[layer].router = W_dev;
+    return MOE_OK;
+}
+
+int moe_cache_lookup(moe_cache *c, int layer, moe_layer_view *out) {
+    if (!c || !out || layer < 0 || layer >= (int)c->L.size()) return fail(MOE_ERR_ARG, "bad arguments");
+    const Layer &ls = c->L[layer];
+    out->il = ls.il;
+    out->n_slots = ls.S;
+    out->n_experts = ls.E;
+    out->down_type = ls.down_type;
+    out->slot_bytes = ls.slot_bytes;
+    out->expert_bytes = ls.expert_bytes;
+    out->slot_pool = ls.pool;
+    out->dev_table = c->d_tbl + (size_t)layer * c->E;
+    out->prior = c->d_prior ? c->d_prior + (size_t)layer * c->E : nullptr;
+    out->host_store = ls.store_host;
+    out->router = ls.router;
+    return MOE_OK;
+}
+
+int moe_cache_trace_open(moe_cache *c, const char *route_path, const char *map_path) {
+    if (!c) return fail(MOE_ERR_ARG, "null cache");
+    if (route_path) {
+        c->route = fopen(route_path, "w");
+        if (!c->route) return fail(MOE_ERR_IO, "cannot open %s", route_path);
+    }
+    if (map_path) {
+        c->map = fopen(map_path, "w");
+        if (!c->map) return fail(MOE_ERR_IO, "cannot open %s", map_path);
+        fprintf(c->map, "moe-map 1 %zu\n", c->L.size());
+        for (const Layer &ls : c->L) fprintf(c->map, "layer %d %d %d\n", ls.il, ls.S, ls.E);
+        map_frame(c);
+    }
+    return MOE_OK;
+}
+
+int moe_cache_observe(moe_cache *c, int layer, const int32_t *ids, int n_ids, int n_tok) {
+    if (!c || !ids || layer < 0 || layer >= (int)c->L.size() || n_ids <= 0 || n_tok <= 0)
+        return fail(MOE_ERR_ARG, "bad arguments");
+    return cache_observe(c, layer, ids, n_ids, n_tok);
+}
+
+int moe_cache_step(moe_cache *c) {
+    if (!c) return fail(MOE_ERR_ARG, "null cache");
+    return cache_step(c);
+}
+
+int moe_cache_requires_sync(const moe_cache *c) { return c && c->cfg.publish == MOE_PUBLISH_SORTED ? 1 : 0; }
+
+int moe_cache_frame(moe_cache *c, int layer, int32_t *out) {
+    if (!c || !out || layer < 0 || layer >= (int)c->L.size()) return fail(MOE_ERR_ARG, "bad arguments");
+    const Layer &ls = c->L[layer];
+    for (int s = 0; s < ls.S; ++s) out[s] = -1;
+    for (int e = 0; e < ls.E; ++e)
+        if (ls.expert_slot[e] >= 0) out[ls.expert_slot[e]] = e;
+    return MOE_OK;
+}
+
+int moe_cache_table(moe_cache *c, int layer, int32_t *tbl, float *prior) {
+    if (!c || layer < 0 || layer >= (int)c->L.size()) return fail(MOE_ERR_ARG, "bad arguments");
+    if (tbl) memcpy(tbl, c->h_tbl + (size_t)layer * c->E, (size_t)c->E * 4);
+    if (prior) {
+        if (c->h_prior) memcpy(prior, c->h_prior + (size_t)layer * c->E, (size_t)c->E * 4);
+        else memset(prior, 0, (size_t)c->E * 4);
+    }
+    return MOE_OK;
+}
+
+int moe_cache_stats_get(moe_cache *c, moe_cache_stats *s) {
+    if (!c || !s) return fail(MOE_ERR_ARG, "bad arguments");
+    memset(s, 0, sizeof *s);
+    s->n_steps = c->n_steps;
+    s->clock = c->clock;
+    for (const Layer &ls : c->L) { s->n_hit += ls.n_hit; s->n_miss += ls.n_miss; }
+    s->n_uploads = c->n_uploads;
+    s->n_scheduled = c->n_scheduled;
+    s->n_copied = c->n_copied;
+    s->n_published = c->n_published;
+    s->n_admit_ok = c->n_admit_ok;
+    s->n_admit_denied = c->n_admit_denied;
+    s->n_table_flushes = c->n_table_flushes;
+    s->bytes_uploaded = c->bytes_uploaded;
+    s->publication_wait_us = c->wait_us;
+    return MOE_OK;
+}
+
+int moe_cache_sync(moe_cache *c) {
+    if (!c) return fail(MOE_ERR_ARG, "null cache");
+    if (c->host_only) return MOE_OK;
+    HIPCHK(hipStreamSynchronize(c->up_stream));
+    return MOE_OK;
+}
+
+int moe_decode_layer(moe_cache *c, int layer, const float *x, const float *bias, float *out, int32_t *ids_dev,
+                     float *w_dev, void *stream) {
+    if (!c || !x || !out || layer < 0 || layer >= (int)c->L.size()) return fail(MOE_ERR_ARG, "bad arguments");
+    if (c->host_only) return fail(MOE_ERR_STATE, "host-only cache (device < 0) cannot decode");
+    const Layer &ls = c->L[layer];
+    if (!ls.router || !ls.store_dev) return fail(MOE_ERR_STATE, "layer %d: router or host store missing", layer);
+    hipStream_t st = (hipStream_t)stream;
+    int32_t *ids = ids_dev ? ids_dev : c->d_ids + (size_t)layer * c->K;
+    float *w = w_dev ? w_dev : c->d_w + (size_t)layer * c->K;
+    int32_t *slots = c->d_slots + (size_t)layer * c->K;
+    moe_route_desc rd{};
+    rd.W = ls.router; rd.x = x; rd.bias = bias;
+    rd.prior = c->d_prior ? c->d_prior + (size_t)layer * c->E : nullptr;
+    rd.table = c->d_tbl + (size_t)layer * c->E;
+    rd.dummy = ls.S;
+    rd.E = c->E; rd.H = c->H; rd.K = c->K; rd.n_tok = 1;
+    rd.ids = ids; rd.w = w; rd.slots = slots; rd.probs = nullptr; rd.q8x = c->d_q8x;
+    rd.workspace = c->route_ws;
+    int r = run_route(&rd, st);
+    if (r != MOE_OK) return r;
+    moe_experts_desc ed{};
+    ed.ids = ids; ed.slots = slots; ed.w = w;
+    ed.slot_pool = ls.pool; ed.slot_bytes = ls.slot_bytes; ed.n_slots = ls.S;
+    ed.host_store = ls.store_dev; ed.expert_bytes = ls.expert_bytes; ed.n_experts = c->E;
+    ed.q8x = c->d_q8x; ed.out = out; ed.accumulate = 0;
+    ed.H = c->H; ed.I = c->I; ed.K = c->K; ed.down_type = ls.down_type;
+    ed.workspace = c->exp_ws;
+    return run_experts(&ed, st);
+}
+
+int moe_decode_token(moe_cache *c, const float *x, const float *bias, float *out, int32_t *ids_host, void *stream) {
+    if (!c || !x || !out) return fail(MOE_ERR_ARG, "bad arguments");
+    if (c->host_only) return fail(MOE_ERR_STATE, "host-only cache (device < 0) cannot decode");
+    hipStream_t st = (hipStream_t)stream;
+    const int NL = (int)c->L.size();
+    for (int l = 0; l < NL; ++l) {
+        const int r = moe_decode_layer(c, l, x + (size_t)l * c->H, bias ? bias + (size_t)l * c->E : nullptr,
+                                       out + (size_t)l * c->H, nullptr, nullptr, stream);
+        if (r != MOE_OK) return r;
+    }
+    HIPCHK(hipMemcpyAsync(c->h_ids, c->d_ids, (size_t)NL * c->K * 4, hipMemcpyDeviceToHost, st));
+    HIPCHK(hipStreamSynchronize(st));
+    for (int l = 0; l < NL; ++l) {
+        const int r = cache_observe(c, l, c->h_ids + (size_t)l * c->K, c->K, 1);
+        if (r != MOE_OK) return r;
+    }
+    if (ids_host) memcpy(ids_host, c->h_ids, (size_t)NL * c->K * 4);
+    return cache_step(c);
+}
+
+// ---- slab pool --------------------------------------------------------------
+int moe_pool_create(int n_layers, int capacity, size_t bytes_per_expert, int device, moe_pool **out) {
+    if (!out || n_layers <= 0 || capacity <= 0 || bytes_per_expert == 0) return fail(MOE_ERR_ARG, "bad arguments");
+    *out = nullptr;
+    moe_pool *p = new moe_pool();
+    p->n_layers = n_layers;
+    p->capacity = capacity;
+    p->bytes = align_up(bytes_per_expert, 256);
+    p->device = device;
+    auto bail = [&](int code) {
+        if (p->base) hipFree(p->base);
+        for (hipEvent_t e : p->ev) if (e) hipEventDestroy(e);
+        if (p->stream) hipStreamDestroy(p->stream);
+        delete p;
+        return code;
+    };
+    if (hipSetDevice(device) != hipSuccess) return bail(fail(MOE_ERR_HIP, "hipSetDevice"));
+    if (hipMalloc(&p->base, p->bytes * (size_t)n_layers * capacity) != hipSuccess)
+        return bail(fail(MOE_ERR_NOMEM, "pool of %zu bytes", p->bytes * (size_t)n_layers * capacity));
+    if (hipStreamCreateWithFlags(&p->stream, hipStreamNonBlocking) != hipSuccess)
+        return bail(fail(MOE_ERR_HIP, "stream"));
+    p->ev.assign((size_t)n_layers * capacity, nullptr);
+    p->armed.assign((size_t)n_layers * capacity, 0);
+    for (auto &e : p->ev)
+        if (hipEventCreateWithFlags(&e, hipEventDisableTiming) != hipSuccess) return bail(fail(MOE_ERR_HIP, "events"));
+    *out = p;
+    return MOE_OK;
+}
+
+int moe_pool_destroy(moe_pool *p) {
+    if (!p) return MOE_OK;
+    hipStreamSynchronize(p->stream);
+    for (hipEvent_t e : p->ev) hipEventDestroy(e);
+    hipStreamDestroy(p->stream);
+    hipFree(p->base);
+    delete p;
+    return MOE_OK;
+}
+
+int moe_pool_copy(moe_pool *p, int layer, int slot, const void *src_host, size_t bytes) {
+    if (!p || layer < 0 || layer >= p->n_layers || slot < 0 || slot >= p->capacity || !src_host || bytes > p->bytes)
+        return fail(MOE_ERR_ARG, "bad arguments");
+    const size_t i = (size_t)layer * p->capacity + slot;
+    HIPCHK(hipMemcpyAsync(p->base + i * p->bytes, src_host, bytes, hipMemcpyHostToDevice, p->stream));
+    HIPCHK(hipEventRecord(p->ev[i], p->stream));
+    p->armed[i] = 1;
+    return MOE_OK;
+}
+
+int moe_pool_ready(moe_pool *p, int layer, int slot) {
+    if (!p || layer < 0 || layer >= p->n_layers || slot < 0 || slot >= p->capacity)
+        return fail(MOE_ERR_ARG, "bad arguments");
+    const size_t i = (size_t)layer * p->capacity + slot;
+    if (!p->armed[i]) return 1;
+    const hipError_t q = hipEventQuery(p->ev[i]);
+    if (q == hipSuccess) return 1;
+    if (q == hipErrorNotReady) return 0;
+    return fail(MOE_ERR_HIP, "hipEventQuery: %s", hipGetErrorString(q));
+}
+
+int moe_pool_sync(moe_pool *p) {
+    if (!p) return fail(MOE_ERR_ARG, "null pool");
+    HIPCHK(hipStreamSynchronize(p->stream));
+    return MOE_OK;
+}
+
+void *moe_pool_slot_ptr(moe_pool *p, int layer, int slot) {
+    if (!p || layer < 0 || layer >= p->n_layers || slot < 0 || slot >= p->capacity) return nullptr;
+    return p->base + ((size_t)layer * p->capacity + slot) * p->bytes;
+}
+
+}  // extern "C"

@@ -1,0 +1,135 @@
+"""ctypes binding of libmoeprefetch.so (include/moe_prefetch.h).
+
+The library is built in-tree by moe-prefetch_amd/build.py; importing this
+module never falls back to anything else: a missing library raises.
+"""
+import ctypes
+import os
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libmoeprefetch.so")
+
+MOE_OK = 0
+TYPE_Q4K, TYPE_Q6K = 12, 14
+ADMIT = {"off": 0, "heat": 1, "window": 2}
+PUBLISH = {"fifo": 0, "sorted": 1, "live": 2}
+
+P = ctypes.c_void_p
+I32 = ctypes.c_int32
+U64 = ctypes.c_uint64
+F32 = ctypes.c_float
+SZ = ctypes.c_size_t
+
+
+class MoeError(RuntimeError):
+    pass
+
+
+class RouteDesc(ctypes.Structure):
+    _fields_ = [("W", P), ("x", P), ("bias", P), ("prior", P), ("table", P), ("dummy", I32),
+                ("E", I32), ("H", I32), ("K", I32), ("n_tok", I32),
+                ("ids", P), ("w", P), ("slots", P), ("probs", P), ("q8x", P), ("workspace", P)]
+
+
+class ExpertsDesc(ctypes.Structure):
+    _fields_ = [("ids", P), ("slots", P), ("w", P), ("slot_pool", P), ("slot_bytes", U64),
+                ("n_slots", I32), ("host_store", P), ("expert_bytes", U64), ("n_experts", I32),
+                ("q8x", P), ("out", P),
+                ("accumulate", I32), ("H", I32), ("I", I32), ("K", I32), ("down_type", I32),
+                ("workspace", P)]
+
+
+class CacheConfig(ctypes.Structure):
+    _fields_ = [("n_layers", I32), ("n_experts", I32), ("n_expert_used", I32),
+                ("hidden", I32), ("intermediate", I32), ("n_slots", I32),
+                ("slot_profile", P), ("down_type", P), ("max_inserts", I32), ("admit_mode", I32),
+                ("admit_window", I32), ("admit_half", I32), ("admit_floor", F32),
+                ("batch_tables", I32), ("early_issue", I32), ("cache_prior", F32),
+                ("publish", I32), ("device", I32)]
+
+
+class CacheStats(ctypes.Structure):
+    _fields_ = [(n, U64) for n in ("n_steps", "clock", "n_hit", "n_miss", "n_uploads", "n_scheduled",
+                                   "n_copied", "n_published", "n_admit_ok", "n_admit_denied",
+                                   "n_table_flushes", "bytes_uploaded")] + \
+               [("publication_wait_us", ctypes.c_double)]
+
+
+class LayerView(ctypes.Structure):
+    _fields_ = [("il", I32), ("n_slots", I32), ("n_experts", I32), ("down_type", I32),
+                ("slot_bytes", U64), ("expert_bytes", U64), ("slot_pool", P), ("dev_table", P),
+                ("prior", P), ("host_store", P), ("router", P)]
+
+
+# name -> (restype, argtypes); mirrors include/moe_prefetch.h one to one
+SIGNATURES = {
+    "moe_last_error": (ctypes.c_char_p, []),
+    "moe_abi_version": (ctypes.c_int, []),
+    "moe_host_alloc": (P, [SZ]),
+    "moe_host_free": (ctypes.c_int, [P]),
+    "moe_host_device_ptr": (P, [P]),
+    "moe_device_alloc": (P, [SZ]),
+    "moe_device_free": (ctypes.c_int, [P]),
+    "moe_device_synchronize": (ctypes.c_int, []),
+    "moe_memcpy": (ctypes.c_int, [P, P, SZ]),
+    "moe_memcpy_h2d_batch": (ctypes.c_bool, [ctypes.c_int, P, P, P, ctypes.c_int]),
+    "moe_synth_experts": (ctypes.c_int, [U64, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                         ctypes.c_int, ctypes.c_int, F32, P, SZ, P]),
+    "moe_synth_experts_host": (ctypes.c_int, [U64, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                              ctypes.c_int, ctypes.c_int, F32, P, SZ, ctypes.c_int]),
+    "moe_synth_vec": (ctypes.c_int, [U64, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                     ctypes.c_int, ctypes.c_int, F32, P, P]),
+    "moe_synth_vec_host": (ctypes.c_int, [U64, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                          ctypes.c_int, ctypes.c_int, F32, P]),
+    "moe_expert_bytes": (SZ, [ctypes.c_int, ctypes.c_int, ctypes.c_int]),
+    "moe_route_workspace_bytes": (SZ, [ctypes.c_int, ctypes.c_int]),
+    "moe_experts_workspace_bytes": (SZ, [ctypes.c_int, ctypes.c_int]),
+    "moe_route": (ctypes.c_int, [ctypes.POINTER(RouteDesc), P]),
+    "moe_experts": (ctypes.c_int, [ctypes.POINTER(ExpertsDesc), P]),
+    "moe_cache_create": (ctypes.c_int, [ctypes.POINTER(CacheConfig), ctypes.POINTER(P)]),
+    "moe_cache_destroy": (ctypes.c_int, [P]),
+    "moe_cache_set_host_store": (ctypes.c_int, [P, ctypes.c_int, P, SZ]),
+    "moe_cache_set_router": (ctypes.c_int, [P, ctypes.c_int, P]),
+    "moe_cache_lookup": (ctypes.c_int, [P, ctypes.c_int, ctypes.POINTER(LayerView)]),
+    "moe_cache_trace_open": (ctypes.c_int, [P, ctypes.c_char_p, ctypes.c_char_p]),
+    "moe_cache_observe": (ctypes.c_int, [P, ctypes.c_int, P, ctypes.c_int, ctypes.c_int]),
+    "moe_cache_step": (ctypes.c_int, [P]),
+    "moe_cache_requires_sync": (ctypes.c_int, [P]),
+    "moe_cache_frame": (ctypes.c_int, [P, ctypes.c_int, P]),
+    "moe_cache_table": (ctypes.c_int, [P, ctypes.c_int, P, P]),
+    "moe_cache_stats_get": (ctypes.c_int, [P, ctypes.POINTER(CacheStats)]),
+    "moe_cache_sync": (ctypes.c_int, [P]),
+    "moe_decode_layer": (ctypes.c_int, [P, ctypes.c_int, P, P, P, P, P, P]),
+    "moe_decode_token": (ctypes.c_int, [P, P, P, P, P, P]),
+    "moe_pool_create": (ctypes.c_int, [ctypes.c_int, ctypes.c_int, SZ, ctypes.c_int, ctypes.POINTER(P)]),
+    "moe_pool_destroy": (ctypes.c_int, [P]),
+    "moe_pool_copy": (ctypes.c_int, [P, ctypes.c_int, ctypes.c_int, P, SZ]),
+    "moe_pool_ready": (ctypes.c_int, [P, ctypes.c_int, ctypes.c_int]),
+    "moe_pool_sync": (ctypes.c_int, [P]),
+    "moe_pool_slot_ptr": (P, [P, ctypes.c_int, ctypes.c_int]),
+}
+
+_lib = None
+
+
+def lib():
+    """Load the in-tree library (raises if it has not been built)."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise MoeError(f"{LIB_PATH} is missing: run `python moe-prefetch_amd/build.py` "
+                           "(or __graft_entry__.build()) first")
+        L = ctypes.CDLL(LIB_PATH)
+        for name, (res, args) in SIGNATURES.items():
+            f = getattr(L, name)
+            f.restype = res
+            f.argtypes = args
+        _lib = L
+    return _lib
+
+
+def check(rc, what=""):
+    if rc != MOE_OK:
+        msg = lib().moe_last_error().decode(errors="replace")
+        raise MoeError(f"{what}: status {rc}: {msg}")
+    return rc

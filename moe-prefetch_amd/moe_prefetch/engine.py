@@ -1,0 +1,173 @@
+"""The MoE decode engine: slot cache + routed expert kernels, over the C ABI.
+
+`MoeCache` is the llama-moecache runtime of the reference (patches 0006-0008:
+llama_moe_cache_init / lookup / step, the observe callback, map and route
+traces) rebuilt around an HBM slot pool on one MI355X.  Knob names and
+meanings are the reference's: `n_slots` is --moe-expert-cache, `slot_profile`
+LLAMA_MOE_SLOT_PROFILE, `max_inserts` --moe-expert-cache-inserts, `admit`
+LLAMA_MOE_ADMIT (off | heat | window), `admit_window` / `admit_half` /
+`admit_floor` LLAMA_MOE_ADMIT_*, `batch_tables` LLAMA_MOE_BATCH_TABLES,
+`early_issue` LLAMA_MOE_EARLY_ISSUE, `cache_prior` LLAMA_MOE_CACHE_PRIOR (the
+delta added to resident experts' selection probabilities), `deterministic`
+LLAMA_MOE_DETERMINISTIC.  `MoeCache.from_env()` reads those variables.
+
+`device=-1` builds the state machine alone (no GPU, no weights, every upload
+completes at once) -- the CPU-testable core.
+"""
+import ctypes
+import os
+
+import numpy as np
+
+from . import _lib
+from ._lib import check, lib
+
+
+def _ptr(t):
+    """Raw address of a torch tensor, numpy array or int (None -> NULL)."""
+    if t is None:
+        return None
+    if isinstance(t, int):
+        return t
+    if hasattr(t, "data_ptr"):
+        return t.data_ptr()
+    return t.ctypes.data
+
+
+def parse_slot_profile(spec, n_layers, default):
+    """"il:slots,il:slots,..." (patches/0006:447-480) -> per-layer slot counts."""
+    slots = [default] * n_layers
+    if not spec:
+        return slots
+    for part in spec.split(","):
+        il, n = part.split(":")
+        il, n = int(il), int(n)
+        if 0 <= il < n_layers and n > 0:
+            slots[il] = n
+    return slots
+
+
+class MoeCache:
+    def __init__(self, n_layers, n_experts=128, n_expert_used=8, hidden=2048, intermediate=768,
+                 n_slots=56, slot_profile=None, down_types=None, max_inserts=2, admit="off",
+                 admit_window=8, admit_half=64, admit_floor=1.0, batch_tables=False,
+                 early_issue=False, cache_prior=0.0, deterministic=False, publish=None, device=0):
+        if isinstance(slot_profile, str):
+            slot_profile = parse_slot_profile(slot_profile, n_layers, n_slots)
+        if isinstance(admit, str):
+            if admit not in _lib.ADMIT:
+                raise ValueError(f"admit must be off | heat | window, not {admit!r}")
+            admit = _lib.ADMIT[admit]
+        if publish is None:
+            publish = "sorted" if deterministic else "fifo"
+        self.n_layers, self.n_experts, self.K = n_layers, n_experts, n_expert_used
+        self.H, self.I = hidden, intermediate
+        self.slots = list(slot_profile) if slot_profile is not None else [n_slots] * n_layers
+        self.down_types = list(down_types) if down_types is not None else [_lib.TYPE_Q4K] * n_layers
+        self._slots_arr = np.asarray(self.slots, np.int32)
+        self._dt_arr = np.asarray(self.down_types, np.int32)
+        cfg = _lib.CacheConfig(n_layers, n_experts, n_expert_used, hidden, intermediate, n_slots,
+                               self._slots_arr.ctypes.data, self._dt_arr.ctypes.data, max_inserts, admit,
+                               admit_window, admit_half, admit_floor, int(batch_tables),
+                               int(early_issue), float(cache_prior), _lib.PUBLISH[publish], device)
+        h = ctypes.c_void_p()
+        check(lib().moe_cache_create(ctypes.byref(cfg), ctypes.byref(h)), "moe_cache_create")
+        self.h = h.value
+        self.device = device
+        self.cache_prior = cache_prior
+
+    @classmethod
+    def from_env(cls, n_layers, n_slots, max_inserts=2, env=None, **shape):
+        """Knobs from the reference's environment variables (patches 0006:501-539, 0007:492-506)."""
+        env = os.environ if env is None else env
+        g = env.get
+        admit = g("LLAMA_MOE_ADMIT", "off") or "off"
+        if admit == "0":
+            admit = "off"
+        return cls(n_layers, n_slots=n_slots, max_inserts=max_inserts,
+                   slot_profile=parse_slot_profile(g("LLAMA_MOE_SLOT_PROFILE"), n_layers, n_slots),
+                   admit=admit,
+                   admit_window=max(1, int(g("LLAMA_MOE_ADMIT_WINDOW", "8"))),
+                   admit_half=max(1, int(g("LLAMA_MOE_ADMIT_HALF", "64"))),
+                   admit_floor=float(g("LLAMA_MOE_ADMIT_FLOOR", "1")),
+                   batch_tables=int(g("LLAMA_MOE_BATCH_TABLES", "0")) != 0,
+                   early_issue=int(g("LLAMA_MOE_EARLY_ISSUE", "0")) != 0,
+                   cache_prior=max(0.0, float(g("LLAMA_MOE_CACHE_PRIOR", "0"))),
+                   deterministic=int(g("LLAMA_MOE_DETERMINISTIC", "0")) != 0, **shape)
+
+    def close(self):
+        if getattr(self, "h", None):
+            lib().moe_cache_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        self.close()
+
+    # -- weights -----------------------------------------------------------
+    def expert_bytes(self, layer):
+        return lib().moe_expert_bytes(self.H, self.I, self.down_types[layer])
+
+    def set_host_store(self, layer, ptr):
+        check(lib().moe_cache_set_host_store(self.h, layer, _ptr(ptr), self.expert_bytes(layer)),
+              "set_host_store")
+
+    def set_router(self, layer, W):
+        check(lib().moe_cache_set_router(self.h, layer, _ptr(W)), "set_router")
+
+    def lookup(self, layer):
+        v = _lib.LayerView()
+        check(lib().moe_cache_lookup(self.h, layer, ctypes.byref(v)), "lookup")
+        return v
+
+    # -- state machine -------------------------------------------------------
+    def trace_open(self, route_path=None, map_path=None):
+        check(lib().moe_cache_trace_open(self.h, route_path.encode() if route_path else None,
+                                         map_path.encode() if map_path else None), "trace_open")
+
+    def observe(self, layer, ids, n_tok=1):
+        ids = np.ascontiguousarray(ids, np.int32)
+        check(lib().moe_cache_observe(self.h, layer, ids.ctypes.data, ids.size // n_tok, n_tok), "observe")
+
+    def step(self):
+        check(lib().moe_cache_step(self.h), "step")
+
+    def requires_sync(self):
+        return bool(lib().moe_cache_requires_sync(self.h))
+
+    def frame(self, layer):
+        out = np.empty(self.slots[layer], np.int32)
+        check(lib().moe_cache_frame(self.h, layer, out.ctypes.data), "frame")
+        return out
+
+    def table(self, layer):
+        t = np.empty(self.n_experts, np.int32)
+        p = np.empty(self.n_experts, np.float32)
+        check(lib().moe_cache_table(self.h, layer, t.ctypes.data, p.ctypes.data), "table")
+        return t, p
+
+    def stats(self):
+        s = _lib.CacheStats()
+        check(lib().moe_cache_stats_get(self.h, ctypes.byref(s)), "stats")
+        d = {n: getattr(s, n) for n, _ in _lib.CacheStats._fields_}
+        seen = d["n_hit"] + d["n_miss"]
+        d["hit_rate"] = d["n_hit"] / seen if seen else 0.0
+        steps = max(d["n_steps"], 1)
+        d["missed_per_token"] = d["n_miss"] / steps
+        d["uploaded_per_token"] = d["n_scheduled"] / steps
+        return d
+
+    def sync(self):
+        check(lib().moe_cache_sync(self.h), "sync")
+
+    # -- decode ---------------------------------------------------------------
+    def decode_layer(self, layer, x, out, bias=None, ids=None, w=None, stream=None):
+        check(lib().moe_decode_layer(self.h, layer, _ptr(x), _ptr(bias), _ptr(out), _ptr(ids), _ptr(w),
+                                     _ptr(stream)), "decode_layer")
+
+    def decode_token(self, x, out, bias=None, stream=None, ids_out=None):
+        """x [L, H] and out [L, H] on the device (bias [L, E] or None).  Returns the
+        routed ids [L, K] (host) after the step has been applied."""
+        ids = ids_out if ids_out is not None else np.empty((self.n_layers, self.K), np.int32)
+        check(lib().moe_decode_token(self.h, _ptr(x), _ptr(bias), _ptr(out), ids.ctypes.data, _ptr(stream)),
+              "decode_token")
+        return ids

@@ -1,0 +1,133 @@
+"""The product's slot-table state machine (libmoeprefetch.so, device=-1 host
+mode: no GPU, every upload completes at once) against the reference's engine
+traces and against the oracle on synthetic routing streams (CPU only)."""
+import collections
+import os
+
+import numpy as np
+import pytest
+
+import x3t
+from moe_prefetch import MoeCache
+from moe_prefetch.workload import zipf_targets
+from oracle import oracle as O
+
+
+def product_cache(slots, **kw):
+    return MoeCache(len(slots), n_experts=kw.pop("n_experts", 128), slot_profile=list(slots),
+                    device=-1, **kw)
+
+
+@pytest.mark.parametrize("i", [0, 1, 2, 3])
+def test_product_reproduces_x3t(i, tmp_path):
+    slots, experts, frames, routes = x3t.load(i)
+    layers = sorted(slots)
+    c = product_cache([slots[l] for l in layers], max_inserts=2, admit="window", admit_window=8,
+                      batch_tables=True)
+    rp, mp = str(tmp_path / "routes.txt"), str(tmp_path / "map.txt")
+    c.trace_open(rp, mp)
+    by = collections.defaultdict(list)
+    for s, il, n_ids, n_tok, pairs in routes:
+        by[s].append((il, n_tok, [e for e, _ in pairs]))
+    for s in range(max(frames)):
+        for il, n_tok, ids in by.get(s, []):
+            c.observe(il, np.array(ids, np.int32), n_tok)
+        c.step()
+    c.close()
+    # byte-identical trace files
+    assert open(rp).read() == x3t.read_text(os.path.join(x3t.GOLDEN, f"{i}.routes-record.txt.gz"))
+    assert open(mp).read() == x3t.read_text(os.path.join(x3t.GOLDEN, f"{i}.map.txt.gz"))
+
+
+KNOBS = [
+    dict(admit="off"),
+    dict(admit="window", admit_window=8),
+    dict(admit="window", admit_window=3, max_inserts=1),
+    dict(admit="heat", admit_half=16, admit_floor=1.0),
+    dict(admit="heat", admit_half=64, admit_floor=0.0, max_inserts=3),
+    dict(admit="off", early_issue=True),
+    dict(admit="window", early_issue=True),
+    dict(admit="heat", early_issue=True, admit_half=8),
+    dict(admit="window", deterministic=True),
+    dict(admit="window", cache_prior=0.01, batch_tables=True),
+]
+
+
+@pytest.mark.parametrize("knobs", KNOBS, ids=lambda k: ",".join(f"{a}={b}" for a, b in k.items()))
+def test_product_matches_oracle(knobs):
+    L, T = 6, 160
+    slots = [12, 20, 8, 16, 12, 32]
+    tg = [zipf_targets(99, l, T, s=1.0, reuse=0.5) for l in range(L)]
+    ok = dict(knobs)
+    ok["admit"] = knobs.get("admit", "off")
+    oc = O.Cache(slots, **{k: v for k, v in ok.items()})
+    pc = product_cache(slots, **knobs)
+    for t in range(T):
+        for l in range(L):
+            oc.observe(l, tg[l][t])
+            pc.observe(l, tg[l][t])
+        oc.step()
+        pc.step()
+        for l in range(L):
+            assert np.array_equal(oc.frame(l), pc.frame(l)), (t, l)
+            ot, op = oc.table(l)
+            pt, pp = pc.table(l)
+            assert np.array_equal(ot, pt) and np.array_equal(op, pp)
+    os_, ps = oc.stats(), pc.stats()
+    for k in ("n_steps", "clock", "n_hit", "n_miss", "n_uploads", "n_scheduled", "n_published",
+              "n_admit_ok", "n_admit_denied", "n_table_flushes"):
+        assert os_[k] == ps[k], k
+    assert ps["n_hit"] + ps["n_miss"] == L * T * 8
+
+
+def test_batched_tokens_observe_token_major():
+    # n_tok > 1: ids are visited token-major, one pending list, dedup across tokens
+    slots = [16]
+    oc = O.Cache(slots, admit="off")
+    pc = product_cache(slots, admit="off")
+    rng = np.random.default_rng(5)
+    for t in range(40):
+        ids = rng.integers(0, 128, size=(4, 8)).astype(np.int32)
+        oc.observe(0, ids.reshape(-1), 4)
+        pc.observe(0, ids.reshape(-1), 4)
+        oc.step()
+        pc.step()
+        assert np.array_equal(oc.frame(0), pc.frame(0))
+
+
+def test_invariants_hold():
+    L, T = 4, 300
+    slots = [8, 8, 16, 24]
+    pc = product_cache(slots, admit="window")
+    tg = [zipf_targets(7, l, T) for l in range(L)]
+    for t in range(T):
+        for l in range(L):
+            pc.observe(l, tg[l][t])
+        pc.step()
+        for l in range(L):
+            fr = pc.frame(l)
+            res = fr[fr >= 0]
+            assert len(set(res.tolist())) == len(res)           # no expert in two slots
+            tbl, _ = pc.table(l)
+            for s, e in enumerate(fr):
+                if e >= 0:
+                    assert tbl[e] == s
+            assert np.sum(tbl < slots[l]) == len(res)            # dummy for every absent expert
+    st = pc.stats()
+    assert st["n_scheduled"] <= 2 * L * T                         # <= max_inserts per layer per step
+
+
+def test_from_env_reads_reference_variables():
+    env = {"LLAMA_MOE_ADMIT": "window", "LLAMA_MOE_ADMIT_WINDOW": "5", "LLAMA_MOE_BATCH_TABLES": "1",
+           "LLAMA_MOE_CACHE_PRIOR": "0.01", "LLAMA_MOE_SLOT_PROFILE": "0:88,2:40",
+           "LLAMA_MOE_DETERMINISTIC": "1"}
+    c = MoeCache.from_env(4, 56, env=env, device=-1)
+    assert c.slots == [88, 56, 40, 56]
+    assert c.requires_sync()
+    _, prior = c.table(0)
+    assert prior.shape == (128,) and not prior.any()
+
+
+def test_bad_knob_is_loud():
+    with pytest.raises(ValueError):
+        MoeCache(2, admit="sometimes", device=-1)
