@@ -194,6 +194,26 @@ int moe_cache_table(moe_cache *c, int layer, int32_t *tbl, float *prior);  /* ho
 int moe_cache_stats_get(moe_cache *c, moe_cache_stats *out);
 int moe_cache_sync(moe_cache *c);  /* wait for every upload in flight */
 
+/* Kernel time of the decode, from HIP events recorded around each launch on
+ * the stream it runs on (off by default; set before decoding).  Experts
+ * resident in HBM slots and experts read from the pinned store run as
+ * separate launches on two streams (fork/join per layer). */
+typedef struct {
+    double route_ms;                       /* route_logits + route_select */
+    double gateup_hbm_ms, down_hbm_ms;     /* resident experts */
+    double gateup_host_ms, down_host_ms;   /* absent experts (pinned store over PCIe) */
+    uint64_t n_layers;                     /* layer decodes timed */
+    uint64_t gateup_hbm_bytes, down_hbm_bytes, gateup_host_bytes, down_host_bytes;
+} moe_kernel_times;
+int moe_cache_set_timing(moe_cache *c, int on);
+/* split: 0 one expert launch serves resident and absent experts (default);
+ * 1 resident and absent experts as separate launches on two streams, forked
+ * and joined per layer; 2 the same launches one after the other on one stream.
+ * graph: replay each token's launches as one captured HIP graph (default 1;
+ * timing mode launches eagerly).  Results agree to fp32 summation order. */
+int moe_cache_set_decode_path(moe_cache *c, int split, int graph);
+int moe_cache_kernel_times(moe_cache *c, moe_kernel_times *out);
+
 /* One layer at batch 1: route x (+bias), run the K experts, out = sum_k w_k y_k.
  * ids_dev/w_dev receive this layer's routing (dev [K]) when not NULL. */
 int moe_decode_layer(moe_cache *c, int layer, const float *x, const float *bias, float *out,

@@ -1,18 +1,20 @@
 // mp_kernels.hip -- gfx950 kernels of the batch-1 MoE decode step.
 //
-//   route_kernel    router GEMV (W_r f32 [E][H]) -> softmax -> + cache prior ->
-//                   top-k -> renormalised gate weights -> slot lookup, and the
-//                   Q8_K quantization of x the expert kernels consume.  One
-//                   wavefront per expert row; the last workgroup to finish (a
-//                   device-scope ticket, no waiting) does the softmax/top-k.
+//   route_logits    router GEMV (W_r f32 [E][H]), one wavefront per expert row
+//   route_select    softmax -> + cache prior -> top-k -> renormalised gate
+//                   weights -> slot lookup, and the Q8_K quantization of x the
+//                   expert kernels consume (one workgroup per token)
 //   gateup_kernel   for K routed experts: up/gate Q4_K rows against Q8_K(x)
 //                   with v_dot4_i32_i8, h = silu(gate) * up.  Resident experts
 //                   are read from their HBM slot, absent ones straight from the
-//                   pinned host store.  The last workgroup of each expert
-//                   quantizes that expert's h to Q8_K.
-//   down_kernel     down rows (Q4_K or Q6_K) against Q8_K(h), staged through LDS
-//                   in 16-byte aligned chunks of 8 rows (Q6_K rows are only
-//                   2-byte aligned), and the weighted combine over k in order.
+//                   pinned host store.
+//   down_kernel     Q8_K of each expert's h into LDS, down rows (Q4_K or Q6_K)
+//                   staged through LDS in 16-byte aligned chunks of 8 rows (Q6_K
+//                   rows are only 2-byte aligned), and the weighted combine over
+//                   k in order.
+// No kernel communicates across workgroups: on a multi-XCD part that needs a
+// device-scope fence (an L2 write-back and invalidate per workgroup), which
+// cost more than the kernels' own work; kernel boundaries order the phases.
 //
 // Numerics: integer dots are exact; fp32 only at the per-super-block scale and
 // across super-blocks.  The router follows the canonical order documented with
@@ -112,52 +114,51 @@ struct RouteArgs {
     uint8_t *q8x;          // [n_tok][H/256 * 292]
 };
 
-__global__ __launch_bounds__(256) void route_kernel(RouteArgs a) {
+// One wavefront per expert row: logit[e] = <W[e], x> in the canonical order
+// (lane j accumulates W[256 i + 4 j + c] * x[...] with fmaf, i then c, then a
+// butterfly over the 64 lanes), plus the steering bias when given.
+__global__ __launch_bounds__(256) void route_logits_kernel(RouteArgs a) {
     const int tok = blockIdx.y;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int e = blockIdx.x * 4 + wave;
+    if (e >= a.E) return;
     const float *x = a.x + (size_t)tok * a.H;
-    __shared__ uint32_t s_ticket;
-    __shared__ float s_lg[256];
-    __shared__ float s_p[256];
-
-    if (e < a.E) {
-        const float *w = a.W + (size_t)e * a.H;
-        float acc = 0.0f;
-        for (int i = 0; i < a.H / 256; ++i) {
-            const float4 wv = *(const float4 *)(w + 256 * i + 4 * lane);
-            const float4 xv = *(const float4 *)(x + 256 * i + 4 * lane);
-            acc = fmaf(wv.x, xv.x, acc);
-            acc = fmaf(wv.y, xv.y, acc);
-            acc = fmaf(wv.z, xv.z, acc);
-            acc = fmaf(wv.w, xv.w, acc);
-        }
-        acc = bfly_add(acc);
-        if (a.bias) acc = acc + a.bias[(size_t)tok * a.E + e];
-        if (lane == 0) a.logits[(size_t)tok * a.E + e] = acc;
+    const float *w = a.W + (size_t)e * a.H;
+    float acc = 0.0f;
+    for (int i = 0; i < a.H / 256; ++i) {
+        const float4 wv = *(const float4 *)(w + 256 * i + 4 * lane);
+        const float4 xv = *(const float4 *)(x + 256 * i + 4 * lane);
+        acc = fmaf(wv.x, xv.x, acc);
+        acc = fmaf(wv.y, xv.y, acc);
+        acc = fmaf(wv.z, xv.z, acc);
+        acc = fmaf(wv.w, xv.w, acc);
     }
-    __threadfence();
-    __syncthreads();
-    if (threadIdx.x == 0) s_ticket = atomicAdd(&a.counter[tok], 1u);
-    __syncthreads();
-    if (s_ticket != gridDim.x - 1) return;
-    __threadfence();
+    acc = bfly_add(acc);
+    if (a.bias) acc = acc + a.bias[(size_t)tok * a.E + e];
+    if (lane == 0) a.logits[(size_t)tok * a.E + e] = acc;
+}
 
-    // last workgroup of this token: softmax, prior, top-k, weights, slots
-    for (int i = threadIdx.x; i < a.E; i += 256)
-        s_lg[i] = __hip_atomic_load(a.logits + (size_t)tok * a.E + i, __ATOMIC_RELAXED,
-                                    __HIP_MEMORY_SCOPE_AGENT);
-    __syncthreads();
+// One workgroup per token: softmax, + prior, top-k (lower id on ties),
+// renormalised weights, slot lookup (wave 0); Q8_K of x (all four waves).
+__global__ __launch_bounds__(256) void route_select_kernel(RouteArgs a) {
+    const int tok = blockIdx.x;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const float *x = a.x + (size_t)tok * a.H;
+    __shared__ float s_p[256];
+    __shared__ int s_ids[16];
     if (wave == 0) {
+        const float *lg = a.logits + (size_t)tok * a.E;
         const int nc = a.E / 64;
-        float m = s_lg[lane];
-        for (int c = 1; c < nc; ++c) m = fmaxf(m, s_lg[64 * c + lane]);
+        float l4[4];
+        for (int c = 0; c < nc; ++c) l4[c] = lg[64 * c + lane];
+        float m = l4[0];
+        for (int c = 1; c < nc; ++c) m = fmaxf(m, l4[c]);
 #pragma unroll
         for (int o = 32; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
         float ex[4];
         float s = 0.0f;
         for (int c = 0; c < nc; ++c) {
-            ex[c] = canon_expf(s_lg[64 * c + lane] - m);
+            ex[c] = canon_expf(l4[c] - m);
             const float cs = bfly_add(ex[c]);
             s = c == 0 ? cs : s + cs;
         }
@@ -170,7 +171,6 @@ __global__ __launch_bounds__(256) void route_kernel(RouteArgs a) {
             if (a.probs) a.probs[(size_t)tok * a.E + ee] = p;
             sel[c] = a.prior ? p + a.prior[ee] : p;
         }
-        int ids[16];
         for (int k = 0; k < a.K; ++k) {
             float bv = -INFINITY;
             int bi = 1 << 30;
@@ -185,27 +185,36 @@ __global__ __launch_bounds__(256) void route_kernel(RouteArgs a) {
                 if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
             }
             if (bi >= a.E) bi = 0;   // only if every candidate were NaN: keep the index in range
-            ids[k] = bi;
+            if (lane == 0) s_ids[k] = bi;
             if ((bi & 63) == lane) taken |= 1 << (bi >> 6);
         }
         __builtin_amdgcn_wave_barrier();
-        if (lane == 0) {
-            float ws = 0.0f;
-            for (int k = 0; k < a.K; ++k) ws = ws + s_p[ids[k]];
-            for (int k = 0; k < a.K; ++k) {
-                a.ids[(size_t)tok * a.K + k] = ids[k];
-                a.w[(size_t)tok * a.K + k] = s_p[ids[k]] / ws;
-                a.slots[(size_t)tok * a.K + k] = a.table ? a.table[ids[k]] : a.dummy;
-            }
+        // lane k finishes slot k; the weight sum is the same left-to-right sum on every lane
+        float ws = 0.0f;
+        for (int k = 0; k < a.K; ++k) ws = ws + s_p[s_ids[k]];
+        if (lane < a.K) {
+            const int id = s_ids[lane];
+            a.ids[(size_t)tok * a.K + lane] = id;
+            a.w[(size_t)tok * a.K + lane] = s_p[id] / ws;
+            a.slots[(size_t)tok * a.K + lane] = a.table ? a.table[id] : a.dummy;
         }
     }
-    // Q8_K of x for the expert kernels (all four waves)
     uint8_t *q8 = a.q8x + (size_t)tok * (a.H / QK) * Q8K_BYTES;
     for (int b = wave; b < a.H / QK; b += 4) q8k_wave(x + QK * b, q8 + (size_t)b * Q8K_BYTES, lane);
-    if (threadIdx.x == 0) a.counter[tok] = 0;
 }
 
 // ---------------------------------------------------------------------------
+// which experts a launch serves: all of them, only those resident in an HBM
+// slot, or only those read from the pinned host store
+constexpr int SRC_ALL = 0, SRC_HBM = 1, SRC_HOST = 2;
+
+__device__ inline bool serves(const ExpertArgs &a, int k, int src) {
+    if (src == SRC_ALL) return true;
+    const int slot = a.slots[k];
+    const bool resident = a.slot_pool && slot >= 0 && slot < a.n_slots;
+    return src == SRC_HBM ? resident : !resident;
+}
+
 // expert pointers: resident -> HBM slot, absent -> pinned host store
 // (null for an id outside the store: that expert contributes zero)
 __device__ inline const uint8_t *expert_base(const ExpertArgs &a, int k) {
@@ -251,10 +260,11 @@ __device__ inline void q4k_lane(uint4 hdr, uint4 qs, int u, const uint32_t *xlo,
     mi = ml * bslo + mh * bshi;
 }
 
-template <int R>
+template <int R, int SRC>
 __global__ __launch_bounds__(256) void gateup_kernel(ExpertArgs a) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int k = blockIdx.y;
+    if (!serves(a, k, SRC)) return;
     const int b = lane >> 3, u = lane & 7;
     const int j = u >> 1;
     const uint8_t *base = expert_base(a, k);
@@ -313,22 +323,6 @@ __global__ __launch_bounds__(256) void gateup_kernel(ExpertArgs a) {
         }
     }
 
-    // the last workgroup of expert k quantizes its h to Q8_K
-    __shared__ uint32_t s_ticket;
-    __threadfence();
-    __syncthreads();
-    if (threadIdx.x == 0) s_ticket = atomicAdd(&a.counter[k], 1u);
-    __syncthreads();
-    if (s_ticket != gridDim.x - 1) return;
-    __threadfence();
-    const float *hk = a.h + (size_t)k * a.I;
-    uint8_t *q8h = a.q8h + (size_t)k * (a.I / QK) * Q8K_BYTES;
-    __shared__ __attribute__((aligned(16))) float s_h[1024];
-    for (int i = threadIdx.x; i < a.I; i += 256)
-        s_h[i] = __hip_atomic_load(hk + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __syncthreads();
-    for (int bb = wave; bb < a.I / QK; bb += 4) q8k_wave(s_h + QK * bb, q8h + (size_t)bb * Q8K_BYTES, lane);
-    if (threadIdx.x == 0) a.counter[k] = 0;
 }
 
 // ---------------------------------------------------------------------------
@@ -343,7 +337,7 @@ __device__ inline uint32_t lds_u32_at2(const uint8_t *p) {   // 2-byte aligned
     return (uint32_t)q[0] | ((uint32_t)q[1] << 16);
 }
 
-template <int DT>
+template <int DT, int SRC>
 __global__ __launch_bounds__(512) void down_kernel(ExpertArgs a) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int r0 = blockIdx.x * DN_ROWS;
@@ -356,22 +350,32 @@ __global__ __launch_bounds__(512) void down_kernel(ExpertArgs a) {
     const int g = lane >> 3, u = lane & 7;   // g: row within the tile, u: part of a super-block
     for (int kb = 0; kb < a.K; kb += 8) {
         const int k = kb + wave;
-        if (k < a.K) {
+        const bool mine = k < a.K && serves(a, k, SRC);
+        if (k < a.K && !mine && lane < DN_ROWS) s_y[k][lane] = 0.0f;   // other launch's expert
+        if (mine) {
             const uint8_t *eb = expert_base(a, k);
             uint4 *dst = (uint4 *)s_w[wave];
-            const int nvec = DN_ROWS * rowb / 16;
-            if (eb) {
-                const uint4 *src = (const uint4 *)(eb + 2ull * a.I * (a.H / QK) * Q4K_BYTES + (size_t)r0 * rowb);
-                for (int i = lane; i < nvec; i += 64) dst[i] = src[i];
-            } else {
-                for (int i = lane; i < nvec; i += 64) dst[i] = make_uint4(0, 0, 0, 0);
+            const int nvec = DN_ROWS * rowb / 16;           // <= 315
+            uint4 buf[5];
+            const uint4 *src = eb ? (const uint4 *)(eb + 2ull * a.I * (a.H / QK) * Q4K_BYTES + (size_t)r0 * rowb)
+                                  : nullptr;
+#pragma unroll
+            for (int j = 0; j < 5; ++j) {
+                const int i = lane + 64 * j;
+                buf[j] = (src && i < nvec) ? src[i] : make_uint4(0, 0, 0, 0);
             }
-            const uint32_t *q8s = (const uint32_t *)(a.q8h + (size_t)k * nb * Q8K_BYTES);
-            uint32_t *q8d = (uint32_t *)s_q8[wave];
-            for (int i = lane; i < nb * Q8K_BYTES / 4; i += 64) q8d[i] = q8s[i];
+            // Q8_K of this expert's h, straight into LDS, while the weight
+            // loads are in flight (every workgroup quantizes the same h the
+            // same way: identical bytes)
+            for (int b = 0; b < nb; ++b) q8k_wave(a.h + (size_t)k * a.I + QK * b, s_q8[wave] + b * Q8K_BYTES, lane);
+#pragma unroll
+            for (int j = 0; j < 5; ++j) {
+                const int i = lane + 64 * j;
+                if (i < nvec) dst[i] = buf[j];
+            }
         }
         __syncthreads();
-        if (k < a.K) {
+        if (mine) {
             float y = 0.0f;
             for (int b = 0; b < nb; ++b) {
                 const uint8_t *xq = s_q8[wave] + b * Q8K_BYTES;
@@ -475,21 +479,42 @@ hipError_t launch_route(const RouteLaunch &l, hipStream_t st) {
     a.E = l.E; a.H = l.H; a.K = l.K;
     a.logits = l.logits; a.counter = l.counter; a.ids = l.ids; a.w = l.w; a.slots = l.slots;
     a.probs = l.probs; a.q8x = l.q8x;
-    dim3 grid((unsigned)(l.E / 4), (unsigned)l.n_tok);
-    hipLaunchKernelGGL(route_kernel, grid, dim3(256), 0, st, a);
+    hipLaunchKernelGGL(route_logits_kernel, dim3((unsigned)(l.E / 4), (unsigned)l.n_tok), dim3(256), 0, st, a);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(route_select_kernel, dim3((unsigned)l.n_tok), dim3(256), 0, st, a);
     return hipGetLastError();
 }
 
-hipError_t launch_experts(const ExpertArgs &a, hipStream_t st) {
+template <int SRC>
+static hipError_t gateup_src(const ExpertArgs &a, hipStream_t st) {
     constexpr int R = 2;
-    hipLaunchKernelGGL(gateup_kernel<R>, dim3((unsigned)(a.I / (4 * R)), (unsigned)a.K), dim3(256), 0, st, a);
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return e;
-    if (a.down_type == TYPE_Q6K)
-        hipLaunchKernelGGL(down_kernel<TYPE_Q6K>, dim3((unsigned)(a.H / DN_ROWS)), dim3(512), 0, st, a);
-    else
-        hipLaunchKernelGGL(down_kernel<TYPE_Q4K>, dim3((unsigned)(a.H / DN_ROWS)), dim3(512), 0, st, a);
+    hipLaunchKernelGGL((gateup_kernel<R, SRC>), dim3((unsigned)(a.I / (4 * R)), (unsigned)a.K), dim3(256), 0, st, a);
     return hipGetLastError();
+}
+
+template <int SRC>
+static hipError_t down_src(const ExpertArgs &a, hipStream_t st) {
+    if (a.down_type == TYPE_Q6K)
+        hipLaunchKernelGGL((down_kernel<TYPE_Q6K, SRC>), dim3((unsigned)(a.H / DN_ROWS)), dim3(512), 0, st, a);
+    else
+        hipLaunchKernelGGL((down_kernel<TYPE_Q4K, SRC>), dim3((unsigned)(a.H / DN_ROWS)), dim3(512), 0, st, a);
+    return hipGetLastError();
+}
+
+hipError_t launch_gateup(const ExpertArgs &a, int src, hipStream_t st) {
+    return src == SRC_HBM ? gateup_src<SRC_HBM>(a, st) : src == SRC_HOST ? gateup_src<SRC_HOST>(a, st)
+                                                                           : gateup_src<SRC_ALL>(a, st);
+}
+
+hipError_t launch_down(const ExpertArgs &a, int src, hipStream_t st) {
+    return src == SRC_HBM ? down_src<SRC_HBM>(a, st) : src == SRC_HOST ? down_src<SRC_HOST>(a, st)
+                                                                         : down_src<SRC_ALL>(a, st);
+}
+
+hipError_t launch_experts(const ExpertArgs &a, hipStream_t st) {
+    const hipError_t e = launch_gateup(a, SRC_ALL, st);
+    return e != hipSuccess ? e : launch_down(a, SRC_ALL, st);
 }
 
 hipError_t launch_synth_experts(uint64_t seed, int layer, int e0, int n_experts, int H, int I, int down_type,

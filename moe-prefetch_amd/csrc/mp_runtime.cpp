@@ -94,6 +94,8 @@ struct moe_cache {
     uint8_t *d_q8x = nullptr;
     uint8_t *pool_base = nullptr;
     hipStream_t up_stream = nullptr, tbl_stream = nullptr;
+    hipStream_t host_stream = nullptr;     // absent-expert launches (fork/join per layer)
+    hipEvent_t ev_route = nullptr, ev_hbm = nullptr, ev_host = nullptr;
     hipEvent_t up_mark = nullptr;
     std::deque<Job> jobs;              // issued, not yet published, in issue order
     std::vector<hipEvent_t> free_events;
@@ -101,6 +103,22 @@ struct moe_cache {
     uint64_t n_admit_ok = 0, n_admit_denied = 0, n_table_flushes = 0, bytes_uploaded = 0;
     double wait_us = 0.0;
     FILE *route = nullptr, *map = nullptr;
+    // optional kernel timing: 8 events per layer, read back after the token's sync
+    bool timing = false;
+    std::vector<hipEvent_t> tev;
+    moe_kernel_times kt{};
+    // decode path: `split` runs resident and absent experts as separate launches
+    // on two streams (fork/join per layer), otherwise one launch serves both;
+    // `graph` replays the token's launches as one captured HIP graph over fixed
+    // device buffers (x_buf, bias_buf, out_buf)
+    int split = 0;                     // 0 one launch, 1 fork/join over two streams, 2 serial on one stream
+    bool graph = true;
+    hipStream_t cap_stream = nullptr;
+    hipEvent_t ev_user = nullptr, ev_done = nullptr;
+    float *x_buf = nullptr, *bias_buf = nullptr, *out_buf = nullptr;
+    hipGraph_t g[2] = {nullptr, nullptr};
+    hipGraphExec_t gx[2] = {nullptr, nullptr};
+    int g_mode[2] = {-1, -1};          // (timing, split) the graph was captured with
 };
 
 struct moe_pool {
@@ -449,6 +467,7 @@ int run_experts(const moe_experts_desc *d, hipStream_t st) {
 
 void free_cache(moe_cache *c) {
     if (!c) return;
+    for (hipEvent_t e : c->tev) hipEventDestroy(e);
     if (c->host_only) {
         free(c->h_tbl);
         free(c->h_prior);
@@ -462,6 +481,17 @@ void free_cache(moe_cache *c) {
         if (j.ev) hipEventDestroy(j.ev);
     for (hipEvent_t e : c->free_events) hipEventDestroy(e);
     if (c->up_mark) hipEventDestroy(c->up_mark);
+    for (hipEvent_t e : {c->ev_route, c->ev_hbm, c->ev_host, c->ev_user, c->ev_done})
+        if (e) hipEventDestroy(e);
+    for (int i = 0; i < 2; ++i) {
+        if (c->gx[i]) hipGraphExecDestroy(c->gx[i]);
+        if (c->g[i]) hipGraphDestroy(c->g[i]);
+    }
+    if (c->host_stream) hipStreamDestroy(c->host_stream);
+    if (c->cap_stream) hipStreamDestroy(c->cap_stream);
+    hipFree(c->x_buf);
+    hipFree(c->bias_buf);
+    hipFree(c->out_buf);
     if (c->up_stream) hipStreamDestroy(c->up_stream);
     if (c->tbl_stream) hipStreamDestroy(c->tbl_stream);
     hipFree(c->pool_base);
@@ -735,8 +765,19 @@ int moe_cache_create(const moe_cache_config *cfg, moe_cache **out) {
         return bail(fail(MOE_ERR_HIP, "scratch clear"));
     if (hipStreamCreateWithFlags(&c->up_stream, hipStreamNonBlocking) != hipSuccess ||
         hipStreamCreateWithFlags(&c->tbl_stream, hipStreamNonBlocking) != hipSuccess ||
-        hipEventCreateWithFlags(&c->up_mark, hipEventDisableTiming) != hipSuccess)
+        hipStreamCreateWithFlags(&c->host_stream, hipStreamNonBlocking) != hipSuccess ||
+        hipEventCreateWithFlags(&c->up_mark, hipEventDisableTiming) != hipSuccess ||
+        hipEventCreateWithFlags(&c->ev_route, hipEventDisableTiming) != hipSuccess ||
+        hipEventCreateWithFlags(&c->ev_hbm, hipEventDisableTiming) != hipSuccess ||
+        hipEventCreateWithFlags(&c->ev_host, hipEventDisableTiming) != hipSuccess ||
+        hipStreamCreateWithFlags(&c->cap_stream, hipStreamNonBlocking) != hipSuccess ||
+        hipEventCreateWithFlags(&c->ev_user, hipEventDisableTiming) != hipSuccess ||
+        hipEventCreateWithFlags(&c->ev_done, hipEventDisableTiming) != hipSuccess)
         return bail(fail(MOE_ERR_HIP, "streams"));
+    if (hipMalloc(&c->x_buf, (size_t)NL * c->H * 4) != hipSuccess ||
+        hipMalloc(&c->bias_buf, (size_t)NL * E * 4) != hipSuccess ||
+        hipMalloc(&c->out_buf, (size_t)NL * c->H * 4) != hipSuccess)
+        return bail(fail(MOE_ERR_NOMEM, "decode buffers"));
     *out = c;
     return MOE_OK;
 }
@@ -851,6 +892,28 @@ int moe_cache_stats_get(moe_cache *c, moe_cache_stats *s) {
     return MOE_OK;
 }
 
+int moe_cache_set_decode_path(moe_cache *c, int split, int graph) {
+    if (!c) return fail(MOE_ERR_ARG, "null cache");
+    if (split < 0 || split > 2) return fail(MOE_ERR_ARG, "split must be 0, 1 or 2");
+    c->split = split;
+    c->graph = graph != 0;
+    return MOE_OK;
+}
+
+int moe_cache_set_timing(moe_cache *c, int on) {
+    if (!c) return fail(MOE_ERR_ARG, "null cache");
+    if (c->host_only && on) return fail(MOE_ERR_STATE, "host-only cache has no kernels to time");
+    c->timing = on != 0;
+    c->kt = moe_kernel_times{};
+    return MOE_OK;
+}
+
+int moe_cache_kernel_times(moe_cache *c, moe_kernel_times *out) {
+    if (!c || !out) return fail(MOE_ERR_ARG, "bad arguments");
+    *out = c->kt;
+    return MOE_OK;
+}
+
 int moe_cache_sync(moe_cache *c) {
     if (!c) return fail(MOE_ERR_ARG, "null cache");
     if (c->host_only) return MOE_OK;
@@ -858,13 +921,20 @@ int moe_cache_sync(moe_cache *c) {
     return MOE_OK;
 }
 
+static int decode_layer_impl(moe_cache *c, int layer, const float *x, const float *bias, float *out,
+                             int32_t *ids_dev, float *w_dev, hipStream_t st, hipEvent_t *ev);
+
 int moe_decode_layer(moe_cache *c, int layer, const float *x, const float *bias, float *out, int32_t *ids_dev,
                      float *w_dev, void *stream) {
+    return decode_layer_impl(c, layer, x, bias, out, ids_dev, w_dev, (hipStream_t)stream, nullptr);
+}
+
+static int decode_layer_impl(moe_cache *c, int layer, const float *x, const float *bias, float *out,
+                             int32_t *ids_dev, float *w_dev, hipStream_t st, hipEvent_t *ev) {
     if (!c || !x || !out || layer < 0 || layer >= (int)c->L.size()) return fail(MOE_ERR_ARG, "bad arguments");
     if (c->host_only) return fail(MOE_ERR_STATE, "host-only cache (device < 0) cannot decode");
     const Layer &ls = c->L[layer];
     if (!ls.router || !ls.store_dev) return fail(MOE_ERR_STATE, "layer %d: router or host store missing", layer);
-    hipStream_t st = (hipStream_t)stream;
     int32_t *ids = ids_dev ? ids_dev : c->d_ids + (size_t)layer * c->K;
     float *w = w_dev ? w_dev : c->d_w + (size_t)layer * c->K;
     int32_t *slots = c->d_slots + (size_t)layer * c->K;
@@ -876,8 +946,10 @@ int moe_decode_layer(moe_cache *c, int layer, const float *x, const float *bias,
     rd.E = c->E; rd.H = c->H; rd.K = c->K; rd.n_tok = 1;
     rd.ids = ids; rd.w = w; rd.slots = slots; rd.probs = nullptr; rd.q8x = c->d_q8x;
     rd.workspace = c->route_ws;
+    if (ev) HIPCHK(hipEventRecord(ev[0], st));
     int r = run_route(&rd, st);
     if (r != MOE_OK) return r;
+    if (ev) HIPCHK(hipEventRecord(ev[1], st));
     moe_experts_desc ed{};
     ed.ids = ids; ed.slots = slots; ed.w = w;
     ed.slot_pool = ls.pool; ed.slot_bytes = ls.slot_bytes; ed.n_slots = ls.S;
@@ -885,7 +957,69 @@ int moe_decode_layer(moe_cache *c, int layer, const float *x, const float *bias,
     ed.q8x = c->d_q8x; ed.out = out; ed.accumulate = 0;
     ed.H = c->H; ed.I = c->I; ed.K = c->K; ed.down_type = ls.down_type;
     ed.workspace = c->exp_ws;
-    return run_experts(&ed, st);
+    mp::ExpertArgs a{};
+    a.ids = ed.ids; a.slots = ed.slots; a.w = ed.w;
+    a.slot_pool = ed.slot_pool; a.slot_bytes = ed.slot_bytes; a.n_slots = ed.n_slots;
+    a.host_store = ed.host_store; a.expert_bytes = ed.expert_bytes; a.n_experts = ed.n_experts;
+    a.q8x = ed.q8x; a.out = ed.out;
+    a.H = ed.H; a.I = ed.I; a.K = ed.K; a.down_type = ed.down_type;
+    uint8_t *ws = (uint8_t *)ed.workspace;
+    a.h = (float *)ws;
+    size_t o = align_up((size_t)ed.K * ed.I * 4, 256);
+    a.q8h = ws + o;
+    o += align_up((size_t)ed.K * (ed.I / 256) * mp::Q8K_BYTES, 256);
+    a.counter = (uint32_t *)(ws + o);
+    if (c->split == 2) {
+        a.accumulate = 0;
+        HIPCHK(mp::launch_gateup(a, 1, st));
+        if (ev) HIPCHK(hipEventRecord(ev[2], st));
+        HIPCHK(mp::launch_down(a, 1, st));
+        if (ev) HIPCHK(hipEventRecord(ev[3], st));
+        mp::ExpertArgs ah = a;
+        ah.accumulate = 1;
+        if (ev) HIPCHK(hipEventRecord(ev[4], st));
+        HIPCHK(mp::launch_gateup(ah, 2, st));
+        if (ev) HIPCHK(hipEventRecord(ev[5], st));
+        if (ev) HIPCHK(hipEventRecord(ev[6], st));
+        HIPCHK(mp::launch_down(ah, 2, st));
+        if (ev) HIPCHK(hipEventRecord(ev[7], st));
+        return MOE_OK;
+    }
+    if (!c->split) {
+        a.accumulate = 0;
+        if (ev) HIPCHK(hipEventRecord(ev[4], st));
+        if (ev) HIPCHK(hipEventRecord(ev[5], st));
+        HIPCHK(mp::launch_gateup(a, 0, st));
+        if (ev) HIPCHK(hipEventRecord(ev[2], st));
+        HIPCHK(mp::launch_down(a, 0, st));
+        if (ev) HIPCHK(hipEventRecord(ev[3], st));
+        if (ev) HIPCHK(hipEventRecord(ev[6], st));
+        if (ev) HIPCHK(hipEventRecord(ev[7], st));
+        return MOE_OK;
+    }
+    // fork: resident experts on st, absent ones on the host stream; the host
+    // stream's down launch adds onto what the resident one wrote; join.
+    hipStream_t hs = c->host_stream;
+    HIPCHK(hipEventRecord(c->ev_route, st));
+    HIPCHK(hipStreamWaitEvent(hs, c->ev_route, 0));
+    if (ev) HIPCHK(hipEventRecord(ev[4], hs));
+    mp::ExpertArgs ah = a;
+    ah.accumulate = 1;
+    HIPCHK(mp::launch_gateup(ah, 2, hs));
+    if (ev) HIPCHK(hipEventRecord(ev[5], hs));
+    a.accumulate = 0;
+    HIPCHK(mp::launch_gateup(a, 1, st));
+    if (ev) HIPCHK(hipEventRecord(ev[2], st));
+    HIPCHK(mp::launch_down(a, 1, st));
+    if (ev) HIPCHK(hipEventRecord(ev[3], st));
+    HIPCHK(hipEventRecord(c->ev_hbm, st));
+    HIPCHK(hipStreamWaitEvent(hs, c->ev_hbm, 0));
+    if (ev) HIPCHK(hipEventRecord(ev[6], hs));
+    HIPCHK(mp::launch_down(ah, 2, hs));
+    if (ev) HIPCHK(hipEventRecord(ev[7], hs));
+    HIPCHK(hipEventRecord(c->ev_host, hs));
+    HIPCHK(hipStreamWaitEvent(st, c->ev_host, 0));
+    return MOE_OK;
 }
 
 int moe_decode_token(moe_cache *c, const float *x, const float *bias, float *out, int32_t *ids_host, void *stream) {
@@ -893,13 +1027,70 @@ int moe_decode_token(moe_cache *c, const float *x, const float *bias, float *out
     if (c->host_only) return fail(MOE_ERR_STATE, "host-only cache (device < 0) cannot decode");
     hipStream_t st = (hipStream_t)stream;
     const int NL = (int)c->L.size();
-    for (int l = 0; l < NL; ++l) {
-        const int r = moe_decode_layer(c, l, x + (size_t)l * c->H, bias ? bias + (size_t)l * c->E : nullptr,
-                                       out + (size_t)l * c->H, nullptr, nullptr, stream);
-        if (r != MOE_OK) return r;
+    if (c->timing && c->tev.size() != (size_t)NL * 8) {
+        c->tev.assign((size_t)NL * 8, nullptr);
+        for (auto &e : c->tev) HIPCHK(hipEventCreate(&e));
+    }
+    // per-kernel HIP-event timing needs eager launches: hipEventElapsedTime
+    // does not accept events recorded as nodes of a graph
+    if (!c->graph || c->timing) {
+        for (int l = 0; l < NL; ++l) {
+            const int r = decode_layer_impl(c, l, x + (size_t)l * c->H, bias ? bias + (size_t)l * c->E : nullptr,
+                                            out + (size_t)l * c->H, nullptr, nullptr, st,
+                                            c->timing ? c->tev.data() + (size_t)l * 8 : nullptr);
+            if (r != MOE_OK) return r;
+        }
+    } else {
+        const int key = bias ? 1 : 0;
+        const int mode = c->split;
+        if (!c->gx[key] || c->g_mode[key] != mode) {
+            if (c->gx[key]) { hipGraphExecDestroy(c->gx[key]); c->gx[key] = nullptr; }
+            if (c->g[key]) { hipGraphDestroy(c->g[key]); c->g[key] = nullptr; }
+            HIPCHK(hipStreamBeginCapture(c->cap_stream, hipStreamCaptureModeThreadLocal));
+            int r = MOE_OK;
+            for (int l = 0; l < NL && r == MOE_OK; ++l)
+                r = decode_layer_impl(c, l, c->x_buf + (size_t)l * c->H, key ? c->bias_buf + (size_t)l * c->E : nullptr,
+                                      c->out_buf + (size_t)l * c->H, nullptr, nullptr, c->cap_stream, nullptr);
+            hipGraph_t g = nullptr;
+            const hipError_t ec = hipStreamEndCapture(c->cap_stream, &g);
+            if (r != MOE_OK) { if (g) hipGraphDestroy(g); return r; }
+            if (ec != hipSuccess) return fail(MOE_ERR_HIP, "hipStreamEndCapture: %s", hipGetErrorString(ec));
+            c->g[key] = g;
+            HIPCHK(hipGraphInstantiate(&c->gx[key], g, nullptr, nullptr, 0));
+            c->g_mode[key] = mode;
+        }
+        HIPCHK(hipMemcpyAsync(c->x_buf, x, (size_t)NL * c->H * 4, hipMemcpyDeviceToDevice, st));
+        if (bias) HIPCHK(hipMemcpyAsync(c->bias_buf, bias, (size_t)NL * c->E * 4, hipMemcpyDeviceToDevice, st));
+        HIPCHK(hipGraphLaunch(c->gx[key], st));
+        HIPCHK(hipMemcpyAsync(out, c->out_buf, (size_t)NL * c->H * 4, hipMemcpyDeviceToDevice, st));
     }
     HIPCHK(hipMemcpyAsync(c->h_ids, c->d_ids, (size_t)NL * c->K * 4, hipMemcpyDeviceToHost, st));
     HIPCHK(hipStreamSynchronize(st));
+    if (c->timing) {
+        const uint64_t gu_b = 2ull * c->I * (c->H / 256) * mp::Q4K_BYTES;
+        for (int l = 0; l < NL; ++l) {
+            float t[5] = {0, 0, 0, 0, 0};
+            hipEvent_t *e = c->tev.data() + (size_t)l * 8;
+            HIPCHK(hipEventElapsedTime(&t[0], e[0], e[1]));
+            HIPCHK(hipEventElapsedTime(&t[1], e[1], e[2]));
+            HIPCHK(hipEventElapsedTime(&t[2], e[2], e[3]));
+            HIPCHK(hipEventElapsedTime(&t[3], e[4], e[5]));
+            HIPCHK(hipEventElapsedTime(&t[4], e[6], e[7]));
+            c->kt.route_ms += t[0];
+            c->kt.gateup_hbm_ms += t[1];
+            c->kt.down_hbm_ms += t[2];
+            c->kt.gateup_host_ms += t[3];
+            c->kt.down_host_ms += t[4];
+            c->kt.n_layers++;
+            const Layer &ls = c->L[l];
+            for (int k = 0; k < c->K; ++k) {
+                const int id = c->h_ids[(size_t)l * c->K + k];
+                const bool res = id >= 0 && id < ls.E && ls.expert_slot[id] >= 0;
+                (res ? c->kt.gateup_hbm_bytes : c->kt.gateup_host_bytes) += gu_b;
+                (res ? c->kt.down_hbm_bytes : c->kt.down_host_bytes) += ls.expert_bytes - gu_b;
+            }
+        }
+    }
     for (int l = 0; l < NL; ++l) {
         const int r = cache_observe(c, l, c->h_ids + (size_t)l * c->K, c->K, 1);
         if (r != MOE_OK) return r;

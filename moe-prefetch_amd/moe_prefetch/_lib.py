@@ -61,6 +61,13 @@ class LayerView(ctypes.Structure):
                 ("prior", P), ("host_store", P), ("router", P)]
 
 
+class KernelTimes(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_double) for n in ("route_ms", "gateup_hbm_ms", "down_hbm_ms", "gateup_host_ms",
+                                               "down_host_ms")] + \
+               [(n, U64) for n in ("n_layers", "gateup_hbm_bytes", "down_hbm_bytes", "gateup_host_bytes",
+                                   "down_host_bytes")]
+
+
 # name -> (restype, argtypes); mirrors include/moe_prefetch.h one to one
 SIGNATURES = {
     "moe_last_error": (ctypes.c_char_p, []),
@@ -99,6 +106,9 @@ SIGNATURES = {
     "moe_cache_table": (ctypes.c_int, [P, ctypes.c_int, P, P]),
     "moe_cache_stats_get": (ctypes.c_int, [P, ctypes.POINTER(CacheStats)]),
     "moe_cache_sync": (ctypes.c_int, [P]),
+    "moe_cache_set_timing": (ctypes.c_int, [P, ctypes.c_int]),
+    "moe_cache_set_decode_path": (ctypes.c_int, [P, ctypes.c_int, ctypes.c_int]),
+    "moe_cache_kernel_times": (ctypes.c_int, [P, ctypes.POINTER(KernelTimes)]),
     "moe_decode_layer": (ctypes.c_int, [P, ctypes.c_int, P, P, P, P, P, P]),
     "moe_decode_token": (ctypes.c_int, [P, P, P, P, P, P]),
     "moe_pool_create": (ctypes.c_int, [ctypes.c_int, ctypes.c_int, SZ, ctypes.c_int, ctypes.POINTER(P)]),

@@ -159,6 +159,19 @@ class MoeCache:
     def sync(self):
         check(lib().moe_cache_sync(self.h), "sync")
 
+    def set_decode_path(self, split=0, graph=True):
+        """split: 0 one launch for all routed experts, 1 resident/absent experts on
+        two forked streams, 2 resident then absent on one stream."""
+        check(lib().moe_cache_set_decode_path(self.h, int(split), int(graph)), "set_decode_path")
+
+    def set_timing(self, on=True):
+        check(lib().moe_cache_set_timing(self.h, int(on)), "set_timing")
+
+    def kernel_times(self):
+        t = _lib.KernelTimes()
+        check(lib().moe_cache_kernel_times(self.h, ctypes.byref(t)), "kernel_times")
+        return {n: getattr(t, n) for n, _ in _lib.KernelTimes._fields_}
+
     # -- decode ---------------------------------------------------------------
     def decode_layer(self, layer, x, out, bias=None, ids=None, w=None, stream=None):
         check(lib().moe_decode_layer(self.h, layer, _ptr(x), _ptr(bias), _ptr(out), _ptr(ids), _ptr(w),

@@ -77,14 +77,15 @@ class Rig:
 
     def run(self, tokens=None, keep_out=None):
         tokens = range(self.T) if tokens is None else tokens
-        ids_all, outs = {}, {}
+        ids_all, outs, frames = {}, {}, {}
         out = torch.empty((self.nl, H), dtype=torch.float32, device=self.dev)
         for t in tokens:
             b = None if self.bias is None else self.bias[t]
             ids_all[t] = self.cache.decode_token(self.x[t], out, bias=b, stream=stream()).copy()
+            frames[t] = [self.cache.frame(l) for l in range(self.nl)]
             if keep_out is None or t in keep_out:
                 outs[t] = out.cpu().numpy().copy()
-        return ids_all, outs
+        return ids_all, outs, frames
 
     def oracle_cache(self):
         kn = dict(self.knobs)

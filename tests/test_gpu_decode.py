@@ -26,7 +26,7 @@ def check_run(rig, tmp_path, out_every=1, tol=1e-3):
     oc = rig.oracle_cache()
     oc.trace_open(orp, omp)
     keep = set(range(0, rig.T, out_every))
-    ids_all, outs = rig.run(keep_out=keep)
+    ids_all, outs, frames = rig.run(keep_out=keep)
     worst = 0.0
     for t in range(rig.T):
         for l in range(rig.nl):
@@ -43,7 +43,7 @@ def check_run(rig, tmp_path, out_every=1, tol=1e-3):
             oc.observe(l, rids)
         oc.step()
         for l in range(rig.nl):
-            assert np.array_equal(rig.cache.frame(l), oc.frame(l)), (t, l)
+            assert np.array_equal(frames[t][l], oc.frame(l)), (t, l)
     rig.cache.close()
     oc.close()
     assert open(rp).read() == open(orp).read()
@@ -51,8 +51,18 @@ def check_run(rig, tmp_path, out_every=1, tol=1e-3):
     return worst
 
 
-def test_decode_4_layers_window_admission(tmp_path):
+@pytest.mark.parametrize("split,graph", [(1, 1), (0, 1), (2, 1), (1, 0), (0, 0), (2, 0)],
+                         ids=["fork-graph", "fused-graph", "serial-graph", "fork-eager", "fused-eager",
+                              "serial-eager"])
+def test_decode_4_layers_window_admission(tmp_path, split, graph):
+    # every decode path (resident/absent experts split over two streams or one
+    # launch; captured graph replayed per token or eager launches) must give
+    # the oracle's ids, frames and outputs; the graph is replayed 40 times
+    # with eager copies, host work and synchronisation between replays
     rig = Rig([16, 24, 12, 40], [Q4, Q6, Q4, Q6], T=40, admit="window", batch_tables=True)
+    rig.cache.set_decode_path(split=split, graph=bool(graph))
+    if split and not graph:
+        rig.cache.set_timing(True)          # per-kernel events around every launch
     try:
         worst = check_run(rig, tmp_path)
         print("worst rel-L2", worst)
@@ -88,7 +98,6 @@ def test_decode_48_layers_full_shape(tmp_path):
     rig = Rig([56] * 48, [Q6 if l % 2 else Q4 for l in range(48)], T=12, admit="window", batch_tables=True)
     try:
         check_run(rig, tmp_path, out_every=6)
-        st = rig.cache.stats() if rig.cache.h else None
     finally:
         rig.close()
 
