@@ -47,6 +47,8 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="bounded CPU-baseline sample")
     ap.add_argument("--kernel-steps", type=int, default=64, help="eager tokens timed per kernel")
     ap.add_argument("--path", type=int, default=0, help="0 fused, 1 fork/join, 2 serial expert launches")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="end with a plain 256 MiB device copy (scale for rocprofv3 FETCH_SIZE/WRITE_SIZE)")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-check", action="store_true")
     args = ap.parse_args()
@@ -164,6 +166,18 @@ def main():
     host_gbs = sum(v[1] for v in host.values()) / (host_ms * 1e-3) / 1e9 if host_ms > 0 else 0.0
     times = {"route": kt["route_ms"], **{k: v[0] for k, v in hbm.items()}, **{k: v[0] for k, v in host.items()}}
     nt = max(kernel_tokens, 1)
+    # HBM bytes per launch of this kernel: the (read + write) / algorithmic
+    # ratio measured with rocprofv3 PMC counters (profiles/traffic.json) times
+    # this run's algorithmic bytes per launch
+    traffic = None
+    tpath = os.path.join(ROOT, "profiles", "traffic.json")
+    if os.path.exists(tpath):
+        with open(tpath) as f:
+            tr = json.load(f).get(dom)
+        if tr:
+            ratio = (tr["hbm_read_bytes_per_launch"] + tr["hbm_write_bytes_per_launch"]) / \
+                tr["algorithmic_bytes_per_launch"]
+            traffic = round(ratio * dom_bytes / n)
     result = {
         "metric": METRIC, "value": round(tok_s, 2), "unit": "tok/s", "n_gpus": 1,
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(1e3 * elapsed / args.steps, 4),
@@ -185,9 +199,12 @@ def main():
                          f"(graph replay cannot carry per-kernel events)",
         "decode_path": {0: "fused", 1: "fork/join", 2: "serial"}[args.path] + " expert launches, HIP graph per token",
         "roofline": {"bound": "hbm", "kernel": dom, "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
                      "bytes_per_launch": round(dom_bytes / n), "avg_launch_us": round(avg_ms * 1e3, 2),
                      "launches": n},
+        "hbm_kernels": {k: {"bytes_per_launch": round(v[1] / n), "avg_launch_us": round(v[0] / n * 1e3, 2),
+                            "gbs": round(v[1] / (v[0] * 1e-3) / 1e9, 1) if v[0] > 0 else 0.0}
+                        for k, v in hbm.items()},
         "pcie": {"kernels": "gateup_host + down_host (absent experts read from the pinned store)",
                  "achieved": round(host_gbs, 1), "unit": "GB/s", "peak_nominal": 64.0,
                  "ms_per_token": round(host_ms / nt, 4),
@@ -256,6 +273,12 @@ def main():
     cache.close()
     for p in stores:
         L.moe_host_free(p)
+    if args.calibrate_copy:
+        src = torch.ones(256 << 20, dtype=torch.uint8, device=dev)
+        for _ in range(3):
+            dst = src.clone()
+        torch.cuda.synchronize()
+        del src, dst
     print(json.dumps(result), flush=True)
 
 

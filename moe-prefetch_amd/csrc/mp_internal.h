@@ -43,13 +43,15 @@ struct ExpertArgs {
     int H, I, K, down_type;
 };
 
-hipError_t launch_route(const RouteLaunch &l, hipStream_t st);
+// ev (optional): [logits start, logits end, select start, select end]
+hipError_t launch_route(const RouteLaunch &l, hipStream_t st, hipEvent_t *ev = nullptr);
 hipError_t launch_experts(const ExpertArgs &a, hipStream_t st);
 // src: 0 every routed expert, 1 only those resident in HBM slots, 2 only
 // those read from the pinned host store.  A src = 2 down launch accumulates
 // into out when the caller sets accumulate.
-hipError_t launch_gateup(const ExpertArgs &a, int src, hipStream_t st);
-hipError_t launch_down(const ExpertArgs &a, int src, hipStream_t st);
+// e0/e1 (optional): stamped at the kernel's start and end of execution
+hipError_t launch_gateup(const ExpertArgs &a, int src, hipStream_t st, hipEvent_t e0, hipEvent_t e1);
+hipError_t launch_down(const ExpertArgs &a, int src, hipStream_t st, hipEvent_t e0, hipEvent_t e1);
 hipError_t launch_synth_experts(uint64_t seed, int layer, int e0, int n_experts, int H, int I, int down_type,
                                 float sigma, uint8_t *out, uint64_t stride, hipStream_t st);
 hipError_t launch_synth_vec(uint64_t seed, int kind, int a0, int na, int b0, int nb, int n, float sigma,

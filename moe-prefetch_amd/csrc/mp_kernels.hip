@@ -19,6 +19,7 @@
 // Numerics: integer dots are exact; fp32 only at the per-super-block scale and
 // across super-blocks.  The router follows the canonical order documented with
 // the oracle bit for bit (explicit fmaf, fixed butterflies, -ffp-contract=off).
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 
 #include "mp_format.h"
@@ -472,49 +473,56 @@ __global__ void synth_vec_kernel(uint64_t seed, int kind, int a0, int na, int b0
 }
 
 // ---------------------------------------------------------------------------
-// launchers (shapes were checked by the caller)
-hipError_t launch_route(const RouteLaunch &l, hipStream_t st) {
+// launchers (shapes were checked by the caller).  With events, the launch
+// goes through hipExtLaunchKernelGGL: the dispatch itself stamps ev0/ev1 at
+// the start and end of the kernel's execution (the window a profiler reports),
+// with no host or queue latency inside it.
+template <typename F, typename... A>
+static hipError_t launch(F k, dim3 grid, dim3 block, hipStream_t st, hipEvent_t ev0, hipEvent_t ev1, A... args) {
+    if (ev0) hipExtLaunchKernelGGL(k, grid, block, 0, st, ev0, ev1, 0, args...);
+    else hipLaunchKernelGGL(k, grid, block, 0, st, args...);
+    return hipGetLastError();
+}
+
+hipError_t launch_route(const RouteLaunch &l, hipStream_t st, hipEvent_t *ev) {
     RouteArgs a;
     a.W = l.W; a.x = l.x; a.bias = l.bias; a.prior = l.prior; a.table = l.table; a.dummy = l.dummy;
     a.E = l.E; a.H = l.H; a.K = l.K;
     a.logits = l.logits; a.counter = l.counter; a.ids = l.ids; a.w = l.w; a.slots = l.slots;
     a.probs = l.probs; a.q8x = l.q8x;
-    hipLaunchKernelGGL(route_logits_kernel, dim3((unsigned)(l.E / 4), (unsigned)l.n_tok), dim3(256), 0, st, a);
-    const hipError_t e = hipGetLastError();
+    const hipError_t e = launch(route_logits_kernel, dim3((unsigned)(l.E / 4), (unsigned)l.n_tok), dim3(256), st,
+                                ev ? ev[0] : nullptr, ev ? ev[1] : nullptr, a);
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(route_select_kernel, dim3((unsigned)l.n_tok), dim3(256), 0, st, a);
-    return hipGetLastError();
+    return launch(route_select_kernel, dim3((unsigned)l.n_tok), dim3(256), st, ev ? ev[2] : nullptr,
+                  ev ? ev[3] : nullptr, a);
 }
 
 template <int SRC>
-static hipError_t gateup_src(const ExpertArgs &a, hipStream_t st) {
+static hipError_t gateup_src(const ExpertArgs &a, hipStream_t st, hipEvent_t e0, hipEvent_t e1) {
     constexpr int R = 2;
-    hipLaunchKernelGGL((gateup_kernel<R, SRC>), dim3((unsigned)(a.I / (4 * R)), (unsigned)a.K), dim3(256), 0, st, a);
-    return hipGetLastError();
+    return launch(gateup_kernel<R, SRC>, dim3((unsigned)(a.I / (4 * R)), (unsigned)a.K), dim3(256), st, e0, e1, a);
 }
 
 template <int SRC>
-static hipError_t down_src(const ExpertArgs &a, hipStream_t st) {
+static hipError_t down_src(const ExpertArgs &a, hipStream_t st, hipEvent_t e0, hipEvent_t e1) {
     if (a.down_type == TYPE_Q6K)
-        hipLaunchKernelGGL((down_kernel<TYPE_Q6K, SRC>), dim3((unsigned)(a.H / DN_ROWS)), dim3(512), 0, st, a);
-    else
-        hipLaunchKernelGGL((down_kernel<TYPE_Q4K, SRC>), dim3((unsigned)(a.H / DN_ROWS)), dim3(512), 0, st, a);
-    return hipGetLastError();
+        return launch(down_kernel<TYPE_Q6K, SRC>, dim3((unsigned)(a.H / DN_ROWS)), dim3(512), st, e0, e1, a);
+    return launch(down_kernel<TYPE_Q4K, SRC>, dim3((unsigned)(a.H / DN_ROWS)), dim3(512), st, e0, e1, a);
 }
 
-hipError_t launch_gateup(const ExpertArgs &a, int src, hipStream_t st) {
-    return src == SRC_HBM ? gateup_src<SRC_HBM>(a, st) : src == SRC_HOST ? gateup_src<SRC_HOST>(a, st)
-                                                                           : gateup_src<SRC_ALL>(a, st);
+hipError_t launch_gateup(const ExpertArgs &a, int src, hipStream_t st, hipEvent_t e0, hipEvent_t e1) {
+    return src == SRC_HBM ? gateup_src<SRC_HBM>(a, st, e0, e1) : src == SRC_HOST ? gateup_src<SRC_HOST>(a, st, e0, e1)
+                                                                                   : gateup_src<SRC_ALL>(a, st, e0, e1);
 }
 
-hipError_t launch_down(const ExpertArgs &a, int src, hipStream_t st) {
-    return src == SRC_HBM ? down_src<SRC_HBM>(a, st) : src == SRC_HOST ? down_src<SRC_HOST>(a, st)
-                                                                         : down_src<SRC_ALL>(a, st);
+hipError_t launch_down(const ExpertArgs &a, int src, hipStream_t st, hipEvent_t e0, hipEvent_t e1) {
+    return src == SRC_HBM ? down_src<SRC_HBM>(a, st, e0, e1) : src == SRC_HOST ? down_src<SRC_HOST>(a, st, e0, e1)
+                                                                                 : down_src<SRC_ALL>(a, st, e0, e1);
 }
 
 hipError_t launch_experts(const ExpertArgs &a, hipStream_t st) {
-    const hipError_t e = launch_gateup(a, SRC_ALL, st);
-    return e != hipSuccess ? e : launch_down(a, SRC_ALL, st);
+    const hipError_t e = launch_gateup(a, SRC_ALL, st, nullptr, nullptr);
+    return e != hipSuccess ? e : launch_down(a, SRC_ALL, st, nullptr, nullptr);
 }
 
 hipError_t launch_synth_experts(uint64_t seed, int layer, int e0, int n_experts, int H, int I, int down_type,

@@ -436,7 +436,7 @@ size_t exp_ws_bytes(int I, int K) {
            align_up((size_t)K * 4, 256);
 }
 
-int run_route(const moe_route_desc *d, hipStream_t st) {
+int run_route(const moe_route_desc *d, hipStream_t st, hipEvent_t *ev = nullptr) {
     mp::RouteLaunch l{};
     l.W = d->W; l.x = d->x; l.bias = d->bias; l.prior = d->prior; l.table = d->table; l.dummy = d->dummy;
     l.E = d->E; l.H = d->H; l.K = d->K; l.n_tok = d->n_tok;
@@ -444,7 +444,7 @@ int run_route(const moe_route_desc *d, hipStream_t st) {
     l.logits = (float *)ws;
     l.counter = (uint32_t *)(ws + align_up((size_t)d->n_tok * d->E * 4, 256));
     l.ids = d->ids; l.w = d->w; l.slots = d->slots; l.probs = d->probs; l.q8x = d->q8x;
-    HIPCHK(mp::launch_route(l, st));
+    HIPCHK(mp::launch_route(l, st, ev));
     return MOE_OK;
 }
 
@@ -946,10 +946,11 @@ static int decode_layer_impl(moe_cache *c, int layer, const float *x, const floa
     rd.E = c->E; rd.H = c->H; rd.K = c->K; rd.n_tok = 1;
     rd.ids = ids; rd.w = w; rd.slots = slots; rd.probs = nullptr; rd.q8x = c->d_q8x;
     rd.workspace = c->route_ws;
-    if (ev) HIPCHK(hipEventRecord(ev[0], st));
-    int r = run_route(&rd, st);
+    // ev (timing mode), 12 per layer, stamped by the dispatches themselves:
+    // [0,1] route_logits [2,3] route_select [4,5] gate/up (resident or all)
+    // [6,7] down (resident or all) [8,9] gate/up absent [10,11] down absent
+    int r = run_route(&rd, st, ev);
     if (r != MOE_OK) return r;
-    if (ev) HIPCHK(hipEventRecord(ev[1], st));
     moe_experts_desc ed{};
     ed.ids = ids; ed.slots = slots; ed.w = w;
     ed.slot_pool = ls.pool; ed.slot_bytes = ls.slot_bytes; ed.n_slots = ls.S;
@@ -969,32 +970,20 @@ static int decode_layer_impl(moe_cache *c, int layer, const float *x, const floa
     a.q8h = ws + o;
     o += align_up((size_t)ed.K * (ed.I / 256) * mp::Q8K_BYTES, 256);
     a.counter = (uint32_t *)(ws + o);
-    if (c->split == 2) {
-        a.accumulate = 0;
-        HIPCHK(mp::launch_gateup(a, 1, st));
-        if (ev) HIPCHK(hipEventRecord(ev[2], st));
-        HIPCHK(mp::launch_down(a, 1, st));
-        if (ev) HIPCHK(hipEventRecord(ev[3], st));
-        mp::ExpertArgs ah = a;
-        ah.accumulate = 1;
-        if (ev) HIPCHK(hipEventRecord(ev[4], st));
-        HIPCHK(mp::launch_gateup(ah, 2, st));
-        if (ev) HIPCHK(hipEventRecord(ev[5], st));
-        if (ev) HIPCHK(hipEventRecord(ev[6], st));
-        HIPCHK(mp::launch_down(ah, 2, st));
-        if (ev) HIPCHK(hipEventRecord(ev[7], st));
+    auto E_ = [ev](int i) -> hipEvent_t { return ev ? ev[i] : nullptr; };
+    a.accumulate = 0;
+    mp::ExpertArgs ah = a;
+    ah.accumulate = 1;
+    if (c->split == 0) {
+        HIPCHK(mp::launch_gateup(a, 0, st, E_(4), E_(5)));
+        HIPCHK(mp::launch_down(a, 0, st, E_(6), E_(7)));
         return MOE_OK;
     }
-    if (!c->split) {
-        a.accumulate = 0;
-        if (ev) HIPCHK(hipEventRecord(ev[4], st));
-        if (ev) HIPCHK(hipEventRecord(ev[5], st));
-        HIPCHK(mp::launch_gateup(a, 0, st));
-        if (ev) HIPCHK(hipEventRecord(ev[2], st));
-        HIPCHK(mp::launch_down(a, 0, st));
-        if (ev) HIPCHK(hipEventRecord(ev[3], st));
-        if (ev) HIPCHK(hipEventRecord(ev[6], st));
-        if (ev) HIPCHK(hipEventRecord(ev[7], st));
+    if (c->split == 2) {
+        HIPCHK(mp::launch_gateup(a, 1, st, E_(4), E_(5)));
+        HIPCHK(mp::launch_down(a, 1, st, E_(6), E_(7)));
+        HIPCHK(mp::launch_gateup(ah, 2, st, E_(8), E_(9)));
+        HIPCHK(mp::launch_down(ah, 2, st, E_(10), E_(11)));
         return MOE_OK;
     }
     // fork: resident experts on st, absent ones on the host stream; the host
@@ -1002,21 +991,12 @@ static int decode_layer_impl(moe_cache *c, int layer, const float *x, const floa
     hipStream_t hs = c->host_stream;
     HIPCHK(hipEventRecord(c->ev_route, st));
     HIPCHK(hipStreamWaitEvent(hs, c->ev_route, 0));
-    if (ev) HIPCHK(hipEventRecord(ev[4], hs));
-    mp::ExpertArgs ah = a;
-    ah.accumulate = 1;
-    HIPCHK(mp::launch_gateup(ah, 2, hs));
-    if (ev) HIPCHK(hipEventRecord(ev[5], hs));
-    a.accumulate = 0;
-    HIPCHK(mp::launch_gateup(a, 1, st));
-    if (ev) HIPCHK(hipEventRecord(ev[2], st));
-    HIPCHK(mp::launch_down(a, 1, st));
-    if (ev) HIPCHK(hipEventRecord(ev[3], st));
+    HIPCHK(mp::launch_gateup(ah, 2, hs, E_(8), E_(9)));
+    HIPCHK(mp::launch_gateup(a, 1, st, E_(4), E_(5)));
+    HIPCHK(mp::launch_down(a, 1, st, E_(6), E_(7)));
     HIPCHK(hipEventRecord(c->ev_hbm, st));
     HIPCHK(hipStreamWaitEvent(hs, c->ev_hbm, 0));
-    if (ev) HIPCHK(hipEventRecord(ev[6], hs));
-    HIPCHK(mp::launch_down(ah, 2, hs));
-    if (ev) HIPCHK(hipEventRecord(ev[7], hs));
+    HIPCHK(mp::launch_down(ah, 2, hs, E_(10), E_(11)));
     HIPCHK(hipEventRecord(c->ev_host, hs));
     HIPCHK(hipStreamWaitEvent(st, c->ev_host, 0));
     return MOE_OK;
@@ -1027,8 +1007,9 @@ int moe_decode_token(moe_cache *c, const float *x, const float *bias, float *out
     if (c->host_only) return fail(MOE_ERR_STATE, "host-only cache (device < 0) cannot decode");
     hipStream_t st = (hipStream_t)stream;
     const int NL = (int)c->L.size();
-    if (c->timing && c->tev.size() != (size_t)NL * 8) {
-        c->tev.assign((size_t)NL * 8, nullptr);
+    if (c->timing && c->tev.size() != (size_t)NL * 12) {
+        for (hipEvent_t e : c->tev) hipEventDestroy(e);
+        c->tev.assign((size_t)NL * 12, nullptr);
         for (auto &e : c->tev) HIPCHK(hipEventCreate(&e));
     }
     // per-kernel HIP-event timing needs eager launches: hipEventElapsedTime
@@ -1037,7 +1018,7 @@ int moe_decode_token(moe_cache *c, const float *x, const float *bias, float *out
         for (int l = 0; l < NL; ++l) {
             const int r = decode_layer_impl(c, l, x + (size_t)l * c->H, bias ? bias + (size_t)l * c->E : nullptr,
                                             out + (size_t)l * c->H, nullptr, nullptr, st,
-                                            c->timing ? c->tev.data() + (size_t)l * 8 : nullptr);
+                                            c->timing ? c->tev.data() + (size_t)l * 12 : nullptr);
             if (r != MOE_OK) return r;
         }
     } else {
@@ -1069,18 +1050,17 @@ int moe_decode_token(moe_cache *c, const float *x, const float *bias, float *out
     if (c->timing) {
         const uint64_t gu_b = 2ull * c->I * (c->H / 256) * mp::Q4K_BYTES;
         for (int l = 0; l < NL; ++l) {
-            float t[5] = {0, 0, 0, 0, 0};
-            hipEvent_t *e = c->tev.data() + (size_t)l * 8;
-            HIPCHK(hipEventElapsedTime(&t[0], e[0], e[1]));
-            HIPCHK(hipEventElapsedTime(&t[1], e[1], e[2]));
-            HIPCHK(hipEventElapsedTime(&t[2], e[2], e[3]));
-            HIPCHK(hipEventElapsedTime(&t[3], e[4], e[5]));
-            HIPCHK(hipEventElapsedTime(&t[4], e[6], e[7]));
-            c->kt.route_ms += t[0];
-            c->kt.gateup_hbm_ms += t[1];
-            c->kt.down_hbm_ms += t[2];
-            c->kt.gateup_host_ms += t[3];
-            c->kt.down_host_ms += t[4];
+            float t[6] = {0, 0, 0, 0, 0, 0};
+            hipEvent_t *e = c->tev.data() + (size_t)l * 12;
+            for (int i = 0; i < 6; ++i) {
+                if (c->split == 0 && i >= 4) break;            // no separate absent-expert launches
+                HIPCHK(hipEventElapsedTime(&t[i], e[2 * i], e[2 * i + 1]));
+            }
+            c->kt.route_ms += t[0] + t[1];
+            c->kt.gateup_hbm_ms += t[2];
+            c->kt.down_hbm_ms += t[3];
+            c->kt.gateup_host_ms += t[4];
+            c->kt.down_host_ms += t[5];
             c->kt.n_layers++;
             const Layer &ls = c->L[l];
             for (int k = 0; k < c->K; ++k) {
