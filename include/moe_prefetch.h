@@ -98,6 +98,8 @@ typedef struct {
     const float *prior;    /* dev [E] or NULL: added to the probabilities for selection only */
     const int32_t *table;  /* dev [E] or NULL: expert -> slot (n_slots = absent) */
     int32_t dummy;         /* slot written when table is NULL */
+    int32_t prior_on_logits; /* 0: prior added to the probabilities (the reference's
+                                LLAMA_MOE_CACHE_PRIOR); 1: added to the logits */
     int32_t E, H, K, n_tok;
     int32_t *ids;          /* dev out [n_tok][K], descending selection, lower id first on ties */
     float *w;              /* dev out [n_tok][K], probs[ids] / sum(probs[ids]) */
@@ -154,7 +156,8 @@ typedef struct {
     float admit_floor;                           /* LLAMA_MOE_ADMIT_FLOOR, default 1 */
     int32_t batch_tables;                        /* LLAMA_MOE_BATCH_TABLES */
     int32_t early_issue;                         /* LLAMA_MOE_EARLY_ISSUE */
-    float cache_prior;                           /* LLAMA_MOE_CACHE_PRIOR (delta, probabilities) */
+    float cache_prior;                           /* LLAMA_MOE_CACHE_PRIOR (delta) */
+    int32_t prior_on_logits;                     /* 0: delta on probabilities (the reference), 1: on logits */
     int32_t publish;                             /* MOE_PUBLISH_*; LLAMA_MOE_DETERMINISTIC=1 is SORTED */
     int32_t device;                              /* HIP device; < 0: state machine only (no GPU, no
                                                     weights: every upload completes at once) */

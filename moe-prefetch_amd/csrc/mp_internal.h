@@ -14,6 +14,7 @@ struct RouteLaunch {
     const float *prior;    // [E] or null (cache prior: delta on resident experts)
     const int32_t *table;  // [E] or null (expert -> slot, n_slots = absent)
     int32_t dummy;
+    int prior_on_logits;   // 1: the prior is added to the logits (selection only)
     int E, H, K, n_tok;
     float *logits;         // scratch [n_tok][E]
     uint32_t *counter;     // scratch [n_tok], zero

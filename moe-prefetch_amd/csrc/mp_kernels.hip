@@ -105,6 +105,7 @@ struct RouteArgs {
     const float *prior;    // [E] or null
     const int32_t *table;  // [E] or null
     int32_t dummy;         // slot value for "absent" when no table
+    int prior_on_logits;   // 1: prior added to the logits for the selection
     int E, H, K;
     float *logits;         // scratch [n_tok][E]
     uint32_t *counter;     // scratch [n_tok], zero between launches
@@ -170,7 +171,7 @@ __global__ __launch_bounds__(256) void route_select_kernel(RouteArgs a) {
             const float p = ex[c] / s;
             s_p[ee] = p;
             if (a.probs) a.probs[(size_t)tok * a.E + ee] = p;
-            sel[c] = a.prior ? p + a.prior[ee] : p;
+            sel[c] = !a.prior ? p : (a.prior_on_logits ? l4[c] + a.prior[ee] : p + a.prior[ee]);
         }
         for (int k = 0; k < a.K; ++k) {
             float bv = -INFINITY;
@@ -487,6 +488,7 @@ static hipError_t launch(F k, dim3 grid, dim3 block, hipStream_t st, hipEvent_t 
 hipError_t launch_route(const RouteLaunch &l, hipStream_t st, hipEvent_t *ev) {
     RouteArgs a;
     a.W = l.W; a.x = l.x; a.bias = l.bias; a.prior = l.prior; a.table = l.table; a.dummy = l.dummy;
+    a.prior_on_logits = l.prior_on_logits;
     a.E = l.E; a.H = l.H; a.K = l.K;
     a.logits = l.logits; a.counter = l.counter; a.ids = l.ids; a.w = l.w; a.slots = l.slots;
     a.probs = l.probs; a.q8x = l.q8x;

@@ -439,6 +439,7 @@ size_t exp_ws_bytes(int I, int K) {
 int run_route(const moe_route_desc *d, hipStream_t st, hipEvent_t *ev = nullptr) {
     mp::RouteLaunch l{};
     l.W = d->W; l.x = d->x; l.bias = d->bias; l.prior = d->prior; l.table = d->table; l.dummy = d->dummy;
+    l.prior_on_logits = d->prior_on_logits;
     l.E = d->E; l.H = d->H; l.K = d->K; l.n_tok = d->n_tok;
     uint8_t *ws = (uint8_t *)d->workspace;
     l.logits = (float *)ws;
@@ -943,6 +944,7 @@ static int decode_layer_impl(moe_cache *c, int layer, const float *x, const floa
     rd.prior = c->d_prior ? c->d_prior + (size_t)layer * c->E : nullptr;
     rd.table = c->d_tbl + (size_t)layer * c->E;
     rd.dummy = ls.S;
+    rd.prior_on_logits = c->cfg.prior_on_logits;
     rd.E = c->E; rd.H = c->H; rd.K = c->K; rd.n_tok = 1;
     rd.ids = ids; rd.w = w; rd.slots = slots; rd.probs = nullptr; rd.q8x = c->d_q8x;
     rd.workspace = c->route_ws;

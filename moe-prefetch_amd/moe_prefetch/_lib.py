@@ -27,7 +27,7 @@ class MoeError(RuntimeError):
 
 class RouteDesc(ctypes.Structure):
     _fields_ = [("W", P), ("x", P), ("bias", P), ("prior", P), ("table", P), ("dummy", I32),
-                ("E", I32), ("H", I32), ("K", I32), ("n_tok", I32),
+                ("prior_on_logits", I32), ("E", I32), ("H", I32), ("K", I32), ("n_tok", I32),
                 ("ids", P), ("w", P), ("slots", P), ("probs", P), ("q8x", P), ("workspace", P)]
 
 
@@ -45,7 +45,7 @@ class CacheConfig(ctypes.Structure):
                 ("slot_profile", P), ("down_type", P), ("max_inserts", I32), ("admit_mode", I32),
                 ("admit_window", I32), ("admit_half", I32), ("admit_floor", F32),
                 ("batch_tables", I32), ("early_issue", I32), ("cache_prior", F32),
-                ("publish", I32), ("device", I32)]
+                ("prior_on_logits", I32), ("publish", I32), ("device", I32)]
 
 
 class CacheStats(ctypes.Structure):

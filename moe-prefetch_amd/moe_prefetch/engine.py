@@ -8,7 +8,8 @@ LLAMA_MOE_SLOT_PROFILE, `max_inserts` --moe-expert-cache-inserts, `admit`
 LLAMA_MOE_ADMIT (off | heat | window), `admit_window` / `admit_half` /
 `admit_floor` LLAMA_MOE_ADMIT_*, `batch_tables` LLAMA_MOE_BATCH_TABLES,
 `early_issue` LLAMA_MOE_EARLY_ISSUE, `cache_prior` LLAMA_MOE_CACHE_PRIOR (the
-delta added to resident experts' selection probabilities), `deterministic`
+delta added to resident experts' selection probabilities; `prior_space="logits"`
+adds it to the logits instead), `deterministic`
 LLAMA_MOE_DETERMINISTIC.  `MoeCache.from_env()` reads those variables.
 
 `device=-1` builds the state machine alone (no GPU, no weights, every upload
@@ -51,7 +52,8 @@ class MoeCache:
     def __init__(self, n_layers, n_experts=128, n_expert_used=8, hidden=2048, intermediate=768,
                  n_slots=56, slot_profile=None, down_types=None, max_inserts=2, admit="off",
                  admit_window=8, admit_half=64, admit_floor=1.0, batch_tables=False,
-                 early_issue=False, cache_prior=0.0, deterministic=False, publish=None, device=0):
+                 early_issue=False, cache_prior=0.0, prior_space="probs", deterministic=False, publish=None,
+                 device=0):
         if isinstance(slot_profile, str):
             slot_profile = parse_slot_profile(slot_profile, n_layers, n_slots)
         if isinstance(admit, str):
@@ -69,12 +71,14 @@ class MoeCache:
         cfg = _lib.CacheConfig(n_layers, n_experts, n_expert_used, hidden, intermediate, n_slots,
                                self._slots_arr.ctypes.data, self._dt_arr.ctypes.data, max_inserts, admit,
                                admit_window, admit_half, admit_floor, int(batch_tables),
-                               int(early_issue), float(cache_prior), _lib.PUBLISH[publish], device)
+                               int(early_issue), float(cache_prior), int(prior_space == "logits"),
+                               _lib.PUBLISH[publish], device)
         h = ctypes.c_void_p()
         check(lib().moe_cache_create(ctypes.byref(cfg), ctypes.byref(h)), "moe_cache_create")
         self.h = h.value
         self.device = device
         self.cache_prior = cache_prior
+        self.prior_space = prior_space
 
     @classmethod
     def from_env(cls, n_layers, n_slots, max_inserts=2, env=None, **shape):

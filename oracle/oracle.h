@@ -50,7 +50,8 @@
  *   ex[e]     = or_expf(logit[e] - m)
  *   s         = per 64-expert chunk a butterfly sum, chunks added in order.
  *   p[e]      = ex[e] / s
- *   sel[e]    = p[e] + prior[e]           (only when a prior table is given)
+ *   sel[e]    = p[e] + prior[e]           (only when a prior table is given;
+ *               logit[e] + prior[e] in the logits-space variant)
  *   ids       = k largest sel, descending, lower id first on equal values
  *   wsum      = p[ids[0]] + p[ids[1]] + ... (left to right)
  *   w[k]      = p[ids[k]] / wsum
@@ -95,6 +96,11 @@ float or_expf(float x);
 void or_route(int E, int H, int K, const float *W, const float *x, const float *bias,
               const float *prior, const int32_t *table, int32_t *ids, float *w,
               int32_t *slots, float *probs);
+/* as or_route; prior_on_logits = 1 adds the prior to the logits for the
+ * selection instead of to the probabilities (weights stay unbiased) */
+void or_route_space(int E, int H, int K, const float *W, const float *x, const float *bias,
+                    const float *prior, int prior_on_logits, const int32_t *table, int32_t *ids,
+                    float *w, int32_t *slots, float *probs);
 /* softmax/top-k part only, from given logits (batched prefill input) */
 void or_route_logits(int E, int K, const float *logits, const float *prior,
                      int32_t *ids, float *w, float *probs);

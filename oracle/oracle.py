@@ -72,6 +72,8 @@ def _declare(L):
     d("or_dot_deq_f64", ctypes.c_double, ctypes.c_int, ctypes.c_int, P, P)
     d("or_expf", F32, F32)
     d("or_route", None, ctypes.c_int, ctypes.c_int, ctypes.c_int, P, P, P, P, P, P, P, P, P)
+    d("or_route_space", None, ctypes.c_int, ctypes.c_int, ctypes.c_int, P, P, P, P, ctypes.c_int, P, P, P,
+      P, P)
     d("or_route_logits", None, ctypes.c_int, ctypes.c_int, P, P, P, P, P)
     d("or_expert_chain", None, ctypes.c_int, ctypes.c_int, ctypes.c_int, P, P, P, P, P, P)
     d("or_moe_layer", None, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, P, P, P, P,
@@ -141,7 +143,7 @@ def expf(x):
     return lib().or_expf(float(x))
 
 
-def route(W, x, K, bias=None, prior=None, table=None):
+def route(W, x, K, bias=None, prior=None, table=None, prior_on_logits=False):
     """W [E, H] f32, x [H] f32 -> (ids[K] i32, w[K] f32, slots[K] or None, probs[E])."""
     W = np.ascontiguousarray(W, np.float32)
     x = np.ascontiguousarray(x, np.float32)
@@ -153,8 +155,8 @@ def route(W, x, K, bias=None, prior=None, table=None):
     bias = None if bias is None else np.ascontiguousarray(bias, np.float32)
     prior = None if prior is None else np.ascontiguousarray(prior, np.float32)
     table = None if table is None else np.ascontiguousarray(table, np.int32)
-    lib().or_route(E, H, K, _p(W), _p(x), _p(bias), _p(prior), _p(table), _p(ids), _p(w),
-                   _p(slots), _p(probs))
+    lib().or_route_space(E, H, K, _p(W), _p(x), _p(bias), _p(prior), int(prior_on_logits), _p(table),
+                         _p(ids), _p(w), _p(slots), _p(probs))
     return ids, w, slots, probs
 
 

@@ -58,7 +58,7 @@ static float row_logit(int H, const float *w, const float *x) {
     return p[0];
 }
 
-static void softmax_topk(int E, int K, const float *logits, const float *prior,
+static void softmax_topk(int E, int K, const float *logits, const float *prior, int prior_on_logits,
                          int32_t *ids, float *w, float *probs_out) {
     float m = logits[0];
     for (int e = 1; e < E; ++e) if (logits[e] > m) m = logits[e];
@@ -77,7 +77,8 @@ static void softmax_topk(int E, int K, const float *logits, const float *prior,
     }
     for (int e = 0; e < E; ++e) {
         probs[e] = ex[e] / s;
-        sel[e] = prior ? probs[e] + prior[e] : probs[e];
+        if (!prior) sel[e] = probs[e];
+        else sel[e] = prior_on_logits ? logits[e] + prior[e] : probs[e] + prior[e];
     }
     unsigned char taken[1024] = {0};
     for (int k = 0; k < K; ++k) {
@@ -98,12 +99,18 @@ static void softmax_topk(int E, int K, const float *logits, const float *prior,
 void or_route(int E, int H, int K, const float *W, const float *x, const float *bias,
               const float *prior, const int32_t *table, int32_t *ids, float *w,
               int32_t *slots, float *probs) {
+    or_route_space(E, H, K, W, x, bias, prior, 0, table, ids, w, slots, probs);
+}
+
+void or_route_space(int E, int H, int K, const float *W, const float *x, const float *bias,
+                    const float *prior, int prior_on_logits, const int32_t *table, int32_t *ids,
+                    float *w, int32_t *slots, float *probs) {
     float logits[1024];
     for (int e = 0; e < E; ++e) {
         logits[e] = row_logit(H, W + (size_t)e * H, x);
         if (bias) logits[e] = logits[e] + bias[e];
     }
-    softmax_topk(E, K, logits, prior, ids, w, probs);
+    softmax_topk(E, K, logits, prior, prior_on_logits, ids, w, probs);
     if (table && slots) {
         for (int k = 0; k < K; ++k) slots[k] = table[ids[k]];
     }
@@ -111,5 +118,5 @@ void or_route(int E, int H, int K, const float *W, const float *x, const float *
 
 void or_route_logits(int E, int K, const float *logits, const float *prior,
                      int32_t *ids, float *w, float *probs) {
-    softmax_topk(E, K, logits, prior, ids, w, probs);
+    softmax_topk(E, K, logits, prior, 0, ids, w, probs);
 }

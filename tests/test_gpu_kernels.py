@@ -46,7 +46,7 @@ def test_device_generator_matches_host(dt, I):
     assert np.array_equal(v.cpu().numpy(), vh)
 
 
-def run_route(W, x, K, bias=None, prior=None, table=None, dummy=None, probs=True):
+def run_route(W, x, K, bias=None, prior=None, table=None, dummy=None, probs=True, prior_on_logits=False):
     E, Hh = W.shape
     n_tok = x.shape[0]
     Wd, xd = t_(W), t_(x)
@@ -61,7 +61,7 @@ def run_route(W, x, K, bias=None, prior=None, table=None, dummy=None, probs=True
     ws = torch.zeros(L().moe_route_workspace_bytes(E, n_tok), dtype=torch.uint8, device=DEV)
     d = _lib.RouteDesc(Wd.data_ptr(), xd.data_ptr(), None if bd is None else bd.data_ptr(),
                        None if pd is None else pd.data_ptr(), None if td is None else td.data_ptr(),
-                       E if dummy is None else dummy, E, Hh, K, n_tok, ids.data_ptr(), w.data_ptr(),
+                       E if dummy is None else dummy, int(prior_on_logits), E, Hh, K, n_tok, ids.data_ptr(), w.data_ptr(),
                        slots.data_ptr(), pr.data_ptr() if probs else None, q8.data_ptr(), ws.data_ptr())
     _lib.check(L().moe_route(ctypes.byref(d), stream()), "moe_route")
     torch.cuda.synchronize()
@@ -95,6 +95,26 @@ def test_route_bit_exact(E, K, n_tok):
             else:
                 assert np.all(slots[t] == 56)
             assert np.array_equal(q8[t], O.quant_q8k(x[t]))
+
+
+def test_route_prior_on_logits_bit_exact():
+    rng = np.random.default_rng(8)
+    E, K = 128, 8
+    for trial in range(4):
+        W = (rng.standard_normal((E, H)) * 0.02).astype(np.float32)
+        x = rng.standard_normal((3, H)).astype(np.float32)
+        table = np.where(rng.random(E) < 0.5, np.arange(E) % 56, 56).astype(np.int32)
+        prior = np.where(table < 56, 0.3, 0.0).astype(np.float32)
+        ids, w, slots, probs, _ = run_route(W, x, K, None, prior, table, dummy=56, prior_on_logits=True)
+        for t in range(3):
+            rids, rw, rslots, _ = O.route(W, x[t], K, prior=prior, table=table, prior_on_logits=True)
+            assert np.array_equal(ids[t], rids)
+            assert np.array_equal(w[t].view(np.uint32), rw.view(np.uint32))
+            assert np.array_equal(slots[t], rslots)
+            pids, _, _, _ = O.route(W, x[t], K, prior=prior, table=table)
+            # with a 0.3 bonus the two spaces pick differently on these inputs
+            if trial == 0 and t == 0:
+                assert not np.array_equal(pids, rids)
 
 
 def test_route_integer_ties_lower_id_wins():

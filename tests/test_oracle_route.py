@@ -106,6 +106,20 @@ def test_route_prior_changes_selection_not_weights():
     assert np.array_equal(slots, table[ids1])
 
 
+def test_route_prior_on_logits():
+    # logits-space prior: selection = logit + prior (weights unbiased), checked in fp64
+    E, H, K = 128, 2048, 8
+    rng2 = np.random.default_rng(4)
+    W = (rng2.standard_normal((E, H)) * 0.02).astype(np.float32)
+    x = rng2.standard_normal(H).astype(np.float32)
+    prior = np.where(rng2.random(E) < 0.4, 0.25, 0.0).astype(np.float32)
+    ids, w, _, probs = O.route(W, x, K, prior=prior, prior_on_logits=True)
+    lg = W.astype(np.float64) @ x.astype(np.float64) + prior
+    order = sorted(range(E), key=lambda e: (-lg[e], e))
+    assert sorted(ids.tolist()) == sorted(order[:K])
+    assert np.allclose(w, probs[ids] / probs[ids].sum(), rtol=1e-6)
+
+
 def test_route_bias_steers():
     E, H, K = 128, 2048, 8
     W = (rng.standard_normal((E, H)) * 0.02).astype(np.float32)
