@@ -26,6 +26,13 @@
  *   moe_decode_token        llama_context::decode for one token over every cached layer followed by
  *                           llama_moe_cache_step (0008:362-369)
  *   moe_pool_*              the slab/slot store behind src/prefetch_engine.py ExpertCache (:45-168)
+ *   moe_dispatch            ggml mul_mat_id's batch row mapping (per-expert counts + mmid_row_mapping,
+ *                           visible in 0008:157-167): histogram, exclusive scan, stable (token, k) order
+ *   moe_grouped_experts     build_moe_ffn at n_tokens > 1: mul_mat_id(up/gate) -> swiglu ->
+ *                           mul_mat_id(down) -> mul(weights) over the dispatched pairs (un-vendored upstream;
+ *                           the reference's cache path stops at one token, 0007:114)
+ *   moe_combine             the sum over k of the weighted expert rows (0009:697-703, order per 0009:355)
+ *   moe_quant_rows          ggml's quantize_row_q8_K of the activations, in the form the matrix cores read
  * No counterpart in the reference: moe_host_alloc/free (the reference pins the model buffer
  * through ggml's CUDA_Host buffer type), moe_synth_* (seeded synthetic weights and inputs).
  */
@@ -51,6 +58,9 @@ extern "C" {
 
 #define MOE_TYPE_Q4K 12     /* ggml type ids */
 #define MOE_TYPE_Q6K 14
+
+#define MOE_DTYPE_F32  0    /* activation element types */
+#define MOE_DTYPE_BF16 1
 
 const char *moe_last_error(void);   /* message of the last failure on this thread */
 int moe_abi_version(void);
@@ -82,8 +92,9 @@ int moe_synth_experts(uint64_t seed, int layer, int e0, int n, int H, int I, int
                       float sigma, void *out_dev, size_t stride, void *stream);
 int moe_synth_experts_host(uint64_t seed, int layer, int e0, int n, int H, int I, int down_type,
                            float sigma, void *out_host, size_t stride, int n_threads);
-/* out[(a - a0)][(b - b0)][i] = N(0, sigma) value (kind, a, b, i), n values per (a, b).
- * kinds: 0 router rows (a = layer, b = expert), 1 activations (a = token, b = layer). */
+/* out[(a - a0)][(b - b0)][i] = value (kind, a, b, i), n values per (a, b).
+ * kinds: 0 router rows (a = layer, b = expert), 1 activations (a = token, b = layer): N(0, sigma);
+ *        2 router logits (a = token, b = layer): uniform on [0, sigma). */
 int moe_synth_vec(uint64_t seed, int kind, int a0, int na, int b0, int nb, int n, float sigma,
                   float *out_dev, void *stream);
 int moe_synth_vec_host(uint64_t seed, int kind, int a0, int na, int b0, int nb, int n, float sigma,
@@ -105,8 +116,11 @@ typedef struct {
     float *w;              /* dev out [n_tok][K], probs[ids] / sum(probs[ids]) */
     int32_t *slots;        /* dev out [n_tok][K] */
     float *probs;          /* dev out [n_tok][E] or NULL */
-    uint8_t *q8x;          /* dev out [n_tok][H/256] Q8_K blocks of x (292 B each) */
+    uint8_t *q8x;          /* dev out [n_tok][H/256] Q8_K blocks of x (292 B each); may be NULL
+                              with given logits */
     void *workspace;       /* dev, moe_route_workspace_bytes(); zero before first use */
+    const float *logits;   /* dev [n_tok][E] or NULL: given router logits (W and x unused for
+                              them; bias still added) */
 } moe_route_desc;
 
 typedef struct {
@@ -226,6 +240,51 @@ int moe_decode_layer(moe_cache *c, int layer, const float *x, const float *bias,
  * layer order and the cache steps.  ids_host [L][K] receives them when not NULL. */
 int moe_decode_token(moe_cache *c, const float *x, const float *bias, float *out, int32_t *ids_host,
                      void *stream);
+
+/* ---- batched path: prefill chunks and decode at batch > 1 ------------------- */
+/* Dispatch of the (token, k) pairs of ids dev [n_tok][K] (pair i = t*K + k):
+ * counts[e] pairs routed to expert e, offsets[e] = exclusive scan (offsets[E] =
+ * pairs placed), perm[offsets[e] + r] = i of the r-th pair routed to e in pair
+ * order.  Ids outside [0, E) are not placed.  E <= 256, n_tok * K <= 65535. */
+int moe_dispatch(const int32_t *ids, int n_tok, int K, int E, int32_t *counts, int32_t *offsets,
+                 int32_t *perm, void *stream);
+/* Q8_K of n_rows rows of n values (n a multiple of 256), f32 or bf16: q16 the
+ * int8 values as fp16 codes [n_rows][n], d the block scales [n_rows][n/256],
+ * bsum16 the 16-value group sums as fp16 [n_rows][n/16].  All exact; the values
+ * and scales are those of ggml's quantize_row_q8_K. */
+int moe_quant_rows(const void *src, int src_type, int n_rows, int n, uint16_t *q16, float *d,
+                   uint16_t *bsum16, void *stream);
+
+typedef struct {
+    const int32_t *offsets;     /* dev [E+1] from moe_dispatch */
+    const int32_t *perm;        /* dev [n_tok*K] from moe_dispatch */
+    const float *w;             /* dev [n_tok][K] gate weights */
+    const void *x;              /* dev [n_tok][H] activations, MOE_DTYPE_F32 or MOE_DTYPE_BF16 */
+    int32_t x_type;
+    int32_t n_tok, K, E, H, I, down_type;
+    const int32_t *table;       /* dev [E] slot per expert (>= n_slots: not resident) or NULL */
+    const uint8_t *slot_pool;   /* dev [n_slots][slot_bytes] or NULL */
+    uint64_t slot_bytes;
+    int32_t n_slots;
+    const uint8_t *store;       /* device address of [n_store][expert_bytes]: HBM, or pinned host
+                                   memory through moe_host_device_ptr */
+    uint64_t expert_bytes;
+    int32_t n_store;            /* an expert neither resident nor in the store contributes zero */
+    float *out;                 /* dev [n_tok][H] */
+    int32_t accumulate;         /* 1: out += result */
+    float *pair_out;            /* dev [n_tok*K][H] weighted expert rows in pair order, or NULL */
+    float *h_out;               /* dev [n_tok*K][I] SwiGLU activations in dispatch order, or NULL */
+    void *workspace;            /* dev, moe_grouped_workspace_bytes() */
+    float *kernel_ms;           /* host [2] or NULL: when set the call waits for its kernels and
+                                   stores the up/gate and down kernel durations (HIP events) */
+} moe_grouped_desc;
+
+size_t moe_grouped_workspace_bytes(int n_tok, int K, int H, int I);
+/* Q8_K of x, up/gate over each expert's pairs with the SwiGLU, Q8_K of h, down
+ * times the gate weight, and the sum over k (moe_combine) into out. */
+int moe_grouped_experts(const moe_grouped_desc *d, void *stream);
+/* out[t] (+)= sum_k pair_rows[t*K + k], k ascending */
+int moe_combine(const float *pair_rows, int n_tok, int K, int H, float *out, int accumulate, void *stream);
 
 /* ---- slab pool behind the Python ExpertCache ------------------------------- */
 typedef struct moe_pool moe_pool;

@@ -1,0 +1,99 @@
+// mp_device.h -- device helpers shared by the batch-1 kernels (mp_kernels.hip)
+// and the batched kernels (mp_batched.hip).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include "mp_format.h"
+
+namespace mp {
+
+// canonical exp (same polynomial and constants as the oracle's or_expf)
+__device__ inline float canon_expf(float x) {
+    if (x < -87.0f) return 0.0f;
+    if (x > 88.0f) x = 88.0f;
+    const float n = rintf(x * 1.44269504088896341f);
+    float r = fmaf(n, -0.693145751953125f, x);
+    r = fmaf(n, -1.428606765330187045e-06f, r);
+    float p = 1.9841269841269841e-04f;
+    p = fmaf(p, r, 1.3888888888888889e-03f);
+    p = fmaf(p, r, 8.3333333333333333e-03f);
+    p = fmaf(p, r, 4.1666666666666667e-02f);
+    p = fmaf(p, r, 1.6666666666666667e-01f);
+    p = fmaf(p, r, 0.5f);
+    p = fmaf(p, r, 1.0f);
+    p = fmaf(p, r, 1.0f);
+    const uint32_t e = (uint32_t)((int32_t)n + 127);
+    return p * bits_f32(e << 23);
+}
+
+__device__ inline float bfly_add(float v) {
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) v = v + __shfl_xor(v, o, 64);
+    return v;
+}
+
+__device__ inline int32_t sdot4(uint32_t a, uint32_t b, int32_t c) {
+    return __builtin_amdgcn_sdot4((int)a, (int)b, c, false);
+}
+
+// Q8_K of 256 values held 4 per lane (lane-major) by one wavefront: the
+// largest magnitude (first index on a tie) maps to -127, q = min(127,
+// rint(x * iscale)); d = 1 / iscale, 0 for an all-zero block.
+__device__ inline void q8k_wave_vals(const float xv[4], int lane, int q[4], float &d) {
+    float amax = 0.0f, mx = 0.0f;
+    int idx = 1 << 30;
+    for (int i = 0; i < 4; ++i) {
+        const float ax = fabsf(xv[i]);
+        if (ax > amax) { amax = ax; mx = xv[i]; idx = 4 * lane + i; }
+    }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) {
+        const float oa = __shfl_xor(amax, o, 64);
+        const float om = __shfl_xor(mx, o, 64);
+        const int oi = __shfl_xor(idx, o, 64);
+        if (oa > amax || (oa == amax && oi < idx)) { amax = oa; mx = om; idx = oi; }
+    }
+    q[0] = q[1] = q[2] = q[3] = 0;
+    d = 0.0f;
+    if (amax != 0.0f) {
+        const float iscale = -127.0f / mx;
+        for (int i = 0; i < 4; ++i) {
+            const int t = (int)rintf(iscale * xv[i]);
+            q[i] = t < 127 ? t : 127;
+        }
+        d = 1.0f / iscale;
+    }
+}
+
+// the 16-value group sum of the Q8_K block, valid on lanes with (lane & 3) == 0
+__device__ inline int q8k_group_sum(const int q[4]) {
+    int gs = q[0] + q[1] + q[2] + q[3];
+    gs += __shfl_xor(gs, 1, 64);
+    gs += __shfl_xor(gs, 2, 64);
+    return gs;
+}
+
+// byte i (0..11) of the Q4_K scale field held in three words
+__device__ inline int sc_byte(const uint4 &hdr, int i) {
+    const uint32_t w = i < 4 ? hdr.y : (i < 8 ? hdr.z : hdr.w);
+    return (int)((w >> (8 * (i & 3))) & 0xffu);
+}
+
+// six-bit (scale, min) of sub-block j from a Q4_K header (d, dmin, 12 scale bytes)
+__device__ inline void q4k_sm(const uint4 &hdr, int j, int &sc, int &m) {
+    if (j < 4) {
+        sc = sc_byte(hdr, j) & 63;
+        m = sc_byte(hdr, j + 4) & 63;
+    } else {
+        sc = (sc_byte(hdr, j + 4) & 0xF) | ((sc_byte(hdr, j - 4) >> 6) << 4);
+        m = (sc_byte(hdr, j + 4) >> 4) | ((sc_byte(hdr, j) >> 6) << 4);
+    }
+}
+
+__device__ inline uint32_t lds_u32_at2(const uint8_t *p) {   // 2-byte aligned
+    const uint16_t *q = (const uint16_t *)p;
+    return (uint32_t)q[0] | ((uint32_t)q[1] << 16);
+}
+
+}  // namespace mp

@@ -16,6 +16,7 @@ struct RouteLaunch {
     int32_t dummy;
     int prior_on_logits;   // 1: the prior is added to the logits (selection only)
     int E, H, K, n_tok;
+    const float *logits_in; // [n_tok][E] given logits (no router GEMV) or null
     float *logits;         // scratch [n_tok][E]
     uint32_t *counter;     // scratch [n_tok], zero
     int32_t *ids;          // out [n_tok][K]
@@ -43,6 +44,39 @@ struct ExpertArgs {
     int accumulate;           // 1: out += result
     int H, I, K, down_type;
 };
+
+constexpr int MAX_E = 256;   // experts per layer the kernels support
+
+// batched layer: pairs dispatched expert-major, experts from slots or a store
+struct GroupedArgs {
+    const int32_t *offsets;     // [E+1] from the dispatch
+    const int32_t *perm;        // [P] pair index t*K + k, expert-major
+    const float *w;             // [n_tok*K] gate weights
+    const int32_t *table;       // [E] slot per expert (>= n_slots: not resident) or null
+    const uint8_t *slot_pool;   // [n_slots][slot_bytes] in HBM
+    uint64_t slot_bytes;
+    int n_slots;
+    const uint8_t *store;       // [n_store][expert_bytes]: HBM or device view of pinned memory
+    uint64_t expert_bytes;
+    int n_store;
+    int E, K, H, I, down_type;
+    const uint16_t *xa;         // [n_tok][H] Q8_K values of x as fp16
+    const float *xdx;           // [n_tok][H/256]
+    const uint16_t *xbs;        // [n_tok][H/16] group sums as fp16
+    float *h;                   // [P][I] dispatch order
+    const uint16_t *ha;         // [P][I] Q8_K of h as fp16
+    const float *hdx;           // [P][I/256]
+    const uint16_t *hbs;        // [P][I/16]
+    float *ypair;               // [P][H] weighted rows, pair (t*K + k) order
+};
+
+hipError_t launch_dispatch(const int32_t *ids, int P, int E, int32_t *counts, int32_t *offsets, int32_t *perm,
+                           hipStream_t st);
+hipError_t launch_quant_rows(const void *src, int bf16, int n_rows, int n, uint16_t *q16, float *dx, uint16_t *bs16,
+                             hipStream_t st);
+hipError_t launch_gateup_grouped(const GroupedArgs &a, hipStream_t st, hipEvent_t e0, hipEvent_t e1);
+hipError_t launch_down_grouped(const GroupedArgs &a, hipStream_t st, hipEvent_t e0, hipEvent_t e1);
+hipError_t launch_combine(const float *ypair, int n_tok, int K, int H, float *out, int accumulate, hipStream_t st);
 
 // ev (optional): [logits start, logits end, select start, select end]
 hipError_t launch_route(const RouteLaunch &l, hipStream_t st, hipEvent_t *ev = nullptr);

@@ -22,73 +22,21 @@
 #include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 
+#include "mp_device.h"
 #include "mp_format.h"
 #include "mp_internal.h"
 #include "mp_synth.h"
 
 namespace mp {
 
-// ---------------------------------------------------------------------------
-// canonical exp (same polynomial and constants as the oracle's or_expf)
-__device__ inline float canon_expf(float x) {
-    if (x < -87.0f) return 0.0f;
-    if (x > 88.0f) x = 88.0f;
-    const float n = rintf(x * 1.44269504088896341f);
-    float r = fmaf(n, -0.693145751953125f, x);
-    r = fmaf(n, -1.428606765330187045e-06f, r);
-    float p = 1.9841269841269841e-04f;
-    p = fmaf(p, r, 1.3888888888888889e-03f);
-    p = fmaf(p, r, 8.3333333333333333e-03f);
-    p = fmaf(p, r, 4.1666666666666667e-02f);
-    p = fmaf(p, r, 1.6666666666666667e-01f);
-    p = fmaf(p, r, 0.5f);
-    p = fmaf(p, r, 1.0f);
-    p = fmaf(p, r, 1.0f);
-    const uint32_t e = (uint32_t)((int32_t)n + 127);
-    return p * bits_f32(e << 23);
-}
-
-__device__ inline float bfly_add(float v) {
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) v = v + __shfl_xor(v, o, 64);
-    return v;
-}
-
-__device__ inline int32_t sdot4(uint32_t a, uint32_t b, int32_t c) {
-    return __builtin_amdgcn_sdot4((int)a, (int)b, c, false);
-}
-
-// One wavefront quantizes 256 values (4 per lane, lane-major) to a Q8_K block:
-// largest magnitude (first index on a tie) -> -127, q = min(127, rint(x*iscale)).
+// One wavefront quantizes 256 values (4 per lane, lane-major) to a Q8_K block.
 __device__ void q8k_wave(const float *x, uint8_t *out, int lane) {
     const float4 v = *(const float4 *)(x + 4 * lane);
-    float xv[4] = {v.x, v.y, v.z, v.w};
-    float amax = 0.0f, mx = 0.0f;
-    int idx = 1 << 30;
-    for (int i = 0; i < 4; ++i) {
-        const float ax = fabsf(xv[i]);
-        if (ax > amax) { amax = ax; mx = xv[i]; idx = 4 * lane + i; }
-    }
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) {
-        const float oa = __shfl_xor(amax, o, 64);
-        const float om = __shfl_xor(mx, o, 64);
-        const int oi = __shfl_xor(idx, o, 64);
-        if (oa > amax || (oa == amax && oi < idx)) { amax = oa; mx = om; idx = oi; }
-    }
-    int q[4] = {0, 0, 0, 0};
-    float d = 0.0f;
-    if (amax != 0.0f) {
-        const float iscale = -127.0f / mx;
-        for (int i = 0; i < 4; ++i) {
-            const int t = (int)rintf(iscale * xv[i]);
-            q[i] = t < 127 ? t : 127;
-        }
-        d = 1.0f / iscale;
-    }
-    int gs = q[0] + q[1] + q[2] + q[3];
-    gs += __shfl_xor(gs, 1, 64);
-    gs += __shfl_xor(gs, 2, 64);
+    const float xv[4] = {v.x, v.y, v.z, v.w};
+    int q[4];
+    float d;
+    q8k_wave_vals(xv, lane, q, d);
+    const int gs = q8k_group_sum(q);
     const uint32_t packed = (uint32_t)(q[0] & 0xff) | ((uint32_t)(q[1] & 0xff) << 8) |
                             ((uint32_t)(q[2] & 0xff) << 16) | ((uint32_t)(q[3] & 0xff) << 24);
     *(uint32_t *)(out + 4 + 4 * lane) = packed;
@@ -107,6 +55,7 @@ struct RouteArgs {
     int32_t dummy;         // slot value for "absent" when no table
     int prior_on_logits;   // 1: prior added to the logits for the selection
     int E, H, K;
+    const float *logits_in; // [n_tok][E] given logits (the GEMV is skipped; bias still added) or null
     float *logits;         // scratch [n_tok][E]
     uint32_t *counter;     // scratch [n_tok], zero between launches
     int32_t *ids;          // [n_tok][K]
@@ -141,18 +90,24 @@ __global__ __launch_bounds__(256) void route_logits_kernel(RouteArgs a) {
 }
 
 // One workgroup per token: softmax, + prior, top-k (lower id on ties),
-// renormalised weights, slot lookup (wave 0); Q8_K of x (all four waves).
+// renormalised weights, slot lookup (wave 0); Q8_K of x (all four waves)
+// when x and q8x are given.
 __global__ __launch_bounds__(256) void route_select_kernel(RouteArgs a) {
     const int tok = blockIdx.x;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const float *x = a.x + (size_t)tok * a.H;
     __shared__ float s_p[256];
     __shared__ int s_ids[16];
     if (wave == 0) {
-        const float *lg = a.logits + (size_t)tok * a.E;
         const int nc = a.E / 64;
         float l4[4];
-        for (int c = 0; c < nc; ++c) l4[c] = lg[64 * c + lane];
+        if (a.logits_in) {
+            const float *lg = a.logits_in + (size_t)tok * a.E;
+            const float *bs = a.bias ? a.bias + (size_t)tok * a.E : nullptr;
+            for (int c = 0; c < nc; ++c) l4[c] = bs ? lg[64 * c + lane] + bs[64 * c + lane] : lg[64 * c + lane];
+        } else {
+            const float *lg = a.logits + (size_t)tok * a.E;
+            for (int c = 0; c < nc; ++c) l4[c] = lg[64 * c + lane];
+        }
         float m = l4[0];
         for (int c = 1; c < nc; ++c) m = fmaxf(m, l4[c]);
 #pragma unroll
@@ -201,6 +156,8 @@ __global__ __launch_bounds__(256) void route_select_kernel(RouteArgs a) {
             a.slots[(size_t)tok * a.K + lane] = a.table ? a.table[id] : a.dummy;
         }
     }
+    if (!a.x || !a.q8x) return;
+    const float *x = a.x + (size_t)tok * a.H;
     uint8_t *q8 = a.q8x + (size_t)tok * (a.H / QK) * Q8K_BYTES;
     for (int b = wave; b < a.H / QK; b += 4) q8k_wave(x + QK * b, q8 + (size_t)b * Q8K_BYTES, lane);
 }
@@ -225,22 +182,6 @@ __device__ inline const uint8_t *expert_base(const ExpertArgs &a, int k) {
     const int id = a.ids[k];
     if (!a.host_store || id < 0 || id >= a.n_experts) return nullptr;
     return a.host_store + (size_t)id * a.expert_bytes;
-}
-
-// byte i (0..11) of the Q4_K scale field held in three words
-__device__ inline int sc_byte(const uint4 &hdr, int i) {
-    const uint32_t w = i < 4 ? hdr.y : (i < 8 ? hdr.z : hdr.w);
-    return (int)((w >> (8 * (i & 3))) & 0xffu);
-}
-
-__device__ inline void q4k_sm(const uint4 &hdr, int j, int &sc, int &m) {
-    if (j < 4) {
-        sc = sc_byte(hdr, j) & 63;
-        m = sc_byte(hdr, j + 4) & 63;
-    } else {
-        sc = (sc_byte(hdr, j + 4) & 0xF) | ((sc_byte(hdr, j - 4) >> 6) << 4);
-        m = (sc_byte(hdr, j + 4) >> 4) | ((sc_byte(hdr, j) >> 6) << 4);
-    }
 }
 
 // Q4_K super-block partial of one lane: 16 qs bytes (chunk u) against the
@@ -321,7 +262,7 @@ __global__ __launch_bounds__(256) void gateup_kernel(ExpertArgs a) {
         }
         if (lane == 0) {
             const float g = res[0], uu = res[1];
-            a.h[(size_t)k * a.I + row0 + r] = g / (1.0f + expf(-g)) * uu;
+            a.h[(size_t)k * a.I + row0 + r] = g / (1.0f + canon_expf(-g)) * uu;
         }
     }
 
@@ -333,11 +274,6 @@ __global__ __launch_bounds__(256) void gateup_kernel(ExpertArgs a) {
 constexpr int DN_ROWS = 8;
 constexpr int DN_LDS_ROWS = 5040;           // 8 Q6_K rows at I = 768
 constexpr int DN_LDS_Q8 = 3 * Q8K_BYTES;    // I <= 768
-
-__device__ inline uint32_t lds_u32_at2(const uint8_t *p) {   // 2-byte aligned
-    const uint16_t *q = (const uint16_t *)p;
-    return (uint32_t)q[0] | ((uint32_t)q[1] << 16);
-}
 
 template <int DT, int SRC>
 __global__ __launch_bounds__(512) void down_kernel(ExpertArgs a) {
@@ -491,7 +427,10 @@ hipError_t launch_route(const RouteLaunch &l, hipStream_t st, hipEvent_t *ev) {
     a.prior_on_logits = l.prior_on_logits;
     a.E = l.E; a.H = l.H; a.K = l.K;
     a.logits = l.logits; a.counter = l.counter; a.ids = l.ids; a.w = l.w; a.slots = l.slots;
-    a.probs = l.probs; a.q8x = l.q8x;
+    a.probs = l.probs; a.q8x = l.q8x; a.logits_in = l.logits_in;
+    if (l.logits_in)
+        return launch(route_select_kernel, dim3((unsigned)l.n_tok), dim3(256), st, ev ? ev[2] : nullptr,
+                      ev ? ev[3] : nullptr, a);
     const hipError_t e = launch(route_logits_kernel, dim3((unsigned)(l.E / 4), (unsigned)l.n_tok), dim3(256), st,
                                 ev ? ev[0] : nullptr, ev ? ev[1] : nullptr, a);
     if (e != hipSuccess) return e;

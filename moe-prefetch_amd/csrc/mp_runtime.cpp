@@ -445,6 +445,7 @@ int run_route(const moe_route_desc *d, hipStream_t st, hipEvent_t *ev = nullptr)
     l.logits = (float *)ws;
     l.counter = (uint32_t *)(ws + align_up((size_t)d->n_tok * d->E * 4, 256));
     l.ids = d->ids; l.w = d->w; l.slots = d->slots; l.probs = d->probs; l.q8x = d->q8x;
+    l.logits_in = d->logits;
     HIPCHK(mp::launch_route(l, st, ev));
     return MOE_OK;
 }
@@ -464,6 +465,43 @@ int run_experts(const moe_experts_desc *d, hipStream_t st) {
     a.counter = (uint32_t *)(ws + o);
     HIPCHK(mp::launch_experts(a, st));
     return MOE_OK;
+}
+
+// A kernel read of unmapped memory faults the GPU: refuse anything the runtime
+// does not know as device memory or device-mapped pinned memory.
+int check_weight_ptrs(const char *who, const void *a, const void *b) {
+    for (const void *p : {a, b}) {
+        if (!p) continue;
+        hipPointerAttribute_t at{};
+        if (hipPointerGetAttributes(&at, p) != hipSuccess || (at.type != hipMemoryTypeDevice &&
+                                                              at.type != hipMemoryTypeHost &&
+                                                              at.type != hipMemoryTypeUnified))
+            return fail(MOE_ERR_ARG, "%s: %p is not device memory or mapped pinned memory", who, p);
+        if (at.type == hipMemoryTypeHost && at.devicePointer != p)
+            return fail(MOE_ERR_ARG, "%s: pass the device address of pinned memory (moe_host_device_ptr)", who);
+    }
+    return MOE_OK;
+}
+
+// workspace of the batched expert path, offsets in bytes
+struct GroupedWs {
+    size_t xa, xdx, xbs, h, ha, hdx, hbs, ypair, total;
+};
+
+GroupedWs grouped_ws(int n_tok, int K, int H, int I) {
+    const size_t T = (size_t)n_tok, P = (size_t)n_tok * K;
+    GroupedWs w{};
+    size_t o = 0;
+    w.xa = o;    o += align_up(T * H * 2, 256);
+    w.xdx = o;   o += align_up(T * (H / 256) * 4, 256);
+    w.xbs = o;   o += align_up(T * (H / 16) * 2, 256);
+    w.h = o;     o += align_up(P * I * 4, 256);
+    w.ha = o;    o += align_up(P * I * 2, 256);
+    w.hdx = o;   o += align_up(P * (I / 256) * 4, 256);
+    w.hbs = o;   o += align_up(P * (I / 16) * 2, 256);
+    w.ypair = o; o += align_up(P * H * 4, 256);
+    w.total = o;
+    return w;
 }
 
 void free_cache(moe_cache *c) {
@@ -635,8 +673,9 @@ size_t moe_route_workspace_bytes(int E, int n_tok) { return route_ws_bytes(E, n_
 size_t moe_experts_workspace_bytes(int I, int K) { return exp_ws_bytes(I, K); }
 
 int moe_route(const moe_route_desc *d, void *stream) {
-    if (!d || !d->W || !d->x || !d->ids || !d->w || !d->slots || !d->q8x || !d->workspace)
-        return fail(MOE_ERR_ARG, "moe_route: null argument");
+    if (!d || !d->ids || !d->w || !d->slots || !d->workspace) return fail(MOE_ERR_ARG, "moe_route: null argument");
+    if (!d->logits && (!d->W || !d->x || !d->q8x))
+        return fail(MOE_ERR_ARG, "moe_route: W, x and q8x are required without given logits");
     int r = check_shape(d->E, d->H, 0, d->K);
     if (r != MOE_OK) return r;
     if (d->n_tok < 1 || d->n_tok > 65535) return fail(MOE_ERR_ARG, "n_tok %d out of range", d->n_tok);
@@ -658,18 +697,8 @@ int moe_experts(const moe_experts_desc *d, void *stream) {
         return fail(MOE_ERR_ARG, "slot_bytes must be >= expert_bytes and a multiple of 16");
     if (((uintptr_t)d->slot_pool | (uintptr_t)d->host_store | (uintptr_t)d->q8x) % 16)
         return fail(MOE_ERR_ARG, "weights and activations must be 16-byte aligned");
-    // a kernel read of unmapped memory faults the GPU: refuse anything the
-    // runtime does not know as device memory or device-mapped pinned memory
-    for (const void *p : {(const void *)d->slot_pool, (const void *)d->host_store}) {
-        if (!p) continue;
-        hipPointerAttribute_t at{};
-        if (hipPointerGetAttributes(&at, p) != hipSuccess || (at.type != hipMemoryTypeDevice &&
-                                                              at.type != hipMemoryTypeHost &&
-                                                              at.type != hipMemoryTypeUnified))
-            return fail(MOE_ERR_ARG, "moe_experts: %p is not device memory or mapped pinned memory", p);
-        if (at.type == hipMemoryTypeHost && at.devicePointer != p)
-            return fail(MOE_ERR_ARG, "moe_experts: pass the device address of pinned memory (moe_host_device_ptr)");
-    }
+    const int r2 = check_weight_ptrs("moe_experts", d->slot_pool, d->host_store);
+    if (r2 != MOE_OK) return r2;
     return run_experts(d, (hipStream_t)stream);
 }
 
@@ -1079,6 +1108,103 @@ int moe_decode_token(moe_cache *c, const float *x, const float *bias, float *out
     }
     if (ids_host) memcpy(ids_host, c->h_ids, (size_t)NL * c->K * 4);
     return cache_step(c);
+}
+
+// ---- batched path -------------------------------------------------------------
+int moe_dispatch(const int32_t *ids, int n_tok, int K, int E, int32_t *counts, int32_t *offsets, int32_t *perm,
+                 void *stream) {
+    if (!ids || !counts || !offsets || !perm) return fail(MOE_ERR_ARG, "moe_dispatch: null argument");
+    if (E < 1 || E > mp::MAX_E) return fail(MOE_ERR_ARG, "moe_dispatch: n_experts %d must be 1..%d", E, mp::MAX_E);
+    if (n_tok < 0 || K < 1 || (int64_t)n_tok * K > 65535)
+        return fail(MOE_ERR_ARG, "moe_dispatch: n_tok * K must be <= 65535 (n_tok %d, K %d)", n_tok, K);
+    HIPCHK(mp::launch_dispatch(ids, n_tok * K, E, counts, offsets, perm, (hipStream_t)stream));
+    return MOE_OK;
+}
+
+int moe_quant_rows(const void *src, int src_type, int n_rows, int n, uint16_t *q16, float *d, uint16_t *bsum16,
+                   void *stream) {
+    if (!src || !q16 || !d || !bsum16) return fail(MOE_ERR_ARG, "moe_quant_rows: null argument");
+    if (src_type != MOE_DTYPE_F32 && src_type != MOE_DTYPE_BF16)
+        return fail(MOE_ERR_ARG, "moe_quant_rows: src_type %d unsupported", src_type);
+    if (n_rows < 0 || n <= 0 || n % 256) return fail(MOE_ERR_ARG, "moe_quant_rows: n %d must be a multiple of 256", n);
+    if (((uintptr_t)src | (uintptr_t)q16) % 16) return fail(MOE_ERR_ARG, "moe_quant_rows: src and q16 must be 16-byte aligned");
+    HIPCHK(mp::launch_quant_rows(src, src_type == MOE_DTYPE_BF16, n_rows, n, q16, d, bsum16, (hipStream_t)stream));
+    return MOE_OK;
+}
+
+size_t moe_grouped_workspace_bytes(int n_tok, int K, int H, int I) {
+    if (n_tok < 0 || K < 1 || H < 256 || I < 256) return 0;
+    return grouped_ws(n_tok, K, H, I).total;
+}
+
+int moe_combine(const float *pair_rows, int n_tok, int K, int H, float *out, int accumulate, void *stream) {
+    if (!pair_rows || !out) return fail(MOE_ERR_ARG, "moe_combine: null argument");
+    if (n_tok < 0 || K < 1 || H <= 0 || H % 4) return fail(MOE_ERR_ARG, "moe_combine: bad shape");
+    if (((uintptr_t)pair_rows | (uintptr_t)out) % 16) return fail(MOE_ERR_ARG, "moe_combine: 16-byte alignment");
+    HIPCHK(mp::launch_combine(pair_rows, n_tok, K, H, out, accumulate, (hipStream_t)stream));
+    return MOE_OK;
+}
+
+int moe_grouped_experts(const moe_grouped_desc *d, void *stream) {
+    if (!d || !d->offsets || !d->perm || !d->w || !d->x || !d->out || !d->workspace)
+        return fail(MOE_ERR_ARG, "moe_grouped_experts: null argument");
+    if (d->H != 2048) return fail(MOE_ERR_ARG, "hidden size %d unsupported (the kernels are built for 2048)", d->H);
+    if (d->I % 256 || d->I < 256 || d->I > 768) return fail(MOE_ERR_ARG, "intermediate %d must be 256, 512 or 768", d->I);
+    if (d->E < 1 || d->E > mp::MAX_E) return fail(MOE_ERR_ARG, "n_experts %d must be 1..%d", d->E, mp::MAX_E);
+    if (d->K < 1 || d->n_tok < 1 || (int64_t)d->n_tok * d->K > 65535)
+        return fail(MOE_ERR_ARG, "n_tok %d x K %d out of range", d->n_tok, d->K);
+    if (d->x_type != MOE_DTYPE_F32 && d->x_type != MOE_DTYPE_BF16)
+        return fail(MOE_ERR_ARG, "x_type %d unsupported", d->x_type);
+    if (d->down_type != MOE_TYPE_Q4K && d->down_type != MOE_TYPE_Q6K)
+        return fail(MOE_ERR_ARG, "down type %d unsupported", d->down_type);
+    if (!d->store && !d->slot_pool) return fail(MOE_ERR_ARG, "no weights");
+    if (d->expert_bytes != mp::expert_bytes(d->H, d->I, d->down_type))
+        return fail(MOE_ERR_ARG, "expert_bytes %llu does not match the shape", (unsigned long long)d->expert_bytes);
+    if (d->slot_pool && (d->slot_bytes < d->expert_bytes || d->slot_bytes % 16))
+        return fail(MOE_ERR_ARG, "slot_bytes must be >= expert_bytes and a multiple of 16");
+    if (((uintptr_t)d->slot_pool | (uintptr_t)d->store | (uintptr_t)d->x | (uintptr_t)d->out |
+         (uintptr_t)d->workspace | (uintptr_t)d->pair_out | (uintptr_t)d->h_out) % 16)
+        return fail(MOE_ERR_ARG, "weights, activations and outputs must be 16-byte aligned");
+    const int r = check_weight_ptrs("moe_grouped_experts", d->slot_pool, d->store);
+    if (r != MOE_OK) return r;
+    const hipStream_t st = (hipStream_t)stream;
+    const GroupedWs w = grouped_ws(d->n_tok, d->K, d->H, d->I);
+    uint8_t *ws = (uint8_t *)d->workspace;
+    mp::GroupedArgs a{};
+    a.offsets = d->offsets; a.perm = d->perm; a.w = d->w;
+    a.table = d->table; a.slot_pool = d->slot_pool; a.slot_bytes = d->slot_bytes; a.n_slots = d->n_slots;
+    a.store = d->store; a.expert_bytes = d->expert_bytes; a.n_store = d->n_store;
+    a.E = d->E; a.K = d->K; a.H = d->H; a.I = d->I; a.down_type = d->down_type;
+    a.xa = (const uint16_t *)(ws + w.xa); a.xdx = (const float *)(ws + w.xdx); a.xbs = (const uint16_t *)(ws + w.xbs);
+    a.h = d->h_out ? d->h_out : (float *)(ws + w.h);
+    a.ha = (const uint16_t *)(ws + w.ha); a.hdx = (const float *)(ws + w.hdx); a.hbs = (const uint16_t *)(ws + w.hbs);
+    a.ypair = d->pair_out ? d->pair_out : (float *)(ws + w.ypair);
+    const int P = d->n_tok * d->K;
+    hipEvent_t ev[4] = {};
+    const bool timed = d->kernel_ms != nullptr;
+    if (timed)
+        for (auto &e : ev) HIPCHK(hipEventCreate(&e));
+    auto run = [&]() -> int {
+        HIPCHK(mp::launch_quant_rows(d->x, d->x_type == MOE_DTYPE_BF16, d->n_tok, d->H, (uint16_t *)a.xa,
+                                     (float *)a.xdx, (uint16_t *)a.xbs, st));
+        HIPCHK(mp::launch_gateup_grouped(a, st, ev[0], ev[1]));
+        HIPCHK(mp::launch_quant_rows(a.h, 0, P, d->I, (uint16_t *)a.ha, (float *)a.hdx, (uint16_t *)a.hbs, st));
+        HIPCHK(mp::launch_down_grouped(a, st, ev[2], ev[3]));
+        HIPCHK(mp::launch_combine(a.ypair, d->n_tok, d->K, d->H, d->out, d->accumulate, st));
+        return MOE_OK;
+    };
+    int rc = run();
+    if (timed) {
+        if (rc == MOE_OK && hipEventSynchronize(ev[3]) == hipSuccess) {
+            float ms = 0.0f;
+            hipEventElapsedTime(&ms, ev[0], ev[1]);
+            d->kernel_ms[0] = ms;
+            hipEventElapsedTime(&ms, ev[2], ev[3]);
+            d->kernel_ms[1] = ms;
+        }
+        for (auto e : ev) hipEventDestroy(e);
+    }
+    return rc;
 }
 
 // ---- slab pool --------------------------------------------------------------

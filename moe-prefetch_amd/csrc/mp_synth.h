@@ -294,8 +294,13 @@ MP_HD void expert_block(uint64_t seed, int layer, int expert, const ExpertShape 
 }
 
 // n values of an N(0, sigma) vector identified by (kind, a, b)
+// kinds 0 (router rows) and 1 (activations): N(0, sigma); kind 2 (router
+// logits): uniform on [0, sigma), 24-bit grid, exact in fp32
+constexpr int KIND_UNIFORM_LOGITS = 2;
+
 MP_HD float vec_value(uint64_t seed, int kind, int a, int b, int i, float sigma) {
     uint64_t s = key(seed, 2 + (uint64_t)kind, (uint64_t)a, (uint64_t)b, (uint64_t)i);
+    if (kind == KIND_UNIFORM_LOGITS) return (float)(splitmix(s) >> 40) * (1.0f / 16777216.0f) * sigma;
     return normal(s) * sigma;
 }
 

@@ -11,6 +11,7 @@ LIB_PATH = os.path.join(HERE, "libmoeprefetch.so")
 
 MOE_OK = 0
 TYPE_Q4K, TYPE_Q6K = 12, 14
+DTYPE_F32, DTYPE_BF16 = 0, 1
 ADMIT = {"off": 0, "heat": 1, "window": 2}
 PUBLISH = {"fifo": 0, "sorted": 1, "live": 2}
 
@@ -28,7 +29,8 @@ class MoeError(RuntimeError):
 class RouteDesc(ctypes.Structure):
     _fields_ = [("W", P), ("x", P), ("bias", P), ("prior", P), ("table", P), ("dummy", I32),
                 ("prior_on_logits", I32), ("E", I32), ("H", I32), ("K", I32), ("n_tok", I32),
-                ("ids", P), ("w", P), ("slots", P), ("probs", P), ("q8x", P), ("workspace", P)]
+                ("ids", P), ("w", P), ("slots", P), ("probs", P), ("q8x", P), ("workspace", P),
+                ("logits", P)]
 
 
 class ExpertsDesc(ctypes.Structure):
@@ -37,6 +39,15 @@ class ExpertsDesc(ctypes.Structure):
                 ("q8x", P), ("out", P),
                 ("accumulate", I32), ("H", I32), ("I", I32), ("K", I32), ("down_type", I32),
                 ("workspace", P)]
+
+
+class GroupedDesc(ctypes.Structure):
+    _fields_ = [("offsets", P), ("perm", P), ("w", P), ("x", P), ("x_type", I32),
+                ("n_tok", I32), ("K", I32), ("E", I32), ("H", I32), ("I", I32), ("down_type", I32),
+                ("table", P), ("slot_pool", P), ("slot_bytes", U64), ("n_slots", I32),
+                ("store", P), ("expert_bytes", U64), ("n_store", I32),
+                ("out", P), ("accumulate", I32), ("pair_out", P), ("h_out", P), ("workspace", P),
+                ("kernel_ms", P)]
 
 
 class CacheConfig(ctypes.Structure):
@@ -111,6 +122,11 @@ SIGNATURES = {
     "moe_cache_kernel_times": (ctypes.c_int, [P, ctypes.POINTER(KernelTimes)]),
     "moe_decode_layer": (ctypes.c_int, [P, ctypes.c_int, P, P, P, P, P, P]),
     "moe_decode_token": (ctypes.c_int, [P, P, P, P, P, P]),
+    "moe_dispatch": (ctypes.c_int, [P, ctypes.c_int, ctypes.c_int, ctypes.c_int, P, P, P, P]),
+    "moe_quant_rows": (ctypes.c_int, [P, ctypes.c_int, ctypes.c_int, ctypes.c_int, P, P, P, P]),
+    "moe_grouped_workspace_bytes": (SZ, [ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int]),
+    "moe_grouped_experts": (ctypes.c_int, [ctypes.POINTER(GroupedDesc), P]),
+    "moe_combine": (ctypes.c_int, [P, ctypes.c_int, ctypes.c_int, ctypes.c_int, P, ctypes.c_int, P]),
     "moe_pool_create": (ctypes.c_int, [ctypes.c_int, ctypes.c_int, SZ, ctypes.c_int, ctypes.POINTER(P)]),
     "moe_pool_destroy": (ctypes.c_int, [P]),
     "moe_pool_copy": (ctypes.c_int, [P, ctypes.c_int, ctypes.c_int, P, SZ]),

@@ -5,7 +5,9 @@
  * Order of operations follows experiments/x2_cpu_expert_cost.cpp:115-156 (the
  * reference's own restatement of the engine's CPU chain): x -> Q8_K once; one
  * vec_dot per up and gate row; h = silu(gate) * up in fp32 (silu(g) =
- * g / (1 + expf(-g))); h -> Q8_K; one vec_dot per down row.  The combine is
+ * g / (1 + exp(-g)), exp being the oracle's canonical or_expf, <= 2 ulp from
+ * libm's expf, the same function the GPU kernels evaluate); h -> Q8_K; one
+ * vec_dot per down row.  The combine is
  * out = sum_k w_k * y_k accumulated in k order (patches/0009-moe-sidecar.patch:
  * 697-703: experts = host_rows + cached_rows, times the weights, summed).
  *
@@ -38,7 +40,7 @@ void or_expert_chain(int H, int I, int down_type, const void *up, const void *ga
     for (int r = 0; r < I; ++r) {
         const float u = or_dot_q4k_q8k(H, (const uint8_t *)up + r * rb_in, qx);
         const float g = or_dot_q4k_q8k(H, (const uint8_t *)gate + r * rb_in, qx);
-        h[r] = g / (1.0f + expf(-g)) * u;
+        h[r] = g / (1.0f + or_expf(-g)) * u;
     }
     or_quant_q8k(h, qh, I);
     for (int r = 0; r < H; ++r) {
@@ -80,7 +82,7 @@ void or_moe_layer(int H, int I, int down_type, int K, const void *const *experts
         for (int k = 0; k < K; ++k) {
             for (int r = 0; r < I; ++r) {
                 const float g = gt[k * I + r];
-                h[k * I + r] = g / (1.0f + expf(-g)) * up[k * I + r];
+                h[k * I + r] = g / (1.0f + or_expf(-g)) * up[k * I + r];
             }
             or_quant_q8k(h + (size_t)k * I, qh + (size_t)k * q8h_b, I);
         }
@@ -106,6 +108,40 @@ void or_moe_layer(int H, int I, int down_type, int K, const void *const *experts
     free(gt);
     free(h);
     free(y);
+}
+
+void or_moe_tokens(int H, int I, int down_type, int T, int K, const void *store, size_t expert_bytes,
+                   int n_store, const int32_t *ids, const float *w, const float *x, float *out,
+                   float *h_out, int n_threads) {
+    const size_t upb = (size_t)I * (H / OR_QK) * OR_Q4K_BYTES;
+    if (n_threads < 1) n_threads = 1;
+#pragma omp parallel num_threads(n_threads)
+    {
+        float *y = (float *)malloc(sizeof(float) * (size_t)H);
+        float *h = (float *)malloc(sizeof(float) * (size_t)I);
+#pragma omp for schedule(dynamic, 1)
+        for (int t = 0; t < T; ++t) {
+            float *o = out + (size_t)t * H;
+            for (int k = 0; k < K; ++k) {
+                const int e = ids[(size_t)t * K + k];
+                if (e >= 0 && e < n_store) {
+                    const uint8_t *b = (const uint8_t *)store + (size_t)e * expert_bytes;
+                    or_expert_chain(H, I, down_type, b, b + upb, b + 2 * upb, x + (size_t)t * H, y, h);
+                } else {
+                    memset(y, 0, sizeof(float) * (size_t)H);
+                    memset(h, 0, sizeof(float) * (size_t)I);
+                }
+                if (h_out) memcpy(h_out + ((size_t)t * K + k) * I, h, sizeof(float) * (size_t)I);
+                const float wk = w[(size_t)t * K + k];
+                for (int r = 0; r < H; ++r) {
+                    const float v = (e >= 0 && e < n_store) ? wk * y[r] : 0.0f;
+                    o[r] = k == 0 ? v : o[r] + v;
+                }
+            }
+        }
+        free(y);
+        free(h);
+    }
 }
 
 void or_dispatch(int T, int K, int E, const int32_t *ids, int32_t *counts,

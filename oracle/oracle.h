@@ -23,7 +23,7 @@
  *       softmax/sort on random and tie-heavy inputs, and by the reference's own
  *       integer-valued top-k case (cpp/test-moe-sidecar.cpp:155-217: lower id
  *       wins a tie).
- *   or_expert_chain, or_moe_layer
+ *   or_expert_chain, or_moe_layer, or_moe_tokens
  *       ggml CPU expert chain: quantize x to Q8_K once, one integer vec_dot per
  *       gate/up row, SwiGLU in fp32, quantize h to Q8_K, one vec_dot per down
  *       row (experiments/x2_cpu_expert_cost.cpp:115-156), weighted combine in k
@@ -116,6 +116,13 @@ void or_expert_chain(int H, int I, int down_type, const void *up, const void *ga
 void or_moe_layer(int H, int I, int down_type, int K, const void *const *experts,
                   const float *w, const float *x, float *out, int n_threads);
 size_t or_expert_bytes(int H, int I, int down_type);
+/* A batch of T tokens: token t through experts ids[t][k] of a [n_store][expert_bytes]
+ * store (an id outside it contributes zero), out[t] = sum_k w[t][k] y_{t,k} in k
+ * order -- or_moe_layer's combine -- with OpenMP over tokens.  h_out [T][K][I]
+ * (optional) receives each pair's SwiGLU activations. */
+void or_moe_tokens(int H, int I, int down_type, int T, int K, const void *store, size_t expert_bytes,
+                   int n_store, const int32_t *ids, const float *w, const float *x, float *out,
+                   float *h_out, int n_threads);
 
 /* ---- dispatch ---------------------------------------------------------- */
 /* ids [T][K].  counts[E], offsets[E+1] (exclusive scan), perm[T*K]:

@@ -79,6 +79,8 @@ def _declare(L):
     d("or_moe_layer", None, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, P, P, P, P,
       ctypes.c_int)
     d("or_expert_bytes", ctypes.c_size_t, ctypes.c_int, ctypes.c_int, ctypes.c_int)
+    d("or_moe_tokens", None, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, P,
+      ctypes.c_size_t, ctypes.c_int, P, P, P, P, P, ctypes.c_int)
     d("or_dispatch", None, ctypes.c_int, ctypes.c_int, ctypes.c_int, P, P, P, P)
     d("or_cache_create", P, ctypes.c_int, ctypes.c_int, P, ctypes.POINTER(Knobs))
     d("or_cache_destroy", None, P)
@@ -198,6 +200,21 @@ def moe_layer(H, I, down_type, experts, w, x, n_threads=1):
     lib().or_moe_layer(H, I, down_type, K, ctypes.cast(ptrs, ctypes.c_void_p), _p(w), _p(x),
                        _p(out), n_threads)
     return out
+
+
+def moe_tokens(H, I, down_type, store, expert_bytes, n_store, ids, w, x, n_threads=8, want_h=False):
+    """Batch oracle: store is a uint8 array (or raw address) of [n_store][expert_bytes];
+    ids/w [T][K]; x [T][H] f32.  Returns out [T][H] (and h [T][K][I])."""
+    ids = np.ascontiguousarray(ids, np.int32)
+    T, K = ids.shape
+    w = np.ascontiguousarray(w, np.float32)
+    x = np.ascontiguousarray(x, np.float32)
+    out = np.empty((T, H), np.float32)
+    h = np.empty((T, K, I), np.float32) if want_h else None
+    base = store if isinstance(store, int) else store.ctypes.data
+    lib().or_moe_tokens(H, I, down_type, T, K, base, expert_bytes, n_store, _p(ids), _p(w), _p(x), _p(out),
+                        _p(h) if want_h else None, n_threads)
+    return (out, h) if want_h else out
 
 
 def dispatch(ids, E):

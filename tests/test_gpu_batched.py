@@ -1,0 +1,295 @@
+"""GPU parity of the batched path (prefill chunks, decode at batch > 1) through
+the C ABI against the oracle on the same seeded inputs.
+
+  moe_dispatch         counts, offsets and the (token, k)-stable permutation
+                       bit-exact (uniform, skewed, all-one-expert, ragged,
+                       several 4096-pair passes, E = 64/128/256, ids outside
+                       [0, E) dropped)
+  moe_quant_rows       Q8_K values, scales and group sums bit-exact (f32, bf16,
+                       zero rows, ties of the largest magnitude)
+  moe_route (logits)   ids / weights / probabilities from given logits
+                       bit-exact, with and without a bias
+  moe_grouped_experts  every token's output and every pair's SwiGLU
+                       activations within 1e-3 relative L2 of the ggml-style
+                       oracle, and in fact bit-exact (Q4_K and Q6_K down,
+                       intermediate 768/512/256, batch 1..512, tokens crowding
+                       a few experts into several passes, experts in HBM slots
+                       / a pinned host store / nowhere)
+"""
+import zlib
+
+import numpy as np
+import pytest
+import torch
+
+from gpu_rig import H, L, Pinned, stream, synth_experts_dev
+from moe_prefetch import _lib
+from moe_prefetch.batched import BatchedMoe
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+DEV = torch.device("cuda:0")
+TOL = 1e-3   # relative L2 against the oracle, per token / per pair
+
+
+def t_(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(DEV)
+
+
+def ref_dispatch(ids, E):
+    flat = np.asarray(ids, np.int64).reshape(-1)
+    valid = (flat >= 0) & (flat < E)
+    counts = np.bincount(flat[valid], minlength=E).astype(np.int32)
+    offsets = np.concatenate([[0], np.cumsum(counts)]).astype(np.int32)
+    idx = np.flatnonzero(valid)
+    return counts, offsets, idx[np.argsort(flat[valid], kind="stable")].astype(np.int32)
+
+
+def gpu_dispatch(ids, E):
+    T, K = ids.shape
+    d_ids = t_(ids.astype(np.int32))
+    counts = torch.full((E,), -7, dtype=torch.int32, device=DEV)
+    offsets = torch.full((E + 1,), -7, dtype=torch.int32, device=DEV)
+    perm = torch.full((max(T * K, 1),), -7, dtype=torch.int32, device=DEV)
+    _lib.check(L().moe_dispatch(d_ids.data_ptr(), T, K, E, counts.data_ptr(), offsets.data_ptr(),
+                                perm.data_ptr(), stream()), "dispatch")
+    torch.cuda.synchronize()
+    return counts.cpu().numpy(), offsets.cpu().numpy(), perm.cpu().numpy()
+
+
+DISPATCH_CASES = {
+    "uniform_512x8_e128": (512, 8, 128, "uniform"),
+    "single_token": (1, 8, 128, "uniform"),
+    "batch16_k9_e256": (16, 9, 256, "uniform"),
+    "two_passes_1024x8": (1024, 8, 128, "uniform"),
+    "max_pairs_8191x8": (8191, 8, 128, "zipf"),
+    "one_expert": (300, 8, 64, "one"),
+    "skewed_e64": (777, 6, 64, "zipf"),
+}
+
+
+@pytest.mark.parametrize("case", list(DISPATCH_CASES))
+def test_dispatch_bit_exact(case):
+    T, K, E, kind = DISPATCH_CASES[case]
+    rng = np.random.default_rng(zlib.crc32(case.encode()))
+    if kind == "uniform":
+        ids = rng.integers(0, E, size=(T, K))
+    elif kind == "one":
+        ids = np.full((T, K), 5)
+    else:
+        p = 1.0 / np.arange(1, E + 1) ** 1.2
+        ids = rng.choice(E, size=(T, K), p=p / p.sum())
+    ids = ids.astype(np.int32)
+    c, o, p = gpu_dispatch(ids, E)
+    oc, oo, op = O.dispatch(ids, E)
+    assert np.array_equal(c, oc) and np.array_equal(o, oo)
+    assert np.array_equal(p[:T * K], op)
+
+
+def test_dispatch_drops_ids_outside_range():
+    rng = np.random.default_rng(3)
+    ids = rng.integers(-3, 131, size=(200, 8)).astype(np.int32)
+    c, o, p = gpu_dispatch(ids, 128)
+    rc, ro, rp = ref_dispatch(ids, 128)
+    assert np.array_equal(c, rc) and np.array_equal(o, ro)
+    assert np.array_equal(p[:ro[-1]], rp)
+
+
+@pytest.mark.parametrize("src", ["f32", "bf16"])
+@pytest.mark.parametrize("n", [2048, 768])
+def test_quant_rows_bit_exact(src, n):
+    rng = np.random.default_rng(n)
+    rows = 37
+    x = (rng.standard_normal((rows, n)) * rng.uniform(0.01, 3, size=(rows, 1))).astype(np.float32)
+    x[3] = 0.0                                     # all-zero blocks
+    x[5, :256] = 0.0
+    x[5, 7], x[5, 9] = -2.5, 2.5                   # tie of the largest magnitude: first index wins
+    x[6, 300], x[6, 301] = 4.0, -4.0
+    xd = t_(x)
+    if src == "bf16":
+        xd = xd.to(torch.bfloat16)
+        x = xd.float().cpu().numpy()
+    q16 = torch.empty((rows, n), dtype=torch.int16, device=DEV)
+    d = torch.empty((rows, n // 256), dtype=torch.float32, device=DEV)
+    bs = torch.empty((rows, n // 16), dtype=torch.int16, device=DEV)
+    st = _lib.DTYPE_BF16 if src == "bf16" else _lib.DTYPE_F32
+    _lib.check(L().moe_quant_rows(xd.data_ptr(), st, rows, n, q16.data_ptr(), d.data_ptr(), bs.data_ptr(),
+                                  stream()), "quant_rows")
+    torch.cuda.synchronize()
+    qv = q16.cpu().view(torch.float16).float().numpy()
+    bv = bs.cpu().view(torch.float16).float().numpy()
+    dv = d.cpu().numpy()
+    for r in range(rows):
+        blocks = O.quant_q8k(x[r]).reshape(-1, 292)
+        for b in range(n // 256):
+            blk = blocks[b]
+            assert dv[r, b].tobytes() == blk[:4].tobytes(), (r, b)
+            assert np.array_equal(qv[r, 256 * b:256 * (b + 1)], blk[4:260].view(np.int8).astype(np.float32)), (r, b)
+            assert np.array_equal(bv[r, 16 * b:16 * (b + 1)], blk[260:292].view(np.int16).astype(np.float32)), (r, b)
+
+
+@pytest.mark.parametrize("bias", [False, True])
+@pytest.mark.parametrize("E,K", [(128, 8), (256, 8), (64, 6)])
+def test_route_given_logits_bit_exact(E, K, bias):
+    T = 96
+    lg = torch.empty((T, E), dtype=torch.float32, device=DEV)
+    _lib.check(L().moe_synth_vec(5, 2, 0, T, 0, 1, E, 1.0, lg.data_ptr(), stream()), "logits")
+    b = None
+    if bias:
+        b = t_(np.random.default_rng(E).standard_normal((T, E)).astype(np.float32) * 0.3)
+    bm = BatchedMoe(T, n_experts=E, n_expert_used=K)
+    ids, w = bm.route(T, logits=lg, bias=b, stream=stream())
+    torch.cuda.synchronize()
+    lh = lg.cpu().numpy()
+    assert lh.min() >= 0.0 and lh.max() < 1.0
+    bh = None if b is None else b.cpu().numpy()
+    gi, gw = ids.cpu().numpy(), w.cpu().numpy()
+    for t in range(T):
+        l_ = lh[t] if bh is None else lh[t] + bh[t]
+        oi, ow, _ = O.route_logits(l_, K)
+        assert np.array_equal(gi[t], oi), t
+        assert gw[t].tobytes() == ow.tobytes(), t
+
+
+# ---- grouped experts ---------------------------------------------------------
+class Store:
+    """n experts of one layer in HBM (device generator)."""
+
+    def __init__(self, n, I, dt, seed=42, layer=3):
+        self.n, self.I, self.dt = n, I, dt
+        self.eb = L().moe_expert_bytes(H, I, dt)
+        self.t = torch.empty(n * self.eb, dtype=torch.uint8, device=DEV)
+        synth_experts_dev(seed, layer, 0, n, I, dt, self.t.data_ptr(), self.eb)
+        torch.cuda.synchronize()
+        self.host = self.t.cpu().numpy()
+
+
+def routing(rng, T, K, E, kind):
+    if kind == "uniform":
+        ids = np.stack([rng.choice(E, size=K, replace=False) for _ in range(T)])
+    else:   # crowd: most tokens share a handful of experts (several passes of 64 pairs)
+        hot = rng.choice(E, size=K + 2, replace=False)
+        ids = np.stack([rng.choice(hot, size=K, replace=False) if rng.random() < 0.8 else
+                        rng.choice(E, size=K, replace=False) for _ in range(T)])
+    w = rng.random((T, K)).astype(np.float32) + 0.05
+    return ids.astype(np.int32), (w / w.sum(1, keepdims=True)).astype(np.float32)
+
+
+def rel_l2(a, b):
+    return float(np.linalg.norm(a.astype(np.float64) - b) / max(np.linalg.norm(b.astype(np.float64)), 1e-30))
+
+
+def run_grouped(store, T, K, E, ids, w, x_dtype, table=None, slot_pool=None, slot_bytes=0, n_slots=0,
+                store_ptr=None, n_store=None, seed=0):
+    xf = torch.empty((T, H), dtype=torch.float32, device=DEV)
+    _lib.check(L().moe_synth_vec(seed, 1, 0, T, 7, 1, H, 1.0, xf.data_ptr(), stream()), "x")
+    x = xf.to(torch.bfloat16) if x_dtype == "bf16" else xf
+    bm = BatchedMoe(T, n_experts=E, n_expert_used=K, intermediate=store.I)
+    d_ids, d_w = t_(ids), t_(w)
+    bm.dispatch(T, ids=d_ids, stream=stream())
+    out = torch.empty((T, H), dtype=torch.float32, device=DEV)
+    h_out = torch.empty((T * K, store.I), dtype=torch.float32, device=DEV)
+    pair = torch.empty((T * K, H), dtype=torch.float32, device=DEV)
+    bm.experts(x, out, T, store.t.data_ptr() if store_ptr is None else store_ptr, store.eb,
+               store.n if n_store is None else n_store, store.dt, w=d_w, table=table, slot_pool=slot_pool,
+               slot_bytes=slot_bytes, n_slots=n_slots, pair_out=pair, h_out=h_out, stream=stream())
+    torch.cuda.synchronize()
+    xh = x.float().cpu().numpy()
+    return out.cpu().numpy(), h_out.cpu().numpy(), pair.cpu().numpy(), bm.perm[:T * K].cpu().numpy(), xh
+
+
+GROUPED_CASES = {
+    "q4k_i768_t64": (_lib.TYPE_Q4K, 768, 64, 128, "uniform", "bf16"),
+    "q6k_i768_t64": (_lib.TYPE_Q6K, 768, 64, 128, "uniform", "bf16"),
+    "q4k_i512_t33_f32": (_lib.TYPE_Q4K, 512, 33, 128, "uniform", "f32"),
+    "q6k_i512_t1": (_lib.TYPE_Q6K, 512, 1, 128, "uniform", "bf16"),
+    "q4k_i768_t512": (_lib.TYPE_Q4K, 768, 512, 128, "uniform", "bf16"),
+    "q6k_i768_t200_crowded": (_lib.TYPE_Q6K, 768, 200, 128, "crowd", "bf16"),
+    "q4k_i256_t150_e64_crowded": (_lib.TYPE_Q4K, 256, 150, 64, "crowd", "f32"),
+}
+
+
+@pytest.mark.parametrize("case", list(GROUPED_CASES))
+def test_grouped_experts_vs_oracle(case):
+    dt, I, T, E, kind, xt = GROUPED_CASES[case]
+    K = 8
+    rng = np.random.default_rng(zlib.crc32(case.encode()))
+    store = Store(E, I, dt)
+    ids, w = routing(rng, T, K, E, kind)
+    out, h_out, pair, perm, xh = run_grouped(store, T, K, E, ids, w, xt)
+    want, want_h = O.moe_tokens(H, I, dt, store.host, store.eb, E, ids, w, xh, n_threads=16, want_h=True)
+    assert all(np.linalg.norm(want[t]) > 0 for t in range(T))
+    worst = max(rel_l2(out[t], want[t]) for t in range(T))
+    # h in dispatch order: position j holds pair perm[j]
+    hw = want_h.reshape(T * K, I)[perm]
+    assert all(np.linalg.norm(hw[j]) > 0 for j in range(T * K))
+    worst_h = max(rel_l2(h_out[j], hw[j]) for j in range(T * K))
+    n_exact = sum(np.array_equal(out[t], want[t]) for t in range(T))
+    h_exact = sum(np.array_equal(h_out[j], hw[j]) for j in range(T * K))
+    print(f"{case}: worst rel-L2 out {worst:.3e}, h {worst_h:.3e}; bit-exact tokens {n_exact}/{T}, "
+          f"pairs {h_exact}/{T * K}")
+    assert worst < TOL, worst
+    assert worst_h < TOL, worst_h
+    # integer products are exact on the matrix cores and the fp32 scale follows
+    # the CPU chain's order: the values are the oracle's bit for bit
+    assert n_exact == T and h_exact == T * K
+    # the per-pair rows summed over k in order give out exactly
+    s = pair.reshape(T, K, H)
+    acc = s[:, 0].copy()
+    for k in range(1, K):
+        acc = acc + s[:, k]
+    assert np.array_equal(acc, out)
+
+
+def test_grouped_experts_slots_pinned_and_absent():
+    """Experts resident in an HBM slot pool, the rest read from a pinned host
+    store, ids past the store contributing zero."""
+    dt, I, T, E, K = _lib.TYPE_Q4K, 768, 48, 128, 8
+    rng = np.random.default_rng(5)
+    store = Store(E, I, dt, layer=1)
+    pinned = Pinned(E * store.eb)
+    pinned.arr[:] = store.host
+    n_slots = 20
+    slot_bytes = (store.eb + 255) // 256 * 256
+    pool = torch.zeros(n_slots * slot_bytes, dtype=torch.uint8, device=DEV)
+    table = np.full(E, n_slots, np.int32)
+    resident = rng.choice(E - 10, size=n_slots, replace=False)
+    for s, e in enumerate(resident):
+        table[e] = s
+        pool[s * slot_bytes:s * slot_bytes + store.eb] = store.t[e * store.eb:(e + 1) * store.eb]
+    n_store = E - 10                        # the last 10 ids are in no store and not resident
+    table[E - 3] = 0 if table[E - 3] == n_slots else table[E - 3]   # one of them resident after all
+    ids, w = routing(rng, T, K, E, "uniform")
+    ids[0, :3] = [E - 1, E - 2, E - 3]
+    try:
+        out, h_out, pair, perm, xh = run_grouped(store, T, K, E, ids, w, "bf16", table=t_(table),
+                                                 slot_pool=pool.data_ptr(), slot_bytes=slot_bytes,
+                                                 n_slots=n_slots, store_ptr=pinned.dev, n_store=n_store)
+    finally:
+        pinned.free()
+    # what each id reads: the bytes its slot holds when the table maps it, else
+    # the store (ids below n_store), else nothing (expert E of the padded store)
+    src = np.array([resident[table[e]] if table[e] < n_slots else (e if e < n_store else E) for e in range(E)])
+    flat_store = np.concatenate([store.host, np.zeros(store.eb, np.uint8)])
+    want = O.moe_tokens(H, I, dt, flat_store, store.eb, E, src[ids], w, xh, n_threads=16)
+    assert all(np.linalg.norm(want[t]) > 0 for t in range(T))
+    worst = max(rel_l2(out[t], want[t]) for t in range(T))
+    print(f"slots/pinned/absent: worst rel-L2 {worst:.3e}")
+    assert worst < TOL, worst
+    assert np.array_equal(out, want)
+    # the absent ids of token 0 contribute nothing: its output equals the sum over its other experts
+    assert src[E - 1] == E and src[E - 2] == E
+
+
+def test_combine_accumulates_in_k_order():
+    T, K = 9, 8
+    rng = np.random.default_rng(2)
+    rows = rng.standard_normal((T * K, H)).astype(np.float32)
+    base = rng.standard_normal((T, H)).astype(np.float32)
+    out = t_(base)
+    _lib.check(L().moe_combine(t_(rows).data_ptr(), T, K, H, out.data_ptr(), 1, stream()), "combine")
+    s = rows.reshape(T, K, H)
+    acc = s[:, 0].copy()
+    for k in range(1, K):
+        acc = acc + s[:, k]
+    assert np.array_equal(out.cpu().numpy(), base + acc)
