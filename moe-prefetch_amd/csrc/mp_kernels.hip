@@ -67,13 +67,14 @@ struct RouteArgs {
 
 // One wavefront per expert row: logit[e] = <W[e], x> in the canonical order
 // (lane j accumulates W[256 i + 4 j + c] * x[...] with fmaf, i then c, then a
-// butterfly over the 64 lanes), plus the steering bias when given.
+// butterfly over the 64 lanes), plus the steering bias when given.  The first
+// H/256 workgroups also write the Q8_K blocks of x.
 __global__ __launch_bounds__(256) void route_logits_kernel(RouteArgs a) {
     const int tok = blockIdx.y;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int e = blockIdx.x * 4 + wave;
-    if (e >= a.E) return;
     const float *x = a.x + (size_t)tok * a.H;
+    if (e >= a.E) return;
     const float *w = a.W + (size_t)e * a.H;
     float acc = 0.0f;
     for (int i = 0; i < a.H / 256; ++i) {
@@ -87,65 +88,75 @@ __global__ __launch_bounds__(256) void route_logits_kernel(RouteArgs a) {
     acc = bfly_add(acc);
     if (a.bias) acc = acc + a.bias[(size_t)tok * a.E + e];
     if (lane == 0) a.logits[(size_t)tok * a.E + e] = acc;
+    // Q8_K of x: workgroup b (one of the first H/256) quantizes block b
+    if (a.q8x && wave == 0 && (int)blockIdx.x < a.H / QK)
+        q8k_wave(x + QK * blockIdx.x, a.q8x + ((size_t)tok * (a.H / QK) + blockIdx.x) * Q8K_BYTES, lane);
 }
 
-// One workgroup per token: softmax, + prior, top-k (lower id on ties),
-// renormalised weights, slot lookup (wave 0); Q8_K of x (all four waves)
-// when x and q8x are given.
+// One workgroup per token.  Wave c owns experts 64c .. 64c+63: logits, the
+// wave's max and its 64-lane butterfly sum of exp (the canonical per-chunk
+// sums, added in chunk order), probabilities and the selection value (+ prior).
+// Top-k by rank: thread e counts the experts ahead of e in (selection
+// descending, id ascending) order -- no dependent shuffle chain -- and rank < K
+// places e.  With given logits, also the Q8_K of x (all four waves) when x and
+// q8x are given; otherwise the router GEMV kernel wrote it.
 __global__ __launch_bounds__(256) void route_select_kernel(RouteArgs a) {
     const int tok = blockIdx.x;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int nc = a.E / 64;
     __shared__ float s_p[256];
+    __shared__ __attribute__((aligned(16))) float s_sel[256];
+    __shared__ float s_m[4], s_cs[4];
     __shared__ int s_ids[16];
-    if (wave == 0) {
-        const int nc = a.E / 64;
-        float l4[4];
+    float l = 0.0f;
+    if (wave < nc) {
+        const int ee = 64 * wave + lane;
         if (a.logits_in) {
-            const float *lg = a.logits_in + (size_t)tok * a.E;
-            const float *bs = a.bias ? a.bias + (size_t)tok * a.E : nullptr;
-            for (int c = 0; c < nc; ++c) l4[c] = bs ? lg[64 * c + lane] + bs[64 * c + lane] : lg[64 * c + lane];
+            l = a.logits_in[(size_t)tok * a.E + ee];
+            if (a.bias) l = l + a.bias[(size_t)tok * a.E + ee];
         } else {
-            const float *lg = a.logits + (size_t)tok * a.E;
-            for (int c = 0; c < nc; ++c) l4[c] = lg[64 * c + lane];
+            l = a.logits[(size_t)tok * a.E + ee];
         }
-        float m = l4[0];
-        for (int c = 1; c < nc; ++c) m = fmaxf(m, l4[c]);
+        float m = l;
 #pragma unroll
         for (int o = 32; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
-        float ex[4];
-        float s = 0.0f;
-        for (int c = 0; c < nc; ++c) {
-            ex[c] = canon_expf(l4[c] - m);
-            const float cs = bfly_add(ex[c]);
-            s = c == 0 ? cs : s + cs;
+        if (lane == 0) s_m[wave] = m;
+    }
+    __syncthreads();
+    float ex = 0.0f;
+    if (wave < nc) {
+        float m = s_m[0];
+        for (int c = 1; c < nc; ++c) m = fmaxf(m, s_m[c]);
+        ex = canon_expf(l - m);
+        const float cs = bfly_add(ex);
+        if (lane == 0) s_cs[wave] = cs;
+    }
+    __syncthreads();
+    if (wave < nc) {
+        float sum = s_cs[0];
+        for (int c = 1; c < nc; ++c) sum = sum + s_cs[c];
+        const int ee = 64 * wave + lane;
+        const float p = ex / sum;
+        s_p[ee] = p;
+        if (a.probs) a.probs[(size_t)tok * a.E + ee] = p;
+        float sel = !a.prior ? p : (a.prior_on_logits ? l + a.prior[ee] : p + a.prior[ee]);
+        s_sel[ee] = sel != sel ? -INFINITY : sel;     // a NaN sorts last
+    }
+    __syncthreads();
+    if (tid < a.E) {
+        const float v = s_sel[tid];
+        int rank = 0;
+        for (int j = 0; j < a.E; j += 4) {
+            const float4 u = *(const float4 *)&s_sel[j];
+            rank += (u.x > v) | ((u.x == v) & (j < tid));
+            rank += (u.y > v) | ((u.y == v) & (j + 1 < tid));
+            rank += (u.z > v) | ((u.z == v) & (j + 2 < tid));
+            rank += (u.w > v) | ((u.w == v) & (j + 3 < tid));
         }
-        float sel[4];
-        int taken = 0;
-        for (int c = 0; c < nc; ++c) {
-            const int ee = 64 * c + lane;
-            const float p = ex[c] / s;
-            s_p[ee] = p;
-            if (a.probs) a.probs[(size_t)tok * a.E + ee] = p;
-            sel[c] = !a.prior ? p : (a.prior_on_logits ? l4[c] + a.prior[ee] : p + a.prior[ee]);
-        }
-        for (int k = 0; k < a.K; ++k) {
-            float bv = -INFINITY;
-            int bi = 1 << 30;
-            for (int c = 0; c < nc; ++c) {
-                if (taken & (1 << c)) continue;
-                if (sel[c] > bv) { bv = sel[c]; bi = 64 * c + lane; }  // c ascending: lower id keeps a tie
-            }
-#pragma unroll
-            for (int o = 32; o >= 1; o >>= 1) {
-                const float ov = __shfl_xor(bv, o, 64);
-                const int oi = __shfl_xor(bi, o, 64);
-                if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
-            }
-            if (bi >= a.E) bi = 0;   // only if every candidate were NaN: keep the index in range
-            if (lane == 0) s_ids[k] = bi;
-            if ((bi & 63) == lane) taken |= 1 << (bi >> 6);
-        }
-        __builtin_amdgcn_wave_barrier();
+        if (rank < a.K) s_ids[rank] = tid;
+    }
+    __syncthreads();
+    if (wave == 0) {
         // lane k finishes slot k; the weight sum is the same left-to-right sum on every lane
         float ws = 0.0f;
         for (int k = 0; k < a.K; ++k) ws = ws + s_p[s_ids[k]];
@@ -156,7 +167,7 @@ __global__ __launch_bounds__(256) void route_select_kernel(RouteArgs a) {
             a.slots[(size_t)tok * a.K + lane] = a.table ? a.table[id] : a.dummy;
         }
     }
-    if (!a.x || !a.q8x) return;
+    if (!a.logits_in || !a.x || !a.q8x) return;
     const float *x = a.x + (size_t)tok * a.H;
     uint8_t *q8 = a.q8x + (size_t)tok * (a.H / QK) * Q8K_BYTES;
     for (int b = wave; b < a.H / QK; b += 4) q8k_wave(x + QK * b, q8 + (size_t)b * Q8K_BYTES, lane);
