@@ -1,17 +1,19 @@
 // mp_batched.hip -- gfx950 kernels of the batched MoE layer (prefill chunks and
 // decode at batch > 1).
 //
-//   dispatch_kernel    per-expert histogram, exclusive scan and the stable
-//                      permutation of (token, k) pairs (one workgroup)
-//   quant_rows_kernel  Q8_K of rows (x per token, h per dispatched pair) into
-//                      the form the matrix cores consume: the int8 values as
-//                      fp16 codes, the block scale, and the 16-value group
-//                      sums as fp16 -- all exact
-//   gateup_grouped     per expert: [tokens x H] . [H x I] for up and gate on
-//                      MFMA 16x16x32 f16, SwiGLU fused, h in dispatch order
-//   down_grouped       per expert: [pairs x I] . [I x H], times the gate
-//                      weight, scattered to the pair's (token, k) row
-//   combine_kernel     out[t] = sum over k of the weighted rows, k in order
+//   dispatch_kernel      per-expert histogram, exclusive scan and the stable
+//                        permutation of (token, k) pairs (one workgroup)
+//   quant_rows_kernel    Q8_K of rows (x per token) into the form the matrix
+//                        cores consume: the int8 values as fp16 codes, the
+//                        block scale, and the 16-value group sums as fp16 --
+//                        all exact
+//   grouped_gemm_kernel  per (64-row tile, expert): the expert's rows against
+//                        the activations of every pair dispatched to it, on
+//                        MFMA 16x16x32 f16; up and gate as one 2I-row matrix
+//                        (the expert's [up | gate] layout), then down with the
+//                        pair's gate weight, scattered to the pair's row
+//   swiglu_quant_kernel  h = silu(gate) * up, and its Q8_K
+//   combine_kernel       out[t] = sum over k of the weighted rows, k in order
 //
 // Exact integer products on fp16 matrix cores.  A Q4_K weight is
 // d*sc*q - dmin*m with q a nibble and sc, m six-bit.  The B operand holds sc*q
@@ -41,6 +43,8 @@ namespace mp {
 typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
 typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
 typedef float float4_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(1))) void gptr_t;
+typedef __attribute__((address_space(3))) void lptr_t;
 
 // ---------------------------------------------------------------------------
 // dispatch: ids [P] (P = n_tok * K, pair i = t*K + k) -> counts[E], offsets[E+1],
@@ -120,6 +124,21 @@ __global__ __launch_bounds__(1024) void dispatch_kernel(const int32_t *ids, int 
 // Q8_K rows for the matrix cores: one wavefront per (row, 256-value block)
 __device__ inline uint32_t h16(int v) { return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)(float)v); }
 
+// the wave's 4 values per lane -> fp16 codes, block scale and group sums
+__device__ inline void q8_rows_out(const float xv[4], int lane, size_t off, size_t row, int b, int n,
+                                   uint16_t *q16, float *dx, uint16_t *bs16) {
+    int q[4];
+    float d;
+    q8k_wave_vals(xv, lane, q, d);
+    const int gs = q8k_group_sum(q);
+    uint2 o;
+    o.x = h16(q[0]) | (h16(q[1]) << 16);
+    o.y = h16(q[2]) | (h16(q[3]) << 16);
+    *(uint2 *)(q16 + off) = o;
+    if ((lane & 3) == 0) bs16[row * (n / 16) + b * 16 + (lane >> 2)] = (uint16_t)h16(gs);
+    if (lane == 0) dx[row * (n / QK) + b] = d;
+}
+
 __global__ __launch_bounds__(256) void quant_rows_kernel(const void *src, int bf16, int n_rows, int n,
                                                          uint16_t *q16, float *dx, uint16_t *bs16) {
     const int lane = threadIdx.x & 63;
@@ -140,16 +159,29 @@ __global__ __launch_bounds__(256) void quant_rows_kernel(const void *src, int bf
         const float4 v = *(const float4 *)((const float *)src + off);
         xv[0] = v.x; xv[1] = v.y; xv[2] = v.z; xv[3] = v.w;
     }
-    int q[4];
-    float d;
-    q8k_wave_vals(xv, lane, q, d);
-    const int gs = q8k_group_sum(q);
-    uint2 o;
-    o.x = h16(q[0]) | (h16(q[1]) << 16);
-    o.y = h16(q[2]) | (h16(q[3]) << 16);
-    *(uint2 *)(q16 + off) = o;
-    if ((lane & 3) == 0) bs16[(size_t)row * (n / 16) + b * 16 + (lane >> 2)] = (uint16_t)h16(gs);
-    if (lane == 0) dx[(size_t)row * nb + b] = d;
+    q8_rows_out(xv, lane, off, (size_t)row, b, n, q16, dx, bs16);
+}
+
+// SiLU with the canonical exp (the oracle evaluates the same function)
+__device__ inline float silu_mul(float g, float u) { return g / (1.0f + canon_expf(-g)) * u; }
+
+// h = silu(gate) * up from the up/gate rows y2 [P][2I] (up first), then its
+// Q8_K: one wavefront per (pair, 256-value block); h itself to h_out if given
+__global__ __launch_bounds__(256) void swiglu_quant_kernel(const float *y2, int P, int I, float *h_out, uint16_t *q16,
+                                                           float *dx, uint16_t *bs16) {
+    const int lane = threadIdx.x & 63;
+    const int nb = I / QK;
+    const int64_t blk = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (blk >= (int64_t)P * nb) return;
+    const int64_t p = blk / nb;
+    const int b = (int)(blk % nb);
+    const float *yr = y2 + (size_t)p * 2 * I + (size_t)b * QK + 4 * lane;
+    const float4 u = *(const float4 *)yr;
+    const float4 g = *(const float4 *)(yr + I);
+    const float hv[4] = {silu_mul(g.x, u.x), silu_mul(g.y, u.y), silu_mul(g.z, u.z), silu_mul(g.w, u.w)};
+    const size_t off = (size_t)p * I + (size_t)b * QK + 4 * lane;
+    if (h_out) *(float4 *)(h_out + off) = make_float4(hv[0], hv[1], hv[2], hv[3]);
+    q8_rows_out(hv, lane, off, (size_t)p, b, I, q16, dx, bs16);
 }
 
 // ---------------------------------------------------------------------------
@@ -189,155 +221,45 @@ __device__ inline float4_t mfma32(half8_t a, half8_t b, float4_t c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }
 
-// SiLU with the canonical exp (the oracle evaluates the same function)
-__device__ inline float silu_mul(float g, float u) { return g / (1.0f + canon_expf(-g)) * u; }
-
-// B operands of one Q4_K super-block for the lane's row: two 16-byte qs loads
-// (group g_L = (h >> 1) + 2L, elements 16*(h & 1) .. +15 of sub-blocks 2g_L and
-// 2g_L + 1), MFMA index 4L + 2*nibble + half.  Also the min operand for the
-// sub-blocks of group g_{h & 1} and the row's d, dmin.
-struct Q4Frag {
-    half8_t b[8];
-    half4_t bm;
-    float d, dmin;
-};
-
-__device__ inline void q4_frag(const uint8_t *blk, int h, Q4Frag &f) {
-    const uint4 hdr = *(const uint4 *)blk;
-    const uint4 q0 = *(const uint4 *)(blk + 16 + 16 * h);
-    const uint4 q1 = *(const uint4 *)(blk + 16 + 64 + 16 * h);
-    f.d = h2f((uint16_t)(hdr.x & 0xffff));
-    f.dmin = h2f((uint16_t)(hdr.x >> 16));
-#pragma unroll
-    for (int L = 0; L < 2; ++L) {
-        const uint4 q = L ? q1 : q0;
-        const int g = (h >> 1) + 2 * L;
-        int sl, ml, sh, mh;
-        q4k_sm(hdr, 2 * g, sl, ml);
-        q4k_sm(hdr, 2 * g + 1, sh, mh);
-        const uint32_t M = 0x0F0F0F0Fu;
-        f.b[4 * L + 0] = q4_scaled(q.x & M, q.y & M, sl);
-        f.b[4 * L + 1] = q4_scaled(q.z & M, q.w & M, sl);
-        f.b[4 * L + 2] = q4_scaled((q.x >> 4) & M, (q.y >> 4) & M, sh);
-        f.b[4 * L + 3] = q4_scaled((q.z >> 4) & M, (q.w >> 4) & M, sh);
-        if (L == (h & 1)) {
-            const _Float16 a = (_Float16)(float)ml, b = (_Float16)(float)mh;
-            f.bm = half4_t{a, a, b, b};
-        }
-    }
-}
-
-// A operand: the 8 activation values MFMA `i` pairs with the lane's weights
+// Q4_K lane layout.  Lane (n = lane & 15: row, h = lane >> 4) of a wave loads
+// the 16-byte header and qs bytes 16h .. 16h+15 (group g_0 = h >> 1) and
+// 64+16h .. 64+16h+15 (group g_1 = 2 + (h >> 1)) of each super-block: elements
+// 16*(h & 1) .. +15 of sub-blocks 2g_L (low nibbles) and 2g_L + 1 (high).  MFMA
+// i = 4L + 2*nibble + half multiplies 8 of them; the activation values at the
+// same positions sit at this offset of the 256-value block:
 __device__ inline int q4_a_offset(int h, int i) {
     const int L = i >> 2, nib = (i >> 1) & 1, half = i & 1;
     const int g = (h >> 1) + 2 * L;
     return 32 * (2 * g + nib) + 16 * (h & 1) + 8 * half;
 }
 
-// The pass covers up to NT tiles of 16 dispatched pairs of one expert.
-template <int NT>
-struct Tiles {
-    int n;                 // tiles in this pass
-    int arow[NT];          // A-side activation row (lane & 15) of each tile, clamped to a valid one
-    int drow[NT][4];       // D-side pair positions 4*(lane>>4) + i, -1 past the expert's pairs
-    int dact[NT][4];       // their activation rows (for the block scales), clamped
-};
-
-// rows: for the gate/up pass the activation row is the pair's token, for the
-// down pass the pair's own position
-template <int NT, bool TOKEN_ROWS>
-__device__ inline void tile_rows(const GroupedArgs &a, int n0, int ne, int pb, int lane, Tiles<NT> &T) {
-    const int left = ne - pb;
-    T.n = min(NT, (left + 15) / 16);
-#pragma unroll
-    for (int t = 0; t < NT; ++t) {
-        const int ma = 16 * t + (lane & 15);
-        const int pa = n0 + pb + (ma < left ? ma : 0);
-        T.arow[t] = TOKEN_ROWS ? a.perm[pa] / a.K : pa;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int md = 16 * t + 4 * (lane >> 4) + i;
-            const int pd = n0 + pb + (md < left ? md : 0);
-            T.drow[t][i] = md < left ? pd : -1;
-            T.dact[t][i] = TOKEN_ROWS ? a.perm[pd] / a.K : pd;
-        }
-    }
+// Q4_K B operand of MFMA i from the lane's raw 16-byte qs load of group g_L
+__device__ inline half8_t q4_b(const uint4 &q, int i, int sc) {
+    const uint32_t M = 0x0F0F0F0Fu;
+    uint32_t w0 = (i & 1) ? q.z : q.x, w1 = (i & 1) ? q.w : q.y;
+    if ((i >> 1) & 1) { w0 >>= 4; w1 >>= 4; }
+    return q4_scaled(w0 & M, w1 & M, sc);
 }
 
-// Workgroup = 8 waves: waves 0-3 take 64 rows of up, waves 4-7 the same 64
-// rows of gate (16 rows per wave); one workgroup per (row tile, expert).  Up
-// results meet their gate rows in LDS for the SwiGLU.  Every pass streams the
-// rows once for up to NT*16 of the expert's pairs.
-template <int NT>
-__global__ __launch_bounds__(512) void gateup_grouped_kernel(GroupedArgs a) {
-    const int e = blockIdx.y;
-    const int n0 = a.offsets[e], ne = a.offsets[e + 1] - n0;
-    if (ne <= 0) return;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int n = lane & 15, h = lane >> 4;
-    const bool is_gate = wave >= 4;
-    const int lrow = (wave & 3) * 16 + n;          // row within the tile
-    const int row = blockIdx.x * 64 + lrow;
-    const int nb = a.H / QK;
-    const size_t rb = (size_t)nb * Q4K_BYTES;
-    const uint8_t *base = grouped_expert(a, e);
-    const uint8_t *mat = base ? base + (is_gate ? (size_t)a.I * rb : 0) + (size_t)row * rb : nullptr;
-    __shared__ float s_up[64][16 * NT + 1];
+struct Q4Scales {
+    int sc[2][2];      // [L][nibble]
+    half4_t bm;        // min operand: mins of sub-blocks 2g, 2g+1, g = g_{h & 1}, each twice
+    float d, dmin;
+};
 
-    for (int pb = 0; pb < ne; pb += 16 * NT) {
-        Tiles<NT> T;
-        tile_rows<NT, true>(a, n0, ne, pb, lane, T);
-        float y[NT][4];
+__device__ inline void q4_scales(const uint4 &hdr, int h, Q4Scales &o) {
+    o.d = h2f_dev((uint16_t)(hdr.x & 0xffff));
+    o.dmin = h2f_dev((uint16_t)(hdr.x >> 16));
 #pragma unroll
-        for (int t = 0; t < NT; ++t)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) y[t][i] = 0.0f;
-        if (base) {
-            for (int s = 0; s < nb; ++s) {
-                Q4Frag f;
-                q4_frag(mat + (size_t)s * Q4K_BYTES, h, f);
-#pragma unroll
-                for (int t = 0; t < NT; ++t) {
-                    if (t >= T.n) break;
-                    const _Float16 *xr = (const _Float16 *)a.xa + (size_t)T.arow[t] * a.H + (size_t)s * QK;
-                    float4_t acc = {0, 0, 0, 0};
-#pragma unroll
-                    for (int i = 0; i < 8; ++i) acc = mfma32(*(const half8_t *)(xr + q4_a_offset(h, i)), f.b[i], acc);
-                    const int gm = (h >> 1) + 2 * (h & 1);
-                    const half4_t am = *(const half4_t *)((const _Float16 *)a.xbs +
-                                                          (size_t)T.arow[t] * (a.H / 16) + s * 16 + 4 * gm);
-                    const float4_t z = __builtin_amdgcn_mfma_f32_16x16x16f16(am, f.bm, float4_t{0, 0, 0, 0}, 0, 0, 0);
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) {
-                        // ggml's order: acc += (d*dx)*sumi; acc -= (dmin*dx)*summ
-                        const float dx = a.xdx[(size_t)T.dact[t][i] * nb + s];
-                        y[t][i] = y[t][i] + (f.d * dx) * acc[i];
-                        y[t][i] = y[t][i] - (f.dmin * dx) * z[i];
-                    }
-                    __builtin_amdgcn_sched_barrier(0);
-                }
-            }
+    for (int L = 0; L < 2; ++L) {
+        const int g = (h >> 1) + 2 * L;
+        int m0, m1;
+        q4k_sm(hdr, 2 * g, o.sc[L][0], m0);
+        q4k_sm(hdr, 2 * g + 1, o.sc[L][1], m1);
+        if (L == (h & 1)) {
+            const _Float16 x0 = (_Float16)(float)m0, x1 = (_Float16)(float)m1;
+            o.bm = half4_t{x0, x0, x1, x1};
         }
-        if (!is_gate) {
-#pragma unroll
-            for (int t = 0; t < NT; ++t)
-#pragma unroll
-                for (int i = 0; i < 4; ++i) s_up[lrow][16 * t + 4 * h + i] = y[t][i];
-        }
-        __syncthreads();
-        if (is_gate) {
-#pragma unroll
-            for (int t = 0; t < NT; ++t) {
-                if (t >= T.n) break;
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const int dr = T.drow[t][i];
-                    if (dr >= 0)
-                        a.h[(size_t)dr * a.I + row] = base ? silu_mul(y[t][i], s_up[lrow][16 * t + 4 * h + i]) : 0.0f;
-                }
-            }
-        }
-        __syncthreads();
     }
 }
 
@@ -347,7 +269,7 @@ __global__ __launch_bounds__(512) void gateup_grouped_kernel(GroupedArgs a) {
 // fp16's exact integers, so sc = 16*sh + sl splits it into two exact operands
 // (|(q-32)*sh| <= 256, (q-32)*sl <= 480): sumi = 16*acc_h + acc_l.
 __device__ inline void q6_frag(const uint8_t *blk, int h, half8_t bh[8], half8_t bl[8], float &d) {
-    d = h2f(*(const uint16_t *)(blk + 208));
+    d = h2f_dev(*(const uint16_t *)(blk + 208));
     const uint32_t M = 0x0F0F0F0Fu, HM = 0x30303030u;
     const half8_t c1056 = splat8((_Float16)1056.0f);
 #pragma unroll
@@ -370,101 +292,213 @@ __device__ inline void q6_frag(const uint8_t *blk, int h, half8_t bh[8], half8_t
     }
 }
 
-constexpr int DG_LDS = 64 * 3 * Q6K_BYTES;   // 64 Q6_K rows at I <= 768
+// ---- activation staging ------------------------------------------------------
+// One 256-value block of the activation rows of a pass's pairs, in LDS.  The
+// 16-byte chunk c of row r sits at position c ^ (r & 15), so the 16 rows one
+// fragment read touches fall in distinct banks.
+constexpr int GT = 32;   // pairs per pass (2 M tiles of 16)
 
-// Workgroup = 4 waves = 64 output rows (16 per wave); one workgroup per (row
-// tile, expert).  y times the pair's gate weight goes to the pair's row.
-template <int DT, int NT>
-__global__ __launch_bounds__(256) void down_grouped_kernel(GroupedArgs a) {
+struct __attribute__((aligned(16))) AStage {
+    _Float16 a[GT][QK];
+    _Float16 bs[GT][16];
+};
+
+// Direct global -> LDS loads: lane l of an instruction writes base + 16*l.
+// rows[r]: activation row of pair r of the pass (r < np); rows are K values
+// long.  Wave w stages rows 8w .. 8w+7 (two per instruction), wave 0 also the
+// group sums.  Rows past np are not loaded.
+__device__ inline void stage_a(AStage &st, const int *rows, int np, const uint16_t *xa, const uint16_t *xbs, int K,
+                               int s, int wave, int lane) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int r0 = 8 * wave + 2 * j;
+        if (r0 >= np) break;
+        const int r = min(r0 + (lane >> 5), np - 1);
+        const int c = (lane & 31) ^ ((r0 + (lane >> 5)) & 15);
+        const uint16_t *src = xa + (size_t)rows[r] * K + (size_t)s * QK + 8 * c;
+        __builtin_amdgcn_global_load_lds((gptr_t *)src, (lptr_t *)&st.a[r0][0], 16, 0, 0);
+    }
+    if (wave == 0) {
+        const int r = min(lane >> 1, np - 1);
+        const uint16_t *src = xbs + (size_t)rows[r] * (K / 16) + (size_t)s * 16 + 8 * (lane & 1);
+        __builtin_amdgcn_global_load_lds((gptr_t *)src, (lptr_t *)&st.bs[0][0], 16, 0, 0);
+    }
+}
+
+__device__ inline half8_t stage_frag(const AStage &st, int r, int off) {
+    const int c = (off >> 3) ^ (r & 15);
+    return *(const half8_t *)&st.a[r][8 * c];
+}
+
+constexpr int G6_LDS = 64 * 3 * Q6K_BYTES;   // 64 Q6_K rows at K <= 768
+
+// The grouped product of one (64-row tile, expert): rows of the expert's
+// matrix (up and gate as one 2I-row matrix, or down) against the activation
+// rows of every pair dispatched to the expert, K = NB*256.  Workgroup = 4
+// waves of 16 rows.  Each pass covers up to 32 pairs: block s+1 of their
+// activations is staged in LDS, and block s+1 of the lane's Q4_K row loaded
+// into registers, while block s is decoded and multiplied; a Q6_K tile (rows
+// only 2-byte aligned) is copied into LDS once with direct loads.  up/gate: y2[pair position][row]; down: the pair's
+// gate weight times y, to the pair's (t*K + k) row.
+// (256, 4): at most 128 registers, so four waves share each SIMD and one wave's
+// loads hide behind another's dequantization
+template <int NB, int DT, bool DOWN>
+__global__ __launch_bounds__(256, 4) void grouped_gemm_kernel(GroupedArgs a) {
     const int e = blockIdx.y;
     const int n0 = a.offsets[e], ne = a.offsets[e + 1] - n0;
     if (ne <= 0) return;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int n = lane & 15, h = lane >> 4;
     const int r0 = blockIdx.x * 64;
     const int row = r0 + wave * 16 + n;
-    const int nb = a.I / QK;
-    const int rowb = nb * (DT == TYPE_Q6K ? Q6K_BYTES : Q4K_BYTES);
+    constexpr int K = NB * QK;
+    constexpr int ROWB = NB * (DT == TYPE_Q6K ? Q6K_BYTES : Q4K_BYTES);
+    const int out_n = DOWN ? a.H : 2 * a.I;   // columns of the output rows
     const uint8_t *base = grouped_expert(a, e);
-    const uint8_t *down = base ? base + 2ull * a.I * (a.H / QK) * Q4K_BYTES : nullptr;
-    __shared__ __attribute__((aligned(16))) uint8_t s_w[DT == TYPE_Q6K ? DG_LDS : 16];
-    if (DT == TYPE_Q6K && down) {
-        // 64 rows * rowb bytes from a 16-byte aligned start (64 * 210 = 840 * 16)
-        const uint4 *src = (const uint4 *)(down + (size_t)r0 * rowb);
-        uint4 *dst = (uint4 *)s_w;
-        const int nvec = 64 * rowb / 16;
-        for (int i = threadIdx.x; i < nvec; i += 256) dst[i] = src[i];
-        __syncthreads();
+    if (!base) {
+        for (int i = tid; i < ne * 64; i += 256) {
+            const int pos = n0 + i / 64, c = r0 + (i % 64);
+            if (DOWN) a.ypair[(size_t)a.perm[pos] * a.H + c] = 0.0f;
+            else a.y2[(size_t)pos * out_n + c] = 0.0f;
+        }
+        return;
+    }
+    const uint8_t *mat = DOWN ? base + 2ull * a.I * (a.H / QK) * Q4K_BYTES : base;
+    const uint16_t *act = DOWN ? a.ha : a.xa;
+    const uint16_t *abs16 = DOWN ? a.hbs : a.xbs;
+    const float *adx = DOWN ? a.hdx : a.xdx;
+
+    __shared__ AStage st[2];
+    __shared__ int s_rows[GT];
+    __shared__ float s_dx[GT][NB];
+    __shared__ __attribute__((aligned(16))) uint8_t s_w6[DT == TYPE_Q6K ? G6_LDS : 16];
+
+    const uint8_t *wrow = mat + (size_t)row * ROWB;   // the lane's Q4_K row
+    if (DT == TYPE_Q6K) {
+        // 64 rows * ROWB bytes from a 16-byte aligned start (64 * 210 = 840 * 16)
+        const uint8_t *src = mat + (size_t)r0 * ROWB;
+        constexpr int NV = 64 * ROWB / 16;
+        for (int c0 = 64 * wave; c0 < NV; c0 += 256) {
+            if (c0 + lane < NV)
+                __builtin_amdgcn_global_load_lds((gptr_t *)(src + 16 * (c0 + lane)), (lptr_t *)(s_w6 + 16 * c0), 16,
+                                                 0, 0);
+        }
     }
 
-    for (int pb = 0; pb < ne; pb += 16 * NT) {
-        Tiles<NT> T;
-        tile_rows<NT, false>(a, n0, ne, pb, lane, T);
-        float y[NT][4];
+    for (int pb = 0; pb < ne; pb += GT) {
+        const int np = min(GT, ne - pb);
+        const int nt = (np + 15) / 16;
+        if (tid < GT) {
+            const int pos = n0 + pb + min(tid, np - 1);
+            s_rows[tid] = DOWN ? pos : a.perm[pos] / a.K;
+        }
+        __syncthreads();
+        if (tid < GT * NB) s_dx[tid / NB][tid % NB] = adx[(size_t)s_rows[tid / NB] * NB + (tid % NB)];
+        // block 0: activations staged, the lane's weights in registers; then
+        // block s+1 is in flight (weights to registers, activations to LDS)
+        // while block s is multiplied
+        uint4 cw[3], nw[3];
+        stage_a(st[0], s_rows, np, act, abs16, K, 0, wave, lane);
+        if (DT == TYPE_Q4K) {
+            cw[0] = *(const uint4 *)wrow;
+            cw[1] = *(const uint4 *)(wrow + 16 + 16 * h);
+            cw[2] = *(const uint4 *)(wrow + 80 + 16 * h);
+        }
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+        float y[2][4] = {{0, 0, 0, 0}, {0, 0, 0, 0}};
+        const int gm = (h >> 1) + 2 * (h & 1);
+#pragma unroll 1
+        for (int s = 0; s < NB; ++s) {
+            const AStage &S = st[s & 1];
+            if (s + 1 < NB) {
+                stage_a(st[(s + 1) & 1], s_rows, np, act, abs16, K, s + 1, wave, lane);
+                if (DT == TYPE_Q4K) {
+                    const uint8_t *p = wrow + (s + 1) * Q4K_BYTES;
+                    nw[0] = *(const uint4 *)p;
+                    nw[1] = *(const uint4 *)(p + 16 + 16 * h);
+                    nw[2] = *(const uint4 *)(p + 80 + 16 * h);
+                }
+            }
+            float4_t acc[2] = {{0, 0, 0, 0}, {0, 0, 0, 0}};
+            float d, dmin = 0.0f;
+            half4_t bm;
+            if (DT == TYPE_Q4K) {
+                Q4Scales sc;
+                q4_scales(cw[0], h, sc);
+                d = sc.d;
+                dmin = sc.dmin;
+                bm = sc.bm;
 #pragma unroll
-        for (int t = 0; t < NT; ++t)
+                for (int i = 0; i < 8; ++i) {
+                    const int L = i >> 2, nib = (i >> 1) & 1;
+                    const half8_t b = q4_b(L ? cw[2] : cw[1], i, sc.sc[L][nib]);
+                    const int off = q4_a_offset(h, i);
 #pragma unroll
-            for (int i = 0; i < 4; ++i) y[t][i] = 0.0f;
-        if (base) {
-            for (int s = 0; s < nb; ++s) {
-                half8_t b[8], bl[8];
-                half4_t bm;
-                float d, dmin = 0.0f;
-                if (DT == TYPE_Q6K) {
-                    q6_frag(s_w + (size_t)(wave * 16 + n) * rowb + (size_t)s * Q6K_BYTES, h, b, bl, d);
-                } else {
-                    Q4Frag f;
-                    q4_frag(down + (size_t)row * rowb + (size_t)s * Q4K_BYTES, h, f);
+                    for (int t = 0; t < 2; ++t) acc[t] = mfma32(stage_frag(S, 16 * t + n, off), b, acc[t]);
+                }
+            } else {
+                half8_t bh[8], bl[8];
+                q6_frag(s_w6 + (size_t)(wave * 16 + n) * ROWB + (size_t)s * Q6K_BYTES, h, bh, bl, d);
+                float4_t accl[2] = {{0, 0, 0, 0}, {0, 0, 0, 0}};
 #pragma unroll
-                    for (int i = 0; i < 8; ++i) b[i] = f.b[i];
-                    bm = f.bm;
-                    d = f.d;
-                    dmin = f.dmin;
+                for (int i = 0; i < 8; ++i) {
+                    const int off = 128 * (i >> 2) + 32 * (i & 3) + 8 * h;
+#pragma unroll
+                    for (int t = 0; t < 2; ++t) {
+                        const half8_t av = stage_frag(S, 16 * t + n, off);
+                        acc[t] = mfma32(av, bh[i], acc[t]);
+                        accl[t] = mfma32(av, bl[i], accl[t]);
+                    }
                 }
 #pragma unroll
-                for (int t = 0; t < NT; ++t) {
-                    if (t >= T.n) break;
-                    const _Float16 *hr = (const _Float16 *)a.ha + (size_t)T.arow[t] * a.I + (size_t)s * QK;
-                    float4_t acc = {0, 0, 0, 0}, accl = {0, 0, 0, 0};
+                for (int t = 0; t < 2; ++t)
 #pragma unroll
-                    for (int i = 0; i < 8; ++i) {
-                        const int off = DT == TYPE_Q6K ? 128 * (i >> 2) + 32 * (i & 3) + 8 * h : q4_a_offset(h, i);
-                        const half8_t av = *(const half8_t *)(hr + off);
-                        acc = mfma32(av, b[i], acc);
-                        if (DT == TYPE_Q6K) accl = mfma32(av, bl[i], accl);
-                    }
-                    if (DT == TYPE_Q6K) {
+                    for (int i = 0; i < 4; ++i) acc[t][i] = 16.0f * acc[t][i] + accl[t][i];   // exact integers
+            }
+            // both M tiles every time (no branch merges around the accumulators);
+            // rows past the pass's pairs compute on stale LDS and are never written
 #pragma unroll
-                        for (int i = 0; i < 4; ++i) acc[i] = 16.0f * acc[i] + accl[i];   // exact integers
-                    }
-                    float4_t z = {0, 0, 0, 0};
-                    if (DT == TYPE_Q4K) {
-                        const int gm = (h >> 1) + 2 * (h & 1);
-                        const half4_t am = *(const half4_t *)((const _Float16 *)a.hbs +
-                                                              (size_t)T.arow[t] * (a.I / 16) + s * 16 + 4 * gm);
-                        z = __builtin_amdgcn_mfma_f32_16x16x16f16(am, bm, z, 0, 0, 0);
-                    }
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) {
-                        const float dx = a.hdx[(size_t)T.dact[t][i] * nb + s];
-                        y[t][i] = y[t][i] + (d * dx) * acc[i];
-                        if (DT == TYPE_Q4K) y[t][i] = y[t][i] - (dmin * dx) * z[i];
-                    }
-                    __builtin_amdgcn_sched_barrier(0);
+            for (int t = 0; t < 2; ++t) {
+                float4_t z = {0, 0, 0, 0};
+                if (DT == TYPE_Q4K) {
+                    const half4_t am = *(const half4_t *)&S.bs[16 * t + n][4 * gm];
+                    z = __builtin_amdgcn_mfma_f32_16x16x16f16(am, bm, z, 0, 0, 0);
                 }
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    // ggml's order: acc += (d*dx)*sumi; acc -= (dmin*dx)*summ
+                    const float dx = s_dx[16 * t + 4 * h + i][s];
+                    y[t][i] = y[t][i] + (d * dx) * acc[t][i];
+                    if (DT == TYPE_Q4K) y[t][i] = y[t][i] - (dmin * dx) * z[i];
+                }
+            }
+            __builtin_amdgcn_s_waitcnt(0);
+            __syncthreads();
+            if (DT == TYPE_Q4K) {
+                cw[0] = nw[0];
+                cw[1] = nw[1];
+                cw[2] = nw[2];
             }
         }
 #pragma unroll
-        for (int t = 0; t < NT; ++t) {
-            if (t >= T.n) break;
+        for (int t = 0; t < 2; ++t) {
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                const int dr = T.drow[t][i];
-                if (dr < 0) continue;
-                const int p = a.perm[dr];
-                a.ypair[(size_t)p * a.H + row] = base ? a.w[p] * y[t][i] : 0.0f;
+                const int r = 16 * t + 4 * h + i;
+                if (t < nt && r < np) {
+                    const int pos = n0 + pb + r;
+                    if (DOWN) {
+                        const int p = a.perm[pos];
+                        a.ypair[(size_t)p * a.H + row] = a.w[p] * y[t][i];
+                    } else {
+                        a.y2[(size_t)pos * out_n + row] = y[t][i];
+                    }
+                }
             }
         }
+        __syncthreads();
     }
 }
 
@@ -511,16 +545,38 @@ hipError_t launch_quant_rows(const void *src, int bf16, int n_rows, int n, uint1
                     q16, dx, bs16);
 }
 
-constexpr int GG_NT = 4;
+hipError_t launch_swiglu_quant(const float *y2, int P, int I, float *h_out, uint16_t *q16, float *dx, uint16_t *bs16,
+                               hipStream_t st) {
+    const int64_t blocks = ((int64_t)P * (I / QK) + 3) / 4;
+    if (blocks == 0) return hipSuccess;
+    return launch_b(swiglu_quant_kernel, dim3((unsigned)blocks), dim3(256), st, nullptr, nullptr, y2, P, I, h_out, q16,
+                    dx, bs16);
+}
+
+template <bool DOWN>
+static hipError_t launch_gg(const GroupedArgs &a, hipStream_t st, hipEvent_t e0, hipEvent_t e1) {
+    const int rows = DOWN ? a.H : 2 * a.I;
+    const int nb = (DOWN ? a.I : a.H) / QK;
+    const dim3 grid((unsigned)(rows / 64), (unsigned)a.E), blk(256);
+    if (DOWN) {
+        if (a.down_type == TYPE_Q6K) {
+            if (nb == 3) return launch_b(grouped_gemm_kernel<3, TYPE_Q6K, true>, grid, blk, st, e0, e1, a);
+            if (nb == 2) return launch_b(grouped_gemm_kernel<2, TYPE_Q6K, true>, grid, blk, st, e0, e1, a);
+            return launch_b(grouped_gemm_kernel<1, TYPE_Q6K, true>, grid, blk, st, e0, e1, a);
+        }
+        if (nb == 3) return launch_b(grouped_gemm_kernel<3, TYPE_Q4K, true>, grid, blk, st, e0, e1, a);
+        if (nb == 2) return launch_b(grouped_gemm_kernel<2, TYPE_Q4K, true>, grid, blk, st, e0, e1, a);
+        return launch_b(grouped_gemm_kernel<1, TYPE_Q4K, true>, grid, blk, st, e0, e1, a);
+    }
+    return launch_b(grouped_gemm_kernel<8, TYPE_Q4K, false>, grid, blk, st, e0, e1, a);
+}
 
 hipError_t launch_gateup_grouped(const GroupedArgs &a, hipStream_t st, hipEvent_t e0, hipEvent_t e1) {
-    return launch_b(gateup_grouped_kernel<GG_NT>, dim3((unsigned)(a.I / 64), (unsigned)a.E), dim3(512), st, e0, e1, a);
+    return launch_gg<false>(a, st, e0, e1);
 }
 
 hipError_t launch_down_grouped(const GroupedArgs &a, hipStream_t st, hipEvent_t e0, hipEvent_t e1) {
-    const dim3 grid((unsigned)(a.H / 64), (unsigned)a.E);
-    if (a.down_type == TYPE_Q6K) return launch_b(down_grouped_kernel<TYPE_Q6K, GG_NT>, grid, dim3(256), st, e0, e1, a);
-    return launch_b(down_grouped_kernel<TYPE_Q4K, GG_NT>, grid, dim3(256), st, e0, e1, a);
+    return launch_gg<true>(a, st, e0, e1);
 }
 
 hipError_t launch_combine(const float *ypair, int n_tok, int K, int H, float *out, int accumulate, hipStream_t st) {

@@ -27,6 +27,10 @@ __device__ inline float canon_expf(float x) {
     return p * bits_f32(e << 23);
 }
 
+// binary16 -> binary32 in one hardware conversion (exact for every code,
+// subnormals included: each is a normal fp32 value)
+__device__ inline float h2f_dev(uint16_t h) { return (float)__builtin_bit_cast(_Float16, h); }
+
 __device__ inline float bfly_add(float v) {
 #pragma unroll
     for (int o = 32; o >= 1; o >>= 1) v = v + __shfl_xor(v, o, 64);

@@ -63,7 +63,7 @@ struct GroupedArgs {
     const uint16_t *xa;         // [n_tok][H] Q8_K values of x as fp16
     const float *xdx;           // [n_tok][H/256]
     const uint16_t *xbs;        // [n_tok][H/16] group sums as fp16
-    float *h;                   // [P][I] dispatch order
+    float *y2;                  // [P][2I] up and gate rows of every pair, dispatch order
     const uint16_t *ha;         // [P][I] Q8_K of h as fp16
     const float *hdx;           // [P][I/256]
     const uint16_t *hbs;        // [P][I/16]
@@ -77,6 +77,9 @@ hipError_t launch_quant_rows(const void *src, int bf16, int n_rows, int n, uint1
 hipError_t launch_gateup_grouped(const GroupedArgs &a, hipStream_t st, hipEvent_t e0, hipEvent_t e1);
 hipError_t launch_down_grouped(const GroupedArgs &a, hipStream_t st, hipEvent_t e0, hipEvent_t e1);
 hipError_t launch_combine(const float *ypair, int n_tok, int K, int H, float *out, int accumulate, hipStream_t st);
+// h = silu(gate) * up from y2 and its Q8_K (h itself to h_out when not null)
+hipError_t launch_swiglu_quant(const float *y2, int P, int I, float *h_out, uint16_t *q16, float *dx, uint16_t *bs16,
+                               hipStream_t st);
 
 // ev (optional): [logits start, logits end, select start, select end]
 hipError_t launch_route(const RouteLaunch &l, hipStream_t st, hipEvent_t *ev = nullptr);

@@ -263,8 +263,8 @@ __global__ __launch_bounds__(256) void gateup_kernel(ExpertArgs a) {
             mi += __shfl_xor(mi, 2, 64);
             si += __shfl_xor(si, 4, 64);
             mi += __shfl_xor(mi, 4, 64);
-            const float d = h2f((uint16_t)(hdr.x & 0xffff)) * dx;
-            const float dm = h2f((uint16_t)(hdr.x >> 16)) * dx;
+            const float d = h2f_dev((uint16_t)(hdr.x & 0xffff)) * dx;
+            const float dm = h2f_dev((uint16_t)(hdr.x >> 16)) * dx;
             float v = d * (float)si - dm * (float)mi;
             v = v + __shfl_xor(v, 8, 64);
             v = v + __shfl_xor(v, 16, 64);
@@ -342,8 +342,8 @@ __global__ __launch_bounds__(512) void down_kernel(ExpertArgs a) {
                     for (int i = 0; i < 4; ++i) { xlo[i] = plo[i]; xhi[i] = phi[i]; }
                     const int16_t *bs = (const int16_t *)(xq + 4 + QK);
                     q4k_lane(hdr, qs, u, xlo, xhi, bs[4 * j + (u & 1)], bs[4 * j + 2 + (u & 1)], si, mi);
-                    d = h2f((uint16_t)(hdr.x & 0xffff)) * dx;
-                    dm = h2f((uint16_t)(hdr.x >> 16)) * dx;
+                    d = h2f_dev((uint16_t)(hdr.x & 0xffff)) * dx;
+                    dm = h2f_dev((uint16_t)(hdr.x >> 16)) * dx;
                 } else {
                     const uint8_t *blk = s_w[wave] + g * rowb + b * Q6K_BYTES;
                     const int hh = u >> 2, up4 = u & 3;
@@ -369,7 +369,7 @@ __global__ __launch_bounds__(512) void down_kernel(ExpertArgs a) {
                         dq -= 32 * sx;
                         si += (int32_t)sc[2 * q] * dq;
                     }
-                    d = h2f(*(const uint16_t *)(blk + 208)) * dx;
+                    d = h2f_dev(*(const uint16_t *)(blk + 208)) * dx;
                 }
                 si += __shfl_xor(si, 1, 64);
                 si += __shfl_xor(si, 2, 64);

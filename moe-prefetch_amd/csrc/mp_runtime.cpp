@@ -495,7 +495,7 @@ GroupedWs grouped_ws(int n_tok, int K, int H, int I) {
     w.xa = o;    o += align_up(T * H * 2, 256);
     w.xdx = o;   o += align_up(T * (H / 256) * 4, 256);
     w.xbs = o;   o += align_up(T * (H / 16) * 2, 256);
-    w.h = o;     o += align_up(P * I * 4, 256);
+    w.h = o;     o += align_up(P * 2 * I * 4, 256);   // up and gate rows
     w.ha = o;    o += align_up(P * I * 2, 256);
     w.hdx = o;   o += align_up(P * (I / 256) * 4, 256);
     w.hbs = o;   o += align_up(P * (I / 16) * 2, 256);
@@ -1176,7 +1176,7 @@ int moe_grouped_experts(const moe_grouped_desc *d, void *stream) {
     a.store = d->store; a.expert_bytes = d->expert_bytes; a.n_store = d->n_store;
     a.E = d->E; a.K = d->K; a.H = d->H; a.I = d->I; a.down_type = d->down_type;
     a.xa = (const uint16_t *)(ws + w.xa); a.xdx = (const float *)(ws + w.xdx); a.xbs = (const uint16_t *)(ws + w.xbs);
-    a.h = d->h_out ? d->h_out : (float *)(ws + w.h);
+    a.y2 = (float *)(ws + w.h);
     a.ha = (const uint16_t *)(ws + w.ha); a.hdx = (const float *)(ws + w.hdx); a.hbs = (const uint16_t *)(ws + w.hbs);
     a.ypair = d->pair_out ? d->pair_out : (float *)(ws + w.ypair);
     const int P = d->n_tok * d->K;
@@ -1188,7 +1188,8 @@ int moe_grouped_experts(const moe_grouped_desc *d, void *stream) {
         HIPCHK(mp::launch_quant_rows(d->x, d->x_type == MOE_DTYPE_BF16, d->n_tok, d->H, (uint16_t *)a.xa,
                                      (float *)a.xdx, (uint16_t *)a.xbs, st));
         HIPCHK(mp::launch_gateup_grouped(a, st, ev[0], ev[1]));
-        HIPCHK(mp::launch_quant_rows(a.h, 0, P, d->I, (uint16_t *)a.ha, (float *)a.hdx, (uint16_t *)a.hbs, st));
+        HIPCHK(mp::launch_swiglu_quant(a.y2, P, d->I, d->h_out, (uint16_t *)a.ha, (float *)a.hdx, (uint16_t *)a.hbs,
+                                       st));
         HIPCHK(mp::launch_down_grouped(a, st, ev[2], ev[3]));
         HIPCHK(mp::launch_combine(a.ypair, d->n_tok, d->K, d->H, d->out, d->accumulate, st));
         return MOE_OK;
