@@ -23,8 +23,13 @@
  *   moe_experts             build_moe_ffn expert chain: mul_mat_id(up/gate) -> swiglu -> mul_mat_id(down)
  *                           -> mul(weights) -> sum over k (0008:372-390, 0009:684-704; CPU twin ggml_cpu_moe_rows 0008:186-251)
  *   moe_decode_layer        one cached MoE layer of the decode graph (0009:659-705)
+ *   moe_cache_set_shared    the shared-expert FFN build_moe_ffn's callers add beside the routed
+ *                           experts (ffn_*_shexp; llama.cpp, un-vendored), always resident
  *   moe_decode_token        llama_context::decode for one token over every cached layer followed by
  *                           llama_moe_cache_step (0008:362-369)
+ *   moe_decode_batch        the same for a batch of tokens: the observe callback sees ids [n_tok][K]
+ *                           token-major (0006:295-400); the reference's cached graph handles one token
+ *                           (0007:114), this build serves batches from the same slots
  *   moe_pool_*              the slab/slot store behind src/prefetch_engine.py ExpertCache (:45-168)
  *   moe_dispatch            ggml mul_mat_id's batch row mapping (per-expert counts + mmid_row_mapping,
  *                           visible in 0008:157-167): histogram, exclusive scan, stable (token, k) order
@@ -139,6 +144,8 @@ typedef struct {
     int32_t accumulate;       /* 1: out += sum_k w_k y_k */
     int32_t H, I, K, down_type;
     void *workspace;          /* dev, moe_experts_workspace_bytes(); zero before first use */
+    const uint8_t *shared;    /* dev or NULL: an always-on shared expert ([up|gate|down], expert_bytes),
+                                 weight 1, added after the K routed experts */
 } moe_experts_desc;
 
 size_t moe_route_workspace_bytes(int E, int n_tok);
@@ -199,6 +206,10 @@ int moe_cache_destroy(moe_cache *c);
 /* register caller-owned memory: pinned [E][expert_bytes] store, device [E][H] router */
 int moe_cache_set_host_store(moe_cache *c, int layer, const void *experts, size_t expert_bytes);
 int moe_cache_set_router(moe_cache *c, int layer, const float *W_dev);
+/* Copy an always-on shared expert of `layer` into HBM (host or device source,
+ * the layer's expert_bytes; NULL removes it).  Decoding adds it with weight 1
+ * after the routed experts; the cache never evicts or counts it. */
+int moe_cache_set_shared(moe_cache *c, int layer, const void *expert, size_t expert_bytes);
 int moe_cache_lookup(moe_cache *c, int layer, moe_layer_view *out);
 int moe_cache_trace_open(moe_cache *c, const char *route_path, const char *map_path);
 /* host ids, token-major [n_tok][n_ids] */
@@ -277,6 +288,8 @@ typedef struct {
     void *workspace;            /* dev, moe_grouped_workspace_bytes() */
     float *kernel_ms;           /* host [2] or NULL: when set the call waits for its kernels and
                                    stores the up/gate and down kernel durations (HIP events) */
+    const uint8_t *shared;      /* dev or NULL: an always-on shared expert (expert_bytes), weight 1,
+                                   added to every token after the routed experts */
 } moe_grouped_desc;
 
 size_t moe_grouped_workspace_bytes(int n_tok, int K, int H, int I);
@@ -285,6 +298,15 @@ size_t moe_grouped_workspace_bytes(int n_tok, int K, int H, int I);
 int moe_grouped_experts(const moe_grouped_desc *d, void *stream);
 /* out[t] (+)= sum_k pair_rows[t*K + k], k ascending */
 int moe_combine(const float *pair_rows, int n_tok, int K, int H, float *out, int accumulate, void *stream);
+
+/* One decode step of n_tok tokens (batch > 1) over every layer: x dev [L][n_tok][H],
+ * bias dev [L][n_tok][E] or NULL, out dev [L][n_tok][H].  Per layer: route (with the
+ * cache prior), dispatch, the grouped experts from HBM slots or the pinned store,
+ * and the shared expert; then the routed ids come back in one copy, each layer
+ * observes them token-major and the cache steps.  ids_host [L][n_tok][K] receives
+ * them when not NULL.  n_tok <= 4096. */
+int moe_decode_batch(moe_cache *c, const float *x, const float *bias, float *out, int n_tok, int32_t *ids_host,
+                     void *stream);
 
 /* ---- slab pool behind the Python ExpertCache ------------------------------- */
 typedef struct moe_pool moe_pool;

@@ -502,6 +502,20 @@ __global__ __launch_bounds__(256, 4) void grouped_gemm_kernel(GroupedArgs a) {
     }
 }
 
+// the trivial dispatch of one expert over n pairs: offsets {0, n}, perm = 0..n-1,
+// weights 1 (the always-on shared expert)
+__global__ void iota_kernel(int n, int32_t *offsets, int32_t *perm, float *ones) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) {
+        perm[i] = i;
+        ones[i] = 1.0f;
+    }
+    if (i == 0) {
+        offsets[0] = 0;
+        offsets[1] = n;
+    }
+}
+
 // out[t] (+)= sum_k ypair[t*K + k], k ascending; one float4 per thread
 __global__ __launch_bounds__(256) void combine_kernel(const float *ypair, int n_tok, int K, int H, float *out,
                                                       int accumulate) {
@@ -577,6 +591,11 @@ hipError_t launch_gateup_grouped(const GroupedArgs &a, hipStream_t st, hipEvent_
 
 hipError_t launch_down_grouped(const GroupedArgs &a, hipStream_t st, hipEvent_t e0, hipEvent_t e1) {
     return launch_gg<true>(a, st, e0, e1);
+}
+
+hipError_t launch_iota(int n, int32_t *offsets, int32_t *perm, float *ones, hipStream_t st) {
+    return launch_b(iota_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), st, nullptr, nullptr, n, offsets, perm,
+                    ones);
 }
 
 hipError_t launch_combine(const float *ypair, int n_tok, int K, int H, float *out, int accumulate, hipStream_t st) {

@@ -37,12 +37,15 @@ struct ExpertArgs {
     uint64_t expert_bytes;
     int n_experts;
     const uint8_t *q8x;       // [H/256][292]
-    float *h;                 // scratch [K][I]
-    uint8_t *q8h;             // scratch [K][I/256][292]
+    float *h;                 // scratch [K + n_shared][I]
+    uint8_t *q8h;             // scratch [K + n_shared][I/256][292]
     uint32_t *counter;        // scratch [K], zero
     float *out;               // [H]
     int accumulate;           // 1: out += result
     int H, I, K, down_type;
+    const uint8_t *shared;    // always-on shared expert in HBM (weight 1, combined after the K routed
+                              // ones) or null; it is expert K of the launch
+    int n_shared;             // 1 with a shared expert
 };
 
 constexpr int MAX_E = 256;   // experts per layer the kernels support
@@ -77,6 +80,7 @@ hipError_t launch_quant_rows(const void *src, int bf16, int n_rows, int n, uint1
 hipError_t launch_gateup_grouped(const GroupedArgs &a, hipStream_t st, hipEvent_t e0, hipEvent_t e1);
 hipError_t launch_down_grouped(const GroupedArgs &a, hipStream_t st, hipEvent_t e0, hipEvent_t e1);
 hipError_t launch_combine(const float *ypair, int n_tok, int K, int H, float *out, int accumulate, hipStream_t st);
+hipError_t launch_iota(int n, int32_t *offsets, int32_t *perm, float *ones, hipStream_t st);
 // h = silu(gate) * up from y2 and its Q8_K (h itself to h_out when not null)
 hipError_t launch_swiglu_quant(const float *y2, int P, int I, float *h_out, uint16_t *q16, float *dx, uint16_t *bs16,
                                hipStream_t st);

@@ -180,6 +180,7 @@ constexpr int SRC_ALL = 0, SRC_HBM = 1, SRC_HOST = 2;
 
 __device__ inline bool serves(const ExpertArgs &a, int k, int src) {
     if (src == SRC_ALL) return true;
+    if (k >= a.K) return src == SRC_HBM;     // the shared expert lives in HBM
     const int slot = a.slots[k];
     const bool resident = a.slot_pool && slot >= 0 && slot < a.n_slots;
     return src == SRC_HBM ? resident : !resident;
@@ -188,6 +189,7 @@ __device__ inline bool serves(const ExpertArgs &a, int k, int src) {
 // expert pointers: resident -> HBM slot, absent -> pinned host store
 // (null for an id outside the store: that expert contributes zero)
 __device__ inline const uint8_t *expert_base(const ExpertArgs &a, int k) {
+    if (k >= a.K) return a.shared;
     const int slot = a.slots[k];
     if (a.slot_pool && slot >= 0 && slot < a.n_slots) return a.slot_pool + (size_t)slot * a.slot_bytes;
     const int id = a.ids[k];
@@ -294,13 +296,14 @@ __global__ __launch_bounds__(512) void down_kernel(ExpertArgs a) {
     const int rowb = nb * (DT == TYPE_Q6K ? Q6K_BYTES : Q4K_BYTES);
     __shared__ __attribute__((aligned(16))) uint8_t s_w[8][DN_LDS_ROWS];
     __shared__ __attribute__((aligned(16))) uint8_t s_q8[8][DN_LDS_Q8 + 4];
-    __shared__ float s_y[16][DN_ROWS];
+    __shared__ float s_y[17][DN_ROWS];   // up to 16 routed experts + the shared one
 
     const int g = lane >> 3, u = lane & 7;   // g: row within the tile, u: part of a super-block
-    for (int kb = 0; kb < a.K; kb += 8) {
+    const int kt = a.K + a.n_shared;
+    for (int kb = 0; kb < kt; kb += 8) {
         const int k = kb + wave;
-        const bool mine = k < a.K && serves(a, k, SRC);
-        if (k < a.K && !mine && lane < DN_ROWS) s_y[k][lane] = 0.0f;   // other launch's expert
+        const bool mine = k < kt && serves(a, k, SRC);
+        if (k < kt && !mine && lane < DN_ROWS) s_y[k][lane] = 0.0f;   // other launch's expert
         if (mine) {
             const uint8_t *eb = expert_base(a, k);
             uint4 *dst = (uint4 *)s_w[wave];
@@ -393,6 +396,7 @@ __global__ __launch_bounds__(512) void down_kernel(ExpertArgs a) {
         const int t = threadIdx.x;
         float acc = a.w[0] * s_y[0][t];
         for (int k = 1; k < a.K; ++k) acc = acc + a.w[k] * s_y[k][t];
+        if (a.n_shared) acc = acc + s_y[a.K][t];        // weight 1, after the routed experts
         a.out[r0 + t] = a.accumulate ? a.out[r0 + t] + acc : acc;
     }
 }
@@ -452,7 +456,8 @@ hipError_t launch_route(const RouteLaunch &l, hipStream_t st, hipEvent_t *ev) {
 template <int SRC>
 static hipError_t gateup_src(const ExpertArgs &a, hipStream_t st, hipEvent_t e0, hipEvent_t e1) {
     constexpr int R = 2;
-    return launch(gateup_kernel<R, SRC>, dim3((unsigned)(a.I / (4 * R)), (unsigned)a.K), dim3(256), st, e0, e1, a);
+    return launch(gateup_kernel<R, SRC>, dim3((unsigned)(a.I / (4 * R)), (unsigned)(a.K + a.n_shared)), dim3(256), st,
+                  e0, e1, a);
 }
 
 template <int SRC>

@@ -64,6 +64,7 @@ struct Layer {
     const uint8_t *store_host = nullptr;      // host address of the pinned store
     const uint8_t *store_dev = nullptr;       // device view of it
     const float *router = nullptr;
+    uint8_t *shared = nullptr;                // dev: the always-on shared expert (owned) or null
     std::vector<int32_t> slot_expert, expert_slot, free_slots, pending;
     std::vector<uint64_t> slot_last_use, slot_protect, miss_last, miss_prev;
     std::vector<uint8_t> slot_in_flight;
@@ -119,6 +120,13 @@ struct moe_cache {
     hipGraph_t g[2] = {nullptr, nullptr};
     hipGraphExec_t gx[2] = {nullptr, nullptr};
     int g_mode[2] = {-1, -1};          // (timing, split) the graph was captured with
+    // batched decode (moe_decode_batch): buffers for up to b_cap tokens, grown on demand
+    int b_cap = 0;
+    int32_t *b_ids = nullptr, *b_slots = nullptr, *b_counts = nullptr, *b_offs = nullptr, *b_perm = nullptr;
+    int32_t *bh_ids = nullptr;         // pinned host [L][b_cap][K]
+    float *b_w = nullptr;
+    uint8_t *b_q8x = nullptr;
+    void *b_route_ws = nullptr, *b_ws = nullptr;
 };
 
 struct moe_pool {
@@ -431,9 +439,10 @@ int check_shape(int E, int H, int I, int K) {
 }
 
 size_t route_ws_bytes(int E, int n_tok) { return align_up((size_t)n_tok * E * 4, 256) + align_up((size_t)n_tok * 4, 256); }
+// room for K routed experts and a shared one
 size_t exp_ws_bytes(int I, int K) {
-    return align_up((size_t)K * I * 4, 256) + align_up((size_t)K * (I / 256) * mp::Q8K_BYTES, 256) +
-           align_up((size_t)K * 4, 256);
+    const size_t k1 = (size_t)K + 1;
+    return align_up(k1 * I * 4, 256) + align_up(k1 * (I / 256) * mp::Q8K_BYTES, 256) + align_up(k1 * 4, 256);
 }
 
 int run_route(const moe_route_desc *d, hipStream_t st, hipEvent_t *ev = nullptr) {
@@ -457,11 +466,12 @@ int run_experts(const moe_experts_desc *d, hipStream_t st) {
     a.host_store = d->host_store; a.expert_bytes = d->expert_bytes; a.n_experts = d->n_experts;
     a.q8x = d->q8x; a.out = d->out; a.accumulate = d->accumulate;
     a.H = d->H; a.I = d->I; a.K = d->K; a.down_type = d->down_type;
+    a.shared = d->shared; a.n_shared = d->shared ? 1 : 0;
     uint8_t *ws = (uint8_t *)d->workspace;
     a.h = (float *)ws;
-    size_t o = align_up((size_t)d->K * d->I * 4, 256);
+    size_t o = align_up((size_t)(d->K + 1) * d->I * 4, 256);
     a.q8h = ws + o;
-    o += align_up((size_t)d->K * (d->I / 256) * mp::Q8K_BYTES, 256);
+    o += align_up((size_t)(d->K + 1) * (d->I / 256) * mp::Q8K_BYTES, 256);
     a.counter = (uint32_t *)(ws + o);
     HIPCHK(mp::launch_experts(a, st));
     return MOE_OK;
@@ -485,7 +495,7 @@ int check_weight_ptrs(const char *who, const void *a, const void *b) {
 
 // workspace of the batched expert path, offsets in bytes
 struct GroupedWs {
-    size_t xa, xdx, xbs, h, ha, hdx, hbs, ypair, total;
+    size_t xa, xdx, xbs, h, ha, hdx, hbs, ypair, sh_offs, sh_perm, sh_ones, total;
 };
 
 GroupedWs grouped_ws(int n_tok, int K, int H, int I) {
@@ -500,6 +510,9 @@ GroupedWs grouped_ws(int n_tok, int K, int H, int I) {
     w.hdx = o;   o += align_up(P * (I / 256) * 4, 256);
     w.hbs = o;   o += align_up(P * (I / 16) * 2, 256);
     w.ypair = o; o += align_up(P * H * 4, 256);
+    w.sh_offs = o; o += 256;                              // shared expert: trivial dispatch
+    w.sh_perm = o; o += align_up(T * 4, 256);
+    w.sh_ones = o; o += align_up(T * 4, 256);
     w.total = o;
     return w;
 }
@@ -534,6 +547,11 @@ void free_cache(moe_cache *c) {
     if (c->up_stream) hipStreamDestroy(c->up_stream);
     if (c->tbl_stream) hipStreamDestroy(c->tbl_stream);
     hipFree(c->pool_base);
+    for (auto &ls : c->L) hipFree(ls.shared);
+    for (void *p : {(void *)c->b_ids, (void *)c->b_slots, (void *)c->b_counts, (void *)c->b_offs, (void *)c->b_perm,
+                    (void *)c->b_w, (void *)c->b_q8x, c->b_route_ws, c->b_ws})
+        hipFree(p);
+    if (c->bh_ids) hipHostFree(c->bh_ids);
     hipFree(c->d_tbl);
     hipFree(c->d_prior);
     hipFree(c->route_ws);
@@ -817,6 +835,15 @@ int moe_cache_destroy(moe_cache *c) {
     return MOE_OK;
 }
 
+// captured token graphs hold kernel arguments: drop them when weights move
+static void drop_graphs(moe_cache *c) {
+    for (int i = 0; i < 2; ++i) {
+        if (c->gx[i]) { hipGraphExecDestroy(c->gx[i]); c->gx[i] = nullptr; }
+        if (c->g[i]) { hipGraphDestroy(c->g[i]); c->g[i] = nullptr; }
+        c->g_mode[i] = -1;
+    }
+}
+
 int moe_cache_set_host_store(moe_cache *c, int layer, const void *experts, size_t expert_bytes) {
     if (!c || layer < 0 || layer >= (int)c->L.size() || !experts) return fail(MOE_ERR_ARG, "bad arguments");
     if (c->host_only) return fail(MOE_ERR_STATE, "host-only cache (device < 0) holds no weights");
@@ -827,6 +854,7 @@ int moe_cache_set_host_store(moe_cache *c, int layer, const void *experts, size_
     void *dev = nullptr;
     HIPCHK(hipHostGetDevicePointer(&dev, const_cast<void *>(experts), 0));
     if (((uintptr_t)dev | (uintptr_t)experts) % 16) return fail(MOE_ERR_ARG, "host store must be 16-byte aligned");
+    if (ls.store_dev != dev) drop_graphs(c);
     ls.store_host = (const uint8_t *)experts;
     ls.store_dev = (const uint8_t *)dev;
     return MOE_OK;
@@ -835,7 +863,32 @@ int moe_cache_set_host_store(moe_cache *c, int layer, const void *experts, size_
 int moe_cache_set_router(moe_cache *c, int layer, const float *W_dev) {
     if (!c || layer < 0 || layer >= (int)c->L.size() || !W_dev) return fail(MOE_ERR_ARG, "bad arguments");
     if ((uintptr_t)W_dev % 16) return fail(MOE_ERR_ARG, "router must be 16-byte aligned");
+    if (c->L[layer].router != W_dev) drop_graphs(c);
     c->L[layer].router = W_dev;
+    return MOE_OK;
+}
+
+int moe_cache_set_shared(moe_cache *c, int layer, const void *expert, size_t expert_bytes) {
+    if (!c || layer < 0 || layer >= (int)c->L.size()) return fail(MOE_ERR_ARG, "bad arguments");
+    if (c->host_only) return fail(MOE_ERR_STATE, "host-only cache (device < 0) holds no weights");
+    Layer &ls = c->L[layer];
+    if (!expert) {
+        if (ls.shared) drop_graphs(c);
+        hipFree(ls.shared);
+        ls.shared = nullptr;
+        return MOE_OK;
+    }
+    if (expert_bytes != ls.expert_bytes)
+        return fail(MOE_ERR_ARG, "shared expert of %zu bytes, the layer's experts are %llu", expert_bytes,
+                    (unsigned long long)ls.expert_bytes);
+    if (c->K + 1 > 17) return fail(MOE_ERR_ARG, "a shared expert needs n_expert_used <= 16");
+    HIPCHK(hipSetDevice(c->cfg.device));
+    if (!ls.shared) {
+        if (hipMalloc(&ls.shared, ls.expert_bytes) != hipSuccess)
+            return fail(MOE_ERR_NOMEM, "shared expert of %llu bytes", (unsigned long long)ls.expert_bytes);
+        drop_graphs(c);
+    }
+    HIPCHK(hipMemcpy(ls.shared, expert, expert_bytes, hipMemcpyDefault));
     return MOE_OK;
 }
 
@@ -995,11 +1048,12 @@ static int decode_layer_impl(moe_cache *c, int layer, const float *x, const floa
     a.host_store = ed.host_store; a.expert_bytes = ed.expert_bytes; a.n_experts = ed.n_experts;
     a.q8x = ed.q8x; a.out = ed.out;
     a.H = ed.H; a.I = ed.I; a.K = ed.K; a.down_type = ed.down_type;
+    a.shared = ls.shared; a.n_shared = ls.shared ? 1 : 0;
     uint8_t *ws = (uint8_t *)ed.workspace;
     a.h = (float *)ws;
-    size_t o = align_up((size_t)ed.K * ed.I * 4, 256);
+    size_t o = align_up((size_t)(ed.K + 1) * ed.I * 4, 256);
     a.q8h = ws + o;
-    o += align_up((size_t)ed.K * (ed.I / 256) * mp::Q8K_BYTES, 256);
+    o += align_up((size_t)(ed.K + 1) * (ed.I / 256) * mp::Q8K_BYTES, 256);
     a.counter = (uint32_t *)(ws + o);
     auto E_ = [ev](int i) -> hipEvent_t { return ev ? ev[i] : nullptr; };
     a.accumulate = 0;
@@ -1100,6 +1154,10 @@ int moe_decode_token(moe_cache *c, const float *x, const float *bias, float *out
                 (res ? c->kt.gateup_hbm_bytes : c->kt.gateup_host_bytes) += gu_b;
                 (res ? c->kt.down_hbm_bytes : c->kt.down_host_bytes) += ls.expert_bytes - gu_b;
             }
+            if (ls.shared) {
+                c->kt.gateup_hbm_bytes += gu_b;
+                c->kt.down_hbm_bytes += ls.expert_bytes - gu_b;
+            }
         }
     }
     for (int l = 0; l < NL; ++l) {
@@ -1165,8 +1223,10 @@ int moe_grouped_experts(const moe_grouped_desc *d, void *stream) {
     if (((uintptr_t)d->slot_pool | (uintptr_t)d->store | (uintptr_t)d->x | (uintptr_t)d->out |
          (uintptr_t)d->workspace | (uintptr_t)d->pair_out | (uintptr_t)d->h_out) % 16)
         return fail(MOE_ERR_ARG, "weights, activations and outputs must be 16-byte aligned");
-    const int r = check_weight_ptrs("moe_grouped_experts", d->slot_pool, d->store);
+    int r = check_weight_ptrs("moe_grouped_experts", d->slot_pool, d->store);
     if (r != MOE_OK) return r;
+    if (d->shared && (r = check_weight_ptrs("moe_grouped_experts", d->shared, nullptr)) != MOE_OK) return r;
+    if ((uintptr_t)d->shared % 16) return fail(MOE_ERR_ARG, "shared expert must be 16-byte aligned");
     const hipStream_t st = (hipStream_t)stream;
     const GroupedWs w = grouped_ws(d->n_tok, d->K, d->H, d->I);
     uint8_t *ws = (uint8_t *)d->workspace;
@@ -1192,6 +1252,21 @@ int moe_grouped_experts(const moe_grouped_desc *d, void *stream) {
                                        st));
         HIPCHK(mp::launch_down_grouped(a, st, ev[2], ev[3]));
         HIPCHK(mp::launch_combine(a.ypair, d->n_tok, d->K, d->H, d->out, d->accumulate, st));
+        if (d->shared) {
+            // the shared expert as a one-expert dispatch of every token, added after the routed sum
+            mp::GroupedArgs sa = a;
+            sa.offsets = (const int32_t *)(ws + w.sh_offs);
+            sa.perm = (const int32_t *)(ws + w.sh_perm);
+            sa.w = (const float *)(ws + w.sh_ones);
+            sa.table = nullptr; sa.slot_pool = nullptr; sa.n_slots = 0;
+            sa.store = d->shared; sa.n_store = 1; sa.E = 1; sa.K = 1;
+            HIPCHK(mp::launch_iota(d->n_tok, (int32_t *)sa.offsets, (int32_t *)sa.perm, (float *)sa.w, st));
+            HIPCHK(mp::launch_gateup_grouped(sa, st, nullptr, nullptr));
+            HIPCHK(mp::launch_swiglu_quant(sa.y2, d->n_tok, d->I, nullptr, (uint16_t *)sa.ha, (float *)sa.hdx,
+                                           (uint16_t *)sa.hbs, st));
+            HIPCHK(mp::launch_down_grouped(sa, st, nullptr, nullptr));
+            HIPCHK(mp::launch_combine(sa.ypair, d->n_tok, 1, d->H, d->out, 1, st));
+        }
         return MOE_OK;
     };
     int rc = run();
@@ -1206,6 +1281,78 @@ int moe_grouped_experts(const moe_grouped_desc *d, void *stream) {
         for (auto e : ev) hipEventDestroy(e);
     }
     return rc;
+}
+
+// ---- batched decode through the cache ------------------------------------------
+static int batch_buffers(moe_cache *c, int n_tok) {
+    if (n_tok <= c->b_cap) return MOE_OK;
+    for (void *p : {(void *)c->b_ids, (void *)c->b_slots, (void *)c->b_counts, (void *)c->b_offs, (void *)c->b_perm,
+                    (void *)c->b_w, (void *)c->b_q8x, c->b_route_ws, c->b_ws})
+        hipFree(p);
+    if (c->bh_ids) hipHostFree(c->bh_ids);
+    c->b_ids = c->b_slots = c->b_counts = c->b_offs = c->b_perm = c->bh_ids = nullptr;
+    c->b_w = nullptr;
+    c->b_q8x = nullptr;
+    c->b_route_ws = c->b_ws = nullptr;
+    c->b_cap = 0;
+    const size_t NL = c->L.size(), TK = (size_t)n_tok * c->K;
+    const size_t rws = route_ws_bytes(c->E, n_tok), gws = grouped_ws(n_tok, c->K, c->H, c->I).total;
+    bool ok = hipMalloc(&c->b_ids, NL * TK * 4) == hipSuccess && hipMalloc(&c->b_slots, TK * 4) == hipSuccess &&
+              hipMalloc(&c->b_w, TK * 4) == hipSuccess && hipMalloc(&c->b_counts, (size_t)c->E * 4) == hipSuccess &&
+              hipMalloc(&c->b_offs, ((size_t)c->E + 1) * 4) == hipSuccess && hipMalloc(&c->b_perm, TK * 4) == hipSuccess &&
+              hipMalloc(&c->b_q8x, (size_t)n_tok * (c->H / 256) * mp::Q8K_BYTES) == hipSuccess &&
+              hipMalloc(&c->b_route_ws, rws) == hipSuccess && hipMalloc(&c->b_ws, gws) == hipSuccess &&
+              hipHostMalloc((void **)&c->bh_ids, NL * TK * 4, hipHostMallocDefault) == hipSuccess;
+    if (!ok || hipMemset(c->b_route_ws, 0, rws) != hipSuccess) return fail(MOE_ERR_NOMEM, "batch buffers for %d tokens", n_tok);
+    c->b_cap = n_tok;
+    return MOE_OK;
+}
+
+int moe_decode_batch(moe_cache *c, const float *x, const float *bias, float *out, int n_tok, int32_t *ids_host,
+                     void *stream) {
+    if (!c || !x || !out) return fail(MOE_ERR_ARG, "bad arguments");
+    if (c->host_only) return fail(MOE_ERR_STATE, "host-only cache (device < 0) cannot decode");
+    if (n_tok < 1 || n_tok > 4096) return fail(MOE_ERR_ARG, "n_tok %d out of range 1..4096", n_tok);
+    if (((uintptr_t)x | (uintptr_t)out) % 16) return fail(MOE_ERR_ARG, "x and out must be 16-byte aligned");
+    HIPCHK(hipSetDevice(c->cfg.device));
+    int r = batch_buffers(c, n_tok);
+    if (r != MOE_OK) return r;
+    const hipStream_t st = (hipStream_t)stream;
+    const int NL = (int)c->L.size(), TK = n_tok * c->K;
+    // (the last step published only finished copies: its tables are safe to read)
+    for (int l = 0; l < NL; ++l) {
+        const Layer &ls = c->L[l];
+        if (!ls.router || !ls.store_dev) return fail(MOE_ERR_STATE, "layer %d: router or host store missing", l);
+        const float *xl = x + (size_t)l * n_tok * c->H;
+        moe_route_desc rd{};
+        rd.W = ls.router; rd.x = xl; rd.bias = bias ? bias + (size_t)l * n_tok * c->E : nullptr;
+        rd.prior = c->d_prior ? c->d_prior + (size_t)l * c->E : nullptr;
+        rd.table = c->d_tbl + (size_t)l * c->E;
+        rd.dummy = ls.S;
+        rd.prior_on_logits = c->cfg.prior_on_logits;
+        rd.E = c->E; rd.H = c->H; rd.K = c->K; rd.n_tok = n_tok;
+        rd.ids = c->b_ids + (size_t)l * TK; rd.w = c->b_w; rd.slots = c->b_slots; rd.q8x = c->b_q8x;
+        rd.workspace = c->b_route_ws;
+        if ((r = run_route(&rd, st)) != MOE_OK) return r;
+        HIPCHK(mp::launch_dispatch(rd.ids, TK, c->E, c->b_counts, c->b_offs, c->b_perm, st));
+        moe_grouped_desc gd{};
+        gd.offsets = c->b_offs; gd.perm = c->b_perm; gd.w = c->b_w;
+        gd.x = xl; gd.x_type = MOE_DTYPE_F32;
+        gd.n_tok = n_tok; gd.K = c->K; gd.E = c->E; gd.H = c->H; gd.I = c->I; gd.down_type = ls.down_type;
+        gd.table = c->d_tbl + (size_t)l * c->E;
+        gd.slot_pool = ls.pool; gd.slot_bytes = ls.slot_bytes; gd.n_slots = ls.S;
+        gd.store = ls.store_dev; gd.expert_bytes = ls.expert_bytes; gd.n_store = c->E;
+        gd.out = out + (size_t)l * n_tok * c->H; gd.accumulate = 0;
+        gd.workspace = c->b_ws; gd.shared = ls.shared;
+        if ((r = moe_grouped_experts(&gd, stream)) != MOE_OK) return r;
+    }
+    HIPCHK(hipMemcpyAsync(c->bh_ids, c->b_ids, (size_t)NL * TK * 4, hipMemcpyDeviceToHost, st));
+    HIPCHK(hipStreamSynchronize(st));
+    for (int l = 0; l < NL; ++l) {
+        if ((r = cache_observe(c, l, c->bh_ids + (size_t)l * TK, c->K, n_tok)) != MOE_OK) return r;
+    }
+    if (ids_host) memcpy(ids_host, c->bh_ids, (size_t)NL * TK * 4);
+    return cache_step(c);
 }
 
 // ---- slab pool --------------------------------------------------------------

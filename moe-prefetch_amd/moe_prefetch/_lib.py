@@ -38,7 +38,7 @@ class ExpertsDesc(ctypes.Structure):
                 ("n_slots", I32), ("host_store", P), ("expert_bytes", U64), ("n_experts", I32),
                 ("q8x", P), ("out", P),
                 ("accumulate", I32), ("H", I32), ("I", I32), ("K", I32), ("down_type", I32),
-                ("workspace", P)]
+                ("workspace", P), ("shared", P)]
 
 
 class GroupedDesc(ctypes.Structure):
@@ -47,7 +47,7 @@ class GroupedDesc(ctypes.Structure):
                 ("table", P), ("slot_pool", P), ("slot_bytes", U64), ("n_slots", I32),
                 ("store", P), ("expert_bytes", U64), ("n_store", I32),
                 ("out", P), ("accumulate", I32), ("pair_out", P), ("h_out", P), ("workspace", P),
-                ("kernel_ms", P)]
+                ("kernel_ms", P), ("shared", P)]
 
 
 class CacheConfig(ctypes.Structure):
@@ -108,6 +108,7 @@ SIGNATURES = {
     "moe_cache_destroy": (ctypes.c_int, [P]),
     "moe_cache_set_host_store": (ctypes.c_int, [P, ctypes.c_int, P, SZ]),
     "moe_cache_set_router": (ctypes.c_int, [P, ctypes.c_int, P]),
+    "moe_cache_set_shared": (ctypes.c_int, [P, ctypes.c_int, P, SZ]),
     "moe_cache_lookup": (ctypes.c_int, [P, ctypes.c_int, ctypes.POINTER(LayerView)]),
     "moe_cache_trace_open": (ctypes.c_int, [P, ctypes.c_char_p, ctypes.c_char_p]),
     "moe_cache_observe": (ctypes.c_int, [P, ctypes.c_int, P, ctypes.c_int, ctypes.c_int]),
@@ -122,6 +123,7 @@ SIGNATURES = {
     "moe_cache_kernel_times": (ctypes.c_int, [P, ctypes.POINTER(KernelTimes)]),
     "moe_decode_layer": (ctypes.c_int, [P, ctypes.c_int, P, P, P, P, P, P]),
     "moe_decode_token": (ctypes.c_int, [P, P, P, P, P, P]),
+    "moe_decode_batch": (ctypes.c_int, [P, P, P, P, ctypes.c_int, P, P]),
     "moe_dispatch": (ctypes.c_int, [P, ctypes.c_int, ctypes.c_int, ctypes.c_int, P, P, P, P]),
     "moe_quant_rows": (ctypes.c_int, [P, ctypes.c_int, ctypes.c_int, ctypes.c_int, P, P, P, P]),
     "moe_grouped_workspace_bytes": (SZ, [ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int]),

@@ -118,6 +118,11 @@ class MoeCache:
     def set_router(self, layer, W):
         check(lib().moe_cache_set_router(self.h, layer, _ptr(W)), "set_router")
 
+    def set_shared(self, layer, expert):
+        """Always-on shared expert of `layer` (its [up|gate|down] bytes, host or device); None removes it."""
+        check(lib().moe_cache_set_shared(self.h, layer, _ptr(expert), self.expert_bytes(layer) if expert is not None
+                                         else 0), "set_shared")
+
     def lookup(self, layer):
         v = _lib.LayerView()
         check(lib().moe_cache_lookup(self.h, layer, ctypes.byref(v)), "lookup")
@@ -180,6 +185,15 @@ class MoeCache:
     def decode_layer(self, layer, x, out, bias=None, ids=None, w=None, stream=None):
         check(lib().moe_decode_layer(self.h, layer, _ptr(x), _ptr(bias), _ptr(out), _ptr(ids), _ptr(w),
                                      _ptr(stream)), "decode_layer")
+
+    def decode_batch(self, x, out, bias=None, stream=None, ids_out=None):
+        """x [L, n_tok, H] and out [L, n_tok, H] on the device (bias [L, n_tok, E] or None).
+        Returns the routed ids [L, n_tok, K] (host) after the step has been applied."""
+        n_tok = x.shape[1]
+        ids = ids_out if ids_out is not None else np.empty((self.n_layers, n_tok, self.K), np.int32)
+        check(lib().moe_decode_batch(self.h, _ptr(x), _ptr(bias), _ptr(out), n_tok, ids.ctypes.data, _ptr(stream)),
+              "decode_batch")
+        return ids
 
     def decode_token(self, x, out, bias=None, stream=None, ids_out=None):
         """x [L, H] and out [L, H] on the device (bias [L, E] or None).  Returns the

@@ -46,31 +46,43 @@ def synth_experts_dev(seed, layer, e0, n, I, dt, out_ptr, stride):
 
 
 class Rig:
-    def __init__(self, slots, down_types, T, I=768, seed=42, steer=True, zipf_s=1.1, reuse=0.6, **knobs):
+    def __init__(self, slots, down_types, T, I=768, seed=42, steer=True, zipf_s=1.1, reuse=0.6, E=E, shared=False,
+                 **knobs):
         self.nl = len(slots)
         self.slots, self.down_types, self.T, self.I, self.seed = list(slots), list(down_types), T, I, seed
+        self.E = E
         self.dev = torch.device("cuda:0")
         self.eb = [L().moe_expert_bytes(H, I, dt) for dt in self.down_types]
         self.stores = []
+        self.shared = []        # per layer: uint8 tensor in HBM (expert index E of the generator) or None
         for l in range(self.nl):
             st = Pinned(E * self.eb[l])
             synth_experts_dev(seed, l, 0, E, I, self.down_types[l], st.dev, self.eb[l])
             self.stores.append(st)
+            if shared:
+                sh = torch.empty(self.eb[l], dtype=torch.uint8, device=self.dev)
+                synth_experts_dev(seed, l, E, 1, I, self.down_types[l], sh.data_ptr(), self.eb[l])
+                self.shared.append(sh)
+            else:
+                self.shared.append(None)
         self.W = torch.empty((self.nl, E, H), dtype=torch.float32, device=self.dev)
         _lib.check(L().moe_synth_vec(seed, KIND_ROUTER, 0, self.nl, 0, E, H, 0.02, self.W.data_ptr(), stream()), "W")
         self.x = torch.empty((T, self.nl, H), dtype=torch.float32, device=self.dev)
         _lib.check(L().moe_synth_vec(seed, KIND_X, 0, T, 0, self.nl, H, 1.0, self.x.data_ptr(), stream()), "x")
         self.bias = None
         if steer:
-            tg = [zipf_targets(seed, l, T, s=zipf_s, reuse=reuse) for l in range(self.nl)]
-            self.bias = torch.from_numpy(steering_bias(tg)).to(self.dev)
+            tg = [zipf_targets(seed, l, T, n_experts=E, s=zipf_s, reuse=reuse) for l in range(self.nl)]
+            self.bias = torch.from_numpy(steering_bias(tg, n_experts=E)).to(self.dev)
         torch.cuda.synchronize()
         self.knobs = knobs
-        self.cache = MoeCache(self.nl, intermediate=I, slot_profile=self.slots, down_types=self.down_types,
-                              device=0, **knobs)
+        self.cache = MoeCache(self.nl, n_experts=E, intermediate=I, slot_profile=self.slots,
+                              down_types=self.down_types, device=0, **knobs)
         for l in range(self.nl):
             self.cache.set_host_store(l, self.stores[l].ptr)
             self.cache.set_router(l, self.W[l])
+            if self.shared[l] is not None:
+                self.cache.set_shared(l, self.shared[l])
+        self.shared_h = [None if sh is None else sh.cpu().numpy() for sh in self.shared]
         self.Wh = self.W.cpu().numpy()
         self.xh = self.x.cpu().numpy()
         self.bh = None if self.bias is None else self.bias.cpu().numpy()
@@ -90,12 +102,18 @@ class Rig:
     def oracle_cache(self):
         kn = dict(self.knobs)
         kn.setdefault("admit", "off")
-        return O.Cache(self.slots, **kn)
+        return O.Cache(self.slots, n_experts=self.E, **kn)
 
-    def oracle_layer(self, t, l, ids, w):
+    def oracle_layer(self, t, l, ids, w, x=None):
+        """Routed experts in k order, then the shared expert with weight 1."""
         st, eb = self.stores[l].arr, self.eb[l]
         experts = [st[e * eb:(e + 1) * eb] for e in ids]
-        return O.moe_layer(H, self.I, self.down_types[l], experts, w, self.xh[t, l])
+        w = list(w)
+        if self.shared_h[l] is not None:
+            experts.append(self.shared_h[l])
+            w.append(1.0)
+        return O.moe_layer(H, self.I, self.down_types[l], experts, np.asarray(w, np.float32),
+                           self.xh[t, l] if x is None else x)
 
     def close(self):
         self.cache.close()

@@ -70,6 +70,62 @@ def test_decode_4_layers_window_admission(tmp_path, split, graph):
         rig.close()
 
 
+def test_decode_256_experts_shared_expert(tmp_path):
+    # the wide variant: 256 routed experts (top-8) plus an always-on shared
+    # expert, I = 512, cache prior 0.01, Zipf(1.0) popularity with reuse 0.5
+    rig = Rig([40, 24], [Q4, Q6], T=40, I=512, E=256, shared=True, zipf_s=1.0, reuse=0.5, admit="window",
+              batch_tables=True, cache_prior=0.01)
+    try:
+        worst = check_run(rig, tmp_path)
+        print("worst rel-L2", worst)
+    finally:
+        rig.close()
+
+
+@pytest.mark.parametrize("shape", ["e256_shared_i512", "e128_i768"])
+def test_decode_batch_matches_oracle(shape):
+    # moe_decode_batch: batches of 16 tokens through every layer (route with the
+    # cache prior, dispatch, grouped experts from slots or the pinned store, the
+    # shared expert), observed token-major and stepped: ids, frames and counters
+    # equal to the oracle's, outputs bit for bit
+    if shape == "e256_shared_i512":
+        rig = Rig([48, 32], [Q4, Q6], T=64, I=512, E=256, shared=True, zipf_s=1.0, reuse=0.5, admit="window",
+                  batch_tables=True, cache_prior=0.01)
+    else:
+        rig = Rig([20, 28], [Q6, Q4], T=64, I=768, admit="window", batch_tables=True)
+    nb, B = 4, 16
+    oc = rig.oracle_cache()
+    try:
+        out = torch.empty((rig.nl, B, 2048), dtype=torch.float32, device=rig.dev)
+        for b in range(nb):
+            toks = range(B * b, B * (b + 1))
+            xb = rig.x[B * b:B * (b + 1)].transpose(0, 1).contiguous()
+            bb = None if rig.bias is None else rig.bias[B * b:B * (b + 1)].transpose(0, 1).contiguous()
+            ids = rig.cache.decode_batch(xb, out, bias=bb, stream=torch.cuda.current_stream().cuda_stream)
+            got = out.cpu().numpy()
+            for l in range(rig.nl):
+                tbl, prior = oc.table(l)
+                use_prior = prior if rig.knobs.get("cache_prior", 0.0) > 0 else None
+                want_ids = []
+                for j, t in enumerate(toks):
+                    bias = None if rig.bh is None else rig.bh[t, l]
+                    rids, rw, _, _ = O.route(rig.Wh[l], rig.xh[t, l], 8, bias=bias, prior=use_prior, table=tbl)
+                    assert np.array_equal(ids[l, j], rids), (b, l, j)
+                    want = rig.oracle_layer(t, l, rids, rw)
+                    assert np.array_equal(got[l, j], want), (b, l, j, float(np.abs(got[l, j] - want).max()))
+                    want_ids.append(rids)
+                oc.observe(l, np.stack(want_ids), n_tok=B)
+            oc.step()
+            for l in range(rig.nl):
+                assert np.array_equal(rig.cache.frame(l), oc.frame(l)), (b, l)
+        st, ost = rig.cache.stats(), oc.stats()
+        for k in ("n_hit", "n_miss", "n_scheduled", "n_published", "n_admit_ok", "n_admit_denied"):
+            assert st[k] == ost[k], (k, st[k], ost[k])
+    finally:
+        oc.close()
+        rig.close()
+
+
 def test_decode_cache_prior_delta(tmp_path):
     # no steering: routing is W x alone, and the 0.01 prior on resident
     # experts' probabilities changes the selection
