@@ -25,6 +25,13 @@ delta = 0.01 on the logits; reports the change in hit rate and the relative L2
 of the block outputs against delta = 0, with every routed id of every run
 replayed through the oracle.
 
+--workload wide40: the larger-expert-count shape -- 40 layers of 256 routed
+experts + 1 always-on shared expert (in HBM), intermediate 512, Q4_K/Q6_K mix,
+96 slots/layer, delta = 0.01, Zipf(1.0) reuse 0.5 -- decoded 1024 tokens at
+batch 1 (--warmup 64 + --steps 960), then 128 tokens at batch 16 through the
+batched kernels on the same cache; every routed id of both phases is replayed
+through the oracle.
+
 Prints ONE JSON line (N = 1).  Inputs are resident before timing: weights in
 the pinned store / HBM slots, activations and steering on the device.
 """
@@ -50,9 +57,12 @@ def log(*a):
 
 
 class Workload:
-    """Pinned expert stores, router weights and activations of one 48-layer run."""
+    """Pinned expert stores, router weights, activations and (optionally) a
+    shared expert per layer in HBM for one stacked decode run.  `T1` tokens
+    are decoded one at a time, the `T - T1` after them in batches."""
 
-    def __init__(self, args, steer):
+    def __init__(self, args, steer, n_experts=E, inter=I, shared=False, zipf_s=1.1, reuse=0.6, slots=None,
+                 batch_tokens=0):
         import torch
         import moe_prefetch
         from moe_prefetch import _lib
@@ -61,38 +71,67 @@ class Workload:
         self.L = L = moe_prefetch.lib()
         self.dev = dev = torch.device("cuda:0")
         self.stream = stream = torch.cuda.current_stream().cuda_stream
-        self.NL, self.T = NL, T = args.layers, args.warmup + args.steps
+        self.E, self.I, self.zipf_s, self.reuse = n_experts, inter, zipf_s, reuse
+        self.slots = args.slots if slots is None else slots
+        self.NL = NL = args.layers
+        self.T1 = args.warmup + args.steps
+        self.T = T = self.T1 + batch_tokens
         self.dts = down_types(NL)
-        self.eb = [L.moe_expert_bytes(H, I, dt) for dt in self.dts]
+        self.eb = [L.moe_expert_bytes(H, inter, dt) for dt in self.dts]
         self.zipf_targets, self.steering_bias, self.KIND_X = zipf_targets, steering_bias, KIND_X
         t0 = time.time()
-        log(f"[bench] setup: {NL} layers x {E} experts, store {sum(self.eb) * E / 1e9:.2f} GB pinned")
-        self.stores = []
+        log(f"[bench] setup: {NL} layers x {n_experts} experts{' + shared' if shared else ''}, "
+            f"store {sum(self.eb) * n_experts / 1e9:.2f} GB pinned")
+        self.stores, self.shared = [], []
         for l in range(NL):
-            p = L.moe_host_alloc(E * self.eb[l])
+            p = L.moe_host_alloc(n_experts * self.eb[l])
             if not p:
                 raise MemoryError(L.moe_last_error())
             self.stores.append(p)
-            _lib.check(L.moe_synth_experts(args.seed, l, 0, E, H, I, self.dts[l], 0.02, L.moe_host_device_ptr(p),
-                                           self.eb[l], stream), "synth")
-        self.W = torch.empty((NL, E, H), dtype=torch.float32, device=dev)
-        _lib.check(L.moe_synth_vec(args.seed, KIND_ROUTER, 0, NL, 0, E, H, 0.02, self.W.data_ptr(), stream), "W")
+            _lib.check(L.moe_synth_experts(args.seed, l, 0, n_experts, H, inter, self.dts[l], 0.02,
+                                           L.moe_host_device_ptr(p), self.eb[l], stream), "synth")
+            if shared:     # the generator's expert index n_experts, kept in HBM
+                sh = torch.empty(self.eb[l], dtype=torch.uint8, device=dev)
+                _lib.check(L.moe_synth_experts(args.seed, l, n_experts, 1, H, inter, self.dts[l], 0.02,
+                                               sh.data_ptr(), self.eb[l], stream), "synth shared")
+                self.shared.append(sh)
+            else:
+                self.shared.append(None)
+        self.W = torch.empty((NL, n_experts, H), dtype=torch.float32, device=dev)
+        _lib.check(L.moe_synth_vec(args.seed, KIND_ROUTER, 0, NL, 0, n_experts, H, 0.02, self.W.data_ptr(), stream),
+                   "W")
         self.x = torch.empty((T, NL, H), dtype=torch.float32, device=dev)
         _lib.check(L.moe_synth_vec(args.seed, KIND_X, 0, T, 0, NL, H, 1.0, self.x.data_ptr(), stream), "x")
         self.bias = None
         if steer:
-            tg = [zipf_targets(args.seed, l, T, s=1.1, reuse=0.6) for l in range(NL)]
-            self.bias = torch.from_numpy(steering_bias(tg)).to(dev)
+            tg = [zipf_targets(args.seed, l, T, n_experts=n_experts, s=zipf_s, reuse=reuse) for l in range(NL)]
+            self.bias = torch.from_numpy(steering_bias(tg, n_experts=n_experts)).to(dev)
         torch.cuda.synchronize()
+        self.shared_h = [None if sh is None else sh.cpu().numpy() for sh in self.shared]
         log(f"[bench] setup done in {time.time() - t0:.1f}s")
+
+    def oracle_layer(self, stores, l, rids, rw, x, n_threads):
+        """The oracle's layer output: routed experts in k order, then the shared
+        expert with weight 1."""
+        import numpy as np
+        from oracle import oracle as O
+        eb, base = self.eb[l], stores[l]
+        experts = [base + int(e) * eb if isinstance(base, int) else base[e * eb:(e + 1) * eb] for e in rids]
+        w = list(rw)
+        if self.shared_h[l] is not None:
+            experts.append(self.shared_h[l])
+            w.append(1.0)
+        return O.moe_layer(H, self.I, self.dts[l], experts, np.asarray(w, np.float32), x, n_threads=n_threads)
 
     def cache(self, **knobs):
         from moe_prefetch import MoeCache
-        c = MoeCache(self.NL, intermediate=I, n_slots=self.args.slots, down_types=self.dts, batch_tables=True,
-                     device=0, **knobs)
+        c = MoeCache(self.NL, n_experts=self.E, intermediate=self.I, n_slots=self.slots, down_types=self.dts,
+                     batch_tables=True, device=0, **knobs)
         for l in range(self.NL):
             c.set_host_store(l, self.stores[l])
             c.set_router(l, self.W[l])
+            if self.shared[l] is not None:
+                c.set_shared(l, self.shared[l])
         return c
 
     def decode(self, cache, keep=(), all_out=None):
@@ -101,7 +140,7 @@ class Workload:
         import numpy as np
         torch = self.torch
         out = torch.empty((self.NL, H), dtype=torch.float32, device=self.dev)
-        ids_log = np.empty((self.T, self.NL, K), np.int32)
+        ids_log = np.empty((self.T, self.NL, K), np.int32)     # batched tokens are filled in by decode_batches
         kept = {}
 
         def token(t):
@@ -117,7 +156,7 @@ class Workload:
         torch.cuda.synchronize()
         log(f"[bench] warmup {self.args.warmup} tokens done; timing {self.args.steps}")
         t0 = time.perf_counter()
-        for t in range(self.args.warmup, self.T):
+        for t in range(self.args.warmup, self.T1):
             token(t)
         torch.cuda.synchronize()
         elapsed = time.perf_counter() - t0
@@ -139,8 +178,9 @@ class Workload:
                                    self.stream), "x2")
         b2 = None
         if self.bias is not None:
-            tg2 = [self.zipf_targets(self.args.seed + 1, l, n, s=1.1, reuse=0.6) for l in range(self.NL)]
-            b2 = torch.from_numpy(self.steering_bias(tg2)).to(self.dev)
+            tg2 = [self.zipf_targets(self.args.seed + 1, l, n, n_experts=self.E, s=self.zipf_s, reuse=self.reuse)
+                   for l in range(self.NL)]
+            b2 = torch.from_numpy(self.steering_bias(tg2, n_experts=self.E)).to(self.dev)
         out = torch.empty((self.NL, H), dtype=torch.float32, device=self.dev)
         for t in range(n):
             cache.decode_token(xs[t], out, bias=None if b2 is None else b2[t], stream=self.stream)
@@ -150,48 +190,85 @@ class Workload:
         log(f"[bench] per-kernel timing pass: {n} tokens")
         return kt, n
 
-    def check(self, ids_log, kept, frames, s1, knobs, every=False):
+    def decode_batches(self, cache, B, keep=()):
+        """Tokens T1.. decoded B at a time with moe_decode_batch.  Returns
+        (elapsed s, per-batch ms, stats before / after, ids [T-T1][L][K], kept
+        outputs)."""
+        import numpy as np
+        torch = self.torch
+        n = self.T - self.T1
+        xb, bb = [], []
+        for t0 in range(self.T1, self.T, B):
+            xb.append(self.x[t0:t0 + B].transpose(0, 1).contiguous())
+            bb.append(None if self.bias is None else self.bias[t0:t0 + B].transpose(0, 1).contiguous())
+        out = torch.empty((self.NL, B, H), dtype=torch.float32, device=self.dev)
+        ids = np.empty((n // B, self.NL, B, K), np.int32)
+        kept, per = {}, []
+        s0 = cache.stats()
+        torch.cuda.synchronize()
+        log(f"[bench] timing {n} tokens at batch {B}")
+        t0 = time.perf_counter()
+        for i in range(n // B):
+            ti = time.perf_counter()
+            cache.decode_batch(xb[i], out, bias=bb[i], stream=self.stream, ids_out=ids[i])
+            per.append(round(1e3 * (time.perf_counter() - ti), 3))
+            for j in range(B):
+                if self.T1 + B * i + j in keep:
+                    kept[self.T1 + B * i + j] = out[:, j].cpu().numpy().copy()
+        torch.cuda.synchronize()
+        elapsed = time.perf_counter() - t0
+        s1 = cache.stats()
+        log(f"[bench] timed {n} batched tokens in {elapsed:.3f}s")
+        return elapsed, per, s0, s1, ids.transpose(0, 2, 1, 3).reshape(n, self.NL, K), kept
+
+    def check(self, ids_log, kept, frames, s1, knobs, every=False, batch=1):
         """Full-size properties against the oracle, outside every timed region:
         routed ids (every token and layer when `every` or a prior is on, else
-        one layer per token), frames, counters, and the kept outputs."""
+        one layer per token), frames, counters, and the kept outputs.  Tokens
+        from T1 on were decoded `batch` at a time: observed together, one step
+        per batch, no prior (it biases single-token selection only)."""
         import ctypes
         import numpy as np
         from oracle import oracle as O
         prior_on = knobs.get("cache_prior", 0.0) > 0
         logits_space = knobs.get("prior_space", "probs") == "logits"
-        oc = O.Cache([self.args.slots] * self.NL, admit=knobs.get("admit", "off"), batch_tables=True,
+        oc = O.Cache([self.slots] * self.NL, n_experts=self.E, admit=knobs.get("admit", "off"), batch_tables=True,
                      cache_prior=knobs.get("cache_prior", 0.0))
         Wh, xh = self.W.cpu().numpy(), self.x.cpu().numpy()
         bh = None if self.bias is None else self.bias.cpu().numpy()
-        stores = [np.ctypeslib.as_array((ctypes.c_uint8 * (E * self.eb[l])).from_address(self.stores[l]))
+        stores = [np.ctypeslib.as_array((ctypes.c_uint8 * (self.E * self.eb[l])).from_address(self.stores[l]))
                   for l in range(self.NL)]
         bad, worst, checked = 0, 0.0, 0
-        for t in range(self.T):
+        t = 0
+        while t < self.T:
+            n = 1 if t < self.T1 else batch
             for l in range(self.NL):
-                if every or prior_on or t in kept or l == t % self.NL:
-                    tbl, prior = oc.table(l)
-                    rids, rw, _, _ = O.route(Wh[l], xh[t, l], K, bias=None if bh is None else bh[t, l],
-                                             prior=prior if prior_on else None, table=tbl,
-                                             prior_on_logits=logits_space)
-                    bad += not np.array_equal(rids, ids_log[t, l])
-                    checked += 1
-                    if t in kept:
-                        want = O.moe_layer(H, I, self.dts[l],
-                                           [stores[l][e * self.eb[l]:(e + 1) * self.eb[l]] for e in rids],
-                                           rw, xh[t, l], n_threads=8)
-                        worst = max(worst, float(np.linalg.norm(kept[t][l].astype(np.float64) - want)
-                                                 / np.linalg.norm(want)))
-                oc.observe(l, ids_log[t, l])
+                tbl, prior = oc.table(l)
+                use_prior = prior if prior_on and n == 1 else None
+                for tt in range(t, t + n):
+                    if every or prior_on or tt in kept or l == tt % self.NL:
+                        rids, rw, _, _ = O.route(Wh[l], xh[tt, l], K, bias=None if bh is None else bh[tt, l],
+                                                 prior=use_prior, table=tbl, prior_on_logits=logits_space)
+                        bad += not np.array_equal(rids, ids_log[tt, l])
+                        checked += 1
+                        if tt in kept:
+                            want = self.oracle_layer(stores, l, rids, rw, xh[tt, l], 8)
+                            worst = max(worst, float(np.linalg.norm(kept[tt][l].astype(np.float64) - want)
+                                                     / np.linalg.norm(want)))
+                oc.observe(l, np.ascontiguousarray(ids_log[t:t + n, l]), n_tok=n)
             oc.step()
+            t += n
         os_ = oc.stats()
-        return {"ids_checked": checked, "ids_mismatched": int(bad),
-                "frames_equal": bool(all(np.array_equal(oc.frame(l), frames[l]) for l in range(self.NL))),
-                "counters_equal": bool(all(os_[k] == s1[k] for k in COUNTERS)),
-                "worst_rel_l2": worst, "outputs_checked": len(kept) * self.NL}
+        res = {"ids_checked": checked, "ids_mismatched": int(bad),
+               "frames_equal": bool(all(np.array_equal(oc.frame(l), frames[l]) for l in range(self.NL))),
+               "counters_equal": bool(all(os_[k] == s1[k] for k in COUNTERS)),
+               "worst_rel_l2": worst, "outputs_checked": len(kept) * self.NL}
+        oc.close()
+        return res
 
     def cpu_baseline(self):
-        from oracle import oracle as O
         cores = min(len(os.sched_getaffinity(0)), 16)
+        from oracle import oracle as O
         Wh, xh = self.W.cpu().numpy(), self.x.cpu().numpy()
         bh = None if self.bias is None else self.bias.cpu().numpy()
         log(f"[bench] CPU baseline: oracle decode on {cores} threads for ~{self.args.cpu_seconds}s")
@@ -200,14 +277,13 @@ class Workload:
         while done < self.T and (time.perf_counter() - t0) < self.args.cpu_seconds:
             for l in range(self.NL):
                 rids, rw, _, _ = O.route(Wh[l], xh[done, l], K, bias=None if bh is None else bh[done, l])
-                O.moe_layer(H, I, self.dts[l], [self.stores[l] + int(e) * self.eb[l] for e in rids], rw,
-                            xh[done, l], n_threads=cores)
+                self.oracle_layer(self.stores, l, rids, rw, xh[done, l], cores)
             done += 1
         el = time.perf_counter() - t0
         return {"value": round(done / el, 3), "unit": "tok/s", "cores": cores, "kind": "port",
-                "sample": f"{done} tokens x {self.NL} layers of the same workload, every routed expert computed "
-                          f"on the host from the pinned store (Q8_K activations, integer dots, OpenMP over rows), "
-                          f"{el:.1f}s"}
+                "sample": f"{done} tokens x {self.NL} layers of the same workload, every routed "
+                          f"{'and shared ' if self.shared[0] is not None else ''}expert computed on the host from "
+                          f"the pinned store (Q8_K activations, integer dots, OpenMP over rows), {el:.1f}s"}
 
     def close(self):
         for p in self.stores:
@@ -335,6 +411,52 @@ def run_prior(args, wl):
                    "batch": 1, "layers": args.layers, "slots": args.slots, "cache_prior": 0.01},
         "runs": runs,
     }
+
+
+def run_wide(args, wl):
+    """256 routed experts + 1 shared per layer: --warmup + --steps tokens at
+    batch 1, then the next tokens --batch at a time through moe_decode_batch,
+    on the same cache (delta = 0.01 on selection probabilities, window
+    admission)."""
+    B = args.batch
+    knobs = dict(admit=args.admit, cache_prior=0.01)
+    cache = wl.cache(**knobs)
+    cache.set_decode_path(split=args.path, graph=True)
+    T1, n_b = wl.T1, wl.T - wl.T1
+    el1, s0, s1, ids_log, kept, _ = wl.decode(cache, keep={args.warmup, T1 - 1})
+    el2, per, s2, s3, ids_b, kept_b = wl.decode_batches(cache, B, keep={T1, wl.T - 1})
+    ids_log[T1:] = ids_b
+    kept.update(kept_b)
+    frames = [cache.frame(l) for l in range(wl.NL)]
+    result = {
+        "metric": f"MoE decode tok/s @bs1 ({wl.NL} layers x {wl.E} experts + shared, {wl.slots} slots) + achieved "
+                  f"HBM GB/s; cache hit %",
+        "value": round(args.steps / el1, 2), "unit": "tok/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(1e3 * el1 / args.steps, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "q4_k/q6_k x q8_k int8-dot, fp32 scale (router fp32)",
+        "data": "synthetic (seeded N(0,0.02) experts quantized to Q4_K/Q6_K, N(0,1) activations)",
+        "config": {"workload": f"wide{wl.NL}: {wl.NL} layers x {wl.E} routed experts + 1 shared (HBM), H {H}, "
+                               f"I {wl.I}, top-{K}, {wl.slots} HBM slots/layer over a pinned store, Q6_K down in "
+                               f"odd layers, Zipf({wl.zipf_s}) reuse {wl.reuse}, delta 0.01, admission "
+                               f"{args.admit}, batched tables; {T1} tokens at batch 1 ({args.warmup} warmup), "
+                               f"then {n_b} at batch {B}",
+                   "batch": 1, "layers": wl.NL, "slots": wl.slots, "cache_prior": 0.01},
+        "decode_path": {0: "fused", 1: "fork/join", 2: "serial"}[args.path] + " expert launches, HIP graph per token",
+        "cache": cache_summary(s0, s1, args.steps),
+        f"batch{B}": {"tok_s": round(n_b / el2, 2), "tokens": n_b, "ms_per_batch": per,
+                      "cache": cache_summary(s2, s3, n_b),
+                      "path": "moe_decode_batch: route, dispatch, grouped up/gate + SwiGLU and down on the matrix "
+                              "cores from slots or the pinned store, shared expert, combine; ids back, one cache "
+                              "step per batch (batch buffers allocated in the first call)"},
+    }
+    result.update(kernel_report(*wl.kernel_pass(cache), args.steps, s0, s1))
+    if not args.no_check:
+        log("[bench] replaying every routed id of both phases through the oracle (outside the timed region)")
+        result["check"] = wl.check(ids_log, kept, frames, s3, knobs, every=True, batch=B)
+        log(f"[bench] check: {result['check']}")
+    cache.close()
+    return result
 
 
 MFMA_PEAK_TFLOPS = 2500.0   # dense fp16/bf16
@@ -514,12 +636,14 @@ def run_prefill(args):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=448)
+    ap.add_argument("--steps", type=int, default=None, help="timed batch-1 tokens (448; wide40: 960)")
     ap.add_argument("--warmup", type=int, default=64)
-    ap.add_argument("--workload", default="stacked48", choices=["stacked48", "prior48", "prefill48"])
-    ap.add_argument("--batch", type=int, default=512, help="tokens per chunk (prefill48)")
-    ap.add_argument("--layers", type=int, default=48)
-    ap.add_argument("--slots", type=int, default=56)
+    ap.add_argument("--workload", default="stacked48", choices=["stacked48", "prior48", "prefill48", "wide40"])
+    ap.add_argument("--batch", type=int, default=None, help="tokens per chunk (prefill48: 512) or per batched "
+                                                            "decode step (wide40: 16)")
+    ap.add_argument("--batch-tokens", type=int, default=128, help="wide40: tokens decoded in batches")
+    ap.add_argument("--layers", type=int, default=None, help="48; wide40: 40")
+    ap.add_argument("--slots", type=int, default=None, help="56; wide40: 96")
     ap.add_argument("--admit", default="window")
     ap.add_argument("--seed", type=int, default=42)
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="bounded CPU-baseline sample")
@@ -536,12 +660,28 @@ def main():
               "(the expert-sharded design is described in DESIGN.md); run with --gpus 1", file=sys.stderr)
         sys.exit(2)
 
+    wide = args.workload == "wide40"
+    if args.steps is None:
+        args.steps = 960 if wide else 448
+    if args.layers is None:
+        args.layers = 40 if wide else 48
+    if args.slots is None:
+        args.slots = 96 if wide else 56
+    if args.batch is None:
+        args.batch = 16 if wide else 512
     if args.workload == "prefill48":
         print(json.dumps(run_prefill(args)), flush=True)
         return
     import torch
-    wl = Workload(args, steer=args.workload == "stacked48")
-    result = run_stacked(args, wl) if args.workload == "stacked48" else run_prior(args, wl)
+    if wide:
+        if args.batch_tokens % args.batch:
+            sys.exit("--batch-tokens must be a multiple of --batch")
+        wl = Workload(args, steer=True, n_experts=256, inter=512, shared=True, zipf_s=1.0, reuse=0.5,
+                      batch_tokens=args.batch_tokens)
+        result = run_wide(args, wl)
+    else:
+        wl = Workload(args, steer=args.workload == "stacked48")
+        result = run_stacked(args, wl) if args.workload == "stacked48" else run_prior(args, wl)
     if not args.no_cpu:
         result["cpu_baseline"] = wl.cpu_baseline()
     wl.close()

@@ -42,6 +42,10 @@ struct ExpertArgs {
     uint32_t *counter;        // scratch [K], zero
     float *out;               // [H]
     int accumulate;           // 1: out += result
+    float *ypart;             // scratch [K + n_shared][H] or null: each expert's down rows, kept by the
+                              // first launch of a resident/absent pair for the second
+    int join;                 // 1: second launch of a pair; rows of the experts the first launch
+                              // served come from ypart and out is the whole k-order sum
     int H, I, K, down_type;
     const uint8_t *shared;    // always-on shared expert in HBM (weight 1, combined after the K routed
                               // ones) or null; it is expert K of the launch

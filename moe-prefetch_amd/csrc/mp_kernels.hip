@@ -267,10 +267,15 @@ __global__ __launch_bounds__(256) void gateup_kernel(ExpertArgs a) {
             mi += __shfl_xor(mi, 4, 64);
             const float d = h2f_dev((uint16_t)(hdr.x & 0xffff)) * dx;
             const float dm = h2f_dev((uint16_t)(hdr.x >> 16)) * dx;
-            float v = d * (float)si - dm * (float)mi;
-            v = v + __shfl_xor(v, 8, 64);
-            v = v + __shfl_xor(v, 16, 64);
-            v = v + __shfl_xor(v, 32, 64);
+            const int ps = __builtin_bit_cast(int, d * (float)si), pm = __builtin_bit_cast(int, dm * (float)mi);
+            // the 8 super-blocks in row order, scale term then min term, as
+            // the CPU vec_dot accumulates them (lane 8b holds block b)
+            float v = 0.0f;
+#pragma unroll
+            for (int bb = 0; bb < 8; ++bb) {
+                v = v + __builtin_bit_cast(float, __builtin_amdgcn_readlane(ps, 8 * bb));
+                v = v - __builtin_bit_cast(float, __builtin_amdgcn_readlane(pm, 8 * bb));
+            }
             res[m] = v;
         }
         if (lane == 0) {
@@ -303,7 +308,8 @@ __global__ __launch_bounds__(512) void down_kernel(ExpertArgs a) {
     for (int kb = 0; kb < kt; kb += 8) {
         const int k = kb + wave;
         const bool mine = k < kt && serves(a, k, SRC);
-        if (k < kt && !mine && lane < DN_ROWS) s_y[k][lane] = 0.0f;   // other launch's expert
+        if (k < kt && !mine && lane < DN_ROWS)      // the other launch's expert
+            s_y[k][lane] = a.join ? a.ypart[(size_t)k * a.H + r0 + lane] : 0.0f;
         if (mine) {
             const uint8_t *eb = expert_base(a, k);
             uint4 *dst = (uint4 *)s_w[wave];
@@ -377,18 +383,19 @@ __global__ __launch_bounds__(512) void down_kernel(ExpertArgs a) {
                 si += __shfl_xor(si, 1, 64);
                 si += __shfl_xor(si, 2, 64);
                 si += __shfl_xor(si, 4, 64);
-                float v;
+                // super-block order, scale term then min term (CPU vec_dot order)
+                y = y + d * (float)si;
                 if (DT == TYPE_Q4K) {
                     mi += __shfl_xor(mi, 1, 64);
                     mi += __shfl_xor(mi, 2, 64);
                     mi += __shfl_xor(mi, 4, 64);
-                    v = d * (float)si - dm * (float)mi;
-                } else {
-                    v = d * (float)si;
+                    y = y - dm * (float)mi;
                 }
-                y = b == 0 ? v : y + v;
             }
-            if (u == 0) s_y[k][g] = y;
+            if (u == 0) {
+                s_y[k][g] = y;
+                if (a.ypart && !a.join) a.ypart[(size_t)k * a.H + r0 + g] = y;
+            }
         }
         __syncthreads();
     }

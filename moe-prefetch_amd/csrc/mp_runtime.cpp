@@ -90,6 +90,7 @@ struct moe_cache {
     float *d_prior = nullptr, *h_prior = nullptr;
     // kernel scratch
     void *route_ws = nullptr, *exp_ws = nullptr;
+    float *ypart = nullptr;            // [K + 1][H]: per-expert down rows between the two launches of a split
     int32_t *d_ids = nullptr, *d_slots = nullptr, *h_ids = nullptr;
     float *d_w = nullptr;
     uint8_t *d_q8x = nullptr;
@@ -556,6 +557,7 @@ void free_cache(moe_cache *c) {
     hipFree(c->d_prior);
     hipFree(c->route_ws);
     hipFree(c->exp_ws);
+    hipFree(c->ypart);
     hipFree(c->d_ids);
     hipFree(c->d_slots);
     hipFree(c->d_w);
@@ -803,6 +805,7 @@ int moe_cache_create(const moe_cache_config *cfg, moe_cache **out) {
         return bail(fail(MOE_ERR_HIP, "initial table write"));
     const size_t rws = route_ws_bytes(E, 1), ews = exp_ws_bytes(c->I, c->K);
     if (hipMalloc(&c->route_ws, rws) != hipSuccess || hipMalloc(&c->exp_ws, ews) != hipSuccess ||
+        hipMalloc(&c->ypart, ((size_t)c->K + 1) * c->H * 4) != hipSuccess ||
         hipMalloc(&c->d_ids, (size_t)NL * c->K * 4) != hipSuccess ||
         hipMalloc(&c->d_slots, (size_t)NL * c->K * 4) != hipSuccess ||
         hipMalloc(&c->d_w, (size_t)NL * c->K * 4) != hipSuccess ||
@@ -1057,8 +1060,12 @@ static int decode_layer_impl(moe_cache *c, int layer, const float *x, const floa
     a.counter = (uint32_t *)(ws + o);
     auto E_ = [ev](int i) -> hipEvent_t { return ev ? ev[i] : nullptr; };
     a.accumulate = 0;
+    // split: the first down launch keeps every expert's rows, the second
+    // reads the ones it did not compute and writes sum_k w_k y_k in k order
+    // (the order of one launch over all experts)
+    a.ypart = c->ypart;
     mp::ExpertArgs ah = a;
-    ah.accumulate = 1;
+    ah.join = 1;
     if (c->split == 0) {
         HIPCHK(mp::launch_gateup(a, 0, st, E_(4), E_(5)));
         HIPCHK(mp::launch_down(a, 0, st, E_(6), E_(7)));
@@ -1326,7 +1333,8 @@ int moe_decode_batch(moe_cache *c, const float *x, const float *bias, float *out
         const float *xl = x + (size_t)l * n_tok * c->H;
         moe_route_desc rd{};
         rd.W = ls.router; rd.x = xl; rd.bias = bias ? bias + (size_t)l * n_tok * c->E : nullptr;
-        rd.prior = c->d_prior ? c->d_prior + (size_t)l * c->E : nullptr;
+        // the cache prior biases single-token selection only (patches/0007:114)
+        rd.prior = c->d_prior && n_tok == 1 ? c->d_prior + (size_t)l * c->E : nullptr;
         rd.table = c->d_tbl + (size_t)l * c->E;
         rd.dummy = ls.S;
         rd.prior_on_logits = c->cfg.prior_on_logits;
