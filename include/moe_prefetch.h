@@ -189,6 +189,7 @@ typedef struct {
     uint64_t n_admit_ok, n_admit_denied, n_table_flushes;
     uint64_t bytes_uploaded;
     double publication_wait_us;                  /* time step() spent waiting for copies */
+    uint64_t n_staged;                           /* uploads copied from the HBM staging area */
 } moe_cache_stats;
 
 typedef struct {
@@ -238,8 +239,15 @@ int moe_cache_set_timing(moe_cache *c, int on);
  * 1 resident and absent experts as separate launches on two streams, forked
  * and joined per layer; 2 the same launches one after the other on one stream.
  * graph: replay each token's launches as one captured HIP graph (default 1;
- * timing mode launches eagerly).  Results agree to fp32 summation order. */
+ * timing mode launches eagerly).  Every path gives the same bits. */
 int moe_cache_set_decode_path(moe_cache *c, int split, int graph);
+/* Staged uploads (default on; no counterpart in the reference, which uploads
+ * from the host store, P6:428-440): moe_decode_token's kernels also write each
+ * expert they read from the pinned store into an HBM staging area ([L][K]
+ * experts, allocated at the first token), and an upload scheduled for one of
+ * them in that token's step copies it device to device instead of over PCIe.
+ * The bytes, slots, publication and traces are the same either way. */
+int moe_cache_set_staging(moe_cache *c, int on);
 int moe_cache_kernel_times(moe_cache *c, moe_kernel_times *out);
 
 /* One layer at batch 1: route x (+bias), run the K experts, out = sum_k w_k y_k.

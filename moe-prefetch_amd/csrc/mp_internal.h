@@ -46,6 +46,10 @@ struct ExpertArgs {
                               // first launch of a resident/absent pair for the second
     int join;                 // 1: second launch of a pair; rows of the experts the first launch
                               // served come from ypart and out is the whole k-order sum
+    uint8_t *stage;           // [K][stage_stride] in HBM or null: an expert read from the pinned
+                              // store is also written here, byte for byte, so that an upload of it
+                              // can be a device-to-device copy
+    uint64_t stage_stride;
     int H, I, K, down_type;
     const uint8_t *shared;    // always-on shared expert in HBM (weight 1, combined after the K routed
                               // ones) or null; it is expert K of the launch

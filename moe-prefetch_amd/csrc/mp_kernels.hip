@@ -197,6 +197,17 @@ __device__ inline const uint8_t *expert_base(const ExpertArgs &a, int k) {
     return a.host_store + (size_t)id * a.expert_bytes;
 }
 
+// where the bytes of routed expert k go when the launch reads it from the
+// pinned store: its staging area (null when not staging or not absent)
+__device__ inline uint8_t *stage_base(const ExpertArgs &a, int k) {
+    if (!a.stage || k >= a.K) return nullptr;
+    const int slot = a.slots[k];
+    if (a.slot_pool && slot >= 0 && slot < a.n_slots) return nullptr;
+    const int id = a.ids[k];
+    if (!a.host_store || id < 0 || id >= a.n_experts) return nullptr;
+    return a.stage + (size_t)k * a.stage_stride;
+}
+
 // Q4_K super-block partial of one lane: 16 qs bytes (chunk u) against the
 // matching 32 activation bytes; returns (scale-weighted int dot, min-weighted bsum)
 __device__ inline void q4k_lane(uint4 hdr, uint4 qs, int u, const uint32_t *xlo, const uint32_t *xhi,
@@ -249,6 +260,22 @@ __global__ __launch_bounds__(256) void gateup_kernel(ExpertArgs a) {
         qg[r] = valid ? *(const uint4 *)(gate + off + 16 + 16 * u) : z;
         hu[r] = valid ? *(const uint4 *)(up + off) : z;
         qu[r] = valid ? *(const uint4 *)(up + off + 16 + 16 * u) : z;
+    }
+    if (SRC != SRC_HBM) {
+        uint8_t *sb = stage_base(a, k);
+        if (sb) {       // the same bytes, same offsets, into the staging area
+            uint8_t *su = sb, *sg = sb + (size_t)a.I * rb;
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                const size_t off = (size_t)(row0 + r) * rb + (size_t)b * Q4K_BYTES;
+                if (u == 0) {
+                    *(uint4 *)(sg + off) = hg[r];
+                    *(uint4 *)(su + off) = hu[r];
+                }
+                *(uint4 *)(sg + off + 16 + 16 * u) = qg[r];
+                *(uint4 *)(su + off + 16 + 16 * u) = qu[r];
+            }
+        }
     }
 #pragma unroll
     for (int r = 0; r < R; ++r) {
@@ -330,6 +357,17 @@ __global__ __launch_bounds__(512) void down_kernel(ExpertArgs a) {
             for (int j = 0; j < 5; ++j) {
                 const int i = lane + 64 * j;
                 if (i < nvec) dst[i] = buf[j];
+            }
+            if (SRC != SRC_HBM) {
+                uint8_t *sb = stage_base(a, k);
+                if (sb) {
+                    uint4 *sd = (uint4 *)(sb + 2ull * a.I * (a.H / QK) * Q4K_BYTES + (size_t)r0 * rowb);
+#pragma unroll
+                    for (int j = 0; j < 5; ++j) {
+                        const int i = lane + 64 * j;
+                        if (i < nvec) sd[i] = buf[j];
+                    }
+                }
             }
         }
         __syncthreads();

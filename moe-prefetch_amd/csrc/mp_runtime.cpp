@@ -66,6 +66,7 @@ struct Layer {
     const float *router = nullptr;
     uint8_t *shared = nullptr;                // dev: the always-on shared expert (owned) or null
     std::vector<int32_t> slot_expert, expert_slot, free_slots, pending;
+    std::vector<int32_t> staged;              // [K] expert read from the store at k this token (staged), or -1
     std::vector<uint64_t> slot_last_use, slot_protect, miss_last, miss_prev;
     std::vector<uint8_t> slot_in_flight;
     std::vector<float> heat;
@@ -101,6 +102,18 @@ struct moe_cache {
     hipEvent_t up_mark = nullptr;
     std::deque<Job> jobs;              // issued, not yet published, in issue order
     std::vector<hipEvent_t> free_events;
+    // staged uploads: a decode token's kernels also write every expert they read
+    // from the pinned store into stage [L][K][stage_stride] (HBM); an upload of
+    // such an expert in the step that follows is a device-to-device copy on
+    // stg_stream instead of a PCIe transfer.  The next token's kernels wait for
+    // ev_stg before they overwrite the staging area.
+    bool staging = true;
+    uint8_t *stage = nullptr;
+    size_t stage_stride = 0;
+    bool stage_valid = false, stg_pending = false;
+    hipStream_t stg_stream = nullptr;
+    hipEvent_t ev_stg = nullptr;
+    uint64_t n_staged = 0;
     uint64_t clock = 0, n_steps = 0, n_uploads = 0, n_scheduled = 0, n_copied = 0, n_published = 0;
     uint64_t n_admit_ok = 0, n_admit_denied = 0, n_table_flushes = 0, bytes_uploaded = 0;
     double wait_us = 0.0;
@@ -197,12 +210,24 @@ int start_upload(moe_cache *c, int li, int expert, int slot) {
         return MOE_OK;
     }
     if (!ls.store_host) return fail(MOE_ERR_STATE, "layer %d has no host store registered", li);
-    HIPCHK(hipMemcpyAsync(ls.pool + (size_t)slot * ls.slot_bytes, ls.store_host + (size_t)expert * ls.expert_bytes,
-                          ls.expert_bytes, hipMemcpyHostToDevice, c->up_stream));
+    const uint8_t *staged = nullptr;
+    if (c->stage_valid)
+        for (int k = 0; k < c->K; ++k)
+            if (ls.staged[k] == expert) staged = c->stage + ((size_t)li * c->K + k) * c->stage_stride;
+    uint8_t *dst = ls.pool + (size_t)slot * ls.slot_bytes;
+    hipStream_t s = staged ? c->stg_stream : c->up_stream;
+    if (staged) {
+        HIPCHK(hipMemcpyAsync(dst, staged, ls.expert_bytes, hipMemcpyDeviceToDevice, s));
+        c->stg_pending = true;
+        c->n_staged++;
+    } else {
+        HIPCHK(hipMemcpyAsync(dst, ls.store_host + (size_t)expert * ls.expert_bytes, ls.expert_bytes,
+                              hipMemcpyHostToDevice, s));
+    }
     if (c->cfg.publish == MOE_PUBLISH_LIVE) {
         j.ev = take_event(c);
         if (!j.ev) return fail(MOE_ERR_HIP, "event creation failed");
-        HIPCHK(hipEventRecord(j.ev, c->up_stream));
+        HIPCHK(hipEventRecord(j.ev, s));
     }
     c->jobs.push_back(j);
     c->bytes_uploaded += ls.expert_bytes;
@@ -300,6 +325,7 @@ int cache_step(moe_cache *c) {
             const auto t0 = std::chrono::steady_clock::now();
             HIPCHK(hipEventRecord(c->up_mark, c->up_stream));
             HIPCHK(hipEventSynchronize(c->up_mark));
+            HIPCHK(hipStreamSynchronize(c->stg_stream));
             c->wait_us += std::chrono::duration<double, std::micro>(std::chrono::steady_clock::now() - t0).count();
             done.assign(c->jobs.begin(), c->jobs.end());
             c->jobs.clear();
@@ -530,6 +556,7 @@ void free_cache(moe_cache *c) {
         return;
     }
     if (c->up_stream) hipStreamSynchronize(c->up_stream);
+    if (c->stg_stream) hipStreamSynchronize(c->stg_stream);
     for (Job &j : c->jobs)
         if (j.ev) hipEventDestroy(j.ev);
     for (hipEvent_t e : c->free_events) hipEventDestroy(e);
@@ -546,6 +573,9 @@ void free_cache(moe_cache *c) {
     hipFree(c->bias_buf);
     hipFree(c->out_buf);
     if (c->up_stream) hipStreamDestroy(c->up_stream);
+    if (c->stg_stream) hipStreamDestroy(c->stg_stream);
+    if (c->ev_stg) hipEventDestroy(c->ev_stg);
+    hipFree(c->stage);
     if (c->tbl_stream) hipStreamDestroy(c->tbl_stream);
     hipFree(c->pool_base);
     for (auto &ls : c->L) hipFree(ls.shared);
@@ -766,6 +796,7 @@ int moe_cache_create(const moe_cache_config *cfg, moe_cache **out) {
         ls.slot_last_use.assign(ls.S, 0);
         ls.slot_protect.assign(ls.S, 0);
         ls.slot_in_flight.assign(ls.S, 0);
+        ls.staged.assign(c->K, -1);
         ls.free_slots.resize(ls.S);
         for (int s = 0; s < ls.S; ++s) ls.free_slots[s] = ls.S - 1 - s;
         if (cfg->admit_mode == MOE_ADMIT_HEAT) ls.heat.assign(E, 0.0f);
@@ -818,6 +849,8 @@ int moe_cache_create(const moe_cache_config *cfg, moe_cache **out) {
         hipStreamCreateWithFlags(&c->tbl_stream, hipStreamNonBlocking) != hipSuccess ||
         hipStreamCreateWithFlags(&c->host_stream, hipStreamNonBlocking) != hipSuccess ||
         hipEventCreateWithFlags(&c->up_mark, hipEventDisableTiming) != hipSuccess ||
+        hipStreamCreateWithFlags(&c->stg_stream, hipStreamNonBlocking) != hipSuccess ||
+        hipEventCreateWithFlags(&c->ev_stg, hipEventDisableTiming) != hipSuccess ||
         hipEventCreateWithFlags(&c->ev_route, hipEventDisableTiming) != hipSuccess ||
         hipEventCreateWithFlags(&c->ev_hbm, hipEventDisableTiming) != hipSuccess ||
         hipEventCreateWithFlags(&c->ev_host, hipEventDisableTiming) != hipSuccess ||
@@ -973,6 +1006,7 @@ int moe_cache_stats_get(moe_cache *c, moe_cache_stats *s) {
     s->n_admit_ok = c->n_admit_ok;
     s->n_admit_denied = c->n_admit_denied;
     s->n_table_flushes = c->n_table_flushes;
+    s->n_staged = c->n_staged;
     s->bytes_uploaded = c->bytes_uploaded;
     s->publication_wait_us = c->wait_us;
     return MOE_OK;
@@ -983,6 +1017,13 @@ int moe_cache_set_decode_path(moe_cache *c, int split, int graph) {
     if (split < 0 || split > 2) return fail(MOE_ERR_ARG, "split must be 0, 1 or 2");
     c->split = split;
     c->graph = graph != 0;
+    return MOE_OK;
+}
+
+int moe_cache_set_staging(moe_cache *c, int on) {
+    if (!c) return fail(MOE_ERR_ARG, "null cache");
+    if (c->staging != (on != 0)) drop_graphs(c);      // the captured launches carry the staging pointers
+    c->staging = on != 0;
     return MOE_OK;
 }
 
@@ -1004,11 +1045,12 @@ int moe_cache_sync(moe_cache *c) {
     if (!c) return fail(MOE_ERR_ARG, "null cache");
     if (c->host_only) return MOE_OK;
     HIPCHK(hipStreamSynchronize(c->up_stream));
+    HIPCHK(hipStreamSynchronize(c->stg_stream));
     return MOE_OK;
 }
 
 static int decode_layer_impl(moe_cache *c, int layer, const float *x, const float *bias, float *out,
-                             int32_t *ids_dev, float *w_dev, hipStream_t st, hipEvent_t *ev);
+                             int32_t *ids_dev, float *w_dev, hipStream_t st, hipEvent_t *ev, bool stage = false);
 
 int moe_decode_layer(moe_cache *c, int layer, const float *x, const float *bias, float *out, int32_t *ids_dev,
                      float *w_dev, void *stream) {
@@ -1016,7 +1058,7 @@ int moe_decode_layer(moe_cache *c, int layer, const float *x, const float *bias,
 }
 
 static int decode_layer_impl(moe_cache *c, int layer, const float *x, const float *bias, float *out,
-                             int32_t *ids_dev, float *w_dev, hipStream_t st, hipEvent_t *ev) {
+                             int32_t *ids_dev, float *w_dev, hipStream_t st, hipEvent_t *ev, bool stage) {
     if (!c || !x || !out || layer < 0 || layer >= (int)c->L.size()) return fail(MOE_ERR_ARG, "bad arguments");
     if (c->host_only) return fail(MOE_ERR_STATE, "host-only cache (device < 0) cannot decode");
     const Layer &ls = c->L[layer];
@@ -1052,6 +1094,10 @@ static int decode_layer_impl(moe_cache *c, int layer, const float *x, const floa
     a.q8x = ed.q8x; a.out = ed.out;
     a.H = ed.H; a.I = ed.I; a.K = ed.K; a.down_type = ed.down_type;
     a.shared = ls.shared; a.n_shared = ls.shared ? 1 : 0;
+    if (stage && c->stage) {
+        a.stage = c->stage + (size_t)layer * c->K * c->stage_stride;
+        a.stage_stride = c->stage_stride;
+    }
     uint8_t *ws = (uint8_t *)ed.workspace;
     a.h = (float *)ws;
     size_t o = align_up((size_t)(ed.K + 1) * ed.I * 4, 256);
@@ -1104,13 +1150,30 @@ int moe_decode_token(moe_cache *c, const float *x, const float *bias, float *out
         c->tev.assign((size_t)NL * 12, nullptr);
         for (auto &e : c->tev) HIPCHK(hipEventCreate(&e));
     }
+    if (c->staging && !c->stage) {
+        size_t sb = 0;
+        for (const Layer &ls : c->L) sb = std::max(sb, (size_t)ls.slot_bytes);
+        if (hipMalloc(&c->stage, (size_t)NL * c->K * sb) != hipSuccess) {
+            c->stage = nullptr;
+            return fail(MOE_ERR_NOMEM, "staging area of %zu bytes", (size_t)NL * c->K * sb);
+        }
+        c->stage_stride = sb;
+        drop_graphs(c);
+    }
+    const bool stage = c->staging && c->stage;
+    // the last step's device-to-device uploads read the staging area this
+    // token's kernels are about to overwrite
+    if (c->stg_pending) {
+        HIPCHK(hipStreamWaitEvent(st, c->ev_stg, 0));
+        c->stg_pending = false;
+    }
     // per-kernel HIP-event timing needs eager launches: hipEventElapsedTime
     // does not accept events recorded as nodes of a graph
     if (!c->graph || c->timing) {
         for (int l = 0; l < NL; ++l) {
             const int r = decode_layer_impl(c, l, x + (size_t)l * c->H, bias ? bias + (size_t)l * c->E : nullptr,
                                             out + (size_t)l * c->H, nullptr, nullptr, st,
-                                            c->timing ? c->tev.data() + (size_t)l * 12 : nullptr);
+                                            c->timing ? c->tev.data() + (size_t)l * 12 : nullptr, stage);
             if (r != MOE_OK) return r;
         }
     } else {
@@ -1123,7 +1186,7 @@ int moe_decode_token(moe_cache *c, const float *x, const float *bias, float *out
             int r = MOE_OK;
             for (int l = 0; l < NL && r == MOE_OK; ++l)
                 r = decode_layer_impl(c, l, c->x_buf + (size_t)l * c->H, key ? c->bias_buf + (size_t)l * c->E : nullptr,
-                                      c->out_buf + (size_t)l * c->H, nullptr, nullptr, c->cap_stream, nullptr);
+                                      c->out_buf + (size_t)l * c->H, nullptr, nullptr, c->cap_stream, nullptr, stage);
             hipGraph_t g = nullptr;
             const hipError_t ec = hipStreamEndCapture(c->cap_stream, &g);
             if (r != MOE_OK) { if (g) hipGraphDestroy(g); return r; }
@@ -1167,12 +1230,28 @@ int moe_decode_token(moe_cache *c, const float *x, const float *bias, float *out
             }
         }
     }
-    for (int l = 0; l < NL; ++l) {
-        const int r = cache_observe(c, l, c->h_ids + (size_t)l * c->K, c->K, 1);
-        if (r != MOE_OK) return r;
+    // which routed experts the kernels read from the store (and staged): the
+    // tables have not changed since the route, so absent now = absent then
+    if (stage) {
+        for (int l = 0; l < NL; ++l) {
+            Layer &ls = c->L[l];
+            for (int k = 0; k < c->K; ++k) {
+                const int id = c->h_ids[(size_t)l * c->K + k];
+                ls.staged[k] = id >= 0 && id < ls.E && ls.expert_slot[id] < 0 ? id : -1;
+            }
+        }
     }
-    if (ids_host) memcpy(ids_host, c->h_ids, (size_t)NL * c->K * 4);
-    return cache_step(c);
+    // (early issue starts uploads inside observe: staged copies apply there too)
+    c->stage_valid = stage;
+    int r = MOE_OK;
+    for (int l = 0; l < NL && r == MOE_OK; ++l) r = cache_observe(c, l, c->h_ids + (size_t)l * c->K, c->K, 1);
+    if (r == MOE_OK) {
+        if (ids_host) memcpy(ids_host, c->h_ids, (size_t)NL * c->K * 4);
+        r = cache_step(c);
+    }
+    c->stage_valid = false;
+    if (c->stg_pending) HIPCHK(hipEventRecord(c->ev_stg, c->stg_stream));
+    return r;
 }
 
 // ---- batched path -------------------------------------------------------------

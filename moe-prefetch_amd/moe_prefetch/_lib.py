@@ -63,7 +63,7 @@ class CacheStats(ctypes.Structure):
     _fields_ = [(n, U64) for n in ("n_steps", "clock", "n_hit", "n_miss", "n_uploads", "n_scheduled",
                                    "n_copied", "n_published", "n_admit_ok", "n_admit_denied",
                                    "n_table_flushes", "bytes_uploaded")] + \
-               [("publication_wait_us", ctypes.c_double)]
+               [("publication_wait_us", ctypes.c_double), ("n_staged", ctypes.c_uint64)]
 
 
 class LayerView(ctypes.Structure):
@@ -120,6 +120,7 @@ SIGNATURES = {
     "moe_cache_sync": (ctypes.c_int, [P]),
     "moe_cache_set_timing": (ctypes.c_int, [P, ctypes.c_int]),
     "moe_cache_set_decode_path": (ctypes.c_int, [P, ctypes.c_int, ctypes.c_int]),
+    "moe_cache_set_staging": (ctypes.c_int, [P, ctypes.c_int]),
     "moe_cache_kernel_times": (ctypes.c_int, [P, ctypes.POINTER(KernelTimes)]),
     "moe_decode_layer": (ctypes.c_int, [P, ctypes.c_int, P, P, P, P, P, P]),
     "moe_decode_token": (ctypes.c_int, [P, P, P, P, P, P]),

@@ -176,6 +176,11 @@ class MoeCache:
     def set_timing(self, on=True):
         check(lib().moe_cache_set_timing(self.h, int(on)), "set_timing")
 
+    def set_staging(self, on=True):
+        """Uploads of experts a decode token just read from the pinned store are
+        copied from an HBM staging area instead of over PCIe (default on)."""
+        check(lib().moe_cache_set_staging(self.h, int(on)), "set_staging")
+
     def kernel_times(self):
         t = _lib.KernelTimes()
         check(lib().moe_cache_kernel_times(self.h, ctypes.byref(t)), "kernel_times")

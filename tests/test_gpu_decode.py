@@ -13,7 +13,7 @@ import numpy as np
 import pytest
 import torch
 
-from gpu_rig import Rig
+from gpu_rig import L, Rig
 from moe_prefetch import ExpertCache, _lib
 from oracle import oracle as O
 
@@ -151,6 +151,45 @@ def test_decode_knobs(tmp_path, knobs):
         check_run(rig, tmp_path, out_every=3)
     finally:
         rig.close()
+
+
+@pytest.mark.parametrize("knobs", [dict(admit="window", batch_tables=True),
+                                   dict(admit="off", early_issue=True, max_inserts=3)], ids=["window", "early"])
+def test_staged_uploads_fill_slots(knobs):
+    # uploads of experts the token read from the pinned store are copied from
+    # the HBM staging area: afterwards every occupied slot holds its expert's
+    # bytes, and ids, frames, outputs and counters equal a run with staging off
+    T = 40
+    runs = {}
+    for staging in (True, False):
+        rig = Rig([12, 20, 16], [Q4, Q6, Q4], T=T, **knobs)
+        rig.cache.set_staging(staging)
+        try:
+            ids, outs, frames = rig.run()
+            rig.cache.sync()
+            st = rig.cache.stats()
+            for l in range(rig.nl):
+                v = rig.cache.lookup(l)
+                eb = rig.eb[l]
+                back = np.empty(eb, np.uint8)
+                for s, e in enumerate(rig.cache.frame(l)):
+                    if e < 0:
+                        continue
+                    assert L().moe_memcpy(back.ctypes.data, v.slot_pool + s * v.slot_bytes, eb) == 0
+                    assert np.array_equal(back, rig.stores[l].arr[e * eb:(e + 1) * eb]), (staging, l, s, e)
+            runs[staging] = (ids, outs, frames, st)
+        finally:
+            rig.close()
+    on, off = runs[True], runs[False]
+    assert on[3]["n_scheduled"] > 0
+    assert on[3]["n_staged"] == on[3]["n_scheduled"]      # every upload was of an expert the token read
+    assert off[3]["n_staged"] == 0
+    for t in range(T):
+        assert np.array_equal(on[0][t], off[0][t]) and np.array_equal(on[1][t], off[1][t]), t
+        for l in range(3):
+            assert np.array_equal(on[2][t][l], off[2][t][l]), (t, l)
+    for k in ("n_hit", "n_miss", "n_scheduled", "n_published", "bytes_uploaded"):
+        assert on[3][k] == off[3][k], k
 
 
 def test_decode_48_layers_full_shape(tmp_path):
