@@ -171,6 +171,7 @@ class Workload:
         resident and absent experts as separate launches."""
         torch, L, _lib = self.torch, self.L, self._lib
         n = min(self.args.kernel_steps, self.args.steps)
+        cache.set_sidecar(0)                    # GPU kernels only, resident and absent experts apart
         cache.set_decode_path(split=2, graph=False)
         cache.set_timing(True)
         xs = torch.empty((n, self.NL, H), dtype=torch.float32, device=self.dev)
@@ -346,11 +347,38 @@ def kernel_report(kt, n_tok, steps, s0, s1):
     }
 
 
+def sidecar_setup(args, cache):
+    if args.sidecar > 0:
+        num, den = (int(v) for v in args.share.split("/"))
+        cache.set_sidecar(args.sidecar, (num, den))
+
+
+def sidecar_report(args, s0, s1, steps, log_rows=None):
+    if args.sidecar <= 0:
+        return {"threads": 0}
+    extra = {}
+    if log_rows is not None and len(log_rows):
+        import numpy as np
+        for n in (1, 2, 3):
+            sel = log_rows[log_rows[:, 2] == n]
+            if len(sel):
+                extra[f"cpu_us_{n}_experts_p50_p90_max"] = [round(float(np.percentile(sel[:, 1], q)), 1)
+                                                           for q in (50, 90, 100)]
+        extra["wait_us_p50_p90_max"] = [round(float(np.percentile(log_rows[:, 0], q)), 1) for q in (50, 90, 100)]
+    return {"threads": args.sidecar, "share": args.share, **extra,
+            "cpu_served_per_token": round((s1["n_cpu_served"] - s0["n_cpu_served"]) / steps, 2),
+            "host_wait_ms_per_token": round((s1["sidecar_wait_us"] - s0["sidecar_wait_us"]) / 1e3 / steps, 4),
+            "host_cpu_ms_per_token": round((s1["sidecar_cpu_us"] - s0["sidecar_cpu_us"]) / 1e3 / steps, 4),
+            "path": "absent experts assigned to the host computed by its CPU team (AVX-512 VNNI integer dots) "
+                    "from the pinned store while the GPU runs the rest; posted / joined through mapped memory"}
+
+
 def run_stacked(args, wl):
     T = args.warmup + args.steps
     knobs = dict(admit=args.admit)
     cache = wl.cache(**knobs)
     cache.set_decode_path(split=args.path, graph=True)
+    sidecar_setup(args, cache)
     elapsed, s0, s1, ids_log, kept, frames = wl.decode(cache, keep={args.warmup, T - 1})
     result = {
         "metric": METRIC, "value": round(args.steps / elapsed, 2), "unit": "tok/s", "n_gpus": 1,
@@ -365,6 +393,7 @@ def run_stacked(args, wl):
                    "batch": 1, "layers": args.layers, "slots": args.slots},
         "decode_path": {0: "fused", 1: "fork/join", 2: "serial"}[args.path] + " expert launches, HIP graph per token",
         "cache": cache_summary(s0, s1, args.steps),
+        "sidecar": sidecar_report(args, s0, s1, args.steps, cache.sidecar_log() if args.sidecar > 0 else None),
     }
     result.update(kernel_report(*wl.kernel_pass(cache), args.steps, s0, s1))
     if not args.no_check:
@@ -422,6 +451,7 @@ def run_wide(args, wl):
     knobs = dict(admit=args.admit, cache_prior=0.01)
     cache = wl.cache(**knobs)
     cache.set_decode_path(split=args.path, graph=True)
+    sidecar_setup(args, cache)
     T1, n_b = wl.T1, wl.T - wl.T1
     el1, s0, s1, ids_log, kept, _ = wl.decode(cache, keep={args.warmup, T1 - 1})
     el2, per, s2, s3, ids_b, kept_b = wl.decode_batches(cache, B, keep={T1, wl.T - 1})
@@ -444,6 +474,7 @@ def run_wide(args, wl):
                    "batch": 1, "layers": wl.NL, "slots": wl.slots, "cache_prior": 0.01},
         "decode_path": {0: "fused", 1: "fork/join", 2: "serial"}[args.path] + " expert launches, HIP graph per token",
         "cache": cache_summary(s0, s1, args.steps),
+        "sidecar": sidecar_report(args, s0, s1, args.steps),
         f"batch{B}": {"tok_s": round(n_b / el2, 2), "tokens": n_b, "ms_per_batch": per,
                       "cache": cache_summary(s2, s3, n_b),
                       "path": "moe_decode_batch: route, dispatch, grouped up/gate + SwiGLU and down on the matrix "
@@ -649,6 +680,9 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="bounded CPU-baseline sample")
     ap.add_argument("--kernel-steps", type=int, default=64, help="eager tokens timed per kernel")
     ap.add_argument("--path", type=int, default=0, help="0 fused, 1 fork/join, 2 serial expert launches")
+    ap.add_argument("--sidecar", type=int, default=0, help="host threads serving absent experts (0: GPU only)")
+    ap.add_argument("--share", default="1/1", help="num/den: absent experts of rank r with r %% den < num go to "
+                                                   "the CPU")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="end with a plain 256 MiB device copy (scale for rocprofv3 FETCH_SIZE/WRITE_SIZE)")
     ap.add_argument("--no-cpu", action="store_true")

@@ -153,6 +153,17 @@ size_t moe_experts_workspace_bytes(int I, int K);
 int moe_route(const moe_route_desc *d, void *stream);
 int moe_experts(const moe_experts_desc *d, void *stream);
 
+/* The same expert chain on the host CPU (the reference's CPU path for
+ * missed experts, P8:186-251 / experiments/x2_cpu_expert_cost.cpp:115-156):
+ * rows[k][H] = W_down,k . Q8_K(silu(W_gate,k . x) * (W_up,k . x)) for the n
+ * experts at host addresses experts[k] ([up][gate][down] bytes), given the
+ * Q8_K of x (host, [H/256][292]).  n_threads workers (the caller included);
+ * AVX-512 VNNI integer dots when the CPU has them, or the portable path
+ * (portable != 0 forces it).  Results equal the device kernels' bit for bit. */
+int moe_cpu_experts(const void *const *experts, int n, const uint8_t *q8x, int H, int I, int down_type, float *rows,
+                    int n_threads, int portable);
+int moe_cpu_has_vnni(void);
+
 /* ---- cache runtime --------------------------------------------------------- */
 typedef struct moe_cache moe_cache;
 
@@ -190,6 +201,8 @@ typedef struct {
     uint64_t bytes_uploaded;
     double publication_wait_us;                  /* time step() spent waiting for copies */
     uint64_t n_staged;                           /* uploads copied from the HBM staging area */
+    uint64_t n_cpu_served;                       /* absent experts computed on the host CPU */
+    double sidecar_wait_us, sidecar_cpu_us;      /* host time waiting for the GPU's posts / computing */
 } moe_cache_stats;
 
 typedef struct {
@@ -248,6 +261,20 @@ int moe_cache_set_decode_path(moe_cache *c, int split, int graph);
  * them in that token's step copies it device to device instead of over PCIe.
  * The bytes, slots, publication and traces are the same either way. */
 int moe_cache_set_staging(moe_cache *c, int on);
+/* CPU-assisted serving of absent experts (the reference's sidecar,
+ * patches/0009: MOE_POST P9:277-320, MOE_JOIN P9:322-359, sidecar_serve
+ * P9:841-912).  With n_threads > 0, moe_decode_token's router kernel posts
+ * each layer's ids and Q8_K(x) to mapped host memory; the calling thread and
+ * n_threads - 1 workers compute the absent experts whose rank r among the
+ * layer's absent experts (k order) has r % den < num, from the pinned store,
+ * while the GPU runs the others; a join kernel waits (at most 2 s, bounded
+ * by the GPU wall clock) for the host's rows and combines sum_k w_k y_k in k
+ * order.  Outputs, ids and cache traces are identical to the GPU-only path.
+ * Needs split 0.  n_threads <= 0 turns it off. */
+int moe_cache_set_sidecar(moe_cache *c, int n_threads, int num, int den);
+/* Per served layer since the last call: (host wait us, host compute us,
+ * experts computed), up to max_rows rows into out [rows][3]; returns rows. */
+int moe_cache_sidecar_log(moe_cache *c, float *out, int max_rows);
 int moe_cache_kernel_times(moe_cache *c, moe_kernel_times *out);
 
 /* One layer at batch 1: route x (+bias), run the K experts, out = sum_k w_k y_k.

@@ -1,0 +1,437 @@
+// mp_cpu.cpp -- the routed-expert chain on the host CPU.
+//
+// Integer dots with AVX-512 VNNI (vpdpbusd: unsigned weight codes x signed
+// Q8_K values, no saturation) when the CPU has it, a portable path otherwise;
+// both give identical results.  Per super-block the dot is an exact int32,
+// and the fp32 steps run in row order exactly as the CPU reference chain
+// (experiments/x2_cpu_expert_cost.cpp:115-156, ggml vec_dot_q4_K_q8_K /
+// vec_dot_q6_K_q8_K) and the device kernels take them: acc + (d*dx)*sumi,
+// then - (dmin*dx)*summ.  Built with -ffp-contract=off.
+#include "mp_cpu.h"
+
+#include <immintrin.h>
+#include <math.h>
+#include <string.h>
+#include <sys/mman.h>
+#include <unistd.h>
+
+#include <algorithm>
+#include <atomic>
+#include <condition_variable>
+#include <mutex>
+#include <thread>
+#include <vector>
+
+#include "mp_format.h"
+
+namespace mpc {
+
+using mp::QK;
+using mp::Q4K_BYTES;
+using mp::Q6K_BYTES;
+using mp::Q8K_BYTES;
+
+static bool g_portable = false;     // set by the tests to pin the portable path
+
+bool has_vnni() {
+    static const bool v = __builtin_cpu_supports("avx512f") && __builtin_cpu_supports("avx512bw") &&
+                          __builtin_cpu_supports("avx512vl") && __builtin_cpu_supports("avx512vnni");
+    return v;
+}
+
+void set_portable(bool on) { g_portable = on; }
+
+// canonical exp: Cody-Waite reduction by ln 2 in two parts, degree-7
+// polynomial by Horner with fused multiply-adds, scale by 2^n (the device's
+// canon_expf, step for step)
+static inline float canon_expf(float x) {
+    if (x < -87.0f) return 0.0f;
+    if (x > 88.0f) x = 88.0f;
+    const float n = rintf(x * 1.44269504088896341f);
+    float r = fmaf(n, -0.693145751953125f, x);
+    r = fmaf(n, -1.428606765330187045e-06f, r);
+    float p = 1.9841269841269841e-04f;
+    p = fmaf(p, r, 1.3888888888888889e-03f);
+    p = fmaf(p, r, 8.3333333333333333e-03f);
+    p = fmaf(p, r, 4.1666666666666667e-02f);
+    p = fmaf(p, r, 1.6666666666666667e-01f);
+    p = fmaf(p, r, 0.5f);
+    p = fmaf(p, r, 1.0f);
+    p = fmaf(p, r, 1.0f);
+    const uint32_t e = (uint32_t)((int32_t)n + 127);
+    return p * mp::bits_f32(e << 23);
+}
+
+void quant_q8k(const float *x, int n, uint8_t *out) {
+    for (int b = 0; b < n / QK; ++b) {
+        const float *v = x + (size_t)b * QK;
+        uint8_t *o = out + (size_t)b * Q8K_BYTES;
+        float amax = 0.0f, mx = 0.0f;
+        for (int i = 0; i < QK; ++i) {
+            const float a = fabsf(v[i]);
+            if (a > amax) { amax = a; mx = v[i]; }     // first index of the largest magnitude
+        }
+        int8_t q[QK];
+        float d = 0.0f;
+        if (amax != 0.0f) {
+            const float iscale = -127.0f / mx;
+            for (int i = 0; i < QK; ++i) {
+                const int t = (int)rintf(iscale * v[i]);
+                q[i] = (int8_t)(t < 127 ? t : 127);
+            }
+            d = 1.0f / iscale;
+        } else {
+            memset(q, 0, sizeof q);
+        }
+        memcpy(o, &d, 4);
+        memcpy(o + 4, q, QK);
+        for (int g = 0; g < 16; ++g) {
+            int s = 0;
+            for (int i = 0; i < 16; ++i) s += q[16 * g + i];
+            const int16_t s16 = (int16_t)s;
+            memcpy(o + 4 + QK + 2 * g, &s16, 2);
+        }
+    }
+}
+
+static inline void q4k_scale_min(const uint8_t *s, int j, int &sc, int &m) {
+    if (j < 4) {
+        sc = s[j] & 63;
+        m = s[j + 4] & 63;
+    } else {
+        sc = (s[j + 4] & 0xF) | ((s[j - 4] >> 6) << 4);
+        m = (s[j + 4] >> 4) | ((s[j] >> 6) << 4);
+    }
+}
+
+static inline float f32_at(const uint8_t *p) { float f; memcpy(&f, p, 4); return f; }
+static inline uint16_t u16_at(const uint8_t *p) { uint16_t v; memcpy(&v, p, 2); return v; }
+static inline int16_t i16_at(const uint8_t *p) { int16_t v; memcpy(&v, p, 2); return v; }
+
+// ---- portable dots -----------------------------------------------------------
+static float dot_q4k_port(const uint8_t *row, const uint8_t *q8, int nb) {
+    float acc = 0.0f;
+    for (int i = 0; i < nb; ++i, row += Q4K_BYTES, q8 += Q8K_BYTES) {
+        const int8_t *qx = (const int8_t *)(q8 + 4);
+        int32_t sumi = 0, summ = 0;
+        for (int j = 0; j < 8; ++j) {
+            int sc, m;
+            q4k_scale_min(row + 4, j, sc, m);
+            const uint8_t *qs = row + 16 + 32 * (j >> 1);
+            const int sh = 4 * (j & 1);
+            int32_t dot = 0;
+            for (int l = 0; l < 32; ++l) dot += ((qs[l] >> sh) & 0xF) * qx[32 * j + l];
+            sumi += sc * dot;
+            summ += m * (i16_at(q8 + 4 + QK + 4 * j) + i16_at(q8 + 4 + QK + 4 * j + 2));
+        }
+        const float dx = f32_at(q8);
+        const float d = mp::h2f(u16_at(row)) * dx, dm = mp::h2f(u16_at(row + 2)) * dx;
+        acc = acc + d * (float)sumi;
+        acc = acc - dm * (float)summ;
+    }
+    return acc;
+}
+
+static float dot_q6k_port(const uint8_t *row, const uint8_t *q8, int nb) {
+    float acc = 0.0f;
+    for (int i = 0; i < nb; ++i, row += Q6K_BYTES, q8 += Q8K_BYTES) {
+        const uint8_t *ql = row, *qh = row + 128;
+        const int8_t *sc = (const int8_t *)(row + 192);
+        const int8_t *qx = (const int8_t *)(q8 + 4);
+        int32_t sumi = 0;
+        for (int h = 0; h < 2; ++h)
+            for (int g = 0; g < 4; ++g)
+                for (int s = 0; s < 2; ++s) {
+                    int32_t dq = 0;
+                    for (int l = 16 * s; l < 16 * s + 16; ++l) {
+                        const uint8_t lo = ql[64 * h + 32 * (g & 1) + l];
+                        const int low = g >= 2 ? (lo >> 4) : (lo & 0xF);
+                        const int high = (qh[32 * h + l] >> (2 * g)) & 3;
+                        dq += ((low | (high << 4)) - 32) * qx[128 * h + 32 * g + l];
+                    }
+                    sumi += sc[8 * h + 2 * g + s] * dq;
+                }
+        const float d = mp::h2f(u16_at(row + 208)) * f32_at(q8);
+        acc = acc + d * (float)sumi;
+    }
+    return acc;
+}
+
+// ---- AVX-512 VNNI dots ---------------------------------------------------------
+#define MPC_VNNI __attribute__((target("avx512f,avx512bw,avx512vl,avx512vnni")))
+
+// Q4_K: 32 code bytes of a 64-value group -> [low nibbles | high nibbles] =
+// sub-blocks 2g and 2g+1, against the group's 64 Q8_K values: dpbusd lanes
+// 0-7 hold sub-block 2g, lanes 8-15 sub-block 2g+1; times the six-bit scales.
+MPC_VNNI static float dot_q4k_vnni(const uint8_t *row, const uint8_t *q8, int nb) {
+    float acc = 0.0f;
+    const __m256i m4 = _mm256_set1_epi8(0x0F);
+    for (int i = 0; i < nb; ++i, row += Q4K_BYTES, q8 += Q8K_BYTES) {
+        int sc[8], mn[8];
+        for (int j = 0; j < 8; ++j) q4k_scale_min(row + 4, j, sc[j], mn[j]);
+        __m512i a = _mm512_setzero_si512();
+        for (int g = 0; g < 4; ++g) {
+            const __m256i raw = _mm256_loadu_si256((const __m256i *)(row + 16 + 32 * g));
+            const __m256i lo = _mm256_and_si256(raw, m4);
+            const __m256i hi = _mm256_and_si256(_mm256_srli_epi16(raw, 4), m4);
+            const __m512i wv = _mm512_inserti64x4(_mm512_castsi256_si512(lo), hi, 1);
+            const __m512i xv = _mm512_loadu_si512((const void *)(q8 + 4 + 64 * g));
+            const __m512i p = _mm512_dpbusd_epi32(_mm512_setzero_si512(), wv, xv);
+            const __m512i s = _mm512_inserti64x4(_mm512_castsi256_si512(_mm256_set1_epi32(sc[2 * g])),
+                                                 _mm256_set1_epi32(sc[2 * g + 1]), 1);
+            a = _mm512_add_epi32(a, _mm512_mullo_epi32(p, s));
+        }
+        const int32_t sumi = _mm512_reduce_add_epi32(a);
+        int32_t summ = 0;
+        for (int j = 0; j < 8; ++j) summ += mn[j] * (i16_at(q8 + 4 + QK + 4 * j) + i16_at(q8 + 4 + QK + 4 * j + 2));
+        const float dx = f32_at(q8);
+        const float d = mp::h2f(u16_at(row)) * dx, dm = mp::h2f(u16_at(row + 2)) * dx;
+        acc = acc + d * (float)sumi;
+        acc = acc - dm * (float)summ;
+    }
+    return acc;
+}
+
+// Q6_K: per 128-value half, the six-bit codes of quarters (0,1) and (2,3)
+// as two 64-byte vectors against the matching Q8_K values; 16-value groups
+// are 4 dpbusd lanes each, so lane group i carries scale i.  The -32 offset
+// is taken as 32 * (sum of the group's Q8_K values), from a dpbusd by ones.
+MPC_VNNI static float dot_q6k_vnni(const uint8_t *row, const uint8_t *q8, int nb) {
+    float acc = 0.0f;
+    const __m256i m4 = _mm256_set1_epi8(0x0F), m30 = _mm256_set1_epi8(0x30);
+    const __m512i ones = _mm512_set1_epi8(1);
+    for (int i = 0; i < nb; ++i, row += Q6K_BYTES, q8 += Q8K_BYTES) {
+        const __m128i sc16 = _mm_loadu_si128((const __m128i *)(row + 192));
+        __m512i a = _mm512_setzero_si512();
+        for (int h = 0; h < 2; ++h) {
+            const __m256i ql0 = _mm256_loadu_si256((const __m256i *)(row + 64 * h));
+            const __m256i ql1 = _mm256_loadu_si256((const __m256i *)(row + 64 * h + 32));
+            const __m256i qh = _mm256_loadu_si256((const __m256i *)(row + 128 + 32 * h));
+            const __m256i q0 = _mm256_or_si256(_mm256_and_si256(ql0, m4), _mm256_and_si256(_mm256_slli_epi16(qh, 4), m30));
+            const __m256i q1 = _mm256_or_si256(_mm256_and_si256(ql1, m4), _mm256_and_si256(_mm256_slli_epi16(qh, 2), m30));
+            const __m256i q2 = _mm256_or_si256(_mm256_and_si256(_mm256_srli_epi16(ql0, 4), m4), _mm256_and_si256(qh, m30));
+            const __m256i q3 = _mm256_or_si256(_mm256_and_si256(_mm256_srli_epi16(ql1, 4), m4),
+                                               _mm256_and_si256(_mm256_srli_epi16(qh, 2), m30));
+            for (int p = 0; p < 2; ++p) {
+                const __m512i wv = p == 0 ? _mm512_inserti64x4(_mm512_castsi256_si512(q0), q1, 1)
+                                          : _mm512_inserti64x4(_mm512_castsi256_si512(q2), q3, 1);
+                const __m512i xv = _mm512_loadu_si512((const void *)(q8 + 4 + 128 * h + 64 * p));
+                const __m512i dq = _mm512_dpbusd_epi32(_mm512_setzero_si512(), wv, xv);
+                const __m512i sx = _mm512_dpbusd_epi32(_mm512_setzero_si512(), ones, xv);
+                const __m512i t = _mm512_sub_epi32(dq, _mm512_slli_epi32(sx, 5));
+                // scales 8h+4p .. 8h+4p+3, each on 4 lanes
+                const int b0 = 8 * h + 4 * p;
+                const __m128i idx = _mm_setr_epi8(b0, b0, b0, b0, b0 + 1, b0 + 1, b0 + 1, b0 + 1, b0 + 2, b0 + 2, b0 + 2,
+                                                  b0 + 2, b0 + 3, b0 + 3, b0 + 3, b0 + 3);
+                const __m512i s = _mm512_cvtepi8_epi32(_mm_shuffle_epi8(sc16, idx));
+                a = _mm512_add_epi32(a, _mm512_mullo_epi32(t, s));
+            }
+        }
+        const int32_t sumi = _mm512_reduce_add_epi32(a);
+        const float d = mp::h2f(u16_at(row + 208)) * f32_at(q8);
+        acc = acc + d * (float)sumi;
+    }
+    return acc;
+}
+
+float dot_q4k(const uint8_t *row, const uint8_t *q8, int nb) {
+    return (!g_portable && has_vnni()) ? dot_q4k_vnni(row, q8, nb) : dot_q4k_port(row, q8, nb);
+}
+
+float dot_q6k(const uint8_t *row, const uint8_t *q8, int nb) {
+    return (!g_portable && has_vnni()) ? dot_q6k_vnni(row, q8, nb) : dot_q6k_port(row, q8, nb);
+}
+
+// ---- team --------------------------------------------------------------------
+// Work is claimed item by item with a compare-and-swap on one word packing
+// (generation, next item), so a worker that wakes late can never take an item
+// of a newer job with an older job's function; the caller waits for the
+// items to be done, not for every worker to check in (a worker the OS has
+// descheduled holds nothing up unless it claimed an item).  Idle workers spin
+// while the team is hot and for a grace period after, then sleep.
+class Team {
+  public:
+    explicit Team(int n) {
+        for (int i = 1; i < n; ++i) th_.emplace_back([this] { work(); });
+    }
+    ~Team() {
+        {
+            std::lock_guard<std::mutex> lk(mu_);
+            quit_.store(true);
+        }
+        cv_.notify_all();
+        for (auto &t : th_) t.join();
+    }
+    int size() const { return (int)th_.size() + 1; }
+    void hot(bool on) {
+        {
+            std::lock_guard<std::mutex> lk(mu_);
+            hot_.store(on);
+        }
+        if (on) cv_.notify_all();
+    }
+    // fn(ctx, item) for item in [0, n), spread over the team and the caller
+    void run(int n, void (*fn)(void *, int), void *ctx) {
+        if (n <= 0) return;
+        const uint64_t g = ++gen_;
+        Slot &sl = slot_[g & 1];
+        sl.fn.store(fn, std::memory_order_relaxed);
+        sl.ctx.store(ctx, std::memory_order_relaxed);
+        sl.n.store(n, std::memory_order_relaxed);
+        done_.store(0, std::memory_order_relaxed);
+        {
+            std::lock_guard<std::mutex> lk(mu_);
+            state_.store(g << 32, std::memory_order_release);
+        }
+        if (!hot_.load(std::memory_order_relaxed)) cv_.notify_all();
+        claim(g);
+        while (done_.load(std::memory_order_acquire) < n) _mm_pause();
+    }
+
+  private:
+    struct Slot {
+        std::atomic<void (*)(void *, int)> fn{nullptr};
+        std::atomic<void *> ctx{nullptr};
+        std::atomic<int> n{0};
+    };
+    // take items of generation g until none is left or a newer job started
+    void claim(uint64_t g) {
+        const Slot &sl = slot_[g & 1];
+        void (*fn)(void *, int) = sl.fn.load(std::memory_order_relaxed);
+        void *ctx = sl.ctx.load(std::memory_order_relaxed);
+        const uint32_t n = (uint32_t)sl.n.load(std::memory_order_relaxed);
+        uint64_t st = state_.load(std::memory_order_acquire);
+        for (;;) {
+            if ((st >> 32) != g || (uint32_t)st >= n) return;
+            if (state_.compare_exchange_weak(st, st + 1, std::memory_order_acq_rel, std::memory_order_acquire)) {
+                fn(ctx, (int)(uint32_t)st);
+                done_.fetch_add(1, std::memory_order_release);
+                st = state_.load(std::memory_order_acquire);
+            }
+        }
+    }
+    void work() {
+        uint64_t seen = 0;
+        for (;;) {
+            uint64_t g;
+            int idle = 0;
+            while ((g = state_.load(std::memory_order_acquire) >> 32) == seen) {
+                if (quit_.load(std::memory_order_relaxed)) return;
+                if (hot_.load(std::memory_order_relaxed) || ++idle < kGraceSpins) {
+                    _mm_pause();
+                    continue;
+                }
+                std::unique_lock<std::mutex> lk(mu_);
+                cv_.wait(lk, [&] { return (state_.load() >> 32) != seen || quit_.load() || hot_.load(); });
+                idle = 0;
+            }
+            seen = g;
+            claim(g);
+        }
+    }
+    static constexpr int kGraceSpins = 1 << 16;     // ~1-2 ms of pause instructions
+    std::vector<std::thread> th_;
+    std::mutex mu_;
+    std::condition_variable cv_;
+    uint64_t gen_ = 0;                               // the caller's job count
+    alignas(64) std::atomic<uint64_t> state_{0};    // (generation << 32) | next item
+    alignas(64) std::atomic<int> done_{0};
+    alignas(64) Slot slot_[2];
+    std::atomic<bool> quit_{false}, hot_{false};
+};
+
+namespace {
+struct Touch {
+    const volatile uint8_t *base;
+    size_t n, page, per;
+    std::atomic<unsigned> sink{0};
+};
+void touch_item(void *p, int item) {
+    Touch &t = *(Touch *)p;
+    unsigned s = 0;
+    const size_t b = (size_t)item * t.per, e = std::min(t.n, b + t.per);
+    for (size_t o = b; o < e; o += t.page) s += t.base[o];
+    t.sink.fetch_add(s, std::memory_order_relaxed);
+}
+}  // namespace
+
+#ifndef MADV_POPULATE_READ
+#define MADV_POPULATE_READ 22
+#endif
+
+void prefault(Team *t, const void *p, size_t n) {
+    if (!p || !n) return;
+    const size_t page = (size_t)sysconf(_SC_PAGESIZE);
+    const uintptr_t a = (uintptr_t)p / page * page;
+    const size_t len = ((uintptr_t)p + n - a + page - 1) / page * page;
+    if (madvise((void *)a, len, MADV_POPULATE_READ) == 0) return;
+    Touch tc;                       // kernel without MADV_POPULATE_READ: read one byte per page
+    tc.base = (const volatile uint8_t *)p;
+    tc.n = n;
+    tc.page = page;
+    tc.per = 64 * page * 64;
+    t->run((int)((n + tc.per - 1) / tc.per), touch_item, &tc);
+}
+
+Team *team_create(int n_threads) { return new Team(std::max(1, n_threads)); }
+void team_destroy(Team *t) { delete t; }
+int team_size(const Team *t) { return t->size(); }
+void team_hot(Team *t, bool on) { t->hot(on); }
+
+// ---- the chain -----------------------------------------------------------------
+namespace {
+constexpr int UP_ROWS = 16;     // up/gate rows per work item
+constexpr int DN_ROWS = 32;     // down rows per work item
+
+struct Chain {
+    const CpuExpert *e;
+    int n, H, I, down_type;
+    float *h;
+    uint8_t *q8h;
+    std::atomic<int> left[16];   // up/gate items of expert k not finished yet
+};
+
+// rows of up and gate; the item that finishes an expert's h quantizes it
+void up_item(void *p, int item) {
+    Chain &c = *(Chain *)p;
+    const int per = c.I / UP_ROWS;
+    const int k = item / per, r0 = (item % per) * UP_ROWS;
+    const size_t rb = (size_t)(c.H / QK) * Q4K_BYTES;
+    const uint8_t *up = c.e[k].w, *gate = c.e[k].w + (size_t)c.I * rb;
+    float *h = c.h + (size_t)k * c.I;
+    for (int r = r0; r < r0 + UP_ROWS; ++r) {
+        const float u = dot_q4k(up + r * rb, c.e[k].q8x, c.H / QK);
+        const float g = dot_q4k(gate + r * rb, c.e[k].q8x, c.H / QK);
+        h[r] = g / (1.0f + canon_expf(-g)) * u;
+    }
+    if (c.left[k].fetch_sub(1, std::memory_order_acq_rel) == 1)
+        quant_q8k(h, c.I, c.q8h + (size_t)k * (c.I / QK) * Q8K_BYTES);
+}
+
+void down_item(void *p, int item) {
+    const Chain &c = *(const Chain *)p;
+    const int k = item % c.n, r0 = (item / c.n) * DN_ROWS;       // experts interleaved: even load
+    const size_t rb_in = (size_t)(c.H / QK) * Q4K_BYTES;
+    const size_t rb = (size_t)(c.I / QK) * (c.down_type == mp::TYPE_Q6K ? Q6K_BYTES : Q4K_BYTES);
+    const uint8_t *down = c.e[k].w + 2 * (size_t)c.I * rb_in;
+    const uint8_t *q = c.q8h + (size_t)k * (c.I / QK) * Q8K_BYTES;
+    float *y = c.e[k].y;
+    for (int r = r0; r < r0 + DN_ROWS; ++r)
+        y[r] = c.down_type == mp::TYPE_Q6K ? dot_q6k(down + r * rb, q, c.I / QK) : dot_q4k(down + r * rb, q, c.I / QK);
+}
+}  // namespace
+
+void experts(Team *t, const CpuExpert *e, int n, int H, int I, int down_type, float *h_scratch,
+             uint8_t *q8h_scratch) {
+    for (int b = 0; b < n; b += 16) {         // at most 16 experts per pass
+        Chain c;
+        c.e = e + b; c.n = std::min(16, n - b); c.H = H; c.I = I; c.down_type = down_type;
+        c.h = h_scratch + (size_t)b * I;
+        c.q8h = q8h_scratch + (size_t)b * (I / QK) * Q8K_BYTES;
+        for (int k = 0; k < c.n; ++k) c.left[k].store(I / UP_ROWS, std::memory_order_relaxed);
+        t->run(c.n * (I / UP_ROWS), up_item, &c);
+        t->run(c.n * (H / DN_ROWS), down_item, &c);
+    }
+}
+
+}  // namespace mpc

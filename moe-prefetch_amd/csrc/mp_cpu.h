@@ -1,0 +1,49 @@
+// mp_cpu.h -- the routed-expert chain on the host CPU (internal interface).
+//
+// Used to serve experts that are absent from the HBM slots from the pinned
+// store by the CPU instead of streaming their bytes over PCIe.  Arithmetic is
+// the device kernels' and the CPU reference chain's: Q8_K activations, exact
+// integer dots, fp32 per super-block in row order (scale term, then min term),
+// SiLU with the canonical exp, Q8_K of h, then the down rows.
+#pragma once
+
+#include <stddef.h>
+#include <stdint.h>
+
+namespace mpc {
+
+// One expert of a batch of host work: its bytes ([up][gate][down], host
+// memory), the Q8_K of its input ([H/256][292]) and its output rows [H].
+struct CpuExpert {
+    const uint8_t *w;
+    const uint8_t *q8x;
+    float *y;
+};
+
+// A persistent team of worker threads.  Between `hot(true)` and `hot(false)`
+// idle workers poll for work (microsecond hand-off); otherwise they sleep.
+class Team;
+Team *team_create(int n_threads);     // n_threads includes the caller
+void team_destroy(Team *t);
+int team_size(const Team *t);
+void team_hot(Team *t, bool on);
+
+// y_k = W_down,k . Q8_K(silu(W_gate,k . x) * (W_up,k . x)) for every expert,
+// rows split over the team (the caller works too).  h_scratch holds n * I
+// floats and q8h_scratch n * (I/256) * 292 bytes.
+void experts(Team *t, const CpuExpert *e, int n, int H, int I, int down_type, float *h_scratch,
+             uint8_t *q8h_scratch);
+
+// Map every page of [p, p + n) into this process's page tables for reading
+// (memory another device filled has never been touched by the CPU: its first
+// reads would fault page by page, ~1 ms per expert, in the middle of a decode)
+void prefault(Team *t, const void *p, size_t n);
+
+// building blocks (exposed for the tests of this file's arithmetic)
+void quant_q8k(const float *x, int n, uint8_t *out);
+float dot_q4k(const uint8_t *row, const uint8_t *q8, int nb);
+float dot_q6k(const uint8_t *row, const uint8_t *q8, int nb);
+bool has_vnni();
+void set_portable(bool on);     // force the portable dots (tests)
+
+}  // namespace mpc

@@ -7,6 +7,26 @@
 
 namespace mp {
 
+// CPU-assisted serving of absent experts: per-layer exchange blocks in
+// mapped, fine-grained host memory.  The GPU posts the routed ids and the Q8_K
+// of x and then the token's sequence number (system-scope release); the host
+// computes the experts assigned to it, writes their rows and answers with
+// the sequence number (or SC_ABORT).
+constexpr int SC_Q8X_BYTES = 8 * 292;          // Q8_K of x at H = 2048
+struct alignas(256) SidecarPost {
+    uint32_t seq;
+    uint32_t pad0[31];
+    int32_t ids[16];
+    uint8_t q8x[SC_Q8X_BYTES];
+};
+struct alignas(128) SidecarResp {
+    uint32_t seq;                              // host -> GPU
+    uint32_t pad0[15];
+    uint32_t err;                              // GPU -> host: the join gave up waiting
+    uint32_t pad1[15];
+};
+constexpr uint32_t SC_ABORT = 0xffffffffu;
+
 struct RouteLaunch {
     const float *W;        // [E][H] f32
     const float *x;        // [n_tok][H] f32
@@ -24,6 +44,8 @@ struct RouteLaunch {
     int32_t *slots;        // out [n_tok][K]
     float *probs;          // out [n_tok][E] or null
     uint8_t *q8x;          // out [n_tok][H/256][292]
+    SidecarPost *post;     // batch-1 decode with CPU-assisted serving: post ids + Q8_K(x), or null
+    const uint32_t *seq;   // device: the token's sequence number
 };
 
 struct ExpertArgs {
@@ -54,6 +76,26 @@ struct ExpertArgs {
     const uint8_t *shared;    // always-on shared expert in HBM (weight 1, combined after the K routed
                               // ones) or null; it is expert K of the launch
     int n_shared;             // 1 with a shared expert
+    int cpu_num, cpu_den;     // CPU-assisted serving (den > 0): the CPU computes absent expert k when
+                              // its rank among the absent ones (k order) r has r % den < num
+};
+
+// batch-1 combine after CPU-assisted serving: waits (bounded) for the host's
+// answer, then out = sum_k w_k y_k in k order (rows from the host or from
+// ypart) + the shared expert's row
+struct JoinArgs {
+    const int32_t *ids, *slots;
+    const float *w;
+    const uint8_t *slot_pool;
+    int n_slots;
+    const uint8_t *host_store;
+    int n_experts, K, H, n_shared, cpu_num, cpu_den;
+    const float *ypart;       // dev [K + n_shared][H]
+    const float *hrows;       // mapped host [K][H]
+    SidecarResp *resp;        // mapped host
+    const uint32_t *seq;      // dev
+    uint64_t timeout_ticks;   // of the 100 MHz wall clock
+    float *out;               // dev [H]
 };
 
 constexpr int MAX_E = 256;   // experts per layer the kernels support
@@ -96,6 +138,7 @@ hipError_t launch_swiglu_quant(const float *y2, int P, int I, float *h_out, uint
 // ev (optional): [logits start, logits end, select start, select end]
 hipError_t launch_route(const RouteLaunch &l, hipStream_t st, hipEvent_t *ev = nullptr);
 hipError_t launch_experts(const ExpertArgs &a, hipStream_t st);
+hipError_t launch_join(const JoinArgs &a, hipStream_t st);
 // src: 0 every routed expert, 1 only those resident in HBM slots, 2 only
 // those read from the pinned host store.  A src = 2 down launch accumulates
 // into out when the caller sets accumulate.

@@ -63,6 +63,8 @@ struct RouteArgs {
     int32_t *slots;        // [n_tok][K]
     float *probs;          // [n_tok][E] or null
     uint8_t *q8x;          // [n_tok][H/256 * 292]
+    SidecarPost *post;     // batch 1 with CPU-assisted serving, or null
+    const uint32_t *seq;
 };
 
 // One wavefront per expert row: logit[e] = <W[e], x> in the canonical order
@@ -167,6 +169,19 @@ __global__ __launch_bounds__(256) void route_select_kernel(RouteArgs a) {
             a.slots[(size_t)tok * a.K + lane] = a.table ? a.table[id] : a.dummy;
         }
     }
+    // CPU-assisted serving: post the ids and the Q8_K of x (written by the
+    // router GEMV kernel) to the host, then the sequence number.  One wave:
+    // its release store waits for all of the wave's earlier stores.  (Only
+    // on the router-GEMV path, where x's Q8_K is complete before this kernel.)
+    if (a.post && !a.logits_in) {
+        if (wave == 0) {
+            if (lane < a.K) a.post->ids[lane] = s_ids[lane];
+            const uint4 *src = (const uint4 *)a.q8x;
+            uint4 *dst = (uint4 *)a.post->q8x;
+            for (int i = lane; i < (a.H / QK) * Q8K_BYTES / 16; i += 64) dst[i] = src[i];
+            if (lane == 0) __hip_atomic_store(&a.post->seq, *a.seq, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
+        }
+    }
     if (!a.logits_in || !a.x || !a.q8x) return;
     const float *x = a.x + (size_t)tok * a.H;
     uint8_t *q8 = a.q8x + (size_t)tok * (a.H / QK) * Q8K_BYTES;
@@ -178,7 +193,31 @@ __global__ __launch_bounds__(256) void route_select_kernel(RouteArgs a) {
 // slot, or only those read from the pinned host store
 constexpr int SRC_ALL = 0, SRC_HBM = 1, SRC_HOST = 2;
 
+// routed expert k is absent from the slots and inside the store
+__device__ inline bool absent_in_store(const int32_t *slots, const int32_t *ids, const uint8_t *slot_pool,
+                                       int n_slots, const uint8_t *host_store, int n_experts, int k) {
+    const int slot = slots[k], id = ids[k];
+    return !(slot_pool && slot >= 0 && slot < n_slots) && host_store && id >= 0 && id < n_experts;
+}
+
+// CPU-assisted serving: the host computes absent expert k when its rank r
+// among the absent experts (in k order) has r % den < num
+__device__ inline bool cpu_served(const int32_t *slots, const int32_t *ids, const uint8_t *slot_pool, int n_slots,
+                                  const uint8_t *host_store, int n_experts, int num, int den, int K, int k) {
+    if (den <= 0 || k >= K) return false;
+    if (!absent_in_store(slots, ids, slot_pool, n_slots, host_store, n_experts, k)) return false;
+    int r = 0;
+    for (int j = 0; j < k; ++j) r += absent_in_store(slots, ids, slot_pool, n_slots, host_store, n_experts, j);
+    return r % den < num;
+}
+
+__device__ inline bool cpu_served(const ExpertArgs &a, int k) {
+    return cpu_served(a.slots, a.ids, a.slot_pool, a.n_slots, a.host_store, a.n_experts, a.cpu_num, a.cpu_den, a.K,
+                      k);
+}
+
 __device__ inline bool serves(const ExpertArgs &a, int k, int src) {
+    if (cpu_served(a, k)) return false;
     if (src == SRC_ALL) return true;
     if (k >= a.K) return src == SRC_HBM;     // the shared expert lives in HBM
     const int slot = a.slots[k];
@@ -200,7 +239,7 @@ __device__ inline const uint8_t *expert_base(const ExpertArgs &a, int k) {
 // where the bytes of routed expert k go when the launch reads it from the
 // pinned store: its staging area (null when not staging or not absent)
 __device__ inline uint8_t *stage_base(const ExpertArgs &a, int k) {
-    if (!a.stage || k >= a.K) return nullptr;
+    if (!a.stage || k >= a.K || cpu_served(a, k)) return nullptr;
     const int slot = a.slots[k];
     if (a.slot_pool && slot >= 0 && slot < a.n_slots) return nullptr;
     const int id = a.ids[k];
@@ -488,6 +527,7 @@ hipError_t launch_route(const RouteLaunch &l, hipStream_t st, hipEvent_t *ev) {
     a.E = l.E; a.H = l.H; a.K = l.K;
     a.logits = l.logits; a.counter = l.counter; a.ids = l.ids; a.w = l.w; a.slots = l.slots;
     a.probs = l.probs; a.q8x = l.q8x; a.logits_in = l.logits_in;
+    a.post = l.post; a.seq = l.seq;
     if (l.logits_in)
         return launch(route_select_kernel, dim3((unsigned)l.n_tok), dim3(256), st, ev ? ev[2] : nullptr,
                       ev ? ev[3] : nullptr, a);
@@ -520,6 +560,55 @@ hipError_t launch_gateup(const ExpertArgs &a, int src, hipStream_t st, hipEvent_
 hipError_t launch_down(const ExpertArgs &a, int src, hipStream_t st, hipEvent_t e0, hipEvent_t e1) {
     return src == SRC_HBM ? down_src<SRC_HBM>(a, st, e0, e1) : src == SRC_HOST ? down_src<SRC_HOST>(a, st, e0, e1)
                                                                                  : down_src<SRC_ALL>(a, st, e0, e1);
+}
+
+// ---------------------------------------------------------------------------
+// join after CPU-assisted serving.  One thread per workgroup waits for the
+// host's answer: bounded by the 100 MHz wall clock, and ended early by
+// SC_ABORT; a timeout is reported through resp->err and the rows are zero.
+__global__ __launch_bounds__(256) void join_kernel(JoinArgs a) {
+    __shared__ int s_ok;
+    __shared__ int s_cpu[16];
+    if (threadIdx.x == 0) {
+        const uint32_t want = *a.seq;
+        const uint64_t t0 = wall_clock64();
+        int ok = 0;
+        for (;;) {
+            const uint32_t v = __hip_atomic_load(&a.resp->seq, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_SYSTEM);
+            if (v == want) { ok = 1; break; }
+            if (v == SC_ABORT) break;
+            if (wall_clock64() - t0 > a.timeout_ticks) {
+                if (blockIdx.x == 0) __hip_atomic_store(&a.resp->err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+                break;
+            }
+            __builtin_amdgcn_s_sleep(4);
+        }
+        s_ok = ok;
+    }
+    if (threadIdx.x < 16)
+        s_cpu[threadIdx.x] = cpu_served(a.slots, a.ids, a.slot_pool, a.n_slots, a.host_store, a.n_experts, a.cpu_num,
+                                        a.cpu_den, a.K, (int)threadIdx.x);
+    __syncthreads();
+    const int r = blockIdx.x * 256 + threadIdx.x;
+    if (r >= a.H) return;
+    if (!s_ok) {
+        a.out[r] = 0.0f;
+        return;
+    }
+    float acc = 0.0f;
+    for (int k = 0; k < a.K; ++k) {
+        const float y = s_cpu[k] ? __hip_atomic_load(&a.hrows[(size_t)k * a.H + r], __ATOMIC_RELAXED,
+                                                     __HIP_MEMORY_SCOPE_SYSTEM)
+                                 : a.ypart[(size_t)k * a.H + r];
+        acc = k == 0 ? a.w[0] * y : acc + a.w[k] * y;
+    }
+    if (a.n_shared) acc = acc + a.ypart[(size_t)a.K * a.H + r];   // weight 1, after the routed experts
+    a.out[r] = acc;
+}
+
+hipError_t launch_join(const JoinArgs &a, hipStream_t st) {
+    hipLaunchKernelGGL(join_kernel, dim3((unsigned)((a.H + 255) / 256)), dim3(256), 0, st, a);
+    return hipGetLastError();
 }
 
 hipError_t launch_experts(const ExpertArgs &a, hipStream_t st) {

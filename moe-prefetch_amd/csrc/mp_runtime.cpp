@@ -17,8 +17,10 @@
 // ([up|gate|down] in the store and in the slot) on a dedicated stream,
 // completion by hipEvent, tables in one pinned mirror flushed with one copy.
 #include <hip/hip_runtime.h>
+#include <immintrin.h>
 
 #include <algorithm>
+#include <atomic>
 #include <chrono>
 #include <cstdarg>
 #include <cstdio>
@@ -29,6 +31,7 @@
 #include <vector>
 
 #include "../../include/moe_prefetch.h"
+#include "mp_cpu.h"
 #include "mp_format.h"
 #include "mp_internal.h"
 #include "mp_synth.h"
@@ -114,6 +117,24 @@ struct moe_cache {
     hipStream_t stg_stream = nullptr;
     hipEvent_t ev_stg = nullptr;
     uint64_t n_staged = 0;
+    // CPU-assisted serving of absent experts (off while sc_den == 0): the
+    // decode kernels post each layer's ids and Q8_K(x) to sc_post; the host
+    // team computes the absent experts assigned to it into sc_rows and
+    // answers in sc_resp; the join kernel combines.  Host addresses here,
+    // device views in the *_d pointers.
+    int sc_num = 0, sc_den = 0;
+    mpc::Team *team = nullptr;
+    mp::SidecarPost *sc_post = nullptr, *sc_post_d = nullptr;     // [L]
+    mp::SidecarResp *sc_resp = nullptr, *sc_resp_d = nullptr;     // [L]
+    float *sc_rows = nullptr, *sc_rows_d = nullptr;               // [L][K][H]
+    uint32_t *d_seq = nullptr, *h_seq = nullptr;
+    uint32_t sc_seq = 0;
+    double sc_timeout_s = 2.0;
+    std::vector<float> sc_h, sc_y;         // host scratch: h, and the rows before they are published
+    std::vector<uint8_t> sc_q8h, sc_q8x;
+    uint64_t n_cpu_served = 0;
+    double sc_wait_us = 0.0, sc_cpu_us = 0.0;   // host time waiting for posts / computing experts
+    std::vector<float> sc_log;                  // per served layer: wait us, cpu us, experts (last 64K)
     uint64_t clock = 0, n_steps = 0, n_uploads = 0, n_scheduled = 0, n_copied = 0, n_published = 0;
     uint64_t n_admit_ok = 0, n_admit_denied = 0, n_table_flushes = 0, bytes_uploaded = 0;
     double wait_us = 0.0;
@@ -472,7 +493,8 @@ size_t exp_ws_bytes(int I, int K) {
     return align_up(k1 * I * 4, 256) + align_up(k1 * (I / 256) * mp::Q8K_BYTES, 256) + align_up(k1 * 4, 256);
 }
 
-int run_route(const moe_route_desc *d, hipStream_t st, hipEvent_t *ev = nullptr) {
+int run_route(const moe_route_desc *d, hipStream_t st, hipEvent_t *ev = nullptr, mp::SidecarPost *post = nullptr,
+              const uint32_t *seq = nullptr) {
     mp::RouteLaunch l{};
     l.W = d->W; l.x = d->x; l.bias = d->bias; l.prior = d->prior; l.table = d->table; l.dummy = d->dummy;
     l.prior_on_logits = d->prior_on_logits;
@@ -482,6 +504,8 @@ int run_route(const moe_route_desc *d, hipStream_t st, hipEvent_t *ev = nullptr)
     l.counter = (uint32_t *)(ws + align_up((size_t)d->n_tok * d->E * 4, 256));
     l.ids = d->ids; l.w = d->w; l.slots = d->slots; l.probs = d->probs; l.q8x = d->q8x;
     l.logits_in = d->logits;
+    l.post = post;
+    l.seq = seq;
     HIPCHK(mp::launch_route(l, st, ev));
     return MOE_OK;
 }
@@ -574,6 +598,10 @@ void free_cache(moe_cache *c) {
     hipFree(c->out_buf);
     if (c->up_stream) hipStreamDestroy(c->up_stream);
     if (c->stg_stream) hipStreamDestroy(c->stg_stream);
+    if (c->team) mpc::team_destroy(c->team);
+    for (void *p : {(void *)c->sc_post, (void *)c->sc_resp, (void *)c->sc_rows, (void *)c->h_seq})
+        if (p) hipHostFree(p);
+    hipFree(c->d_seq);
     if (c->ev_stg) hipEventDestroy(c->ev_stg);
     hipFree(c->stage);
     if (c->tbl_stream) hipStreamDestroy(c->tbl_stream);
@@ -731,6 +759,31 @@ int moe_route(const moe_route_desc *d, void *stream) {
     if (d->n_tok < 1 || d->n_tok > 65535) return fail(MOE_ERR_ARG, "n_tok %d out of range", d->n_tok);
     return run_route(d, (hipStream_t)stream);
 }
+
+int moe_cpu_experts(const void *const *experts, int n, const uint8_t *q8x, int H, int I, int down_type, float *rows,
+                    int n_threads, int portable) {
+    if (!experts || !q8x || !rows || n < 0) return fail(MOE_ERR_ARG, "moe_cpu_experts: bad arguments");
+    int r = check_shape(64, H, I, 1);
+    if (r != MOE_OK) return r;
+    if (I == 0) return fail(MOE_ERR_ARG, "intermediate size 0");
+    if (down_type != MOE_TYPE_Q4K && down_type != MOE_TYPE_Q6K)
+        return fail(MOE_ERR_ARG, "down type %d unsupported", down_type);
+    std::vector<mpc::CpuExpert> e((size_t)n);
+    for (int k = 0; k < n; ++k) {
+        if (!experts[k]) return fail(MOE_ERR_ARG, "moe_cpu_experts: expert %d is null", k);
+        e[k] = {(const uint8_t *)experts[k], q8x, rows + (size_t)k * H};
+    }
+    std::vector<float> h((size_t)n * I);
+    std::vector<uint8_t> q8h((size_t)n * (I / 256) * mp::Q8K_BYTES);
+    mpc::Team *t = mpc::team_create(n_threads < 1 ? 1 : n_threads);
+    mpc::set_portable(portable != 0);
+    mpc::experts(t, e.data(), n, H, I, down_type, h.data(), q8h.data());
+    mpc::set_portable(false);
+    mpc::team_destroy(t);
+    return MOE_OK;
+}
+
+int moe_cpu_has_vnni(void) { return mpc::has_vnni() ? 1 : 0; }
 
 int moe_experts(const moe_experts_desc *d, void *stream) {
     if (!d || !d->ids || !d->slots || !d->w || !d->q8x || !d->out || !d->workspace)
@@ -893,6 +946,7 @@ int moe_cache_set_host_store(moe_cache *c, int layer, const void *experts, size_
     if (ls.store_dev != dev) drop_graphs(c);
     ls.store_host = (const uint8_t *)experts;
     ls.store_dev = (const uint8_t *)dev;
+    if (c->sc_den > 0) mpc::prefault(c->team, ls.store_host, (size_t)ls.E * ls.expert_bytes);
     return MOE_OK;
 }
 
@@ -1007,6 +1061,9 @@ int moe_cache_stats_get(moe_cache *c, moe_cache_stats *s) {
     s->n_admit_denied = c->n_admit_denied;
     s->n_table_flushes = c->n_table_flushes;
     s->n_staged = c->n_staged;
+    s->n_cpu_served = c->n_cpu_served;
+    s->sidecar_wait_us = c->sc_wait_us;
+    s->sidecar_cpu_us = c->sc_cpu_us;
     s->bytes_uploaded = c->bytes_uploaded;
     s->publication_wait_us = c->wait_us;
     return MOE_OK;
@@ -1015,9 +1072,114 @@ int moe_cache_stats_get(moe_cache *c, moe_cache_stats *s) {
 int moe_cache_set_decode_path(moe_cache *c, int split, int graph) {
     if (!c) return fail(MOE_ERR_ARG, "null cache");
     if (split < 0 || split > 2) return fail(MOE_ERR_ARG, "split must be 0, 1 or 2");
+    if (split != 0 && c->sc_den > 0)
+        return fail(MOE_ERR_STATE, "CPU-assisted serving runs with the one-launch path (split 0); turn it off first");
     c->split = split;
     c->graph = graph != 0;
     return MOE_OK;
+}
+
+int moe_cache_set_sidecar(moe_cache *c, int n_threads, int num, int den) {
+    if (!c) return fail(MOE_ERR_ARG, "null cache");
+    if (c->host_only) return fail(MOE_ERR_STATE, "host-only cache (device < 0) cannot decode");
+    if (n_threads <= 0) {
+        if (c->sc_den) drop_graphs(c);
+        c->sc_den = c->sc_num = 0;
+        return MOE_OK;
+    }
+    if (den < 1 || num < 0 || num > den) return fail(MOE_ERR_ARG, "share %d/%d: need 0 <= num <= den, den >= 1", num, den);
+    if (c->split != 0) return fail(MOE_ERR_STATE, "CPU-assisted serving runs with the one-launch path (split 0)");
+    if (c->K > 16 || (c->H / 256) * mp::Q8K_BYTES > mp::SC_Q8X_BYTES) return fail(MOE_ERR_ARG, "shape too large");
+    HIPCHK(hipSetDevice(c->cfg.device));
+    const size_t NL = c->L.size();
+    const unsigned fl = hipHostMallocMapped | hipHostMallocCoherent;
+    if (!c->sc_post) {
+        if (hipHostMalloc((void **)&c->sc_post, NL * sizeof(mp::SidecarPost), fl) != hipSuccess ||
+            hipHostMalloc((void **)&c->sc_resp, NL * sizeof(mp::SidecarResp), fl) != hipSuccess ||
+            hipHostMalloc((void **)&c->sc_rows, NL * c->K * c->H * sizeof(float), fl) != hipSuccess ||
+            hipHostMalloc((void **)&c->h_seq, 64, hipHostMallocDefault) != hipSuccess ||
+            hipMalloc(&c->d_seq, 64) != hipSuccess)
+            return fail(MOE_ERR_NOMEM, "CPU-assisted serving buffers");
+        memset((void *)c->sc_post, 0, NL * sizeof(mp::SidecarPost));
+        memset((void *)c->sc_resp, 0, NL * sizeof(mp::SidecarResp));
+        HIPCHK(hipHostGetDevicePointer((void **)&c->sc_post_d, c->sc_post, 0));
+        HIPCHK(hipHostGetDevicePointer((void **)&c->sc_resp_d, c->sc_resp, 0));
+        HIPCHK(hipHostGetDevicePointer((void **)&c->sc_rows_d, c->sc_rows, 0));
+        HIPCHK(hipMemset(c->d_seq, 0, 64));
+    }
+    if (c->team && mpc::team_size(c->team) != n_threads) {
+        mpc::team_destroy(c->team);
+        c->team = nullptr;
+    }
+    if (!c->team) c->team = mpc::team_create(n_threads);
+    c->sc_h.resize((size_t)c->K * c->I);
+    c->sc_y.resize((size_t)c->K * c->H);
+    c->sc_q8h.resize((size_t)c->K * (c->I / 256) * mp::Q8K_BYTES);
+    c->sc_q8x.resize((size_t)(c->H / 256) * mp::Q8K_BYTES);
+    // the CPU reads the stores from now on: fault their pages in here, not
+    // expert by expert in the middle of a token
+    for (const Layer &ls : c->L)
+        if (ls.store_host) mpc::prefault(c->team, ls.store_host, (size_t)ls.E * ls.expert_bytes);
+    c->sc_num = num;
+    c->sc_den = den;
+    drop_graphs(c);
+    return MOE_OK;
+}
+
+// wait (bounded) for layer l's post, compute the absent experts assigned to
+// the CPU, publish their rows, answer
+static int sidecar_serve(moe_cache *c, int l, uint32_t seq) {
+    const volatile uint32_t *ps = &c->sc_post[l].seq;
+    const auto t0 = std::chrono::steady_clock::now();
+    unsigned spins = 0;
+    while (*ps != seq) {
+        _mm_pause();
+        if ((++spins & 1023u) == 0 &&
+            std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count() > c->sc_timeout_s)
+            return fail(MOE_ERR_HIP, "layer %d: no post from the GPU within %.1f s", l, c->sc_timeout_s);
+    }
+    std::atomic_thread_fence(std::memory_order_acquire);
+    const auto t1 = std::chrono::steady_clock::now();
+    c->sc_wait_us += std::chrono::duration<double, std::micro>(t1 - t0).count();
+    const Layer &ls = c->L[l];
+    const mp::SidecarPost &p = c->sc_post[l];
+    // the exchange block is memory the GPU reads and writes over PCIe: copy
+    // x's Q8_K out of it once, compute into host scratch, publish the rows once
+    memcpy(c->sc_q8x.data(), p.q8x, c->sc_q8x.size());
+    mpc::CpuExpert e[16];
+    int kk[16];
+    int n = 0, r = 0;
+    for (int k = 0; k < c->K; ++k) {
+        const int id = p.ids[k];
+        if (id < 0 || id >= ls.E || ls.expert_slot[id] >= 0) continue;     // outside the store, or resident
+        if (r++ % c->sc_den < c->sc_num) {
+            kk[n] = k;
+            e[n] = {ls.store_host + (size_t)id * ls.expert_bytes, c->sc_q8x.data(), c->sc_y.data() + (size_t)n * c->H};
+            ++n;
+        }
+    }
+    mpc::experts(c->team, e, n, c->H, c->I, ls.down_type, c->sc_h.data(), c->sc_q8h.data());
+    for (int j = 0; j < n; ++j)
+        memcpy(c->sc_rows + ((size_t)l * c->K + kk[j]) * c->H, c->sc_y.data() + (size_t)j * c->H, (size_t)c->H * 4);
+    c->n_cpu_served += n;
+    const double cpu_us = std::chrono::duration<double, std::micro>(std::chrono::steady_clock::now() - t1).count();
+    c->sc_cpu_us += cpu_us;
+    if (c->sc_log.size() < 3 * 65536) {
+        c->sc_log.push_back((float)std::chrono::duration<double, std::micro>(t1 - t0).count());
+        c->sc_log.push_back((float)cpu_us);
+        c->sc_log.push_back((float)n);
+    }
+    std::atomic_thread_fence(std::memory_order_release);
+    *(volatile uint32_t *)&c->sc_resp[l].seq = seq;
+    return MOE_OK;
+}
+
+int moe_cache_sidecar_log(moe_cache *c, float *out, int max_rows) {
+    if (!c) return -1;
+    const int rows = (int)std::min<size_t>(c->sc_log.size() / 3, (size_t)std::max(0, max_rows));
+    if (out) memcpy(out, c->sc_log.data(), (size_t)rows * 3 * sizeof(float));
+    c->sc_log.clear();
+    return rows;
 }
 
 int moe_cache_set_staging(moe_cache *c, int on) {
@@ -1050,7 +1212,8 @@ int moe_cache_sync(moe_cache *c) {
 }
 
 static int decode_layer_impl(moe_cache *c, int layer, const float *x, const float *bias, float *out,
-                             int32_t *ids_dev, float *w_dev, hipStream_t st, hipEvent_t *ev, bool stage = false);
+                             int32_t *ids_dev, float *w_dev, hipStream_t st, hipEvent_t *ev, bool stage = false,
+                             bool sidecar = false);
 
 int moe_decode_layer(moe_cache *c, int layer, const float *x, const float *bias, float *out, int32_t *ids_dev,
                      float *w_dev, void *stream) {
@@ -1058,7 +1221,8 @@ int moe_decode_layer(moe_cache *c, int layer, const float *x, const float *bias,
 }
 
 static int decode_layer_impl(moe_cache *c, int layer, const float *x, const float *bias, float *out,
-                             int32_t *ids_dev, float *w_dev, hipStream_t st, hipEvent_t *ev, bool stage) {
+                             int32_t *ids_dev, float *w_dev, hipStream_t st, hipEvent_t *ev, bool stage,
+                             bool sidecar) {
     if (!c || !x || !out || layer < 0 || layer >= (int)c->L.size()) return fail(MOE_ERR_ARG, "bad arguments");
     if (c->host_only) return fail(MOE_ERR_STATE, "host-only cache (device < 0) cannot decode");
     const Layer &ls = c->L[layer];
@@ -1078,7 +1242,7 @@ static int decode_layer_impl(moe_cache *c, int layer, const float *x, const floa
     // ev (timing mode), 12 per layer, stamped by the dispatches themselves:
     // [0,1] route_logits [2,3] route_select [4,5] gate/up (resident or all)
     // [6,7] down (resident or all) [8,9] gate/up absent [10,11] down absent
-    int r = run_route(&rd, st, ev);
+    int r = run_route(&rd, st, ev, sidecar ? c->sc_post_d + layer : nullptr, c->d_seq);
     if (r != MOE_OK) return r;
     moe_experts_desc ed{};
     ed.ids = ids; ed.slots = slots; ed.w = w;
@@ -1098,6 +1262,10 @@ static int decode_layer_impl(moe_cache *c, int layer, const float *x, const floa
         a.stage = c->stage + (size_t)layer * c->K * c->stage_stride;
         a.stage_stride = c->stage_stride;
     }
+    if (sidecar) {
+        a.cpu_num = c->sc_num;
+        a.cpu_den = c->sc_den;
+    }
     uint8_t *ws = (uint8_t *)ed.workspace;
     a.h = (float *)ws;
     size_t o = align_up((size_t)(ed.K + 1) * ed.I * 4, 256);
@@ -1115,6 +1283,20 @@ static int decode_layer_impl(moe_cache *c, int layer, const float *x, const floa
     if (c->split == 0) {
         HIPCHK(mp::launch_gateup(a, 0, st, E_(4), E_(5)));
         HIPCHK(mp::launch_down(a, 0, st, E_(6), E_(7)));
+        if (sidecar) {
+            mp::JoinArgs j{};
+            j.ids = a.ids; j.slots = a.slots; j.w = a.w;
+            j.slot_pool = a.slot_pool; j.n_slots = a.n_slots;
+            j.host_store = a.host_store; j.n_experts = a.n_experts;
+            j.K = a.K; j.H = a.H; j.n_shared = a.n_shared; j.cpu_num = a.cpu_num; j.cpu_den = a.cpu_den;
+            j.ypart = c->ypart;
+            j.hrows = c->sc_rows_d + (size_t)layer * c->K * c->H;
+            j.resp = c->sc_resp_d + layer;
+            j.seq = c->d_seq;
+            j.timeout_ticks = (uint64_t)(c->sc_timeout_s * 1e8);     // 100 MHz wall clock
+            j.out = a.out;
+            HIPCHK(mp::launch_join(j, st));
+        }
         return MOE_OK;
     }
     if (c->split == 2) {
@@ -1167,14 +1349,32 @@ int moe_decode_token(moe_cache *c, const float *x, const float *bias, float *out
         HIPCHK(hipStreamWaitEvent(st, c->ev_stg, 0));
         c->stg_pending = false;
     }
+    // CPU-assisted serving: this token's sequence number, for the posts and
+    // the answers of every layer
+    const bool sc = c->sc_den > 0;
+    uint32_t seq = 0;
+    if (sc) {
+        seq = ++c->sc_seq;
+        if (seq == 0 || seq == mp::SC_ABORT) seq = c->sc_seq = 1;
+        *c->h_seq = seq;
+        HIPCHK(hipMemcpyAsync(c->d_seq, c->h_seq, 4, hipMemcpyHostToDevice, st));
+    }
+    auto abort_joins = [&] {        // end every join kernel still waiting
+        if (sc)
+            for (int l = 0; l < NL; ++l) *(volatile uint32_t *)&c->sc_resp[l].seq = mp::SC_ABORT;
+    };
     // per-kernel HIP-event timing needs eager launches: hipEventElapsedTime
     // does not accept events recorded as nodes of a graph
     if (!c->graph || c->timing) {
         for (int l = 0; l < NL; ++l) {
             const int r = decode_layer_impl(c, l, x + (size_t)l * c->H, bias ? bias + (size_t)l * c->E : nullptr,
                                             out + (size_t)l * c->H, nullptr, nullptr, st,
-                                            c->timing ? c->tev.data() + (size_t)l * 12 : nullptr, stage);
-            if (r != MOE_OK) return r;
+                                            c->timing ? c->tev.data() + (size_t)l * 12 : nullptr, stage, sc);
+            if (r != MOE_OK) {
+                abort_joins();
+                hipStreamSynchronize(st);
+                return r;
+            }
         }
     } else {
         const int key = bias ? 1 : 0;
@@ -1186,7 +1386,8 @@ int moe_decode_token(moe_cache *c, const float *x, const float *bias, float *out
             int r = MOE_OK;
             for (int l = 0; l < NL && r == MOE_OK; ++l)
                 r = decode_layer_impl(c, l, c->x_buf + (size_t)l * c->H, key ? c->bias_buf + (size_t)l * c->E : nullptr,
-                                      c->out_buf + (size_t)l * c->H, nullptr, nullptr, c->cap_stream, nullptr, stage);
+                                      c->out_buf + (size_t)l * c->H, nullptr, nullptr, c->cap_stream, nullptr, stage,
+                                      sc);
             hipGraph_t g = nullptr;
             const hipError_t ec = hipStreamEndCapture(c->cap_stream, &g);
             if (r != MOE_OK) { if (g) hipGraphDestroy(g); return r; }
@@ -1200,8 +1401,24 @@ int moe_decode_token(moe_cache *c, const float *x, const float *bias, float *out
         HIPCHK(hipGraphLaunch(c->gx[key], st));
         HIPCHK(hipMemcpyAsync(out, c->out_buf, (size_t)NL * c->H * 4, hipMemcpyDeviceToDevice, st));
     }
+    int serve_err = MOE_OK;
+    if (sc) {               // serve the layers as the GPU reaches them
+        mpc::team_hot(c->team, true);
+        for (int l = 0; l < NL && serve_err == MOE_OK; ++l) serve_err = sidecar_serve(c, l, seq);
+        mpc::team_hot(c->team, false);
+        if (serve_err != MOE_OK) abort_joins();
+    }
     HIPCHK(hipMemcpyAsync(c->h_ids, c->d_ids, (size_t)NL * c->K * 4, hipMemcpyDeviceToHost, st));
     HIPCHK(hipStreamSynchronize(st));
+    if (sc) {
+        bool late = false;
+        for (int l = 0; l < NL; ++l) {
+            late |= c->sc_resp[l].err != 0;
+            c->sc_resp[l].err = 0;
+        }
+        if (serve_err != MOE_OK) return serve_err;
+        if (late) return fail(MOE_ERR_HIP, "a join kernel gave up waiting for the host (%.1f s)", c->sc_timeout_s);
+    }
     if (c->timing) {
         const uint64_t gu_b = 2ull * c->I * (c->H / 256) * mp::Q4K_BYTES;
         for (int l = 0; l < NL; ++l) {
@@ -1235,9 +1452,13 @@ int moe_decode_token(moe_cache *c, const float *x, const float *bias, float *out
     if (stage) {
         for (int l = 0; l < NL; ++l) {
             Layer &ls = c->L[l];
+            int r = 0;         // (absent experts the CPU served were not read by the kernels)
             for (int k = 0; k < c->K; ++k) {
                 const int id = c->h_ids[(size_t)l * c->K + k];
-                ls.staged[k] = id >= 0 && id < ls.E && ls.expert_slot[id] < 0 ? id : -1;
+                const bool absent = id >= 0 && id < ls.E && ls.expert_slot[id] < 0;
+                const bool cpu = absent && sc && r % c->sc_den < c->sc_num;
+                r += absent;
+                ls.staged[k] = absent && !cpu ? id : -1;
             }
         }
     }

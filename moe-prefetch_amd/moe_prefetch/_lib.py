@@ -63,7 +63,9 @@ class CacheStats(ctypes.Structure):
     _fields_ = [(n, U64) for n in ("n_steps", "clock", "n_hit", "n_miss", "n_uploads", "n_scheduled",
                                    "n_copied", "n_published", "n_admit_ok", "n_admit_denied",
                                    "n_table_flushes", "bytes_uploaded")] + \
-               [("publication_wait_us", ctypes.c_double), ("n_staged", ctypes.c_uint64)]
+               [("publication_wait_us", ctypes.c_double), ("n_staged", ctypes.c_uint64),
+                ("n_cpu_served", ctypes.c_uint64), ("sidecar_wait_us", ctypes.c_double),
+                ("sidecar_cpu_us", ctypes.c_double)]
 
 
 class LayerView(ctypes.Structure):
@@ -102,6 +104,9 @@ SIGNATURES = {
     "moe_expert_bytes": (SZ, [ctypes.c_int, ctypes.c_int, ctypes.c_int]),
     "moe_route_workspace_bytes": (SZ, [ctypes.c_int, ctypes.c_int]),
     "moe_experts_workspace_bytes": (SZ, [ctypes.c_int, ctypes.c_int]),
+    "moe_cpu_experts": (ctypes.c_int, [P, ctypes.c_int, P, ctypes.c_int, ctypes.c_int, ctypes.c_int, P,
+                                       ctypes.c_int, ctypes.c_int]),
+    "moe_cpu_has_vnni": (ctypes.c_int, []),
     "moe_route": (ctypes.c_int, [ctypes.POINTER(RouteDesc), P]),
     "moe_experts": (ctypes.c_int, [ctypes.POINTER(ExpertsDesc), P]),
     "moe_cache_create": (ctypes.c_int, [ctypes.POINTER(CacheConfig), ctypes.POINTER(P)]),
@@ -121,6 +126,8 @@ SIGNATURES = {
     "moe_cache_set_timing": (ctypes.c_int, [P, ctypes.c_int]),
     "moe_cache_set_decode_path": (ctypes.c_int, [P, ctypes.c_int, ctypes.c_int]),
     "moe_cache_set_staging": (ctypes.c_int, [P, ctypes.c_int]),
+    "moe_cache_set_sidecar": (ctypes.c_int, [P, ctypes.c_int, ctypes.c_int, ctypes.c_int]),
+    "moe_cache_sidecar_log": (ctypes.c_int, [P, P, ctypes.c_int]),
     "moe_cache_kernel_times": (ctypes.c_int, [P, ctypes.POINTER(KernelTimes)]),
     "moe_decode_layer": (ctypes.c_int, [P, ctypes.c_int, P, P, P, P, P, P]),
     "moe_decode_token": (ctypes.c_int, [P, P, P, P, P, P]),

@@ -176,6 +176,21 @@ class MoeCache:
     def set_timing(self, on=True):
         check(lib().moe_cache_set_timing(self.h, int(on)), "set_timing")
 
+    def set_sidecar(self, n_threads, share=(1, 1)):
+        """CPU-assisted serving of absent experts (the reference's sidecar):
+        n_threads host threads (0 = off) compute the absent experts whose rank
+        r among a layer's absent ones has r % den < num, share = (num, den),
+        while the GPU runs the rest.  Same outputs and traces."""
+        num, den = share
+        check(lib().moe_cache_set_sidecar(self.h, int(n_threads), int(num), int(den)), "set_sidecar")
+
+    def sidecar_log(self, max_rows=65536):
+        """[rows][3] float32: host wait us, host compute us, experts computed,
+        per served layer since the last call."""
+        out = np.empty((max_rows, 3), np.float32)
+        n = lib().moe_cache_sidecar_log(self.h, out.ctypes.data, max_rows)
+        return out[:max(n, 0)].copy()
+
     def set_staging(self, on=True):
         """Uploads of experts a decode token just read from the pinned store are
         copied from an HBM staging area instead of over PCIe (default on)."""

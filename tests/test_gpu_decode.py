@@ -192,6 +192,42 @@ def test_staged_uploads_fill_slots(knobs):
         assert on[3][k] == off[3][k], k
 
 
+@pytest.mark.parametrize("case", ["all-graph", "two-thirds-graph", "all-eager", "e256-shared"])
+def test_sidecar_decode_matches_oracle(tmp_path, case):
+    # CPU-assisted serving: the router kernel posts ids and Q8_K(x) to mapped
+    # host memory, the host computes the absent experts assigned to it, the
+    # join kernel combines in k order -- ids, frames, traces and outputs bit
+    # for bit as the oracle's
+    if case == "e256-shared":
+        rig = Rig([40, 24], [Q4, Q6], T=32, I=512, E=256, shared=True, zipf_s=1.0, reuse=0.5, admit="window",
+                  batch_tables=True, cache_prior=0.01)
+    else:
+        rig = Rig([16, 24, 12, 40], [Q4, Q6, Q4, Q6], T=40, admit="window", batch_tables=True)
+    share = (2, 3) if case == "two-thirds-graph" else (1, 1)
+    rig.cache.set_decode_path(split=0, graph=case != "all-eager")
+    rig.cache.set_sidecar(6, share)
+    try:
+        check_run(rig, tmp_path)
+    finally:
+        rig.close()
+
+
+def test_sidecar_counts_cpu_served():
+    rig = Rig([16, 24], [Q4, Q6], T=24, admit="window", batch_tables=True)
+    try:
+        rig.cache.set_sidecar(4)
+        ids_on, outs_on, _ = rig.run()
+        st = rig.cache.stats()
+        assert st["n_cpu_served"] == st["n_miss"] > 0       # every absent expert went to the CPU
+        assert st["n_staged"] == 0                          # none was read by the kernels
+        with pytest.raises(_lib.MoeError):
+            rig.cache.set_decode_path(split=1)              # the split paths need the sidecar off
+        rig.cache.set_sidecar(0)
+        rig.cache.set_decode_path(split=1)
+    finally:
+        rig.close()
+
+
 def test_decode_48_layers_full_shape(tmp_path):
     """The stacked Qwen3-30B-A3B shape at full size (48 layers, 56 slots, Q6_K
     down in odd layers, pinned store of all 128 experts per layer), for the
