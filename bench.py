@@ -11,7 +11,9 @@ inserts per layer per step.  A step is one batch-1 decode token through all 48
 layers (router, experts from HBM slots or the pinned store, combine, routed ids
 back, cache step with uploads on the side stream), replayed as one HIP graph.
 The synthetic sequence is 512 tokens: --warmup tokens warm the cache, the next
---steps are timed.
+--steps are timed.  Absent experts are served by the host CPU (14 threads on a
+16-CPU host, 3 of every 4 absent experts of a layer; --sidecar 0 for the
+GPU-only path) while the GPU runs the resident ones.
 
 --workload prefill48 [--batch 512|64]: batched MoE layers -- a chunk of
 tokens (bf16 activations, uniform router logits) through 48 layers whose 128
@@ -680,8 +682,9 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="bounded CPU-baseline sample")
     ap.add_argument("--kernel-steps", type=int, default=64, help="eager tokens timed per kernel")
     ap.add_argument("--path", type=int, default=0, help="0 fused, 1 fork/join, 2 serial expert launches")
-    ap.add_argument("--sidecar", type=int, default=0, help="host threads serving absent experts (0: GPU only)")
-    ap.add_argument("--share", default="1/1", help="num/den: absent experts of rank r with r %% den < num go to "
+    ap.add_argument("--sidecar", type=int, default=-1,
+                    help="host threads serving absent experts (0: GPU only; default: 14 on a 16-CPU host)")
+    ap.add_argument("--share", default="3/4", help="num/den: absent experts of rank r with r %% den < num go to "
                                                    "the CPU")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="end with a plain 256 MiB device copy (scale for rocprofv3 FETCH_SIZE/WRITE_SIZE)")
@@ -694,6 +697,9 @@ def main():
               "(the expert-sharded design is described in DESIGN.md); run with --gpus 1", file=sys.stderr)
         sys.exit(2)
 
+    if args.sidecar < 0:
+        n_cpu = len(os.sched_getaffinity(0))
+        args.sidecar = 14 if n_cpu >= 16 else (n_cpu - 2 if n_cpu >= 8 else 0)
     wide = args.workload == "wide40"
     if args.steps is None:
         args.steps = 960 if wide else 448
