@@ -403,6 +403,16 @@ def run_stacked(args, wl):
         result["check"] = wl.check(ids_log, kept, frames, s1, knobs)
         log(f"[bench] check: {result['check']}")
     cache.close()
+    if args.sidecar > 0 and not args.no_gpu_only:
+        log("[bench] the same decode with the GPU alone serving absent experts")
+        c2 = wl.cache(**knobs)
+        c2.set_decode_path(split=args.path, graph=True)
+        el2, g0, g1, ids2, _, _ = wl.decode(c2)
+        c2.close()
+        result["gpu_only"] = {"value": round(args.steps / el2, 2), "unit": "tok/s",
+                              "ids_equal": bool((ids2 == ids_log).all()),
+                              "path": "absent experts read by the kernels from the pinned store over PCIe, "
+                                      "staged uploads"}
     return result
 
 
@@ -689,6 +699,7 @@ def main():
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="end with a plain 256 MiB device copy (scale for rocprofv3 FETCH_SIZE/WRITE_SIZE)")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-gpu-only", action="store_true", help="skip the GPU-only decode beside the default one")
     ap.add_argument("--no-check", action="store_true")
     args = ap.parse_args()
 

@@ -82,13 +82,14 @@ class MoeCache:
 
     @classmethod
     def from_env(cls, n_layers, n_slots, max_inserts=2, env=None, **shape):
-        """Knobs from the reference's environment variables (patches 0006:501-539, 0007:492-506)."""
+        """Knobs from the reference's environment variables (patches 0006:501-539, 0007:492-506;
+        LLAMA_MOE_SIDECAR / LLAMA_MOE_SIDECAR_THREADS, patches 0009:954-960, 1084-1086)."""
         env = os.environ if env is None else env
         g = env.get
         admit = g("LLAMA_MOE_ADMIT", "off") or "off"
         if admit == "0":
             admit = "off"
-        return cls(n_layers, n_slots=n_slots, max_inserts=max_inserts,
+        c = cls(n_layers, n_slots=n_slots, max_inserts=max_inserts,
                    slot_profile=parse_slot_profile(g("LLAMA_MOE_SLOT_PROFILE"), n_layers, n_slots),
                    admit=admit,
                    admit_window=max(1, int(g("LLAMA_MOE_ADMIT_WINDOW", "8"))),
@@ -98,6 +99,9 @@ class MoeCache:
                    early_issue=int(g("LLAMA_MOE_EARLY_ISSUE", "0")) != 0,
                    cache_prior=max(0.0, float(g("LLAMA_MOE_CACHE_PRIOR", "0"))),
                    deterministic=int(g("LLAMA_MOE_DETERMINISTIC", "0")) != 0, **shape)
+        if int(g("LLAMA_MOE_SIDECAR", "0") or "0") != 0:
+            c.set_sidecar(max(1, int(g("LLAMA_MOE_SIDECAR_THREADS", "8"))))
+        return c
 
     def close(self):
         if getattr(self, "h", None):
