@@ -235,6 +235,23 @@ int moe_cache_frame(moe_cache *c, int layer, int32_t *out);   /* out[slot] = exp
 int moe_cache_table(moe_cache *c, int layer, int32_t *tbl, float *prior);  /* host mirrors */
 int moe_cache_stats_get(moe_cache *c, moe_cache_stats *out);
 int moe_cache_sync(moe_cache *c);  /* wait for every upload in flight */
+/* Heat file, LLAMA_MOE_HEAT_FILE (patches/0007:431-485 load/save, 568-621 warm
+ * start, 745-752 periodic save): from now on every observed id is counted and
+ * the counts are written to `path` every 512 steps ("moe-heat 1 <layers>
+ * <experts>", then "<il> <expert> <count>"; via <path>.tmp and a rename).  If
+ * `path` holds this cache's dimensions, its counts are loaded halved and the
+ * hottest experts of every layer are copied into slots 0.. before the first
+ * token (a reserve of max_inserts slots is kept free with early issue).  Call
+ * after registering the host stores and before the first step. */
+int moe_cache_heat_file(moe_cache *c, const char *path, int64_t *n_records, int64_t *n_placed);
+/* LLAMA_MOE_CACHE_FREEZE (patches/0008:496-500, 825-832): no uploads from now on */
+int moe_cache_freeze(moe_cache *c);
+/* LLAMA_MOE_MAP_REPLAY (patches/0008:436-474, 559-565): every step ends with
+ * the placement `path` recorded for it (a moe_cache_trace_open map file),
+ * copying mismatched slots from the host store; freezes the cache.  Call
+ * before the first step, after registering the stores; exclusive with a map
+ * record.  A step whose frame is missing fails. */
+int moe_cache_map_replay(moe_cache *c, const char *path);
 
 /* Kernel time of the decode, from HIP events recorded around each launch on
  * the stream it runs on (off by default; set before decoding).  Experts

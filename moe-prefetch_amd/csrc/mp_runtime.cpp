@@ -70,6 +70,7 @@ struct Layer {
     uint8_t *shared = nullptr;                // dev: the always-on shared expert (owned) or null
     std::vector<int32_t> slot_expert, expert_slot, free_slots, pending;
     std::vector<int32_t> staged;              // [K] expert read from the store at k this token (staged), or -1
+    std::vector<uint32_t> use_count;          // heat file: observations per expert (empty: no heat file)
     std::vector<uint64_t> slot_last_use, slot_protect, miss_last, miss_prev;
     std::vector<uint8_t> slot_in_flight;
     std::vector<float> heat;
@@ -134,6 +135,11 @@ struct moe_cache {
     std::vector<uint8_t> sc_q8h, sc_q8x;
     uint64_t n_cpu_served = 0;
     double sc_wait_us = 0.0, sc_cpu_us = 0.0;   // host time waiting for posts / computing experts
+    // heat file (LLAMA_MOE_HEAT_FILE), freeze (LLAMA_MOE_CACHE_FREEZE) and
+    // placement-map replay (LLAMA_MOE_MAP_REPLAY)
+    std::string heat_path;
+    bool freeze = false;
+    FILE *replay = nullptr;
     std::vector<float> sc_log;                  // per served layer: wait us, cpu us, experts (last 64K)
     uint64_t clock = 0, n_steps = 0, n_uploads = 0, n_scheduled = 0, n_copied = 0, n_published = 0;
     uint64_t n_admit_ok = 0, n_admit_denied = 0, n_table_flushes = 0, bytes_uploaded = 0;
@@ -258,6 +264,7 @@ int start_upload(moe_cache *c, int li, int expert, int slot) {
 int issue_uploads(moe_cache *c, int li, const int32_t *ids, int n, int budget, int min_keep) {
     Layer &ls = c->L[li];
     int issued = 0;
+    if (c->freeze) return 0;
     for (int i = 0; i < n && issued < budget; ++i) {
         const int id = ids[i];
         if (id < 0 || id >= ls.E) continue;
@@ -279,8 +286,61 @@ int issue_uploads(moe_cache *c, int li, const int32_t *ids, int n, int budget, i
     return issued;
 }
 
-void map_frame(moe_cache *c) {
-    if (!c->map) return;
+int flush_tables(moe_cache *c);
+
+// copy expert e of layer ls from the pinned store into a slot (replay and
+// warm start: synchronous, before any kernel reads the slot)
+static int place_bytes(moe_cache *c, const Layer &ls, int e, int slot) {
+    if (c->host_only) return MOE_OK;
+    if (!ls.store_host) return fail(MOE_ERR_STATE, "layer %d: host store missing for a placement", ls.il);
+    HIPCHK(hipMemcpyAsync(ls.pool + (size_t)slot * ls.slot_bytes, ls.store_host + (size_t)e * ls.expert_bytes,
+                          ls.expert_bytes, hipMemcpyHostToDevice, c->up_stream));
+    return MOE_OK;
+}
+
+// replay: this step's recorded frame becomes the placement, every table entry
+// rewritten (patches/0008:436-474)
+static int replay_frame(moe_cache *c) {
+    unsigned long long step = 0;
+    if (fscanf(c->replay, " step %llu", &step) != 1 || step != c->n_steps)
+        return fail(MOE_ERR_STATE, "map replay: no frame for step %llu", (unsigned long long)c->n_steps);
+    for (Layer &ls : c->L) {
+        int il = -1;
+        if (fscanf(c->replay, " map %d", &il) != 1 || il != ls.il)
+            return fail(MOE_ERR_STATE, "map replay: step %llu has no frame for layer %d", step, ls.il);
+        std::vector<int32_t> want(ls.S);
+        std::vector<uint8_t> seen(ls.E, 0);
+        for (auto &v : want) {
+            if (fscanf(c->replay, "%d", &v) != 1 || v < -1 || v >= ls.E || (v >= 0 && seen[v]))
+                return fail(MOE_ERR_STATE, "map replay: bad frame for layer %d at step %llu", ls.il, step);
+            if (v >= 0) seen[v] = 1;
+        }
+        for (int s = 0; s < ls.S; ++s)
+            if (want[s] >= 0 && ls.slot_expert[s] != want[s]) {
+                const int r = place_bytes(c, ls, want[s], s);
+                if (r != MOE_OK) return r;
+            }
+        std::fill(ls.expert_slot.begin(), ls.expert_slot.end(), -1);
+        for (int e = 0; e < ls.E; ++e) set_table_entry(c, ls, e, ls.S);
+        for (int s = 0; s < ls.S; ++s) {
+            ls.slot_expert[s] = want[s];
+            ls.slot_in_flight[s] = 0;
+            if (want[s] >= 0) {
+                ls.expert_slot[want[s]] = s;
+                set_table_entry(c, ls, want[s], s);
+            }
+        }
+    }
+    if (!c->host_only) HIPCHK(hipStreamSynchronize(c->up_stream));
+    return flush_tables(c);
+}
+
+int map_frame(moe_cache *c) {
+    if (c->replay) {
+        const int r = replay_frame(c);
+        if (r != MOE_OK) return r;
+    }
+    if (!c->map) return MOE_OK;
     fprintf(c->map, "step %llu\n", (unsigned long long)c->n_steps);
     for (const Layer &ls : c->L) {
         std::vector<int32_t> pub(ls.S, -1);
@@ -291,6 +351,21 @@ void map_frame(moe_cache *c) {
         fputc('\n', c->map);
     }
     fflush(c->map);
+    return MOE_OK;
+}
+
+// "moe-heat 1 <layers> <experts>", then "<il> <expert> <count>" for every
+// non-zero count; written to <path>.tmp and renamed (patches/0007:468-485)
+static bool save_heat(const moe_cache *c) {
+    const std::string tmp = c->heat_path + ".tmp";
+    FILE *f = fopen(tmp.c_str(), "w");
+    if (!f) return false;
+    fprintf(f, "moe-heat 1 %zu %d\n", c->L.size(), c->E);
+    for (const Layer &ls : c->L)
+        for (int e = 0; e < ls.E; ++e)
+            if (ls.use_count[e]) fprintf(f, "%d %d %u\n", ls.il, e, ls.use_count[e]);
+    const bool ok = fclose(f) == 0;
+    return ok && rename(tmp.c_str(), c->heat_path.c_str()) == 0;
 }
 
 int flush_tables(moe_cache *c) {
@@ -399,7 +474,7 @@ int cache_step(moe_cache *c) {
             continue;
         }
         ls.pending.clear();
-        const int pool_target = c->cfg.max_inserts;
+        const int pool_target = c->freeze ? 0 : c->cfg.max_inserts;
         while ((int)ls.free_slots.size() < pool_target) {
             int slot = -1;
             uint64_t best = U64MAX;
@@ -426,9 +501,12 @@ int cache_step(moe_cache *c) {
     const int r = flush_tables(c);
     if (r != MOE_OK) return r;
 
-    map_frame(c);
+    // 5) heat file every 512 steps (not while frozen), then the map frame
+    if (!c->freeze && !c->heat_path.empty() && c->n_steps % 512 == 0 && !save_heat(c))
+        fprintf(stderr, "moe-cache: heat file write FAILED: %s\n", c->heat_path.c_str());
+    const int r2 = map_frame(c);
     if (c->route) fflush(c->route);
-    return MOE_OK;
+    return r2;
 }
 
 int cache_observe(moe_cache *c, int li, const int32_t *ids, int n_ids, int n_tok) {
@@ -444,6 +522,7 @@ int cache_observe(moe_cache *c, int li, const int32_t *ids, int n_ids, int n_tok
             const int id = ids[t * n_ids + i];
             if (id < 0 || id >= ls.E) continue;
             if (!ls.heat.empty()) ls.heat[id] += 1.0f;
+            if (!ls.use_count.empty()) ls.use_count[id]++;
             const int slot = ls.expert_slot[id];
             if (slot >= 0) {
                 ls.n_hit++;
@@ -460,7 +539,7 @@ int cache_observe(moe_cache *c, int li, const int32_t *ids, int n_ids, int n_tok
         }
     }
     if (c->cfg.early_issue) {
-        const int pool_target = c->cfg.max_inserts;
+        const int pool_target = c->freeze ? 0 : c->cfg.max_inserts;
         const int next_victim = c->cfg.admit_mode == MOE_ADMIT_OFF ? -1
                                 : ((int)ls.free_slots.size() > pool_target ? -1 : lru_resident(ls));
         int r;
@@ -575,6 +654,7 @@ void free_cache(moe_cache *c) {
         free(c->h_tbl);
         free(c->h_prior);
         if (c->route) fclose(c->route);
+        if (c->replay) fclose(c->replay);
         if (c->map) fclose(c->map);
         delete c;
         return;
@@ -625,6 +705,7 @@ void free_cache(moe_cache *c) {
     if (c->h_ids) hipHostFree(c->h_ids);
     if (c->route) fclose(c->route);
     if (c->map) fclose(c->map);
+    if (c->replay) fclose(c->replay);
     delete c;
 }
 
@@ -1006,6 +1087,7 @@ int moe_cache_trace_open(moe_cache *c, const char *route_path, const char *map_p
         if (!c->route) return fail(MOE_ERR_IO, "cannot open %s", route_path);
     }
     if (map_path) {
+        if (c->replay) return fail(MOE_ERR_STATE, "a map is being replayed: it cannot be recorded too");
         c->map = fopen(map_path, "w");
         if (!c->map) return fail(MOE_ERR_IO, "cannot open %s", map_path);
         fprintf(c->map, "moe-map 1 %zu\n", c->L.size());
@@ -1026,7 +1108,106 @@ int moe_cache_step(moe_cache *c) {
     return cache_step(c);
 }
 
-int moe_cache_requires_sync(const moe_cache *c) { return c && c->cfg.publish == MOE_PUBLISH_SORTED ? 1 : 0; }
+int moe_cache_requires_sync(const moe_cache *c) {
+    return c && (c->cfg.publish == MOE_PUBLISH_SORTED || c->replay) ? 1 : 0;
+}
+
+int moe_cache_freeze(moe_cache *c) {
+    if (!c) return fail(MOE_ERR_ARG, "null cache");
+    c->freeze = true;
+    c->cfg.max_inserts = 0;
+    return MOE_OK;
+}
+
+int moe_cache_heat_file(moe_cache *c, const char *path, int64_t *n_records, int64_t *n_placed) {
+    if (!c || !path) return fail(MOE_ERR_ARG, "bad arguments");
+    if (c->n_steps != 0 || !c->jobs.empty()) return fail(MOE_ERR_STATE, "the heat file is read before the first step");
+    for (const Layer &ls : c->L)
+        for (int s = 0; s < ls.S; ++s)
+            if (ls.slot_expert[s] >= 0) return fail(MOE_ERR_STATE, "the heat file needs an empty cache");
+    if (!c->host_only)
+        for (const Layer &ls : c->L)
+            if (!ls.store_host) return fail(MOE_ERR_STATE, "layer %d: register the host store first", ls.il);
+    c->heat_path = path;
+    for (Layer &ls : c->L) ls.use_count.assign(ls.E, 0);
+    // load (patches/0007:434-466): another model's dimensions are refused by name
+    int64_t n_rec = 0, placed = 0;
+    if (FILE *f = fopen(path, "r")) {
+        int ver = 0, nl = 0, ne = 0;
+        if (fscanf(f, "moe-heat %d %d %d", &ver, &nl, &ne) != 3 || ver != 1 || nl != (int)c->L.size() || ne != c->E) {
+            fprintf(stderr, "moe-cache: HEAT FILE REFUSED: %s is v%d for %d layers x %d experts, this cache holds "
+                            "%zu x %d\n", path, ver, nl, ne, c->L.size(), c->E);
+        } else {
+            int il = 0, e = 0;
+            unsigned cnt = 0;
+            while (fscanf(f, "%d %d %u", &il, &e, &cnt) == 3) {
+                if (il < 0 || il >= (int)c->L.size() || e < 0 || e >= c->L[il].E) continue;
+                c->L[il].use_count[e] = cnt / 2;     // halved, so an old workload fades
+                n_rec++;
+            }
+        }
+        fclose(f);
+    }
+    // warm start (patches/0007:568-611): hottest first into slots 0.., a reserve
+    // for early issue; the hottest is the most recent use, so LRU evicts the
+    // coldest of the warm set first
+    if (n_rec > 0) {
+        const int reserve = c->cfg.early_issue ? c->cfg.max_inserts : 0;
+        for (Layer &ls : c->L) {
+            std::vector<int32_t> order(ls.E);
+            for (int e = 0; e < ls.E; ++e) order[e] = e;
+            std::stable_sort(order.begin(), order.end(),
+                             [&](int32_t a, int32_t b) { return ls.use_count[a] > ls.use_count[b]; });
+            const int fill = std::max(0, ls.S - reserve);
+            int slot = 0;
+            for (int k = 0; k < ls.E && slot < fill; ++k) {
+                const int e = order[k];
+                if (ls.use_count[e] == 0) break;         // never routed to: not worth a slot on a guess
+                const int r = place_bytes(c, ls, e, slot);
+                if (r != MOE_OK) return r;
+                ls.slot_expert[slot] = e;
+                ls.expert_slot[e] = slot;
+                ls.slot_last_use[slot] = (uint64_t)(fill - slot);
+                set_table_entry(c, ls, e, slot);
+                ++slot;
+                ++placed;
+            }
+            c->clock = std::max<uint64_t>(c->clock, (uint64_t)fill);
+            ls.free_slots.clear();
+            for (int f2 = ls.S - 1; f2 >= slot; --f2) ls.free_slots.push_back(f2);   // lowest free on top
+        }
+        if (!c->host_only) HIPCHK(hipStreamSynchronize(c->up_stream));
+        const int r = flush_tables(c);
+        if (r != MOE_OK) return r;
+    }
+    fprintf(stderr, "moe-cache: heat file %s: %lld records, %lld experts placed before the first token%s\n", path,
+            (long long)n_rec, (long long)placed, n_rec ? "" : " (COLD START - file missing, empty or refused)");
+    if (n_records) *n_records = n_rec;
+    if (n_placed) *n_placed = placed;
+    return MOE_OK;
+}
+
+int moe_cache_map_replay(moe_cache *c, const char *path) {
+    if (!c || !path) return fail(MOE_ERR_ARG, "bad arguments");
+    if (c->map) return fail(MOE_ERR_STATE, "a map is being recorded: it cannot be replayed too");
+    if (c->replay) return fail(MOE_ERR_STATE, "a map is already being replayed");
+    if (c->n_steps != 0 || !c->jobs.empty()) return fail(MOE_ERR_STATE, "a replay starts before the first step");
+    FILE *f = fopen(path, "r");
+    if (!f) return fail(MOE_ERR_IO, "cannot open %s", path);
+    int ver = 0, nl = 0;
+    bool ok = fscanf(f, "moe-map %d %d", &ver, &nl) == 2 && ver == 1 && nl == (int)c->L.size();
+    for (const Layer &ls : c->L) {
+        int il = -1, s = 0, e = 0;
+        ok = ok && fscanf(f, " layer %d %d %d", &il, &s, &e) == 3 && il == ls.il && s == ls.S && e == ls.E;
+    }
+    if (!ok) {
+        fclose(f);
+        return fail(MOE_ERR_ARG, "%s does not describe this cache's layers and slots", path);
+    }
+    c->replay = f;
+    moe_cache_freeze(c);
+    return map_frame(c);             // the frame of step 0, as at the reference's init (patches/0008:571)
+}
 
 int moe_cache_frame(moe_cache *c, int layer, int32_t *out) {
     if (!c || !out || layer < 0 || layer >= (int)c->L.size()) return fail(MOE_ERR_ARG, "bad arguments");

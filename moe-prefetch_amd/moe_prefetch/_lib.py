@@ -128,6 +128,10 @@ SIGNATURES = {
     "moe_cache_set_staging": (ctypes.c_int, [P, ctypes.c_int]),
     "moe_cache_set_sidecar": (ctypes.c_int, [P, ctypes.c_int, ctypes.c_int, ctypes.c_int]),
     "moe_cache_sidecar_log": (ctypes.c_int, [P, P, ctypes.c_int]),
+    "moe_cache_heat_file": (ctypes.c_int, [P, ctypes.c_char_p, ctypes.POINTER(ctypes.c_int64),
+                                           ctypes.POINTER(ctypes.c_int64)]),
+    "moe_cache_freeze": (ctypes.c_int, [P]),
+    "moe_cache_map_replay": (ctypes.c_int, [P, ctypes.c_char_p]),
     "moe_cache_kernel_times": (ctypes.c_int, [P, ctypes.POINTER(KernelTimes)]),
     "moe_decode_layer": (ctypes.c_int, [P, ctypes.c_int, P, P, P, P, P, P]),
     "moe_decode_token": (ctypes.c_int, [P, P, P, P, P, P]),

@@ -99,6 +99,8 @@ class MoeCache:
                    early_issue=int(g("LLAMA_MOE_EARLY_ISSUE", "0")) != 0,
                    cache_prior=max(0.0, float(g("LLAMA_MOE_CACHE_PRIOR", "0"))),
                    deterministic=int(g("LLAMA_MOE_DETERMINISTIC", "0")) != 0, **shape)
+        if int(g("LLAMA_MOE_CACHE_FREEZE", "0") or "0") != 0:
+            c.freeze()
         if int(g("LLAMA_MOE_SIDECAR", "0") or "0") != 0:
             c.set_sidecar(max(1, int(g("LLAMA_MOE_SIDECAR_THREADS", "8"))))
         return c
@@ -187,6 +189,24 @@ class MoeCache:
         while the GPU runs the rest.  Same outputs and traces."""
         num, den = share
         check(lib().moe_cache_set_sidecar(self.h, int(n_threads), int(num), int(den)), "set_sidecar")
+
+    def heat_file(self, path):
+        """LLAMA_MOE_HEAT_FILE: count observations, save every 512 steps, and
+        warm-start from `path` if it holds this cache's dimensions.  Returns
+        (records loaded, experts placed).  After set_host_store, before decoding."""
+        nr, npl = ctypes.c_int64(), ctypes.c_int64()
+        check(lib().moe_cache_heat_file(self.h, str(path).encode(), ctypes.byref(nr), ctypes.byref(npl)),
+              "heat_file")
+        return nr.value, npl.value
+
+    def freeze(self):
+        """LLAMA_MOE_CACHE_FREEZE: no uploads from now on."""
+        check(lib().moe_cache_freeze(self.h), "freeze")
+
+    def map_replay(self, path):
+        """LLAMA_MOE_MAP_REPLAY: every step ends with the placement recorded in
+        `path` (a trace_open map file).  Freezes the cache."""
+        check(lib().moe_cache_map_replay(self.h, str(path).encode()), "map_replay")
 
     def sidecar_log(self, max_rows=65536):
         """[rows][3] float32: host wait us, host compute us, experts computed,

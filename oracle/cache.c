@@ -9,10 +9,12 @@
  *   step      0006:765-953, 0007:655-771, 0008:607-660 (deterministic publication)
  *   admission 0007:398-429 (lru_resident, admit_ok)
  *   tables    0007:327-396 (set_table_entry, flush_tables)
- *   map trace 0008:417-489
- * The predictor/evictor, heat file, speculative probation and freeze are not
- * restated (out of scope); slot_protect is kept at 0, which is what it is when
- * no speculative upload exists.
+ *   map trace 0008:417-489 (record and replay)
+ *   heat file 0007:431-485 (load/save), 0007:568-621 (warm start), 0007:745-752
+ *   freeze    0008:496-500, 825-832
+ * The predictor/evictor and speculative probation are not restated (out of
+ * scope); slot_protect is kept at 0, which is what it is when no speculative
+ * upload exists.
  *
  * Upload completion: every job is published at the step after the one that
  * scheduled (or, early path, issued) it.  With `deterministic` the order is
@@ -40,6 +42,7 @@ typedef struct {
     int32_t *pending;
     int n_pending;
     float *heat;
+    uint32_t *use_count;            /* heat-file counts, or NULL */
     uint64_t *miss_last, *miss_prev;
     int32_t *tbl_mirror;
     float *prior_mirror;
@@ -63,7 +66,9 @@ struct or_cache {
     int n_jobs, cap_jobs;
     job_t *holds;
     int n_holds;
-    FILE *route, *map;
+    FILE *route, *map, *replay;
+    char *heat_path;
+    int freeze, replay_err;
 };
 
 static void push_job(or_cache *c, int li, int e, int slot) {
@@ -156,17 +161,52 @@ void or_cache_destroy(or_cache *c) {
         free(ls->slot_expert); free(ls->expert_slot); free(ls->slot_last_use);
         free(ls->slot_protect); free(ls->slot_in_flight); free(ls->free_slots);
         free(ls->pending); free(ls->tbl_mirror); free(ls->prior_mirror);
-        free(ls->heat); free(ls->miss_last); free(ls->miss_prev);
+        free(ls->heat); free(ls->miss_last); free(ls->miss_prev); free(ls->use_count);
     }
     if (c->route) fclose(c->route);
     if (c->map) fclose(c->map);
+    if (c->replay) fclose(c->replay);
+    free(c->heat_path);
     free(c->L);
     free(c->jobs);
     free(c->holds);
     free(c);
 }
 
+static void flush_tables(or_cache *c);
+static int save_heat(or_cache *c);
+
+/* 0008:436-474: read this step's frame and make it the placement */
+static void replay_frame(or_cache *c) {
+    unsigned long long step = 0;
+    if (fscanf(c->replay, " step %llu", &step) != 1 || step != c->n_steps) { c->replay_err = 1; return; }
+    int32_t *want = (int32_t *)malloc(sizeof(int32_t) * 4096);
+    uint8_t *seen = (uint8_t *)malloc((size_t)c->E);
+    for (int l = 0; l < c->n_layers && !c->replay_err; ++l) {
+        layer_t *ls = &c->L[l];
+        int il = -1;
+        if (fscanf(c->replay, " map %d", &il) != 1 || il != ls->il) { c->replay_err = 1; break; }
+        memset(seen, 0, (size_t)c->E);
+        for (int s = 0; s < ls->S; ++s) {
+            if (fscanf(c->replay, "%d", &want[s]) != 1 || want[s] < -1 || want[s] >= ls->E ||
+                (want[s] >= 0 && seen[want[s]])) { c->replay_err = 1; break; }
+            if (want[s] >= 0) seen[want[s]] = 1;
+        }
+        if (c->replay_err) break;
+        for (int e = 0; e < ls->E; ++e) { ls->expert_slot[e] = -1; set_table_entry(c, ls, e, ls->S); }
+        for (int s = 0; s < ls->S; ++s) {
+            ls->slot_expert[s] = want[s];
+            ls->slot_in_flight[s] = 0;
+            if (want[s] >= 0) { ls->expert_slot[want[s]] = s; set_table_entry(c, ls, want[s], s); }
+        }
+    }
+    free(want);
+    free(seen);
+    if (!c->replay_err) flush_tables(c);
+}
+
 static void map_frame(or_cache *c) {
+    if (c->replay && !c->replay_err) replay_frame(c);
     if (!c->map) return;
     fprintf(c->map, "step %llu\n", (unsigned long long)c->n_steps);
     int32_t *pub = (int32_t *)malloc(sizeof(int32_t) * 1024);
@@ -201,6 +241,7 @@ int or_cache_trace_open(or_cache *c, const char *route_path, const char *map_pat
 static int issue_uploads(or_cache *c, int li, const int32_t *ids, int n, int budget, int min_keep) {
     layer_t *ls = &c->L[li];
     int issued = 0;
+    if (c->freeze) return 0;
     for (int i = 0; i < n && issued < budget; ++i) {
         const int id = ids[i];
         if (id < 0 || id >= ls->E) continue;
@@ -233,6 +274,7 @@ void or_cache_observe(or_cache *c, int li, const int32_t *ids, int n_ids, int n_
             const int id = ids[t * n_ids + i];
             if (id < 0 || id >= ls->E) continue;
             if (ls->heat) ls->heat[id] += 1.0f;
+            if (ls->use_count) ls->use_count[id]++;
             const int slot = ls->expert_slot[id];
             if (slot >= 0) {
                 ls->n_hit++;
@@ -250,7 +292,7 @@ void or_cache_observe(or_cache *c, int li, const int32_t *ids, int n_ids, int n_
         }
     }
     if (c->k.early_issue) {
-        const int pool_target = c->k.max_inserts;
+        const int pool_target = c->freeze ? 0 : c->k.max_inserts;
         const int next_victim = c->k.admit_mode == 0 ? -1 :
             (ls->n_free > pool_target ? -1 : lru_resident(ls));
         if (c->k.admit_mode == 0) {
@@ -331,7 +373,7 @@ void or_cache_step(or_cache *c) {
             continue;
         }
         ls->n_pending = 0;
-        const int pool_target = c->k.max_inserts;
+        const int pool_target = c->freeze ? 0 : c->k.max_inserts;
         while (ls->n_free < pool_target) {
             int slot = -1;
             uint64_t best = U64MAX;
@@ -356,6 +398,15 @@ void or_cache_step(or_cache *c) {
     }
 
     /* 4) flush_tables: one batched write of every dirty layer */
+    flush_tables(c);
+
+    /* 5) heat file every 512 steps (not while frozen), then the map frame */
+    if (!c->freeze && c->heat_path && c->n_steps % 512 == 0) save_heat(c);
+    map_frame(c);
+    if (c->route) fflush(c->route);
+}
+
+static void flush_tables(or_cache *c) {
     if (c->k.batch_tables) {
         int any = 0;
         for (int li = 0; li < c->n_layers; ++li) {
@@ -365,10 +416,111 @@ void or_cache_step(or_cache *c) {
     } else {
         for (int li = 0; li < c->n_layers; ++li) c->L[li].tbl_dirty = 0;
     }
-
-    map_frame(c);
-    if (c->route) fflush(c->route);
 }
+
+/* 0007:468-485: "moe-heat 1 <layers> <experts>", then "<il> <expert> <count>"
+ * for every non-zero count, written to <path>.tmp and renamed */
+static int save_heat(or_cache *c) {
+    const size_t n = strlen(c->heat_path);
+    char *tmp = (char *)malloc(n + 5);
+    memcpy(tmp, c->heat_path, n);
+    memcpy(tmp + n, ".tmp", 5);
+    FILE *f = fopen(tmp, "w");
+    int ok = f != NULL;
+    if (f) {
+        fprintf(f, "moe-heat 1 %d %d\n", c->n_layers, c->E);
+        for (int l = 0; l < c->n_layers; ++l)
+            for (int e = 0; e < c->E; ++e)
+                if (c->L[l].use_count[e]) fprintf(f, "%d %d %u\n", c->L[l].il, e, c->L[l].use_count[e]);
+        ok = fclose(f) == 0 && rename(tmp, c->heat_path) == 0;
+    }
+    free(tmp);
+    return ok ? 0 : -1;
+}
+
+int or_cache_heat_file(or_cache *c, const char *path, long long *n_records, long long *n_placed) {
+    long long n_rec = 0, placed = 0;
+    free(c->heat_path);
+    c->heat_path = (char *)malloc(strlen(path) + 1);
+    memcpy(c->heat_path, path, strlen(path) + 1);
+    for (int l = 0; l < c->n_layers; ++l) {
+        free(c->L[l].use_count);
+        c->L[l].use_count = (uint32_t *)calloc((size_t)c->E, sizeof(uint32_t));
+    }
+    /* 0007:434-466: load, refusing another model's dimensions; counts halved */
+    FILE *f = fopen(path, "r");
+    if (f) {
+        int ver = 0, nl = 0, ne = 0;
+        if (fscanf(f, "moe-heat %d %d %d", &ver, &nl, &ne) == 3 && ver == 1 && nl == c->n_layers && ne == c->E) {
+            int il = 0, e = 0;
+            unsigned cnt = 0;
+            while (fscanf(f, "%d %d %u", &il, &e, &cnt) == 3) {
+                if (il < 0 || il >= c->n_layers || e < 0 || e >= c->E) continue;
+                c->L[il].use_count[e] = cnt / 2;
+                n_rec++;
+            }
+        }
+        fclose(f);
+    }
+    /* 0007:576-611: hottest first into slots 0.., a reserve left for early issue */
+    if (n_rec > 0) {
+        const int reserve = c->k.early_issue ? (c->freeze ? 0 : c->k.max_inserts) : 0;
+        int32_t *order = (int32_t *)malloc(sizeof(int32_t) * (size_t)c->E);
+        for (int l = 0; l < c->n_layers; ++l) {
+            layer_t *ls = &c->L[l];
+            for (int e = 0; e < ls->E; ++e) order[e] = e;
+            for (int i = 1; i < ls->E; ++i) {             /* stable insertion sort, count descending */
+                const int32_t v = order[i];
+                int j = i - 1;
+                while (j >= 0 && ls->use_count[order[j]] < ls->use_count[v]) { order[j + 1] = order[j]; --j; }
+                order[j + 1] = v;
+            }
+            const int fill = ls->S - reserve > 0 ? ls->S - reserve : 0;
+            int slot = 0;
+            for (int k = 0; k < ls->E && slot < fill; ++k) {
+                const int e = order[k];
+                if (ls->use_count[e] == 0) break;
+                ls->slot_expert[slot] = e;
+                ls->expert_slot[e] = slot;
+                ls->slot_last_use[slot] = (uint64_t)(fill - slot);
+                set_table_entry(c, ls, e, slot);
+                ++slot;
+                ++placed;
+            }
+            if ((uint64_t)fill > c->clock) c->clock = (uint64_t)fill;
+            ls->n_free = 0;
+            for (int s = ls->S - 1; s >= slot; --s) ls->free_slots[ls->n_free++] = s;
+        }
+        free(order);
+        flush_tables(c);
+    }
+    if (n_records) *n_records = n_rec;
+    if (n_placed) *n_placed = placed;
+    return 0;
+}
+
+void or_cache_freeze(or_cache *c) {
+    c->freeze = 1;
+    c->k.max_inserts = 0;
+}
+
+int or_cache_map_replay(or_cache *c, const char *path) {
+    FILE *f = fopen(path, "r");
+    if (!f) return -1;
+    int ver = 0, nl = 0;
+    int ok = fscanf(f, "moe-map %d %d", &ver, &nl) == 2 && ver == 1 && nl == c->n_layers;
+    for (int l = 0; ok && l < c->n_layers; ++l) {
+        int il = -1, s = 0, e = 0;
+        ok = fscanf(f, " layer %d %d %d", &il, &s, &e) == 3 && il == c->L[l].il && s == c->L[l].S && e == c->L[l].E;
+    }
+    if (!ok) { fclose(f); return -1; }
+    c->replay = f;
+    or_cache_freeze(c);
+    map_frame(c);                   /* the frame of step 0, as at init (0008:571) */
+    return c->replay_err ? -1 : 0;
+}
+
+int or_cache_replay_error(const or_cache *c) { return c->replay_err; }
 
 void or_cache_hold_job(or_cache *c, int layer, int expert, int slot, uint64_t sched_step) {
     c->holds = (job_t *)realloc(c->holds, sizeof(job_t) * (size_t)(c->n_holds + 1));

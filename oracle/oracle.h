@@ -166,6 +166,19 @@ void      or_cache_frame(const or_cache *c, int layer, int32_t *out);
 /* table mirror (expert -> slot or dummy) and prior mirror of a layer */
 void      or_cache_table(const or_cache *c, int layer, int32_t *tbl, float *prior);
 void      or_cache_stats(const or_cache *c, or_stats *s);
+/* heat file (0007:431-485, warm start 0007:568-621, save 0007:745-752): counts of
+ * every observed id, saved every 512 steps; on load halved, and the hottest
+ * experts placed in slots 0.. before the first token.  Returns 0 (records and
+ * placed experts in *n_records, *n_placed), -1 when the file cannot be used
+ * (a refused header counts as zero records, as in the reference). */
+int       or_cache_heat_file(or_cache *c, const char *path, long long *n_records, long long *n_placed);
+/* LLAMA_MOE_CACHE_FREEZE (0008:825-832): no uploads from now on */
+void      or_cache_freeze(or_cache *c);
+/* LLAMA_MOE_MAP_REPLAY (0008:436-474, 559-565): force every step's recorded
+ * placement; freezes the cache.  Returns 0, or -1 for a header that does not
+ * match; or_cache_replay_error() != 0 once a frame was missing or malformed. */
+int       or_cache_map_replay(or_cache *c, const char *path);
+int       or_cache_replay_error(const or_cache *c);
 
 #ifdef __cplusplus
 }

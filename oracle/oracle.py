@@ -91,6 +91,11 @@ def _declare(L):
     d("or_cache_frame", None, P, ctypes.c_int, P)
     d("or_cache_table", None, P, ctypes.c_int, P, P)
     d("or_cache_stats", None, P, ctypes.POINTER(Stats))
+    d("or_cache_heat_file", ctypes.c_int, P, ctypes.c_char_p, ctypes.POINTER(ctypes.c_longlong),
+      ctypes.POINTER(ctypes.c_longlong))
+    d("or_cache_freeze", None, P)
+    d("or_cache_map_replay", ctypes.c_int, P, ctypes.c_char_p)
+    d("or_cache_replay_error", ctypes.c_int, P)
 
 
 def _p(a):
@@ -262,6 +267,23 @@ class Cache:
 
     def step(self):
         lib().or_cache_step(self.h)
+
+    def heat_file(self, path):
+        """LLAMA_MOE_HEAT_FILE: returns (records loaded, experts placed)."""
+        nr, npl = ctypes.c_longlong(), ctypes.c_longlong()
+        if lib().or_cache_heat_file(self.h, path.encode(), ctypes.byref(nr), ctypes.byref(npl)) != 0:
+            raise OSError(path)
+        return nr.value, npl.value
+
+    def freeze(self):
+        lib().or_cache_freeze(self.h)
+
+    def map_replay(self, path):
+        if lib().or_cache_map_replay(self.h, path.encode()) != 0:
+            raise ValueError(f"map replay refused: {path}")
+
+    def replay_error(self):
+        return lib().or_cache_replay_error(self.h)
 
     def hold_job(self, layer, expert, slot, sched_step):
         lib().or_cache_hold_job(self.h, layer, expert, slot, sched_step)

@@ -21,11 +21,11 @@ pytestmark = pytest.mark.gpu
 Q4, Q6 = _lib.TYPE_Q4K, _lib.TYPE_Q6K
 
 
-def check_run(rig, tmp_path, out_every=1, tol=1e-3):
-    rp, mp = str(tmp_path / "gpu.routes"), str(tmp_path / "gpu.map")
-    orp, omp = str(tmp_path / "ora.routes"), str(tmp_path / "ora.map")
+def check_run(rig, tmp_path, out_every=1, tol=1e-3, oc=None, record_map=True):
+    rp, mp = str(tmp_path / "gpu.routes"), str(tmp_path / "gpu.map") if record_map else None
+    orp, omp = str(tmp_path / "ora.routes"), str(tmp_path / "ora.map") if record_map else None
     rig.cache.trace_open(rp, mp)
-    oc = rig.oracle_cache()
+    oc = rig.oracle_cache() if oc is None else oc
     oc.trace_open(orp, omp)
     keep = set(range(0, rig.T, out_every))
     ids_all, outs, frames = rig.run(keep_out=keep)
@@ -50,7 +50,8 @@ def check_run(rig, tmp_path, out_every=1, tol=1e-3):
     rig.cache.close()
     oc.close()
     assert open(rp).read() == open(orp).read()
-    assert open(mp).read() == open(omp).read()
+    if record_map:
+        assert open(mp).read() == open(omp).read()
     return worst
 
 
@@ -226,6 +227,49 @@ def test_sidecar_counts_cpu_served():
         rig.cache.set_decode_path(split=1)
     finally:
         rig.close()
+
+
+def test_heat_warm_start_and_map_replay_on_gpu(tmp_path):
+    # a heat file places the hottest experts' bytes in their slots before the
+    # first token; the decode that follows matches an oracle warm-started from
+    # the same file.  Its recorded placement map, replayed on a fresh cache,
+    # puts the same experts in the same slots step by step (bytes copied from
+    # the store), and the decode under replay matches the oracle's replay.
+    E = 128
+    rng = np.random.default_rng(21)
+    heat = tmp_path / "warm.heat"
+    lines = [f"moe-heat 1 2 {E}"]
+    for l in range(2):
+        for e in sorted(rng.choice(E, 50, replace=False)):
+            lines.append(f"{l} {e} {int(rng.integers(1, 30))}")
+    heat.write_text("\n".join(lines) + "\n")
+    slots = [16, 24]
+    rig = Rig(slots, [Q4, Q6], T=24, admit="window", batch_tables=True)
+    try:
+        n_rec, n_placed = rig.cache.heat_file(str(heat))
+        assert n_rec == 100 and n_placed > 0
+        for l in range(2):
+            v, eb = rig.cache.lookup(l), rig.eb[l]
+            back = np.empty(eb, np.uint8)
+            for s, e in enumerate(rig.cache.frame(l)):
+                if e >= 0:
+                    assert L().moe_memcpy(back.ctypes.data, v.slot_pool + s * v.slot_bytes, eb) == 0
+                    assert np.array_equal(back, rig.stores[l].arr[e * eb:(e + 1) * eb]), (l, s, e)
+        oc = rig.oracle_cache()
+        assert oc.heat_file(str(heat)) == (n_rec, n_placed)
+        check_run(rig, tmp_path, oc=oc)
+    finally:
+        rig.close()
+    rec = str(tmp_path / "gpu.map")
+    rig2 = Rig(slots, [Q4, Q6], T=24, admit="window", batch_tables=True)
+    try:
+        rig2.cache.map_replay(rec)
+        assert rig2.cache.requires_sync()          # replay overwrites slots: sync before the step
+        oc2 = rig2.oracle_cache()
+        oc2.map_replay(rec)
+        check_run(rig2, tmp_path, oc=oc2, record_map=False)
+    finally:
+        rig2.close()
 
 
 def test_decode_48_layers_full_shape(tmp_path):
