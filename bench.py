@@ -294,6 +294,30 @@ class Workload:
         self.stores = []
 
 
+def size_matched(roof, iters=50):
+    """The same bytes per launch read by a plain streaming-read kernel, each
+    launch from a fresh window of a 4 GiB buffer, timed the same way: the
+    ceiling a kernel of this size can reach on this GPU."""
+    import ctypes
+    import torch
+    import moe_prefetch
+    from moe_prefetch import _lib
+    L = moe_prefetch.lib()
+    buf = torch.empty(4 << 30, dtype=torch.uint8, device="cuda:0")
+    buf.fill_(1)
+    us = ctypes.c_double()
+    b = int(roof["bytes_per_launch"])
+    _lib.check(L.moe_probe_stream_read(buf.data_ptr(), buf.numel(), b, iters, ctypes.byref(us),
+                                       torch.cuda.current_stream().cuda_stream), "probe")
+    del buf
+    torch.cuda.synchronize()
+    gbs = b / (us.value * 1e-6) / 1e9
+    return {"bytes": b, "avg_launch_us": round(us.value, 2), "gbs": round(gbs, 1),
+            "frac": round(roof["achieved"] / gbs, 4),
+            "what": "plain streaming-read kernel (8 x 16 B loads in flight per thread) over the same bytes, a cold "
+                    "window per launch, dispatch-stamped events"}
+
+
 def cache_summary(s0, s1, steps):
     seen = (s1["n_hit"] - s0["n_hit"]) + (s1["n_miss"] - s0["n_miss"])
     return {"hit_rate": round((s1["n_hit"] - s0["n_hit"]) / max(seen, 1), 4),
@@ -398,6 +422,7 @@ def run_stacked(args, wl):
         "sidecar": sidecar_report(args, s0, s1, args.steps, cache.sidecar_log() if args.sidecar > 0 else None),
     }
     result.update(kernel_report(*wl.kernel_pass(cache), args.steps, s0, s1))
+    result["roofline"]["size_matched"] = size_matched(result["roofline"])
     if not args.no_check:
         log("[bench] checking the full-size run against the oracle (outside the timed region)")
         result["check"] = wl.check(ids_log, kept, frames, s1, knobs)
@@ -494,6 +519,7 @@ def run_wide(args, wl):
                               "step per batch (batch buffers allocated in the first call)"},
     }
     result.update(kernel_report(*wl.kernel_pass(cache), args.steps, s0, s1))
+    result["roofline"]["size_matched"] = size_matched(result["roofline"])
     if not args.no_check:
         log("[bench] replaying every routed id of both phases through the oracle (outside the timed region)")
         result["check"] = wl.check(ids_log, kept, frames, s3, knobs, every=True, batch=B)
@@ -626,6 +652,7 @@ def run_prefill(args):
         "hbm": {"gateup_gbs": round(gu_gbs, 1), "down_gbs": round(dn_gbs, 1),
                 "experts_touched_per_layer": round(touched / NL, 1), "pairs_per_layer": pairs // NL},
     }
+    result["roofline"]["size_matched"] = size_matched(result["roofline"], iters=10)
     if not args.no_check:
         from oracle import oracle as O
         log("[bench] checking routing and dispatch of every layer, outputs of two layers, against the oracle")

@@ -102,6 +102,12 @@ int moe_synth_experts_host(uint64_t seed, int layer, int e0, int n, int H, int I
  *        2 router logits (a = token, b = layer): uniform on [0, sigma). */
 int moe_synth_vec(uint64_t seed, int kind, int a0, int na, int b0, int nb, int n, float sigma,
                   float *out_dev, void *stream);
+/* Measurement only (no counterpart in the reference): the average duration,
+ * from dispatch-stamped events, of a plain streaming-read kernel over `bytes`,
+ * each of `iters` launches reading a fresh window of the device buffer `buf`
+ * (cold for the caches when buf_bytes is well above 256 MiB). */
+int moe_probe_stream_read(const void *buf, size_t buf_bytes, size_t bytes, int iters, double *avg_us,
+                          void *stream);
 int moe_synth_vec_host(uint64_t seed, int kind, int a0, int na, int b0, int nb, int n, float sigma,
                        float *out_host);
 size_t moe_expert_bytes(int H, int I, int down_type);

@@ -147,6 +147,10 @@ hipError_t launch_gateup(const ExpertArgs &a, int src, hipStream_t st, hipEvent_
 hipError_t launch_down(const ExpertArgs &a, int src, hipStream_t st, hipEvent_t e0, hipEvent_t e1);
 hipError_t launch_synth_experts(uint64_t seed, int layer, int e0, int n_experts, int H, int I, int down_type,
                                 float sigma, uint8_t *out, uint64_t stride, hipStream_t st);
+// measurement: a streaming read of `bytes` (8 16-byte loads in flight per thread)
+hipError_t launch_stream_read(const void *p, uint64_t bytes, uint32_t *out, hipStream_t st, hipEvent_t e0,
+                              hipEvent_t e1);
+unsigned stream_read_blocks(uint64_t bytes);
 hipError_t launch_synth_vec(uint64_t seed, int kind, int a0, int na, int b0, int nb, int n, float sigma,
                             float *out, hipStream_t st);
 

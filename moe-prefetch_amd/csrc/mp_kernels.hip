@@ -616,6 +616,40 @@ hipError_t launch_experts(const ExpertArgs &a, hipStream_t st) {
     return e != hipSuccess ? e : launch_down(a, SRC_ALL, st, nullptr, nullptr);
 }
 
+// ---------------------------------------------------------------------------
+// streaming read, for the size-matched read ceiling the decode kernels are
+// compared with: each thread issues 8 independent 16-byte loads, xors them,
+// one word per workgroup
+constexpr int SR_U = 8;
+__global__ __launch_bounds__(256) void stream_read_kernel(const uint4 *__restrict__ p, uint64_t n16, uint32_t *out) {
+    const uint64_t base = (uint64_t)blockIdx.x * 256 * SR_U + threadIdx.x;
+    uint4 v[SR_U];
+#pragma unroll
+    for (int i = 0; i < SR_U; ++i) {
+        const uint64_t j = base + (uint64_t)i * 256;
+        v[i] = j < n16 ? p[j] : make_uint4(0, 0, 0, 0);
+    }
+    uint32_t a = 0;
+#pragma unroll
+    for (int i = 0; i < SR_U; ++i) a ^= v[i].x ^ v[i].y ^ v[i].z ^ v[i].w;
+    __shared__ uint32_t s[256];
+    s[threadIdx.x] = a;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        uint32_t t = 0;
+        for (int i = 0; i < 256; ++i) t ^= s[i];
+        out[blockIdx.x] = t;
+    }
+}
+
+unsigned stream_read_blocks(uint64_t bytes) { return (unsigned)((bytes / 16 + 256 * SR_U - 1) / (256 * SR_U)); }
+
+hipError_t launch_stream_read(const void *p, uint64_t bytes, uint32_t *out, hipStream_t st, hipEvent_t e0,
+                              hipEvent_t e1) {
+    return launch(stream_read_kernel, dim3(stream_read_blocks(bytes)), dim3(256), st, e0, e1, (const uint4 *)p,
+                  (uint64_t)(bytes / 16), out);
+}
+
 hipError_t launch_synth_experts(uint64_t seed, int layer, int e0, int n_experts, int H, int I, int down_type,
                                 float sigma, uint8_t *out, uint64_t stride, hipStream_t st) {
     const synth::ExpertShape sh{H, I, down_type};

@@ -819,6 +819,39 @@ int moe_synth_vec(uint64_t seed, int kind, int a0, int na, int b0, int nb, int n
     return MOE_OK;
 }
 
+int moe_probe_stream_read(const void *buf, size_t buf_bytes, size_t bytes, int iters, double *avg_us,
+                          void *stream) {
+    if (!buf || !avg_us || bytes < 16 || bytes > buf_bytes || iters < 1 || (uintptr_t)buf % 16)
+        return fail(MOE_ERR_ARG, "moe_probe_stream_read: bad arguments");
+    const hipStream_t st = (hipStream_t)stream;
+    uint32_t *out = nullptr;
+    hipEvent_t e0 = nullptr, e1 = nullptr;
+    if (hipMalloc(&out, (size_t)mp::stream_read_blocks(bytes) * 4) != hipSuccess)
+        return fail(MOE_ERR_NOMEM, "probe scratch");
+    const size_t step = (bytes + 4095) / 4096 * 4096;
+    double sum = 0.0;
+    int r = MOE_OK;
+    if (hipEventCreate(&e0) != hipSuccess || hipEventCreate(&e1) != hipSuccess) r = fail(MOE_ERR_HIP, "events");
+    size_t off = 0;
+    for (int i = 0; i < iters + 3 && r == MOE_OK; ++i) {   // 3 untimed; a fresh window each launch
+        if (off + bytes > buf_bytes) off = 0;
+        if (mp::launch_stream_read((const uint8_t *)buf + off, bytes, out, st, e0, e1) != hipSuccess ||
+            hipEventSynchronize(e1) != hipSuccess) {
+            r = fail(MOE_ERR_HIP, "stream read launch");
+            break;
+        }
+        float ms = 0.0f;
+        if (hipEventElapsedTime(&ms, e0, e1) != hipSuccess) r = fail(MOE_ERR_HIP, "event time");
+        if (i >= 3) sum += ms * 1e3;
+        off += step;
+    }
+    if (e0) hipEventDestroy(e0);
+    if (e1) hipEventDestroy(e1);
+    hipFree(out);
+    if (r == MOE_OK) *avg_us = sum / iters;
+    return r;
+}
+
 int moe_synth_vec_host(uint64_t seed, int kind, int a0, int na, int b0, int nb, int n, float sigma, float *out) {
     if (na <= 0 || nb <= 0 || n <= 0 || !out) return fail(MOE_ERR_ARG, "bad synth_vec arguments");
     size_t t = 0;

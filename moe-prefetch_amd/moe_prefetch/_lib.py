@@ -131,6 +131,7 @@ SIGNATURES = {
     "moe_cache_heat_file": (ctypes.c_int, [P, ctypes.c_char_p, ctypes.POINTER(ctypes.c_int64),
                                            ctypes.POINTER(ctypes.c_int64)]),
     "moe_cache_freeze": (ctypes.c_int, [P]),
+    "moe_probe_stream_read": (ctypes.c_int, [P, SZ, SZ, ctypes.c_int, ctypes.POINTER(ctypes.c_double), P]),
     "moe_cache_map_replay": (ctypes.c_int, [P, ctypes.c_char_p]),
     "moe_cache_kernel_times": (ctypes.c_int, [P, ctypes.POINTER(KernelTimes)]),
     "moe_decode_layer": (ctypes.c_int, [P, ctypes.c_int, P, P, P, P, P, P]),
