@@ -332,6 +332,21 @@ __device__ inline half8_t stage_frag(const AStage &st, int r, int off) {
 
 constexpr int G6_LDS = 64 * 3 * Q6K_BYTES;   // 64 Q6_K rows at K <= 768
 
+// Workgroup -> (row tile, expert).  Workgroups go to the 8 XCDs round-robin
+// (workgroup L on XCD L % 8); with E a multiple of 8, every row tile of
+// expert e lands on XCD e % 8, so the tiles of an expert share one L2 copy of
+// its activation rows instead of fetching them into all eight.
+__device__ inline void tile_expert(int L, int T, int E, int &tile, int &e) {
+    if (E % 8 == 0) {
+        const int j = L >> 3;
+        e = (L & 7) + 8 * (j / T);
+        tile = j % T;
+    } else {
+        e = L / T;
+        tile = L % T;
+    }
+}
+
 // The grouped product of one (64-row tile, expert): rows of the expert's
 // matrix (up and gate as one 2I-row matrix, or down) against the activation
 // rows of every pair dispatched to the expert, K = NB*256.  Workgroup = 4
@@ -344,13 +359,14 @@ constexpr int G6_LDS = 64 * 3 * Q6K_BYTES;   // 64 Q6_K rows at K <= 768
 // loads hide behind another's dequantization
 template <int NB, int DT, bool DOWN>
 __global__ __launch_bounds__(256, 4) void grouped_gemm_kernel(GroupedArgs a) {
-    const int e = blockIdx.y;
+    int e, tile;
+    tile_expert(blockIdx.x, (DOWN ? a.H : 2 * a.I) / 64, a.E, tile, e);
     const int n0 = a.offsets[e], ne = a.offsets[e + 1] - n0;
     if (ne <= 0) return;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int n = lane & 15, h = lane >> 4;
-    const int r0 = blockIdx.x * 64;
+    const int r0 = tile * 64;
     const int row = r0 + wave * 16 + n;
     constexpr int K = NB * QK;
     constexpr int ROWB = NB * (DT == TYPE_Q6K ? Q6K_BYTES : Q4K_BYTES);
@@ -567,22 +583,183 @@ hipError_t launch_swiglu_quant(const float *y2, int P, int I, float *h_out, uint
                     dx, bs16);
 }
 
+// ---------------------------------------------------------------------------
+// The Q4_K grouped product with the weights read and decoded once per chunk
+// of up to CH passes (CH * 32 pairs): for each super-block s, the lane's
+// weights are loaded once (block s+1 in flight meanwhile) and turned into the
+// eight MFMA B operands once, then every pass of the chunk multiplies its
+// staged activation rows by them.  Each pair still accumulates its
+// super-blocks in order 0, 1, ..., so the arithmetic is the one-pass kernel's.
+// CH = 2 for large batches, (256, 3): up to 168 registers, which the eight
+// operands of two passes need; CH = 1 when experts rarely get more than 32
+// pairs, (256, 4): four waves per SIMD.
+template <int NB, bool DOWN, int CH>
+__global__ __launch_bounds__(256, CH == 1 ? 4 : 3) void grouped_q4_kernel(GroupedArgs a) {
+    int e, tile;
+    tile_expert(blockIdx.x, (DOWN ? a.H : 2 * a.I) / 64, a.E, tile, e);
+    const int n0 = a.offsets[e], ne = a.offsets[e + 1] - n0;
+    if (ne <= 0) return;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int n = lane & 15, h = lane >> 4;
+    const int r0 = tile * 64;
+    const int row = r0 + wave * 16 + n;
+    constexpr int K = NB * QK;
+    constexpr int ROWB = NB * Q4K_BYTES;
+    const int out_n = DOWN ? a.H : 2 * a.I;
+    const uint8_t *base = grouped_expert(a, e);
+    if (!base) {
+        for (int i = tid; i < ne * 64; i += 256) {
+            const int pos = n0 + i / 64, c = r0 + (i % 64);
+            if (DOWN) a.ypair[(size_t)a.perm[pos] * a.H + c] = 0.0f;
+            else a.y2[(size_t)pos * out_n + c] = 0.0f;
+        }
+        return;
+    }
+    const uint8_t *mat = DOWN ? base + 2ull * a.I * (a.H / QK) * Q4K_BYTES : base;
+    const uint16_t *act = DOWN ? a.ha : a.xa;
+    const uint16_t *abs16 = DOWN ? a.hbs : a.xbs;
+    const float *adx = DOWN ? a.hdx : a.xdx;
+
+    __shared__ AStage st[2];
+    __shared__ int s_rows[CH * GT];
+    __shared__ float s_dx[CH * GT][NB];
+    const uint8_t *wrow = mat + (size_t)row * ROWB;
+    const int gm = (h >> 1) + 2 * (h & 1);
+
+    for (int cb = 0; cb < ne; cb += CH * GT) {
+        const int npc = min(CH * GT, ne - cb);
+        const int nps = (npc + GT - 1) / GT;
+        if (tid < CH * GT) {
+            const int pos = n0 + cb + min(tid, npc - 1);
+            s_rows[tid] = DOWN ? pos : a.perm[pos] / a.K;
+        }
+        __syncthreads();
+        for (int i = tid; i < CH * GT * NB; i += 256) s_dx[i / NB][i % NB] = adx[(size_t)s_rows[i / NB] * NB + (i % NB)];
+        stage_a(st[0], s_rows, min(GT, npc), act, abs16, K, 0, wave, lane);
+        uint4 cw[3], nw[3];
+        cw[0] = *(const uint4 *)wrow;
+        cw[1] = *(const uint4 *)(wrow + 16 + 16 * h);
+        cw[2] = *(const uint4 *)(wrow + 80 + 16 * h);
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+        float y[CH][2][4];
+#pragma unroll
+        for (int p = 0; p < CH; ++p)
+#pragma unroll
+            for (int t = 0; t < 2; ++t)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) y[p][t][i] = 0.0f;
+        int j = 0;                       // step j = s * nps + p
+#pragma unroll 1
+        for (int s = 0; s < NB; ++s) {
+            if (s + 1 < NB) {
+                const uint8_t *q = wrow + (s + 1) * Q4K_BYTES;
+                nw[0] = *(const uint4 *)q;
+                nw[1] = *(const uint4 *)(q + 16 + 16 * h);
+                nw[2] = *(const uint4 *)(q + 80 + 16 * h);
+            }
+            Q4Scales sc;
+            q4_scales(cw[0], h, sc);
+            half8_t b[CH > 1 ? 8 : 1];          // kept across the passes (one pass: built where used)
+            if constexpr (CH > 1) {
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    const int L = i >> 2, nib = (i >> 1) & 1;
+                    b[i] = q4_b(L ? cw[2] : cw[1], i, sc.sc[L][nib]);
+                }
+            }
+#pragma unroll
+            for (int p = 0; p < CH; ++p) {
+                if (p < nps) {
+                    const AStage &S = st[j & 1];
+                    const int jn = j + 1;
+                    if (jn < NB * nps) {
+                        const int s2 = jn / nps, p2 = jn - s2 * nps;
+                        stage_a(st[jn & 1], s_rows + p2 * GT, min(GT, npc - p2 * GT), act, abs16, K, s2, wave, lane);
+                    }
+                    float4_t acc[2] = {{0, 0, 0, 0}, {0, 0, 0, 0}};
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) {
+                        const int off = q4_a_offset(h, i);
+                        half8_t bi;
+                        if constexpr (CH > 1) {
+                            bi = b[i];
+                        } else {
+                            const int L = i >> 2, nib = (i >> 1) & 1;
+                            bi = q4_b(L ? cw[2] : cw[1], i, sc.sc[L][nib]);
+                        }
+#pragma unroll
+                        for (int t = 0; t < 2; ++t) acc[t] = mfma32(stage_frag(S, 16 * t + n, off), bi, acc[t]);
+                    }
+#pragma unroll
+                    for (int t = 0; t < 2; ++t) {
+                        const half4_t am = *(const half4_t *)&S.bs[16 * t + n][4 * gm];
+                        float4_t z = {0, 0, 0, 0};
+                        z = __builtin_amdgcn_mfma_f32_16x16x16f16(am, sc.bm, z, 0, 0, 0);
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) {
+                            // ggml's order: acc += (d*dx)*sumi; acc -= (dmin*dx)*summ
+                            const float dx = s_dx[p * GT + 16 * t + 4 * h + i][s];
+                            y[p][t][i] = y[p][t][i] + (sc.d * dx) * acc[t][i];
+                            y[p][t][i] = y[p][t][i] - (sc.dmin * dx) * z[i];
+                        }
+                    }
+                    __builtin_amdgcn_s_waitcnt(0);
+                    __syncthreads();
+                    ++j;
+                }
+            }
+            cw[0] = nw[0];
+            cw[1] = nw[1];
+            cw[2] = nw[2];
+        }
+#pragma unroll
+        for (int p = 0; p < CH; ++p) {
+#pragma unroll
+            for (int t = 0; t < 2; ++t) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int r = p * GT + 16 * t + 4 * h + i;
+                    if (r < npc) {
+                        const int pos = n0 + cb + r;
+                        if (DOWN) {
+                            const int pp = a.perm[pos];
+                            a.ypair[(size_t)pp * a.H + row] = a.w[pp] * y[p][t][i];
+                        } else {
+                            a.y2[(size_t)pos * out_n + row] = y[p][t][i];
+                        }
+                    }
+                }
+            }
+        }
+        __syncthreads();
+    }
+}
+
 template <bool DOWN>
 static hipError_t launch_gg(const GroupedArgs &a, hipStream_t st, hipEvent_t e0, hipEvent_t e1) {
     const int rows = DOWN ? a.H : 2 * a.I;
     const int nb = (DOWN ? a.I : a.H) / QK;
-    const dim3 grid((unsigned)(rows / 64), (unsigned)a.E), blk(256);
+    const dim3 grid((unsigned)(rows / 64 * a.E)), blk(256);     // (row tile, expert) from the linear id
+    const bool two = a.P > 16 * a.E;                            // many experts above 32 pairs
     if (DOWN) {
         if (a.down_type == TYPE_Q6K) {
             if (nb == 3) return launch_b(grouped_gemm_kernel<3, TYPE_Q6K, true>, grid, blk, st, e0, e1, a);
             if (nb == 2) return launch_b(grouped_gemm_kernel<2, TYPE_Q6K, true>, grid, blk, st, e0, e1, a);
             return launch_b(grouped_gemm_kernel<1, TYPE_Q6K, true>, grid, blk, st, e0, e1, a);
         }
-        if (nb == 3) return launch_b(grouped_gemm_kernel<3, TYPE_Q4K, true>, grid, blk, st, e0, e1, a);
-        if (nb == 2) return launch_b(grouped_gemm_kernel<2, TYPE_Q4K, true>, grid, blk, st, e0, e1, a);
-        return launch_b(grouped_gemm_kernel<1, TYPE_Q4K, true>, grid, blk, st, e0, e1, a);
+        if (two) {
+            if (nb == 3) return launch_b(grouped_q4_kernel<3, true, 2>, grid, blk, st, e0, e1, a);
+            if (nb == 2) return launch_b(grouped_q4_kernel<2, true, 2>, grid, blk, st, e0, e1, a);
+            return launch_b(grouped_q4_kernel<1, true, 2>, grid, blk, st, e0, e1, a);
+        }
+        if (nb == 3) return launch_b(grouped_q4_kernel<3, true, 1>, grid, blk, st, e0, e1, a);
+        if (nb == 2) return launch_b(grouped_q4_kernel<2, true, 1>, grid, blk, st, e0, e1, a);
+        return launch_b(grouped_q4_kernel<1, true, 1>, grid, blk, st, e0, e1, a);
     }
-    return launch_b(grouped_gemm_kernel<8, TYPE_Q4K, false>, grid, blk, st, e0, e1, a);
+    return two ? launch_b(grouped_q4_kernel<8, false, 2>, grid, blk, st, e0, e1, a)
+               : launch_b(grouped_q4_kernel<8, false, 1>, grid, blk, st, e0, e1, a);
 }
 
 hipError_t launch_gateup_grouped(const GroupedArgs &a, hipStream_t st, hipEvent_t e0, hipEvent_t e1) {

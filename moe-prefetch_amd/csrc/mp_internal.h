@@ -113,6 +113,7 @@ struct GroupedArgs {
     uint64_t expert_bytes;
     int n_store;
     int E, K, H, I, down_type;
+    int P;                      // pairs dispatched (n_tok * K): picks the pass chunking
     const uint16_t *xa;         // [n_tok][H] Q8_K values of x as fp16
     const float *xdx;           // [n_tok][H/256]
     const uint16_t *xbs;        // [n_tok][H/16] group sums as fp16

@@ -1761,6 +1761,7 @@ int moe_grouped_experts(const moe_grouped_desc *d, void *stream) {
     a.ha = (const uint16_t *)(ws + w.ha); a.hdx = (const float *)(ws + w.hdx); a.hbs = (const uint16_t *)(ws + w.hbs);
     a.ypair = d->pair_out ? d->pair_out : (float *)(ws + w.ypair);
     const int P = d->n_tok * d->K;
+    a.P = P;
     hipEvent_t ev[4] = {};
     const bool timed = d->kernel_ms != nullptr;
     if (timed)
@@ -1780,7 +1781,7 @@ int moe_grouped_experts(const moe_grouped_desc *d, void *stream) {
             sa.perm = (const int32_t *)(ws + w.sh_perm);
             sa.w = (const float *)(ws + w.sh_ones);
             sa.table = nullptr; sa.slot_pool = nullptr; sa.n_slots = 0;
-            sa.store = d->shared; sa.n_store = 1; sa.E = 1; sa.K = 1;
+            sa.store = d->shared; sa.n_store = 1; sa.E = 1; sa.K = 1; sa.P = d->n_tok;
             HIPCHK(mp::launch_iota(d->n_tok, (int32_t *)sa.offsets, (int32_t *)sa.perm, (float *)sa.w, st));
             HIPCHK(mp::launch_gateup_grouped(sa, st, nullptr, nullptr));
             HIPCHK(mp::launch_swiglu_quant(sa.y2, d->n_tok, d->I, nullptr, (uint16_t *)sa.ha, (float *)sa.hdx,
