@@ -136,18 +136,34 @@ class Workload:
                 c.set_shared(l, self.shared[l])
         return c
 
-    def decode(self, cache, keep=(), all_out=None):
+    def residual(self):
+        """Router inputs and norm weights of the residual-stream workload (the
+        lookahead workload): x [T][L][H], g [L][H] on the device."""
+        if getattr(self, "x_res", None) is None:
+            from moe_prefetch.workload import residual_stream
+            t0 = time.time()
+            self.x_res, self.g_res = residual_stream(self.args.seed, self.T, self.NL, self.torch, self.dev,
+                                                     self.stream)
+            self.torch.cuda.synchronize()
+            self.g_res_h = self.g_res.cpu().numpy()
+            log(f"[bench] residual stream of {self.T} tokens x {self.NL} layers in {time.time() - t0:.1f}s")
+        return self.x_res, self.g_res_h
+
+    def decode(self, cache, keep=(), all_out=None, x=None, steer=True):
         """Warm up, then time the rest of the sequence.  Returns (elapsed s, stats
-        before / after the timed tokens, ids [T][L][K], kept outputs, frames)."""
+        before / after the timed tokens, ids [T][L][K], kept outputs, frames).
+        x: other router inputs [T][L][H]; steer=False: no steering bias."""
         import numpy as np
         torch = self.torch
         out = torch.empty((self.NL, H), dtype=torch.float32, device=self.dev)
         ids_log = np.empty((self.T, self.NL, K), np.int32)     # batched tokens are filled in by decode_batches
         kept = {}
+        xs = self.x if x is None else x
+        bias = self.bias if steer else None
 
         def token(t):
             dst = all_out[t] if all_out is not None else out
-            cache.decode_token(self.x[t], dst, bias=None if self.bias is None else self.bias[t],
+            cache.decode_token(xs[t], dst, bias=None if bias is None else bias[t],
                                stream=self.stream, ids_out=ids_log[t])
             if t in keep:
                 kept[t] = dst.cpu().numpy().copy()
@@ -428,6 +444,8 @@ def run_stacked(args, wl):
         result["check"] = wl.check(ids_log, kept, frames, s1, knobs)
         log(f"[bench] check: {result['check']}")
     cache.close()
+    if not args.no_lookahead:
+        result["lookahead"] = lookahead_compare(args, wl)
     if args.sidecar > 0 and not args.no_gpu_only:
         log("[bench] the same decode with the GPU alone serving absent experts")
         c2 = wl.cache(**knobs)
@@ -439,6 +457,103 @@ def run_stacked(args, wl):
                               "path": "absent experts read by the kernels from the pinned store over PCIe, "
                                       "staged uploads"}
     return result
+
+
+def lookahead_compare(args, wl):
+    """Router lookahead + just-in-time streaming (LLAMA_MOE_STREAM) on the
+    residual-stream workload: the same decode with streaming on and off (CPU-
+    assisted serving and early issue in both), same stores and routers as
+    stacked48.  Returns the 'lookahead' object (stream-on tok/s and the
+    comparison, the mover's counters per token, what it achieved)."""
+    import numpy as np
+    x, g = wl.residual()
+    knobs = dict(admit=args.admit, early_issue=True)
+    runs = {}
+    T = args.warmup + args.steps
+    keep = {args.warmup, T - 1}
+    for on in (True, False):
+        c = wl.cache(**knobs)
+        for l in range(wl.NL):
+            c.set_norm(l, g[l])
+        c.set_decode_path(split=args.path, graph=True)
+        if args.sidecar > 0:
+            num, den = (int(v) for v in args.share.split("/"))
+            c.set_sidecar(max(1, args.sidecar - 1) if on else args.sidecar, (num, den))   # the mover takes a core
+        if on:
+            c.set_streaming(True, per_layer=args.stream_per_layer, reserve=args.stream_reserve, top_k=8,
+                            gbps=args.stream_gbps, chunk_kib=args.stream_chunk_kib)
+        log(f"[bench] lookahead: residual48 decode, streaming {'on' if on else 'off'}")
+        el, s0, s1, ids, kept, frames = wl.decode(c, keep=keep, x=x, steer=False)
+        ss = c.stream_stats() if on else None
+        runs[on] = (el, s0, s1, ids, kept, ss)
+        c.close()
+    el_on, s0, s1, ids_on, kept_on, ss = runs[True]
+    el_off, o0, o1, ids_off, kept_off, _ = runs[False]
+    steps = args.steps
+    check = {"ids_checked": 0, "ids_mismatched": 0, "outputs_checked": 0, "outputs_bit_exact": True}
+    if not args.no_check:
+        # the oracle on the kept tokens, every layer (outside the timed regions)
+        import ctypes
+        from oracle import oracle as O
+        Wh, xh = wl.W.cpu().numpy(), x.cpu().numpy()
+        stores = [np.ctypeslib.as_array((ctypes.c_uint8 * (wl.E * wl.eb[l])).from_address(wl.stores[l]))
+                  for l in range(wl.NL)]
+        for t in sorted(keep):
+            for l in range(wl.NL):
+                rids, rw, _, _ = O.route(Wh[l], xh[t, l], K)
+                check["ids_checked"] += 1
+                check["ids_mismatched"] += int(not np.array_equal(rids, ids_on[t, l]))
+                want = wl.oracle_layer(stores, l, rids, rw, xh[t, l], 8)
+                check["outputs_checked"] += 1
+                check["outputs_bit_exact"] &= bool(np.array_equal(kept_on[t][l], want))
+    per = {k: round(ss[k] / T, 3) for k in ("offered", "landed", "in_time", "late", "unused", "dropped_late",
+                                            "dropped_posted", "not_sent", "gpu_miss")}
+    served = ss["in_time"] / max(1, ss["in_time"] + ss["gpu_miss"])
+    res = {
+        "workload": f"residual48: stacked48's shape and stores ({args.layers} layers x {E} experts, {args.slots} "
+                    f"slots), routed by the routers on a synthetic residual stream (MU 1.2, RHO 0.7, BETA 0.975, "
+                    f"norm weights 1 + 0.1 N(0,1)); early issue, admission {args.admit}, "
+                    + ("CPU-assisted serving" if args.sidecar > 0 else "absent experts read by the GPU over PCIe"),
+        "value": round(steps / el_on, 2), "unit": "tok/s",
+        "stream_off": round(steps / el_off, 2),
+        "speedup": round(el_off / el_on, 4),
+        "ids_equal": bool((ids_on == ids_off).all()),
+        "outputs_equal": bool(all(np.array_equal(kept_on[t], kept_off[t]) for t in keep)),
+        "check": check,
+        "hit_rate_on": cache_summary(s0, s1, steps)["hit_rate"],
+        "hit_rate_off": cache_summary(o0, o1, steps)["hit_rate"],
+        "stream_per_token": per,
+        "served_from_vram": round(served, 4),
+        "landed_used_in_time": round(ss["in_time"] / max(1, ss["landed"]), 4),
+        "copied_mib_per_token": round(ss["bytes"] / T / 1048576, 2),
+        "lead_us_d1_d2": [round(v, 1) for v in ss["lead_us"]],
+        "tau_us": round(ss["tau_us"], 1),
+        "failed": int(ss["failed"]),
+        "knobs": {"per_layer": args.stream_per_layer, "reserve": args.stream_reserve, "top_k": 8,
+                  "gbps": args.stream_gbps, "chunk_kib": args.stream_chunk_kib,
+                  "sidecar_threads_on_off": [max(1, args.sidecar - 1) if args.sidecar > 0 else 0, args.sidecar]},
+    }
+    log(f"[bench] lookahead: {res['value']} tok/s on, {res['stream_off']} off; served from VRAM "
+        f"{res['served_from_vram']}, landed used {res['landed_used_in_time']}")
+    return res
+
+
+def run_residual(args, wl):
+    """The lookahead workload as the line's own metric: residual48 with
+    streaming on, with the comparison against streaming off."""
+    la = lookahead_compare(args, wl)
+    wl.x = wl.x_res                     # the CPU baseline routes the same inputs
+    T = args.warmup + args.steps
+    return {
+        "metric": "MoE decode tok/s @bs1 (48 layers, 56 slots), router lookahead + just-in-time streaming",
+        "value": la["value"], "unit": "tok/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(1e3 / la["value"], 4), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "q4_k/q6_k x q8_k int8-dot, fp32 scale (router fp32)",
+        "data": "synthetic (seeded N(0,0.02) experts quantized to Q4_K/Q6_K, residual-stream router inputs)",
+        "config": {"workload": la["workload"] + f", {T} tokens ({args.warmup} warmup)", "batch": 1,
+                   "layers": args.layers, "slots": args.slots},
+        "lookahead": la,
+    }
 
 
 def run_prior(args, wl):
@@ -708,7 +823,8 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=None, help="timed batch-1 tokens (448; wide40: 960)")
     ap.add_argument("--warmup", type=int, default=64)
-    ap.add_argument("--workload", default="stacked48", choices=["stacked48", "prior48", "prefill48", "wide40"])
+    ap.add_argument("--workload", default="stacked48",
+                    choices=["stacked48", "prior48", "prefill48", "wide40", "residual48"])
     ap.add_argument("--batch", type=int, default=None, help="tokens per chunk (prefill48: 512) or per batched "
                                                             "decode step (wide40: 16)")
     ap.add_argument("--batch-tokens", type=int, default=128, help="wide40: tokens decoded in batches")
@@ -728,6 +844,11 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-gpu-only", action="store_true", help="skip the GPU-only decode beside the default one")
     ap.add_argument("--no-check", action="store_true")
+    ap.add_argument("--no-lookahead", action="store_true", help="skip the residual48 streaming comparison")
+    ap.add_argument("--stream-per-layer", type=int, default=4)
+    ap.add_argument("--stream-reserve", type=int, default=2)
+    ap.add_argument("--stream-gbps", type=float, default=45.7)
+    ap.add_argument("--stream-chunk-kib", type=int, default=0, help="0: a whole expert per copy")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -757,6 +878,9 @@ def main():
         wl = Workload(args, steer=True, n_experts=256, inter=512, shared=True, zipf_s=1.0, reuse=0.5,
                       batch_tokens=args.batch_tokens)
         result = run_wide(args, wl)
+    elif args.workload == "residual48":
+        wl = Workload(args, steer=False)
+        result = run_residual(args, wl)
     else:
         wl = Workload(args, steer=args.workload == "stacked48")
         result = run_stacked(args, wl) if args.workload == "stacked48" else run_prior(args, wl)

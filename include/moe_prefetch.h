@@ -259,6 +259,112 @@ int moe_cache_freeze(moe_cache *c);
  * record.  A step whose frame is missing fails. */
 int moe_cache_map_replay(moe_cache *c, const char *path);
 
+/* ---- router lookahead and just-in-time streaming ---------------------------
+ * LLAMA_MOE_STREAM (patches/0010-team-and-streaming.patch:957-1021 state,
+ * 1096-1129 map record, 1183-1210 accounting, 1466-1760 take/reap/issue/
+ * loop/adopt, 1671-1790 init).  Layer L's router launch also scores the
+ * routers of layers L+1 and L+2 on L's input rescaled by g_T / g_L (which is
+ * rmsnorm(residual_L) * g_T) and posts, per target, its top-k experts whose
+ * table word is the dummy.  A host mover thread turns them into copies on its
+ * own stream, earliest deadline first in 512 KiB chunks, dropping what would
+ * land after the target reads its table; after an expert's last chunk it
+ * writes the expert's table word (slot | STREAM_BIT) on the same stream.  The
+ * GPU's kernels read the table at system scope and posts say which slot each
+ * routed expert was read from, so an expert that landed in time is a hit of
+ * this very token.  At the boundary the landed experts join the cache (routed
+ * ones as recently used, the others as the first to go) and every word is
+ * rewritten without the bit.  Batch-1 decode only. */
+typedef struct {
+    int32_t on;                /* 0 off, 1 on */
+    int32_t per_layer;         /* LLAMA_MOE_STREAM_PER_LAYER, default 4: streamed experts per layer per token */
+    int32_t reserve;           /* LLAMA_MOE_STREAM_RESERVE, default 2: extra free slots kept per layer */
+    int32_t top_k;             /* LLAMA_MOE_STREAM_TOPK, default 8 (<= 8): candidates scored per target */
+    double gbps;               /* LLAMA_MOE_STREAM_GBPS, default 45.7: the copy engine's rate for deadlines */
+    int32_t chunk_kib;         /* LLAMA_MOE_STREAM_CHUNK_KIB (this build's): largest copy per push; 0 (default):
+                                  a whole expert per push (the reference used 512 KiB) */
+} moe_stream_config;
+
+typedef struct {
+    uint64_t records, offered, landed, in_time, late, unused, dropped_late, dropped_posted, not_sent,
+             gpu_miss, bytes;
+    double lead_us[3];         /* mean time from a prediction d layers ahead to its target's table read, d = 1, 2 */
+    uint64_t lead_n[3];
+    double tau_us;             /* the running estimate of GPU time per layer */
+    int32_t failed;            /* a copy or channel error stopped streaming for this cache */
+} moe_stream_stats;
+
+/* The RMS-norm weight g_L [H] (host, copied) that produced layer L's router
+ * input; the lookahead of L onto T uses g_T / g_L (a zero weight skips the
+ * pair).  Set for every layer before moe_cache_set_streaming. */
+int moe_cache_set_norm(moe_cache *c, int layer, const float *g_host, int n);
+/* Needs early issue, no deterministic publication, replay or freeze, and no
+ * open map record (the stream's map frames are written one step late); on a
+ * live cache also the routers and norm weights of every layer.  On a host-only
+ * cache (device < 0) it turns on the bookkeeping for the scripted calls below. */
+int moe_cache_set_streaming(moe_cache *c, const moe_stream_config *cfg);
+int moe_cache_stream_stats(moe_cache *c, moe_stream_stats *out);
+/* Batch-1 observation with the slots the GPU read (n_slots = absent): the
+ * route trace prints those slots, and streamed experts count as in time (the
+ * GPU read their slot) or late.  The batch-1 decode uses it internally. */
+int moe_cache_observe_gpu(moe_cache *c, int layer, const int32_t *ids, const int32_t *gpu_slots, int n_ids);
+/* Scripted streaming on a host-only cache, the mover's steps one by one:
+ * take one lookahead record of source `layer` (targets[2], n[2], ids[2][8])
+ * at host time now_ns and GPU time t_ns, each job an expert of expert_bytes
+ * (returns jobs created); posted: `layer` read its table; next: the next chunk
+ * with the copy engine free at free_at_ns and jobs beyond hold_after held
+ * (hold_after < 0: none) -- returns 1 and the chunk, 0 when none; land: the
+ * job's last chunk and table word arrived; job: slot (and target layer,
+ * expert) of a job, < 0 when none. */
+typedef struct {
+    int32_t job;
+    uint64_t offset, len;
+    int32_t last;
+} moe_stream_chunk;
+int moe_cache_stream_take(moe_cache *c, int layer, const int32_t *targets, const int32_t *n, const int32_t *ids,
+                          uint64_t now_ns, uint64_t t_ns, uint64_t expert_bytes);
+int moe_cache_stream_posted(moe_cache *c, int layer);
+int moe_cache_stream_next(moe_cache *c, uint64_t free_at_ns, int hold_after, moe_stream_chunk *out);
+int moe_cache_stream_land(moe_cache *c, int job);
+int moe_cache_stream_job(moe_cache *c, int job, int32_t *layer, int32_t *expert);
+
+/* The lookahead alone (k_moe_ahead_scores/_post, patches/0010:382-474), for
+ * checking: runs the batch-1 router of d (n_tok 1) with n_targets (1..2)
+ * target routers W[t] [E][H] (device), ratios r[t] [H] (device) and tables
+ * tbl[t] [E] (device, dummy[t] = absent), and writes the record: out_n[t] and
+ * out_ids[t][0..n-1] (host, int32 [2] and [2][8]), the top_k experts of
+ * W[t] . (x * r[t]) with the dummy table word, best first, lower id on a tie.
+ * Synchronous. */
+typedef struct {
+    int32_t n_targets, top_k;
+    const float *W[2];
+    const float *r[2];
+    const int32_t *tbl[2];
+    int32_t dummy[2];
+} moe_ahead_desc;
+int moe_route_ahead(const moe_route_desc *d, const moe_ahead_desc *a, int32_t *out_n, int32_t *out_ids,
+                    void *stream);
+
+/* The copy planner of the mover (moe_planner, patches/0010:777-909), exported
+ * so that its decisions can be checked: offer returns a job id or -1; next
+ * returns 1 and a chunk, or 0; get fills target, expert, bytes, sent,
+ * deadline, dropped, drop reason (0 none, 1 late, 2 layer posted);
+ * counters: offered, duplicates, dropped late, dropped posted. */
+typedef struct moe_planner moe_planner;
+typedef struct {
+    int32_t target, expert;
+    uint64_t bytes, sent, deadline_ns;
+    int32_t dropped, drop;
+} moe_planner_job;
+moe_planner *moe_planner_create(uint64_t chunk_bytes);
+void moe_planner_destroy(moe_planner *p);
+void moe_planner_reset(moe_planner *p);
+int moe_planner_offer(moe_planner *p, int target, int32_t expert, uint64_t bytes, uint64_t deadline_ns);
+void moe_planner_posted(moe_planner *p, int target);
+int moe_planner_next(moe_planner *p, uint64_t free_at_ns, double bytes_per_ns, int hold_after, moe_stream_chunk *out);
+int moe_planner_size(const moe_planner *p);
+int moe_planner_get(const moe_planner *p, int id, moe_planner_job *out);
+void moe_planner_counters(const moe_planner *p, uint64_t out[4]);
+
 /* Kernel time of the decode, from HIP events recorded around each launch on
  * the stream it runs on (off by default; set before decoding).  Experts
  * resident in HBM slots and experts read from the pinned store run as

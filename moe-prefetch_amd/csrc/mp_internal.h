@@ -17,6 +17,7 @@ struct alignas(256) SidecarPost {
     uint32_t seq;
     uint32_t pad0[31];
     int32_t ids[16];
+    int32_t slots[16];                         // the slot the GPU read for each id (n_slots = absent)
     uint8_t q8x[SC_Q8X_BYTES];
 };
 struct alignas(128) SidecarResp {
@@ -26,6 +27,28 @@ struct alignas(128) SidecarResp {
     uint32_t pad1[15];
 };
 constexpr uint32_t SC_ABORT = 0xffffffffu;
+
+// Just-in-time streaming.  A table word written in the middle of a token
+// carries STREAM_BIT next to the slot: the expert's bytes were copied into
+// the slot by the host's copy stream while the token ran, and kernels that
+// read that slot first invalidate their caches (agent-scope acquire).  The
+// boundary's table flush rewrites every such word without the bit.
+constexpr int32_t STREAM_BIT = 0x40000000;
+constexpr int32_t SLOT_MASK = 0x0fffffff;
+constexpr int AHEAD_K = 8;                     // candidates per target layer at most
+
+// Router lookahead record: layer L's router launch scores the routers of
+// layers L+1 and L+2 on L's input (x * g_T / g_L) and posts, per target, the
+// experts of its top-k whose table word is the dummy, best first.  seq last
+// (system-scope release).  t: the GPU's 100 MHz wall clock at the post.
+struct alignas(256) AheadPost {
+    uint32_t seq;
+    uint32_t layer;
+    uint32_t t_lo, t_hi;
+    int32_t target[2];                         // -1: none
+    int32_t n[2];
+    int32_t ids[2][AHEAD_K];
+};
 
 struct RouteLaunch {
     const float *W;        // [E][H] f32
@@ -46,6 +69,18 @@ struct RouteLaunch {
     uint8_t *q8x;          // out [n_tok][H/256][292]
     SidecarPost *post;     // batch-1 decode with CPU-assisted serving: post ids + Q8_K(x), or null
     const uint32_t *seq;   // device: the token's sequence number
+    // router lookahead (batch 1, router GEMV path): an > 0 target layers
+    int an, ak;            // targets (0..2), candidates kept per target (<= AHEAD_K)
+    const float *aW[2];    // [E][H] f32 routers of the targets
+    const float *ar[2];    // [H] g_target / g_this
+    const int32_t *atbl[2];
+    int32_t adummy[2];
+    int32_t atarget[2];
+    int32_t alayer;
+    float *alog;           // scratch [2][E]
+    AheadPost *apost;      // the record (mapped host memory, or device memory for a test)
+    uint32_t *fresh;       // non-null: read the table at system scope (words may flip in the middle
+                           // of the token) and set *fresh when a word carries STREAM_BIT
 };
 
 struct ExpertArgs {
@@ -78,6 +113,8 @@ struct ExpertArgs {
     int n_shared;             // 1 with a shared expert
     int cpu_num, cpu_den;     // CPU-assisted serving (den > 0): the CPU computes absent expert k when
                               // its rank among the absent ones (k order) r has r % den < num
+    const uint32_t *fresh;    // non-null and set: a slot of this layer was filled by the copy stream
+                              // during the token; invalidate caches before reading weights
 };
 
 // batch-1 combine after CPU-assisted serving: waits (bounded) for the host's

@@ -65,18 +65,47 @@ struct RouteArgs {
     uint8_t *q8x;          // [n_tok][H/256 * 292]
     SidecarPost *post;     // batch 1 with CPU-assisted serving, or null
     const uint32_t *seq;
+    int an, ak;            // router lookahead: target layers (0..2), candidates per target
+    const float *aW[2];
+    const float *ar[2];
+    const int32_t *atbl[2];
+    int32_t adummy[2], atarget[2], alayer;
+    float *alog;           // [2][E]
+    AheadPost *apost;
+    uint32_t *fresh;       // table words may flip during the token (see STREAM_BIT)
 };
 
 // One wavefront per expert row: logit[e] = <W[e], x> in the canonical order
 // (lane j accumulates W[256 i + 4 j + c] * x[...] with fmaf, i then c, then a
 // butterfly over the 64 lanes), plus the steering bias when given.  The first
-// H/256 workgroups also write the Q8_K blocks of x.
+// H/256 workgroups also write the Q8_K blocks of x.  With router lookahead
+// (batch 1) E/4 more workgroups per target layer T score T's router on the
+// products x[i] * r_T[i] (rounded to f32) in the same order.
 __global__ __launch_bounds__(256) void route_logits_kernel(RouteArgs a) {
     const int tok = blockIdx.y;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int e = blockIdx.x * 4 + wave;
+    const int per = (a.E + 3) / 4;
+    const int t = (int)blockIdx.x / per;             // 0: this layer, 1..an: lookahead target t - 1
+    const int e = ((int)blockIdx.x - t * per) * 4 + wave;
     const float *x = a.x + (size_t)tok * a.H;
     if (e >= a.E) return;
+    if (t > 0) {
+        const float *w = a.aW[t - 1] + (size_t)e * a.H;
+        const float *r = a.ar[t - 1];
+        float acc = 0.0f;
+        for (int i = 0; i < a.H / 256; ++i) {
+            const float4 wv = *(const float4 *)(w + 256 * i + 4 * lane);
+            const float4 xv = *(const float4 *)(x + 256 * i + 4 * lane);
+            const float4 rv = *(const float4 *)(r + 256 * i + 4 * lane);
+            acc = fmaf(wv.x, xv.x * rv.x, acc);
+            acc = fmaf(wv.y, xv.y * rv.y, acc);
+            acc = fmaf(wv.z, xv.z * rv.z, acc);
+            acc = fmaf(wv.w, xv.w * rv.w, acc);
+        }
+        acc = bfly_add(acc);
+        if (lane == 0) a.alog[(size_t)(t - 1) * a.E + e] = acc;
+        return;
+    }
     const float *w = a.W + (size_t)e * a.H;
     float acc = 0.0f;
     for (int i = 0; i < a.H / 256; ++i) {
@@ -95,6 +124,61 @@ __global__ __launch_bounds__(256) void route_logits_kernel(RouteArgs a) {
         q8k_wave(x + QK * blockIdx.x, a.q8x + ((size_t)tok * (a.H / QK) + blockIdx.x) * Q8K_BYTES, lane);
 }
 
+// ---------------------------------------------------------------------------
+// Router lookahead (batch 1).  The router's GEMV kernel scored the target
+// layers' routers on x * r_T; the select kernel ranks those scores with the
+// threads its own ranking leaves idle (descending, the lower id first on a
+// tie, a NaN with -inf) into s_top, and one wave -- beside the wave that posts
+// the layer's own routing -- keeps the top ak whose table word is the dummy
+// (best first) and posts the record with the GPU clock and the token's
+// sequence number last (system-scope release).  Every layer posts, with no
+// target too: the record also tells the host the layer has read its table.
+__device__ inline void ahead_rank(const RouteArgs &a, const float (*s_asel)[256], int (*s_top)[AHEAD_K], int i) {
+    const int t = i / a.E, e = i - t * a.E;
+    const float v = s_asel[t][e];
+    int rank = 0;
+    for (int j = 0; j < a.E; j += 4) {
+        const float4 u = *(const float4 *)&s_asel[t][j];
+        rank += (u.x > v) | ((u.x == v) & (j < e));
+        rank += (u.y > v) | ((u.y == v) & (j + 1 < e));
+        rank += (u.z > v) | ((u.z == v) & (j + 2 < e));
+        rank += (u.w > v) | ((u.w == v) & (j + 3 < e));
+    }
+    if (rank < a.ak) s_top[t][rank] = e;
+}
+
+__device__ void ahead_post(const RouteArgs &a, const int (*s_top)[AHEAD_K], int lane) {
+    AheadPost *r = a.apost;
+    const int t = lane >> 3, j = lane & 7;          // lanes 0-7 target 0, 8-15 target 1: one round of loads
+    bool keep = false;
+    int e = -1;
+    if (lane < 16 && t < a.an && j < a.ak) {
+        // a plain load: a word the copy stream flipped a moment ago may still
+        // read as the dummy here, which only offers the host an expert it
+        // already streams (it drops it); the layer's own read is fresh
+        e = s_top[t][j];
+        keep = a.atbl[t][e] == a.adummy[t];
+    }
+    const uint64_t m = __ballot(keep);
+    const uint64_t mt = (m >> (8 * t)) & 0xffull;
+    if (keep) r->ids[t][__popcll(mt & ((1ull << j) - 1ull))] = e;
+    if (lane < 2) {
+        r->n[lane] = lane < a.an ? __popcll((m >> (8 * lane)) & 0xffull) : 0;
+        r->target[lane] = lane < a.an ? a.atarget[lane] : -1;
+    }
+    if (lane == 0) {
+        const uint64_t now = wall_clock64();
+        r->layer = (uint32_t)a.alayer;
+        r->t_lo = (uint32_t)now;
+        r->t_hi = (uint32_t)(now >> 32);
+    }
+    // The record lives in fine-grained host memory, which the stores reach
+    // without passing through L2: waiting for them (vmcnt 0) orders them
+    // before the sequence number; no L2 write-back is needed here.
+    __builtin_amdgcn_s_waitcnt(0x0f70);
+    if (lane == 0) __hip_atomic_store(&r->seq, a.seq ? *a.seq : 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+
 // One workgroup per token.  Wave c owns experts 64c .. 64c+63: logits, the
 // wave's max and its 64-lane butterfly sum of exp (the canonical per-chunk
 // sums, added in chunk order), probabilities and the selection value (+ prior).
@@ -110,6 +194,15 @@ __global__ __launch_bounds__(256) void route_select_kernel(RouteArgs a) {
     __shared__ __attribute__((aligned(16))) float s_sel[256];
     __shared__ float s_m[4], s_cs[4];
     __shared__ int s_ids[16];
+    __shared__ __attribute__((aligned(16))) float s_asel[2][256];   // lookahead scores
+    __shared__ int s_top[2][AHEAD_K];
+    const bool look = a.apost && !a.logits_in;
+    if (look)
+        for (int i = tid; i < a.an * a.E; i += 256) {
+            const int t = i / a.E, e = i - t * a.E;
+            const float v = a.alog[(size_t)t * a.E + e];
+            s_asel[t][e] = v != v ? -INFINITY : v;
+        }
     float l = 0.0f;
     if (wave < nc) {
         const int ee = 64 * wave + lane;
@@ -156,32 +249,55 @@ __global__ __launch_bounds__(256) void route_select_kernel(RouteArgs a) {
             rank += (u.w > v) | ((u.w == v) & (j + 3 < tid));
         }
         if (rank < a.K) s_ids[rank] = tid;
+    } else if (look) {
+        for (int i = tid - a.E; i < a.an * a.E; i += 256 - a.E) ahead_rank(a, s_asel, s_top, i);
     }
     __syncthreads();
+    if (look && a.E >= 256) {            // no idle threads above: a phase of its own
+        for (int i = tid; i < a.an * a.E; i += 256) ahead_rank(a, s_asel, s_top, i);
+        __syncthreads();
+    }
     if (wave == 0) {
         // lane k finishes slot k; the weight sum is the same left-to-right sum on every lane
         float ws = 0.0f;
         for (int k = 0; k < a.K; ++k) ws = ws + s_p[s_ids[k]];
+        int slot = a.dummy;
+        bool streamed = false;
         if (lane < a.K) {
             const int id = s_ids[lane];
             a.ids[(size_t)tok * a.K + lane] = id;
             a.w[(size_t)tok * a.K + lane] = s_p[id] / ws;
-            a.slots[(size_t)tok * a.K + lane] = a.table ? a.table[id] : a.dummy;
+            if (a.table && a.fresh) {
+                // the host's copy stream may write this word while the token runs
+                const int32_t v = __hip_atomic_load(a.table + id, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+                streamed = (v & STREAM_BIT) != 0;
+                slot = v & SLOT_MASK;
+            } else if (a.table) {
+                slot = a.table[id];
+            }
+            a.slots[(size_t)tok * a.K + lane] = slot;
         }
-    }
-    // CPU-assisted serving: post the ids and the Q8_K of x (written by the
-    // router GEMV kernel) to the host, then the sequence number.  One wave:
-    // its release store waits for all of the wave's earlier stores.  (Only
-    // on the router-GEMV path, where x's Q8_K is complete before this kernel.)
-    if (a.post && !a.logits_in) {
-        if (wave == 0) {
-            if (lane < a.K) a.post->ids[lane] = s_ids[lane];
+        if (a.fresh) {
+            const bool any = __ballot(streamed) != 0;
+            if (lane == 0) *a.fresh = any ? 1u : 0u;
+        }
+        // CPU-assisted serving: post the ids, the slots read and the Q8_K of
+        // x (written by the router GEMV kernel) to the host, then the sequence
+        // number.  One wave: its release store waits for all of the wave's
+        // earlier stores.  (Only on the router-GEMV path, where x's Q8_K is
+        // complete before this kernel.)
+        if (a.post && !a.logits_in) {
+            if (lane < a.K) {
+                a.post->ids[lane] = s_ids[lane];
+                a.post->slots[lane] = slot;
+            }
             const uint4 *src = (const uint4 *)a.q8x;
             uint4 *dst = (uint4 *)a.post->q8x;
             for (int i = lane; i < (a.H / QK) * Q8K_BYTES / 16; i += 64) dst[i] = src[i];
             if (lane == 0) __hip_atomic_store(&a.post->seq, *a.seq, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
         }
     }
+    if (look && wave == 1) ahead_post(a, s_top, lane);      // beside wave 0's own post
     if (!a.logits_in || !a.x || !a.q8x) return;
     const float *x = a.x + (size_t)tok * a.H;
     uint8_t *q8 = a.q8x + (size_t)tok * (a.H / QK) * Q8K_BYTES;
@@ -271,6 +387,9 @@ __global__ __launch_bounds__(256) void gateup_kernel(ExpertArgs a) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int k = blockIdx.y;
     if (!serves(a, k, SRC)) return;
+    // a slot of this layer was written by the copy stream during the token:
+    // drop cached lines of its previous contents before reading weights
+    if (a.fresh && *a.fresh) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
     const int b = lane >> 3, u = lane & 7;
     const int j = u >> 1;
     const uint8_t *base = expert_base(a, k);
@@ -371,6 +490,7 @@ __global__ __launch_bounds__(512) void down_kernel(ExpertArgs a) {
 
     const int g = lane >> 3, u = lane & 7;   // g: row within the tile, u: part of a super-block
     const int kt = a.K + a.n_shared;
+    if (a.fresh && *a.fresh) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");   // as in gateup_kernel
     for (int kb = 0; kb < kt; kb += 8) {
         const int k = kb + wave;
         const bool mine = k < kt && serves(a, k, SRC);
@@ -528,11 +648,18 @@ hipError_t launch_route(const RouteLaunch &l, hipStream_t st, hipEvent_t *ev) {
     a.logits = l.logits; a.counter = l.counter; a.ids = l.ids; a.w = l.w; a.slots = l.slots;
     a.probs = l.probs; a.q8x = l.q8x; a.logits_in = l.logits_in;
     a.post = l.post; a.seq = l.seq;
+    a.an = l.an; a.ak = l.ak;
+    for (int t = 0; t < 2; ++t) {
+        a.aW[t] = l.aW[t]; a.ar[t] = l.ar[t]; a.atbl[t] = l.atbl[t];
+        a.adummy[t] = l.adummy[t]; a.atarget[t] = l.atarget[t];
+    }
+    a.alayer = l.alayer; a.alog = l.alog; a.apost = l.apost; a.fresh = l.fresh;
     if (l.logits_in)
         return launch(route_select_kernel, dim3((unsigned)l.n_tok), dim3(256), st, ev ? ev[2] : nullptr,
                       ev ? ev[3] : nullptr, a);
-    const hipError_t e = launch(route_logits_kernel, dim3((unsigned)(l.E / 4), (unsigned)l.n_tok), dim3(256), st,
-                                ev ? ev[0] : nullptr, ev ? ev[1] : nullptr, a);
+    const unsigned per = (unsigned)((l.E + 3) / 4);
+    const hipError_t e = launch(route_logits_kernel, dim3(per * (unsigned)(1 + (l.apost ? l.an : 0)), (unsigned)l.n_tok),
+                                dim3(256), st, ev ? ev[0] : nullptr, ev ? ev[1] : nullptr, a);
     if (e != hipSuccess) return e;
     return launch(route_select_kernel, dim3((unsigned)l.n_tok), dim3(256), st, ev ? ev[2] : nullptr,
                   ev ? ev[3] : nullptr, a);

@@ -20,12 +20,15 @@
 #include <immintrin.h>
 
 #include <algorithm>
+#include <array>
 #include <atomic>
 #include <chrono>
+#include <condition_variable>
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
 #include <deque>
+#include <mutex>
 #include <string>
 #include <thread>
 #include <vector>
@@ -34,6 +37,7 @@
 #include "mp_cpu.h"
 #include "mp_format.h"
 #include "mp_internal.h"
+#include "mp_stream.h"
 #include "mp_synth.h"
 
 namespace {
@@ -81,6 +85,62 @@ struct Layer {
 struct Job {
     int li, expert, slot;
     hipEvent_t ev;     // live mode only
+};
+
+// Just-in-time streaming (LLAMA_MOE_STREAM; state as in patches/0010:957-1021).
+// One job per planner job, same index: the slot it took and what the GPU made
+// of it.  Between tokens the mover thread is idle and the cache's own thread
+// owns all of this; during a token only the mover touches it.
+struct StreamJob {
+    int li, slot, d;
+    int64_t ticket;           // the push that carried the last chunk and the table word (live)
+    bool landed, in_time, late;
+};
+
+enum { SN_RECORDS, SN_OFFERED, SN_LANDED, SN_IN_TIME, SN_LATE, SN_UNUSED, SN_DROP_LATE, SN_DROP_POSTED,
+       SN_NOT_SENT, SN_GPU_MISS, SN_BYTES, SN_COUNT };
+
+struct Streamer {
+    int per_layer = 4, reserve = 2, top_k = 8;
+    double bytes_per_ns = 45.7, tau_ns = 103000.0;
+    uint64_t margin_ns = 5000;
+    size_t max_outstanding = 1u << 20;
+    mps::Planner planner{512 * 1024};
+    std::vector<StreamJob> jobs;
+    std::vector<int32_t> mark;                 // [layer][E]: job + 1 while streamed this token
+    std::vector<int> n_this_token;             // [layer]
+    uint32_t last_layer = UINT32_MAX;
+    uint64_t last_t_ns = 0;
+    uint64_t n[SN_COUNT] = {};
+    double lead_sum[3] = {0, 0, 0};
+    uint64_t lead_n[3] = {0, 0, 0};
+    std::vector<uint64_t> arrive_ns;           // [layer]: host time its record arrived this token, 0 if not
+    std::vector<int32_t> rec_frame;            // map record: the boundary's frame, held back one step
+    uint64_t rec_step = 0;
+    bool rec_have = false;
+    std::vector<std::array<int32_t, 3>> rec_used;   // (layer, slot, expert) used in time this token
+    // live mode (a GPU cache): lookahead launch arguments, the copy queue, the mover thread
+    bool live = false;
+    std::vector<std::array<int32_t, 2>> targets;    // [layer]: lookahead targets, -1 none
+    float *ratio = nullptr;                    // dev [layer][2][H]: g_T / g_L
+    float *alog = nullptr;                     // dev [2][E]
+    uint32_t *fresh = nullptr;                 // dev [layer]
+    mp::AheadPost *post = nullptr, *post_d = nullptr;   // mapped host [layer]
+    int32_t *words = nullptr;                  // pinned [max slots]: s | STREAM_BIT, sources of table writes
+    hipStream_t stream = nullptr;              // the copy queue
+    std::vector<hipEvent_t> ev;                // ring of pushes
+    std::vector<int64_t> ev_ticket;
+    int ev_head = 0, ev_count = 0;
+    int64_t next_ticket = 1, done_ticket = 0;
+    std::deque<std::pair<int64_t, size_t>> outstanding;   // (ticket, bytes) pushed, not landed
+    std::thread thr;
+    std::mutex m;
+    std::condition_variable cv, cv_done;
+    uint32_t gen = 0, gen_done = 0;            // tokens started / drained (guarded by m)
+    bool quit = false;                         // guarded by m
+    std::atomic<bool> stop{false};             // the token's GPU work is over: drain
+    std::atomic<bool> failed{false};
+    uint32_t seq = 0;                          // the token's sequence number
 };
 
 }  // namespace
@@ -168,6 +228,12 @@ struct moe_cache {
     float *b_w = nullptr;
     uint8_t *b_q8x = nullptr;
     void *b_route_ws = nullptr, *b_ws = nullptr;
+    // router lookahead and just-in-time streaming
+    Streamer *st = nullptr;
+    std::vector<float> norm;                   // [layer][H] RMS-norm weights of the router inputs
+    std::vector<uint8_t> has_norm;             // [layer]
+    int32_t *h_slots = nullptr;                // pinned [layer][K]: the slots the GPU read this token
+    std::atomic<int> sc_computing{-1};         // layer whose absent experts the host team is computing
 };
 
 struct moe_pool {
@@ -188,6 +254,24 @@ void set_table_entry(moe_cache *c, Layer &ls, int expert, int v) {
     c->h_tbl[o] = v;
     if (c->h_prior) c->h_prior[o] = v == ls.S ? 0.0f : c->cfg.cache_prior;
     ls.tbl_dirty = true;
+}
+
+// free slots a layer keeps at the boundary: the demand path's inserts and the
+// streaming reserve (patches/0010:1135-1142)
+int pool_target_of(const moe_cache *c) {
+    if (c->freeze) return 0;
+    return c->cfg.max_inserts + (c->st ? c->st->reserve : 0);
+}
+
+// expert `id` of layer `li` is being streamed in this token
+bool streamed(const moe_cache *c, int li, int id) {
+    return c->st && c->st->mark[(size_t)li * c->E + id] != 0;
+}
+
+uint64_t mono_ns() {
+    return (uint64_t)std::chrono::duration_cast<std::chrono::nanoseconds>(
+               std::chrono::steady_clock::now().time_since_epoch())
+        .count();
 }
 
 int32_t lru_resident(const Layer &ls) {
@@ -269,6 +353,7 @@ int issue_uploads(moe_cache *c, int li, const int32_t *ids, int n, int budget, i
         const int id = ids[i];
         if (id < 0 || id >= ls.E) continue;
         if (ls.expert_slot[id] >= 0) continue;
+        if (streamed(c, li, id)) continue;                    // being streamed in this token
         if ((int)ls.free_slots.size() <= min_keep) break;
         bool dup = false;
         for (const Job &j : c->jobs)
@@ -335,22 +420,52 @@ static int replay_frame(moe_cache *c) {
     return flush_tables(c);
 }
 
+void write_frame(moe_cache *c, uint64_t step, const std::vector<int32_t> &frame) {
+    fprintf(c->map, "step %llu\n", (unsigned long long)step);
+    size_t o = 0;
+    for (const Layer &ls : c->L) {
+        fprintf(c->map, "map %d", ls.il);
+        for (int s = 0; s < ls.S; ++s) fprintf(c->map, " %d", frame[o + (size_t)s]);
+        o += (size_t)ls.S;
+        fputc('\n', c->map);
+    }
+    fflush(c->map);
+}
+
 int map_frame(moe_cache *c) {
     if (c->replay) {
         const int r = replay_frame(c);
         if (r != MOE_OK) return r;
     }
     if (!c->map) return MOE_OK;
-    fprintf(c->map, "step %llu\n", (unsigned long long)c->n_steps);
+    std::vector<int32_t> frame;
     for (const Layer &ls : c->L) {
-        std::vector<int32_t> pub(ls.S, -1);
+        const size_t o = frame.size();
+        frame.resize(o + (size_t)ls.S, -1);
         for (int e = 0; e < ls.E; ++e)
-            if (ls.expert_slot[e] >= 0) pub[ls.expert_slot[e]] = e;
-        fprintf(c->map, "map %d", ls.il);
-        for (int v : pub) fprintf(c->map, " %d", v);
-        fputc('\n', c->map);
+            if (ls.expert_slot[e] >= 0) frame[o + (size_t)ls.expert_slot[e]] = e;
     }
-    fflush(c->map);
+    Streamer *st = c->st;
+    if (!st) {
+        write_frame(c, c->n_steps, frame);
+        return MOE_OK;
+    }
+    // streaming (patches/0010:1096-1129): the token after a boundary also used
+    // the experts that streamed in before their layer read its table, so the
+    // boundary's frame is written one step late with those experts in the
+    // slots they used; a replay then gives every token what its GPU saw
+    if (st->rec_have) {
+        for (const auto &u : st->rec_used) {
+            size_t o = 0;
+            for (int l = 0; l < u[0]; ++l) o += (size_t)c->L[l].S;
+            st->rec_frame[o + (size_t)u[1]] = u[2];
+        }
+        write_frame(c, st->rec_step, st->rec_frame);
+    }
+    st->rec_used.clear();
+    st->rec_frame = std::move(frame);
+    st->rec_step = c->n_steps;
+    st->rec_have = true;
     return MOE_OK;
 }
 
@@ -397,6 +512,326 @@ void publish(moe_cache *c, const Job &j) {
     c->n_published++;
 }
 
+// ---- just-in-time streaming: the mover's bookkeeping ---------------------------
+// layer `li` has read its table this token (patches/0010:1164-1181): its
+// unfinished jobs are dropped, and the time since the records of the layers
+// one and two before it arrived is the lead their predictions had
+void stream_posted(moe_cache *c, int li, uint64_t now) {
+    Streamer *st = c->st;
+    st->planner.posted(li);
+    for (int d = 1; d <= 2 && li - d >= 0; ++d) {
+        const uint64_t a = st->arrive_ns[(size_t)(li - d)];
+        if (a && now > a) {
+            st->lead_sum[d] += (double)(now - a);
+            st->lead_n[d]++;
+        }
+    }
+}
+
+// one lookahead record (patches/0010:1466-1530): candidates become planner
+// jobs, each with a free slot of its target layer; t_ns is the GPU's time at
+// the post (the time per layer is estimated from consecutive layers)
+int stream_take(moe_cache *c, int layer, const int32_t *targets, const int32_t *n, const int32_t *ids,
+                uint64_t now, uint64_t t_ns, uint64_t bytes_given) {
+    Streamer *st = c->st;
+    const int NL = (int)c->L.size();
+    if (layer >= 0 && layer < NL) st->arrive_ns[(size_t)layer] = now;
+    if (st->last_layer != UINT32_MAX && (uint32_t)layer == st->last_layer + 1 && t_ns > st->last_t_ns) {
+        const double dt = (double)(t_ns - st->last_t_ns);
+        if (dt > 10000.0 && dt < 1000000.0) st->tau_ns = 0.9 * st->tau_ns + 0.1 * dt;
+    }
+    st->last_layer = (uint32_t)layer;
+    st->last_t_ns = t_ns;
+    st->n[SN_RECORDS]++;
+    int taken = 0;
+    for (int t = 0; t < 2; ++t) {
+        const int T = targets[t];
+        if (T < 0 || T >= NL) continue;
+        Layer &ls = c->L[(size_t)T];
+        const int d = T - layer;
+        const uint64_t lead = (uint64_t)(d * st->tau_ns);
+        const uint64_t deadline = now + (lead > st->margin_ns ? lead - st->margin_ns : 0);
+        const uint64_t bytes = bytes_given ? bytes_given : ls.expert_bytes;
+        for (int j = 0; j < n[t] && j < mp::AHEAD_K; ++j) {
+            const int e = ids[t * mp::AHEAD_K + j];
+            if (e < 0 || e >= ls.E || ls.expert_slot[e] >= 0) continue;
+            int32_t &mk = st->mark[(size_t)T * c->E + e];
+            if (mk) {
+                st->planner.offer(T, e, bytes, deadline);       // a job already: may tighten its deadline
+                continue;
+            }
+            if (st->n_this_token[(size_t)T] >= st->per_layer) continue;
+            if ((int)ls.free_slots.size() <= c->cfg.max_inserts) {
+                st->n[SN_NOT_SENT]++;                           // the demand path keeps its share
+                continue;
+            }
+            bool upl = false;
+            for (const Job &jb : c->jobs)
+                if (jb.li == T && jb.expert == e) { upl = true; break; }
+            if (upl) continue;                                  // an upload of it is in flight
+            const int id = st->planner.offer(T, e, bytes, deadline);
+            if (id < 0) continue;                               // the layer has read its table already
+            StreamJob sj{T, ls.free_slots.back(), d, 0, false, false, false};
+            ls.free_slots.pop_back();
+            ls.slot_in_flight[(size_t)sj.slot] = 1;
+            st->jobs.push_back(sj);
+            mk = id + 1;
+            st->n_this_token[(size_t)T]++;
+            st->n[SN_OFFERED]++;
+            taken++;
+        }
+    }
+    return taken;
+}
+
+bool stream_next(moe_cache *c, uint64_t free_at, int hold_after, mps::Chunk &ch) {
+    Streamer *st = c->st;
+    if (!st->planner.next(free_at, st->bytes_per_ns, hold_after, ch)) return false;
+    st->n[SN_BYTES] += ch.len;
+    return true;
+}
+
+void stream_land(moe_cache *c, int job) {
+    Streamer *st = c->st;
+    if (job < 0 || job >= (int)st->jobs.size() || st->jobs[(size_t)job].landed) return;
+    st->jobs[(size_t)job].landed = true;
+    st->n[SN_LANDED]++;
+}
+
+// the GPU's slots say whether each streamed expert made it (patches/0010:1183-1210)
+void stream_account(moe_cache *c, int li, const int32_t *ids, const int32_t *gslots, int n_ids) {
+    Streamer *st = c->st;
+    const Layer &l0 = c->L[(size_t)li];
+    for (int i = 0; i < n_ids; ++i) {
+        const int id = ids[i];
+        if (id < 0 || id >= l0.E) continue;
+        const bool miss = gslots[i] >= l0.S;
+        const int32_t m = st->mark[(size_t)li * c->E + id];
+        if (!m) {
+            st->n[SN_GPU_MISS] += miss;
+            continue;
+        }
+        StreamJob &j = st->jobs[(size_t)m - 1];
+        Layer &ls = c->L[(size_t)j.li];
+        if (!miss && !j.in_time) {
+            j.in_time = true;
+            st->n[SN_IN_TIME]++;
+            ls.n_hit++;
+        } else if (miss && !j.in_time && !j.late) {
+            j.late = true;
+            st->n[SN_LATE]++;
+            st->n[SN_GPU_MISS]++;
+            ls.n_miss++;
+        }
+    }
+}
+
+// boundary, mover idle (patches/0010:1722-1760): landed experts join the
+// cache -- routed ones as recently used, the others as the first to go --
+// and the slots of the rest go back to the pool.  Every layer a table word
+// was written for is flushed from the mirrors, which clears STREAM_BIT.
+void stream_adopt(moe_cache *c) {
+    Streamer *st = c->st;
+    st->rec_used.clear();
+    for (size_t k = 0; k < st->jobs.size(); ++k) {
+        const StreamJob &sj = st->jobs[k];
+        const int e = st->planner.get((int)k).expert;
+        Layer &ls = c->L[(size_t)sj.li];
+        ls.slot_in_flight[(size_t)sj.slot] = 0;
+        if (sj.ticket > 0) ls.tbl_dirty = true;
+        if (sj.in_time) st->rec_used.push_back({sj.li, sj.slot, e});
+        if (sj.landed && ls.expert_slot[e] >= 0) {
+            ls.free_slots.push_back(sj.slot);             // an upload of it was published meanwhile
+            st->n[SN_UNUSED] += !sj.in_time && !sj.late;
+            ls.tbl_dirty = true;
+        } else if (sj.landed) {
+            ls.slot_expert[(size_t)sj.slot] = e;
+            ls.expert_slot[e] = sj.slot;
+            ls.slot_last_use[(size_t)sj.slot] = sj.in_time || sj.late ? ++c->clock : 1;
+            set_table_entry(c, ls, e, sj.slot);
+            c->n_published++;
+            if (!sj.in_time && !sj.late) st->n[SN_UNUSED]++;
+        } else {
+            ls.free_slots.push_back(sj.slot);
+        }
+        st->mark[(size_t)sj.li * c->E + e] = 0;
+    }
+    st->n[SN_DROP_LATE] = st->planner.n_drop_late;
+    st->n[SN_DROP_POSTED] = st->planner.n_drop_posted;
+    st->jobs.clear();
+    st->planner.reset();
+    std::fill(st->n_this_token.begin(), st->n_this_token.end(), 0);
+    std::fill(st->arrive_ns.begin(), st->arrive_ns.end(), 0);
+    st->last_layer = UINT32_MAX;
+}
+
+// ---- the mover thread (live): copy queue, planner, records -------------------
+// The copy queue is one stream with a ring of events: a push is some copies
+// then an event, and its ticket is done when that event has fired.  A push is
+// ordered after every earlier one, which is what makes "the expert's last
+// chunk, then its table word" safe as one push.
+int64_t mover_done(Streamer *st) {
+    while (st->ev_count > 0) {
+        const hipError_t q = hipEventQuery(st->ev[(size_t)st->ev_head]);
+        if (q == hipErrorNotReady) break;
+        if (q != hipSuccess) return -1;
+        st->done_ticket = st->ev_ticket[(size_t)st->ev_head];
+        st->ev_head = (st->ev_head + 1) % (int)st->ev.size();
+        st->ev_count--;
+    }
+    return st->done_ticket;
+}
+
+// ticket of the push, 0 when the ring is full, -1 on a HIP error
+int64_t mover_push(Streamer *st, void *dst, const void *src, size_t len, void *wdst, const void *wsrc) {
+    if (st->ev_count == (int)st->ev.size()) {
+        if (mover_done(st) < 0) return -1;
+        if (st->ev_count == (int)st->ev.size()) return 0;
+    }
+    if (hipMemcpyAsync(dst, src, len, hipMemcpyHostToDevice, st->stream) != hipSuccess) return -1;
+    if (wdst && hipMemcpyAsync(wdst, wsrc, sizeof(int32_t), hipMemcpyHostToDevice, st->stream) != hipSuccess)
+        return -1;
+    const int i = (st->ev_head + st->ev_count) % (int)st->ev.size();
+    if (hipEventRecord(st->ev[(size_t)i], st->stream) != hipSuccess) return -1;
+    st->ev_ticket[(size_t)i] = st->next_ticket++;
+    st->ev_count++;
+    return st->ev_ticket[(size_t)i];
+}
+
+// copies whose event fired: the expert and its table word are on the device
+void stream_reap(moe_cache *c, int64_t done) {
+    Streamer *st = c->st;
+    if (done < 0) {
+        if (!st->failed.exchange(true)) fprintf(stderr, "moe-cache: stream copy queue error; streaming stops\n");
+        return;
+    }
+    while (!st->outstanding.empty() && st->outstanding.front().first <= done) st->outstanding.pop_front();
+    for (size_t k = 0; k < st->jobs.size(); ++k) {
+        const StreamJob &j = st->jobs[k];
+        if (j.ticket > 0 && j.ticket <= done && !j.landed) stream_land(c, (int)k);
+    }
+}
+
+// hand the copy engine the next chunks, up to max_outstanding bytes queued
+bool stream_issue(moe_cache *c) {
+    Streamer *st = c->st;
+    size_t queued = 0;
+    for (const auto &o : st->outstanding) queued += o.second;
+    bool any = false;
+    while (queued < st->max_outstanding && st->outstanding.size() < 32) {
+        // while the host computes a layer's absent experts, copies for later layers wait
+        const int comp = c->sc_computing.load(std::memory_order_relaxed);
+        const uint64_t free_at = mono_ns() + (uint64_t)((double)queued / st->bytes_per_ns);
+        mps::Chunk ch;
+        if (!stream_next(c, free_at, comp >= 0 ? comp + 1 : -1, ch)) break;
+        const int e = st->planner.get(ch.job).expert;
+        StreamJob &sj = st->jobs[(size_t)ch.job];
+        const Layer &ls = c->L[(size_t)sj.li];
+        uint8_t *dst = ls.pool + (size_t)sj.slot * ls.slot_bytes + ch.offset;
+        const uint8_t *src = ls.store_host + (size_t)e * ls.expert_bytes + ch.offset;
+        int32_t *wdst = ch.last ? c->d_tbl + (size_t)ls.il * c->E + e : nullptr;
+        const int32_t *wsrc = ch.last ? st->words + sj.slot : nullptr;
+        const int64_t ticket = mover_push(st, dst, src, ch.len, wdst, wsrc);
+        if (ticket <= 0) {
+            if (!st->failed.exchange(true))
+                fprintf(stderr, "moe-cache: stream copy push failed (%lld); streaming stops\n", (long long)ticket);
+            return any;
+        }
+        st->outstanding.push_back({ticket, ch.len});
+        queued += ch.len;
+        if (ch.last) sj.ticket = ticket;
+        any = true;
+    }
+    return any;
+}
+
+// One generation per token: take each layer's lookahead record as it
+// arrives (the layer has then read its table), keep the copy engine fed, and
+// when the token's GPU work is over wait for the queued copies and hand the
+// bookkeeping back to the cache's thread.
+void mover_loop(moe_cache *c) {
+    Streamer *st = c->st;
+    if (hipSetDevice(c->cfg.device) != hipSuccess) st->failed = true;
+    uint32_t served = 0;
+    const int NL = (int)c->L.size();
+    for (;;) {
+        uint32_t gen;
+        {
+            std::unique_lock<std::mutex> lk(st->m);
+            st->cv.wait(lk, [&] { return st->quit || st->gen != served; });
+            if (st->quit) return;
+            gen = st->gen;
+        }
+        const uint32_t seq = st->seq;
+        int next = 0;
+        int64_t last_done = st->done_ticket;
+        while (!st->stop.load(std::memory_order_acquire)) {
+            bool progress = false;
+            while (!st->failed && next < NL &&
+                   __atomic_load_n(&st->post[next].seq, __ATOMIC_ACQUIRE) == seq) {
+                const mp::AheadPost rec = st->post[next];
+                const uint64_t now = mono_ns();
+                stream_posted(c, next, now);
+                const uint64_t t = ((uint64_t)rec.t_hi << 32 | rec.t_lo) * 10;     // 100 MHz clock -> ns
+                stream_take(c, next, rec.target, rec.n, &rec.ids[0][0], now, t, 0);
+                ++next;
+                progress = true;
+            }
+            if (!st->failed) {
+                const int64_t done = mover_done(st);
+                if (done != last_done) {
+                    stream_reap(c, done);
+                    last_done = done;
+                    progress = true;
+                }
+                progress |= stream_issue(c);
+            }
+            if (!progress) _mm_pause();
+        }
+        // the token is over: what landed stays, the rest goes back at the boundary
+        if (hipStreamSynchronize(st->stream) != hipSuccess) st->failed = true;
+        stream_reap(c, st->failed ? -1 : mover_done(st));
+        st->outstanding.clear();
+        served = gen;
+        {
+            std::lock_guard<std::mutex> lk(st->m);
+            st->gen_done = gen;
+        }
+        st->cv_done.notify_all();
+    }
+}
+
+void stream_stop_thread(Streamer *st) {
+    if (!st->thr.joinable()) return;
+    st->stop.store(true, std::memory_order_release);      // ends a token the mover may still serve
+    {
+        std::lock_guard<std::mutex> lk(st->m);
+        st->quit = true;
+    }
+    st->cv.notify_all();
+    st->thr.join();
+}
+
+void stream_free(moe_cache *c) {
+    Streamer *st = c->st;
+    if (!st) return;
+    stream_stop_thread(st);
+    if (c->map && st->rec_have) write_frame(c, st->rec_step, st->rec_frame);   // the last boundary
+    if (st->live) {
+        if (st->stream) hipStreamSynchronize(st->stream);
+        for (hipEvent_t e : st->ev)
+            if (e) hipEventDestroy(e);
+        if (st->stream) hipStreamDestroy(st->stream);
+        hipFree(st->ratio);
+        hipFree(st->alog);
+        hipFree(st->fresh);
+        if (st->post) hipHostFree(st->post);
+        if (st->words) hipHostFree(st->words);
+    }
+    delete st;
+    c->st = nullptr;
+}
+
 int cache_step(moe_cache *c) {
     // 1) publish finished uploads (no kernel of the cache is running)
     if (!c->jobs.empty()) {
@@ -433,6 +868,7 @@ int cache_step(moe_cache *c) {
         c->n_copied += done.size();
         for (const Job &j : done) publish(c, j);
     }
+    if (c->st) stream_adopt(c);         // after the uploads: an expert both copied is kept once
 
     c->n_steps++;
 
@@ -474,7 +910,7 @@ int cache_step(moe_cache *c) {
             continue;
         }
         ls.pending.clear();
-        const int pool_target = c->freeze ? 0 : c->cfg.max_inserts;
+        const int pool_target = pool_target_of(c);
         while ((int)ls.free_slots.size() < pool_target) {
             int slot = -1;
             uint64_t best = U64MAX;
@@ -509,12 +945,16 @@ int cache_step(moe_cache *c) {
     return r2;
 }
 
-int cache_observe(moe_cache *c, int li, const int32_t *ids, int n_ids, int n_tok) {
+// gslots (batch 1 with streaming): the slots the GPU read, n_slots = absent
+int cache_observe(moe_cache *c, int li, const int32_t *ids, int n_ids, int n_tok, const int32_t *gslots = nullptr) {
     Layer &ls = c->L[li];
     if (c->route) {
         fprintf(c->route, "route %llu %d %d %d", (unsigned long long)c->n_steps, ls.il, n_ids, n_tok);
-        for (int i = 0; i < n_ids * n_tok; ++i)
-            fprintf(c->route, " %d:%d", ids[i], (ids[i] >= 0 && ids[i] < ls.E) ? ls.expert_slot[ids[i]] : -1);
+        for (int i = 0; i < n_ids * n_tok; ++i) {
+            int slot = (ids[i] >= 0 && ids[i] < ls.E) ? ls.expert_slot[ids[i]] : -1;
+            if (gslots) slot = gslots[i] >= ls.S ? -1 : gslots[i];    // what the GPU used (0010:1147-1154)
+            fprintf(c->route, " %d:%d", ids[i], slot);
+        }
         fputc('\n', c->route);
     }
     for (int t = 0; t < n_tok; ++t) {
@@ -524,6 +964,7 @@ int cache_observe(moe_cache *c, int li, const int32_t *ids, int n_ids, int n_tok
             if (!ls.heat.empty()) ls.heat[id] += 1.0f;
             if (!ls.use_count.empty()) ls.use_count[id]++;
             const int slot = ls.expert_slot[id];
+            if (slot < 0 && streamed(c, li, id)) continue;      // the GPU's table decides (accounted below)
             if (slot >= 0) {
                 ls.n_hit++;
                 ls.slot_last_use[slot] = ++c->clock;
@@ -539,7 +980,7 @@ int cache_observe(moe_cache *c, int li, const int32_t *ids, int n_ids, int n_tok
         }
     }
     if (c->cfg.early_issue) {
-        const int pool_target = c->freeze ? 0 : c->cfg.max_inserts;
+        const int pool_target = pool_target_of(c);
         const int next_victim = c->cfg.admit_mode == MOE_ADMIT_OFF ? -1
                                 : ((int)ls.free_slots.size() > pool_target ? -1 : lru_resident(ls));
         int r;
@@ -553,6 +994,7 @@ int cache_observe(moe_cache *c, int li, const int32_t *ids, int n_ids, int n_tok
         }
         if (r < 0) return r;
     }
+    if (gslots && c->st) stream_account(c, li, ids, gslots, n_ids);
     return MOE_OK;
 }
 
@@ -573,8 +1015,9 @@ size_t exp_ws_bytes(int I, int K) {
 }
 
 int run_route(const moe_route_desc *d, hipStream_t st, hipEvent_t *ev = nullptr, mp::SidecarPost *post = nullptr,
-              const uint32_t *seq = nullptr) {
+              const uint32_t *seq = nullptr, const mp::RouteLaunch *ahead = nullptr) {
     mp::RouteLaunch l{};
+    if (ahead) l = *ahead;          // lookahead and table-freshness fields; the rest is set below
     l.W = d->W; l.x = d->x; l.bias = d->bias; l.prior = d->prior; l.table = d->table; l.dummy = d->dummy;
     l.prior_on_logits = d->prior_on_logits;
     l.E = d->E; l.H = d->H; l.K = d->K; l.n_tok = d->n_tok;
@@ -649,6 +1092,7 @@ GroupedWs grouped_ws(int n_tok, int K, int H, int I) {
 
 void free_cache(moe_cache *c) {
     if (!c) return;
+    stream_free(c);
     for (hipEvent_t e : c->tev) hipEventDestroy(e);
     if (c->host_only) {
         free(c->h_tbl);
@@ -703,6 +1147,7 @@ void free_cache(moe_cache *c) {
     if (c->h_tbl) hipHostFree(c->h_tbl);
     if (c->h_prior) hipHostFree(c->h_prior);
     if (c->h_ids) hipHostFree(c->h_ids);
+    if (c->h_slots) hipHostFree(c->h_slots);
     if (c->route) fclose(c->route);
     if (c->map) fclose(c->map);
     if (c->replay) fclose(c->replay);
@@ -1008,7 +1453,8 @@ int moe_cache_create(const moe_cache_config *cfg, moe_cache **out) {
         hipMalloc(&c->d_slots, (size_t)NL * c->K * 4) != hipSuccess ||
         hipMalloc(&c->d_w, (size_t)NL * c->K * 4) != hipSuccess ||
         hipMalloc(&c->d_q8x, (size_t)(c->H / 256) * mp::Q8K_BYTES + 256) != hipSuccess ||
-        hipHostMalloc(&c->h_ids, (size_t)NL * c->K * 4, 0) != hipSuccess)
+        hipHostMalloc(&c->h_ids, (size_t)NL * c->K * 4, 0) != hipSuccess ||
+        hipHostMalloc(&c->h_slots, (size_t)NL * c->K * 4, 0) != hipSuccess)
         return bail(fail(MOE_ERR_NOMEM, "decode scratch"));
     if (hipMemset(c->route_ws, 0, rws) != hipSuccess || hipMemset(c->exp_ws, 0, ews) != hipSuccess)
         return bail(fail(MOE_ERR_HIP, "scratch clear"));
@@ -1242,6 +1688,288 @@ int moe_cache_map_replay(moe_cache *c, const char *path) {
     return map_frame(c);             // the frame of step 0, as at the reference's init (patches/0008:571)
 }
 
+// ---- router lookahead and just-in-time streaming ----------------------------
+int moe_cache_set_norm(moe_cache *c, int layer, const float *g_host, int n) {
+    if (!c || !g_host || layer < 0 || layer >= (int)c->L.size()) return fail(MOE_ERR_ARG, "bad arguments");
+    if (n != c->H) return fail(MOE_ERR_ARG, "norm of %d values, the hidden size is %d", n, c->H);
+    if (c->norm.empty()) {
+        c->norm.assign(c->L.size() * (size_t)c->H, 0.0f);
+        c->has_norm.assign(c->L.size(), 0);
+    }
+    memcpy(c->norm.data() + (size_t)layer * c->H, g_host, (size_t)n * sizeof(float));
+    c->has_norm[(size_t)layer] = 1;
+    return MOE_OK;
+}
+
+static int stream_live_init(moe_cache *c, Streamer *st) {
+    const int NL = (int)c->L.size();
+    for (const Layer &ls : c->L)
+        if (!ls.router || !ls.store_host) return fail(MOE_ERR_STATE, "layer %d: router or host store missing", ls.il);
+    // pairs (L, T = L+1, L+2): r = g_T / g_L, so W_T . (x_L * r) = W_T . (rmsnorm(residual_L) * g_T)
+    std::vector<float> ratio((size_t)NL * 2 * c->H, 0.0f);
+    st->targets.assign((size_t)NL, {-1, -1});
+    int pairs = 0;
+    for (int l = 0; l < NL; ++l) {
+        for (int d = 1; d <= 2; ++d) {
+            const int T = l + d;
+            if (T >= NL || c->has_norm.empty() || !c->has_norm[(size_t)l] || !c->has_norm[(size_t)T]) continue;
+            const float *gl = c->norm.data() + (size_t)l * c->H, *gt = c->norm.data() + (size_t)T * c->H;
+            float *r = ratio.data() + ((size_t)l * 2 + (d - 1)) * c->H;
+            bool ok = true;
+            for (int i = 0; i < c->H && ok; ++i) {
+                ok = std::fabs(gl[i]) >= 1e-12f;
+                r[i] = gt[i] / gl[i];
+            }
+            if (!ok) {
+                fprintf(stderr, "moe-cache: lookahead %d -> %d skipped: a zero norm weight in layer %d\n", l, T, l);
+                continue;
+            }
+            st->targets[(size_t)l][(size_t)(d - 1)] = T;
+            pairs++;
+        }
+    }
+    if (!pairs) return fail(MOE_ERR_STATE, "no layer pair has norm weights: call moe_cache_set_norm for every layer");
+    int max_s = 0;
+    for (const Layer &ls : c->L) max_s = std::max(max_s, ls.S);
+    const unsigned fl = hipHostMallocMapped | hipHostMallocCoherent;
+    if (hipMalloc(&st->ratio, ratio.size() * sizeof(float)) != hipSuccess ||
+        hipMalloc(&st->alog, 2 * (size_t)c->E * sizeof(float)) != hipSuccess ||
+        hipMalloc(&st->fresh, (size_t)NL * sizeof(uint32_t)) != hipSuccess ||
+        hipHostMalloc((void **)&st->post, (size_t)NL * sizeof(mp::AheadPost), fl) != hipSuccess ||
+        hipHostMalloc((void **)&st->words, (size_t)max_s * sizeof(int32_t), 0) != hipSuccess)
+        return fail(MOE_ERR_NOMEM, "streaming buffers");
+    memset((void *)st->post, 0, (size_t)NL * sizeof(mp::AheadPost));
+    for (int v = 0; v < max_s; ++v) st->words[v] = v | mp::STREAM_BIT;
+    HIPCHK(hipHostGetDevicePointer((void **)&st->post_d, st->post, 0));
+    HIPCHK(hipMemcpy(st->ratio, ratio.data(), ratio.size() * sizeof(float), hipMemcpyHostToDevice));
+    HIPCHK(hipMemset(st->fresh, 0, (size_t)NL * sizeof(uint32_t)));
+    HIPCHK(hipStreamCreateWithFlags(&st->stream, hipStreamNonBlocking));
+    st->ev.assign(64, nullptr);
+    st->ev_ticket.assign(64, 0);
+    for (auto &e : st->ev) HIPCHK(hipEventCreateWithFlags(&e, hipEventDisableTiming));
+    if (!c->h_seq) {
+        if (hipHostMalloc((void **)&c->h_seq, 64, hipHostMallocDefault) != hipSuccess ||
+            hipMalloc(&c->d_seq, 64) != hipSuccess)
+            return fail(MOE_ERR_NOMEM, "sequence number");
+        HIPCHK(hipMemset(c->d_seq, 0, 64));
+    }
+    st->live = true;
+    st->thr = std::thread(mover_loop, c);
+    return MOE_OK;
+}
+
+int moe_cache_set_streaming(moe_cache *c, const moe_stream_config *cfg) {
+    if (!c || !cfg) return fail(MOE_ERR_ARG, "null argument");
+    if (!cfg->on) {
+        if (c->st) {
+            if (!c->st->jobs.empty()) return fail(MOE_ERR_STATE, "streaming jobs still open: step first");
+            stream_free(c);
+            if (!c->host_only) drop_graphs(c);
+        }
+        return MOE_OK;
+    }
+    if (c->st) return fail(MOE_ERR_STATE, "streaming is on already");
+    if (!c->cfg.early_issue) return fail(MOE_ERR_STATE, "streaming needs early issue (LLAMA_MOE_EARLY_ISSUE=1)");
+    if (c->cfg.publish == MOE_PUBLISH_SORTED || c->replay || c->freeze)
+        return fail(MOE_ERR_STATE, "streaming runs without deterministic publication, replay or freeze");
+    if (c->map) return fail(MOE_ERR_STATE, "enable streaming before opening a map record");
+    if (cfg->top_k < 0 || cfg->top_k > mp::AHEAD_K) return fail(MOE_ERR_ARG, "top_k %d: 1..%d", cfg->top_k, mp::AHEAD_K);
+    Streamer *st = new Streamer();
+    st->per_layer = cfg->per_layer > 0 ? cfg->per_layer : 4;
+    st->reserve = cfg->reserve >= 0 ? cfg->reserve : 2;
+    st->top_k = cfg->top_k > 0 ? cfg->top_k : 8;
+    st->bytes_per_ns = cfg->gbps >= 1.0 ? cfg->gbps : 45.7;
+    // one push per expert by default: each host-to-device copy costs a fixed
+    // ~8 us on this GPU, so 512 KiB chunks move an expert at ~26 GB/s and a
+    // whole expert goes at ~44 GB/s
+    size_t chunk = (size_t)std::max(0, cfg->chunk_kib) << 10;
+    if (!chunk)
+        for (const Layer &ls : c->L) chunk = std::max(chunk, (size_t)ls.expert_bytes);
+    if (!chunk) chunk = (size_t)mp::expert_bytes(c->H, c->I, MOE_TYPE_Q6K);
+    st->planner = mps::Planner(chunk);
+    st->max_outstanding = std::max<size_t>(st->max_outstanding, 2 * chunk);
+    st->mark.assign(c->L.size() * (size_t)c->E, 0);
+    st->n_this_token.assign(c->L.size(), 0);
+    st->arrive_ns.assign(c->L.size(), 0);
+    c->st = st;
+    if (!c->host_only) {
+        HIPCHK(hipSetDevice(c->cfg.device));
+        const int r = stream_live_init(c, st);
+        if (r != MOE_OK) {
+            const std::string msg = g_err;
+            stream_free(c);
+            return fail(r, "%s", msg.c_str());
+        }
+        drop_graphs(c);
+    }
+    return MOE_OK;
+}
+
+int moe_cache_stream_stats(moe_cache *c, moe_stream_stats *out) {
+    if (!c || !out) return fail(MOE_ERR_ARG, "null argument");
+    memset(out, 0, sizeof(*out));
+    const Streamer *st = c->st;
+    if (!st) return MOE_OK;
+    uint64_t v[SN_COUNT];
+    memcpy(v, st->n, sizeof v);
+    v[SN_DROP_LATE] = st->planner.n_drop_late > v[SN_DROP_LATE] ? st->planner.n_drop_late : v[SN_DROP_LATE];
+    v[SN_DROP_POSTED] = st->planner.n_drop_posted > v[SN_DROP_POSTED] ? st->planner.n_drop_posted : v[SN_DROP_POSTED];
+    out->records = v[SN_RECORDS];
+    out->offered = v[SN_OFFERED];
+    out->landed = v[SN_LANDED];
+    out->in_time = v[SN_IN_TIME];
+    out->late = v[SN_LATE];
+    out->unused = v[SN_UNUSED];
+    out->dropped_late = v[SN_DROP_LATE];
+    out->dropped_posted = v[SN_DROP_POSTED];
+    out->not_sent = v[SN_NOT_SENT];
+    out->gpu_miss = v[SN_GPU_MISS];
+    out->bytes = v[SN_BYTES];
+    for (int d = 0; d < 3; ++d) {
+        out->lead_n[d] = st->lead_n[d];
+        out->lead_us[d] = st->lead_n[d] ? st->lead_sum[d] / (double)st->lead_n[d] / 1000.0 : 0.0;
+    }
+    out->tau_us = st->tau_ns / 1000.0;
+    out->failed = st->failed ? 1 : 0;
+    return MOE_OK;
+}
+
+int moe_cache_observe_gpu(moe_cache *c, int layer, const int32_t *ids, const int32_t *gpu_slots, int n_ids) {
+    if (!c || !ids || !gpu_slots || layer < 0 || layer >= (int)c->L.size() || n_ids <= 0)
+        return fail(MOE_ERR_ARG, "bad arguments");
+    return cache_observe(c, layer, ids, n_ids, 1, c->st ? gpu_slots : nullptr);
+}
+
+static int scripted(moe_cache *c) {
+    if (!c) return fail(MOE_ERR_ARG, "null cache");
+    if (!c->st) return fail(MOE_ERR_STATE, "streaming is off");
+    if (!c->host_only) return fail(MOE_ERR_STATE, "scripted streaming is for host-only caches (device < 0)");
+    return MOE_OK;
+}
+
+int moe_cache_stream_take(moe_cache *c, int layer, const int32_t *targets, const int32_t *n, const int32_t *ids,
+                          uint64_t now_ns, uint64_t t_ns, uint64_t expert_bytes) {
+    const int r = scripted(c);
+    if (r != MOE_OK) return r;
+    if (!targets || !n || !ids || layer < 0 || layer >= (int)c->L.size()) return fail(MOE_ERR_ARG, "bad arguments");
+    return stream_take(c, layer, targets, n, ids, now_ns, t_ns, expert_bytes);
+}
+
+int moe_cache_stream_posted(moe_cache *c, int layer) {
+    const int r = scripted(c);
+    if (r != MOE_OK) return r;
+    stream_posted(c, layer, 0);
+    return MOE_OK;
+}
+
+int moe_cache_stream_next(moe_cache *c, uint64_t free_at_ns, int hold_after, moe_stream_chunk *out) {
+    const int r = scripted(c);
+    if (r != MOE_OK) return r;
+    mps::Chunk ch;
+    if (!stream_next(c, free_at_ns, hold_after, ch)) return 0;
+    if (out) *out = moe_stream_chunk{ch.job, ch.offset, ch.len, ch.last};
+    return 1;
+}
+
+int moe_cache_stream_land(moe_cache *c, int job) {
+    const int r = scripted(c);
+    if (r != MOE_OK) return r;
+    stream_land(c, job);
+    return MOE_OK;
+}
+
+int moe_cache_stream_job(moe_cache *c, int job, int32_t *layer, int32_t *expert) {
+    if (!c || !c->st || job < 0 || job >= (int)c->st->jobs.size()) return -1;
+    if (layer) *layer = c->st->jobs[(size_t)job].li;
+    if (expert) *expert = c->st->planner.get(job).expert;
+    return c->st->jobs[(size_t)job].slot;
+}
+
+int moe_route_ahead(const moe_route_desc *d, const moe_ahead_desc *a, int32_t *out_n, int32_t *out_ids,
+                    void *stream) {
+    if (!d || !a || !out_n || !out_ids) return fail(MOE_ERR_ARG, "moe_route_ahead: null argument");
+    if (d->n_tok != 1 || d->logits) return fail(MOE_ERR_ARG, "moe_route_ahead: batch-1 router GEMV only");
+    if (a->n_targets < 1 || a->n_targets > 2 || a->top_k < 1 || a->top_k > mp::AHEAD_K || d->E > mp::MAX_E)
+        return fail(MOE_ERR_ARG, "moe_route_ahead: %d targets, top %d, %d experts", a->n_targets, a->top_k, d->E);
+    for (int t = 0; t < a->n_targets; ++t)
+        if (!a->W[t] || !a->r[t] || !a->tbl[t]) return fail(MOE_ERR_ARG, "moe_route_ahead: target %d incomplete", t);
+    hipStream_t st = (hipStream_t)stream;
+    mp::AheadPost *rec = nullptr;
+    float *alog = nullptr;
+    uint32_t *fresh = nullptr;
+    if (hipMalloc(&rec, sizeof(mp::AheadPost)) != hipSuccess || hipMalloc(&alog, 2 * (size_t)d->E * 4) != hipSuccess ||
+        hipMalloc(&fresh, 4) != hipSuccess) {
+        hipFree(rec);
+        hipFree(alog);
+        return fail(MOE_ERR_NOMEM, "moe_route_ahead scratch");
+    }
+    mp::RouteLaunch ah{};
+    ah.an = a->n_targets;
+    ah.ak = a->top_k;
+    for (int t = 0; t < a->n_targets; ++t) {
+        ah.aW[t] = a->W[t];
+        ah.ar[t] = a->r[t];
+        ah.atbl[t] = a->tbl[t];
+        ah.adummy[t] = a->dummy[t];
+        ah.atarget[t] = t;
+    }
+    ah.alog = alog;
+    ah.apost = rec;
+    ah.fresh = d->table ? fresh : nullptr;
+    int r = run_route(d, st, nullptr, nullptr, nullptr, &ah);
+    mp::AheadPost h{};
+    if (r == MOE_OK && (hipMemcpyAsync(&h, rec, sizeof h, hipMemcpyDeviceToHost, st) != hipSuccess ||
+                        hipStreamSynchronize(st) != hipSuccess))
+        r = fail(MOE_ERR_HIP, "moe_route_ahead: copy back");
+    hipFree(rec);
+    hipFree(alog);
+    hipFree(fresh);
+    if (r != MOE_OK) return r;
+    for (int t = 0; t < 2; ++t) {
+        out_n[t] = h.n[t];
+        for (int j = 0; j < mp::AHEAD_K; ++j) out_ids[t * mp::AHEAD_K + j] = j < h.n[t] ? h.ids[t][j] : -1;
+    }
+    return MOE_OK;
+}
+
+struct moe_planner {
+    mps::Planner p;
+    explicit moe_planner(uint64_t chunk) : p((size_t)chunk) {}
+};
+
+moe_planner *moe_planner_create(uint64_t chunk_bytes) { return chunk_bytes ? new moe_planner(chunk_bytes) : nullptr; }
+void moe_planner_destroy(moe_planner *p) { delete p; }
+void moe_planner_reset(moe_planner *p) {
+    if (p) p->p.reset();
+}
+int moe_planner_offer(moe_planner *p, int target, int32_t expert, uint64_t bytes, uint64_t deadline_ns) {
+    return p ? p->p.offer(target, expert, (size_t)bytes, deadline_ns) : -1;
+}
+void moe_planner_posted(moe_planner *p, int target) {
+    if (p) p->p.posted(target);
+}
+int moe_planner_next(moe_planner *p, uint64_t free_at_ns, double bytes_per_ns, int hold_after, moe_stream_chunk *out) {
+    if (!p || !out || !(bytes_per_ns > 0)) return 0;
+    mps::Chunk ch;
+    if (!p->p.next(free_at_ns, bytes_per_ns, hold_after, ch)) return 0;
+    *out = moe_stream_chunk{ch.job, ch.offset, ch.len, ch.last};
+    return 1;
+}
+int moe_planner_size(const moe_planner *p) { return p ? p->p.size() : 0; }
+int moe_planner_get(const moe_planner *p, int id, moe_planner_job *out) {
+    if (!p || !out || id < 0 || id >= p->p.size()) return -1;
+    const mps::PlanJob &j = p->p.get(id);
+    *out = moe_planner_job{j.target, j.expert, j.bytes, j.sent, j.deadline_ns, j.dropped, j.drop};
+    return 0;
+}
+void moe_planner_counters(const moe_planner *p, uint64_t out[4]) {
+    if (!p || !out) return;
+    out[0] = p->p.n_offered;
+    out[1] = p->p.n_dup;
+    out[2] = p->p.n_drop_late;
+    out[3] = p->p.n_drop_posted;
+}
+
 int moe_cache_frame(moe_cache *c, int layer, int32_t *out) {
     if (!c || !out || layer < 0 || layer >= (int)c->L.size()) return fail(MOE_ERR_ARG, "bad arguments");
     const Layer &ls = c->L[layer];
@@ -1364,15 +2092,17 @@ static int sidecar_serve(moe_cache *c, int l, uint32_t seq) {
     int kk[16];
     int n = 0, r = 0;
     for (int k = 0; k < c->K; ++k) {
-        const int id = p.ids[k];
-        if (id < 0 || id >= ls.E || ls.expert_slot[id] >= 0) continue;     // outside the store, or resident
+        const int id = p.ids[k], slot = p.slots[k];
+        if (id < 0 || id >= ls.E || (slot >= 0 && slot < ls.S)) continue;  // outside the store, or read from a slot
         if (r++ % c->sc_den < c->sc_num) {
             kk[n] = k;
             e[n] = {ls.store_host + (size_t)id * ls.expert_bytes, c->sc_q8x.data(), c->sc_y.data() + (size_t)n * c->H};
             ++n;
         }
     }
+    if (n) c->sc_computing.store(l, std::memory_order_relaxed);
     mpc::experts(c->team, e, n, c->H, c->I, ls.down_type, c->sc_h.data(), c->sc_q8h.data());
+    c->sc_computing.store(-1, std::memory_order_relaxed);
     for (int j = 0; j < n; ++j)
         memcpy(c->sc_rows + ((size_t)l * c->K + kk[j]) * c->H, c->sc_y.data() + (size_t)j * c->H, (size_t)c->H * 4);
     c->n_cpu_served += n;
@@ -1429,6 +2159,7 @@ static int decode_layer_impl(moe_cache *c, int layer, const float *x, const floa
                              int32_t *ids_dev, float *w_dev, hipStream_t st, hipEvent_t *ev, bool stage = false,
                              bool sidecar = false);
 
+
 int moe_decode_layer(moe_cache *c, int layer, const float *x, const float *bias, float *out, int32_t *ids_dev,
                      float *w_dev, void *stream) {
     return decode_layer_impl(c, layer, x, bias, out, ids_dev, w_dev, (hipStream_t)stream, nullptr);
@@ -1456,7 +2187,28 @@ static int decode_layer_impl(moe_cache *c, int layer, const float *x, const floa
     // ev (timing mode), 12 per layer, stamped by the dispatches themselves:
     // [0,1] route_logits [2,3] route_select [4,5] gate/up (resident or all)
     // [6,7] down (resident or all) [8,9] gate/up absent [10,11] down absent
-    int r = run_route(&rd, st, ev, sidecar ? c->sc_post_d + layer : nullptr, c->d_seq);
+    // just-in-time streaming: this layer's router launch also scores the next
+    // layers' routers and posts the record the mover thread works from
+    mp::RouteLaunch look{};
+    const Streamer *stm = c->st && c->st->live ? c->st : nullptr;
+    if (stm) {
+        const auto &tg = stm->targets[(size_t)layer];
+        for (int t = 0; t < 2; ++t) {
+            if (tg[t] < 0) continue;
+            const int i = look.an++;
+            look.aW[i] = c->L[(size_t)tg[t]].router;
+            look.ar[i] = stm->ratio + ((size_t)layer * 2 + t) * c->H;
+            look.atbl[i] = c->d_tbl + (size_t)tg[t] * c->E;
+            look.adummy[i] = c->L[(size_t)tg[t]].S;
+            look.atarget[i] = tg[t];
+        }
+        look.ak = stm->top_k;
+        look.alayer = layer;
+        look.alog = stm->alog;
+        look.apost = stm->post_d + layer;
+        look.fresh = stm->fresh + layer;
+    }
+    int r = run_route(&rd, st, ev, sidecar ? c->sc_post_d + layer : nullptr, c->d_seq, stm ? &look : nullptr);
     if (r != MOE_OK) return r;
     moe_experts_desc ed{};
     ed.ids = ids; ed.slots = slots; ed.w = w;
@@ -1480,6 +2232,7 @@ static int decode_layer_impl(moe_cache *c, int layer, const float *x, const floa
         a.cpu_num = c->sc_num;
         a.cpu_den = c->sc_den;
     }
+    if (stm) a.fresh = stm->fresh + layer;
     uint8_t *ws = (uint8_t *)ed.workspace;
     a.h = (float *)ws;
     size_t o = align_up((size_t)(ed.K + 1) * ed.I * 4, 256);
@@ -1566,13 +2319,37 @@ int moe_decode_token(moe_cache *c, const float *x, const float *bias, float *out
     // CPU-assisted serving: this token's sequence number, for the posts and
     // the answers of every layer
     const bool sc = c->sc_den > 0;
+    Streamer *stm = c->st && c->st->live ? c->st : nullptr;
     uint32_t seq = 0;
-    if (sc) {
+    if (sc || stm) {
         seq = ++c->sc_seq;
         if (seq == 0 || seq == mp::SC_ABORT) seq = c->sc_seq = 1;
         *c->h_seq = seq;
         HIPCHK(hipMemcpyAsync(c->d_seq, c->h_seq, 4, hipMemcpyHostToDevice, st));
     }
+    // streaming: the mover serves this token's lookahead records
+    bool mover_on = false;
+    if (stm && !stm->failed) {
+        stm->seq = seq;
+        stm->stop.store(false, std::memory_order_relaxed);
+        {
+            std::lock_guard<std::mutex> lk(stm->m);
+            stm->gen++;
+        }
+        stm->cv.notify_one();
+        mover_on = true;
+    }
+    // the mover is told the token's GPU work is over and hands the
+    // bookkeeping back (it waits for the copies it queued); bounded
+    auto mover_drain = [&]() -> int {
+        if (!mover_on) return MOE_OK;
+        mover_on = false;
+        stm->stop.store(true, std::memory_order_release);
+        std::unique_lock<std::mutex> lk(stm->m);
+        if (!stm->cv_done.wait_for(lk, std::chrono::seconds(2), [&] { return stm->gen_done == stm->gen; }))
+            return fail(MOE_ERR_HIP, "stream mover did not finish within 2 s");
+        return MOE_OK;
+    };
     auto abort_joins = [&] {        // end every join kernel still waiting
         if (sc)
             for (int l = 0; l < NL; ++l) *(volatile uint32_t *)&c->sc_resp[l].seq = mp::SC_ABORT;
@@ -1587,9 +2364,11 @@ int moe_decode_token(moe_cache *c, const float *x, const float *bias, float *out
             if (r != MOE_OK) {
                 abort_joins();
                 hipStreamSynchronize(st);
+                mover_drain();
                 return r;
             }
         }
+
     } else {
         const int key = bias ? 1 : 0;
         const int mode = c->split;
@@ -1602,10 +2381,14 @@ int moe_decode_token(moe_cache *c, const float *x, const float *bias, float *out
                 r = decode_layer_impl(c, l, c->x_buf + (size_t)l * c->H, key ? c->bias_buf + (size_t)l * c->E : nullptr,
                                       c->out_buf + (size_t)l * c->H, nullptr, nullptr, c->cap_stream, nullptr, stage,
                                       sc);
+
             hipGraph_t g = nullptr;
             const hipError_t ec = hipStreamEndCapture(c->cap_stream, &g);
-            if (r != MOE_OK) { if (g) hipGraphDestroy(g); return r; }
-            if (ec != hipSuccess) return fail(MOE_ERR_HIP, "hipStreamEndCapture: %s", hipGetErrorString(ec));
+            if (r != MOE_OK || ec != hipSuccess) {
+                if (g) hipGraphDestroy(g);
+                mover_drain();
+                return r != MOE_OK ? r : fail(MOE_ERR_HIP, "hipStreamEndCapture: %s", hipGetErrorString(ec));
+            }
             c->g[key] = g;
             HIPCHK(hipGraphInstantiate(&c->gx[key], g, nullptr, nullptr, 0));
             c->g_mode[key] = mode;
@@ -1623,7 +2406,12 @@ int moe_decode_token(moe_cache *c, const float *x, const float *bias, float *out
         if (serve_err != MOE_OK) abort_joins();
     }
     HIPCHK(hipMemcpyAsync(c->h_ids, c->d_ids, (size_t)NL * c->K * 4, hipMemcpyDeviceToHost, st));
-    HIPCHK(hipStreamSynchronize(st));
+    HIPCHK(hipMemcpyAsync(c->h_slots, c->d_slots, (size_t)NL * c->K * 4, hipMemcpyDeviceToHost, st));
+    const hipError_t sync_err = hipStreamSynchronize(st);
+    const int drain_err = mover_drain();
+    if (sync_err != hipSuccess) return fail(MOE_ERR_HIP, "decode: %s", hipGetErrorString(sync_err));
+    if (drain_err != MOE_OK) return drain_err;
+    if (stm && stm->failed) return fail(MOE_ERR_HIP, "streaming stopped on a copy queue error");
     if (sc) {
         bool late = false;
         for (int l = 0; l < NL; ++l) {
@@ -1650,8 +2438,8 @@ int moe_decode_token(moe_cache *c, const float *x, const float *bias, float *out
             c->kt.n_layers++;
             const Layer &ls = c->L[l];
             for (int k = 0; k < c->K; ++k) {
-                const int id = c->h_ids[(size_t)l * c->K + k];
-                const bool res = id >= 0 && id < ls.E && ls.expert_slot[id] >= 0;
+                const int gs = c->h_slots[(size_t)l * c->K + k];
+                const bool res = gs >= 0 && gs < ls.S;
                 (res ? c->kt.gateup_hbm_bytes : c->kt.gateup_host_bytes) += gu_b;
                 (res ? c->kt.down_hbm_bytes : c->kt.down_host_bytes) += ls.expert_bytes - gu_b;
             }
@@ -1662,14 +2450,14 @@ int moe_decode_token(moe_cache *c, const float *x, const float *bias, float *out
         }
     }
     // which routed experts the kernels read from the store (and staged): the
-    // tables have not changed since the route, so absent now = absent then
+    // slots the GPU read say which were absent
     if (stage) {
         for (int l = 0; l < NL; ++l) {
             Layer &ls = c->L[l];
             int r = 0;         // (absent experts the CPU served were not read by the kernels)
             for (int k = 0; k < c->K; ++k) {
-                const int id = c->h_ids[(size_t)l * c->K + k];
-                const bool absent = id >= 0 && id < ls.E && ls.expert_slot[id] < 0;
+                const int id = c->h_ids[(size_t)l * c->K + k], gs = c->h_slots[(size_t)l * c->K + k];
+                const bool absent = id >= 0 && id < ls.E && !(gs >= 0 && gs < ls.S);
                 const bool cpu = absent && sc && r % c->sc_den < c->sc_num;
                 r += absent;
                 ls.staged[k] = absent && !cpu ? id : -1;
@@ -1679,7 +2467,8 @@ int moe_decode_token(moe_cache *c, const float *x, const float *bias, float *out
     // (early issue starts uploads inside observe: staged copies apply there too)
     c->stage_valid = stage;
     int r = MOE_OK;
-    for (int l = 0; l < NL && r == MOE_OK; ++l) r = cache_observe(c, l, c->h_ids + (size_t)l * c->K, c->K, 1);
+    for (int l = 0; l < NL && r == MOE_OK; ++l)
+        r = cache_observe(c, l, c->h_ids + (size_t)l * c->K, c->K, 1, stm ? c->h_slots + (size_t)l * c->K : nullptr);
     if (r == MOE_OK) {
         if (ids_host) memcpy(ids_host, c->h_ids, (size_t)NL * c->K * 4);
         r = cache_step(c);

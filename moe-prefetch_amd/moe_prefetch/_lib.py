@@ -81,6 +81,32 @@ class KernelTimes(ctypes.Structure):
                                    "down_host_bytes")]
 
 
+class StreamConfig(ctypes.Structure):
+    _fields_ = [("on", I32), ("per_layer", I32), ("reserve", I32), ("top_k", I32), ("gbps", ctypes.c_double),
+                ("chunk_kib", I32)]
+
+
+class StreamStats(ctypes.Structure):
+    _fields_ = [(n, U64) for n in ("records", "offered", "landed", "in_time", "late", "unused", "dropped_late",
+                                   "dropped_posted", "not_sent", "gpu_miss", "bytes")] + \
+               [("lead_us", ctypes.c_double * 3), ("lead_n", U64 * 3), ("tau_us", ctypes.c_double),
+                ("failed", I32)]
+
+
+class StreamChunk(ctypes.Structure):
+    _fields_ = [("job", I32), ("offset", U64), ("len", U64), ("last", I32)]
+
+
+class AheadDesc(ctypes.Structure):
+    _fields_ = [("n_targets", I32), ("top_k", I32), ("W", P * 2), ("r", P * 2), ("tbl", P * 2),
+                ("dummy", I32 * 2)]
+
+
+class PlannerJob(ctypes.Structure):
+    _fields_ = [("target", I32), ("expert", I32), ("bytes", U64), ("sent", U64), ("deadline_ns", U64),
+                ("dropped", I32), ("drop", I32)]
+
+
 # name -> (restype, argtypes); mirrors include/moe_prefetch.h one to one
 SIGNATURES = {
     "moe_last_error": (ctypes.c_char_p, []),
@@ -133,6 +159,25 @@ SIGNATURES = {
     "moe_cache_freeze": (ctypes.c_int, [P]),
     "moe_probe_stream_read": (ctypes.c_int, [P, SZ, SZ, ctypes.c_int, ctypes.POINTER(ctypes.c_double), P]),
     "moe_cache_map_replay": (ctypes.c_int, [P, ctypes.c_char_p]),
+    "moe_cache_set_norm": (ctypes.c_int, [P, ctypes.c_int, P, ctypes.c_int]),
+    "moe_cache_set_streaming": (ctypes.c_int, [P, ctypes.POINTER(StreamConfig)]),
+    "moe_cache_stream_stats": (ctypes.c_int, [P, ctypes.POINTER(StreamStats)]),
+    "moe_cache_observe_gpu": (ctypes.c_int, [P, ctypes.c_int, P, P, ctypes.c_int]),
+    "moe_cache_stream_take": (ctypes.c_int, [P, ctypes.c_int, P, P, P, U64, U64, U64]),
+    "moe_cache_stream_posted": (ctypes.c_int, [P, ctypes.c_int]),
+    "moe_cache_stream_next": (ctypes.c_int, [P, U64, ctypes.c_int, ctypes.POINTER(StreamChunk)]),
+    "moe_cache_stream_land": (ctypes.c_int, [P, ctypes.c_int]),
+    "moe_cache_stream_job": (ctypes.c_int, [P, ctypes.c_int, ctypes.POINTER(I32), ctypes.POINTER(I32)]),
+    "moe_route_ahead": (ctypes.c_int, [ctypes.POINTER(RouteDesc), ctypes.POINTER(AheadDesc), P, P, P]),
+    "moe_planner_create": (P, [U64]),
+    "moe_planner_destroy": (None, [P]),
+    "moe_planner_reset": (None, [P]),
+    "moe_planner_offer": (ctypes.c_int, [P, ctypes.c_int, I32, U64, U64]),
+    "moe_planner_posted": (None, [P, ctypes.c_int]),
+    "moe_planner_next": (ctypes.c_int, [P, U64, ctypes.c_double, ctypes.c_int, ctypes.POINTER(StreamChunk)]),
+    "moe_planner_size": (ctypes.c_int, [P]),
+    "moe_planner_get": (ctypes.c_int, [P, ctypes.c_int, ctypes.POINTER(PlannerJob)]),
+    "moe_planner_counters": (None, [P, P]),
     "moe_cache_kernel_times": (ctypes.c_int, [P, ctypes.POINTER(KernelTimes)]),
     "moe_decode_layer": (ctypes.c_int, [P, ctypes.c_int, P, P, P, P, P, P]),
     "moe_decode_token": (ctypes.c_int, [P, P, P, P, P, P]),

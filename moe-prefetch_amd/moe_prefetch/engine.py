@@ -103,6 +103,14 @@ class MoeCache:
             c.freeze()
         if int(g("LLAMA_MOE_SIDECAR", "0") or "0") != 0:
             c.set_sidecar(max(1, int(g("LLAMA_MOE_SIDECAR_THREADS", "8"))))
+        c.stream_knobs = None
+        if int(g("LLAMA_MOE_STREAM", "0") or "0") != 0:
+            # applied by set_streaming() once routers and norm weights are registered
+            c.stream_knobs = dict(per_layer=max(1, int(g("LLAMA_MOE_STREAM_PER_LAYER", "4"))),
+                                  reserve=max(0, int(g("LLAMA_MOE_STREAM_RESERVE", "2"))),
+                                  top_k=min(8, max(1, int(g("LLAMA_MOE_STREAM_TOPK", "8")))),
+                                  gbps=max(1.0, float(g("LLAMA_MOE_STREAM_GBPS", "45.7"))),
+                                  chunk_kib=max(0, int(g("LLAMA_MOE_STREAM_CHUNK_KIB", "0"))))
         return c
 
     def close(self):
@@ -207,6 +215,62 @@ class MoeCache:
         """LLAMA_MOE_MAP_REPLAY: every step ends with the placement recorded in
         `path` (a trace_open map file).  Freezes the cache."""
         check(lib().moe_cache_map_replay(self.h, str(path).encode()), "map_replay")
+
+    # -- router lookahead and just-in-time streaming ------------------------------
+    def set_norm(self, layer, g):
+        """The RMS-norm weight g_L [H] behind layer L's router input (host array)."""
+        g = np.ascontiguousarray(g, np.float32)
+        check(lib().moe_cache_set_norm(self.h, layer, g.ctypes.data, g.size), "set_norm")
+
+    def set_streaming(self, on=True, per_layer=4, reserve=2, top_k=8, gbps=45.7, chunk_kib=0):
+        """LLAMA_MOE_STREAM: layer L's router launch predicts layers L+1 and L+2
+        from L's input; a mover thread copies the predicted absent experts in
+        deadline order and flips their table words as they land.  Needs early
+        issue, the routers, the host stores and the norm weights (live cache)."""
+        cfg = _lib.StreamConfig(int(bool(on)), int(per_layer), int(reserve), int(top_k), float(gbps), int(chunk_kib))
+        check(lib().moe_cache_set_streaming(self.h, ctypes.byref(cfg)), "set_streaming")
+
+    def stream_stats(self):
+        s = _lib.StreamStats()
+        check(lib().moe_cache_stream_stats(self.h, ctypes.byref(s)), "stream_stats")
+        out = {n: getattr(s, n) for n, _ in _lib.StreamStats._fields_ if n not in ("lead_us", "lead_n")}
+        out["lead_us"] = [s.lead_us[1], s.lead_us[2]]
+        out["lead_n"] = [s.lead_n[1], s.lead_n[2]]
+        return out
+
+    def observe_gpu(self, layer, ids, gpu_slots):
+        ids = np.ascontiguousarray(ids, np.int32)
+        gs = np.ascontiguousarray(gpu_slots, np.int32)
+        check(lib().moe_cache_observe_gpu(self.h, layer, ids.ctypes.data, gs.ctypes.data, ids.size), "observe_gpu")
+
+    # scripted streaming (host-only caches): the mover's steps one at a time
+    def stream_take(self, layer, targets, n, ids, now_ns, t_ns, expert_bytes):
+        targets = np.ascontiguousarray(targets, np.int32)
+        n = np.ascontiguousarray(n, np.int32)
+        ids = np.ascontiguousarray(ids, np.int32).reshape(16)
+        r = lib().moe_cache_stream_take(self.h, layer, targets.ctypes.data, n.ctypes.data, ids.ctypes.data,
+                                        int(now_ns), int(t_ns), int(expert_bytes))
+        if r < 0:
+            check(r, "stream_take")
+        return r
+
+    def stream_posted(self, layer):
+        check(lib().moe_cache_stream_posted(self.h, layer), "stream_posted")
+
+    def stream_next(self, free_at_ns, hold_after=-1):
+        c = _lib.StreamChunk()
+        r = lib().moe_cache_stream_next(self.h, int(free_at_ns), int(hold_after), ctypes.byref(c))
+        if r < 0:
+            check(r, "stream_next")
+        return (c.job, c.offset, c.len, bool(c.last)) if r == 1 else None
+
+    def stream_land(self, job):
+        check(lib().moe_cache_stream_land(self.h, job), "stream_land")
+
+    def stream_job(self, job):
+        li, e = ctypes.c_int32(), ctypes.c_int32()
+        slot = lib().moe_cache_stream_job(self.h, job, ctypes.byref(li), ctypes.byref(e))
+        return (li.value, e.value, slot) if slot >= 0 else None
 
     def sidecar_log(self, max_rows=65536):
         """[rows][3] float32: host wait us, host compute us, experts computed,

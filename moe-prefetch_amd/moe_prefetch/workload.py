@@ -11,6 +11,22 @@ variant uses intermediate 512):
                  token's experts
   prior48        the single-layer shape stacked 48 deep with the cache prior
                  delta on resident experts (no steering)
+  residual48     stacked48's shape routed by the routers themselves on a
+                 synthetic residual stream (no steering), so that layer L's
+                 input predicts layers L+1 and L+2 as a real model's does:
+                 the router lookahead workload
+
+Residual stream (residual48): residual_{t,l} = MU m + z_{t,l} with a shared
+direction m; z_{t,0} = RHO z_{t-1,0} + sqrt(1 - RHO^2) n_t and, per layer,
+v_{t,l} = RHO v_{t-1,l} + sqrt(1 - RHO^2) u_{t,l}, z_{t,l} = BETA z_{t,l-1}
++ sqrt(1 - BETA^2) v_{t,l}; the router input is x_{t,l} = rmsnorm(residual)
+* g_l with g_l = 1 + 0.1 N(0, 1).  BETA sets how much of layer l+1's input
+layer l already holds, RHO the token-to-token reuse, MU the popularity skew.
+MU 1.2, RHO 0.7, BETA 0.975 give, at 56 slots, about 20 misses per token and
+a one-layer-ahead recall of 72% of the misses at 73% precision -- the
+reference's probe on Qwen3-30B-A3B measured 21.4, 75% and 68%
+(docs/superpowers/specs/2026-10-04-just-in-time-expert-streaming-design.md,
+section 4).
 
 Routing steering: the router still runs W x for every layer; a per-token bias
 of +STEER on the 8 target experts of that (token, layer) makes them the top-8
@@ -32,6 +48,8 @@ MASK64 = (1 << 64) - 1
 
 # vector kinds of moe_synth_vec
 KIND_ROUTER, KIND_X = 0, 1
+KIND_RES_MEAN, KIND_RES_TOKEN, KIND_RES_LAYER, KIND_NORM = 3, 4, 5, 6
+RESID_MU, RESID_RHO, RESID_BETA, NORM_SIGMA = 1.2, 0.7, 0.975, 0.1
 
 
 class SplitMix:
@@ -97,3 +115,40 @@ def steering_bias(targets_by_layer, n_experts=E):
         for t in range(T):
             bias[t, l, tg[t]] = STEER
     return bias
+
+
+def residual_stream(seed, n_tokens, n_layers, torch, device, stream_ptr, H=H, mu=RESID_MU, rho=RESID_RHO,
+                    beta=RESID_BETA):
+    """Router inputs x [T][L][H] f32 and norm weights g [L][H] f32 of the
+    residual-stream workload, on the device (innovations from moe_synth_vec,
+    recursions in elementwise f32)."""
+    T, L = n_tokens, n_layers
+    f32 = torch.float32
+
+    def vec(kind, na, nb, sigma=1.0):
+        out = torch.empty((na, nb, H), dtype=f32, device=device)
+        _lib.check(_lib.lib().moe_synth_vec(seed, kind, 0, na, 0, nb, H, sigma, out.data_ptr(), stream_ptr),
+                   "residual stream")
+        return out
+
+    m = vec(KIND_RES_MEAN, 1, 1)[0, 0]
+    n_tok = vec(KIND_RES_TOKEN, T, 1)[:, 0]                  # [T][H]
+    u = vec(KIND_RES_LAYER, T, L)                            # [T][L][H]
+    g = 1.0 + vec(KIND_NORM, L, 1, NORM_SIGMA)[:, 0]         # [L][H]
+    cr, cb = math.sqrt(1.0 - rho * rho), math.sqrt(1.0 - beta * beta)
+    v = torch.empty_like(u)                                  # v[t][l], l >= 1 used
+    z0 = torch.empty_like(n_tok)
+    for t in range(T):
+        if t == 0:
+            v[0] = u[0]
+            z0[0] = n_tok[0]
+        else:
+            v[t] = rho * v[t - 1] + cr * u[t]
+            z0[t] = rho * z0[t - 1] + cr * n_tok[t]
+    z = torch.empty_like(u)
+    z[:, 0] = z0
+    for l in range(1, L):
+        z[:, l] = beta * z[:, l - 1] + cb * v[:, l]
+    res = mu * m + z
+    x = res * torch.rsqrt((res * res).mean(dim=2, keepdim=True)) * g
+    return x.contiguous(), g.contiguous()

@@ -12,6 +12,9 @@
  *   map trace 0008:417-489 (record and replay)
  *   heat file 0007:431-485 (load/save), 0007:568-621 (warm start), 0007:745-752
  *   freeze    0008:496-500, 825-832
+ *   streaming 0010:1096-1129 (map frame one step late), 0010:1183-1210 (account),
+ *             0010:1466-1530 (take), 0010:1722-1760 (adopt), 0010:1138-1175 (pool target,
+ *             issue skip, observe skip)
  * The predictor/evictor and speculative probation are not restated (out of
  * scope); slot_protect is kept at 0, which is what it is when no speculative
  * upload exists.
@@ -56,6 +59,14 @@ typedef struct {
     int hold;
 } job_t;
 
+typedef struct {
+    int li, slot, d;
+    int landed, in_time, late;
+} sjob_t;
+
+enum { ST_RECORDS, ST_OFFERED, ST_LANDED, ST_IN_TIME, ST_LATE, ST_UNUSED, ST_DROP_LATE, ST_DROP_POSTED,
+       ST_NOT_SENT, ST_GPU_MISS, ST_BYTES };
+
 struct or_cache {
     int n_layers, E;
     or_knobs k;
@@ -69,6 +80,24 @@ struct or_cache {
     FILE *route, *map, *replay;
     char *heat_path;
     int freeze, replay_err;
+    /* just-in-time streaming (0010): jobs of this token, one per planner job */
+    int st_on, st_per_layer, st_reserve;
+    double st_bytes_per_ns, st_tau_ns;
+    uint64_t st_margin_ns;
+    or_planner *st_planner;
+    sjob_t *sjobs;
+    int n_sjobs, cap_sjobs;
+    int32_t *st_mark;               /* [layer][E]: job + 1 while streamed this token */
+    int *st_n_this_token;
+    uint32_t st_last_layer;
+    uint64_t st_last_t_ns;
+    uint64_t st_n[11];              /* records, offered, landed, in time, late, unused, dropped late,
+                                       dropped posted, not sent, GPU misses, bytes */
+    int32_t *rec_frame;             /* [layer][S] frame held back one step (map record) */
+    uint64_t rec_step;
+    int rec_have;
+    int32_t *rec_used;              /* (layer, slot, expert) triples used in time this step */
+    int n_rec_used;
 };
 
 static void push_job(or_cache *c, int li, int e, int slot) {
@@ -154,6 +183,24 @@ or_cache *or_cache_create(int n_layers, int n_experts, const int32_t *slots, con
     return c;
 }
 
+static int layer_off(const or_cache *c, int li) {
+    int o = 0;
+    for (int l = 0; l < li; ++l) o += c->L[l].S;
+    return o;
+}
+
+static void write_frame(or_cache *c, uint64_t step, const int32_t *frame) {
+    fprintf(c->map, "step %llu\n", (unsigned long long)step);
+    for (int l = 0; l < c->n_layers; ++l) {
+        const layer_t *ls = &c->L[l];
+        const int32_t *f = frame + layer_off(c, l);
+        fprintf(c->map, "map %d", ls->il);
+        for (int s = 0; s < ls->S; ++s) fprintf(c->map, " %d", f[s]);
+        fputc('\n', c->map);
+    }
+    fflush(c->map);
+}
+
 void or_cache_destroy(or_cache *c) {
     if (!c) return;
     for (int l = 0; l < c->n_layers; ++l) {
@@ -163,10 +210,13 @@ void or_cache_destroy(or_cache *c) {
         free(ls->pending); free(ls->tbl_mirror); free(ls->prior_mirror);
         free(ls->heat); free(ls->miss_last); free(ls->miss_prev); free(ls->use_count);
     }
+    if (c->map && c->rec_have) write_frame(c, c->rec_step, c->rec_frame);   /* the last boundary */
     if (c->route) fclose(c->route);
     if (c->map) fclose(c->map);
     if (c->replay) fclose(c->replay);
     free(c->heat_path);
+    or_planner_destroy(c->st_planner);
+    free(c->sjobs); free(c->st_mark); free(c->st_n_this_token); free(c->rec_frame); free(c->rec_used);
     free(c->L);
     free(c->jobs);
     free(c->holds);
@@ -208,17 +258,29 @@ static void replay_frame(or_cache *c) {
 static void map_frame(or_cache *c) {
     if (c->replay && !c->replay_err) replay_frame(c);
     if (!c->map) return;
-    fprintf(c->map, "step %llu\n", (unsigned long long)c->n_steps);
-    int32_t *pub = (int32_t *)malloc(sizeof(int32_t) * 1024);
-    for (int l = 0; l < c->n_layers; ++l) {
-        const layer_t *ls = &c->L[l];
-        or_cache_frame(c, l, pub);
-        fprintf(c->map, "map %d", ls->il);
-        for (int s = 0; s < ls->S; ++s) fprintf(c->map, " %d", pub[s]);
-        fputc('\n', c->map);
+    const int total = layer_off(c, c->n_layers);
+    int32_t *frame = (int32_t *)malloc(sizeof(int32_t) * (size_t)(total + 1));
+    for (int l = 0; l < c->n_layers; ++l) or_cache_frame(c, l, frame + layer_off(c, l));
+    if (!c->st_on) {
+        write_frame(c, c->n_steps, frame);
+        free(frame);
+        return;
     }
-    free(pub);
-    fflush(c->map);
+    /* 0010:1096-1129: the token after a boundary also used the experts that
+     * streamed in before their layer read its table; the boundary's frame is
+     * written one step late with those experts in the slots they used */
+    if (c->rec_have) {
+        for (int u = 0; u < c->n_rec_used; ++u) {
+            const int li = c->rec_used[3 * u], slot = c->rec_used[3 * u + 1], e = c->rec_used[3 * u + 2];
+            c->rec_frame[layer_off(c, li) + slot] = e;
+        }
+        write_frame(c, c->rec_step, c->rec_frame);
+    }
+    c->n_rec_used = 0;
+    free(c->rec_frame);
+    c->rec_frame = frame;
+    c->rec_step = c->n_steps;
+    c->rec_have = 1;
 }
 
 int or_cache_trace_open(or_cache *c, const char *route_path, const char *map_path) {
@@ -246,6 +308,7 @@ static int issue_uploads(or_cache *c, int li, const int32_t *ids, int n, int bud
         const int id = ids[i];
         if (id < 0 || id >= ls->E) continue;
         if (ls->expert_slot[id] >= 0) continue;
+        if (c->st_on && c->st_mark[li * c->E + id]) continue;      /* being streamed this token */
         if (ls->n_free <= min_keep) break;
         int dup = 0;
         for (int j = 0; j < c->n_jobs; ++j)
@@ -261,12 +324,21 @@ static int issue_uploads(or_cache *c, int li, const int32_t *ids, int n, int bud
     return issued;
 }
 
-void or_cache_observe(or_cache *c, int li, const int32_t *ids, int n_ids, int n_tok) {
+static int pool_target_of(const or_cache *c) {
+    if (c->freeze) return 0;
+    return c->k.max_inserts + (c->st_on ? c->st_reserve : 0);
+}
+
+/* gslots (batch 1 with streaming): the slots the GPU used, n_slots = absent */
+static void observe_body(or_cache *c, int li, const int32_t *ids, int n_ids, int n_tok, const int32_t *gslots) {
     layer_t *ls = &c->L[li];
     if (c->route) {
         fprintf(c->route, "route %llu %d %d %d", (unsigned long long)c->n_steps, ls->il, n_ids, n_tok);
-        for (int i = 0; i < n_ids * n_tok; ++i)
-            fprintf(c->route, " %d:%d", ids[i], (ids[i] >= 0 && ids[i] < ls->E) ? ls->expert_slot[ids[i]] : -1);
+        for (int i = 0; i < n_ids * n_tok; ++i) {
+            int slot = (ids[i] >= 0 && ids[i] < ls->E) ? ls->expert_slot[ids[i]] : -1;
+            if (gslots) slot = gslots[i] >= ls->S ? -1 : gslots[i];   /* 0010:1147-1154 */
+            fprintf(c->route, " %d:%d", ids[i], slot);
+        }
         fputc('\n', c->route);
     }
     for (int t = 0; t < n_tok; ++t) {
@@ -276,6 +348,7 @@ void or_cache_observe(or_cache *c, int li, const int32_t *ids, int n_ids, int n_
             if (ls->heat) ls->heat[id] += 1.0f;
             if (ls->use_count) ls->use_count[id]++;
             const int slot = ls->expert_slot[id];
+            if (slot < 0 && c->st_on && c->st_mark[li * c->E + id]) continue;  /* the GPU's table decides */
             if (slot >= 0) {
                 ls->n_hit++;
                 ls->slot_last_use[slot] = ++c->clock;
@@ -292,7 +365,7 @@ void or_cache_observe(or_cache *c, int li, const int32_t *ids, int n_ids, int n_
         }
     }
     if (c->k.early_issue) {
-        const int pool_target = c->freeze ? 0 : c->k.max_inserts;
+        const int pool_target = pool_target_of(c);
         const int next_victim = c->k.admit_mode == 0 ? -1 :
             (ls->n_free > pool_target ? -1 : lru_resident(ls));
         if (c->k.admit_mode == 0) {
@@ -307,6 +380,182 @@ void or_cache_observe(or_cache *c, int li, const int32_t *ids, int n_ids, int n_
             issue_uploads(c, li, adm, n, c->k.max_inserts, 0);
         }
     }
+}
+
+void or_cache_observe(or_cache *c, int li, const int32_t *ids, int n_ids, int n_tok) {
+    observe_body(c, li, ids, n_ids, n_tok, NULL);
+}
+
+/* 0010:1183-1210: the GPU's slots say whether each streamed expert made it */
+static void stream_account(or_cache *c, int li, const int32_t *ids, const int32_t *gslots, int n_ids) {
+    for (int i = 0; i < n_ids; ++i) {
+        const int id = ids[i];
+        layer_t *ls0 = &c->L[li];
+        if (id < 0 || id >= ls0->E) continue;
+        const int miss = gslots[i] >= ls0->S;
+        const int m = c->st_mark[li * c->E + id];
+        if (!m) { c->st_n[ST_GPU_MISS] += miss; continue; }
+        sjob_t *j = &c->sjobs[m - 1];
+        layer_t *ls = &c->L[j->li];
+        if (!miss && !j->in_time) {
+            j->in_time = 1;
+            c->st_n[ST_IN_TIME]++;
+            ls->n_hit++;
+        } else if (miss && !j->in_time && !j->late) {
+            j->late = 1;
+            c->st_n[ST_LATE]++;
+            c->st_n[ST_GPU_MISS]++;
+            ls->n_miss++;
+        }
+    }
+}
+
+void or_cache_observe_gpu(or_cache *c, int li, const int32_t *ids, const int32_t *gslots, int n_ids) {
+    observe_body(c, li, ids, n_ids, 1, c->st_on ? gslots : NULL);
+    if (c->st_on) stream_account(c, li, ids, gslots, n_ids);
+}
+
+int or_cache_stream_enable(or_cache *c, int per_layer, int reserve, double gbps, size_t chunk_bytes) {
+    if (!c->k.early_issue || !c->k.batch_tables || c->k.deterministic || c->replay || c->freeze || c->map)
+        return -1;
+    if (c->st_on) return 0;
+    c->st_on = 1;
+    c->st_per_layer = per_layer < 1 ? 1 : per_layer;
+    c->st_reserve = reserve < 0 ? 0 : reserve;
+    c->st_bytes_per_ns = gbps < 1.0 ? 1.0 : gbps;
+    c->st_tau_ns = 103000.0;
+    c->st_margin_ns = 5000;
+    c->st_planner = or_planner_create(chunk_bytes ? chunk_bytes : 512 * 1024);
+    c->st_mark = (int32_t *)calloc((size_t)c->n_layers * (size_t)c->E, sizeof(int32_t));
+    c->st_n_this_token = (int *)calloc((size_t)c->n_layers, sizeof(int));
+    c->st_last_layer = 0xffffffffu;
+    return 0;
+}
+
+/* 0010:1466-1530: one lookahead record (source layer `layer`, GPU time t_ns)
+ * becomes planner jobs, each with a free slot */
+int or_cache_stream_take(or_cache *c, int layer, const int32_t *targets, const int32_t *n, const int32_t *ids,
+                         uint64_t now_ns, uint64_t t_ns, size_t expert_bytes) {
+    if (!c->st_on) return -1;
+    if (c->st_last_layer != 0xffffffffu && (uint32_t)layer == c->st_last_layer + 1 && t_ns > c->st_last_t_ns) {
+        const double dt = (double)(t_ns - c->st_last_t_ns);
+        if (dt > 10000.0 && dt < 1000000.0) c->st_tau_ns = 0.9 * c->st_tau_ns + 0.1 * dt;
+    }
+    c->st_last_layer = (uint32_t)layer;
+    c->st_last_t_ns = t_ns;
+    c->st_n[ST_RECORDS]++;
+    int taken = 0;
+    for (int t = 0; t < 2; ++t) {
+        const int T = targets[t];
+        if (T < 0 || T >= c->n_layers) continue;
+        layer_t *ls = &c->L[T];
+        const int d = T - layer;
+        const uint64_t lead = (uint64_t)(d * c->st_tau_ns);
+        const uint64_t deadline = now_ns + (lead > c->st_margin_ns ? lead - c->st_margin_ns : 0);
+        for (int j = 0; j < n[t] && j < 8; ++j) {
+            const int e = ids[8 * t + j];
+            if (e < 0 || e >= ls->E || ls->expert_slot[e] >= 0) continue;
+            if (c->st_mark[T * c->E + e]) {
+                or_planner_offer(c->st_planner, T, e, expert_bytes, deadline);     /* may tighten */
+                continue;
+            }
+            if (c->st_n_this_token[T] >= c->st_per_layer) continue;
+            if (ls->n_free <= c->k.max_inserts) { c->st_n[ST_NOT_SENT]++; continue; }
+            int dup = 0;
+            for (int q = 0; q < c->n_jobs; ++q)
+                if (c->jobs[q].li == T && c->jobs[q].expert == e) { dup = 1; break; }
+            if (dup) continue;
+            const int id = or_planner_offer(c->st_planner, T, e, expert_bytes, deadline);
+            if (id < 0) continue;
+            if (c->n_sjobs == c->cap_sjobs) {
+                c->cap_sjobs = c->cap_sjobs ? 2 * c->cap_sjobs : 64;
+                c->sjobs = (sjob_t *)realloc(c->sjobs, sizeof(sjob_t) * (size_t)c->cap_sjobs);
+            }
+            sjob_t sj = {T, ls->free_slots[--ls->n_free], d, 0, 0, 0};
+            ls->slot_in_flight[sj.slot] = 1;
+            c->sjobs[c->n_sjobs++] = sj;
+            c->st_mark[T * c->E + e] = id + 1;
+            c->st_n_this_token[T]++;
+            c->st_n[ST_OFFERED]++;
+            taken++;
+        }
+    }
+    return taken;
+}
+
+void or_cache_stream_posted(or_cache *c, int layer) {
+    if (c->st_on) or_planner_posted(c->st_planner, layer);
+}
+
+int or_cache_stream_next(or_cache *c, uint64_t free_at_ns, int hold_after, or_chunk *out) {
+    if (!c->st_on) return 0;
+    const int r = or_planner_next(c->st_planner, free_at_ns, c->st_bytes_per_ns, hold_after, out);
+    if (r) c->st_n[ST_BYTES] += out->len;
+    return r;
+}
+
+void or_cache_stream_land(or_cache *c, int job) {
+    if (!c->st_on || job < 0 || job >= c->n_sjobs || c->sjobs[job].landed) return;
+    c->sjobs[job].landed = 1;
+    c->st_n[ST_LANDED]++;
+}
+
+/* slot and target layer of a job (-1 when there is none) */
+int or_cache_stream_job(const or_cache *c, int job, int32_t *layer, int32_t *expert) {
+    if (!c->st_on || job < 0 || job >= c->n_sjobs) return -1;
+    or_planner_job pj;
+    or_planner_get(c->st_planner, job, &pj);
+    if (layer) *layer = c->sjobs[job].li;
+    if (expert) *expert = pj.expert;
+    return c->sjobs[job].slot;
+}
+
+void or_cache_stream_stats(const or_cache *c, uint64_t out[11]) {
+    for (int i = 0; i < 11; ++i) out[i] = c->st_n[i];
+}
+
+/* 0010:1722-1760 (mover idle): landed experts join the cache, the slots of the
+ * others go back to the pool */
+static void stream_adopt(or_cache *c) {
+    c->n_rec_used = 0;
+    if (c->n_sjobs) c->rec_used = (int32_t *)realloc(c->rec_used, sizeof(int32_t) * 3 * (size_t)c->n_sjobs);
+    for (int k = 0; k < c->n_sjobs; ++k) {
+        const sjob_t *sj = &c->sjobs[k];
+        or_planner_job pj;
+        or_planner_get(c->st_planner, k, &pj);
+        layer_t *ls = &c->L[sj->li];
+        const int e = pj.expert;
+        ls->slot_in_flight[sj->slot] = 0;
+        if (sj->in_time) {
+            c->rec_used[3 * c->n_rec_used] = sj->li;
+            c->rec_used[3 * c->n_rec_used + 1] = sj->slot;
+            c->rec_used[3 * c->n_rec_used + 2] = e;
+            c->n_rec_used++;
+        }
+        if (sj->landed && ls->expert_slot[e] >= 0) {
+            ls->free_slots[ls->n_free++] = sj->slot;
+            c->st_n[ST_UNUSED] += !sj->in_time && !sj->late;
+            ls->tbl_dirty = 1;
+        } else if (sj->landed) {
+            ls->slot_expert[sj->slot] = e;
+            ls->expert_slot[e] = sj->slot;
+            ls->slot_last_use[sj->slot] = sj->in_time || sj->late ? ++c->clock : 1;
+            set_table_entry(c, ls, e, sj->slot);
+            c->n_published++;
+            if (!sj->in_time && !sj->late) c->st_n[ST_UNUSED]++;
+        } else {
+            ls->free_slots[ls->n_free++] = sj->slot;
+        }
+        c->st_mark[sj->li * c->E + e] = 0;
+    }
+    uint64_t pc[4];
+    or_planner_counters(c->st_planner, pc);
+    c->st_n[ST_DROP_LATE] = pc[2];
+    c->st_n[ST_DROP_POSTED] = pc[3];
+    c->n_sjobs = 0;
+    or_planner_reset(c->st_planner);
+    for (int l = 0; l < c->n_layers; ++l) c->st_n_this_token[l] = 0;
+    c->st_last_layer = 0xffffffffu;
 }
 
 static int job_cmp(const void *a, const void *b) {
@@ -336,6 +585,7 @@ void or_cache_step(or_cache *c) {
         c->n_published++;
     }
     free(done);
+    if (c->st_on) stream_adopt(c);      /* after the uploads: an expert both copied is kept once */
 
     c->n_steps++;
 
@@ -373,7 +623,7 @@ void or_cache_step(or_cache *c) {
             continue;
         }
         ls->n_pending = 0;
-        const int pool_target = c->freeze ? 0 : c->k.max_inserts;
+        const int pool_target = pool_target_of(c);
         while (ls->n_free < pool_target) {
             int slot = -1;
             uint64_t best = U64MAX;

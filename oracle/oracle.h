@@ -40,6 +40,12 @@
  *       reference's engine-recorded traces
  *       (artifacts/x3_logits_1791160431756057451/{0..3}.routes-record.txt) and
  *       requiring every placement frame of {0..3}.map.txt.
+ *   or_ahead, or_planner_*
+ *       router lookahead (k_moe_ahead_scores/post, patches/0010-team-and-streaming.patch:382-474)
+ *       and the just-in-time copy planner (moe_planner, 0010:777-909).  or_ahead is
+ *       pinned by brute-force ranking (fp64 scores of the same products, crafted
+ *       ties) and the table filter; the planner by the reference's own planner
+ *       cases (cpp/test-moe-planner.cpp) and brute-force EDF checks.
  *
  * Canonical router order (shared with the GPU kernel):
  *   logit[e]  = 64 lane partials p_j, p_j accumulated with fmaf over
@@ -179,6 +185,64 @@ void      or_cache_freeze(or_cache *c);
  * match; or_cache_replay_error() != 0 once a frame was missing or malformed. */
 int       or_cache_map_replay(or_cache *c, const char *path);
 int       or_cache_replay_error(const or_cache *c);
+
+/* ---- router lookahead and the copy planner (stream.c) ---------------------
+ * or_ahead: the k best experts of target router W [E][H] applied to x * r
+ * (best first, lower id on a tie, a NaN ranks with -inf), keeping those with
+ * table[e] == dummy; returns how many were kept (ids[0..n-1]), -1 on bad sizes.
+ * scores_out[E] (optional) receives the scores. */
+int or_ahead(int E, int H, int k, const float *W, const float *x, const float *r,
+             const int32_t *table, int32_t dummy, float *scores_out, int32_t *ids);
+
+enum { OR_DROP_NONE = 0, OR_DROP_LATE = 1, OR_DROP_POSTED = 2 };
+typedef struct or_planner or_planner;
+typedef struct {
+    int job;
+    size_t offset, len;
+    int last;
+} or_chunk;
+typedef struct {
+    int target;
+    int32_t expert;
+    size_t bytes, sent;
+    uint64_t deadline_ns;
+    int dropped, drop;
+} or_planner_job;
+or_planner *or_planner_create(size_t chunk_bytes);
+void or_planner_destroy(or_planner *p);
+void or_planner_reset(or_planner *p);
+/* the new job's id, or -1 (a job exists -- an earlier deadline tightens it --
+ * or the target has read its table) */
+int  or_planner_offer(or_planner *p, int target, int32_t expert, size_t bytes, uint64_t deadline_ns);
+void or_planner_posted(or_planner *p, int target);
+/* 1 and the next chunk in *out, or 0 when nothing can go now */
+int  or_planner_next(or_planner *p, uint64_t free_at_ns, double bytes_per_ns, int hold_after, or_chunk *out);
+int  or_planner_size(const or_planner *p);
+void or_planner_get(const or_planner *p, int id, or_planner_job *out);
+/* offered, duplicates, dropped late, dropped posted */
+void or_planner_counters(const or_planner *p, uint64_t out[4]);
+
+/* ---- just-in-time streaming in the state machine (0010) -------------------
+ * Enable before any map trace is opened (chunk_bytes: largest copy per push,
+ * 0 = 512 KiB, the reference's); needs early_issue and batch_tables,
+ * and neither deterministic publication, replay nor freeze (-1 otherwise).
+ * take: one lookahead record of source layer `layer` (targets[2], n[2],
+ * ids[2][8]) at host time now_ns and GPU time t_ns; returns the jobs created.
+ * posted: `layer` has read its table.  next: the planner's next chunk
+ * (returns 0 when none).  land: job's copy and table word have landed.
+ * observe_gpu: batch-1 observation with the slots the GPU used (n_slots =
+ * absent), which also accounts streamed experts as in time or late.
+ * stats: records, offered, landed, in time, late, unused, dropped late,
+ * dropped posted, not sent (no free slot), GPU misses, bytes. */
+int  or_cache_stream_enable(or_cache *c, int per_layer, int reserve, double gbps, size_t chunk_bytes);
+int  or_cache_stream_take(or_cache *c, int layer, const int32_t *targets, const int32_t *n, const int32_t *ids,
+                          uint64_t now_ns, uint64_t t_ns, size_t expert_bytes);
+void or_cache_stream_posted(or_cache *c, int layer);
+int  or_cache_stream_next(or_cache *c, uint64_t free_at_ns, int hold_after, or_chunk *out);
+void or_cache_stream_land(or_cache *c, int job);
+int  or_cache_stream_job(const or_cache *c, int job, int32_t *layer, int32_t *expert);
+void or_cache_observe_gpu(or_cache *c, int layer, const int32_t *ids, const int32_t *gslots, int n_ids);
+void or_cache_stream_stats(const or_cache *c, uint64_t out[11]);
 
 #ifdef __cplusplus
 }

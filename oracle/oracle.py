@@ -50,6 +50,20 @@ class Stats(ctypes.Structure):
         "n_admit_ok", "n_admit_denied", "n_table_flushes")]
 
 
+class Chunk(ctypes.Structure):
+    _fields_ = [("job", ctypes.c_int), ("offset", ctypes.c_size_t), ("len", ctypes.c_size_t), ("last", ctypes.c_int)]
+
+
+class PlannerJob(ctypes.Structure):
+    _fields_ = [("target", ctypes.c_int), ("expert", ctypes.c_int32), ("bytes", ctypes.c_size_t),
+                ("sent", ctypes.c_size_t), ("deadline_ns", ctypes.c_uint64), ("dropped", ctypes.c_int),
+                ("drop", ctypes.c_int)]
+
+
+STREAM_STATS = ("records", "offered", "landed", "in_time", "late", "unused", "dropped_late", "dropped_posted",
+                "not_sent", "gpu_miss", "bytes")
+DROP_NONE, DROP_LATE, DROP_POSTED = 0, 1, 2
+
 P = ctypes.c_void_p
 I32 = ctypes.c_int32
 I64 = ctypes.c_int64
@@ -96,6 +110,25 @@ def _declare(L):
     d("or_cache_freeze", None, P)
     d("or_cache_map_replay", ctypes.c_int, P, ctypes.c_char_p)
     d("or_cache_replay_error", ctypes.c_int, P)
+    d("or_ahead", ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, P, P, P, P, I32, P, P)
+    d("or_planner_create", P, ctypes.c_size_t)
+    d("or_planner_destroy", None, P)
+    d("or_planner_reset", None, P)
+    d("or_planner_offer", ctypes.c_int, P, ctypes.c_int, I32, ctypes.c_size_t, ctypes.c_uint64)
+    d("or_planner_posted", None, P, ctypes.c_int)
+    d("or_planner_next", ctypes.c_int, P, ctypes.c_uint64, ctypes.c_double, ctypes.c_int, ctypes.POINTER(Chunk))
+    d("or_planner_size", ctypes.c_int, P)
+    d("or_planner_get", None, P, ctypes.c_int, ctypes.POINTER(PlannerJob))
+    d("or_planner_counters", None, P, P)
+    d("or_cache_stream_enable", ctypes.c_int, P, ctypes.c_int, ctypes.c_int, ctypes.c_double, ctypes.c_size_t)
+    d("or_cache_stream_take", ctypes.c_int, P, ctypes.c_int, P, P, P, ctypes.c_uint64, ctypes.c_uint64,
+      ctypes.c_size_t)
+    d("or_cache_stream_posted", None, P, ctypes.c_int)
+    d("or_cache_stream_next", ctypes.c_int, P, ctypes.c_uint64, ctypes.c_int, ctypes.POINTER(Chunk))
+    d("or_cache_stream_land", None, P, ctypes.c_int)
+    d("or_cache_stream_job", ctypes.c_int, P, ctypes.c_int, P, P)
+    d("or_cache_observe_gpu", None, P, ctypes.c_int, P, P, ctypes.c_int)
+    d("or_cache_stream_stats", None, P, P)
 
 
 def _p(a):
@@ -176,6 +209,65 @@ def route_logits(logits, K, prior=None):
     prior = None if prior is None else np.ascontiguousarray(prior, np.float32)
     lib().or_route_logits(E, K, _p(logits), _p(prior), _p(ids), _p(w), _p(probs))
     return ids, w, probs
+
+
+def ahead(W, x, r, table, dummy, k=8):
+    """Router lookahead: the k best experts of W [E, H] applied to x * r, best
+    first, lower id on a tie; those with table[e] == dummy.  -> (ids, scores)."""
+    W = np.ascontiguousarray(W, np.float32)
+    x = np.ascontiguousarray(x, np.float32)
+    r = np.ascontiguousarray(r, np.float32)
+    table = np.ascontiguousarray(table, np.int32)
+    E, H = W.shape
+    ids = np.empty(k, np.int32)
+    scores = np.empty(E, np.float32)
+    n = lib().or_ahead(E, H, k, _p(W), _p(x), _p(r), _p(table), int(dummy), _p(scores), _p(ids))
+    if n < 0:
+        raise ValueError("or_ahead: bad sizes")
+    return ids[:n].copy(), scores
+
+
+class Planner:
+    """Earliest-deadline-first copy planner (moe_planner)."""
+
+    def __init__(self, chunk_bytes=512 * 1024):
+        self.h = lib().or_planner_create(chunk_bytes)
+
+    def close(self):
+        if self.h:
+            lib().or_planner_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        self.close()
+
+    def offer(self, target, expert, nbytes, deadline_ns):
+        return lib().or_planner_offer(self.h, target, expert, nbytes, deadline_ns)
+
+    def posted(self, target):
+        lib().or_planner_posted(self.h, target)
+
+    def next(self, free_at_ns, bytes_per_ns, hold_after=-1):
+        c = Chunk()
+        if not lib().or_planner_next(self.h, free_at_ns, bytes_per_ns, hold_after, ctypes.byref(c)):
+            return None
+        return c.job, c.offset, c.len, bool(c.last)
+
+    def reset(self):
+        lib().or_planner_reset(self.h)
+
+    def size(self):
+        return lib().or_planner_size(self.h)
+
+    def get(self, i):
+        j = PlannerJob()
+        lib().or_planner_get(self.h, i, ctypes.byref(j))
+        return {n: getattr(j, n) for n, _ in PlannerJob._fields_}
+
+    def counters(self):
+        out = np.zeros(4, np.uint64)
+        lib().or_planner_counters(self.h, _p(out))
+        return dict(zip(("offered", "dup", "drop_late", "drop_posted"), (int(v) for v in out)))
 
 
 # ---- expert chain -----------------------------------------------------------
@@ -303,3 +395,42 @@ class Cache:
         s = Stats()
         lib().or_cache_stats(self.h, ctypes.byref(s))
         return {n: getattr(s, n) for n, _ in Stats._fields_}
+
+    # ---- just-in-time streaming ----
+    def stream_enable(self, per_layer=4, reserve=2, gbps=45.7, chunk_bytes=512 * 1024):
+        if lib().or_cache_stream_enable(self.h, per_layer, reserve, gbps, chunk_bytes) != 0:
+            raise ValueError("streaming needs early issue and batched tables, no replay/freeze/deterministic, "
+                             "and no open map trace")
+
+    def stream_take(self, layer, targets, n, ids, now_ns, t_ns, expert_bytes):
+        targets = np.ascontiguousarray(targets, np.int32)
+        n = np.ascontiguousarray(n, np.int32)
+        ids = np.ascontiguousarray(ids, np.int32).reshape(16)
+        return lib().or_cache_stream_take(self.h, layer, _p(targets), _p(n), _p(ids), now_ns, t_ns, expert_bytes)
+
+    def stream_posted(self, layer):
+        lib().or_cache_stream_posted(self.h, layer)
+
+    def stream_next(self, free_at_ns, hold_after=-1):
+        c = Chunk()
+        if not lib().or_cache_stream_next(self.h, free_at_ns, hold_after, ctypes.byref(c)):
+            return None
+        return c.job, c.offset, c.len, bool(c.last)
+
+    def stream_land(self, job):
+        lib().or_cache_stream_land(self.h, job)
+
+    def stream_job(self, job):
+        li, e = ctypes.c_int32(), ctypes.c_int32()
+        slot = lib().or_cache_stream_job(self.h, job, ctypes.byref(li), ctypes.byref(e))
+        return (li.value, e.value, slot) if slot >= 0 else None
+
+    def observe_gpu(self, layer, ids, gslots):
+        ids = np.ascontiguousarray(ids, np.int32)
+        gslots = np.ascontiguousarray(gslots, np.int32)
+        lib().or_cache_observe_gpu(self.h, layer, _p(ids), _p(gslots), ids.size)
+
+    def stream_stats(self):
+        out = np.zeros(11, np.uint64)
+        lib().or_cache_stream_stats(self.h, _p(out))
+        return dict(zip(STREAM_STATS, (int(v) for v in out)))

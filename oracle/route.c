@@ -38,7 +38,7 @@ float or_expf(float x) {
     return p * s;
 }
 
-static float row_logit(int H, const float *w, const float *x) {
+float or_row_logit(int H, const float *w, const float *x) {
     float p[64];
     for (int j = 0; j < 64; ++j) {
         float acc = 0.0f;
@@ -107,7 +107,7 @@ void or_route_space(int E, int H, int K, const float *W, const float *x, const f
                     float *w, int32_t *slots, float *probs) {
     float logits[1024];
     for (int e = 0; e < E; ++e) {
-        logits[e] = row_logit(H, W + (size_t)e * H, x);
+        logits[e] = or_row_logit(H, W + (size_t)e * H, x);
         if (bias) logits[e] = logits[e] + bias[e];
     }
     softmax_topk(E, K, logits, prior, prior_on_logits, ids, w, probs);

@@ -9,7 +9,7 @@ import torch
 
 import moe_prefetch
 from moe_prefetch import MoeCache, _lib
-from moe_prefetch.workload import KIND_ROUTER, KIND_X, steering_bias, zipf_targets
+from moe_prefetch.workload import KIND_ROUTER, KIND_X, residual_stream, steering_bias, zipf_targets
 from oracle import oracle as O
 
 H, E, K = 2048, 128, 8
@@ -47,7 +47,7 @@ def synth_experts_dev(seed, layer, e0, n, I, dt, out_ptr, stride):
 
 class Rig:
     def __init__(self, slots, down_types, T, I=768, seed=42, steer=True, zipf_s=1.1, reuse=0.6, E=E, shared=False,
-                 **knobs):
+                 residual=False, **knobs):
         self.nl = len(slots)
         self.slots, self.down_types, self.T, self.I, self.seed = list(slots), list(down_types), T, I, seed
         self.E = E
@@ -67,8 +67,13 @@ class Rig:
                 self.shared.append(None)
         self.W = torch.empty((self.nl, E, H), dtype=torch.float32, device=self.dev)
         _lib.check(L().moe_synth_vec(seed, KIND_ROUTER, 0, self.nl, 0, E, H, 0.02, self.W.data_ptr(), stream()), "W")
-        self.x = torch.empty((T, self.nl, H), dtype=torch.float32, device=self.dev)
-        _lib.check(L().moe_synth_vec(seed, KIND_X, 0, T, 0, self.nl, H, 1.0, self.x.data_ptr(), stream()), "x")
+        self.g = None
+        if residual:            # routing by the routers on a residual stream (lookahead workload)
+            self.x, self.g = residual_stream(seed, T, self.nl, torch, self.dev, stream())
+            steer = False
+        else:
+            self.x = torch.empty((T, self.nl, H), dtype=torch.float32, device=self.dev)
+            _lib.check(L().moe_synth_vec(seed, KIND_X, 0, T, 0, self.nl, H, 1.0, self.x.data_ptr(), stream()), "x")
         self.bias = None
         if steer:
             tg = [zipf_targets(seed, l, T, n_experts=E, s=zipf_s, reuse=reuse) for l in range(self.nl)]
@@ -82,6 +87,8 @@ class Rig:
             self.cache.set_router(l, self.W[l])
             if self.shared[l] is not None:
                 self.cache.set_shared(l, self.shared[l])
+            if self.g is not None:
+                self.cache.set_norm(l, self.g[l].cpu().numpy())
         self.shared_h = [None if sh is None else sh.cpu().numpy() for sh in self.shared]
         self.Wh = self.W.cpu().numpy()
         self.xh = self.x.cpu().numpy()
