@@ -340,7 +340,8 @@ def cache_summary(s0, s1, steps):
             "missed_per_token": round((s1["n_miss"] - s0["n_miss"]) / steps, 2),
             "uploaded_per_token": round((s1["n_scheduled"] - s0["n_scheduled"]) / steps, 2),
             "publication_wait_ms_per_token": round((s1["publication_wait_us"] - s0["publication_wait_us"])
-                                                   / 1e3 / steps, 4)}
+                                                   / 1e3 / steps, 4),
+            "host_boundary_ms_per_token": round((s1["host_boundary_us"] - s0["host_boundary_us"]) / 1e3 / steps, 4)}
 
 
 def kernel_report(kt, n_tok, steps, s0, s1):

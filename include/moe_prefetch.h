@@ -209,6 +209,8 @@ typedef struct {
     uint64_t n_staged;                           /* uploads copied from the HBM staging area */
     uint64_t n_cpu_served;                       /* absent experts computed on the host CPU */
     double sidecar_wait_us, sidecar_cpu_us;      /* host time waiting for the GPU's posts / computing */
+    double host_boundary_us;                     /* batch-1 decode: host time after the token's GPU work
+                                                    (observe, step, table flush) before it returns */
 } moe_cache_stats;
 
 typedef struct {

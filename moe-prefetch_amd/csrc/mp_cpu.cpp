@@ -157,89 +157,187 @@ static float dot_q6k_port(const uint8_t *row, const uint8_t *q8, int nb) {
     return acc;
 }
 
-// ---- AVX-512 VNNI dots ---------------------------------------------------------
-#define MPC_VNNI __attribute__((target("avx512f,avx512bw,avx512vl,avx512vnni")))
+// ---- AVX-512 dots, NR rows at a time --------------------------------------------
+// The rows share the activation loads; per super-block each row's integer sums
+// are exact (u8 codes x s8 Q8_K values with maddubs: pairs stay below 2^15;
+// dpwssd with 16-bit scales), the rows' sums are reduced together, and the fp32
+// steps of every row run in the scalar order (scale term, then min term; no
+// fused multiply-add), so each row's result is the portable dot's bit for bit.
+#define MPC_AVX512 __attribute__((target("avx512f,avx512bw,avx512vl,avx512vnni,f16c")))
 
-// Q4_K: 32 code bytes of a 64-value group -> [low nibbles | high nibbles] =
-// sub-blocks 2g and 2g+1, against the group's 64 Q8_K values: dpbusd lanes
-// 0-7 hold sub-block 2g, lanes 8-15 sub-block 2g+1; times the six-bit scales.
-MPC_VNNI static float dot_q4k_vnni(const uint8_t *row, const uint8_t *q8, int nb) {
-    float acc = 0.0f;
-    const __m256i m4 = _mm256_set1_epi8(0x0F);
-    for (int i = 0; i < nb; ++i, row += Q4K_BYTES, q8 += Q8K_BYTES) {
-        int sc[8], mn[8];
-        for (int j = 0; j < 8; ++j) q4k_scale_min(row + 4, j, sc[j], mn[j]);
-        __m512i a = _mm512_setzero_si512();
-        for (int g = 0; g < 4; ++g) {
-            const __m256i raw = _mm256_loadu_si256((const __m256i *)(row + 16 + 32 * g));
-            const __m256i lo = _mm256_and_si256(raw, m4);
-            const __m256i hi = _mm256_and_si256(_mm256_srli_epi16(raw, 4), m4);
-            const __m512i wv = _mm512_inserti64x4(_mm512_castsi256_si512(lo), hi, 1);
-            const __m512i xv = _mm512_loadu_si512((const void *)(q8 + 4 + 64 * g));
-            const __m512i p = _mm512_dpbusd_epi32(_mm512_setzero_si512(), wv, xv);
-            const __m512i s = _mm512_inserti64x4(_mm512_castsi256_si512(_mm256_set1_epi32(sc[2 * g])),
-                                                 _mm256_set1_epi32(sc[2 * g + 1]), 1);
-            a = _mm512_add_epi32(a, _mm512_mullo_epi32(p, s));
-        }
-        const int32_t sumi = _mm512_reduce_add_epi32(a);
-        int32_t summ = 0;
-        for (int j = 0; j < 8; ++j) summ += mn[j] * (i16_at(q8 + 4 + QK + 4 * j) + i16_at(q8 + 4 + QK + 4 * j + 2));
-        const float dx = f32_at(q8);
-        const float d = mp::h2f(u16_at(row)) * dx, dm = mp::h2f(u16_at(row + 2)) * dx;
-        acc = acc + d * (float)sumi;
-        acc = acc - dm * (float)summ;
-    }
-    return acc;
+MPC_AVX512 static inline __m128i fold4(__m512i v) {
+    const __m256i h = _mm256_add_epi32(_mm512_castsi512_si256(v), _mm512_extracti64x4_epi64(v, 1));
+    return _mm_add_epi32(_mm256_castsi256_si128(h), _mm256_extracti128_si256(h, 1));
 }
 
-// Q6_K: per 128-value half, the six-bit codes of quarters (0,1) and (2,3)
-// as two 64-byte vectors against the matching Q8_K values; 16-value groups
-// are 4 dpbusd lanes each, so lane group i carries scale i.  The -32 offset
-// is taken as 32 * (sum of the group's Q8_K values), from a dpbusd by ones.
-MPC_VNNI static float dot_q6k_vnni(const uint8_t *row, const uint8_t *q8, int nb) {
-    float acc = 0.0f;
-    const __m256i m4 = _mm256_set1_epi8(0x0F), m30 = _mm256_set1_epi8(0x30);
-    const __m512i ones = _mm512_set1_epi8(1);
-    for (int i = 0; i < nb; ++i, row += Q6K_BYTES, q8 += Q8K_BYTES) {
-        const __m128i sc16 = _mm_loadu_si128((const __m128i *)(row + 192));
-        __m512i a = _mm512_setzero_si512();
-        for (int h = 0; h < 2; ++h) {
-            const __m256i ql0 = _mm256_loadu_si256((const __m256i *)(row + 64 * h));
-            const __m256i ql1 = _mm256_loadu_si256((const __m256i *)(row + 64 * h + 32));
-            const __m256i qh = _mm256_loadu_si256((const __m256i *)(row + 128 + 32 * h));
-            const __m256i q0 = _mm256_or_si256(_mm256_and_si256(ql0, m4), _mm256_and_si256(_mm256_slli_epi16(qh, 4), m30));
-            const __m256i q1 = _mm256_or_si256(_mm256_and_si256(ql1, m4), _mm256_and_si256(_mm256_slli_epi16(qh, 2), m30));
-            const __m256i q2 = _mm256_or_si256(_mm256_and_si256(_mm256_srli_epi16(ql0, 4), m4), _mm256_and_si256(qh, m30));
-            const __m256i q3 = _mm256_or_si256(_mm256_and_si256(_mm256_srli_epi16(ql1, 4), m4),
-                                               _mm256_and_si256(_mm256_srli_epi16(qh, 2), m30));
-            for (int p = 0; p < 2; ++p) {
-                const __m512i wv = p == 0 ? _mm512_inserti64x4(_mm512_castsi256_si512(q0), q1, 1)
-                                          : _mm512_inserti64x4(_mm512_castsi256_si512(q2), q3, 1);
-                const __m512i xv = _mm512_loadu_si512((const void *)(q8 + 4 + 128 * h + 64 * p));
-                const __m512i dq = _mm512_dpbusd_epi32(_mm512_setzero_si512(), wv, xv);
-                const __m512i sx = _mm512_dpbusd_epi32(_mm512_setzero_si512(), ones, xv);
-                const __m512i t = _mm512_sub_epi32(dq, _mm512_slli_epi32(sx, 5));
-                // scales 8h+4p .. 8h+4p+3, each on 4 lanes
-                const int b0 = 8 * h + 4 * p;
-                const __m128i idx = _mm_setr_epi8(b0, b0, b0, b0, b0 + 1, b0 + 1, b0 + 1, b0 + 1, b0 + 2, b0 + 2, b0 + 2,
-                                                  b0 + 2, b0 + 3, b0 + 3, b0 + 3, b0 + 3);
-                const __m512i s = _mm512_cvtepi8_epi32(_mm_shuffle_epi8(sc16, idx));
-                a = _mm512_add_epi32(a, _mm512_mullo_epi32(t, s));
-            }
+// [sum(a0), sum(a1), sum(a2), sum(a3)] of four 16-lane int32 vectors
+MPC_AVX512 static inline __m128i hsum4(__m512i a0, __m512i a1, __m512i a2, __m512i a3) {
+    const __m128i c0 = fold4(a0), c1 = fold4(a1), c2 = fold4(a2), c3 = fold4(a3);
+    const __m128i u0 = _mm_add_epi32(_mm_unpacklo_epi32(c0, c1), _mm_unpackhi_epi32(c0, c1));   // c0 c1 c0 c1
+    const __m128i u1 = _mm_add_epi32(_mm_unpacklo_epi32(c2, c3), _mm_unpackhi_epi32(c2, c3));   // c2 c3 c2 c3
+    return _mm_add_epi32(_mm_unpacklo_epi64(u0, u1), _mm_unpackhi_epi64(u0, u1));
+}
+
+// the 8 six-bit scales and mins of a Q4_K super-block (12 bytes at s) as two
+// 64-bit words of bytes: j < 4 from the low six bits of bytes j and j + 4;
+// j >= 4 from the nibbles of byte j + 4 and the top two bits of bytes j - 4, j
+static inline void q4k_scales8(const uint8_t *s, uint64_t &sc, uint64_t &mn) {
+    uint32_t u0, u1, u2;
+    memcpy(&u0, s, 4);
+    memcpy(&u1, s + 4, 4);
+    memcpy(&u2, s + 8, 4);
+    const uint32_t sc_lo = u0 & 0x3f3f3f3fu, mn_lo = u1 & 0x3f3f3f3fu;
+    const uint32_t sc_hi = (u2 & 0x0f0f0f0fu) | (((u0 >> 6) & 0x03030303u) << 4);
+    const uint32_t mn_hi = ((u2 >> 4) & 0x0f0f0f0fu) | (((u1 >> 6) & 0x03030303u) << 4);
+    sc = (uint64_t)sc_lo | ((uint64_t)sc_hi << 32);
+    mn = (uint64_t)mn_lo | ((uint64_t)mn_hi << 32);
+}
+
+template <int NR>
+MPC_AVX512 static void rows_q4k_vnni(const uint8_t *row0, size_t stride, const uint8_t *q8, int nb, float *out) {
+    const __m512i m4 = _mm512_set1_epi8(0x0F);
+    // int16 lane index of the scale for groups g: lanes 0-15 sub-block 2g, 16-31 sub-block 2g + 1
+    __m512i gidx[4];
+    for (int g = 0; g < 4; ++g)
+        gidx[g] = _mm512_inserti64x4(_mm512_castsi256_si512(_mm256_set1_epi16((short)(2 * g))),
+                                     _mm256_set1_epi16((short)(2 * g + 1)), 1);
+    __m128 acc = _mm_setzero_ps();
+    for (int i = 0; i < nb; ++i) {
+        const uint8_t *qb = q8 + (size_t)i * Q8K_BYTES;
+        __m512i xv[4];
+        for (int g = 0; g < 4; ++g) xv[g] = _mm512_loadu_si512((const void *)(qb + 4 + 64 * g));
+        const __m256i bs = _mm256_loadu_si256((const __m256i *)(qb + 4 + QK));   // 16 int16 block sums
+        __m512i si[4], sm[4];
+        alignas(16) uint16_t dh[8] = {0, 0, 0, 0, 0, 0, 0, 0}, mh[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+        for (int r = 0; r < NR; ++r) {
+            const uint8_t *b = row0 + (size_t)r * stride + (size_t)i * Q4K_BYTES;
+            uint64_t sc8, mn8;
+            q4k_scales8(b + 4, sc8, mn8);
+            const __m512i sc16 = _mm512_castsi128_si512(_mm_cvtepu8_epi16(_mm_cvtsi64_si128((long long)sc8)));
+            const __m128i mn16 = _mm_cvtepu8_epi16(_mm_cvtsi64_si128((long long)mn8));
+            const __m512i raw01 = _mm512_loadu_si512((const void *)(b + 16));        // groups 0, 1
+            const __m512i raw23 = _mm512_loadu_si512((const void *)(b + 16 + 64));   // groups 2, 3
+            const __m512i lo01 = _mm512_and_si512(raw01, m4), hi01 = _mm512_and_si512(_mm512_srli_epi16(raw01, 4), m4);
+            const __m512i lo23 = _mm512_and_si512(raw23, m4), hi23 = _mm512_and_si512(_mm512_srli_epi16(raw23, 4), m4);
+            const __m512i w[4] = {_mm512_shuffle_i64x2(lo01, hi01, 0x44), _mm512_shuffle_i64x2(lo01, hi01, 0xEE),
+                                  _mm512_shuffle_i64x2(lo23, hi23, 0x44), _mm512_shuffle_i64x2(lo23, hi23, 0xEE)};
+            __m512i a = _mm512_setzero_si512();
+            for (int g = 0; g < 4; ++g)
+                a = _mm512_dpwssd_epi32(a, _mm512_maddubs_epi16(w[g], xv[g]), _mm512_permutexvar_epi16(gidx[g], sc16));
+            si[r] = a;
+            _mm_prefetch((const char *)(b + 4 * Q4K_BYTES), _MM_HINT_T0);
+            _mm_prefetch((const char *)(b + 4 * Q4K_BYTES + 64), _MM_HINT_T0);
+            _mm_prefetch((const char *)(b + 4 * Q4K_BYTES + 128), _MM_HINT_T0);
+            // min term: m_j * (bs[2j] + bs[2j+1]) with each min on two int16 lanes
+            const __m256i mn2 = _mm256_inserti128_si256(_mm256_castsi128_si256(_mm_unpacklo_epi16(mn16, mn16)),
+                                                        _mm_unpackhi_epi16(mn16, mn16), 1);
+            sm[r] = _mm512_zextsi256_si512(_mm256_madd_epi16(mn2, bs));
+            dh[r] = u16_at(b);
+            mh[r] = u16_at(b + 2);
         }
-        const int32_t sumi = _mm512_reduce_add_epi32(a);
-        const float d = mp::h2f(u16_at(row + 208)) * f32_at(q8);
-        acc = acc + d * (float)sumi;
+        for (int r = NR; r < 4; ++r) si[r] = sm[r] = _mm512_setzero_si512();
+        const __m128 sumi = _mm_cvtepi32_ps(hsum4(si[0], si[1], si[2], si[3]));
+        const __m128 summ = _mm_cvtepi32_ps(hsum4(sm[0], sm[1], sm[2], sm[3]));
+        const __m128 dx = _mm_set1_ps(f32_at(qb));
+        const __m128 d = _mm_mul_ps(_mm_cvtph_ps(_mm_load_si128((const __m128i *)dh)), dx);
+        const __m128 dm = _mm_mul_ps(_mm_cvtph_ps(_mm_load_si128((const __m128i *)mh)), dx);
+        acc = _mm_add_ps(acc, _mm_mul_ps(d, sumi));
+        acc = _mm_sub_ps(acc, _mm_mul_ps(dm, summ));
     }
-    return acc;
+    alignas(16) float o[4];
+    _mm_store_ps(o, acc);
+    for (int r = 0; r < NR; ++r) out[r] = o[r];
+}
+
+// Q6_K: per 128-value half, quarters (0,1) and (2,3) of the six-bit codes as two
+// 64-byte vectors; 16-value group c of the super-block has scale c; the -32
+// offset is 32 * sum_c scale_c * bsum_c from the Q8_K block sums
+template <int NR>
+MPC_AVX512 static void rows_q6k_vnni(const uint8_t *row0, size_t stride, const uint8_t *q8, int nb, float *out) {
+    const __m256i m4 = _mm256_set1_epi8(0x0F), m30 = _mm256_set1_epi8(0x30);
+    __m512i cidx[4];           // chunk c (64 values): lanes 8t..8t+7 take scale 4c + t
+    for (int c = 0; c < 4; ++c) {
+        alignas(64) int16_t ix[32];
+        for (int l = 0; l < 32; ++l) ix[l] = (int16_t)(4 * c + l / 8);
+        cidx[c] = _mm512_load_si512((const void *)ix);
+    }
+    __m128 acc = _mm_setzero_ps();
+    for (int i = 0; i < nb; ++i) {
+        const uint8_t *qb = q8 + (size_t)i * Q8K_BYTES;
+        __m512i xv[4];
+        for (int c = 0; c < 4; ++c) xv[c] = _mm512_loadu_si512((const void *)(qb + 4 + 64 * c));
+        const __m256i bs = _mm256_loadu_si256((const __m256i *)(qb + 4 + QK));
+        __m512i si[4], so[4];
+        alignas(16) uint16_t dh[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+        for (int r = 0; r < NR; ++r) {
+            const uint8_t *b = row0 + (size_t)r * stride + (size_t)i * Q6K_BYTES;
+            const __m256i sc16 = _mm256_cvtepi8_epi16(_mm_loadu_si128((const __m128i *)(b + 192)));
+            const __m512i sc512 = _mm512_castsi256_si512(sc16);
+            __m512i a = _mm512_setzero_si512();
+            for (int h = 0; h < 2; ++h) {
+                const __m256i ql0 = _mm256_loadu_si256((const __m256i *)(b + 64 * h));
+                const __m256i ql1 = _mm256_loadu_si256((const __m256i *)(b + 64 * h + 32));
+                const __m256i qh = _mm256_loadu_si256((const __m256i *)(b + 128 + 32 * h));
+                const __m256i q0 = _mm256_or_si256(_mm256_and_si256(ql0, m4), _mm256_and_si256(_mm256_slli_epi16(qh, 4), m30));
+                const __m256i q1 = _mm256_or_si256(_mm256_and_si256(ql1, m4), _mm256_and_si256(_mm256_slli_epi16(qh, 2), m30));
+                const __m256i q2 = _mm256_or_si256(_mm256_and_si256(_mm256_srli_epi16(ql0, 4), m4), _mm256_and_si256(qh, m30));
+                const __m256i q3 = _mm256_or_si256(_mm256_and_si256(_mm256_srli_epi16(ql1, 4), m4),
+                                                   _mm256_and_si256(_mm256_srli_epi16(qh, 2), m30));
+                const __m512i w0 = _mm512_inserti64x4(_mm512_castsi256_si512(q0), q1, 1);
+                const __m512i w1 = _mm512_inserti64x4(_mm512_castsi256_si512(q2), q3, 1);
+                const __m512i p0 = _mm512_maddubs_epi16(w0, xv[2 * h]);
+                const __m512i p1 = _mm512_maddubs_epi16(w1, xv[2 * h + 1]);
+                a = _mm512_dpwssd_epi32(a, p0, _mm512_permutexvar_epi16(cidx[2 * h], sc512));
+                a = _mm512_dpwssd_epi32(a, p1, _mm512_permutexvar_epi16(cidx[2 * h + 1], sc512));
+            }
+            si[r] = a;
+            so[r] = _mm512_zextsi256_si512(_mm256_madd_epi16(sc16, bs));      // sum_c scale_c * bsum_c
+            dh[r] = u16_at(b + 208);
+            for (int l = 0; l < 4; ++l) _mm_prefetch((const char *)(b + 3 * Q6K_BYTES + 64 * l), _MM_HINT_T0);
+        }
+        for (int r = NR; r < 4; ++r) si[r] = so[r] = _mm512_setzero_si512();
+        const __m128i sum_dot = hsum4(si[0], si[1], si[2], si[3]);
+        const __m128i sum_off = hsum4(so[0], so[1], so[2], so[3]);
+        const __m128 sumi = _mm_cvtepi32_ps(_mm_sub_epi32(sum_dot, _mm_slli_epi32(sum_off, 5)));
+        const __m128 d = _mm_mul_ps(_mm_cvtph_ps(_mm_load_si128((const __m128i *)dh)), _mm_set1_ps(f32_at(qb)));
+        acc = _mm_add_ps(acc, _mm_mul_ps(d, sumi));
+    }
+    alignas(16) float o[4];
+    _mm_store_ps(o, acc);
+    for (int r = 0; r < NR; ++r) out[r] = o[r];
+}
+
+MPC_AVX512 static void rows_vnni(int type, const uint8_t *row0, size_t stride, int nrows, const uint8_t *q8, int nb,
+                                 float *out) {
+    int r = 0;
+    for (; r + 4 <= nrows; r += 4)
+        (type == mp::TYPE_Q6K ? rows_q6k_vnni<4> : rows_q4k_vnni<4>)(row0 + (size_t)r * stride, stride, q8, nb, out + r);
+    for (; r < nrows; ++r)
+        (type == mp::TYPE_Q6K ? rows_q6k_vnni<1> : rows_q4k_vnni<1>)(row0 + (size_t)r * stride, stride, q8, nb, out + r);
 }
 
 float dot_q4k(const uint8_t *row, const uint8_t *q8, int nb) {
-    return (!g_portable && has_vnni()) ? dot_q4k_vnni(row, q8, nb) : dot_q4k_port(row, q8, nb);
+    if (g_portable || !has_vnni()) return dot_q4k_port(row, q8, nb);
+    float y;
+    rows_vnni(mp::TYPE_Q4K, row, 0, 1, q8, nb, &y);
+    return y;
 }
 
 float dot_q6k(const uint8_t *row, const uint8_t *q8, int nb) {
-    return (!g_portable && has_vnni()) ? dot_q6k_vnni(row, q8, nb) : dot_q6k_port(row, q8, nb);
+    if (g_portable || !has_vnni()) return dot_q6k_port(row, q8, nb);
+    float y;
+    rows_vnni(mp::TYPE_Q6K, row, 0, 1, q8, nb, &y);
+    return y;
+}
+
+void dot_rows(int type, const uint8_t *row0, size_t stride, int nrows, const uint8_t *q8, int nb, float *out) {
+    if (!g_portable && has_vnni()) {
+        rows_vnni(type, row0, stride, nrows, q8, nb, out);
+        return;
+    }
+    for (int r = 0; r < nrows; ++r)
+        out[r] = type == mp::TYPE_Q6K ? dot_q6k_port(row0 + (size_t)r * stride, q8, nb)
+                                      : dot_q4k_port(row0 + (size_t)r * stride, q8, nb);
 }
 
 // ---- team --------------------------------------------------------------------
@@ -399,11 +497,10 @@ void up_item(void *p, int item) {
     const size_t rb = (size_t)(c.H / QK) * Q4K_BYTES;
     const uint8_t *up = c.e[k].w, *gate = c.e[k].w + (size_t)c.I * rb;
     float *h = c.h + (size_t)k * c.I;
-    for (int r = r0; r < r0 + UP_ROWS; ++r) {
-        const float u = dot_q4k(up + r * rb, c.e[k].q8x, c.H / QK);
-        const float g = dot_q4k(gate + r * rb, c.e[k].q8x, c.H / QK);
-        h[r] = g / (1.0f + canon_expf(-g)) * u;
-    }
+    float u[UP_ROWS], g[UP_ROWS];
+    dot_rows(mp::TYPE_Q4K, up + r0 * rb, rb, UP_ROWS, c.e[k].q8x, c.H / QK, u);
+    dot_rows(mp::TYPE_Q4K, gate + r0 * rb, rb, UP_ROWS, c.e[k].q8x, c.H / QK, g);
+    for (int r = 0; r < UP_ROWS; ++r) h[r0 + r] = g[r] / (1.0f + canon_expf(-g[r])) * u[r];
     if (c.left[k].fetch_sub(1, std::memory_order_acq_rel) == 1)
         quant_q8k(h, c.I, c.q8h + (size_t)k * (c.I / QK) * Q8K_BYTES);
 }
@@ -415,9 +512,7 @@ void down_item(void *p, int item) {
     const size_t rb = (size_t)(c.I / QK) * (c.down_type == mp::TYPE_Q6K ? Q6K_BYTES : Q4K_BYTES);
     const uint8_t *down = c.e[k].w + 2 * (size_t)c.I * rb_in;
     const uint8_t *q = c.q8h + (size_t)k * (c.I / QK) * Q8K_BYTES;
-    float *y = c.e[k].y;
-    for (int r = r0; r < r0 + DN_ROWS; ++r)
-        y[r] = c.down_type == mp::TYPE_Q6K ? dot_q6k(down + r * rb, q, c.I / QK) : dot_q4k(down + r * rb, q, c.I / QK);
+    dot_rows(c.down_type, down + r0 * rb, rb, DN_ROWS, q, c.I / QK, c.e[k].y + r0);
 }
 }  // namespace
 

@@ -204,6 +204,7 @@ struct moe_cache {
     uint64_t clock = 0, n_steps = 0, n_uploads = 0, n_scheduled = 0, n_copied = 0, n_published = 0;
     uint64_t n_admit_ok = 0, n_admit_denied = 0, n_table_flushes = 0, bytes_uploaded = 0;
     double wait_us = 0.0;
+    double boundary_us = 0.0;          // batch-1 decode: host time from the token's sync to the return
     FILE *route = nullptr, *map = nullptr;
     // optional kernel timing: 8 events per layer, read back after the token's sync
     bool timing = false;
@@ -2008,6 +2009,7 @@ int moe_cache_stats_get(moe_cache *c, moe_cache_stats *s) {
     s->sidecar_cpu_us = c->sc_cpu_us;
     s->bytes_uploaded = c->bytes_uploaded;
     s->publication_wait_us = c->wait_us;
+    s->host_boundary_us = c->boundary_us;
     return MOE_OK;
 }
 
@@ -2408,6 +2410,7 @@ int moe_decode_token(moe_cache *c, const float *x, const float *bias, float *out
     HIPCHK(hipMemcpyAsync(c->h_ids, c->d_ids, (size_t)NL * c->K * 4, hipMemcpyDeviceToHost, st));
     HIPCHK(hipMemcpyAsync(c->h_slots, c->d_slots, (size_t)NL * c->K * 4, hipMemcpyDeviceToHost, st));
     const hipError_t sync_err = hipStreamSynchronize(st);
+    const auto t_sync = std::chrono::steady_clock::now();
     const int drain_err = mover_drain();
     if (sync_err != hipSuccess) return fail(MOE_ERR_HIP, "decode: %s", hipGetErrorString(sync_err));
     if (drain_err != MOE_OK) return drain_err;
@@ -2475,6 +2478,7 @@ int moe_decode_token(moe_cache *c, const float *x, const float *bias, float *out
     }
     c->stage_valid = false;
     if (c->stg_pending) HIPCHK(hipEventRecord(c->ev_stg, c->stg_stream));
+    c->boundary_us += std::chrono::duration<double, std::micro>(std::chrono::steady_clock::now() - t_sync).count();
     return r;
 }
 
