@@ -70,6 +70,51 @@ __device__ inline void q8k_wave_vals(const float xv[4], int lane, int q[4], floa
     }
 }
 
+// NB blocks at once (each exactly as q8k_wave_vals), their cross-lane rounds
+// interleaved so that one block's shuffles fill another's latency
+template <int NB>
+__device__ inline void q8k_wave_vals_n(const float (*xv)[4], int lane, int (*q)[4], float *d) {
+    float amax[NB], mx[NB];
+    int idx[NB];
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+        amax[b] = 0.0f;
+        mx[b] = 0.0f;
+        idx[b] = 1 << 30;
+        for (int i = 0; i < 4; ++i) {
+            const float ax = fabsf(xv[b][i]);
+            if (ax > amax[b]) { amax[b] = ax; mx[b] = xv[b][i]; idx[b] = 4 * lane + i; }
+        }
+    }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) {
+        float oa[NB], om[NB];
+        int oi[NB];
+#pragma unroll
+        for (int b = 0; b < NB; ++b) {
+            oa[b] = __shfl_xor(amax[b], o, 64);
+            om[b] = __shfl_xor(mx[b], o, 64);
+            oi[b] = __shfl_xor(idx[b], o, 64);
+        }
+#pragma unroll
+        for (int b = 0; b < NB; ++b)
+            if (oa[b] > amax[b] || (oa[b] == amax[b] && oi[b] < idx[b])) { amax[b] = oa[b]; mx[b] = om[b]; idx[b] = oi[b]; }
+    }
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+        q[b][0] = q[b][1] = q[b][2] = q[b][3] = 0;
+        d[b] = 0.0f;
+        if (amax[b] != 0.0f) {
+            const float iscale = -127.0f / mx[b];
+            for (int i = 0; i < 4; ++i) {
+                const int t = (int)rintf(iscale * xv[b][i]);
+                q[b][i] = t < 127 ? t : 127;
+            }
+            d[b] = 1.0f / iscale;
+        }
+    }
+}
+
 // the 16-value group sum of the Q8_K block, valid on lanes with (lane & 3) == 0
 __device__ inline int q8k_group_sum(const int q[4]) {
     int gs = q[0] + q[1] + q[2] + q[3];

@@ -30,9 +30,24 @@
 namespace mp {
 
 // One wavefront quantizes 256 values (4 per lane, lane-major) to a Q8_K block.
+__device__ void q8k_wave_from(const float xv[4], uint8_t *out, int lane);
 __device__ void q8k_wave(const float *x, uint8_t *out, int lane) {
     const float4 v = *(const float4 *)(x + 4 * lane);
     const float xv[4] = {v.x, v.y, v.z, v.w};
+    q8k_wave_from(xv, out, lane);
+}
+
+// the bytes of one Q8_K block from a wave's codes (4 per lane) and scale
+__device__ void q8k_store(const int q[4], float d, uint8_t *out, int lane) {
+    const int gs = q8k_group_sum(q);
+    const uint32_t packed = (uint32_t)(q[0] & 0xff) | ((uint32_t)(q[1] & 0xff) << 8) |
+                            ((uint32_t)(q[2] & 0xff) << 16) | ((uint32_t)(q[3] & 0xff) << 24);
+    *(uint32_t *)(out + 4 + 4 * lane) = packed;
+    if ((lane & 3) == 0) *(int16_t *)(out + 4 + QK + 2 * (lane >> 2)) = (int16_t)gs;
+    if (lane == 0) *(float *)out = d;
+}
+
+__device__ void q8k_wave_from(const float xv[4], uint8_t *out, int lane) {
     int q[4];
     float d;
     q8k_wave_vals(xv, lane, q, d);
@@ -510,8 +525,22 @@ __global__ __launch_bounds__(512) void down_kernel(ExpertArgs a) {
             }
             // Q8_K of this expert's h, straight into LDS, while the weight
             // loads are in flight (every workgroup quantizes the same h the
-            // same way: identical bytes)
-            for (int b = 0; b < nb; ++b) q8k_wave(a.h + (size_t)k * a.I + QK * b, s_q8[wave] + b * Q8K_BYTES, lane);
+            // same way: identical bytes); the h loads of all blocks first
+            if (nb == 3) {
+                float xv[3][4];
+                int q[3][4];
+                float d[3];
+#pragma unroll
+                for (int b = 0; b < 3; ++b) {
+                    const float4 v = *(const float4 *)(a.h + (size_t)k * a.I + QK * b + 4 * lane);
+                    xv[b][0] = v.x; xv[b][1] = v.y; xv[b][2] = v.z; xv[b][3] = v.w;
+                }
+                q8k_wave_vals_n<3>(xv, lane, q, d);
+#pragma unroll
+                for (int b = 0; b < 3; ++b) q8k_store(q[b], d[b], s_q8[wave] + b * Q8K_BYTES, lane);
+            } else {
+                for (int b = 0; b < nb; ++b) q8k_wave(a.h + (size_t)k * a.I + QK * b, s_q8[wave] + b * Q8K_BYTES, lane);
+            }
 #pragma unroll
             for (int j = 0; j < 5; ++j) {
                 const int i = lane + 64 * j;
