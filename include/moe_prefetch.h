@@ -367,6 +367,36 @@ int moe_planner_size(const moe_planner *p);
 int moe_planner_get(const moe_planner *p, int id, moe_planner_job *out);
 void moe_planner_counters(const moe_planner *p, uint64_t out[4]);
 
+/* ---- MOEP expert predictor / evictor (host) --------------------------------
+ * moe_predictor of the reference (cpp/moe-predictor.h:35-106, .cpp:21-362):
+ * per-layer linear scores over multi-hot id lists -- prev (the next layer's
+ * ids of the previous token), cur (this layer's), below (the layer below's),
+ * self_prev (this layer's previous ones) -- z-scored per row plus a repeat
+ * prior on prev; top-k with the lower id first on a tie; a logistic SGD step
+ * per resolved prediction; MOEP v3 files read strictly and written back.
+ * Errors: a status code and moe_last_error(). */
+typedef struct moe_predictor moe_predictor;
+typedef struct {
+    uint32_t n_expert, n_layers, feat_dim, top_k, d_model, n_comp, n_present;
+    int32_t has_pca;
+    int32_t off_pca, off_prev, off_cur, off_below, off_self_prev;   /* column offsets, -1 absent */
+} moe_predictor_info;
+typedef struct {
+    const int32_t *ids[4];     /* prev, cur, below, self_prev (NULL: empty) */
+    int32_t n[4];
+} moe_predictor_lists;
+int moe_predictor_load(const char *path, moe_predictor **out);
+void moe_predictor_free(moe_predictor *p);
+int moe_predictor_info_get(const moe_predictor *p, moe_predictor_info *out);
+int moe_predictor_has_layer(const moe_predictor *p, int layer);
+int moe_predictor_score(const moe_predictor *p, int layer, const moe_predictor_lists *in, float *out);
+/* the k best ids of scores[n_expert], best first: returns how many (min(k, n_expert)) */
+int moe_predictor_top_k(const moe_predictor *p, const float *scores, int k, int32_t *out);
+/* one SGD step (learning rate lr) towards the ids `truth`; *recall = recall@8 before it */
+int moe_predictor_update(moe_predictor *p, int layer, const moe_predictor_lists *in, const int32_t *truth,
+                         int n_truth, float lr, float *recall);
+int moe_predictor_save(const moe_predictor *p, const char *path);
+
 /* Kernel time of the decode, from HIP events recorded around each launch on
  * the stream it runs on (off by default; set before decoding).  Experts
  * resident in HBM slots and experts read from the pinned store run as

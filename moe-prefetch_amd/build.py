@@ -11,7 +11,7 @@ import sys
 HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 OUT = os.path.join(HERE, "moe_prefetch", "libmoeprefetch.so")
-SOURCES = ["mp_kernels.hip", "mp_batched.hip", "mp_runtime.cpp", "mp_cpu.cpp"]
+SOURCES = ["mp_kernels.hip", "mp_batched.hip", "mp_runtime.cpp", "mp_cpu.cpp", "mp_predictor.cpp"]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
 FLAGS = [

@@ -28,6 +28,7 @@
 #include <cstdio>
 #include <cstring>
 #include <deque>
+#include <memory>
 #include <mutex>
 #include <string>
 #include <thread>
@@ -37,6 +38,7 @@
 #include "mp_cpu.h"
 #include "mp_format.h"
 #include "mp_internal.h"
+#include "mp_predictor.h"
 #include "mp_stream.h"
 #include "mp_synth.h"
 
@@ -1969,6 +1971,72 @@ void moe_planner_counters(const moe_planner *p, uint64_t out[4]) {
     out[1] = p->p.n_dup;
     out[2] = p->p.n_drop_late;
     out[3] = p->p.n_drop_posted;
+}
+
+// ---- MOEP expert predictor ---------------------------------------------------------
+struct moe_predictor {
+    mpp::Predictor p;
+};
+
+static mpp::Lists to_lists(const moe_predictor_lists *in) {
+    mpp::Lists l;
+    if (!in) return l;
+    for (int b = 0; b < 4; ++b) {
+        l.ids[b] = in->ids[b];
+        l.n[b] = in->ids[b] && in->n[b] > 0 ? (size_t)in->n[b] : 0;
+    }
+    return l;
+}
+
+int moe_predictor_load(const char *path, moe_predictor **out) {
+    if (!path || !out) return fail(MOE_ERR_ARG, "moe_predictor_load: null argument");
+    *out = nullptr;
+    std::unique_ptr<moe_predictor> p(new moe_predictor());
+    std::string err;
+    if (!p->p.load(path, err)) return fail(MOE_ERR_IO, "%s", err.c_str());
+    *out = p.release();
+    return MOE_OK;
+}
+
+void moe_predictor_free(moe_predictor *p) { delete p; }
+
+int moe_predictor_info_get(const moe_predictor *p, moe_predictor_info *out) {
+    if (!p || !out) return fail(MOE_ERR_ARG, "null argument");
+    const mpp::Predictor &q = p->p;
+    *out = moe_predictor_info{q.n_expert, q.n_layers, q.feat_dim, q.top_k, q.d_model, q.n_comp,
+                              (uint32_t)q.layers.size(), q.has_pca ? 1 : 0, q.off[mpp::BLOCK_PCA],
+                              q.off[mpp::BLOCK_PREV], q.off[mpp::BLOCK_CUR], q.off[mpp::BLOCK_BELOW],
+                              q.off[mpp::BLOCK_SELF_PREV]};
+    return MOE_OK;
+}
+
+int moe_predictor_has_layer(const moe_predictor *p, int layer) { return p && p->p.has_layer(layer) ? 1 : 0; }
+
+int moe_predictor_score(const moe_predictor *p, int layer, const moe_predictor_lists *in, float *out) {
+    if (!p || !out) return fail(MOE_ERR_ARG, "null argument");
+    if (!p->p.has_layer(layer)) return fail(MOE_ERR_ARG, "the predictor has no layer %d", layer);
+    p->p.score(layer, to_lists(in), out);
+    return MOE_OK;
+}
+
+int moe_predictor_top_k(const moe_predictor *p, const float *scores, int k, int32_t *out) {
+    if (!p || !scores || !out || k < 0) return fail(MOE_ERR_ARG, "bad arguments");
+    return (int)p->p.top(scores, (size_t)k, out);
+}
+
+int moe_predictor_update(moe_predictor *p, int layer, const moe_predictor_lists *in, const int32_t *truth,
+                         int n_truth, float lr, float *recall) {
+    if (!p || (n_truth > 0 && !truth)) return fail(MOE_ERR_ARG, "bad arguments");
+    const float r = p->p.update(layer, to_lists(in), truth, n_truth > 0 ? (size_t)n_truth : 0, lr);
+    if (recall) *recall = r;
+    return MOE_OK;
+}
+
+int moe_predictor_save(const moe_predictor *p, const char *path) {
+    if (!p || !path) return fail(MOE_ERR_ARG, "null argument");
+    std::string err;
+    if (!p->p.save(path, err)) return fail(MOE_ERR_IO, "%s", err.c_str());
+    return MOE_OK;
 }
 
 int moe_cache_frame(moe_cache *c, int layer, int32_t *out) {

@@ -107,6 +107,16 @@ class PlannerJob(ctypes.Structure):
                 ("dropped", I32), ("drop", I32)]
 
 
+class PredictorInfo(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_uint32) for n in ("n_expert", "n_layers", "feat_dim", "top_k", "d_model", "n_comp",
+                                               "n_present")] + \
+               [(n, I32) for n in ("has_pca", "off_pca", "off_prev", "off_cur", "off_below", "off_self_prev")]
+
+
+class PredictorLists(ctypes.Structure):
+    _fields_ = [("ids", P * 4), ("n", I32 * 4)]
+
+
 # name -> (restype, argtypes); mirrors include/moe_prefetch.h one to one
 SIGNATURES = {
     "moe_last_error": (ctypes.c_char_p, []),
@@ -169,6 +179,15 @@ SIGNATURES = {
     "moe_cache_stream_land": (ctypes.c_int, [P, ctypes.c_int]),
     "moe_cache_stream_job": (ctypes.c_int, [P, ctypes.c_int, ctypes.POINTER(I32), ctypes.POINTER(I32)]),
     "moe_route_ahead": (ctypes.c_int, [ctypes.POINTER(RouteDesc), ctypes.POINTER(AheadDesc), P, P, P]),
+    "moe_predictor_load": (ctypes.c_int, [ctypes.c_char_p, ctypes.POINTER(P)]),
+    "moe_predictor_free": (None, [P]),
+    "moe_predictor_info_get": (ctypes.c_int, [P, ctypes.POINTER(PredictorInfo)]),
+    "moe_predictor_has_layer": (ctypes.c_int, [P, ctypes.c_int]),
+    "moe_predictor_score": (ctypes.c_int, [P, ctypes.c_int, ctypes.POINTER(PredictorLists), P]),
+    "moe_predictor_top_k": (ctypes.c_int, [P, P, ctypes.c_int, P]),
+    "moe_predictor_update": (ctypes.c_int, [P, ctypes.c_int, ctypes.POINTER(PredictorLists), P, ctypes.c_int, F32,
+                                            ctypes.POINTER(F32)]),
+    "moe_predictor_save": (ctypes.c_int, [P, ctypes.c_char_p]),
     "moe_planner_create": (P, [U64]),
     "moe_planner_destroy": (None, [P]),
     "moe_planner_reset": (None, [P]),

@@ -40,6 +40,10 @@
  *       reference's engine-recorded traces
  *       (artifacts/x3_logits_1791160431756057451/{0..3}.routes-record.txt) and
  *       requiring every placement frame of {0..3}.map.txt.
+ *   _ref/libref_predictor.so (ref_predictor_shim.cpp + the reference's own
+ *       cpp/moe-predictor.cpp, built from where it lies by `make ref`)
+ *       the MOEP predictor itself, not restated: the checker of the product's
+ *       moe_predictor_* (tests/test_moep.py, tests/golden/make_moep_golden.py).
  *   or_ahead, or_planner_*
  *       router lookahead (k_moe_ahead_scores/post, patches/0010-team-and-streaming.patch:382-474)
  *       and the just-in-time copy planner (moe_planner, 0010:777-909).  or_ahead is

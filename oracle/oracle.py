@@ -434,3 +434,83 @@ class Cache:
         out = np.zeros(11, np.uint64)
         lib().or_cache_stream_stats(self.h, _p(out))
         return dict(zip(STREAM_STATS, (int(v) for v in out)))
+
+
+# ---- the reference's own MOEP predictor (oracle/_ref, built where the reference is) ----
+REF_PREDICTOR = os.path.join(HERE, "_ref", "libref_predictor.so")
+_ref = None
+
+
+def ref_predictor_lib():
+    """ctypes handle of _ref/libref_predictor.so, or None when it is not built."""
+    global _ref
+    if _ref is None and os.path.exists(REF_PREDICTOR):
+        L = ctypes.CDLL(REF_PREDICTOR)
+        I = ctypes.c_int
+        L.rp_load.restype, L.rp_load.argtypes = P, [ctypes.c_char_p, ctypes.c_char_p, I]
+        L.rp_free.restype, L.rp_free.argtypes = None, [P]
+        L.rp_has_layer.restype, L.rp_has_layer.argtypes = I, [P, I]
+        L.rp_score.restype, L.rp_score.argtypes = None, [P, I, P, I, P, I, P, I, P, I, P]
+        L.rp_top_k.restype, L.rp_top_k.argtypes = I, [P, P, I, P]
+        L.rp_update.restype, L.rp_update.argtypes = F32, [P, I, P, I, P, I, P, I, P, I, P, I, F32]
+        L.rp_save.restype, L.rp_save.argtypes = I, [P, ctypes.c_char_p, ctypes.c_char_p, I]
+        _ref = L
+    return _ref
+
+
+class RefPredictor:
+    """The reference's moe_predictor (checker only)."""
+
+    def __init__(self, path):
+        L = ref_predictor_lib()
+        err = ctypes.create_string_buffer(512)
+        self.h = L.rp_load(str(path).encode(), err, 512)
+        if not self.h:
+            raise ValueError(err.value.decode())
+        self.L = L
+
+    def close(self):
+        if getattr(self, "h", None):
+            self.L.rp_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        self.close()
+
+    @staticmethod
+    def _args(keep, ids):
+        out = []
+        for name in ("prev", "cur", "below", "self_prev"):
+            v = ids.get(name)
+            if v is None or len(v) == 0:
+                out += [None, 0]
+            else:
+                a = np.ascontiguousarray(v, np.int32)
+                keep.append(a)
+                out += [a.ctypes.data, a.size]
+        return out
+
+    def has_layer(self, layer):
+        return bool(self.L.rp_has_layer(self.h, layer))
+
+    def score(self, layer, n_expert, **ids):
+        keep = []
+        out = np.empty(n_expert, np.float32)
+        self.L.rp_score(self.h, layer, *self._args(keep, ids), out.ctypes.data)
+        return out
+
+    def top_k(self, scores, k=8):
+        s = np.ascontiguousarray(scores, np.float32)
+        out = np.empty(k, np.int32)
+        n = self.L.rp_top_k(self.h, s.ctypes.data, k, out.ctypes.data)
+        return out[:n]
+
+    def update(self, layer, truth, lr, **ids):
+        keep = []
+        t = np.ascontiguousarray(truth, np.int32)
+        return self.L.rp_update(self.h, layer, *self._args(keep, ids), t.ctypes.data, t.size, lr)
+
+    def save(self, path):
+        err = ctypes.create_string_buffer(512)
+        if self.L.rp_save(self.h, str(path).encode(), err, 512) != 0:
+            raise OSError(err.value.decode())
