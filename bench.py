@@ -838,7 +838,7 @@ def main():
     ap.add_argument("--path", type=int, default=0, help="0 fused, 1 fork/join, 2 serial expert launches")
     ap.add_argument("--sidecar", type=int, default=-1,
                     help="host threads serving absent experts (0: GPU only; default: 14 on a 16-CPU host)")
-    ap.add_argument("--share", default="3/4", help="num/den: absent experts of rank r with r %% den < num go to "
+    ap.add_argument("--share", default="1/1", help="num/den: absent experts of rank r with r %% den < num go to "
                                                    "the CPU")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="end with a plain 256 MiB device copy (scale for rocprofv3 FETCH_SIZE/WRITE_SIZE)")
