@@ -12,8 +12,9 @@ layers (router, experts from HBM slots or the pinned store, combine, routed ids
 back, cache step with uploads on the side stream), replayed as one HIP graph.
 The synthetic sequence is 512 tokens: --warmup tokens warm the cache, the next
 --steps are timed.  Absent experts are served by the host CPU (14 threads on a
-16-CPU host, 3 of every 4 absent experts of a layer; --sidecar 0 for the
-GPU-only path) while the GPU runs the resident ones.
+16-CPU host, every absent expert of a layer by default, --share num/den for a
+part of them; --sidecar 0 for the GPU-only path) while the GPU runs the
+resident ones.
 
 --workload prefill48 [--batch 512|64]: batched MoE layers -- a chunk of
 tokens (bf16 activations, uniform router logits) through 48 layers whose 128
