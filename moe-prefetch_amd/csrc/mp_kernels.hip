@@ -59,6 +59,19 @@ __device__ void q8k_wave_from(const float xv[4], uint8_t *out, int lane) {
     if (lane == 0) *(float *)out = d;
 }
 
+// A store coherent at system scope: written through the caches to memory
+// (global_store ... sc0 sc1).  The records posted to the host are written with
+// it: a plain store to host memory may stay in L2, and only a write-back of
+// the whole L2 (what a system-scope release does) would push it out.  After
+// the wave waits for its stores (vmcnt 0), every word is visible to the host
+// before the sequence number that publishes them.
+__device__ inline void store_sys(int32_t *p, int32_t v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+__device__ inline void store_sys(uint32_t *p, uint32_t v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+
 // ---------------------------------------------------------------------------
 // router
 struct RouteArgs {
@@ -145,8 +158,8 @@ __global__ __launch_bounds__(256) void route_logits_kernel(RouteArgs a) {
 // threads its own ranking leaves idle (descending, the lower id first on a
 // tie, a NaN with -inf) into s_top, and one wave -- beside the wave that posts
 // the layer's own routing -- keeps the top ak whose table word is the dummy
-// (best first) and posts the record with the GPU clock and the token's
-// sequence number last (system-scope release).  Every layer posts, with no
+// (best first) and posts the record with the GPU clock, every word written
+// through to host memory, and the token's sequence number last.  Every layer posts, with no
 // target too: the record also tells the host the layer has read its table.
 __device__ inline void ahead_rank(const RouteArgs &a, const float (*s_asel)[256], int (*s_top)[AHEAD_K], int i) {
     const int t = i / a.E, e = i - t * a.E;
@@ -174,24 +187,28 @@ __device__ void ahead_post(const RouteArgs &a, const int (*s_top)[AHEAD_K], int 
         e = s_top[t][j];
         keep = a.atbl[t][e] == a.adummy[t];
     }
+    // every load before the first store: a wait after a write-through store
+    // would also wait for it to land
+    const int32_t target = lane == 0 ? a.atarget[0] : a.atarget[1];
+    const uint32_t seq = a.seq ? *a.seq : 1u;
     const uint64_t m = __ballot(keep);
     const uint64_t mt = (m >> (8 * t)) & 0xffull;
-    if (keep) r->ids[t][__popcll(mt & ((1ull << j) - 1ull))] = e;
+    __builtin_amdgcn_s_waitcnt(0x0f70);
+    if (keep) store_sys(&r->ids[t][__popcll(mt & ((1ull << j) - 1ull))], e);
     if (lane < 2) {
-        r->n[lane] = lane < a.an ? __popcll((m >> (8 * lane)) & 0xffull) : 0;
-        r->target[lane] = lane < a.an ? a.atarget[lane] : -1;
+        store_sys(&r->n[lane], lane < a.an ? (int32_t)__popcll((m >> (8 * lane)) & 0xffull) : 0);
+        store_sys(&r->target[lane], lane < a.an ? target : -1);
     }
     if (lane == 0) {
         const uint64_t now = wall_clock64();
-        r->layer = (uint32_t)a.alayer;
-        r->t_lo = (uint32_t)now;
-        r->t_hi = (uint32_t)(now >> 32);
+        store_sys(&r->layer, (uint32_t)a.alayer);
+        store_sys(&r->t_lo, (uint32_t)now);
+        store_sys(&r->t_hi, (uint32_t)(now >> 32));
     }
-    // The record lives in fine-grained host memory, which the stores reach
-    // without passing through L2: waiting for them (vmcnt 0) orders them
-    // before the sequence number; no L2 write-back is needed here.
+    // written through (store_sys): waiting for them orders them before the
+    // sequence number, with no write-back of the whole L2
     __builtin_amdgcn_s_waitcnt(0x0f70);
-    if (lane == 0) __hip_atomic_store(&r->seq, a.seq ? *a.seq : 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    if (lane == 0) __hip_atomic_store(&r->seq, seq, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
 }
 
 // One workgroup per token.  Wave c owns experts 64c .. 64c+63: logits, the
@@ -298,18 +315,32 @@ __global__ __launch_bounds__(256) void route_select_kernel(RouteArgs a) {
         }
         // CPU-assisted serving: post the ids, the slots read and the Q8_K of
         // x (written by the router GEMV kernel) to the host, then the sequence
-        // number.  One wave: its release store waits for all of the wave's
-        // earlier stores.  (Only on the router-GEMV path, where x's Q8_K is
-        // complete before this kernel.)
+        // number.  One wave.  (Only on the router-GEMV path, where x's Q8_K is
+        // complete before this kernel.)  The host reads nothing else the GPU
+        // wrote, so the words go out written through (store_sys) and the wave
+        // waits for them (vmcnt 0) before the sequence number: no write-back
+        // of the whole L2, which a system-scope release would add.
         if (a.post && !a.logits_in) {
+            // every load first (unconditional, the index clamped), one wait,
+            // then the stores: a wait between two stores would also wait for
+            // the first write-through store to land
+            constexpr int NW = (SC_Q8X_BYTES / 4 + 63) / 64;
+            const int n32 = (a.H / QK) * Q8K_BYTES / 4;
+            const uint32_t *src = (const uint32_t *)a.q8x;
+            uint32_t *dst = (uint32_t *)a.post->q8x;
+            uint32_t v[NW];
+#pragma unroll
+            for (int j = 0; j < NW; ++j) v[j] = src[min(lane + 64 * j, n32 - 1)];
+            __builtin_amdgcn_s_waitcnt(0x0f70);
             if (lane < a.K) {
-                a.post->ids[lane] = s_ids[lane];
-                a.post->slots[lane] = slot;
+                store_sys(&a.post->ids[lane], s_ids[lane]);
+                store_sys(&a.post->slots[lane], slot);
             }
-            const uint4 *src = (const uint4 *)a.q8x;
-            uint4 *dst = (uint4 *)a.post->q8x;
-            for (int i = lane; i < (a.H / QK) * Q8K_BYTES / 16; i += 64) dst[i] = src[i];
-            if (lane == 0) __hip_atomic_store(&a.post->seq, *a.seq, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
+#pragma unroll
+            for (int j = 0; j < NW; ++j)
+                if (lane + 64 * j < n32) store_sys(dst + lane + 64 * j, v[j]);
+            __builtin_amdgcn_s_waitcnt(0x0f70);
+            if (lane == 0) __hip_atomic_store(&a.post->seq, *a.seq, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
         }
     }
     if (look && wave == 1) ahead_post(a, s_top, lane);      // beside wave 0's own post
@@ -729,9 +760,15 @@ __global__ __launch_bounds__(256) void join_kernel(JoinArgs a) {
         const uint32_t want = *a.seq;
         const uint64_t t0 = wall_clock64();
         int ok = 0;
+        // relaxed polls (system-scope loads bypass the caches), one acquire
+        // once the answer is there: no cache invalidation per poll
         for (;;) {
-            const uint32_t v = __hip_atomic_load(&a.resp->seq, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_SYSTEM);
-            if (v == want) { ok = 1; break; }
+            const uint32_t v = __hip_atomic_load(&a.resp->seq, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+            if (v == want) {
+                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "");    // system scope
+                ok = 1;
+                break;
+            }
             if (v == SC_ABORT) break;
             if (wall_clock64() - t0 > a.timeout_ticks) {
                 if (blockIdx.x == 0) __hip_atomic_store(&a.resp->err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
