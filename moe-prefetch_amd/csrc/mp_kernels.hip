@@ -72,6 +72,20 @@ __device__ inline void store_sys(uint32_t *p, uint32_t v) {
     __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
 }
 
+// The bytes of one Q8_K block (as q8k_store writes them) as 73 words written
+// through to host memory: d, 64 words of codes, the 16 group sums two to a
+// word.  The wave waits for them before it goes on.
+__device__ void q8k_store_sys(const int q[4], float d, uint32_t *out, int lane) {
+    const int gs = q8k_group_sum(q);
+    const int gs_odd = __shfl_down(gs, 4, 64);       // group 2m + 1 for the lane holding 2m
+    const uint32_t packed = (uint32_t)(q[0] & 0xff) | ((uint32_t)(q[1] & 0xff) << 8) |
+                            ((uint32_t)(q[2] & 0xff) << 16) | ((uint32_t)(q[3] & 0xff) << 24);
+    store_sys(out + 1 + lane, packed);
+    if ((lane & 7) == 0) store_sys(out + 1 + QK / 4 + (lane >> 3), ((uint32_t)gs & 0xffffu) | ((uint32_t)gs_odd << 16));
+    if (lane == 0) store_sys(out, __float_as_uint(d));
+    __builtin_amdgcn_s_waitcnt(0x0f70);
+}
+
 // ---------------------------------------------------------------------------
 // router
 struct RouteArgs {
@@ -147,9 +161,19 @@ __global__ __launch_bounds__(256) void route_logits_kernel(RouteArgs a) {
     acc = bfly_add(acc);
     if (a.bias) acc = acc + a.bias[(size_t)tok * a.E + e];
     if (lane == 0) a.logits[(size_t)tok * a.E + e] = acc;
-    // Q8_K of x: workgroup b (one of the first H/256) quantizes block b
-    if (a.q8x && wave == 0 && (int)blockIdx.x < a.H / QK)
-        q8k_wave(x + QK * blockIdx.x, a.q8x + ((size_t)tok * (a.H / QK) + blockIdx.x) * Q8K_BYTES, lane);
+    // Q8_K of x: workgroup b (one of the first H/256) quantizes block b; with
+    // CPU-assisted serving (batch 1) also into the host's post, written
+    // through before this kernel ends, so that the select kernel's post only
+    // adds the ids
+    if (a.q8x && wave == 0 && (int)blockIdx.x < a.H / QK) {
+        const float4 v = *(const float4 *)(x + QK * blockIdx.x + 4 * lane);
+        const float xv[4] = {v.x, v.y, v.z, v.w};
+        int q[4];
+        float d;
+        q8k_wave_vals(xv, lane, q, d);
+        q8k_store(q, d, a.q8x + ((size_t)tok * (a.H / QK) + blockIdx.x) * Q8K_BYTES, lane);
+        if (a.post && tok == 0) q8k_store_sys(q, d, (uint32_t *)(a.post->q8x + (size_t)blockIdx.x * Q8K_BYTES), lane);
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -175,7 +199,7 @@ __device__ inline void ahead_rank(const RouteArgs &a, const float (*s_asel)[256]
     if (rank < a.ak) s_top[t][rank] = e;
 }
 
-__device__ void ahead_post(const RouteArgs &a, const int (*s_top)[AHEAD_K], int lane) {
+__device__ void ahead_post(const RouteArgs &a, const int (*s_top)[AHEAD_K], uint32_t seq, int lane) {
     AheadPost *r = a.apost;
     const int t = lane >> 3, j = lane & 7;          // lanes 0-7 target 0, 8-15 target 1: one round of loads
     bool keep = false;
@@ -190,7 +214,6 @@ __device__ void ahead_post(const RouteArgs &a, const int (*s_top)[AHEAD_K], int 
     // every load before the first store: a wait after a write-through store
     // would also wait for it to land
     const int32_t target = lane == 0 ? a.atarget[0] : a.atarget[1];
-    const uint32_t seq = a.seq ? *a.seq : 1u;
     const uint64_t m = __ballot(keep);
     const uint64_t mt = (m >> (8 * t)) & 0xffull;
     __builtin_amdgcn_s_waitcnt(0x0f70);
@@ -228,14 +251,21 @@ __global__ __launch_bounds__(256) void route_select_kernel(RouteArgs a) {
     __shared__ int s_ids[16];
     __shared__ __attribute__((aligned(16))) float s_asel[2][256];   // lookahead scores
     __shared__ int s_top[2][AHEAD_K];
+    __shared__ int32_t s_tbl[256];
+    // Every global load first, all in flight together: the table word of
+    // expert tid (at system scope when the host's copy stream may write words
+    // while the token runs), the lookahead scores, the logits, the sequence
+    // number.  The selection then needs no dependent round trip.
     const bool look = a.apost && !a.logits_in;
+    int32_t tword = 0;
+    if (a.table && tid < a.E)
+        tword = a.fresh ? __hip_atomic_load(a.table + tid, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM)
+                        : a.table[tid];
+    float av[2] = {0.0f, 0.0f};
     if (look)
-        for (int i = tid; i < a.an * a.E; i += 256) {
-            const int t = i / a.E, e = i - t * a.E;
-            const float v = a.alog[(size_t)t * a.E + e];
-            s_asel[t][e] = v != v ? -INFINITY : v;
-        }
-    float l = 0.0f;
+        for (int j = 0; j < 2; ++j)
+            if (tid + 256 * j < a.an * a.E) av[j] = a.alog[tid + 256 * j];
+    float l = 0.0f, pr = 0.0f;
     if (wave < nc) {
         const int ee = 64 * wave + lane;
         if (a.logits_in) {
@@ -244,6 +274,19 @@ __global__ __launch_bounds__(256) void route_select_kernel(RouteArgs a) {
         } else {
             l = a.logits[(size_t)tok * a.E + ee];
         }
+        if (a.prior) pr = a.prior[ee];
+    }
+    const uint32_t seqv = a.seq ? *a.seq : 1u;
+    if (a.table && tid < a.E) s_tbl[tid] = tword;
+    if (look)
+        for (int j = 0; j < 2; ++j) {
+            const int i = tid + 256 * j;
+            if (i < a.an * a.E) {
+                const int t = i / a.E, e = i - t * a.E;
+                s_asel[t][e] = av[j] != av[j] ? -INFINITY : av[j];
+            }
+        }
+    if (wave < nc) {
         float m = l;
 #pragma unroll
         for (int o = 32; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
@@ -266,7 +309,7 @@ __global__ __launch_bounds__(256) void route_select_kernel(RouteArgs a) {
         const float p = ex / sum;
         s_p[ee] = p;
         if (a.probs) a.probs[(size_t)tok * a.E + ee] = p;
-        float sel = !a.prior ? p : (a.prior_on_logits ? l + a.prior[ee] : p + a.prior[ee]);
+        float sel = !a.prior ? p : (a.prior_on_logits ? l + pr : p + pr);
         s_sel[ee] = sel != sel ? -INFINITY : sel;     // a NaN sorts last
     }
     __syncthreads();
@@ -300,12 +343,11 @@ __global__ __launch_bounds__(256) void route_select_kernel(RouteArgs a) {
             a.ids[(size_t)tok * a.K + lane] = id;
             a.w[(size_t)tok * a.K + lane] = s_p[id] / ws;
             if (a.table && a.fresh) {
-                // the host's copy stream may write this word while the token runs
-                const int32_t v = __hip_atomic_load(a.table + id, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+                const int32_t v = s_tbl[id];
                 streamed = (v & STREAM_BIT) != 0;
                 slot = v & SLOT_MASK;
             } else if (a.table) {
-                slot = a.table[id];
+                slot = s_tbl[id];
             }
             a.slots[(size_t)tok * a.K + lane] = slot;
         }
@@ -313,37 +355,23 @@ __global__ __launch_bounds__(256) void route_select_kernel(RouteArgs a) {
             const bool any = __ballot(streamed) != 0;
             if (lane == 0) *a.fresh = any ? 1u : 0u;
         }
-        // CPU-assisted serving: post the ids, the slots read and the Q8_K of
-        // x (written by the router GEMV kernel) to the host, then the sequence
-        // number.  One wave.  (Only on the router-GEMV path, where x's Q8_K is
-        // complete before this kernel.)  The host reads nothing else the GPU
-        // wrote, so the words go out written through (store_sys) and the wave
-        // waits for them (vmcnt 0) before the sequence number: no write-back
-        // of the whole L2, which a system-scope release would add.
+        // CPU-assisted serving: post the ids and the slots read to the host,
+        // then the sequence number.  One wave.  (Only on the router-GEMV path,
+        // whose kernel wrote the Q8_K of x into the post and waited for it.)
+        // The host reads nothing else the GPU wrote, so the words go out
+        // written through (store_sys) and the wave waits for them (vmcnt 0)
+        // before the sequence number: no write-back of the whole L2, which a
+        // system-scope release would add.
         if (a.post && !a.logits_in) {
-            // every load first (unconditional, the index clamped), one wait,
-            // then the stores: a wait between two stores would also wait for
-            // the first write-through store to land
-            constexpr int NW = (SC_Q8X_BYTES / 4 + 63) / 64;
-            const int n32 = (a.H / QK) * Q8K_BYTES / 4;
-            const uint32_t *src = (const uint32_t *)a.q8x;
-            uint32_t *dst = (uint32_t *)a.post->q8x;
-            uint32_t v[NW];
-#pragma unroll
-            for (int j = 0; j < NW; ++j) v[j] = src[min(lane + 64 * j, n32 - 1)];
-            __builtin_amdgcn_s_waitcnt(0x0f70);
             if (lane < a.K) {
                 store_sys(&a.post->ids[lane], s_ids[lane]);
                 store_sys(&a.post->slots[lane], slot);
             }
-#pragma unroll
-            for (int j = 0; j < NW; ++j)
-                if (lane + 64 * j < n32) store_sys(dst + lane + 64 * j, v[j]);
             __builtin_amdgcn_s_waitcnt(0x0f70);
-            if (lane == 0) __hip_atomic_store(&a.post->seq, *a.seq, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+            if (lane == 0) __hip_atomic_store(&a.post->seq, seqv, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
         }
     }
-    if (look && wave == 1) ahead_post(a, s_top, lane);      // beside wave 0's own post
+    if (look && wave == 1) ahead_post(a, s_top, seqv, lane);      // beside wave 0's own post
     if (!a.logits_in || !a.x || !a.q8x) return;
     const float *x = a.x + (size_t)tok * a.H;
     uint8_t *q8 = a.q8x + (size_t)tok * (a.H / QK) * Q8K_BYTES;
@@ -788,13 +816,23 @@ __global__ __launch_bounds__(256) void join_kernel(JoinArgs a) {
         a.out[r] = 0.0f;
         return;
     }
-    float acc = 0.0f;
-    for (int k = 0; k < a.K; ++k) {
-        const float y = s_cpu[k] ? __hip_atomic_load(&a.hrows[(size_t)k * a.H + r], __ATOMIC_RELAXED,
-                                                     __HIP_MEMORY_SCOPE_SYSTEM)
-                                 : a.ypart[(size_t)k * a.H + r];
-        acc = k == 0 ? a.w[0] * y : acc + a.w[k] * y;
-    }
+    // every row's load issued before the first is used: one round trip over
+    // PCIe for the host's rows, not one per expert.  One kind of load for
+    // both sources (system scope: the host's rows bypass the caches; the
+    // GPU's partials, from an earlier kernel, are in memory too).
+    constexpr int MK = 16;
+    float y[MK], wk[MK];
+#pragma unroll
+    for (int k = 0; k < MK; ++k)
+        if (k < a.K) {
+            const float *src = s_cpu[k] ? a.hrows + (size_t)k * a.H + r : a.ypart + (size_t)k * a.H + r;
+            y[k] = __hip_atomic_load(src, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+            wk[k] = a.w[k];
+        }
+    float acc = wk[0] * y[0];
+#pragma unroll
+    for (int k = 1; k < MK; ++k)
+        if (k < a.K) acc = acc + wk[k] * y[k];
     if (a.n_shared) acc = acc + a.ypart[(size_t)a.K * a.H + r];   // weight 1, after the routed experts
     a.out[r] = acc;
 }
