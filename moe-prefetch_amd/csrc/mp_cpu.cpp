@@ -484,14 +484,16 @@ constexpr int DN_ROWS = 32;     // down rows per work item
 struct Chain {
     const CpuExpert *e;
     int n, H, I, down_type;
+    int n_up;                    // up/gate items of all experts; the down items follow
     float *h;
     uint8_t *q8h;
-    std::atomic<int> left[16];   // up/gate items of expert k not finished yet
+    alignas(64) std::atomic<int> left[16];    // up/gate items of expert k not finished yet
+    alignas(64) std::atomic<int> ready[16];   // Q8_K of expert k's h written
 };
 
-// rows of up and gate; the item that finishes an expert's h quantizes it
-void up_item(void *p, int item) {
-    Chain &c = *(Chain *)p;
+// rows of up and gate; the item that finishes an expert's h quantizes it and
+// lets the expert's down items go
+void up_item(Chain &c, int item) {
     const int per = c.I / UP_ROWS;
     const int k = item / per, r0 = (item % per) * UP_ROWS;
     const size_t rb = (size_t)(c.H / QK) * Q4K_BYTES;
@@ -501,31 +503,51 @@ void up_item(void *p, int item) {
     dot_rows(mp::TYPE_Q4K, up + r0 * rb, rb, UP_ROWS, c.e[k].q8x, c.H / QK, u);
     dot_rows(mp::TYPE_Q4K, gate + r0 * rb, rb, UP_ROWS, c.e[k].q8x, c.H / QK, g);
     for (int r = 0; r < UP_ROWS; ++r) h[r0 + r] = g[r] / (1.0f + canon_expf(-g[r])) * u[r];
-    if (c.left[k].fetch_sub(1, std::memory_order_acq_rel) == 1)
+    if (c.left[k].fetch_sub(1, std::memory_order_acq_rel) == 1) {
         quant_q8k(h, c.I, c.q8h + (size_t)k * (c.I / QK) * Q8K_BYTES);
+        c.ready[k].store(1, std::memory_order_release);
+    }
 }
 
-void down_item(void *p, int item) {
-    const Chain &c = *(const Chain *)p;
-    const int k = item % c.n, r0 = (item / c.n) * DN_ROWS;       // experts interleaved: even load
+// rows of down, expert by expert.  Every up/gate item is claimed before the
+// first down item (items go out in order) and none of them waits, so the wait
+// for the expert's h always ends.
+void down_item(const Chain &c, int item) {
+    const int per = c.H / DN_ROWS;
+    const int k = item / per, r0 = (item % per) * DN_ROWS;
     const size_t rb_in = (size_t)(c.H / QK) * Q4K_BYTES;
     const size_t rb = (size_t)(c.I / QK) * (c.down_type == mp::TYPE_Q6K ? Q6K_BYTES : Q4K_BYTES);
     const uint8_t *down = c.e[k].w + 2 * (size_t)c.I * rb_in;
+    while (!c.ready[k].load(std::memory_order_acquire)) _mm_pause();
     const uint8_t *q = c.q8h + (size_t)k * (c.I / QK) * Q8K_BYTES;
     dot_rows(c.down_type, down + r0 * rb, rb, DN_ROWS, q, c.I / QK, c.e[k].y + r0);
 }
+
+void chain_item(void *p, int item) {
+    Chain &c = *(Chain *)p;
+    if (item < c.n_up)
+        up_item(c, item);
+    else
+        down_item(c, item - c.n_up);
+}
 }  // namespace
 
+// One team job per pass: up/gate of every expert, then down expert by expert;
+// a down item waits only for its own expert's h, so the down rows of the first
+// expert run while the last up/gate rows finish.
 void experts(Team *t, const CpuExpert *e, int n, int H, int I, int down_type, float *h_scratch,
              uint8_t *q8h_scratch) {
     for (int b = 0; b < n; b += 16) {         // at most 16 experts per pass
         Chain c;
         c.e = e + b; c.n = std::min(16, n - b); c.H = H; c.I = I; c.down_type = down_type;
+        c.n_up = c.n * (I / UP_ROWS);
         c.h = h_scratch + (size_t)b * I;
         c.q8h = q8h_scratch + (size_t)b * (I / QK) * Q8K_BYTES;
-        for (int k = 0; k < c.n; ++k) c.left[k].store(I / UP_ROWS, std::memory_order_relaxed);
-        t->run(c.n * (I / UP_ROWS), up_item, &c);
-        t->run(c.n * (H / DN_ROWS), down_item, &c);
+        for (int k = 0; k < c.n; ++k) {
+            c.left[k].store(I / UP_ROWS, std::memory_order_relaxed);
+            c.ready[k].store(0, std::memory_order_relaxed);
+        }
+        t->run(c.n_up + c.n * (H / DN_ROWS), chain_item, &c);
     }
 }
 
