@@ -193,8 +193,18 @@ static inline void q4k_scales8(const uint8_t *s, uint64_t &sc, uint64_t &mn) {
     mn = (uint64_t)mn_lo | ((uint64_t)mn_hi << 32);
 }
 
+// Prefetch: the same super-block of the next group of four rows (a row is only
+// 6-18 lines, too short for the hardware's stream detection to run ahead),
+// when the caller says a next group follows.
+void prefetch_rows(int type, const uint8_t *row0, size_t stride, int nrows, int nb) {
+    const size_t bytes = (size_t)nb * (type == mp::TYPE_Q6K ? Q6K_BYTES : Q4K_BYTES);
+    for (int r = 0; r < nrows; ++r)
+        for (size_t o = 0; o < bytes; o += 64) _mm_prefetch((const char *)(row0 + (size_t)r * stride + o), _MM_HINT_T0);
+}
+
 template <int NR>
-MPC_AVX512 static void rows_q4k_vnni(const uint8_t *row0, size_t stride, const uint8_t *q8, int nb, float *out) {
+MPC_AVX512 static void rows_q4k_vnni(const uint8_t *row0, size_t stride, const uint8_t *q8, int nb, float *out,
+                                     bool more) {
     const __m512i m4 = _mm512_set1_epi8(0x0F);
     // int16 lane index of the scale for groups g: lanes 0-15 sub-block 2g, 16-31 sub-block 2g + 1
     __m512i gidx[4];
@@ -225,9 +235,12 @@ MPC_AVX512 static void rows_q4k_vnni(const uint8_t *row0, size_t stride, const u
             for (int g = 0; g < 4; ++g)
                 a = _mm512_dpwssd_epi32(a, _mm512_maddubs_epi16(w[g], xv[g]), _mm512_permutexvar_epi16(gidx[g], sc16));
             si[r] = a;
-            _mm_prefetch((const char *)(b + 4 * Q4K_BYTES), _MM_HINT_T0);
-            _mm_prefetch((const char *)(b + 4 * Q4K_BYTES + 64), _MM_HINT_T0);
-            _mm_prefetch((const char *)(b + 4 * Q4K_BYTES + 128), _MM_HINT_T0);
+            if (more) {
+                const char *pf = (const char *)(b + 4 * stride);
+                _mm_prefetch(pf, _MM_HINT_T0);
+                _mm_prefetch(pf + 64, _MM_HINT_T0);
+                _mm_prefetch(pf + 128, _MM_HINT_T0);
+            }
             // min term: m_j * (bs[2j] + bs[2j+1]) with each min on two int16 lanes
             const __m256i mn2 = _mm256_inserti128_si256(_mm256_castsi128_si256(_mm_unpacklo_epi16(mn16, mn16)),
                                                         _mm_unpackhi_epi16(mn16, mn16), 1);
@@ -253,7 +266,8 @@ MPC_AVX512 static void rows_q4k_vnni(const uint8_t *row0, size_t stride, const u
 // 64-byte vectors; 16-value group c of the super-block has scale c; the -32
 // offset is 32 * sum_c scale_c * bsum_c from the Q8_K block sums
 template <int NR>
-MPC_AVX512 static void rows_q6k_vnni(const uint8_t *row0, size_t stride, const uint8_t *q8, int nb, float *out) {
+MPC_AVX512 static void rows_q6k_vnni(const uint8_t *row0, size_t stride, const uint8_t *q8, int nb, float *out,
+                                     bool more) {
     const __m256i m4 = _mm256_set1_epi8(0x0F), m30 = _mm256_set1_epi8(0x30);
     __m512i cidx[4];           // chunk c (64 values): lanes 8t..8t+7 take scale 4c + t
     for (int c = 0; c < 4; ++c) {
@@ -293,7 +307,8 @@ MPC_AVX512 static void rows_q6k_vnni(const uint8_t *row0, size_t stride, const u
             si[r] = a;
             so[r] = _mm512_zextsi256_si512(_mm256_madd_epi16(sc16, bs));      // sum_c scale_c * bsum_c
             dh[r] = u16_at(b + 208);
-            for (int l = 0; l < 4; ++l) _mm_prefetch((const char *)(b + 3 * Q6K_BYTES + 64 * l), _MM_HINT_T0);
+            if (more)
+                for (int l = 0; l < 4; ++l) _mm_prefetch((const char *)(b + 4 * stride + 64 * l), _MM_HINT_T0);
         }
         for (int r = NR; r < 4; ++r) si[r] = so[r] = _mm512_setzero_si512();
         const __m128i sum_dot = hsum4(si[0], si[1], si[2], si[3]);
@@ -309,11 +324,14 @@ MPC_AVX512 static void rows_q6k_vnni(const uint8_t *row0, size_t stride, const u
 
 MPC_AVX512 static void rows_vnni(int type, const uint8_t *row0, size_t stride, int nrows, const uint8_t *q8, int nb,
                                  float *out) {
+    prefetch_rows(type, row0, stride, std::min(nrows, 4), nb);     // the first group; each group fetches the next
     int r = 0;
     for (; r + 4 <= nrows; r += 4)
-        (type == mp::TYPE_Q6K ? rows_q6k_vnni<4> : rows_q4k_vnni<4>)(row0 + (size_t)r * stride, stride, q8, nb, out + r);
+        (type == mp::TYPE_Q6K ? rows_q6k_vnni<4> : rows_q4k_vnni<4>)(row0 + (size_t)r * stride, stride, q8, nb, out + r,
+                                                                      r + 8 <= nrows);
     for (; r < nrows; ++r)
-        (type == mp::TYPE_Q6K ? rows_q6k_vnni<1> : rows_q4k_vnni<1>)(row0 + (size_t)r * stride, stride, q8, nb, out + r);
+        (type == mp::TYPE_Q6K ? rows_q6k_vnni<1> : rows_q4k_vnni<1>)(row0 + (size_t)r * stride, stride, q8, nb, out + r,
+                                                                      false);
 }
 
 float dot_q4k(const uint8_t *row, const uint8_t *q8, int nb) {
@@ -500,6 +518,8 @@ void up_item(Chain &c, int item) {
     const uint8_t *up = c.e[k].w, *gate = c.e[k].w + (size_t)c.I * rb;
     float *h = c.h + (size_t)k * c.I;
     float u[UP_ROWS], g[UP_ROWS];
+    prefetch_rows(mp::TYPE_Q4K, up + r0 * rb, rb, 4, c.H / QK);       // both first groups at once
+    prefetch_rows(mp::TYPE_Q4K, gate + r0 * rb, rb, 4, c.H / QK);
     dot_rows(mp::TYPE_Q4K, up + r0 * rb, rb, UP_ROWS, c.e[k].q8x, c.H / QK, u);
     dot_rows(mp::TYPE_Q4K, gate + r0 * rb, rb, UP_ROWS, c.e[k].q8x, c.H / QK, g);
     for (int r = 0; r < UP_ROWS; ++r) h[r0 + r] = g[r] / (1.0f + canon_expf(-g[r])) * u[r];

@@ -45,6 +45,8 @@ float dot_q4k(const uint8_t *row, const uint8_t *q8, int nb);
 float dot_q6k(const uint8_t *row, const uint8_t *q8, int nb);
 // nrows rows (stride bytes apart) of type Q4_K or Q6_K against one Q8_K vector
 void dot_rows(int type, const uint8_t *row0, size_t stride, int nrows, const uint8_t *q8, int nb, float *out);
+// bring nrows rows of nb super-blocks into the cache (a hint: never faults)
+void prefetch_rows(int type, const uint8_t *row0, size_t stride, int nrows, int nb);
 bool has_vnni();
 void set_portable(bool on);     // force the portable dots (tests)
 
