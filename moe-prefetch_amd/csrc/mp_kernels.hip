@@ -565,6 +565,15 @@ __global__ __launch_bounds__(512) void down_kernel(ExpertArgs a) {
     const int g = lane >> 3, u = lane & 7;   // g: row within the tile, u: part of a super-block
     const int kt = a.K + a.n_shared;
     if (a.fresh && *a.fresh) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");   // as in gateup_kernel
+    // the combine's inputs other than the rows, loaded now rather than after
+    // the last barrier: the gate weights, and the output being added to
+    float wk[16], prev = 0.0f;
+    if (threadIdx.x < DN_ROWS) {
+#pragma unroll
+        for (int k = 0; k < 16; ++k)
+            if (k < a.K) wk[k] = a.w[k];
+        if (a.accumulate) prev = a.out[r0 + threadIdx.x];
+    }
     for (int kb = 0; kb < kt; kb += 8) {
         const int k = kb + wave;
         const bool mine = k < kt && serves(a, k, SRC);
@@ -686,10 +695,12 @@ __global__ __launch_bounds__(512) void down_kernel(ExpertArgs a) {
     }
     if (threadIdx.x < DN_ROWS) {
         const int t = threadIdx.x;
-        float acc = a.w[0] * s_y[0][t];
-        for (int k = 1; k < a.K; ++k) acc = acc + a.w[k] * s_y[k][t];
+        float acc = wk[0] * s_y[0][t];
+#pragma unroll
+        for (int k = 1; k < 16; ++k)
+            if (k < a.K) acc = acc + wk[k] * s_y[k][t];
         if (a.n_shared) acc = acc + s_y[a.K][t];        // weight 1, after the routed experts
-        a.out[r0 + t] = a.accumulate ? a.out[r0 + t] + acc : acc;
+        a.out[r0 + t] = a.accumulate ? prev + acc : acc;
     }
 }
 
