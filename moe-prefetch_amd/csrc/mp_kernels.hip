@@ -545,6 +545,14 @@ __global__ __launch_bounds__(256) void gateup_kernel(ExpertArgs a) {
 
 }
 
+// Order a wave's LDS writes before its own lanes' later reads of them: the
+// LDS executes one wave's instructions in order, so waiting for the wave's
+// LDS operations and keeping the compiler from moving them across is enough.
+__device__ inline void wave_lds_sync() {
+    __builtin_amdgcn_s_waitcnt(0xc07f);          // lgkmcnt(0)
+    __builtin_amdgcn_wave_barrier();
+}
+
 // ---------------------------------------------------------------------------
 // down + combine.  Workgroup = 8 waves, 8 output rows; wave w owns expert
 // kb + w of each group of 8 experts.
@@ -626,7 +634,9 @@ __global__ __launch_bounds__(512) void down_kernel(ExpertArgs a) {
                 }
             }
         }
-        __syncthreads();
+        // s_w[wave] and s_q8[wave] are written and read by this wave only:
+        // the waves go on without waiting for each other's weights
+        wave_lds_sync();
         if (mine) {
             float y = 0.0f;
             for (int b = 0; b < nb; ++b) {
@@ -691,8 +701,9 @@ __global__ __launch_bounds__(512) void down_kernel(ExpertArgs a) {
                 if (a.ypart && !a.join) a.ypart[(size_t)k * a.H + r0 + g] = y;
             }
         }
-        __syncthreads();
+        wave_lds_sync();        // the next group's writes come after this wave's reads
     }
+    __syncthreads();            // every wave's s_y before the combine
     if (threadIdx.x < DN_ROWS) {
         const int t = threadIdx.x;
         float acc = wk[0] * s_y[0][t];
