@@ -8,18 +8,24 @@
 namespace mp {
 
 // CPU-assisted serving of absent experts: per-layer exchange blocks in
-// mapped, fine-grained host memory.  The GPU posts the routed ids and the Q8_K
-// of x and then the token's sequence number (system-scope release); the host
+// mapped, fine-grained host memory.  The GPU posts the Q8_K of x and the
+// routed ids, each id tagged with the token's sequence number; the host
 // computes the experts assigned to it, writes their rows and answers with
 // the sequence number (or SC_ABORT).
 constexpr int SC_Q8X_BYTES = 8 * 292;          // Q8_K of x at H = 2048
+// One word per routed expert k: (token sequence number << 32) | (slot << 16) |
+// id, where slot is the one the GPU read (n_slots = absent).  Each word is one
+// 8-byte store, so the host takes the layer once every word of it carries the
+// token's number: no word has to land before another.  q8x (the Q8_K of x) is
+// written, and waited for, by an earlier kernel of the layer.
 struct alignas(256) SidecarPost {
-    uint32_t seq;
-    uint32_t pad0[31];
-    int32_t ids[16];
-    int32_t slots[16];                         // the slot the GPU read for each id (n_slots = absent)
+    uint64_t tag[16];
+    uint8_t pad0[128];
     uint8_t q8x[SC_Q8X_BYTES];
 };
+__host__ __device__ inline uint64_t sc_tag(uint32_t seq, int32_t slot, int32_t id) {
+    return ((uint64_t)seq << 32) | ((uint64_t)(uint16_t)slot << 16) | (uint64_t)(uint16_t)id;
+}
 struct alignas(128) SidecarResp {
     uint32_t seq;                              // host -> GPU
     uint32_t pad0[15];

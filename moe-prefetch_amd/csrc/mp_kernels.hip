@@ -355,21 +355,14 @@ __global__ __launch_bounds__(256) void route_select_kernel(RouteArgs a) {
             const bool any = __ballot(streamed) != 0;
             if (lane == 0) *a.fresh = any ? 1u : 0u;
         }
-        // CPU-assisted serving: post the ids and the slots read to the host,
-        // then the sequence number.  One wave.  (Only on the router-GEMV path,
-        // whose kernel wrote the Q8_K of x into the post and waited for it.)
-        // The host reads nothing else the GPU wrote, so the words go out
-        // written through (store_sys) and the wave waits for them (vmcnt 0)
-        // before the sequence number: no write-back of the whole L2, which a
-        // system-scope release would add.
-        if (a.post && !a.logits_in) {
-            if (lane < a.K) {
-                store_sys(&a.post->ids[lane], s_ids[lane]);
-                store_sys(&a.post->slots[lane], slot);
-            }
-            __builtin_amdgcn_s_waitcnt(0x0f70);
-            if (lane == 0) __hip_atomic_store(&a.post->seq, seqv, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-        }
+        // CPU-assisted serving: post each id with the slot read, tagged with
+        // the token's sequence number, one 8-byte store written through to
+        // host memory per word (no L2 write-back, no wait: the host checks
+        // every word's tag).  Only on the router-GEMV path, whose kernel wrote
+        // the Q8_K of x into the post and waited for it before this kernel.
+        if (a.post && !a.logits_in && lane < a.K)
+            __hip_atomic_store(&a.post->tag[lane], sc_tag(seqv, slot, s_ids[lane]), __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_SYSTEM);
     }
     if (look && wave == 1) ahead_post(a, s_top, seqv, lane);      // beside wave 0's own post
     if (!a.logits_in || !a.x || !a.q8x) return;

@@ -2140,11 +2140,16 @@ int moe_cache_set_sidecar(moe_cache *c, int n_threads, int num, int den) {
 
 // wait (bounded) for layer l's post, compute the absent experts assigned to
 // the CPU, publish their rows, answer
+static bool post_ready(const mp::SidecarPost &p, int K, uint32_t seq) {
+    for (int k = 0; k < K; ++k)
+        if ((uint32_t)(__atomic_load_n(&p.tag[k], __ATOMIC_ACQUIRE) >> 32) != seq) return false;
+    return true;
+}
+
 static int sidecar_serve(moe_cache *c, int l, uint32_t seq) {
-    const volatile uint32_t *ps = &c->sc_post[l].seq;
     const auto t0 = std::chrono::steady_clock::now();
     unsigned spins = 0;
-    while (*ps != seq) {
+    while (!post_ready(c->sc_post[l], c->K, seq)) {
         _mm_pause();
         if ((++spins & 1023u) == 0 &&
             std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count() > c->sc_timeout_s)
@@ -2162,7 +2167,8 @@ static int sidecar_serve(moe_cache *c, int l, uint32_t seq) {
     int kk[16];
     int n = 0, r = 0;
     for (int k = 0; k < c->K; ++k) {
-        const int id = p.ids[k], slot = p.slots[k];
+        const uint64_t tg = p.tag[k];
+        const int id = (int)(tg & 0xffff), slot = (int)((tg >> 16) & 0xffff);
         if (id < 0 || id >= ls.E || (slot >= 0 && slot < ls.S)) continue;  // outside the store, or read from a slot
         if (r++ % c->sc_den < c->sc_num) {
             kk[n] = k;
