@@ -29,14 +29,6 @@
 
 namespace mp {
 
-// One wavefront quantizes 256 values (4 per lane, lane-major) to a Q8_K block.
-__device__ void q8k_wave_from(const float xv[4], uint8_t *out, int lane);
-__device__ void q8k_wave(const float *x, uint8_t *out, int lane) {
-    const float4 v = *(const float4 *)(x + 4 * lane);
-    const float xv[4] = {v.x, v.y, v.z, v.w};
-    q8k_wave_from(xv, out, lane);
-}
-
 // the bytes of one Q8_K block from a wave's codes (4 per lane) and scale
 __device__ void q8k_store(const int q[4], float d, uint8_t *out, int lane) {
     const int gs = q8k_group_sum(q);
@@ -47,16 +39,14 @@ __device__ void q8k_store(const int q[4], float d, uint8_t *out, int lane) {
     if (lane == 0) *(float *)out = d;
 }
 
-__device__ void q8k_wave_from(const float xv[4], uint8_t *out, int lane) {
+// One wavefront quantizes 256 values (4 per lane, lane-major) to a Q8_K block.
+__device__ void q8k_wave(const float *x, uint8_t *out, int lane) {
+    const float4 v = *(const float4 *)(x + 4 * lane);
+    const float xv[4] = {v.x, v.y, v.z, v.w};
     int q[4];
     float d;
     q8k_wave_vals(xv, lane, q, d);
-    const int gs = q8k_group_sum(q);
-    const uint32_t packed = (uint32_t)(q[0] & 0xff) | ((uint32_t)(q[1] & 0xff) << 8) |
-                            ((uint32_t)(q[2] & 0xff) << 16) | ((uint32_t)(q[3] & 0xff) << 24);
-    *(uint32_t *)(out + 4 + 4 * lane) = packed;
-    if ((lane & 3) == 0) *(int16_t *)(out + 4 + QK + 2 * (lane >> 2)) = (int16_t)gs;
-    if (lane == 0) *(float *)out = d;
+    q8k_store(q, d, out, lane);
 }
 
 // A store coherent at system scope: written through the caches to memory
