@@ -567,46 +567,70 @@ __global__ __launch_bounds__(512) void down_kernel(ExpertArgs a) {
     }
     for (int kb = 0; kb < kt; kb += 8) {
         const int k = kb + wave;
+        // this expert's h first: vector loads return in the order they were
+        // issued, so h is in registers before the weights issued after it
+        // land, and its Q8_K is computed while they are in flight
+        float xv[3][4];
+        if (nb == 3 && k < kt) {
+#pragma unroll
+            for (int b = 0; b < 3; ++b) {
+                const float4 v = *(const float4 *)(a.h + (size_t)k * a.I + QK * b + 4 * lane);
+                xv[b][0] = v.x; xv[b][1] = v.y; xv[b][2] = v.z; xv[b][3] = v.w;
+            }
+        }
         const bool mine = k < kt && serves(a, k, SRC);
+        bool direct = false;
         if (k < kt && !mine && lane < DN_ROWS)      // the other launch's expert
             s_y[k][lane] = a.join ? a.ypart[(size_t)k * a.H + r0 + lane] : 0.0f;
         if (mine) {
             const uint8_t *eb = expert_base(a, k);
-            uint4 *dst = (uint4 *)s_w[wave];
             const int nvec = DN_ROWS * rowb / 16;           // <= 315
-            uint4 buf[5];
             const uint4 *src = eb ? (const uint4 *)(eb + 2ull * a.I * (a.H / QK) * Q4K_BYTES + (size_t)r0 * rowb)
                                   : nullptr;
+            // Q8_K of h into LDS (every workgroup quantizes the same h the
+            // same way: identical bytes)
+            auto quantize_h = [&]() {
+                if (nb == 3) {
+                    int q[3][4];
+                    float d[3];
+                    q8k_wave_vals_n<3>(xv, lane, q, d);
 #pragma unroll
-            for (int j = 0; j < 5; ++j) {
-                const int i = lane + 64 * j;
-                buf[j] = (src && i < nvec) ? src[i] : make_uint4(0, 0, 0, 0);
-            }
-            // Q8_K of this expert's h, straight into LDS, while the weight
-            // loads are in flight (every workgroup quantizes the same h the
-            // same way: identical bytes); the h loads of all blocks first
-            if (nb == 3) {
-                float xv[3][4];
-                int q[3][4];
-                float d[3];
-#pragma unroll
-                for (int b = 0; b < 3; ++b) {
-                    const float4 v = *(const float4 *)(a.h + (size_t)k * a.I + QK * b + 4 * lane);
-                    xv[b][0] = v.x; xv[b][1] = v.y; xv[b][2] = v.z; xv[b][3] = v.w;
+                    for (int b = 0; b < 3; ++b) q8k_store(q[b], d[b], s_q8[wave] + b * Q8K_BYTES, lane);
+                } else {
+                    for (int b = 0; b < nb; ++b)
+                        q8k_wave(a.h + (size_t)k * a.I + QK * b, s_q8[wave] + b * Q8K_BYTES, lane);
                 }
-                q8k_wave_vals_n<3>(xv, lane, q, d);
+            };
+            // Rows that need no staging copy go straight from memory into LDS
+            // (16 bytes a lane, lane-contiguous: the layout the dots read).
+            // The others pass through registers on their way to the staging
+            // area too.  Each branch quantizes h after issuing its loads.
+            uint8_t *sb = SRC != SRC_HBM ? stage_base(a, k) : nullptr;
+            direct = src && !sb;
+            if (direct) {
 #pragma unroll
-                for (int b = 0; b < 3; ++b) q8k_store(q[b], d[b], s_q8[wave] + b * Q8K_BYTES, lane);
+                for (int j = 0; j < 5; ++j) {
+                    const int i = lane + 64 * j;
+                    if (i < nvec)
+                        __builtin_amdgcn_global_load_lds((const void *)(src + i),
+                                                         (__attribute__((address_space(3))) void *)(s_w[wave] + 1024 * j),
+                                                         16, 0, 0);
+                }
+                quantize_h();
             } else {
-                for (int b = 0; b < nb; ++b) q8k_wave(a.h + (size_t)k * a.I + QK * b, s_q8[wave] + b * Q8K_BYTES, lane);
-            }
+                uint4 buf[5];
 #pragma unroll
-            for (int j = 0; j < 5; ++j) {
-                const int i = lane + 64 * j;
-                if (i < nvec) dst[i] = buf[j];
-            }
-            if (SRC != SRC_HBM) {
-                uint8_t *sb = stage_base(a, k);
+                for (int j = 0; j < 5; ++j) {
+                    const int i = lane + 64 * j;
+                    buf[j] = (src && i < nvec) ? src[i] : make_uint4(0, 0, 0, 0);
+                }
+                quantize_h();
+                uint4 *dst = (uint4 *)s_w[wave];
+#pragma unroll
+                for (int j = 0; j < 5; ++j) {
+                    const int i = lane + 64 * j;
+                    if (i < nvec) dst[i] = buf[j];
+                }
                 if (sb) {
                     uint4 *sd = (uint4 *)(sb + 2ull * a.I * (a.H / QK) * Q4K_BYTES + (size_t)r0 * rowb);
 #pragma unroll
@@ -618,7 +642,9 @@ __global__ __launch_bounds__(512) void down_kernel(ExpertArgs a) {
             }
         }
         // s_w[wave] and s_q8[wave] are written and read by this wave only:
-        // the waves go on without waiting for each other's weights
+        // the waves go on without waiting for each other's weights (the
+        // loads into LDS count as vector memory operations: wait for those too)
+        if (direct) __builtin_amdgcn_s_waitcnt(0x0f70);       // vmcnt(0)
         wave_lds_sync();
         if (mine) {
             float y = 0.0f;
