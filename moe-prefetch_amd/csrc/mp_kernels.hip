@@ -786,7 +786,7 @@ hipError_t launch_route(const RouteLaunch &l, hipStream_t st, hipEvent_t *ev) {
 
 template <int SRC>
 static hipError_t gateup_src(const ExpertArgs &a, hipStream_t st, hipEvent_t e0, hipEvent_t e1) {
-    constexpr int R = 2;
+    constexpr int R = 1;
     return launch(gateup_kernel<R, SRC>, dim3((unsigned)(a.I / (4 * R)), (unsigned)(a.K + a.n_shared)), dim3(256), st,
                   e0, e1, a);
 }
