@@ -111,14 +111,15 @@ struct RouteArgs {
 // (lane j accumulates W[256 i + 4 j + c] * x[...] with fmaf, i then c, then a
 // butterfly over the 64 lanes), plus the steering bias when given.  The first
 // H/256 workgroups also write the Q8_K blocks of x.  With router lookahead
-// (batch 1) E/4 more workgroups per target layer T score T's router on the
+// (batch 1) E more single-wave workgroups per target layer T score T's router on the
 // products x[i] * r_T[i] (rounded to f32) in the same order.
-__global__ __launch_bounds__(256) void route_logits_kernel(RouteArgs a) {
+constexpr int RL_WAVES = 1;                      // router GEMV: rows (waves) per workgroup
+__global__ __launch_bounds__(64 * RL_WAVES) void route_logits_kernel(RouteArgs a) {
     const int tok = blockIdx.y;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int per = (a.E + 3) / 4;
+    const int per = (a.E + RL_WAVES - 1) / RL_WAVES;
     const int t = (int)blockIdx.x / per;             // 0: this layer, 1..an: lookahead target t - 1
-    const int e = ((int)blockIdx.x - t * per) * 4 + wave;
+    const int e = ((int)blockIdx.x - t * per) * RL_WAVES + wave;
     const float *x = a.x + (size_t)tok * a.H;
     if (e >= a.E) return;
     if (t > 0) {
@@ -776,9 +777,9 @@ hipError_t launch_route(const RouteLaunch &l, hipStream_t st, hipEvent_t *ev) {
     if (l.logits_in)
         return launch(route_select_kernel, dim3((unsigned)l.n_tok), dim3(256), st, ev ? ev[2] : nullptr,
                       ev ? ev[3] : nullptr, a);
-    const unsigned per = (unsigned)((l.E + 3) / 4);
+    const unsigned per = (unsigned)((l.E + RL_WAVES - 1) / RL_WAVES);
     const hipError_t e = launch(route_logits_kernel, dim3(per * (unsigned)(1 + (l.apost ? l.an : 0)), (unsigned)l.n_tok),
-                                dim3(256), st, ev ? ev[0] : nullptr, ev ? ev[1] : nullptr, a);
+                                dim3(64 * RL_WAVES), st, ev ? ev[0] : nullptr, ev ? ev[1] : nullptr, a);
     if (e != hipSuccess) return e;
     return launch(route_select_kernel, dim3((unsigned)l.n_tok), dim3(256), st, ev ? ev[2] : nullptr,
                   ev ? ev[3] : nullptr, a);
