@@ -440,8 +440,9 @@ __device__ inline void q4k_lane(uint4 hdr, uint4 qs, int u, const uint32_t *xlo,
     mi = ml * bslo + mh * bshi;
 }
 
+constexpr int GU_WAVES = 4;                      // gate/up: waves per workgroup
 template <int R, int SRC>
-__global__ __launch_bounds__(256) void gateup_kernel(ExpertArgs a) {
+__global__ __launch_bounds__(64 * GU_WAVES) void gateup_kernel(ExpertArgs a) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int k = blockIdx.y;
     if (!serves(a, k, SRC)) return;
@@ -466,7 +467,7 @@ __global__ __launch_bounds__(256) void gateup_kernel(ExpertArgs a) {
     const int16_t *bs = (const int16_t *)(xq + 4 + QK);
     const int bslo = bs[4 * j + (u & 1)], bshi = bs[4 * j + 2 + (u & 1)];
 
-    const int row0 = (blockIdx.x * 4 + wave) * R;
+    const int row0 = (blockIdx.x * GU_WAVES + wave) * R;
     uint4 hg[R], qg[R], hu[R], qu[R];
 #pragma unroll
     for (int r = 0; r < R; ++r) {
@@ -788,7 +789,8 @@ hipError_t launch_route(const RouteLaunch &l, hipStream_t st, hipEvent_t *ev) {
 template <int SRC>
 static hipError_t gateup_src(const ExpertArgs &a, hipStream_t st, hipEvent_t e0, hipEvent_t e1) {
     constexpr int R = 1;
-    return launch(gateup_kernel<R, SRC>, dim3((unsigned)(a.I / (4 * R)), (unsigned)(a.K + a.n_shared)), dim3(256), st,
+    return launch(gateup_kernel<R, SRC>, dim3((unsigned)(a.I / (GU_WAVES * R)), (unsigned)(a.K + a.n_shared)),
+                  dim3(64 * GU_WAVES), st,
                   e0, e1, a);
 }
 
