@@ -15,8 +15,9 @@ namespace mp {
 constexpr int SC_Q8X_BYTES = 8 * 292;          // Q8_K of x at H = 2048
 // One word per routed expert k: (token sequence number << 32) | (slot << 16) |
 // id, where slot is the one the GPU read (n_slots = absent).  Each word is one
-// 8-byte store, so the host takes the layer once every word of it carries the
-// token's number: no word has to land before another.  q8x (the Q8_K of x) is
+// aligned 8-byte store (one write on PCIe, read by the host in one 8-byte
+// load), so the host takes the layer once every word of it carries the token's
+// number: no word has to land before another.  q8x (the Q8_K of x) is
 // written, and waited for, by an earlier kernel of the layer.
 struct alignas(256) SidecarPost {
     uint64_t tag[16];
