@@ -46,8 +46,9 @@ constexpr int AHEAD_K = 8;                     // candidates per target layer at
 
 // Router lookahead record: layer L's router launch scores the routers of
 // layers L+1 and L+2 on L's input (x * g_T / g_L) and posts, per target, the
-// experts of its top-k whose table word is the dummy, best first.  seq last
-// (system-scope release).  t: the GPU's 100 MHz wall clock at the post.
+// experts of its top-k whose table word is the dummy, best first: every word
+// written through to host memory, the wave waits for them, seq last.  t: the
+// GPU's 100 MHz wall clock at the post.
 struct alignas(256) AheadPost {
     uint32_t seq;
     uint32_t layer;
