@@ -183,7 +183,7 @@ typedef struct moe_cache moe_cache;
 
 typedef struct {
     int32_t n_layers, n_experts, n_expert_used;  /* L, E, K */
-    int32_t hidden, intermediate;                /* H (2048), I (multiple of 256, <= 1024) */
+    int32_t hidden, intermediate;                /* H (2048), I (256, 512 or 768) */
     int32_t n_slots;                             /* default slots per layer (--moe-expert-cache) */
     const int32_t *slot_profile;                 /* [n_layers] slots per layer or NULL (LLAMA_MOE_SLOT_PROFILE) */
     const int32_t *down_type;                    /* [n_layers] MOE_TYPE_* or NULL = all Q4_K */

@@ -831,7 +831,10 @@ __global__ __launch_bounds__(256) void join_kernel(JoinArgs a) {
                 ok = 1;
                 break;
             }
-            if (v == SC_ABORT) break;
+            if (v == SC_ABORT) {        // the host gave up: the token fails, never passes silently
+                if (blockIdx.x == 0) __hip_atomic_store(&a.resp->err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+                break;
+            }
             if (wall_clock64() - t0 > a.timeout_ticks) {
                 if (blockIdx.x == 0) __hip_atomic_store(&a.resp->err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
                 break;

@@ -1216,6 +1216,15 @@ int moe_memcpy(void *dst, const void *src, size_t bytes) {
 
 bool moe_memcpy_h2d_batch(int device, void **dst, const void **src, const size_t *sizes, int n) {
     if (n <= 0) return true;
+    if (!dst || !src || !sizes) {
+        fail(MOE_ERR_ARG, "moe_memcpy_h2d_batch: null array");
+        return false;
+    }
+    for (int i = 0; i < n; ++i)         // nothing is copied when any slice is unusable
+        if (!dst[i] || !src[i]) {
+            fail(MOE_ERR_ARG, "moe_memcpy_h2d_batch: slice %d of %d has a null address", i, n);
+            return false;
+        }
     if (hipSetDevice(device) != hipSuccess) return false;
     for (int i = 0; i < n; ++i) {
         if (hipMemcpyAsync(dst[i], src[i], sizes[i], hipMemcpyHostToDevice, hipStreamPerThread) != hipSuccess) {
@@ -2108,16 +2117,20 @@ int moe_cache_set_sidecar(moe_cache *c, int n_threads, int num, int den) {
     if (!c->sc_post) {
         if (hipHostMalloc((void **)&c->sc_post, NL * sizeof(mp::SidecarPost), fl) != hipSuccess ||
             hipHostMalloc((void **)&c->sc_resp, NL * sizeof(mp::SidecarResp), fl) != hipSuccess ||
-            hipHostMalloc((void **)&c->sc_rows, NL * c->K * c->H * sizeof(float), fl) != hipSuccess ||
-            hipHostMalloc((void **)&c->h_seq, 64, hipHostMallocDefault) != hipSuccess ||
-            hipMalloc(&c->d_seq, 64) != hipSuccess)
+            hipHostMalloc((void **)&c->sc_rows, NL * c->K * c->H * sizeof(float), fl) != hipSuccess)
             return fail(MOE_ERR_NOMEM, "CPU-assisted serving buffers");
+        // the sequence number may already exist (streaming allocates it too)
+        if (!c->h_seq) {
+            if (hipHostMalloc((void **)&c->h_seq, 64, hipHostMallocDefault) != hipSuccess ||
+                hipMalloc(&c->d_seq, 64) != hipSuccess)
+                return fail(MOE_ERR_NOMEM, "sequence number");
+            HIPCHK(hipMemset(c->d_seq, 0, 64));
+        }
         memset((void *)c->sc_post, 0, NL * sizeof(mp::SidecarPost));
         memset((void *)c->sc_resp, 0, NL * sizeof(mp::SidecarResp));
         HIPCHK(hipHostGetDevicePointer((void **)&c->sc_post_d, c->sc_post, 0));
         HIPCHK(hipHostGetDevicePointer((void **)&c->sc_resp_d, c->sc_resp, 0));
         HIPCHK(hipHostGetDevicePointer((void **)&c->sc_rows_d, c->sc_rows, 0));
-        HIPCHK(hipMemset(c->d_seq, 0, 64));
     }
     if (c->team && mpc::team_size(c->team) != n_threads) {
         mpc::team_destroy(c->team);
@@ -2403,6 +2416,14 @@ int moe_decode_token(moe_cache *c, const float *x, const float *bias, float *out
         *c->h_seq = seq;
         HIPCHK(hipMemcpyAsync(c->d_seq, c->h_seq, 4, hipMemcpyHostToDevice, st));
     }
+    // An earlier token that failed may have left SC_ABORT in the answers; a
+    // join of this token must wait for this token's answer, not end on that.
+    // Nothing of this token runs yet, so plain stores suffice.
+    if (sc)
+        for (int l = 0; l < NL; ++l) {
+            *(volatile uint32_t *)&c->sc_resp[l].seq = 0;
+            *(volatile uint32_t *)&c->sc_resp[l].err = 0;
+        }
     // streaming: the mover serves this token's lookahead records
     bool mover_on = false;
     if (stm && !stm->failed) {

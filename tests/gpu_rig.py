@@ -47,7 +47,7 @@ def synth_experts_dev(seed, layer, e0, n, I, dt, out_ptr, stride):
 
 class Rig:
     def __init__(self, slots, down_types, T, I=768, seed=42, steer=True, zipf_s=1.1, reuse=0.6, E=E, shared=False,
-                 residual=False, **knobs):
+                 residual=False, skip_router=(), **knobs):
         self.nl = len(slots)
         self.slots, self.down_types, self.T, self.I, self.seed = list(slots), list(down_types), T, I, seed
         self.E = E
@@ -84,7 +84,8 @@ class Rig:
                               down_types=self.down_types, device=0, **knobs)
         for l in range(self.nl):
             self.cache.set_host_store(l, self.stores[l].ptr)
-            self.cache.set_router(l, self.W[l])
+            if l not in skip_router:
+                self.cache.set_router(l, self.W[l])
             if self.shared[l] is not None:
                 self.cache.set_shared(l, self.shared[l])
             if self.g is not None:

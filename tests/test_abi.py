@@ -42,3 +42,20 @@ def test_pure_host_queries():
     assert L.moe_expert_bytes(2048, 512, _lib.TYPE_Q6K) == 2039808
     assert L.moe_route_workspace_bytes(128, 1) > 0
     assert L.moe_experts_workspace_bytes(768, 8) >= 8 * 768 * 4
+
+
+def test_h2d_batch_refuses_on_the_host():
+    # the reference's contract (patches/0006...:52-76): n <= 0 is done at once;
+    # a batch that cannot be copied returns false and the caller treats it as
+    # not done.  Null arrays or slice addresses are refused before any copy.
+    import ctypes
+    L = moe_prefetch.lib()
+    assert L.moe_memcpy_h2d_batch(0, None, None, None, 0) is True
+    assert L.moe_memcpy_h2d_batch(0, None, None, None, -3) is True
+    assert L.moe_memcpy_h2d_batch(0, None, None, None, 2) is False
+    P = ctypes.c_void_p * 2
+    buf = ctypes.create_string_buffer(64)
+    dst, src = P(ctypes.addressof(buf), None), P(ctypes.addressof(buf), ctypes.addressof(buf))
+    sizes = (ctypes.c_size_t * 2)(16, 16)
+    assert L.moe_memcpy_h2d_batch(0, dst, src, sizes, 2) is False
+    assert b"slice 1 of 2" in L.moe_last_error()

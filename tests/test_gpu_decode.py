@@ -21,16 +21,23 @@ pytestmark = pytest.mark.gpu
 Q4, Q6 = _lib.TYPE_Q4K, _lib.TYPE_Q6K
 
 
-def check_run(rig, tmp_path, out_every=1, tol=1e-3, oc=None, record_map=True):
+def check_run(rig, tmp_path, out_every=1, tol=1e-3, oc=None, record_map=True, tokens=None):
+    """Decode `tokens` (default: all of the rig's) and compare with the oracle
+    token by token.  Leaves the product's and the oracle's counters and the
+    number of evictions seen in the frames (a slot whose expert was replaced)
+    on the rig as stats, ostats and n_evicted."""
     rp, mp = str(tmp_path / "gpu.routes"), str(tmp_path / "gpu.map") if record_map else None
     orp, omp = str(tmp_path / "ora.routes"), str(tmp_path / "ora.map") if record_map else None
     rig.cache.trace_open(rp, mp)
     oc = rig.oracle_cache() if oc is None else oc
     oc.trace_open(orp, omp)
-    keep = set(range(0, rig.T, out_every))
-    ids_all, outs, frames = rig.run(keep_out=keep)
+    tokens = list(range(rig.T)) if tokens is None else list(tokens)
+    keep = set(tokens[::out_every]) | {tokens[-1]}
+    ids_all, outs, frames = rig.run(tokens=tokens, keep_out=keep)
     worst = 0.0
-    for t in range(rig.T):
+    prev = [oc.frame(l) for l in range(rig.nl)]
+    rig.n_evicted = 0
+    for t in tokens:
         for l in range(rig.nl):
             tbl, prior = oc.table(l)
             use_prior = prior if rig.knobs.get("cache_prior", 0.0) > 0 else None
@@ -46,7 +53,11 @@ def check_run(rig, tmp_path, out_every=1, tol=1e-3, oc=None, record_map=True):
             oc.observe(l, rids)
         oc.step()
         for l in range(rig.nl):
-            assert np.array_equal(frames[t][l], oc.frame(l)), (t, l)
+            f = oc.frame(l)
+            assert np.array_equal(frames[t][l], f), (t, l)
+            rig.n_evicted += int(np.sum((prev[l] >= 0) & (f != prev[l])))
+            prev[l] = f
+    rig.stats, rig.ostats = rig.cache.stats(), oc.stats()
     rig.cache.close()
     oc.close()
     assert open(rp).read() == open(orp).read()
@@ -281,6 +292,49 @@ def test_decode_48_layers_full_shape(tmp_path):
         check_run(rig, tmp_path, out_every=6)
     finally:
         rig.close()
+
+
+def test_decode_48_layers_past_cache_fill(tmp_path):
+    """The stacked shape through the cache fill and into eviction: with at
+    most 2 uploads per layer per token a 56-slot layer cannot fill before
+    token 28, and the first LRU victims come near token 40.  64 tokens: ids,
+    frames, route and map traces bit-exact at every token, outputs sampled,
+    and the run must have evicted and denied admission (P6:785-841,
+    P7:398-429) with the oracle's counters."""
+    rig = Rig([56] * 48, [Q6 if l % 2 else Q4 for l in range(48)], T=64, admit="window", batch_tables=True)
+    try:
+        check_run(rig, tmp_path, out_every=16)
+    finally:
+        rig.close()
+    st, ost = rig.stats, rig.ostats
+    for k in ("n_hit", "n_miss", "n_scheduled", "n_published", "n_admit_ok", "n_admit_denied", "n_table_flushes"):
+        assert st[k] == ost[k], (k, st[k], ost[k])
+    print("evicted", rig.n_evicted, "denied", st["n_admit_denied"], "hit", st["n_hit"] / (st["n_hit"] + st["n_miss"]))
+    assert rig.n_evicted > 100 and st["n_admit_denied"] > 100
+
+
+def test_sidecar_host_abort_then_next_token_exact(tmp_path):
+    """The host gives up on a token (here: layer 1 has no router, so the
+    decode fails after layer 0's kernels, its join included, were launched):
+    the host writes SC_ABORT, layer 0's join ends its bounded wait, the call
+    returns an error, and every kernel has exited.  The next tokens decode
+    bit-exact against an oracle that never saw the failed token: the stale
+    SC_ABORT must not end their joins early (P9:322-359; the reference forces
+    the same case with a dead host, cpp/test-moe-sidecar.cpp:150)."""
+    rig = Rig([16, 24], [Q4, Q6], T=10, admit="window", batch_tables=True, skip_router={1})
+    rig.cache.set_decode_path(split=0, graph=False)
+    rig.cache.set_sidecar(4)
+    out = torch.empty((rig.nl, 2048), dtype=torch.float32, device=rig.dev)
+    with pytest.raises(_lib.MoeError, match="router"):
+        rig.cache.decode_token(rig.x[0], out, bias=rig.bias[0], stream=torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    assert rig.cache.stats()["n_steps"] == 0            # the failed token observed and stepped nothing
+    rig.cache.set_router(1, rig.W[1])
+    try:
+        check_run(rig, tmp_path, tokens=range(1, rig.T))
+    finally:
+        rig.close()
+    assert rig.stats["n_cpu_served"] > 0
 
 
 def test_expert_cache_dropin():

@@ -236,3 +236,33 @@ def test_experts_rejects_unmapped_host_memory():
         assert b"not device memory" in L().moe_last_error()
     finally:
         store.free()
+
+
+def test_h2d_batch_copies_three_slices():
+    # moe_memcpy_h2d_batch through the C ABI as the reference's upload worker
+    # calls ggml_backend_cuda_memcpy_h2d_batch (patches/0006...:52-76,
+    # 428-440): the up, gate and down slices of two experts of the pinned
+    # store, each to its place in a slot, one synchronisation; read back
+    I, dt = 768, _lib.TYPE_Q6K
+    eb = L().moe_expert_bytes(H, I, dt)
+    gu = I * (H // 256) * 144            # one Q4_K matrix (up or gate)
+    store = Pinned(3 * eb)
+    try:
+        _lib.check(L().moe_synth_experts_host(13, 2, 0, 3, H, I, dt, 0.02, store.ptr, eb, 8), "host")
+        slots = torch.zeros(2 * eb, dtype=torch.uint8, device=DEV)
+        torch.cuda.synchronize()
+        cuts = [(0, gu), (gu, gu), (2 * gu, eb - 2 * gu)]
+        dst, src, sizes = [], [], []
+        for slot, e in ((0, 2), (1, 0)):          # expert 2 -> slot 0, expert 0 -> slot 1
+            for off, n in cuts:
+                dst.append(slots.data_ptr() + slot * eb + off)
+                src.append(store.ptr + e * eb + off)
+                sizes.append(n)
+        P = ctypes.c_void_p * 6
+        ok = L().moe_memcpy_h2d_batch(0, P(*dst), P(*src), (ctypes.c_size_t * 6)(*sizes), 6)
+        assert ok is True, L().moe_last_error()
+        got = slots.cpu().numpy()
+        assert np.array_equal(got[:eb], store.arr[2 * eb:3 * eb])
+        assert np.array_equal(got[eb:], store.arr[:eb])
+    finally:
+        store.free()

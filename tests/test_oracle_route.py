@@ -131,7 +131,7 @@ def test_route_bias_steers():
     assert sorted(ids) == want
 
 
-def _rand_expert(H, I, down_type):
+def _rand_expert(H, I, down_type, rng=rng):
     upb = I * (H // 256) * 144
     nb_dn = H * (I // 256)
     parts = []
@@ -158,8 +158,9 @@ def _rand_expert(H, I, down_type):
 def test_expert_chain_vs_f64(down_type):
     H, I = 2048, 768
     upb = I * (H // 256) * 144
-    e = _rand_expert(H, I, down_type)
-    x = rng.standard_normal(H).astype(np.float32)
+    r = np.random.default_rng(1000 + down_type)     # its own stream: independent of test order
+    e = _rand_expert(H, I, down_type, r)
+    x = r.standard_normal(H).astype(np.float32)
     y, h = O.expert_chain(H, I, down_type, e, x)
     Wu = O.dequant(O.Q4K, e[:upb], I * H).reshape(I, H).astype(np.float64)
     Wg = O.dequant(O.Q4K, e[upb:2 * upb], I * H).reshape(I, H).astype(np.float64)
@@ -171,12 +172,12 @@ def test_expert_chain_vs_f64(down_type):
     hq = O.dequant_q8k(O.quant_q8k(h), I).astype(np.float64)   # same h quantization
     y64 = Wd @ hq
     assert np.linalg.norm(y - y64) <= 1e-5 * np.linalg.norm(y64)
-    # without activation quantization the result is ~1e-2 away: the Q8_K step
-    # dominates, which is why the GPU path quantizes exactly like this
+    # without activation quantization the result is 1e-2 .. 1e-1 away: the Q8_K
+    # step dominates, which is why the GPU path quantizes exactly like this
     u2, g2 = Wu @ x, Wg @ x
     yf = Wd @ (g2 / (1 + np.exp(-g2)) * u2)
     rel = np.linalg.norm(y - yf) / np.linalg.norm(yf)
-    assert 1e-3 < rel < 5e-2
+    assert 1e-3 < rel < 0.25, rel
 
 
 def test_moe_layer_combines_in_k_order():
