@@ -397,21 +397,32 @@ int moe_predictor_update(moe_predictor *p, int layer, const moe_predictor_lists 
                          int n_truth, float lr, float *recall);
 int moe_predictor_save(const moe_predictor *p, const char *path);
 
-/* Kernel time of the decode, from HIP events recorded around each launch on
- * the stream it runs on (off by default; set before decoding).  Experts
- * resident in HBM slots and experts read from the pinned store run as
- * separate launches on two streams (fork/join per layer). */
+/* Kernel time of the decode, from HIP events stamped by each launch's
+ * dispatch on the stream it runs on (off by default; set before decoding;
+ * the token's launches then run eagerly).  With the fused layer (split 0)
+ * layer_ms is filled; with split 3 route_ms, gateup_hbm_ms and
+ * down_hbm_ms (one launch each, every expert); with splits 1 and 2 resident
+ * and absent experts run as separate launches.  Bytes count the expert
+ * weights the GPU read, by source (the host's share of absent experts under
+ * CPU-assisted serving is not counted). */
 typedef struct {
     double route_ms;                       /* route_logits + route_select */
     double gateup_hbm_ms, down_hbm_ms;     /* resident experts */
     double gateup_host_ms, down_host_ms;   /* absent experts (pinned store over PCIe) */
     uint64_t n_layers;                     /* layer decodes timed */
     uint64_t gateup_hbm_bytes, down_hbm_bytes, gateup_host_bytes, down_host_bytes;
+    double layer_ms;                       /* split 0: the fused layer launch */
+    uint64_t layer_hbm_bytes;              /* its router rows + resident (and shared) experts' bytes */
+    uint64_t layer_host_bytes;             /* its absent experts' bytes read from the pinned store */
 } moe_kernel_times;
 int moe_cache_set_timing(moe_cache *c, int on);
-/* split: 0 one expert launch serves resident and absent experts (default);
- * 1 resident and absent experts as separate launches on two streams, forked
- * and joined per layer; 2 the same launches one after the other on one stream.
+/* split: 0 (default) the fused layer -- router GEMV, selection, every routed
+ * expert's gate/up and down rows and the weighted combine in one launch,
+ * resident and absent experts alike (moe_decode_token without streaming;
+ * moe_decode_layer and streaming use split 3's launches);
+ * 3 router GEMV, selection, gate/up and down as four launches; 1 resident and
+ * absent experts as separate launches on two streams, forked and joined per
+ * layer; 2 the same launches one after the other on one stream.
  * graph: replay each token's launches as one captured HIP graph (default 1;
  * timing mode launches eagerly).  Every path gives the same bits. */
 int moe_cache_set_decode_path(moe_cache *c, int split, int graph);
@@ -490,8 +501,23 @@ typedef struct {
 
 size_t moe_grouped_workspace_bytes(int n_tok, int K, int H, int I);
 /* Q8_K of x, up/gate over each expert's pairs with the SwiGLU, Q8_K of h, down
- * times the gate weight, and the sum over k (moe_combine) into out. */
+ * times the gate weight, and the sum over k (moe_combine) into out.  Every
+ * pair must be placed by the dispatch (its id in [0, E)): the row of a pair
+ * moe_dispatch left out is never written. */
 int moe_grouped_experts(const moe_grouped_desc *d, void *stream);
+
+/* No counterpart in the reference.  moe_grouped_experts for callers that
+ * cannot allocate device memory (code under HIP graph capture, serving loops
+ * and harnesses that forbid hipMalloc): the same kernels and results, with
+ * the workspace in a static device array of MOE_GROUPED_STATIC_SCRATCH_BYTES
+ * per device instead of d->workspace (which must be NULL; kernel_ms must be
+ * NULL too).  Refuses, with MOE_ERR_ARG, a shape whose workspace
+ * (moe_grouped_workspace_bytes) exceeds that: batch-64 decode at K = 8,
+ * I = 768 needs 8.1 MiB (up to 126 tokens fit).  Calls no allocator.  Every call on one device
+ * shares that device's array: calls that overlap on one device (two streams,
+ * two threads) race and must be serialised by the caller. */
+#define MOE_GROUPED_STATIC_SCRATCH_BYTES (16u << 20)
+int moe_grouped_experts_static(const moe_grouped_desc *d, void *stream);
 /* out[t] (+)= sum_k pair_rows[t*K + k], k ascending */
 int moe_combine(const float *pair_rows, int n_tok, int K, int H, float *out, int accumulate, void *stream);
 

@@ -34,6 +34,8 @@
 #include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 
+#include <mutex>
+
 #include "mp_device.h"
 #include "mp_format.h"
 #include "mp_internal.h"
@@ -780,6 +782,34 @@ hipError_t launch_combine(const float *ypair, int n_tok, int K, int H, float *ou
     if (n4 == 0) return hipSuccess;
     return launch_b(combine_kernel, dim3((unsigned)((n4 + 255) / 256)), dim3(256), st, nullptr, nullptr, ypair, n_tok,
                     K, H, out, accumulate);
+}
+
+// ---------------------------------------------------------------------------
+// Scratch of the allocation-free grouped entry point: the workspace of one
+// call (Q8_K codes of x and h, the up/gate rows, the weighted pair rows) in
+// a file-scope array.  Every device the library runs on holds its own copy
+// at its own address from the code object's load until the process ends.
+// In host code `scratch` names a host-side stand-in, not device memory:
+// kernels are given the address static_scratch() looks up.
+static __device__ __align__(256) uint8_t scratch[STATIC_SCRATCH_BYTES];
+
+hipError_t static_scratch(void **ptr) {
+    constexpr int MAX_DEV = 64;
+    static std::mutex m;
+    static void *addr[MAX_DEV] = {};
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    if (dev < 0 || dev >= MAX_DEV) return hipErrorInvalidDevice;
+    std::lock_guard<std::mutex> lk(m);
+    if (!addr[dev]) {           // once per device, with that device current
+        void *p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return e;
+        addr[dev] = p;
+    }
+    *ptr = addr[dev];
+    return hipSuccess;
 }
 
 }  // namespace mp

@@ -115,6 +115,30 @@ __device__ inline void q8k_wave_vals_n(const float (*xv)[4], int lane, int (*q)[
     }
 }
 
+// Selection value -> 64-bit key whose unsigned order is the selection order:
+// the value's bits mapped onto an unsigned order (a NaN taken as -inf, -0 as
+// +0, so that equal values give equal bits), then the lower id first.  The
+// rank of an expert is the number of keys above its own -- one unsigned
+// comparison per expert, no chain of float compares.
+__device__ inline uint64_t sel_key(float v, int id) {
+    v = v != v ? -INFINITY : v + 0.0f;
+    const uint32_t b = __float_as_uint(v);
+    const uint32_t o = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+    return ((uint64_t)o << 32) | (uint64_t)(0xffffffffu - (uint32_t)id);
+}
+
+// rank of `key` among n keys in LDS (the count of keys above it)
+__device__ inline int key_rank(const uint64_t *s_key, int n, uint64_t key) {
+    int rank = 0;
+#pragma unroll 8
+    for (int j = 0; j < n; j += 2) {
+        const uint4 u = *(const uint4 *)&s_key[j];
+        rank += (((uint64_t)u.y << 32) | u.x) > key;
+        rank += (((uint64_t)u.w << 32) | u.z) > key;
+    }
+    return rank;
+}
+
 // the 16-value group sum of the Q8_K block, valid on lanes with (lane & 3) == 0
 __device__ inline int q8k_group_sum(const int q[4]) {
     int gs = q[0] + q[1] + q[2] + q[3];

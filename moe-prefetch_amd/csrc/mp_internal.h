@@ -143,6 +143,36 @@ struct JoinArgs {
     float *out;               // dev [H]
 };
 
+// A batch-1 decode layer in one launch: the router GEMV, the selection, every
+// routed expert's gate/up rows, its down rows and the weighted combine.
+// Inside the launch the phases pass tagged 8-byte words, (token sequence
+// number << 32) | payload, each written and read whole at agent scope; a word
+// is valid once its tag is the token's number, so nothing is reset between
+// tokens.  Workgroups in index order: [0, E) router rows, the selection,
+// gate/up row tiles, down row tiles, combine tiles; a workgroup waits only
+// for words of workgroups with a lower index.
+constexpr int FUSED_COPIES = 16;    // copies of the routing record (fewer readers per line)
+constexpr int FUSED_REC = 32;       // words per copy: [k] sc_tag(seq, slot, id) of routed expert k,
+                                    // [16 + k] (seq << 32) | bits of its gate weight
+constexpr int FUSED_GU_ROWS = 2;    // gate/up rows per wave
+constexpr int FUSED_DN_TILE = 32;   // down rows per workgroup (8 per wave)
+struct FusedArgs {
+    RouteLaunch r;            // router and selection (seq, table, prior, bias, post; no lookahead)
+    ExpertArgs x;             // the experts; x.ids/slots/w receive the selection.  x.ypart set: the down
+                              // rows go there for the join kernel (CPU-assisted serving) and there is
+                              // no combine; else combine workgroups write x.out
+    uint64_t *xlog;           // [256] tagged logits (bias added)
+    uint64_t *rec;            // [FUSED_COPIES][FUSED_REC] tagged routing words
+    uint64_t *hx;             // [K + 1][I] tagged SwiGLU activations
+    uint64_t *yx;             // [K + 1][H] tagged down rows
+    uint32_t *err;            // a bounded wait ran out: the token's sequence number is written here
+    uint64_t wait_ticks;      // bound of every wait, 100 MHz wall clock
+};
+// exchange words per layer of the fused decode
+inline size_t fused_words(int K, int I, int H) {
+    return 256 + (size_t)FUSED_COPIES * FUSED_REC + (size_t)(K + 1) * I + (size_t)(K + 1) * H;
+}
+
 constexpr int MAX_E = 256;   // experts per layer the kernels support
 
 // batched layer: pairs dispatched expert-major, experts from slots or a store
@@ -177,6 +207,10 @@ hipError_t launch_gateup_grouped(const GroupedArgs &a, hipStream_t st, hipEvent_
 hipError_t launch_down_grouped(const GroupedArgs &a, hipStream_t st, hipEvent_t e0, hipEvent_t e1);
 hipError_t launch_combine(const float *ypair, int n_tok, int K, int H, float *out, int accumulate, hipStream_t st);
 hipError_t launch_iota(int n, int32_t *offsets, int32_t *perm, float *ones, hipStream_t st);
+// the allocation-free grouped entry point's workspace: this device's address
+// of a static device array of STATIC_SCRATCH_BYTES
+constexpr size_t STATIC_SCRATCH_BYTES = 16ull << 20;
+hipError_t static_scratch(void **ptr);
 // h = silu(gate) * up from y2 and its Q8_K (h itself to h_out when not null)
 hipError_t launch_swiglu_quant(const float *y2, int P, int I, float *h_out, uint16_t *q16, float *dx, uint16_t *bs16,
                                hipStream_t st);
@@ -185,6 +219,8 @@ hipError_t launch_swiglu_quant(const float *y2, int P, int I, float *h_out, uint
 hipError_t launch_route(const RouteLaunch &l, hipStream_t st, hipEvent_t *ev = nullptr);
 hipError_t launch_experts(const ExpertArgs &a, hipStream_t st);
 hipError_t launch_join(const JoinArgs &a, hipStream_t st);
+// the fused layer (see FusedArgs); its down rows are of down_type
+hipError_t launch_fused(const FusedArgs &a, hipStream_t st, hipEvent_t e0, hipEvent_t e1);
 // src: 0 every routed expert, 1 only those resident in HBM slots, 2 only
 // those read from the pinned host store.  A src = 2 down launch accumulates
 // into out when the caller sets accumulate.

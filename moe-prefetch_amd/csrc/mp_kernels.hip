@@ -107,56 +107,64 @@ struct RouteArgs {
     uint32_t *fresh;       // table words may flip during the token (see STREAM_BIT)
 };
 
-// One wavefront per expert row: logit[e] = <W[e], x> in the canonical order
-// (lane j accumulates W[256 i + 4 j + c] * x[...] with fmaf, i then c, then a
-// butterfly over the 64 lanes), plus the steering bias when given.  The first
-// H/256 workgroups also write the Q8_K blocks of x.  With router lookahead
-// (batch 1) E more single-wave workgroups per target layer T score T's router on the
-// products x[i] * r_T[i] (rounded to f32) in the same order.
-constexpr int RL_WAVES = 1;                      // router GEMV: rows (waves) per workgroup
-__global__ __launch_bounds__(64 * RL_WAVES) void route_logits_kernel(RouteArgs a) {
-    const int tok = blockIdx.y;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int per = (a.E + RL_WAVES - 1) / RL_WAVES;
-    const int t = (int)blockIdx.x / per;             // 0: this layer, 1..an: lookahead target t - 1
-    const int e = ((int)blockIdx.x - t * per) * RL_WAVES + wave;
-    const float *x = a.x + (size_t)tok * a.H;
-    if (e >= a.E) return;
-    if (t > 0) {
-        const float *w = a.aW[t - 1] + (size_t)e * a.H;
-        const float *r = a.ar[t - 1];
-        float acc = 0.0f;
-        for (int i = 0; i < a.H / 256; ++i) {
-            const float4 wv = *(const float4 *)(w + 256 * i + 4 * lane);
-            const float4 xv = *(const float4 *)(x + 256 * i + 4 * lane);
-            const float4 rv = *(const float4 *)(r + 256 * i + 4 * lane);
-            acc = fmaf(wv.x, xv.x * rv.x, acc);
-            acc = fmaf(wv.y, xv.y * rv.y, acc);
-            acc = fmaf(wv.z, xv.z * rv.z, acc);
-            acc = fmaf(wv.w, xv.w * rv.w, acc);
-        }
-        acc = bfly_add(acc);
-        if (lane == 0) a.alog[(size_t)(t - 1) * a.E + e] = acc;
-        return;
-    }
-    const float *w = a.W + (size_t)e * a.H;
+constexpr int RL_WAVES = 4;                      // router GEMV: waves (row quarters) per workgroup
+
+// One quarter of a router row's dot product in the canonical order: wave q
+// of the row's workgroup, lane j accumulates with fmaf (from 0) the products
+// W[Q q + 256 i + 4 j + c] * x[...] over i, then c, and the 64 lanes are
+// summed by a butterfly.  With r, the product x * r (rounded to f32) takes
+// x's place (router lookahead).
+__device__ inline float router_quarter(const float *w, const float *x, const float *r, int H, int q, int lane) {
+    const int Q = H / RL_WAVES;
     float acc = 0.0f;
-    for (int i = 0; i < a.H / 256; ++i) {
-        const float4 wv = *(const float4 *)(w + 256 * i + 4 * lane);
-        const float4 xv = *(const float4 *)(x + 256 * i + 4 * lane);
+    for (int i = 0; i < Q / 256; ++i) {
+        const int o = Q * q + 256 * i + 4 * lane;
+        const float4 wv = *(const float4 *)(w + o);
+        float4 xv = *(const float4 *)(x + o);
+        if (r) {
+            const float4 rv = *(const float4 *)(r + o);
+            xv.x = xv.x * rv.x; xv.y = xv.y * rv.y; xv.z = xv.z * rv.z; xv.w = xv.w * rv.w;
+        }
         acc = fmaf(wv.x, xv.x, acc);
         acc = fmaf(wv.y, xv.y, acc);
         acc = fmaf(wv.z, xv.z, acc);
         acc = fmaf(wv.w, xv.w, acc);
     }
-    acc = bfly_add(acc);
-    if (a.bias) acc = acc + a.bias[(size_t)tok * a.E + e];
-    if (lane == 0) a.logits[(size_t)tok * a.E + e] = acc;
+    return bfly_add(acc);
+}
+
+// One workgroup of RL_WAVES waves per router row: wave q sums quarter q, and
+// the four quarter sums are added in order (s0 + s1) + s2 + s3, plus the
+// steering bias when given.  The first H/256 workgroups also write the Q8_K
+// blocks of x.  With router lookahead (batch 1) E more workgroups per target
+// layer T score T's router on the products x[i] * r_T[i] in the same order.
+__global__ __launch_bounds__(64 * RL_WAVES) void route_logits_kernel(RouteArgs a) {
+    const int tok = blockIdx.y;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int t = (int)blockIdx.x / a.E;             // 0: this layer, 1..an: lookahead target t - 1
+    const int e = (int)blockIdx.x - t * a.E;
+    const float *x = a.x + (size_t)tok * a.H;
+    __shared__ float s_q[RL_WAVES];
+    const float *w = t > 0 ? a.aW[t - 1] + (size_t)e * a.H : a.W + (size_t)e * a.H;
+    const float part = router_quarter(w, x, t > 0 ? a.ar[t - 1] : nullptr, a.H, wave, lane);
+    if (lane == 0) s_q[wave] = part;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        float acc = s_q[0];
+#pragma unroll
+        for (int q = 1; q < RL_WAVES; ++q) acc = acc + s_q[q];
+        if (t > 0) {
+            a.alog[(size_t)(t - 1) * a.E + e] = acc;
+        } else {
+            if (a.bias) acc = acc + a.bias[(size_t)tok * a.E + e];
+            a.logits[(size_t)tok * a.E + e] = acc;
+        }
+    }
     // Q8_K of x: workgroup b (one of the first H/256) quantizes block b; with
     // CPU-assisted serving (batch 1) also into the host's post, written
     // through before this kernel ends, so that the select kernel's post only
     // adds the ids
-    if (a.q8x && wave == 0 && (int)blockIdx.x < a.H / QK) {
+    if (t == 0 && a.q8x && wave == 0 && (int)blockIdx.x < a.H / QK) {
         const float4 v = *(const float4 *)(x + QK * blockIdx.x + 4 * lane);
         const float xv[4] = {v.x, v.y, v.z, v.w};
         int q[4];
@@ -237,7 +245,7 @@ __global__ __launch_bounds__(256) void route_select_kernel(RouteArgs a) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int nc = a.E / 64;
     __shared__ float s_p[256];
-    __shared__ __attribute__((aligned(16))) float s_sel[256];
+    __shared__ __attribute__((aligned(16))) uint64_t s_key[256];
     __shared__ float s_m[4], s_cs[4];
     __shared__ int s_ids[16];
     __shared__ __attribute__((aligned(16))) float s_asel[2][256];   // lookahead scores
@@ -301,19 +309,11 @@ __global__ __launch_bounds__(256) void route_select_kernel(RouteArgs a) {
         s_p[ee] = p;
         if (a.probs) a.probs[(size_t)tok * a.E + ee] = p;
         float sel = !a.prior ? p : (a.prior_on_logits ? l + pr : p + pr);
-        s_sel[ee] = sel != sel ? -INFINITY : sel;     // a NaN sorts last
+        s_key[ee] = sel_key(sel, ee);                 // a NaN sorts last
     }
     __syncthreads();
     if (tid < a.E) {
-        const float v = s_sel[tid];
-        int rank = 0;
-        for (int j = 0; j < a.E; j += 4) {
-            const float4 u = *(const float4 *)&s_sel[j];
-            rank += (u.x > v) | ((u.x == v) & (j < tid));
-            rank += (u.y > v) | ((u.y == v) & (j + 1 < tid));
-            rank += (u.z > v) | ((u.z == v) & (j + 2 < tid));
-            rank += (u.w > v) | ((u.w == v) & (j + 3 < tid));
-        }
+        const int rank = key_rank(s_key, a.E, s_key[tid]);
         if (rank < a.K) s_ids[rank] = tid;
     } else if (look) {
         for (int i = tid - a.E; i < a.an * a.E; i += 256 - a.E) ahead_rank(a, s_asel, s_top, i);
@@ -545,6 +545,75 @@ constexpr int DN_ROWS = 8;
 constexpr int DN_LDS_ROWS = 5040;           // 8 Q6_K rows at I = 768
 constexpr int DN_LDS_Q8 = 3 * Q8K_BYTES;    // I <= 768
 
+// One wave's 8 down rows (LDS, lane-contiguous as loaded: row g of the tile
+// at g * rowb) against the Q8_K blocks of h (LDS): lane (g, u) works on row g,
+// part u of each super-block; the row's value is complete on lanes with
+// u == 0.  Super-blocks in order, scale term then min term (the CPU vec_dot
+// order).
+template <int DT>
+__device__ inline float down_rows_dot(const uint8_t *s_wt, const uint8_t *s_q8h, int nb, int rowb, int lane) {
+    const int g = lane >> 3, u = lane & 7;
+    float y = 0.0f;
+    for (int b = 0; b < nb; ++b) {
+        const uint8_t *xq = s_q8h + b * Q8K_BYTES;
+        const float dx = *(const float *)xq;
+        int32_t si = 0, mi = 0;
+        float d, dm = 0.0f;
+        if (DT == TYPE_Q4K) {
+            const uint8_t *blk = s_wt + g * rowb + b * Q4K_BYTES;
+            const uint4 hdr = *(const uint4 *)blk;
+            const uint4 qs = *(const uint4 *)(blk + 16 + 16 * u);
+            const int j = u >> 1;
+            const uint32_t *plo = (const uint32_t *)(xq + 4 + 64 * j + 16 * (u & 1));
+            const uint32_t *phi = (const uint32_t *)(xq + 4 + 64 * j + 32 + 16 * (u & 1));
+            uint32_t xlo[4], xhi[4];
+            for (int i = 0; i < 4; ++i) { xlo[i] = plo[i]; xhi[i] = phi[i]; }
+            const int16_t *bs = (const int16_t *)(xq + 4 + QK);
+            q4k_lane(hdr, qs, u, xlo, xhi, bs[4 * j + (u & 1)], bs[4 * j + 2 + (u & 1)], si, mi);
+            d = h2f_dev((uint16_t)(hdr.x & 0xffff)) * dx;
+            dm = h2f_dev((uint16_t)(hdr.x >> 16)) * dx;
+        } else {
+            const uint8_t *blk = s_wt + g * rowb + b * Q6K_BYTES;
+            const int hh = u >> 2, up4 = u & 3;
+            const uint8_t *pa = blk + 64 * hh + 8 * up4;
+            const uint8_t *pb = pa + 32;
+            const uint8_t *ph = blk + 128 + 32 * hh + 8 * up4;
+            const uint32_t a0 = lds_u32_at2(pa), a1 = lds_u32_at2(pa + 4);
+            const uint32_t b0 = lds_u32_at2(pb), b1 = lds_u32_at2(pb + 4);
+            const uint32_t h0 = lds_u32_at2(ph), h1 = lds_u32_at2(ph + 4);
+            const int8_t *sc = (const int8_t *)(blk + 192 + 8 * hh + (up4 >> 1));
+            const uint32_t L = 0x0F0F0F0Fu, Hm = 0x30303030u;
+            const uint32_t qv[4][2] = {
+                {(a0 & L) | ((h0 << 4) & Hm), (a1 & L) | ((h1 << 4) & Hm)},
+                {(b0 & L) | ((h0 << 2) & Hm), (b1 & L) | ((h1 << 2) & Hm)},
+                {((a0 >> 4) & L) | (h0 & Hm), ((a1 >> 4) & L) | (h1 & Hm)},
+                {((b0 >> 4) & L) | ((h0 >> 2) & Hm), ((b1 >> 4) & L) | ((h1 >> 2) & Hm)}};
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const uint32_t *px = (const uint32_t *)(xq + 4 + 128 * hh + 32 * q + 8 * up4);
+                const uint32_t x0 = px[0], x1 = px[1];
+                int32_t dq = sdot4(qv[q][0], x0, sdot4(qv[q][1], x1, 0));
+                const int32_t sx = sdot4(0x01010101u, x0, sdot4(0x01010101u, x1, 0));
+                dq -= 32 * sx;
+                si += (int32_t)sc[2 * q] * dq;
+            }
+            d = h2f_dev(*(const uint16_t *)(blk + 208)) * dx;
+        }
+        si += __shfl_xor(si, 1, 64);
+        si += __shfl_xor(si, 2, 64);
+        si += __shfl_xor(si, 4, 64);
+        // super-block order, scale term then min term (CPU vec_dot order)
+        y = y + d * (float)si;
+        if (DT == TYPE_Q4K) {
+            mi += __shfl_xor(mi, 1, 64);
+            mi += __shfl_xor(mi, 2, 64);
+            mi += __shfl_xor(mi, 4, 64);
+            y = y - dm * (float)mi;
+        }
+    }
+    return y;
+}
+
 template <int DT, int SRC>
 __global__ __launch_bounds__(512) void down_kernel(ExpertArgs a) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -649,64 +718,7 @@ __global__ __launch_bounds__(512) void down_kernel(ExpertArgs a) {
         if (direct) __builtin_amdgcn_s_waitcnt(0x0f70);       // vmcnt(0)
         wave_lds_sync();
         if (mine) {
-            float y = 0.0f;
-            for (int b = 0; b < nb; ++b) {
-                const uint8_t *xq = s_q8[wave] + b * Q8K_BYTES;
-                const float dx = *(const float *)xq;
-                int32_t si = 0, mi = 0;
-                float d, dm = 0.0f;
-                if (DT == TYPE_Q4K) {
-                    const uint8_t *blk = s_w[wave] + g * rowb + b * Q4K_BYTES;
-                    const uint4 hdr = *(const uint4 *)blk;
-                    const uint4 qs = *(const uint4 *)(blk + 16 + 16 * u);
-                    const int j = u >> 1;
-                    const uint32_t *plo = (const uint32_t *)(xq + 4 + 64 * j + 16 * (u & 1));
-                    const uint32_t *phi = (const uint32_t *)(xq + 4 + 64 * j + 32 + 16 * (u & 1));
-                    uint32_t xlo[4], xhi[4];
-                    for (int i = 0; i < 4; ++i) { xlo[i] = plo[i]; xhi[i] = phi[i]; }
-                    const int16_t *bs = (const int16_t *)(xq + 4 + QK);
-                    q4k_lane(hdr, qs, u, xlo, xhi, bs[4 * j + (u & 1)], bs[4 * j + 2 + (u & 1)], si, mi);
-                    d = h2f_dev((uint16_t)(hdr.x & 0xffff)) * dx;
-                    dm = h2f_dev((uint16_t)(hdr.x >> 16)) * dx;
-                } else {
-                    const uint8_t *blk = s_w[wave] + g * rowb + b * Q6K_BYTES;
-                    const int hh = u >> 2, up4 = u & 3;
-                    const uint8_t *pa = blk + 64 * hh + 8 * up4;
-                    const uint8_t *pb = pa + 32;
-                    const uint8_t *ph = blk + 128 + 32 * hh + 8 * up4;
-                    const uint32_t a0 = lds_u32_at2(pa), a1 = lds_u32_at2(pa + 4);
-                    const uint32_t b0 = lds_u32_at2(pb), b1 = lds_u32_at2(pb + 4);
-                    const uint32_t h0 = lds_u32_at2(ph), h1 = lds_u32_at2(ph + 4);
-                    const int8_t *sc = (const int8_t *)(blk + 192 + 8 * hh + (up4 >> 1));
-                    const uint32_t L = 0x0F0F0F0Fu, Hm = 0x30303030u;
-                    const uint32_t qv[4][2] = {
-                        {(a0 & L) | ((h0 << 4) & Hm), (a1 & L) | ((h1 << 4) & Hm)},
-                        {(b0 & L) | ((h0 << 2) & Hm), (b1 & L) | ((h1 << 2) & Hm)},
-                        {((a0 >> 4) & L) | (h0 & Hm), ((a1 >> 4) & L) | (h1 & Hm)},
-                        {((b0 >> 4) & L) | ((h0 >> 2) & Hm), ((b1 >> 4) & L) | ((h1 >> 2) & Hm)}};
-#pragma unroll
-                    for (int q = 0; q < 4; ++q) {
-                        const uint32_t *px = (const uint32_t *)(xq + 4 + 128 * hh + 32 * q + 8 * up4);
-                        const uint32_t x0 = px[0], x1 = px[1];
-                        int32_t dq = sdot4(qv[q][0], x0, sdot4(qv[q][1], x1, 0));
-                        const int32_t sx = sdot4(0x01010101u, x0, sdot4(0x01010101u, x1, 0));
-                        dq -= 32 * sx;
-                        si += (int32_t)sc[2 * q] * dq;
-                    }
-                    d = h2f_dev(*(const uint16_t *)(blk + 208)) * dx;
-                }
-                si += __shfl_xor(si, 1, 64);
-                si += __shfl_xor(si, 2, 64);
-                si += __shfl_xor(si, 4, 64);
-                // super-block order, scale term then min term (CPU vec_dot order)
-                y = y + d * (float)si;
-                if (DT == TYPE_Q4K) {
-                    mi += __shfl_xor(mi, 1, 64);
-                    mi += __shfl_xor(mi, 2, 64);
-                    mi += __shfl_xor(mi, 4, 64);
-                    y = y - dm * (float)mi;
-                }
-            }
+            const float y = down_rows_dot<DT>(s_w[wave], s_q8[wave], nb, rowb, lane);
             if (u == 0) {
                 s_y[k][g] = y;
                 if (a.ypart && !a.join) a.ypart[(size_t)k * a.H + r0 + g] = y;
@@ -723,6 +735,508 @@ __global__ __launch_bounds__(512) void down_kernel(ExpertArgs a) {
             if (k < a.K) acc = acc + wk[k] * s_y[k][t];
         if (a.n_shared) acc = acc + s_y[a.K][t];        // weight 1, after the routed experts
         a.out[r0 + t] = a.accumulate ? prev + acc : acc;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// A batch-1 decode layer in one launch (see FusedArgs).  The phases hand over
+// tagged words written and read at agent scope (coherent across the XCDs'
+// L2s without a cache write-back or invalidation); every wait is for
+// workgroups of a lower index, which the dispatcher starts first, and is
+// bounded by the wall clock.  The down rows' weights are requested as soon as
+// the routing is known, while the gate/up rows are still being read.
+
+__device__ inline void store_tagged(uint64_t *p, uint64_t v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ inline uint64_t load_tagged(const uint64_t *p) {
+    return __hip_atomic_load((uint64_t *)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ inline uint64_t tagged(uint32_t seq, float v) { return ((uint64_t)seq << 32) | __float_as_uint(v); }
+__device__ inline void fused_late(const FusedArgs &a, uint32_t seq) {
+    __hip_atomic_store(a.err, seq, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// One lane's share of the Q8_K of a 256-value block xb, as the gate/up dots
+// of lane (b, u) read it: the 16-value pieces at o0 = 64 (u >> 1) + 16 (u & 1)
+// and o0 + 32, packed four codes a word, their group sums and the block's
+// scale.  The block's largest magnitude (first index on a tie) is found over
+// the block's 8 lanes (xor 1, 2, 4), so every value equals the whole block's
+// quantization (q8k_wave_vals) bit for bit.
+__device__ inline void q8k_lane_part(const float *xb, int u, uint32_t xlo[4], uint32_t xhi[4], int &bslo, int &bshi,
+                                     float &d) {
+    const int o0 = 64 * (u >> 1) + 16 * (u & 1);
+    float v[32];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const float4 a = *(const float4 *)(xb + o0 + 4 * i);
+        const float4 b = *(const float4 *)(xb + o0 + 32 + 4 * i);
+        v[4 * i] = a.x; v[4 * i + 1] = a.y; v[4 * i + 2] = a.z; v[4 * i + 3] = a.w;
+        v[16 + 4 * i] = b.x; v[16 + 4 * i + 1] = b.y; v[16 + 4 * i + 2] = b.z; v[16 + 4 * i + 3] = b.w;
+    }
+    float amax = 0.0f, mx = 0.0f;
+    int idx = 1 << 30;
+#pragma unroll
+    for (int i = 0; i < 32; ++i) {             // positions in increasing order
+        const float ax = fabsf(v[i]);
+        if (ax > amax) { amax = ax; mx = v[i]; idx = i < 16 ? o0 + i : o0 + 16 + i; }
+    }
+#pragma unroll
+    for (int o = 1; o <= 4; o <<= 1) {
+        const float oa = __shfl_xor(amax, o, 64);
+        const float om = __shfl_xor(mx, o, 64);
+        const int oi = __shfl_xor(idx, o, 64);
+        if (oa > amax || (oa == amax && oi < idx)) { amax = oa; mx = om; idx = oi; }
+    }
+    d = 0.0f;
+    float iscale = 0.0f;
+    if (amax != 0.0f) {
+        iscale = -127.0f / mx;
+        d = 1.0f / iscale;
+    }
+    bslo = bshi = 0;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        uint32_t w = 0;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            int q = 0;
+            if (amax != 0.0f) {
+                const int t = (int)rintf(iscale * v[4 * i + c]);
+                q = t < 127 ? t : 127;
+            }
+            w |= (uint32_t)(q & 0xff) << (8 * c);
+            if (i < 4) bslo += q; else bshi += q;
+        }
+        if (i < 4) xlo[i] = w; else xhi[i - 4] = w;
+    }
+}
+
+// LDS of one fused workgroup, shared by the roles (each uses its own part)
+constexpr int FUSED_LDS_W = 4 * DN_LDS_ROWS;                  // down: each wave's 8 weight rows
+constexpr int FUSED_LDS_Q8 = 3 * Q8K_BYTES + 4;               // down: the Q8_K of h (I <= 768)
+constexpr int FUSED_LDS = FUSED_LDS_W + FUSED_LDS_Q8 + 8 * FUSED_REC + 16;
+
+// The routing record (copy `copy`): wave 0 polls until the words the
+// workgroup needs carry seq -- the K routing words, and with need_w the K gate
+// weights too -- and leaves them in s_rec for the workgroup.  false: the wait
+// ran out (reported through a.err).
+__device__ bool fused_record(const FusedArgs &a, int copy, uint32_t seq, bool need_w, uint64_t *s_rec, int *s_flag) {
+    const int K = a.x.K;
+    if (threadIdx.x < 64) {
+        const int lane = threadIdx.x;
+        const uint64_t *src = a.rec + (size_t)copy * FUSED_REC;
+        const bool want = lane < K || (need_w && lane >= 16 && lane < 16 + K);
+        bool ok = !want;
+        uint64_t v = 0;
+        int late = 0;
+        const uint64_t t0 = wall_clock64();
+        for (;;) {
+            if (!ok) {
+                v = load_tagged(src + lane);
+                ok = (uint32_t)(v >> 32) == seq;
+            }
+            if (__all(ok)) break;
+            if (wall_clock64() - t0 > a.wait_ticks) {
+                late = 1;
+                break;
+            }
+            __builtin_amdgcn_s_sleep(2);
+        }
+        if (lane < FUSED_REC) s_rec[lane] = v;
+        if (lane == 0) *s_flag = late;
+    }
+    __syncthreads();
+    const bool late = *s_flag != 0;
+    if (late && threadIdx.x == 0) fused_late(a, seq);
+    return !late;
+}
+
+// where routed expert k's bytes are, from the record: an HBM slot, the pinned
+// store (absent), or nothing (an id outside the store contributes zero); cpu:
+// the host computes it (absent, rank r among the absent experts in k order
+// with r % den < num)
+struct ExpertSrc {
+    const uint8_t *base;
+    bool absent, cpu;
+};
+__device__ inline ExpertSrc fused_src(const ExpertArgs &x, const uint64_t *s_rec, int k) {
+    if (k >= x.K) return {x.shared, false, false};
+    int rank = 0;
+    ExpertSrc r{nullptr, false, false};
+    for (int kk = 0; kk <= k; ++kk) {
+        const uint64_t w = s_rec[kk];
+        const int id = (int)(w & 0xffffu), slot = (int)((w >> 16) & 0xffffu);
+        const bool res = x.slot_pool && slot < x.n_slots;
+        const bool absent = !res && x.host_store && id < x.n_experts;
+        if (kk < k) {
+            rank += absent;
+        } else {
+            r.absent = absent;
+            r.cpu = x.cpu_den > 0 && absent && rank % x.cpu_den < x.cpu_num;
+            if (res) r.base = x.slot_pool + (size_t)slot * x.slot_bytes;
+            else if (absent) r.base = x.host_store + (size_t)id * x.expert_bytes;
+        }
+    }
+    return r;
+}
+
+// router row e: the canonical four-quarter dot, + the steering bias, posted
+// as a tagged word
+__device__ void fused_router(const FusedArgs &a, int e, uint32_t seq, uint8_t *smem) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    float *s_q = (float *)smem;
+    const float part = router_quarter(a.r.W + (size_t)e * a.r.H, a.r.x, nullptr, a.r.H, wave, lane);
+    if (lane == 0) s_q[wave] = part;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        float acc = s_q[0];
+#pragma unroll
+        for (int q = 1; q < RL_WAVES; ++q) acc = acc + s_q[q];
+        if (a.r.bias) acc = acc + a.r.bias[e];
+        store_tagged(a.xlog + e, tagged(seq, acc));
+    }
+}
+
+// the selection: softmax, prior, top-k and gate weights as route_select_kernel
+// computes them (the same order, so the same bits), from the posted logits;
+// then the outputs, the host's post and the routing record
+__device__ void fused_select(const FusedArgs &a, uint32_t seq, uint8_t *smem) {
+    const RouteLaunch &r = a.r;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int nc = r.E / 64;
+    uint64_t *s_key = (uint64_t *)smem;             // 16-byte aligned: read two keys at a time
+    float *s_p = (float *)(s_key + 256);
+    int32_t *s_tbl = (int32_t *)(s_p + 256);
+    float *s_m = (float *)(s_tbl + 256);
+    float *s_cs = s_m + 4;
+    int *s_ids = (int *)(s_cs + 4);
+    int *s_slot = s_ids + 16;
+    float *s_w = (float *)(s_slot + 16);
+    int *s_late = (int *)(s_w + 16);
+    if (tid == 0) *s_late = 0;
+    const int32_t tword = tid < r.E ? r.table[tid] : 0;
+    const float pr = (r.prior && tid < r.E) ? r.prior[tid] : 0.0f;
+    // Q8_K of x for the host's share of absent experts, written through to
+    // host memory (each wave waits for its stores) before the post's words
+    if (r.post)
+        for (int b = wave; b < r.H / QK; b += 4) {
+            const float4 v = *(const float4 *)(r.x + QK * b + 4 * lane);
+            const float xv[4] = {v.x, v.y, v.z, v.w};
+            int q[4];
+            float d;
+            q8k_wave_vals(xv, lane, q, d);
+            q8k_store_sys(q, d, (uint32_t *)(r.post->q8x + (size_t)b * Q8K_BYTES), lane);
+        }
+    __syncthreads();                            // *s_late cleared before any lane may raise it
+    float l = 0.0f;
+    if (tid < r.E) {
+        const uint64_t t0 = wall_clock64();
+        uint64_t v = 0;
+        for (;;) {
+            v = load_tagged(a.xlog + tid);
+            if ((uint32_t)(v >> 32) == seq) break;
+            if (wall_clock64() - t0 > a.wait_ticks) {
+                *s_late = 1;
+                break;
+            }
+            __builtin_amdgcn_s_sleep(1);
+        }
+        l = __uint_as_float((uint32_t)v);
+        s_tbl[tid] = tword;
+    }
+    if (wave < nc) {
+        float m = l;
+#pragma unroll
+        for (int o = 32; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+        if (lane == 0) s_m[wave] = m;
+    }
+    __syncthreads();
+    float ex = 0.0f;
+    if (wave < nc) {
+        float m = s_m[0];
+        for (int c = 1; c < nc; ++c) m = fmaxf(m, s_m[c]);
+        ex = canon_expf(l - m);
+        const float cs = bfly_add(ex);
+        if (lane == 0) s_cs[wave] = cs;
+    }
+    __syncthreads();
+    if (wave < nc) {
+        float sum = s_cs[0];
+        for (int c = 1; c < nc; ++c) sum = sum + s_cs[c];
+        const float p = ex / sum;
+        s_p[tid] = p;
+        const float sel = !r.prior ? p : (r.prior_on_logits ? l + pr : p + pr);
+        s_key[tid] = sel_key(sel, tid);                 // a NaN sorts last
+    }
+    __syncthreads();
+    if (tid < r.E) {       // rank of expert tid: experts ahead of it (larger, or equal with a lower id)
+        const int rank = key_rank(s_key, r.E, s_key[tid]);
+        if (rank < r.K) s_ids[rank] = tid;
+    }
+    __syncthreads();
+    if (wave == 0) {
+        float ws = 0.0f;
+        for (int k = 0; k < r.K; ++k) ws = ws + s_p[s_ids[k]];
+        if (lane < r.K) {
+            const int id = s_ids[lane];
+            const int slot = s_tbl[id];
+            const float w = s_p[id] / ws;
+            r.ids[lane] = id;
+            r.w[lane] = w;
+            r.slots[lane] = slot;
+            s_slot[lane] = slot;
+            s_w[lane] = w;
+            if (r.post)
+                __hip_atomic_store(&r.post->tag[lane], sc_tag(seq, slot, id), __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_SYSTEM);
+        }
+    }
+    __syncthreads();
+    for (int i = tid; i < FUSED_COPIES * FUSED_REC; i += 256) {
+        const int k = i % FUSED_REC;
+        if (k < r.K) store_tagged(a.rec + i, sc_tag(seq, s_slot[k], s_ids[k]));
+        else if (k >= 16 && k - 16 < r.K) store_tagged(a.rec + i, tagged(seq, s_w[k - 16]));
+    }
+    if (tid == 0 && *s_late) fused_late(a, seq);
+}
+
+// FUSED_GU_ROWS gate/up rows per wave of routed expert k (or of the shared
+// expert, which needs no routing): the Q8_K of x first, then the routing
+// record, then the rows exactly as gateup_kernel computes them; h posted as
+// tagged words
+__device__ void fused_gateup(const FusedArgs &a, int g, uint32_t seq, uint8_t *smem) {
+    constexpr int R = FUSED_GU_ROWS;
+    const ExpertArgs &x = a.x;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int per = x.I / (4 * R);
+    const int k = g / per, tile = g - k * per;
+    const int b = lane >> 3, u = lane & 7;
+    uint32_t xlo[4], xhi[4];
+    int bslo, bshi;
+    float dx;
+    q8k_lane_part(a.r.x + QK * b, u, xlo, xhi, bslo, bshi, dx);
+    uint64_t *s_rec = (uint64_t *)(smem + FUSED_LDS_W + FUSED_LDS_Q8);
+    int *s_flag = (int *)(s_rec + FUSED_REC);
+    ExpertSrc src{x.shared, false, false};
+    if (k < x.K) {
+        if (!fused_record(a, g % FUSED_COPIES, seq, false, s_rec, s_flag)) return;
+        src = fused_src(x, s_rec, k);
+        if (src.cpu) return;
+    }
+    uint8_t *sb = src.absent && x.stage ? x.stage + (size_t)k * x.stage_stride : nullptr;
+    const size_t rb = (size_t)(x.H / QK) * Q4K_BYTES;
+    const uint8_t *up = src.base, *gate = src.base + (size_t)x.I * rb;
+    const bool valid = src.base != nullptr;
+    const int row0 = (tile * 4 + wave) * R;
+    uint4 hg[R], qg[R], hu[R], qu[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        const size_t off = (size_t)(row0 + r) * rb + (size_t)b * Q4K_BYTES;
+        const uint4 z = make_uint4(0, 0, 0, 0);
+        hg[r] = valid ? *(const uint4 *)(gate + off) : z;
+        qg[r] = valid ? *(const uint4 *)(gate + off + 16 + 16 * u) : z;
+        hu[r] = valid ? *(const uint4 *)(up + off) : z;
+        qu[r] = valid ? *(const uint4 *)(up + off + 16 + 16 * u) : z;
+    }
+    if (sb) {          // the same bytes, same offsets, into the staging area
+        uint8_t *su = sb, *sg = sb + (size_t)x.I * rb;
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const size_t off = (size_t)(row0 + r) * rb + (size_t)b * Q4K_BYTES;
+            if (u == 0) {
+                *(uint4 *)(sg + off) = hg[r];
+                *(uint4 *)(su + off) = hu[r];
+            }
+            *(uint4 *)(sg + off + 16 + 16 * u) = qg[r];
+            *(uint4 *)(su + off + 16 + 16 * u) = qu[r];
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        float res[2];
+#pragma unroll
+        for (int m = 0; m < 2; ++m) {
+            const uint4 hdr = m == 0 ? hg[r] : hu[r];
+            const uint4 qs = m == 0 ? qg[r] : qu[r];
+            int32_t si, mi;
+            q4k_lane(hdr, qs, u, xlo, xhi, bslo, bshi, si, mi);
+            si += __shfl_xor(si, 1, 64);
+            mi += __shfl_xor(mi, 1, 64);
+            si += __shfl_xor(si, 2, 64);
+            mi += __shfl_xor(mi, 2, 64);
+            si += __shfl_xor(si, 4, 64);
+            mi += __shfl_xor(mi, 4, 64);
+            const float d = h2f_dev((uint16_t)(hdr.x & 0xffff)) * dx;
+            const float dm = h2f_dev((uint16_t)(hdr.x >> 16)) * dx;
+            const int ps = __builtin_bit_cast(int, d * (float)si), pm = __builtin_bit_cast(int, dm * (float)mi);
+            float v = 0.0f;
+#pragma unroll
+            for (int bb = 0; bb < 8; ++bb) {
+                v = v + __builtin_bit_cast(float, __builtin_amdgcn_readlane(ps, 8 * bb));
+                v = v - __builtin_bit_cast(float, __builtin_amdgcn_readlane(pm, 8 * bb));
+            }
+            res[m] = v;
+        }
+        if (lane == 0) {
+            const float gv = res[0], uv = res[1];
+            store_tagged(a.hx + (size_t)k * x.I + row0 + r, tagged(seq, gv / (1.0f + canon_expf(-gv)) * uv));
+        }
+    }
+}
+
+// FUSED_DN_TILE down rows of expert k, 8 per wave: the weights into LDS as
+// soon as the routing is known; then h (posted by the gate/up workgroups) in
+// Q8_K, the dots as down_kernel computes them, and the rows posted as tagged
+// words (or, for the join kernel, stored to x.ypart)
+template <int DT>
+__device__ void fused_down(const FusedArgs &a, int g, uint32_t seq, uint8_t *smem) {
+    const ExpertArgs &x = a.x;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int per = x.H / FUSED_DN_TILE;
+    const int k = g / per, tile = g - k * per;
+    uint8_t *s_wt = smem + wave * DN_LDS_ROWS;
+    uint8_t *s_q8h = smem + FUSED_LDS_W;
+    uint64_t *s_rec = (uint64_t *)(smem + FUSED_LDS_W + FUSED_LDS_Q8);
+    int *s_flag = (int *)(s_rec + FUSED_REC);
+    ExpertSrc src{x.shared, false, false};
+    if (k < x.K) {
+        if (!fused_record(a, g % FUSED_COPIES, seq, false, s_rec, s_flag)) return;
+        src = fused_src(x, s_rec, k);
+        if (src.cpu) return;
+    }
+    const int nb = x.I / QK;
+    const int rowb = nb * (DT == TYPE_Q6K ? Q6K_BYTES : Q4K_BYTES);
+    const int r0 = tile * FUSED_DN_TILE + wave * 8;
+    const int nvec = 8 * rowb / 16;                 // <= 315
+    const size_t dn_off = 2ull * x.I * (x.H / QK) * Q4K_BYTES + (size_t)r0 * rowb;
+    const uint4 *wsrc = src.base ? (const uint4 *)(src.base + dn_off) : nullptr;
+    uint8_t *sb = src.absent && x.stage ? x.stage + (size_t)k * x.stage_stride + dn_off : nullptr;
+    // the weights first: straight into LDS (16 bytes a lane, lane-contiguous),
+    // or through registers when they are also staged
+    uint4 buf[5];
+    if (wsrc && !sb) {
+#pragma unroll
+        for (int j = 0; j < 5; ++j) {
+            const int i = lane + 64 * j;
+            if (i < nvec)
+                __builtin_amdgcn_global_load_lds((const void *)(wsrc + i),
+                                                 (__attribute__((address_space(3))) void *)(s_wt + 1024 * j), 16, 0,
+                                                 0);
+        }
+    } else if (wsrc) {
+#pragma unroll
+        for (int j = 0; j < 5; ++j) {
+            const int i = lane + 64 * j;
+            buf[j] = i < nvec ? wsrc[i] : make_uint4(0, 0, 0, 0);
+        }
+    }
+    // h of expert k, block `wave`, as the gate/up workgroups post it
+    if (wave < nb) {
+        const uint64_t *hp = a.hx + (size_t)k * x.I + QK * wave + 4 * lane;
+        uint64_t hv[4] = {0, 0, 0, 0};
+        bool ok[4] = {false, false, false, false};
+        int late = 0;
+        const uint64_t t0 = wall_clock64();
+        for (;;) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                if (!ok[i]) {
+                    hv[i] = load_tagged(hp + i);
+                    ok[i] = (uint32_t)(hv[i] >> 32) == seq;
+                }
+            if (__all(ok[0] && ok[1] && ok[2] && ok[3])) break;
+            if (wall_clock64() - t0 > a.wait_ticks) {
+                late = 1;
+                break;
+            }
+            __builtin_amdgcn_s_sleep(1);
+        }
+        if (late && lane == 0) fused_late(a, seq);
+        const float xv[4] = {__uint_as_float((uint32_t)hv[0]), __uint_as_float((uint32_t)hv[1]),
+                             __uint_as_float((uint32_t)hv[2]), __uint_as_float((uint32_t)hv[3])};
+        int q[4];
+        float d;
+        q8k_wave_vals(xv, lane, q, d);
+        q8k_store(q, d, s_q8h + wave * Q8K_BYTES, lane);
+    }
+    if (wsrc && !sb) {
+        __builtin_amdgcn_s_waitcnt(0x0f70);             // vmcnt(0): the direct-to-LDS weights have landed
+    } else if (wsrc) {
+        uint4 *dst = (uint4 *)s_wt;
+#pragma unroll
+        for (int j = 0; j < 5; ++j) {
+            const int i = lane + 64 * j;
+            if (i < nvec) dst[i] = buf[j];
+        }
+        uint4 *sd = (uint4 *)sb;
+#pragma unroll
+        for (int j = 0; j < 5; ++j) {
+            const int i = lane + 64 * j;
+            if (i < nvec) sd[i] = buf[j];
+        }
+    }
+    __syncthreads();                // the Q8_K blocks of h and every wave's weights
+    const float y = wsrc ? down_rows_dot<DT>(s_wt, s_q8h, nb, rowb, lane) : 0.0f;
+    if ((lane & 7) == 0) {
+        const int row = r0 + (lane >> 3);
+        if (x.ypart) x.ypart[(size_t)k * x.H + row] = y;
+        else store_tagged(a.yx + (size_t)k * x.H + row, tagged(seq, y));
+    }
+}
+
+// 256 output rows: out = sum_k w_k y_k in k order, then the shared expert
+// (weight 1), as down_kernel's combine adds them
+__device__ void fused_combine(const FusedArgs &a, int c, uint32_t seq, uint8_t *smem) {
+    const ExpertArgs &x = a.x;
+    uint64_t *s_rec = (uint64_t *)(smem + FUSED_LDS_W + FUSED_LDS_Q8);
+    int *s_flag = (int *)(s_rec + FUSED_REC);
+    if (!fused_record(a, c % FUSED_COPIES, seq, true, s_rec, s_flag)) return;
+    const int row = c * 256 + (int)threadIdx.x;
+    if (row >= x.H) return;
+    const int kt = x.K + x.n_shared;
+    float y[17];
+    int late = 0;
+    for (int k = 0; k < kt; ++k) {
+        const uint64_t *p = a.yx + (size_t)k * x.H + row;
+        const uint64_t t0 = wall_clock64();
+        uint64_t v;
+        for (;;) {
+            v = load_tagged(p);
+            if ((uint32_t)(v >> 32) == seq) break;
+            if (wall_clock64() - t0 > a.wait_ticks) {
+                late = 1;
+                break;
+            }
+            __builtin_amdgcn_s_sleep(1);
+        }
+        y[k] = __uint_as_float((uint32_t)v);
+    }
+    if (late) fused_late(a, seq);
+    float acc = __uint_as_float((uint32_t)s_rec[16]) * y[0];
+    for (int k = 1; k < x.K; ++k) acc = acc + __uint_as_float((uint32_t)s_rec[16 + k]) * y[k];
+    if (x.n_shared) acc = acc + y[x.K];
+    x.out[row] = acc;
+}
+
+template <int DT>
+__global__ __launch_bounds__(256) void fused_kernel(FusedArgs a) {
+    __shared__ __attribute__((aligned(16))) uint8_t smem[FUSED_LDS];
+    const uint32_t seq = *a.r.seq;
+    const int E = a.r.E;
+    const int kt = a.x.K + a.x.n_shared;
+    const int nG = kt * (a.x.I / (4 * FUSED_GU_ROWS)), nD = kt * (a.x.H / FUSED_DN_TILE);
+    int g = (int)blockIdx.x;
+    if (g < E) {
+        fused_router(a, g, seq, smem);
+    } else if (g == E) {
+        fused_select(a, seq, smem);
+    } else if ((g -= E + 1) < nG) {
+        fused_gateup(a, g, seq, smem);
+    } else if ((g -= nG) < nD) {
+        fused_down<DT>(a, g, seq, smem);
+    } else {
+        fused_combine(a, g - nD, seq, smem);
     }
 }
 
@@ -778,8 +1292,8 @@ hipError_t launch_route(const RouteLaunch &l, hipStream_t st, hipEvent_t *ev) {
     if (l.logits_in)
         return launch(route_select_kernel, dim3((unsigned)l.n_tok), dim3(256), st, ev ? ev[2] : nullptr,
                       ev ? ev[3] : nullptr, a);
-    const unsigned per = (unsigned)((l.E + RL_WAVES - 1) / RL_WAVES);
-    const hipError_t e = launch(route_logits_kernel, dim3(per * (unsigned)(1 + (l.apost ? l.an : 0)), (unsigned)l.n_tok),
+    const hipError_t e = launch(route_logits_kernel, dim3((unsigned)l.E * (unsigned)(1 + (l.apost ? l.an : 0)),
+                                                         (unsigned)l.n_tok),
                                 dim3(64 * RL_WAVES), st, ev ? ev[0] : nullptr, ev ? ev[1] : nullptr, a);
     if (e != hipSuccess) return e;
     return launch(route_select_kernel, dim3((unsigned)l.n_tok), dim3(256), st, ev ? ev[2] : nullptr,
@@ -877,6 +1391,14 @@ __global__ __launch_bounds__(256) void join_kernel(JoinArgs a) {
 hipError_t launch_join(const JoinArgs &a, hipStream_t st) {
     hipLaunchKernelGGL(join_kernel, dim3((unsigned)((a.H + 255) / 256)), dim3(256), 0, st, a);
     return hipGetLastError();
+}
+
+hipError_t launch_fused(const FusedArgs &a, hipStream_t st, hipEvent_t e0, hipEvent_t e1) {
+    const int kt = a.x.K + a.x.n_shared;
+    const unsigned n = (unsigned)(a.r.E + 1 + kt * (a.x.I / (4 * FUSED_GU_ROWS)) + kt * (a.x.H / FUSED_DN_TILE) +
+                                  (a.x.ypart ? 0 : a.x.H / 256));
+    if (a.x.down_type == TYPE_Q6K) return launch(fused_kernel<TYPE_Q6K>, dim3(n), dim3(256), st, e0, e1, a);
+    return launch(fused_kernel<TYPE_Q4K>, dim3(n), dim3(256), st, e0, e1, a);
 }
 
 hipError_t launch_experts(const ExpertArgs &a, hipStream_t st) {

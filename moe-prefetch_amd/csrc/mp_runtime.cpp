@@ -192,6 +192,13 @@ struct moe_cache {
     float *sc_rows = nullptr, *sc_rows_d = nullptr;               // [L][K][H]
     uint32_t *d_seq = nullptr, *h_seq = nullptr;
     uint32_t sc_seq = 0;
+    // fused layer launches (router, selection, gate/up, down and combine in
+    // one launch): tagged exchange words, fx_words per layer; a bounded wait
+    // that ran out writes the token's sequence number after the routed ids
+    // (d_ids[L * K])
+    uint64_t *fx = nullptr;
+    size_t fx_words = 0;
+    double fused_wait_s = 0.5;
     double sc_timeout_s = 2.0;
     std::vector<float> sc_h, sc_y;         // host scratch: h, and the rows before they are published
     std::vector<uint8_t> sc_q8h, sc_q8x;
@@ -216,7 +223,8 @@ struct moe_cache {
     // on two streams (fork/join per layer), otherwise one launch serves both;
     // `graph` replays the token's launches as one captured HIP graph over fixed
     // device buffers (x_buf, bias_buf, out_buf)
-    int split = 0;                     // 0 one launch, 1 fork/join over two streams, 2 serial on one stream
+    int split = 0;                     // 0 fused layer launch, 1 fork/join over two streams,
+                                       // 2 serial on one stream, 3 router, selection and experts unfused
     bool graph = true;
     hipStream_t cap_stream = nullptr;
     hipEvent_t ev_user = nullptr, ev_done = nullptr;
@@ -1144,6 +1152,7 @@ void free_cache(moe_cache *c) {
     hipFree(c->exp_ws);
     hipFree(c->ypart);
     hipFree(c->d_ids);
+    hipFree(c->fx);
     hipFree(c->d_slots);
     hipFree(c->d_w);
     hipFree(c->d_q8x);
@@ -1461,15 +1470,22 @@ int moe_cache_create(const moe_cache_config *cfg, moe_cache **out) {
     const size_t rws = route_ws_bytes(E, 1), ews = exp_ws_bytes(c->I, c->K);
     if (hipMalloc(&c->route_ws, rws) != hipSuccess || hipMalloc(&c->exp_ws, ews) != hipSuccess ||
         hipMalloc(&c->ypart, ((size_t)c->K + 1) * c->H * 4) != hipSuccess ||
-        hipMalloc(&c->d_ids, (size_t)NL * c->K * 4) != hipSuccess ||
+        hipMalloc(&c->d_ids, ((size_t)NL * c->K + 64) * 4) != hipSuccess ||
         hipMalloc(&c->d_slots, (size_t)NL * c->K * 4) != hipSuccess ||
         hipMalloc(&c->d_w, (size_t)NL * c->K * 4) != hipSuccess ||
         hipMalloc(&c->d_q8x, (size_t)(c->H / 256) * mp::Q8K_BYTES + 256) != hipSuccess ||
-        hipHostMalloc(&c->h_ids, (size_t)NL * c->K * 4, 0) != hipSuccess ||
-        hipHostMalloc(&c->h_slots, (size_t)NL * c->K * 4, 0) != hipSuccess)
+        hipHostMalloc(&c->h_ids, ((size_t)NL * c->K + 64) * 4, 0) != hipSuccess ||
+        hipHostMalloc(&c->h_slots, (size_t)NL * c->K * 4, 0) != hipSuccess ||
+        hipMalloc(&c->fx, (size_t)NL * mp::fused_words(c->K, c->I, c->H) * 8) != hipSuccess ||
+        hipHostMalloc((void **)&c->h_seq, 64, hipHostMallocDefault) != hipSuccess ||
+        hipMalloc(&c->d_seq, 64) != hipSuccess)
         return bail(fail(MOE_ERR_NOMEM, "decode scratch"));
-    if (hipMemset(c->route_ws, 0, rws) != hipSuccess || hipMemset(c->exp_ws, 0, ews) != hipSuccess)
+    // tag 0 is never a token's sequence number: zeroed exchange words are stale
+    if (hipMemset(c->route_ws, 0, rws) != hipSuccess || hipMemset(c->exp_ws, 0, ews) != hipSuccess ||
+        hipMemset(c->fx, 0, (size_t)NL * mp::fused_words(c->K, c->I, c->H) * 8) != hipSuccess ||
+        hipMemset(c->d_ids, 0, ((size_t)NL * c->K + 64) * 4) != hipSuccess || hipMemset(c->d_seq, 0, 64) != hipSuccess)
         return bail(fail(MOE_ERR_HIP, "scratch clear"));
+    c->fx_words = mp::fused_words(c->K, c->I, c->H);
     if (hipStreamCreateWithFlags(&c->up_stream, hipStreamNonBlocking) != hipSuccess ||
         hipStreamCreateWithFlags(&c->tbl_stream, hipStreamNonBlocking) != hipSuccess ||
         hipStreamCreateWithFlags(&c->host_stream, hipStreamNonBlocking) != hipSuccess ||
@@ -2092,9 +2108,9 @@ int moe_cache_stats_get(moe_cache *c, moe_cache_stats *s) {
 
 int moe_cache_set_decode_path(moe_cache *c, int split, int graph) {
     if (!c) return fail(MOE_ERR_ARG, "null cache");
-    if (split < 0 || split > 2) return fail(MOE_ERR_ARG, "split must be 0, 1 or 2");
-    if (split != 0 && c->sc_den > 0)
-        return fail(MOE_ERR_STATE, "CPU-assisted serving runs with the one-launch path (split 0); turn it off first");
+    if (split < 0 || split > 3) return fail(MOE_ERR_ARG, "split must be 0, 1, 2 or 3");
+    if ((split == 1 || split == 2) && c->sc_den > 0)
+        return fail(MOE_ERR_STATE, "CPU-assisted serving runs with one expert launch (split 0 or 3); turn it off first");
     c->split = split;
     c->graph = graph != 0;
     return MOE_OK;
@@ -2109,7 +2125,8 @@ int moe_cache_set_sidecar(moe_cache *c, int n_threads, int num, int den) {
         return MOE_OK;
     }
     if (den < 1 || num < 0 || num > den) return fail(MOE_ERR_ARG, "share %d/%d: need 0 <= num <= den, den >= 1", num, den);
-    if (c->split != 0) return fail(MOE_ERR_STATE, "CPU-assisted serving runs with the one-launch path (split 0)");
+    if (c->split == 1 || c->split == 2)
+        return fail(MOE_ERR_STATE, "CPU-assisted serving runs with one expert launch (split 0 or 3)");
     if (c->K > 16 || (c->H / 256) * mp::Q8K_BYTES > mp::SC_Q8X_BYTES) return fail(MOE_ERR_ARG, "shape too large");
     HIPCHK(hipSetDevice(c->cfg.device));
     const size_t NL = c->L.size();
@@ -2246,7 +2263,7 @@ int moe_cache_sync(moe_cache *c) {
 
 static int decode_layer_impl(moe_cache *c, int layer, const float *x, const float *bias, float *out,
                              int32_t *ids_dev, float *w_dev, hipStream_t st, hipEvent_t *ev, bool stage = false,
-                             bool sidecar = false);
+                             bool sidecar = false, bool fused = false);
 
 
 int moe_decode_layer(moe_cache *c, int layer, const float *x, const float *bias, float *out, int32_t *ids_dev,
@@ -2254,9 +2271,11 @@ int moe_decode_layer(moe_cache *c, int layer, const float *x, const float *bias,
     return decode_layer_impl(c, layer, x, bias, out, ids_dev, w_dev, (hipStream_t)stream, nullptr);
 }
 
+// fused: the token's sequence number is in d_seq (moe_decode_token), split is
+// 0 and streaming is off; the router, selection and gate/up run as one launch
 static int decode_layer_impl(moe_cache *c, int layer, const float *x, const float *bias, float *out,
                              int32_t *ids_dev, float *w_dev, hipStream_t st, hipEvent_t *ev, bool stage,
-                             bool sidecar) {
+                             bool sidecar, bool fused) {
     if (!c || !x || !out || layer < 0 || layer >= (int)c->L.size()) return fail(MOE_ERR_ARG, "bad arguments");
     if (c->host_only) return fail(MOE_ERR_STATE, "host-only cache (device < 0) cannot decode");
     const Layer &ls = c->L[layer];
@@ -2297,8 +2316,6 @@ static int decode_layer_impl(moe_cache *c, int layer, const float *x, const floa
         look.apost = stm->post_d + layer;
         look.fresh = stm->fresh + layer;
     }
-    int r = run_route(&rd, st, ev, sidecar ? c->sc_post_d + layer : nullptr, c->d_seq, stm ? &look : nullptr);
-    if (r != MOE_OK) return r;
     moe_experts_desc ed{};
     ed.ids = ids; ed.slots = slots; ed.w = w;
     ed.slot_pool = ls.pool; ed.slot_bytes = ls.slot_bytes; ed.n_slots = ls.S;
@@ -2336,9 +2353,33 @@ static int decode_layer_impl(moe_cache *c, int layer, const float *x, const floa
     a.ypart = c->ypart;
     mp::ExpertArgs ah = a;
     ah.join = 1;
-    if (c->split == 0) {
-        HIPCHK(mp::launch_gateup(a, 0, st, E_(4), E_(5)));
-        HIPCHK(mp::launch_down(a, 0, st, E_(6), E_(7)));
+    if (fused) {
+        mp::FusedArgs f{};
+        mp::RouteLaunch &rl = f.r;
+        rl.W = rd.W; rl.x = rd.x; rl.bias = rd.bias; rl.prior = rd.prior; rl.table = rd.table; rl.dummy = rd.dummy;
+        rl.prior_on_logits = rd.prior_on_logits;
+        rl.E = rd.E; rl.H = rd.H; rl.K = rd.K; rl.n_tok = 1;
+        rl.ids = ids; rl.w = w; rl.slots = slots;
+        rl.post = sidecar ? c->sc_post_d + layer : nullptr;
+        rl.seq = c->d_seq;
+        f.x = a;
+        f.x.ypart = sidecar ? c->ypart : nullptr;       // the join kernel combines with the host's rows
+        f.xlog = c->fx + (size_t)layer * c->fx_words;
+        f.rec = f.xlog + 256;
+        f.hx = f.rec + (size_t)mp::FUSED_COPIES * mp::FUSED_REC;
+        f.yx = f.hx + (size_t)(c->K + 1) * c->I;
+        f.err = (uint32_t *)(c->d_ids + c->L.size() * (size_t)c->K);
+        f.wait_ticks = (uint64_t)(c->fused_wait_s * 1e8);
+        HIPCHK(mp::launch_fused(f, st, E_(0), E_(1)));
+    } else {
+        const int r = run_route(&rd, st, ev, sidecar ? c->sc_post_d + layer : nullptr, c->d_seq, stm ? &look : nullptr);
+        if (r != MOE_OK) return r;
+    }
+    if (c->split == 0 || c->split == 3) {
+        if (!fused) {
+            HIPCHK(mp::launch_gateup(a, 0, st, E_(4), E_(5)));
+            HIPCHK(mp::launch_down(a, 0, st, E_(6), E_(7)));
+        }
         if (sidecar) {
             mp::JoinArgs j{};
             j.ids = a.ids; j.slots = a.slots; j.w = a.w;
@@ -2409,13 +2450,14 @@ int moe_decode_token(moe_cache *c, const float *x, const float *bias, float *out
     // the answers of every layer
     const bool sc = c->sc_den > 0;
     Streamer *stm = c->st && c->st->live ? c->st : nullptr;
-    uint32_t seq = 0;
-    if (sc || stm) {
-        seq = ++c->sc_seq;
-        if (seq == 0 || seq == mp::SC_ABORT) seq = c->sc_seq = 1;
-        *c->h_seq = seq;
-        HIPCHK(hipMemcpyAsync(c->d_seq, c->h_seq, 4, hipMemcpyHostToDevice, st));
-    }
+    // (the fused layers' exchange words are tagged with it too).  The copy
+    // reads h_seq when the stream reaches it; the previous token synchronised
+    // the stream before returning, so no copy of an older number is pending.
+    uint32_t seq = ++c->sc_seq;
+    if (seq == 0 || seq == mp::SC_ABORT) seq = c->sc_seq = 1;
+    *c->h_seq = seq;
+    HIPCHK(hipMemcpyAsync(c->d_seq, c->h_seq, 4, hipMemcpyHostToDevice, st));
+    const bool fused = c->split == 0 && !stm;
     // An earlier token that failed may have left SC_ABORT in the answers; a
     // join of this token must wait for this token's answer, not end on that.
     // Nothing of this token runs yet, so plain stores suffice.
@@ -2457,7 +2499,7 @@ int moe_decode_token(moe_cache *c, const float *x, const float *bias, float *out
         for (int l = 0; l < NL; ++l) {
             const int r = decode_layer_impl(c, l, x + (size_t)l * c->H, bias ? bias + (size_t)l * c->E : nullptr,
                                             out + (size_t)l * c->H, nullptr, nullptr, st,
-                                            c->timing ? c->tev.data() + (size_t)l * 12 : nullptr, stage, sc);
+                                            c->timing ? c->tev.data() + (size_t)l * 12 : nullptr, stage, sc, fused);
             if (r != MOE_OK) {
                 abort_joins();
                 hipStreamSynchronize(st);
@@ -2467,8 +2509,7 @@ int moe_decode_token(moe_cache *c, const float *x, const float *bias, float *out
         }
 
     } else {
-        const int key = bias ? 1 : 0;
-        const int mode = c->split;
+        const int key = bias ? 1 : 0;        const int mode = c->split + (fused ? 10 : 0);
         if (!c->gx[key] || c->g_mode[key] != mode) {
             if (c->gx[key]) { hipGraphExecDestroy(c->gx[key]); c->gx[key] = nullptr; }
             if (c->g[key]) { hipGraphDestroy(c->g[key]); c->g[key] = nullptr; }
@@ -2477,7 +2518,7 @@ int moe_decode_token(moe_cache *c, const float *x, const float *bias, float *out
             for (int l = 0; l < NL && r == MOE_OK; ++l)
                 r = decode_layer_impl(c, l, c->x_buf + (size_t)l * c->H, key ? c->bias_buf + (size_t)l * c->E : nullptr,
                                       c->out_buf + (size_t)l * c->H, nullptr, nullptr, c->cap_stream, nullptr, stage,
-                                      sc);
+                                      sc, fused);
 
             hipGraph_t g = nullptr;
             const hipError_t ec = hipStreamEndCapture(c->cap_stream, &g);
@@ -2502,13 +2543,16 @@ int moe_decode_token(moe_cache *c, const float *x, const float *bias, float *out
         mpc::team_hot(c->team, false);
         if (serve_err != MOE_OK) abort_joins();
     }
-    HIPCHK(hipMemcpyAsync(c->h_ids, c->d_ids, (size_t)NL * c->K * 4, hipMemcpyDeviceToHost, st));
+    // the routed ids and, after them, the fused layers' late-wait word
+    HIPCHK(hipMemcpyAsync(c->h_ids, c->d_ids, ((size_t)NL * c->K + 1) * 4, hipMemcpyDeviceToHost, st));
     HIPCHK(hipMemcpyAsync(c->h_slots, c->d_slots, (size_t)NL * c->K * 4, hipMemcpyDeviceToHost, st));
     const hipError_t sync_err = hipStreamSynchronize(st);
     const auto t_sync = std::chrono::steady_clock::now();
     const int drain_err = mover_drain();
     if (sync_err != hipSuccess) return fail(MOE_ERR_HIP, "decode: %s", hipGetErrorString(sync_err));
     if (drain_err != MOE_OK) return drain_err;
+    if (fused && (uint32_t)c->h_ids[(size_t)NL * c->K] == seq)
+        return fail(MOE_ERR_HIP, "a fused layer's workgroup gave up waiting for another (%.1f s)", c->fused_wait_s);
     if (stm && stm->failed) return fail(MOE_ERR_HIP, "streaming stopped on a copy queue error");
     if (sc) {
         bool late = false;
@@ -2524,26 +2568,40 @@ int moe_decode_token(moe_cache *c, const float *x, const float *bias, float *out
         for (int l = 0; l < NL; ++l) {
             float t[6] = {0, 0, 0, 0, 0, 0};
             hipEvent_t *e = c->tev.data() + (size_t)l * 12;
-            for (int i = 0; i < 6; ++i) {
-                if (c->split == 0 && i >= 4) break;            // no separate absent-expert launches
-                HIPCHK(hipEventElapsedTime(&t[i], e[2 * i], e[2 * i + 1]));
-            }
-            c->kt.route_ms += t[0] + t[1];
-            c->kt.gateup_hbm_ms += t[2];
-            c->kt.down_hbm_ms += t[3];
-            c->kt.gateup_host_ms += t[4];
-            c->kt.down_host_ms += t[5];
-            c->kt.n_layers++;
             const Layer &ls = c->L[l];
+            if (fused) {            // [0,1] the fused layer
+                HIPCHK(hipEventElapsedTime(&t[0], e[0], e[1]));
+                c->kt.layer_ms += t[0];
+                c->kt.layer_hbm_bytes += (uint64_t)c->E * c->H * 4;       // the router rows
+            } else {
+                for (int i = 0; i < 6; ++i) {
+                    if ((c->split == 0 || c->split == 3) && i >= 4) break;   // no separate absent-expert launches
+                    HIPCHK(hipEventElapsedTime(&t[i], e[2 * i], e[2 * i + 1]));
+                }
+                c->kt.route_ms += t[0] + t[1];
+                c->kt.gateup_hbm_ms += t[2];
+                c->kt.down_hbm_ms += t[3];
+                c->kt.gateup_host_ms += t[4];
+                c->kt.down_host_ms += t[5];
+            }
+            c->kt.n_layers++;
+            int r_abs = 0;          // rank among the absent experts: the host's share is not read by the GPU
             for (int k = 0; k < c->K; ++k) {
                 const int gs = c->h_slots[(size_t)l * c->K + k];
+                const int id = c->h_ids[(size_t)l * c->K + k];
                 const bool res = gs >= 0 && gs < ls.S;
+                const bool absent = !res && id >= 0 && id < ls.E;
+                const bool cpu = absent && sc && r_abs % c->sc_den < c->sc_num;
+                r_abs += absent;
+                if (cpu) continue;
                 (res ? c->kt.gateup_hbm_bytes : c->kt.gateup_host_bytes) += gu_b;
                 (res ? c->kt.down_hbm_bytes : c->kt.down_host_bytes) += ls.expert_bytes - gu_b;
+                if (fused) (res ? c->kt.layer_hbm_bytes : c->kt.layer_host_bytes) += ls.expert_bytes;
             }
             if (ls.shared) {
                 c->kt.gateup_hbm_bytes += gu_b;
                 c->kt.down_hbm_bytes += ls.expert_bytes - gu_b;
+                if (fused) c->kt.layer_hbm_bytes += ls.expert_bytes;
             }
         }
     }
@@ -2612,8 +2670,9 @@ int moe_combine(const float *pair_rows, int n_tok, int K, int H, float *out, int
     return MOE_OK;
 }
 
-int moe_grouped_experts(const moe_grouped_desc *d, void *stream) {
-    if (!d || !d->offsets || !d->perm || !d->w || !d->x || !d->out || !d->workspace)
+// shape and pointer checks shared by both grouped entry points
+static int grouped_check(const moe_grouped_desc *d) {
+    if (!d || !d->offsets || !d->perm || !d->w || !d->x || !d->out)
         return fail(MOE_ERR_ARG, "moe_grouped_experts: null argument");
     if (d->H != 2048) return fail(MOE_ERR_ARG, "hidden size %d unsupported (the kernels are built for 2048)", d->H);
     if (d->I % 256 || d->I < 256 || d->I > 768) return fail(MOE_ERR_ARG, "intermediate %d must be 256, 512 or 768", d->I);
@@ -2636,9 +2695,12 @@ int moe_grouped_experts(const moe_grouped_desc *d, void *stream) {
     if (r != MOE_OK) return r;
     if (d->shared && (r = check_weight_ptrs("moe_grouped_experts", d->shared, nullptr)) != MOE_OK) return r;
     if ((uintptr_t)d->shared % 16) return fail(MOE_ERR_ARG, "shared expert must be 16-byte aligned");
-    const hipStream_t st = (hipStream_t)stream;
+    return MOE_OK;
+}
+
+// the grouped expert chain over a checked descriptor, with ws as its workspace
+static int grouped_run(const moe_grouped_desc *d, uint8_t *ws, hipStream_t st) {
     const GroupedWs w = grouped_ws(d->n_tok, d->K, d->H, d->I);
-    uint8_t *ws = (uint8_t *)d->workspace;
     mp::GroupedArgs a{};
     a.offsets = d->offsets; a.perm = d->perm; a.w = d->w;
     a.table = d->table; a.slot_pool = d->slot_pool; a.slot_bytes = d->slot_bytes; a.n_slots = d->n_slots;
@@ -2691,6 +2753,29 @@ int moe_grouped_experts(const moe_grouped_desc *d, void *stream) {
         for (auto e : ev) hipEventDestroy(e);
     }
     return rc;
+}
+
+int moe_grouped_experts(const moe_grouped_desc *d, void *stream) {
+    int r = grouped_check(d);
+    if (r != MOE_OK) return r;
+    if (!d->workspace) return fail(MOE_ERR_ARG, "moe_grouped_experts: null workspace");
+    return grouped_run(d, (uint8_t *)d->workspace, (hipStream_t)stream);
+}
+
+int moe_grouped_experts_static(const moe_grouped_desc *d, void *stream) {
+    int r = grouped_check(d);
+    if (r != MOE_OK) return r;
+    if (d->workspace) return fail(MOE_ERR_ARG, "moe_grouped_experts_static: workspace must be NULL (it uses its own)");
+    if (d->kernel_ms) return fail(MOE_ERR_ARG, "moe_grouped_experts_static: kernel_ms must be NULL (timing creates events)");
+    const size_t need = grouped_ws(d->n_tok, d->K, d->H, d->I).total;
+    static_assert(mp::STATIC_SCRATCH_BYTES == MOE_GROUPED_STATIC_SCRATCH_BYTES, "header and library disagree");
+    if (need > mp::STATIC_SCRATCH_BYTES)
+        return fail(MOE_ERR_ARG, "moe_grouped_experts_static: n_tok %d x K %d at I %d needs %zu bytes of scratch, "
+                    "more than the %zu it holds", d->n_tok, d->K, d->I, need, (size_t)mp::STATIC_SCRATCH_BYTES);
+    void *ws = nullptr;
+    const hipError_t e = mp::static_scratch(&ws);
+    if (e != hipSuccess) return fail(MOE_ERR_HIP, "static scratch: %s", hipGetErrorString(e));
+    return grouped_run(d, (uint8_t *)ws, (hipStream_t)stream);
 }
 
 // ---- batched decode through the cache ------------------------------------------

@@ -12,6 +12,8 @@ LIB_PATH = os.path.join(HERE, "libmoeprefetch.so")
 MOE_OK = 0
 TYPE_Q4K, TYPE_Q6K = 12, 14
 DTYPE_F32, DTYPE_BF16 = 0, 1
+# the static workspace of moe_grouped_experts_static (MOE_GROUPED_STATIC_SCRATCH_BYTES)
+GROUPED_STATIC_SCRATCH_BYTES = 16 << 20
 ADMIT = {"off": 0, "heat": 1, "window": 2}
 PUBLISH = {"fifo": 0, "sorted": 1, "live": 2}
 
@@ -78,7 +80,8 @@ class KernelTimes(ctypes.Structure):
     _fields_ = [(n, ctypes.c_double) for n in ("route_ms", "gateup_hbm_ms", "down_hbm_ms", "gateup_host_ms",
                                                "down_host_ms")] + \
                [(n, U64) for n in ("n_layers", "gateup_hbm_bytes", "down_hbm_bytes", "gateup_host_bytes",
-                                   "down_host_bytes")]
+                                   "down_host_bytes")] + \
+               [("layer_ms", ctypes.c_double), ("layer_hbm_bytes", U64), ("layer_host_bytes", U64)]
 
 
 class StreamConfig(ctypes.Structure):
@@ -205,6 +208,7 @@ SIGNATURES = {
     "moe_quant_rows": (ctypes.c_int, [P, ctypes.c_int, ctypes.c_int, ctypes.c_int, P, P, P, P]),
     "moe_grouped_workspace_bytes": (SZ, [ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int]),
     "moe_grouped_experts": (ctypes.c_int, [ctypes.POINTER(GroupedDesc), P]),
+    "moe_grouped_experts_static": (ctypes.c_int, [ctypes.POINTER(GroupedDesc), P]),
     "moe_combine": (ctypes.c_int, [P, ctypes.c_int, ctypes.c_int, ctypes.c_int, P, ctypes.c_int, P]),
     "moe_pool_create": (ctypes.c_int, [ctypes.c_int, ctypes.c_int, SZ, ctypes.c_int, ctypes.POINTER(P)]),
     "moe_pool_destroy": (ctypes.c_int, [P]),

@@ -52,9 +52,11 @@
  *       cases (cpp/test-moe-planner.cpp) and brute-force EDF checks.
  *
  * Canonical router order (shared with the GPU kernel):
- *   logit[e]  = 64 lane partials p_j, p_j accumulated with fmaf over
- *               i = 0..H/256-1, c = 0..3 of W[e][256 i + 4 j + c] * x[...],
- *               then a butterfly p_j += p_{j^o} for o = 32,16,8,4,2,1.
+ *   logit[e]  = s_0 + s_1 + s_2 + s_3 (left to right) over the row's four
+ *               quarters of Q = H/4 values; s_q: 64 lane partials p_j, p_j
+ *               accumulated with fmaf (from 0) over i = 0..Q/256-1, c = 0..3
+ *               of W[e][Q q + 256 i + 4 j + c] * x[...], then a butterfly
+ *               p_j += p_{j^o} for o = 32,16,8,4,2,1.  (H a multiple of 1024.)
  *   (+ bias[e], one fp32 add, when a steering bias is given)
  *   m         = max_e logit[e]
  *   ex[e]     = or_expf(logit[e] - m)

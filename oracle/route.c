@@ -39,23 +39,29 @@ float or_expf(float x) {
 }
 
 float or_row_logit(int H, const float *w, const float *x) {
-    float p[64];
-    for (int j = 0; j < 64; ++j) {
-        float acc = 0.0f;
-        for (int i = 0; i < H / 256; ++i) {
-            for (int c = 0; c < 4; ++c) {
-                const int k = 256 * i + 4 * j + c;
-                acc = fmaf(w[k], x[k], acc);
+    /* four quarters of the row, one per wavefront of the GPU's workgroup */
+    const int Q = H / 4;
+    float s[4];
+    for (int q = 0; q < 4; ++q) {
+        float p[64];
+        for (int j = 0; j < 64; ++j) {
+            float acc = 0.0f;
+            for (int i = 0; i < Q / 256; ++i) {
+                for (int c = 0; c < 4; ++c) {
+                    const int k = Q * q + 256 * i + 4 * j + c;
+                    acc = fmaf(w[k], x[k], acc);
+                }
             }
+            p[j] = acc;
         }
-        p[j] = acc;
+        for (int o = 32; o >= 1; o >>= 1) {
+            float t[64];
+            for (int j = 0; j < 64; ++j) t[j] = p[j] + p[j ^ o];
+            memcpy(p, t, sizeof p);
+        }
+        s[q] = p[0];
     }
-    for (int o = 32; o >= 1; o >>= 1) {
-        float q[64];
-        for (int j = 0; j < 64; ++j) q[j] = p[j] + p[j ^ o];
-        memcpy(p, q, sizeof p);
-    }
-    return p[0];
+    return ((s[0] + s[1]) + s[2]) + s[3];
 }
 
 static void softmax_topk(int E, int K, const float *logits, const float *prior, int prior_on_logits,

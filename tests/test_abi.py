@@ -59,3 +59,9 @@ def test_h2d_batch_refuses_on_the_host():
     sizes = (ctypes.c_size_t * 2)(16, 16)
     assert L.moe_memcpy_h2d_batch(0, dst, src, sizes, 2) is False
     assert b"slice 1 of 2" in L.moe_last_error()
+
+
+def test_static_scratch_size_matches_header():
+    text = open(os.path.join(ROOT, "include", "moe_prefetch.h")).read()
+    m = re.search(r"#define MOE_GROUPED_STATIC_SCRATCH_BYTES \((\d+)u << (\d+)\)", text)
+    assert m and int(m.group(1)) << int(m.group(2)) == _lib.GROUPED_STATIC_SCRATCH_BYTES

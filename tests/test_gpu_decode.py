@@ -66,12 +66,14 @@ def check_run(rig, tmp_path, out_every=1, tol=1e-3, oc=None, record_map=True, to
     return worst
 
 
-@pytest.mark.parametrize("split,graph", [(1, 1), (0, 1), (2, 1), (1, 0), (0, 0), (2, 0)],
-                         ids=["fork-graph", "fused-graph", "serial-graph", "fork-eager", "fused-eager",
-                              "serial-eager"])
+@pytest.mark.parametrize("split,graph", [(1, 1), (0, 1), (2, 1), (3, 1), (1, 0), (0, 0), (2, 0), (3, 0)],
+                         ids=["fork-graph", "fused-graph", "serial-graph", "unfused-graph", "fork-eager",
+                              "fused-eager", "serial-eager", "unfused-eager"])
 def test_decode_4_layers_window_admission(tmp_path, split, graph):
-    # every decode path (resident/absent experts split over two streams or one
-    # launch; captured graph replayed per token or eager launches) must give
+    # every decode path (the fused front with one expert launch; router,
+    # selection and experts as four launches; resident/absent experts split
+    # over two streams or one after the other; captured graph replayed per
+    # token or eager launches) must give
     # the oracle's ids, frames and outputs; the graph is replayed 40 times
     # with eager copies, host work and synchronisation between replays
     rig = Rig([16, 24, 12, 40], [Q4, Q6, Q4, Q6], T=40, admit="window", batch_tables=True)
