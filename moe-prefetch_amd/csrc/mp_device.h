@@ -31,14 +31,70 @@ __device__ inline float canon_expf(float x) {
 // subnormals included: each is a normal fp32 value)
 __device__ inline float h2f_dev(uint16_t h) { return (float)__builtin_bit_cast(_Float16, h); }
 
-__device__ inline float bfly_add(float v) {
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) v = v + __shfl_xor(v, o, 64);
-    return v;
+// DPP lane moves within a row of 16 lanes (a VALU operand, no LDS crossbar)
+constexpr int DPP_XOR1 = 0xB1;       // quad_perm [1,0,3,2]
+constexpr int DPP_XOR2 = 0x4E;       // quad_perm [2,3,0,1]
+constexpr int DPP_HALF_MIRROR = 0x141;
+constexpr int DPP_MIRROR = 0x140;
+template <int CTRL>
+__device__ inline int dpp_i(int v) { return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, false); }
+template <int CTRL>
+__device__ inline float dpp_f(float v) { return __int_as_float(dpp_i<CTRL>(__float_as_int(v))); }
+__device__ inline float lane_f(float v, int l) { return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l)); }
+
+// Sum of a wave's 64 values in the canonical butterfly order: p_j += p_{j^o}
+// for o = 1, 2, 4, 8, 16, 32 (every lane ends with the same bits).  After
+// the first two steps each quad holds one value, so the mirror lanes that
+// row_half_mirror and row_mirror reach add exactly what lanes j^4 and j^8
+// hold; the last two steps add the four rows' values as (r0 + r1) + (r2 + r3).
+__device__ inline float wave_sum_canon(float v) {
+    v = v + dpp_f<DPP_XOR1>(v);
+    v = v + dpp_f<DPP_XOR2>(v);
+    v = v + dpp_f<DPP_HALF_MIRROR>(v);
+    v = v + dpp_f<DPP_MIRROR>(v);
+    return (lane_f(v, 0) + lane_f(v, 16)) + (lane_f(v, 32) + lane_f(v, 48));
+}
+
+// maximum over the wave (any order gives the same value)
+__device__ inline float wave_max(float v) {
+    v = fmaxf(v, dpp_f<DPP_XOR1>(v));
+    v = fmaxf(v, dpp_f<DPP_XOR2>(v));
+    v = fmaxf(v, dpp_f<DPP_HALF_MIRROR>(v));
+    v = fmaxf(v, dpp_f<DPP_MIRROR>(v));
+    return fmaxf(fmaxf(lane_f(v, 0), lane_f(v, 16)), fmaxf(lane_f(v, 32), lane_f(v, 48)));
 }
 
 __device__ inline int32_t sdot4(uint32_t a, uint32_t b, int32_t c) {
     return __builtin_amdgcn_sdot4((int)a, (int)b, c, false);
+}
+
+// Q8_K of 256 values held 4 per lane (lane-major) by one wavefront: the
+// largest magnitude (first index on a tie) maps to -127, q = min(127,
+// rint(x * iscale)); d = 1 / iscale, 0 for an all-zero block.
+// the larger of two (magnitude, value, index) candidates: the larger
+// magnitude, the lower index on a tie -- associative and commutative, so any
+// reduction order selects the same element
+__device__ inline void amax_pick(float &amax, float &mx, int &idx, float oa, float om, int oi) {
+    if (oa > amax || (oa == amax && oi < idx)) { amax = oa; mx = om; idx = oi; }
+}
+template <int CTRL>
+__device__ inline void amax_step(float &amax, float &mx, int &idx) {
+    amax_pick(amax, mx, idx, dpp_f<CTRL>(amax), dpp_f<CTRL>(mx), dpp_i<CTRL>(idx));
+}
+// the wave's largest magnitude (first index on a tie), on every lane
+__device__ inline void amax_wave(float &amax, float &mx, int &idx) {
+    amax_step<DPP_XOR1>(amax, mx, idx);
+    amax_step<DPP_XOR2>(amax, mx, idx);
+    amax_step<DPP_HALF_MIRROR>(amax, mx, idx);
+    amax_step<DPP_MIRROR>(amax, mx, idx);
+    float a = lane_f(amax, 0), m = lane_f(mx, 0);
+    int i = __builtin_amdgcn_readlane(idx, 0);
+#pragma unroll
+    for (int r = 16; r < 64; r += 16)
+        amax_pick(a, m, i, lane_f(amax, r), lane_f(mx, r), __builtin_amdgcn_readlane(idx, r));
+    amax = a;
+    mx = m;
+    idx = i;
 }
 
 // Q8_K of 256 values held 4 per lane (lane-major) by one wavefront: the
@@ -51,13 +107,7 @@ __device__ inline void q8k_wave_vals(const float xv[4], int lane, int q[4], floa
         const float ax = fabsf(xv[i]);
         if (ax > amax) { amax = ax; mx = xv[i]; idx = 4 * lane + i; }
     }
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) {
-        const float oa = __shfl_xor(amax, o, 64);
-        const float om = __shfl_xor(mx, o, 64);
-        const int oi = __shfl_xor(idx, o, 64);
-        if (oa > amax || (oa == amax && oi < idx)) { amax = oa; mx = om; idx = oi; }
-    }
+    amax_wave(amax, mx, idx);
     q[0] = q[1] = q[2] = q[3] = 0;
     d = 0.0f;
     if (amax != 0.0f) {
@@ -70,8 +120,7 @@ __device__ inline void q8k_wave_vals(const float xv[4], int lane, int q[4], floa
     }
 }
 
-// NB blocks at once (each exactly as q8k_wave_vals), their cross-lane rounds
-// interleaved so that one block's shuffles fill another's latency
+// NB blocks at once, each exactly as q8k_wave_vals
 template <int NB>
 __device__ inline void q8k_wave_vals_n(const float (*xv)[4], int lane, int (*q)[4], float *d) {
     float amax[NB], mx[NB];
@@ -87,19 +136,7 @@ __device__ inline void q8k_wave_vals_n(const float (*xv)[4], int lane, int (*q)[
         }
     }
 #pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) {
-        float oa[NB], om[NB];
-        int oi[NB];
-#pragma unroll
-        for (int b = 0; b < NB; ++b) {
-            oa[b] = __shfl_xor(amax[b], o, 64);
-            om[b] = __shfl_xor(mx[b], o, 64);
-            oi[b] = __shfl_xor(idx[b], o, 64);
-        }
-#pragma unroll
-        for (int b = 0; b < NB; ++b)
-            if (oa[b] > amax[b] || (oa[b] == amax[b] && oi[b] < idx[b])) { amax[b] = oa[b]; mx[b] = om[b]; idx[b] = oi[b]; }
-    }
+    for (int b = 0; b < NB; ++b) amax_wave(amax[b], mx[b], idx[b]);
 #pragma unroll
     for (int b = 0; b < NB; ++b) {
         q[b][0] = q[b][1] = q[b][2] = q[b][3] = 0;
@@ -139,11 +176,21 @@ __device__ inline int key_rank(const uint64_t *s_key, int n, uint64_t key) {
     return rank;
 }
 
+// Integer sum over each aligned group of 8 lanes, on every lane of the group,
+// by DPP lane moves (no LDS crossbar): swap neighbours, swap pairs, then add
+// the mirror lane of the other quad.  Integer sums are exact in any order.
+__device__ inline int sum8_dpp(int v) {
+    v += __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xF, 0xF, false);     // quad_perm [1,0,3,2]
+    v += __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xF, 0xF, false);     // quad_perm [2,3,0,1]
+    v += __builtin_amdgcn_update_dpp(0, v, 0x141, 0xF, 0xF, false);    // row_half_mirror
+    return v;
+}
+
 // the 16-value group sum of the Q8_K block, valid on lanes with (lane & 3) == 0
 __device__ inline int q8k_group_sum(const int q[4]) {
     int gs = q[0] + q[1] + q[2] + q[3];
-    gs += __shfl_xor(gs, 1, 64);
-    gs += __shfl_xor(gs, 2, 64);
+    gs += dpp_i<DPP_XOR1>(gs);
+    gs += dpp_i<DPP_XOR2>(gs);
     return gs;
 }
 

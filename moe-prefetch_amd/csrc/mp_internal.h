@@ -154,7 +154,7 @@ struct JoinArgs {
 constexpr int FUSED_COPIES = 16;    // copies of the routing record (fewer readers per line)
 constexpr int FUSED_REC = 32;       // words per copy: [k] sc_tag(seq, slot, id) of routed expert k,
                                     // [16 + k] (seq << 32) | bits of its gate weight
-constexpr int FUSED_GU_ROWS = 2;    // gate/up rows per wave
+constexpr int FUSED_GU_TILE = 16;   // gate/up rows per workgroup (4 per wave)
 constexpr int FUSED_DN_TILE = 32;   // down rows per workgroup (8 per wave)
 struct FusedArgs {
     RouteLaunch r;            // router and selection (seq, table, prior, bias, post; no lookahead)

@@ -130,7 +130,7 @@ __device__ inline float router_quarter(const float *w, const float *x, const flo
         acc = fmaf(wv.z, xv.z, acc);
         acc = fmaf(wv.w, xv.w, acc);
     }
-    return bfly_add(acc);
+    return wave_sum_canon(acc);
 }
 
 // One workgroup of RL_WAVES waves per router row: wave q sums quarter q, and
@@ -286,9 +286,7 @@ __global__ __launch_bounds__(256) void route_select_kernel(RouteArgs a) {
             }
         }
     if (wave < nc) {
-        float m = l;
-#pragma unroll
-        for (int o = 32; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+        const float m = wave_max(l);
         if (lane == 0) s_m[wave] = m;
     }
     __syncthreads();
@@ -297,7 +295,7 @@ __global__ __launch_bounds__(256) void route_select_kernel(RouteArgs a) {
         float m = s_m[0];
         for (int c = 1; c < nc; ++c) m = fmaxf(m, s_m[c]);
         ex = canon_expf(l - m);
-        const float cs = bfly_add(ex);
+        const float cs = wave_sum_canon(ex);
         if (lane == 0) s_cs[wave] = cs;
     }
     __syncthreads();
@@ -503,12 +501,8 @@ __global__ __launch_bounds__(64 * GU_WAVES) void gateup_kernel(ExpertArgs a) {
             const uint4 qs = m == 0 ? qg[r] : qu[r];
             int32_t si, mi;
             q4k_lane(hdr, qs, u, xlo, xhi, bslo, bshi, si, mi);
-            si += __shfl_xor(si, 1, 64);
-            mi += __shfl_xor(mi, 1, 64);
-            si += __shfl_xor(si, 2, 64);
-            mi += __shfl_xor(mi, 2, 64);
-            si += __shfl_xor(si, 4, 64);
-            mi += __shfl_xor(mi, 4, 64);
+            si = sum8_dpp(si);
+            mi = sum8_dpp(mi);
             const float d = h2f_dev((uint16_t)(hdr.x & 0xffff)) * dx;
             const float dm = h2f_dev((uint16_t)(hdr.x >> 16)) * dx;
             const int ps = __builtin_bit_cast(int, d * (float)si), pm = __builtin_bit_cast(int, dm * (float)mi);
@@ -599,15 +593,11 @@ __device__ inline float down_rows_dot(const uint8_t *s_wt, const uint8_t *s_q8h,
             }
             d = h2f_dev(*(const uint16_t *)(blk + 208)) * dx;
         }
-        si += __shfl_xor(si, 1, 64);
-        si += __shfl_xor(si, 2, 64);
-        si += __shfl_xor(si, 4, 64);
+        si = sum8_dpp(si);
         // super-block order, scale term then min term (CPU vec_dot order)
         y = y + d * (float)si;
         if (DT == TYPE_Q4K) {
-            mi += __shfl_xor(mi, 1, 64);
-            mi += __shfl_xor(mi, 2, 64);
-            mi += __shfl_xor(mi, 4, 64);
+            mi = sum8_dpp(mi);
             y = y - dm * (float)mi;
         }
     }
@@ -757,61 +747,6 @@ __device__ inline void fused_late(const FusedArgs &a, uint32_t seq) {
     __hip_atomic_store(a.err, seq, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// One lane's share of the Q8_K of a 256-value block xb, as the gate/up dots
-// of lane (b, u) read it: the 16-value pieces at o0 = 64 (u >> 1) + 16 (u & 1)
-// and o0 + 32, packed four codes a word, their group sums and the block's
-// scale.  The block's largest magnitude (first index on a tie) is found over
-// the block's 8 lanes (xor 1, 2, 4), so every value equals the whole block's
-// quantization (q8k_wave_vals) bit for bit.
-__device__ inline void q8k_lane_part(const float *xb, int u, uint32_t xlo[4], uint32_t xhi[4], int &bslo, int &bshi,
-                                     float &d) {
-    const int o0 = 64 * (u >> 1) + 16 * (u & 1);
-    float v[32];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const float4 a = *(const float4 *)(xb + o0 + 4 * i);
-        const float4 b = *(const float4 *)(xb + o0 + 32 + 4 * i);
-        v[4 * i] = a.x; v[4 * i + 1] = a.y; v[4 * i + 2] = a.z; v[4 * i + 3] = a.w;
-        v[16 + 4 * i] = b.x; v[16 + 4 * i + 1] = b.y; v[16 + 4 * i + 2] = b.z; v[16 + 4 * i + 3] = b.w;
-    }
-    float amax = 0.0f, mx = 0.0f;
-    int idx = 1 << 30;
-#pragma unroll
-    for (int i = 0; i < 32; ++i) {             // positions in increasing order
-        const float ax = fabsf(v[i]);
-        if (ax > amax) { amax = ax; mx = v[i]; idx = i < 16 ? o0 + i : o0 + 16 + i; }
-    }
-#pragma unroll
-    for (int o = 1; o <= 4; o <<= 1) {
-        const float oa = __shfl_xor(amax, o, 64);
-        const float om = __shfl_xor(mx, o, 64);
-        const int oi = __shfl_xor(idx, o, 64);
-        if (oa > amax || (oa == amax && oi < idx)) { amax = oa; mx = om; idx = oi; }
-    }
-    d = 0.0f;
-    float iscale = 0.0f;
-    if (amax != 0.0f) {
-        iscale = -127.0f / mx;
-        d = 1.0f / iscale;
-    }
-    bslo = bshi = 0;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        uint32_t w = 0;
-#pragma unroll
-        for (int c = 0; c < 4; ++c) {
-            int q = 0;
-            if (amax != 0.0f) {
-                const int t = (int)rintf(iscale * v[4 * i + c]);
-                q = t < 127 ? t : 127;
-            }
-            w |= (uint32_t)(q & 0xff) << (8 * c);
-            if (i < 4) bslo += q; else bshi += q;
-        }
-        if (i < 4) xlo[i] = w; else xhi[i - 4] = w;
-    }
-}
-
 // LDS of one fused workgroup, shared by the roles (each uses its own part)
 constexpr int FUSED_LDS_W = 4 * DN_LDS_ROWS;                  // down: each wave's 8 weight rows
 constexpr int FUSED_LDS_Q8 = 3 * Q8K_BYTES + 4;               // down: the Q8_K of h (I <= 768)
@@ -914,6 +849,7 @@ __device__ void fused_select(const FusedArgs &a, uint32_t seq, uint8_t *smem) {
     int *s_slot = s_ids + 16;
     float *s_w = (float *)(s_slot + 16);
     int *s_late = (int *)(s_w + 16);
+    int *s_part = s_late + 4;                       // [256] partial ranks
     if (tid == 0) *s_late = 0;
     const int32_t tword = tid < r.E ? r.table[tid] : 0;
     const float pr = (r.prior && tid < r.E) ? r.prior[tid] : 0.0f;
@@ -946,9 +882,7 @@ __device__ void fused_select(const FusedArgs &a, uint32_t seq, uint8_t *smem) {
         s_tbl[tid] = tword;
     }
     if (wave < nc) {
-        float m = l;
-#pragma unroll
-        for (int o = 32; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+        const float m = wave_max(l);
         if (lane == 0) s_m[wave] = m;
     }
     __syncthreads();
@@ -957,7 +891,7 @@ __device__ void fused_select(const FusedArgs &a, uint32_t seq, uint8_t *smem) {
         float m = s_m[0];
         for (int c = 1; c < nc; ++c) m = fmaxf(m, s_m[c]);
         ex = canon_expf(l - m);
-        const float cs = bfly_add(ex);
+        const float cs = wave_sum_canon(ex);
         if (lane == 0) s_cs[wave] = cs;
     }
     __syncthreads();
@@ -970,8 +904,15 @@ __device__ void fused_select(const FusedArgs &a, uint32_t seq, uint8_t *smem) {
         s_key[tid] = sel_key(sel, tid);                 // a NaN sorts last
     }
     __syncthreads();
-    if (tid < r.E) {       // rank of expert tid: experts ahead of it (larger, or equal with a lower id)
-        const int rank = key_rank(s_key, r.E, s_key[tid]);
+    // rank of expert e: experts ahead of it (larger, or equal with a lower
+    // id), counted by all 256 threads, 256 / E parts of the keys each
+    const int parts = 256 / r.E, span = r.E / parts;
+    const int e = tid % r.E, part = tid / r.E;
+    if (part < parts) s_part[tid] = key_rank(s_key + part * span, span, s_key[e]);
+    __syncthreads();
+    if (tid < r.E) {
+        int rank = 0;
+        for (int q = 0; q < parts; ++q) rank += s_part[tid + q * r.E];
         if (rank < r.K) s_ids[rank] = tid;
     }
     __syncthreads();
@@ -1001,87 +942,95 @@ __device__ void fused_select(const FusedArgs &a, uint32_t seq, uint8_t *smem) {
     if (tid == 0 && *s_late) fused_late(a, seq);
 }
 
-// FUSED_GU_ROWS gate/up rows per wave of routed expert k (or of the shared
-// expert, which needs no routing): the Q8_K of x first, then the routing
-// record, then the rows exactly as gateup_kernel computes them; h posted as
-// tagged words
+// Gate/up rows of routed expert k (or of the shared expert, which needs no
+// routing), 16 rows a workgroup, 4 a wave: lane (m, i, b) -- m gate or up,
+// row i, super-block b -- holds one whole Q4_K super-block (144 bytes, 256
+// weights) and its integer dots against the Q8_K of x (in LDS, quantized by
+// the workgroup before the routing is known).  The row's eight terms are
+// added in super-block order by a lane-to-lane scan, scale term then min
+// term, as the CPU vec_dot accumulates them; h = silu(gate) * up is posted as
+// a tagged word.
 __device__ void fused_gateup(const FusedArgs &a, int g, uint32_t seq, uint8_t *smem) {
-    constexpr int R = FUSED_GU_ROWS;
     const ExpertArgs &x = a.x;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int per = x.I / (4 * R);
+    const int per = x.I / FUSED_GU_TILE;
     const int k = g / per, tile = g - k * per;
-    const int b = lane >> 3, u = lane & 7;
-    uint32_t xlo[4], xhi[4];
-    int bslo, bshi;
-    float dx;
-    q8k_lane_part(a.r.x + QK * b, u, xlo, xhi, bslo, bshi, dx);
+    uint8_t *s_q8x = smem;                                          // [H / 256][292]
     uint64_t *s_rec = (uint64_t *)(smem + FUSED_LDS_W + FUSED_LDS_Q8);
     int *s_flag = (int *)(s_rec + FUSED_REC);
+    for (int b = wave; b < x.H / QK; b += 4) {         // the bytes route_logits_kernel writes
+        const float4 v = *(const float4 *)(a.r.x + QK * b + 4 * lane);
+        const float xv[4] = {v.x, v.y, v.z, v.w};
+        int q[4];
+        float d;
+        q8k_wave_vals(xv, lane, q, d);
+        q8k_store(q, d, s_q8x + b * Q8K_BYTES, lane);
+    }
     ExpertSrc src{x.shared, false, false};
-    if (k < x.K) {
+    if (k < x.K) {                                     // (fused_record's barrier orders the LDS writes)
         if (!fused_record(a, g % FUSED_COPIES, seq, false, s_rec, s_flag)) return;
         src = fused_src(x, s_rec, k);
         if (src.cpu) return;
+    } else {
+        __syncthreads();
     }
-    uint8_t *sb = src.absent && x.stage ? x.stage + (size_t)k * x.stage_stride : nullptr;
-    const size_t rb = (size_t)(x.H / QK) * Q4K_BYTES;
-    const uint8_t *up = src.base, *gate = src.base + (size_t)x.I * rb;
-    const bool valid = src.base != nullptr;
-    const int row0 = (tile * 4 + wave) * R;
-    uint4 hg[R], qg[R], hu[R], qu[R];
+    const int b = lane & 7, i = (lane >> 3) & 3;
+    const bool is_gate = lane < 32;
+    const size_t rb = (size_t)(x.H / QK) * Q4K_BYTES;     // 1152 at H = 2048
+    const int row = tile * FUSED_GU_TILE + wave * 4 + i;
+    const size_t off = (size_t)(is_gate ? x.I : 0) * rb + (size_t)row * rb + (size_t)b * Q4K_BYTES;
+    uint4 blk[9];
+    if (src.base) {
+        const uint4 *p = (const uint4 *)(src.base + off);
 #pragma unroll
-    for (int r = 0; r < R; ++r) {
-        const size_t off = (size_t)(row0 + r) * rb + (size_t)b * Q4K_BYTES;
-        const uint4 z = make_uint4(0, 0, 0, 0);
-        hg[r] = valid ? *(const uint4 *)(gate + off) : z;
-        qg[r] = valid ? *(const uint4 *)(gate + off + 16 + 16 * u) : z;
-        hu[r] = valid ? *(const uint4 *)(up + off) : z;
-        qu[r] = valid ? *(const uint4 *)(up + off + 16 + 16 * u) : z;
+        for (int j = 0; j < 9; ++j) blk[j] = p[j];
+        if (src.absent && x.stage) {          // the same bytes, same offsets, into the staging area
+            uint4 *sp = (uint4 *)(x.stage + (size_t)k * x.stage_stride + off);
+#pragma unroll
+            for (int j = 0; j < 9; ++j) sp[j] = blk[j];
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < 9; ++j) blk[j] = make_uint4(0, 0, 0, 0);
     }
-    if (sb) {          // the same bytes, same offsets, into the staging area
-        uint8_t *su = sb, *sg = sb + (size_t)x.I * rb;
+    const uint8_t *xb = s_q8x + b * Q8K_BYTES;
+    const float dx = *(const float *)xb;
+    const int16_t *bs = (const int16_t *)(xb + 4 + QK);
+    int32_t si = 0, mi = 0;
 #pragma unroll
-        for (int r = 0; r < R; ++r) {
-            const size_t off = (size_t)(row0 + r) * rb + (size_t)b * Q4K_BYTES;
-            if (u == 0) {
-                *(uint4 *)(sg + off) = hg[r];
-                *(uint4 *)(su + off) = hu[r];
-            }
-            *(uint4 *)(sg + off + 16 + 16 * u) = qg[r];
-            *(uint4 *)(su + off + 16 + 16 * u) = qu[r];
+    for (int j = 0; j < 4; ++j) {
+        int sl, ml, sh, mh;
+        q4k_sm(blk[0], 2 * j, sl, ml);
+        q4k_sm(blk[0], 2 * j + 1, sh, mh);
+        const uint4 *xw = (const uint4 *)(xb + 4 + 64 * j);
+        const uint4 xl0 = xw[0], xl1 = xw[1], xh0 = xw[2], xh1 = xw[3];
+        const uint32_t xl[8] = {xl0.x, xl0.y, xl0.z, xl0.w, xl1.x, xl1.y, xl1.z, xl1.w};
+        const uint32_t xh[8] = {xh0.x, xh0.y, xh0.z, xh0.w, xh1.x, xh1.y, xh1.z, xh1.w};
+        const uint4 q0 = blk[1 + 2 * j], q1 = blk[2 + 2 * j];
+        const uint32_t w[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+        int32_t dl = 0, dh = 0;
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+            dl = sdot4(w[t] & 0x0F0F0F0Fu, xl[t], dl);
+            dh = sdot4((w[t] >> 4) & 0x0F0F0F0Fu, xh[t], dh);
         }
+        si += sl * dl + sh * dh;
+        mi += ml * ((int)bs[4 * j] + (int)bs[4 * j + 1]) + mh * ((int)bs[4 * j + 2] + (int)bs[4 * j + 3]);
     }
+    const float d = h2f_dev((uint16_t)(blk[0].x & 0xffff)) * dx;
+    const float dm = h2f_dev((uint16_t)(blk[0].x >> 16)) * dx;
+    const float t = d * (float)si, m = dm * (float)mi;
+    // v = 0; v += t_0; v -= m_0; v += t_1; ...: lane b continues lane b - 1's sum
+    float acc = (0.0f + t) - m;
 #pragma unroll
-    for (int r = 0; r < R; ++r) {
-        float res[2];
-#pragma unroll
-        for (int m = 0; m < 2; ++m) {
-            const uint4 hdr = m == 0 ? hg[r] : hu[r];
-            const uint4 qs = m == 0 ? qg[r] : qu[r];
-            int32_t si, mi;
-            q4k_lane(hdr, qs, u, xlo, xhi, bslo, bshi, si, mi);
-            si += __shfl_xor(si, 1, 64);
-            mi += __shfl_xor(mi, 1, 64);
-            si += __shfl_xor(si, 2, 64);
-            mi += __shfl_xor(mi, 2, 64);
-            si += __shfl_xor(si, 4, 64);
-            mi += __shfl_xor(mi, 4, 64);
-            const float d = h2f_dev((uint16_t)(hdr.x & 0xffff)) * dx;
-            const float dm = h2f_dev((uint16_t)(hdr.x >> 16)) * dx;
-            const int ps = __builtin_bit_cast(int, d * (float)si), pm = __builtin_bit_cast(int, dm * (float)mi);
-            float v = 0.0f;
-#pragma unroll
-            for (int bb = 0; bb < 8; ++bb) {
-                v = v + __builtin_bit_cast(float, __builtin_amdgcn_readlane(ps, 8 * bb));
-                v = v - __builtin_bit_cast(float, __builtin_amdgcn_readlane(pm, 8 * bb));
-            }
-            res[m] = v;
-        }
-        if (lane == 0) {
-            const float gv = res[0], uv = res[1];
-            store_tagged(a.hx + (size_t)k * x.I + row0 + r, tagged(seq, gv / (1.0f + canon_expf(-gv)) * uv));
-        }
+    for (int sb = 1; sb < 8; ++sb) {
+        const float prev = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(acc), 0x111, 0xF, 0xF, false));
+        if (b == sb) acc = (prev + t) - m;                         // row_shr:1 -- the lane below
+    }
+    const float upv = __shfl(acc, lane + 32, 64);                  // row i's up sum, for the gate lanes
+    if (is_gate && b == 7) {
+        const float gv = acc;
+        store_tagged(a.hx + (size_t)k * x.I + row, tagged(seq, gv / (1.0f + canon_expf(-gv)) * upv));
     }
 }
 
@@ -1195,24 +1144,31 @@ __device__ void fused_combine(const FusedArgs &a, int c, uint32_t seq, uint8_t *
     const int row = c * 256 + (int)threadIdx.x;
     if (row >= x.H) return;
     const int kt = x.K + x.n_shared;
-    float y[17];
+    // every row word requested in each round (one round trip, not one per
+    // expert); a round re-reads only the words not yet valid
+    constexpr int MK = 17;
+    uint64_t v[MK];
+    uint32_t pending = (1u << kt) - 1u;
     int late = 0;
-    for (int k = 0; k < kt; ++k) {
-        const uint64_t *p = a.yx + (size_t)k * x.H + row;
-        const uint64_t t0 = wall_clock64();
-        uint64_t v;
-        for (;;) {
-            v = load_tagged(p);
-            if ((uint32_t)(v >> 32) == seq) break;
-            if (wall_clock64() - t0 > a.wait_ticks) {
-                late = 1;
-                break;
-            }
-            __builtin_amdgcn_s_sleep(1);
+    const uint64_t t0 = wall_clock64();
+    for (;;) {
+#pragma unroll
+        for (int k = 0; k < MK; ++k)
+            if (pending >> k & 1u) v[k] = load_tagged(a.yx + (size_t)k * x.H + row);
+#pragma unroll
+        for (int k = 0; k < MK; ++k)
+            if ((pending >> k & 1u) && (uint32_t)(v[k] >> 32) == seq) pending &= ~(1u << k);
+        if (!pending) break;
+        if (wall_clock64() - t0 > a.wait_ticks) {
+            late = 1;
+            break;
         }
-        y[k] = __uint_as_float((uint32_t)v);
+        __builtin_amdgcn_s_sleep(1);
     }
     if (late) fused_late(a, seq);
+    float y[MK];
+#pragma unroll
+    for (int k = 0; k < MK; ++k) y[k] = __uint_as_float((uint32_t)v[k]);
     float acc = __uint_as_float((uint32_t)s_rec[16]) * y[0];
     for (int k = 1; k < x.K; ++k) acc = acc + __uint_as_float((uint32_t)s_rec[16 + k]) * y[k];
     if (x.n_shared) acc = acc + y[x.K];
@@ -1225,7 +1181,7 @@ __global__ __launch_bounds__(256) void fused_kernel(FusedArgs a) {
     const uint32_t seq = *a.r.seq;
     const int E = a.r.E;
     const int kt = a.x.K + a.x.n_shared;
-    const int nG = kt * (a.x.I / (4 * FUSED_GU_ROWS)), nD = kt * (a.x.H / FUSED_DN_TILE);
+    const int nG = kt * (a.x.I / FUSED_GU_TILE), nD = kt * (a.x.H / FUSED_DN_TILE);
     int g = (int)blockIdx.x;
     if (g < E) {
         fused_router(a, g, seq, smem);
@@ -1395,7 +1351,7 @@ hipError_t launch_join(const JoinArgs &a, hipStream_t st) {
 
 hipError_t launch_fused(const FusedArgs &a, hipStream_t st, hipEvent_t e0, hipEvent_t e1) {
     const int kt = a.x.K + a.x.n_shared;
-    const unsigned n = (unsigned)(a.r.E + 1 + kt * (a.x.I / (4 * FUSED_GU_ROWS)) + kt * (a.x.H / FUSED_DN_TILE) +
+    const unsigned n = (unsigned)(a.r.E + 1 + kt * (a.x.I / FUSED_GU_TILE) + kt * (a.x.H / FUSED_DN_TILE) +
                                   (a.x.ypart ? 0 : a.x.H / 256));
     if (a.x.down_type == TYPE_Q6K) return launch(fused_kernel<TYPE_Q6K>, dim3(n), dim3(256), st, e0, e1, a);
     return launch(fused_kernel<TYPE_Q4K>, dim3(n), dim3(256), st, e0, e1, a);

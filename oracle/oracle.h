@@ -56,11 +56,11 @@
  *               quarters of Q = H/4 values; s_q: 64 lane partials p_j, p_j
  *               accumulated with fmaf (from 0) over i = 0..Q/256-1, c = 0..3
  *               of W[e][Q q + 256 i + 4 j + c] * x[...], then a butterfly
- *               p_j += p_{j^o} for o = 32,16,8,4,2,1.  (H a multiple of 1024.)
+ *               p_j += p_{j^o} for o = 1,2,4,8,16,32.  (H a multiple of 1024.)
  *   (+ bias[e], one fp32 add, when a steering bias is given)
  *   m         = max_e logit[e]
  *   ex[e]     = or_expf(logit[e] - m)
- *   s         = per 64-expert chunk a butterfly sum, chunks added in order.
+ *   s         = per 64-expert chunk the same butterfly sum, chunks added in order.
  *   p[e]      = ex[e] / s
  *   sel[e]    = p[e] + prior[e]           (only when a prior table is given;
  *               logit[e] + prior[e] in the logits-space variant)

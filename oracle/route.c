@@ -38,6 +38,16 @@ float or_expf(float x) {
     return p * s;
 }
 
+/* the canonical 64-lane butterfly: p_j += p_{j^o} for o = 1, 2, 4, 8, 16, 32 */
+static float canon_sum64(float p[64]) {
+    for (int o = 1; o <= 32; o <<= 1) {
+        float t[64];
+        for (int j = 0; j < 64; ++j) t[j] = p[j] + p[j ^ o];
+        memcpy(p, t, 64 * sizeof(float));
+    }
+    return p[0];
+}
+
 float or_row_logit(int H, const float *w, const float *x) {
     /* four quarters of the row, one per wavefront of the GPU's workgroup */
     const int Q = H / 4;
@@ -54,12 +64,7 @@ float or_row_logit(int H, const float *w, const float *x) {
             }
             p[j] = acc;
         }
-        for (int o = 32; o >= 1; o >>= 1) {
-            float t[64];
-            for (int j = 0; j < 64; ++j) t[j] = p[j] + p[j ^ o];
-            memcpy(p, t, sizeof p);
-        }
-        s[q] = p[0];
+        s[q] = canon_sum64(p);
     }
     return ((s[0] + s[1]) + s[2]) + s[3];
 }
@@ -74,12 +79,8 @@ static void softmax_topk(int E, int K, const float *logits, const float *prior, 
     for (int c = 0; c < E / 64; ++c) {
         float p[64];
         memcpy(p, ex + 64 * c, sizeof p);
-        for (int o = 32; o >= 1; o >>= 1) {
-            float q[64];
-            for (int j = 0; j < 64; ++j) q[j] = p[j] + p[j ^ o];
-            memcpy(p, q, sizeof p);
-        }
-        s = c == 0 ? p[0] : s + p[0];
+        const float cs = canon_sum64(p);
+        s = c == 0 ? cs : s + cs;
     }
     for (int e = 0; e < E; ++e) {
         probs[e] = ex[e] / s;
