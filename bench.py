@@ -1,42 +1,44 @@
 #!/usr/bin/env python3
 """Decode throughput of the MoE hot path on one MI355X.
 
-Default workload (stacked48, the one the headline metric is quoted on): 48 MoE
-layers of the Qwen3-30B-A3B shape -- hidden 2048, 128 experts, top-8, SwiGLU
-intermediate 768, gate/up Q4_K, down Q6_K in odd layers and Q4_K in even ones
--- with a 56-slot HBM cache per layer over a pinned host store holding all 128
-experts of every layer.  Routing is steered to a per-layer Zipf(1.1) popularity
-with reuse p = 0.6; window (second-miss) admission, batched table writes, max 2
+The line's `value` is configuration 2 (stacked48): 48 MoE layers of the
+Qwen3-30B-A3B shape -- hidden 2048, 128 experts, top-8, SwiGLU intermediate
+768, gate/up Q4_K, down Q6_K in odd layers and Q4_K in even ones -- with a
+56-slot HBM cache per layer over a pinned host store holding all 128 experts
+of every layer.  Routing is steered to a per-layer Zipf(1.1) popularity with
+reuse p = 0.6; window (second-miss) admission, batched table writes, max 2
 inserts per layer per step.  A step is one batch-1 decode token through all 48
-layers (router, experts from HBM slots or the pinned store, combine, routed ids
-back, cache step with uploads on the side stream), replayed as one HIP graph.
-The synthetic sequence is 512 tokens: --warmup tokens warm the cache, the next
---steps are timed.  Absent experts are served by the host CPU (14 threads on a
-16-CPU host, every absent expert of a layer by default, --share num/den for a
-part of them; --sidecar 0 for the GPU-only path) while the GPU runs the
-resident ones.
+layers (each layer one fused launch: router, selection, experts from HBM
+slots, combine; the routed ids back, cache step with uploads on the side
+stream), replayed as one HIP graph.  Experts absent from the slots are
+computed by the host CPU (14 threads; the reference's sidecar) while the GPU
+runs the resident ones; `gpu_only` is the same decode with the GPU reading
+absent experts from the pinned store over PCIe.
 
---workload prefill48 [--batch 512|64]: batched MoE layers -- a chunk of
-tokens (bf16 activations, uniform router logits) through 48 layers whose 128
-experts all sit in HBM: route, dispatch, grouped up/gate + SwiGLU and down on
-the matrix cores, combine, one HIP graph per chunk.
+The synthetic sequence is 512 tokens.  --warmup tokens warm the cache and the
+next --steps are timed for `value`; the run then continues to token 511 and
+`steady` reports tokens 64..511 (the cache full: evictions and admission
+denials in every step).  Beside it, in the same line:
 
---workload prior48: the single-layer shape (N(0,0.02) router, no steering)
-stacked 48 deep over the same cache, decoded at delta = 0, at delta = 0.01 on
-the selection probabilities (the reference's LLAMA_MOE_CACHE_PRIOR) and at
-delta = 0.01 on the logits; reports the change in hit rate and the relative L2
-of the block outputs against delta = 0, with every routed id of every run
-replayed through the oracle.
+  config1  one layer, all 128 experts resident, 256 steps: GB/s and the
+           fraction of 8 TB/s of the fused layer launch on 21,233,664 expert
+           bytes + 1 MiB of router per step
+  config3  the single-layer shape stacked 48 deep, 512 tokens at delta = 0,
+           0.01 on probabilities and 0.01 on logits: change in hit rate,
+           relative L2 of the block outputs against delta = 0
+  config4  batched layers (48, all experts in HBM): a 512-token prefill chunk
+           and batch-64 decode on the matrix cores, GB/s and MFMA utilisation
+  config5  40 layers x 256 experts + 1 shared, I 512, 96 slots, delta 0.01:
+           1024 tokens at batch 1, then 128 at batch 16
+  cpu_baseline  the host chain (AVX-512 VNNI integer dots, the same numerics)
+           swept over {1, 4, 8, all} threads: us per expert, per layer of 8,
+           tok/s of configuration 2 with every expert on the CPU
 
---workload wide40: the larger-expert-count shape -- 40 layers of 256 routed
-experts + 1 always-on shared expert (in HBM), intermediate 512, Q4_K/Q6_K mix,
-96 slots/layer, delta = 0.01, Zipf(1.0) reuse 0.5 -- decoded 1024 tokens at
-batch 1 (--warmup 64 + --steps 960), then 128 tokens at batch 16 through the
-batched kernels on the same cache; every routed id of both phases is replayed
-through the oracle.
+Other --workload values print their own line: prefill48, prior48, wide40,
+residual48 (router lookahead + just-in-time streaming), single1.
 
-Prints ONE JSON line (N = 1).  Inputs are resident before timing: weights in
-the pinned store / HBM slots, activations and steering on the device.
+Inputs are resident before timing: weights in the pinned store / HBM slots,
+activations and steering on the device.
 """
 import argparse
 import json
@@ -65,7 +67,7 @@ class Workload:
     are decoded one at a time, the `T - T1` after them in batches."""
 
     def __init__(self, args, steer, n_experts=E, inter=I, shared=False, zipf_s=1.1, reuse=0.6, slots=None,
-                 batch_tokens=0):
+                 batch_tokens=0, T=None):
         import torch
         import moe_prefetch
         from moe_prefetch import _lib
@@ -78,7 +80,7 @@ class Workload:
         self.slots = args.slots if slots is None else slots
         self.NL = NL = args.layers
         self.T1 = args.warmup + args.steps
-        self.T = T = self.T1 + batch_tokens
+        self.T = T = max(self.T1 + batch_tokens, T or 0)
         self.dts = down_types(NL)
         self.eb = [L.moe_expert_bytes(H, inter, dt) for dt in self.dts]
         self.zipf_targets, self.steering_bias, self.KIND_X = zipf_targets, steering_bias, KIND_X
@@ -184,14 +186,35 @@ class Workload:
         log(f"[bench] timed {self.args.steps} tokens in {elapsed:.2f}s")
         return elapsed, s0, s1, ids_log, kept, frames
 
-    def kernel_pass(self, cache):
+    def tokens(self, cache, t0, t1, ids_log, keep=(), kept=None, all_out=None, x=None, steer=True):
+        """Decode tokens [t0, t1) one at a time (graph replay); returns the
+        elapsed seconds, synchronised on both sides."""
+        torch = self.torch
+        out = torch.empty((self.NL, H), dtype=torch.float32, device=self.dev)
+        xs = self.x if x is None else x
+        bias = self.bias if steer else None
+        torch.cuda.synchronize()
+        tic = time.perf_counter()
+        for t in range(t0, t1):
+            dst = all_out[t] if all_out is not None else out
+            cache.decode_token(xs[t], dst, bias=None if bias is None else bias[t], stream=self.stream,
+                               ids_out=ids_log[t])
+            if t in keep:
+                kept[t] = dst.cpu().numpy().copy()
+        torch.cuda.synchronize()
+        return time.perf_counter() - tic
+
+    def kernel_pass(self, cache, split=2, keep_serving=False):
         """Per-kernel durations: the same cache continues for --kernel-steps more
-        tokens launched eagerly (HIP events cannot be read from graph nodes),
-        resident and absent experts as separate launches."""
+        tokens launched eagerly (HIP events cannot be read from graph nodes).
+        split 2: resident and absent experts as separate launches, GPU only;
+        split 0 with keep_serving: the fused layer launch as the decode runs it
+        (absent experts on the host CPU)."""
         torch, L, _lib = self.torch, self.L, self._lib
-        n = min(self.args.kernel_steps, self.args.steps)
-        cache.set_sidecar(0)                    # GPU kernels only, resident and absent experts apart
-        cache.set_decode_path(split=2, graph=False)
+        n = min(self.args.kernel_steps, max(self.args.steps, 16))
+        if not keep_serving:
+            cache.set_sidecar(0)                # GPU kernels only
+        cache.set_decode_path(split=split, graph=False)
         cache.set_timing(True)
         xs = torch.empty((n, self.NL, H), dtype=torch.float32, device=self.dev)
         _lib.check(L.moe_synth_vec(self.args.seed, self.KIND_X, self.T, n, 0, self.NL, H, 1.0, xs.data_ptr(),
@@ -241,7 +264,7 @@ class Workload:
         log(f"[bench] timed {n} batched tokens in {elapsed:.3f}s")
         return elapsed, per, s0, s1, ids.transpose(0, 2, 1, 3).reshape(n, self.NL, K), kept
 
-    def check(self, ids_log, kept, frames, s1, knobs, every=False, batch=1):
+    def check(self, ids_log, kept, frames, s1, knobs, every=False, batch=1, steer=True, T=None, heat=None):
         """Full-size properties against the oracle, outside every timed region:
         routed ids (every token and layer when `every` or a prior is on, else
         one layer per token), frames, counters, and the kept outputs.  Tokens
@@ -254,13 +277,16 @@ class Workload:
         logits_space = knobs.get("prior_space", "probs") == "logits"
         oc = O.Cache([self.slots] * self.NL, n_experts=self.E, admit=knobs.get("admit", "off"), batch_tables=True,
                      cache_prior=knobs.get("cache_prior", 0.0))
+        if heat:
+            oc.heat_file(heat)
         Wh, xh = self.W.cpu().numpy(), self.x.cpu().numpy()
-        bh = None if self.bias is None else self.bias.cpu().numpy()
+        bh = None if (self.bias is None or not steer) else self.bias.cpu().numpy()
         stores = [np.ctypeslib.as_array((ctypes.c_uint8 * (self.E * self.eb[l])).from_address(self.stores[l]))
                   for l in range(self.NL)]
         bad, worst, checked = 0, 0.0, 0
         t = 0
-        while t < self.T:
+        T = self.T if T is None else T
+        while t < T:
             n = 1 if t < self.T1 else batch
             for l in range(self.NL):
                 tbl, prior = oc.table(l)
@@ -286,24 +312,66 @@ class Workload:
         oc.close()
         return res
 
-    def cpu_baseline(self):
-        cores = min(len(os.sched_getaffinity(0)), 16)
+    def cpu_baseline(self, seconds):
+        """The host expert chain (moe_cpu_experts: Q8_K activations, AVX-512
+        VNNI integer dots, fp32 steps in the CPU chain's order -- the numerics
+        of the reference's CPU path, experiments/x2_cpu_expert_cost.cpp:115-156)
+        timed as that experiment times it: a tour over experts of the pinned
+        store (cold in the CPU's caches), one expert per call and a layer's 8
+        per call, for 1, 4, 8 and all threads (p50 of the calls)."""
+        import ctypes
+        import numpy as np
         from oracle import oracle as O
-        Wh, xh = self.W.cpu().numpy(), self.x.cpu().numpy()
-        bh = None if self.bias is None else self.bias.cpu().numpy()
-        log(f"[bench] CPU baseline: oracle decode on {cores} threads for ~{self.args.cpu_seconds}s")
-        t0 = time.perf_counter()
-        done = 0
-        while done < self.T and (time.perf_counter() - t0) < self.args.cpu_seconds:
-            for l in range(self.NL):
-                rids, rw, _, _ = O.route(Wh[l], xh[done, l], K, bias=None if bh is None else bh[done, l])
-                self.oracle_layer(self.stores, l, rids, rw, xh[done, l], cores)
-            done += 1
-        el = time.perf_counter() - t0
-        return {"value": round(done / el, 3), "unit": "tok/s", "cores": cores, "kind": "port",
-                "sample": f"{done} tokens x {self.NL} layers of the same workload, every routed "
-                          f"{'and shared ' if self.shared[0] is not None else ''}expert computed on the host from "
-                          f"the pinned store (Q8_K activations, integer dots, OpenMP over rows), {el:.1f}s"}
+        L = self.L
+        nproc = os.cpu_count() or 1
+        usable = len(os.sched_getaffinity(0))
+        phys = set()
+        for c in os.sched_getaffinity(0):
+            try:
+                base = f"/sys/devices/system/cpu/cpu{c}/topology/"
+                phys.add((open(base + "physical_package_id").read().strip(), open(base + "core_id").read().strip()))
+            except OSError:
+                phys.add((c,))
+        threads = sorted({1, 4, 8, usable} & set(range(1, usable + 1)) | {usable})
+        rng = np.random.default_rng(self.args.seed)
+        # Q8_K of one activation (any: the arithmetic per byte does not depend on it)
+        q8 = O.quant_q8k(self.x[0, 0].cpu().numpy())
+        tour = [(int(l), int(e)) for l, e in zip(rng.integers(0, self.NL, 4096), rng.integers(0, self.E, 4096))]
+        budget = seconds / (2 * len(threads))
+        rows, pos = [], 0
+        log(f"[bench] CPU baseline: host chain, threads {threads}, ~{seconds:.0f}s")
+        for th in threads:
+            for m in (1, 8):
+                # one warm-up call starts the thread team
+                times = []
+                tic = time.perf_counter()
+                while time.perf_counter() - tic < budget or len(times) < 3:
+                    l = tour[pos % len(tour)][0]
+                    ptrs = (ctypes.c_void_p * m)(*[self.stores[l] + tour[(pos + j) % len(tour)][1] * self.eb[l]
+                                                   for j in range(m)])
+                    pos += m
+                    rows_out = np.empty((m, H), np.float32)
+                    t0 = time.perf_counter()
+                    self._lib.check(L.moe_cpu_experts(ptrs, m, q8.ctypes.data, H, self.I, self.dts[l],
+                                                      rows_out.ctypes.data, th, 0), "cpu experts")
+                    times.append(time.perf_counter() - t0)
+                t = np.array(times[1:]) * 1e6
+                rows.append({"threads": th, "experts_per_call": m, "us_p50": round(float(np.median(t)), 1),
+                             "us_p90": round(float(np.percentile(t, 90)), 1), "calls": len(t)})
+        best = min((r for r in rows if r["experts_per_call"] == 8), key=lambda r: r["us_p50"])
+        one = min((r for r in rows if r["experts_per_call"] == 1), key=lambda r: r["us_p50"])
+        # a token through the stacked decode with every routed expert on the CPU: K experts per layer
+        tok_s = 1e6 / (self.NL * best["us_p50"])
+        return {"value": round(tok_s, 2), "unit": "tok/s", "cores": best["threads"], "kind": "port",
+                "sample": f"{sum(r['calls'] for r in rows)} host-chain calls over a tour of the pinned store's "
+                          f"experts ({len(threads)} thread counts x 1 and 8 experts per call, ~{seconds:.0f}s); "
+                          f"tok/s = 1 / ({self.NL} layers x the best 8-expert call); the router is not included",
+                "nproc": nproc, "usable_cpus": usable, "physical_cores": len(phys),
+                "us_per_expert": one["us_p50"], "us_per_expert_threads": one["threads"],
+                "us_per_layer_k8": best["us_p50"], "us_per_layer_k8_threads": best["threads"],
+                "sweep": rows,
+                "engine": "moe_cpu_experts (the library's host chain: AVX-512 VNNI dots when present; results "
+                          "equal the oracle's bit for bit)" + ("" if L.moe_cpu_has_vnni() else ", portable path")}
 
     def close(self):
         for p in self.stores:
@@ -391,6 +459,201 @@ def kernel_report(kt, n_tok, steps, s0, s1):
     }
 
 
+def fused_report(kt, n_tok):
+    """Roofline of the fused layer launch (router rows + the resident experts'
+    bytes it reads, over its dispatch-stamped duration)."""
+    n = max(kt["n_layers"], 1)
+    ms, hb, pb = kt["layer_ms"], kt["layer_hbm_bytes"], kt["layer_host_bytes"]
+    achieved = hb / (ms * 1e-3) / 1e9 if ms > 0 else 0.0
+    traffic, tsrc = None, None
+    tpath = os.path.join(ROOT, "profiles", "traffic.json")
+    if os.path.exists(tpath):
+        with open(tpath) as f:
+            tr = json.load(f).get("fused_layer")
+        if tr:
+            ratio = (tr["hbm_read_bytes_per_launch"] + tr["hbm_write_bytes_per_launch"]) / \
+                tr["algorithmic_bytes_per_launch"]
+            traffic = round(ratio * hb / n)
+            tsrc = ("this run's bytes per launch x the (FETCH_SIZE + WRITE_SIZE) / algorithmic ratio of the "
+                    "committed rocprofv3 PMC run (profiles/traffic.json), not counters of this run")
+    return {
+        "kernels_ms_per_token": {"fused_layer": round(ms / max(n_tok, 1), 4)},
+        "kernel_timing": f"HIP events stamped by each dispatch (hipExtLaunchKernelGGL) on its stream, {n_tok} "
+                         f"eager tokens after the timed ones on the same cache and serving path (graph replay "
+                         f"cannot carry per-kernel events)",
+        "roofline": {"bound": "hbm", "kernel": "fused_layer", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
+                     "traffic_source": tsrc, "bytes_per_launch": round(hb / n), "avg_launch_us": round(ms / n * 1e3, 2),
+                     "launches": n,
+                     "bytes": "router rows (1 MiB) + the resident routed experts' weights the launch reads "
+                              "(2,654,208 B per expert with Q4_K down, 3,059,712 with Q6_K); absent experts are "
+                              "computed by the host and not read"},
+        "pcie_bytes_per_launch": round(pb / n),
+    }
+
+
+def window(s0, s1, steps, t0_s=None):
+    """Cache and throughput figures between two stats snapshots."""
+    seen = (s1["n_hit"] - s0["n_hit"]) + (s1["n_miss"] - s0["n_miss"])
+    return {"hit_rate": round((s1["n_hit"] - s0["n_hit"]) / max(seen, 1), 4),
+            "missed_per_token": round((s1["n_miss"] - s0["n_miss"]) / steps, 2),
+            "uploaded_per_token": round((s1["n_scheduled"] - s0["n_scheduled"]) / steps, 2),
+            "evicted_per_token": round((s1["n_evicted"] - s0["n_evicted"]) / steps, 2),
+            "admit_denied_per_token": round((s1["n_admit_denied"] - s0["n_admit_denied"]) / steps, 2),
+            "cpu_served_per_token": round((s1["n_cpu_served"] - s0["n_cpu_served"]) / steps, 2)}
+
+
+def run_default(args):
+    """Configuration 2 as the line's value, steady state, GPU-only, the
+    oracle check, the fused launch's roofline, the CPU baseline, then
+    configurations 3, 1, 4 and 5 as keys."""
+    import numpy as np
+    T_SEQ, STEADY0 = 512, 64
+    wl = Workload(args, steer=True, T=T_SEQ)
+    T = wl.T
+    W, Kt = args.warmup, args.steps
+    knobs = dict(admit=args.admit)
+    cache = wl.cache(**knobs)
+    cache.set_decode_path(split=args.path, graph=True)
+    sidecar_setup(args, cache)
+    ids_log = np.empty((T, wl.NL, K), np.int32)
+    kept = {}
+    keep = {W, W + Kt - 1, T - 1}
+    snaps = {}
+    wl.tokens(cache, 0, W, ids_log, keep, kept)
+    snaps[W] = cache.stats()
+    log(f"[bench] warmup {W} tokens done; timing {Kt}")
+    el = wl.tokens(cache, W, W + Kt, ids_log, keep, kept)
+    snaps[W + Kt] = cache.stats()
+    log(f"[bench] timed {Kt} tokens in {el:.3f}s")
+    # the rest of the 512-token sequence; tokens 64..511 are the steady window
+    s_lo = max(STEADY0, W + Kt)
+    if s_lo > W + Kt:
+        wl.tokens(cache, W + Kt, s_lo, ids_log, keep, kept)
+    snaps[s_lo] = cache.stats()
+    el_s = wl.tokens(cache, s_lo, T, ids_log, keep, kept) if T > s_lo else 0.0
+    snaps[T] = cache.stats()
+    frames = [cache.frame(l) for l in range(wl.NL)]
+    sc = args.sidecar > 0
+    result = {
+        "metric": METRIC, "value": round(Kt / el, 2), "unit": "tok/s", "n_gpus": 1,
+        "steps": Kt, "warmup": W, "ms_per_step": round(1e3 * el / Kt, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "q4_k/q6_k x q8_k int8-dot, fp32 scale (router fp32)",
+        "data": "synthetic (seeded N(0,0.02) experts quantized to Q4_K/Q6_K, N(0,1) activations)",
+        "config": {"workload": f"stacked{wl.NL} (configuration 2): {wl.NL} layers x {E} experts, H {H}, I {I}, "
+                               f"top-{K}, {wl.slots} HBM slots/layer over a pinned store of all experts, Q6_K down "
+                               f"in odd layers, Zipf(1.1) reuse 0.6, admission {args.admit}, batched tables; "
+                               + (f"experts absent from the slots computed by the host CPU ({args.sidecar} threads, "
+                                  f"share {args.share}), resident ones by the GPU" if sc else
+                                  "absent experts read by the GPU from the pinned store over PCIe")
+                               + f"; tokens {W}..{W + Kt - 1} of a {T}-token sequence timed ({W} warmup, cache "
+                                 f"still filling)",
+                   "batch": 1, "layers": wl.NL, "slots": wl.slots},
+        "decode_path": {0: "fused layer launch", 1: "fork/join", 2: "serial", 3: "unfused"}[args.path]
+                       + ", HIP graph per token",
+        "cache": window(snaps[W], snaps[W + Kt], Kt),
+    }
+    if T > s_lo:
+        result["steady"] = {"tokens": f"{s_lo}..{T - 1}", "value": round((T - s_lo) / el_s, 2), "unit": "tok/s",
+                            "ms_per_token": round(1e3 * el_s / (T - s_lo), 4), **window(snaps[s_lo], snaps[T], T - s_lo)}
+    result["sidecar"] = sidecar_report(args, snaps[W], snaps[W + Kt], Kt,
+                                       cache.sidecar_log() if sc else None)
+    kt, n_kt = wl.kernel_pass(cache, split=args.path, keep_serving=sc)
+    result.update(fused_report(kt, n_kt) if args.path == 0 else kernel_report(kt, n_kt, Kt, snaps[W], snaps[W + Kt]))
+    result["roofline"]["size_matched"] = size_matched(result["roofline"])
+    cache.close()
+    if not args.no_check:
+        log("[bench] checking the 512-token run against the oracle (outside the timed regions)")
+        result["check"] = wl.check(ids_log, kept, frames, snaps[T], knobs)
+        result["check"]["tokens"] = T
+        log(f"[bench] check: {result['check']}")
+    if sc and not args.no_gpu_only:
+        log("[bench] the same decode with the GPU alone serving absent experts")
+        c2 = wl.cache(**knobs)
+        c2.set_decode_path(split=args.path, graph=True)
+        ids2 = np.empty_like(ids_log)
+        wl.tokens(c2, 0, W, ids2)
+        e1 = wl.tokens(c2, W, W + Kt, ids2)
+        if s_lo > W + Kt:
+            wl.tokens(c2, W + Kt, s_lo, ids2)
+        g0 = c2.stats()
+        e2 = wl.tokens(c2, s_lo, T, ids2) if T > s_lo else 0.0
+        g1 = c2.stats()
+        c2.close()
+        result["gpu_only"] = {"value": round(Kt / e1, 2), "unit": "tok/s",
+                              "steady": {"tokens": f"{s_lo}..{T - 1}",
+                                         "value": round((T - s_lo) / e2, 2) if e2 else None, **window(g0, g1, T - s_lo)}
+                              if T > s_lo else None,
+                              "ids_equal": bool((ids2 == ids_log).all()),
+                              "path": "absent experts read by the fused launch from the pinned store over PCIe "
+                                      "(and staged, so their uploads are HBM copies)"}
+    if not args.no_cpu:
+        result["cpu_baseline"] = wl.cpu_baseline(args.cpu_seconds)
+    if not args.no_extra:
+        result["config3"] = config3(args, wl)
+    wl.close()
+    del wl
+    if not args.no_extra:
+        result["config1"] = config1(args)
+        result["config4"] = config4(args)
+        result["config5"] = config5(args)
+    return result
+
+
+def _sub(args, **kw):
+    a = argparse.Namespace(**vars(args))
+    for k, v in kw.items():
+        setattr(a, k, v)
+    return a
+
+
+def config3(args, wl):
+    """Cache-aware routing on the single-layer shape stacked 48 deep (no
+    steering), 512 tokens: delta 0, 0.01 on probabilities, 0.01 on logits."""
+    r = run_prior(_sub(args, warmup=64, steps=448), wl, steer=False)
+    runs = r["runs"]
+    out = {"workload": "single-layer shape (N(0,0.02) router, no steering) stacked 48 deep over 56 slots, "
+                       "512 tokens; hit rate over tokens 64..511",
+           "delta0_hit_rate": runs["delta0"]["cache"]["hit_rate"]}
+    for name in ("delta0.01", "delta0.01_logits"):
+        out[name] = {"hit_rate": runs[name]["cache"]["hit_rate"], "delta_hit": runs[name]["hit_rate_change"],
+                     "rel_l2_vs_delta0": round(runs[name]["rel_l2_vs_delta0"], 4), "tok_s": runs[name]["tok_s"]}
+    out["check"] = {n: runs[n].get("check") for n in runs}
+    return out
+
+
+def config1(args):
+    r = run_single(_sub(args, warmup=8, steps=256))
+    keep = ("value", "unit", "config", "roofline", "step", "check")
+    return {k: r[k] for k in keep if k in r}
+
+
+def config4(args):
+    out = {}
+    for B in (512, 64):
+        r = run_prefill(_sub(args, layers=48, batch=B, warmup=2, steps=10, no_cpu=True))
+        out[f"batch{B}"] = {"tok_s": r["value"], "ms_per_chunk": r["ms_per_step"], "roofline": r["roofline"],
+                            "mfma": r["mfma"], "hbm": r["hbm"], "check": r.get("check")}
+    out["workload"] = ("48 batched layers, all 128 experts in HBM; 512-token prefill chunk and 64-token decode batch "
+                       "(bf16 N(0,1) activations, uniform router logits, top-8): route, dispatch, grouped up/gate + "
+                       "SwiGLU and down on fp16 matrix cores (exact integer products), combine; HIP graph per chunk")
+    return out
+
+
+def config5(args):
+    a = _sub(args, layers=40, slots=96, warmup=64, steps=960, batch=16, batch_tokens=128)
+    wl = Workload(a, steer=True, n_experts=256, inter=512, shared=True, zipf_s=1.0, reuse=0.5,
+                  batch_tokens=a.batch_tokens)
+    try:
+        r = run_wide(a, wl)
+    finally:
+        wl.close()
+    return {"workload": r["config"]["workload"], "batch1": {"tok_s": r["value"], "cache": r["cache"]},
+            "batch16": r["batch16"], "check": r.get("check"),
+            "roofline": r.get("roofline")}
+
+
 def sidecar_setup(args, cache):
     if args.sidecar > 0:
         num, den = (int(v) for v in args.share.split("/"))
@@ -415,50 +678,6 @@ def sidecar_report(args, s0, s1, steps, log_rows=None):
             "host_cpu_ms_per_token": round((s1["sidecar_cpu_us"] - s0["sidecar_cpu_us"]) / 1e3 / steps, 4),
             "path": "absent experts assigned to the host computed by its CPU team (AVX-512 VNNI integer dots) "
                     "from the pinned store while the GPU runs the rest; posted / joined through mapped memory"}
-
-
-def run_stacked(args, wl):
-    T = args.warmup + args.steps
-    knobs = dict(admit=args.admit)
-    cache = wl.cache(**knobs)
-    cache.set_decode_path(split=args.path, graph=True)
-    sidecar_setup(args, cache)
-    elapsed, s0, s1, ids_log, kept, frames = wl.decode(cache, keep={args.warmup, T - 1})
-    result = {
-        "metric": METRIC, "value": round(args.steps / elapsed, 2), "unit": "tok/s", "n_gpus": 1,
-        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(1e3 * elapsed / args.steps, 4),
-        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
-        "dtype": "q4_k/q6_k x q8_k int8-dot, fp32 scale (router fp32)",
-        "data": "synthetic (seeded N(0,0.02) experts quantized to Q4_K/Q6_K, N(0,1) activations)",
-        "config": {"workload": f"stacked{args.layers}: {args.layers} layers x {E} experts, H {H}, I {I}, top-{K}, "
-                               f"{args.slots} HBM slots/layer over a pinned store, Q6_K down in odd layers, "
-                               f"Zipf(1.1) reuse 0.6, admission {args.admit}, batched tables, "
-                               f"{T} tokens ({args.warmup} warmup)",
-                   "batch": 1, "layers": args.layers, "slots": args.slots},
-        "decode_path": {0: "fused", 1: "fork/join", 2: "serial"}[args.path] + " expert launches, HIP graph per token",
-        "cache": cache_summary(s0, s1, args.steps),
-        "sidecar": sidecar_report(args, s0, s1, args.steps, cache.sidecar_log() if args.sidecar > 0 else None),
-    }
-    result.update(kernel_report(*wl.kernel_pass(cache), args.steps, s0, s1))
-    result["roofline"]["size_matched"] = size_matched(result["roofline"])
-    if not args.no_check:
-        log("[bench] checking the full-size run against the oracle (outside the timed region)")
-        result["check"] = wl.check(ids_log, kept, frames, s1, knobs)
-        log(f"[bench] check: {result['check']}")
-    cache.close()
-    if not args.no_lookahead:
-        result["lookahead"] = lookahead_compare(args, wl)
-    if args.sidecar > 0 and not args.no_gpu_only:
-        log("[bench] the same decode with the GPU alone serving absent experts")
-        c2 = wl.cache(**knobs)
-        c2.set_decode_path(split=args.path, graph=True)
-        el2, g0, g1, ids2, _, _ = wl.decode(c2)
-        c2.close()
-        result["gpu_only"] = {"value": round(args.steps / el2, 2), "unit": "tok/s",
-                              "ids_equal": bool((ids2 == ids_log).all()),
-                              "path": "absent experts read by the kernels from the pinned store over PCIe, "
-                                      "staged uploads"}
-    return result
 
 
 def lookahead_compare(args, wl):
@@ -558,23 +777,35 @@ def run_residual(args, wl):
     }
 
 
-def run_prior(args, wl):
+def run_prior(args, wl, steer=False):
+    """The three cache-prior runs over tokens [0, warmup + steps) of wl (no
+    steering): delta 0, delta 0.01 on the selection probabilities (the
+    reference's LLAMA_MOE_CACHE_PRIOR), delta 0.01 on the logits; each id of
+    each run replayed through the oracle with the oracle's own tables."""
+    import numpy as np
     torch = wl.torch
-    T = args.warmup + args.steps
+    W, T = args.warmup, args.warmup + args.steps
     runs, outs = {}, {}
     for name, knobs in (("delta0", dict(admit=args.admit)),
                         ("delta0.01", dict(admit=args.admit, cache_prior=0.01)),
                         ("delta0.01_logits", dict(admit=args.admit, cache_prior=0.01, prior_space="logits"))):
-        log(f"[bench] run {name}")
+        log(f"[bench] cache prior run {name}")
         cache = wl.cache(**knobs)
         cache.set_decode_path(split=args.path, graph=True)
-        all_out = torch.empty((T, args.layers, H), dtype=torch.float32, device=wl.dev)
-        elapsed, s0, s1, ids_log, kept, frames = wl.decode(cache, keep={T - 1}, all_out=all_out)
+        sidecar_setup(args, cache)
+        all_out = torch.empty((T, wl.NL, H), dtype=torch.float32, device=wl.dev)
+        ids_log = np.empty((T, wl.NL, K), np.int32)
+        kept = {}
+        wl.tokens(cache, 0, W, ids_log, all_out=all_out, steer=steer)
+        s0 = cache.stats()
+        elapsed = wl.tokens(cache, W, T, ids_log, keep={T - 1}, kept=kept, all_out=all_out, steer=steer)
+        s1 = cache.stats()
+        frames = [cache.frame(l) for l in range(wl.NL)]
         r = {"tok_s": round(args.steps / elapsed, 2), "cache": cache_summary(s0, s1, args.steps),
              "hit_rate_all_tokens": round(s1["n_hit"] / max(s1["n_hit"] + s1["n_miss"], 1), 4)}
         if not args.no_check:
             log(f"[bench] {name}: replaying every routed id through the oracle")
-            r["check"] = wl.check(ids_log, kept, frames, s1, knobs, every=True)
+            r["check"] = wl.check(ids_log, kept, frames, s1, knobs, every=True, steer=steer, T=T)
             log(f"[bench] check: {r['check']}")
         runs[name], outs[name] = r, all_out
         cache.close()
@@ -588,12 +819,64 @@ def run_prior(args, wl):
         "warmup": args.warmup, "ms_per_step": round(1e3 / main_run["tok_s"], 4), "higher_is_better": True,
         "scaling": "weak", "vs_baseline": None, "dtype": "q4_k/q6_k x q8_k int8-dot, fp32 scale (router fp32)",
         "data": "synthetic (seeded N(0,0.02) router and experts, N(0,1) activations, no steering)",
-        "config": {"workload": f"prior{args.layers}: single-layer shape stacked {args.layers} deep, {args.slots} "
+        "config": {"workload": f"prior{wl.NL}: single-layer shape stacked {wl.NL} deep, {wl.slots} "
                                f"slots/layer, admission {args.admit}, batched tables, {T} tokens ({args.warmup} "
                                f"warmup); delta 0, 0.01 on probabilities (value), 0.01 on logits",
-                   "batch": 1, "layers": args.layers, "slots": args.slots, "cache_prior": 0.01},
+                   "batch": 1, "layers": wl.NL, "slots": wl.slots, "cache_prior": 0.01},
         "runs": runs,
     }
+
+
+def run_single(args):
+    """Configuration 1: one layer with all 128 experts resident (a heat-file
+    warm start puts every expert in a slot), independent batch-1 decode steps
+    on N(0,1) inputs (router N(0,0.02), no steering), GPU only.  The roofline
+    is the fused layer launch's: 21,233,664 expert bytes (8 Q4_K experts) +
+    1 MiB of router per step over its dispatch-stamped duration."""
+    import tempfile
+    import numpy as np
+    a = _sub(args, layers=1, slots=E, sidecar=0)
+    wl = Workload(a, steer=False)
+    try:
+        cache = wl.cache(admit="window")
+        # every expert with a count (halved on load, so >= 2), hottest first
+        with tempfile.NamedTemporaryFile("w", suffix=".heat", delete=False) as f:
+            f.write(f"moe-heat 1 1 {E}\n" + "".join(f"0 {e} {2 * (E - e)}\n" for e in range(E)))
+            hp = f.name
+        n_rec, n_placed = cache.heat_file(hp)
+        if n_placed != E:
+            raise RuntimeError(f"warm start placed {n_placed} of {E} experts")
+        cache.set_decode_path(split=0, graph=True)
+        T, W = wl.T, a.warmup
+        ids_log = np.empty((T, 1, K), np.int32)
+        kept = {}
+        wl.tokens(cache, 0, W, ids_log)
+        s0 = cache.stats()
+        el = wl.tokens(cache, W, T, ids_log, keep={W, T - 1}, kept=kept)
+        s1 = cache.stats()
+        frames = [cache.frame(0)]
+        kt, n_kt = wl.kernel_pass(cache, split=0)
+        rep = fused_report(kt, n_kt)
+        n = max(kt["n_layers"], 1)
+        us = kt["layer_ms"] / n * 1e3
+        expert_bytes = K * wl.eb[0]
+        out = {"value": round(a.steps / el, 1), "unit": "steps/s",
+               "config": {"workload": f"one layer x {E} experts all resident, H {H}, I {I}, top-{K}, Q4_K gate/up/down, "
+                                      f"router N(0,0.02), x N(0,1); {a.steps} independent steps timed ({W} warmup)"},
+               "step": {"us_wall": round(1e6 * el / a.steps, 2), "hit_rate": window(s0, s1, a.steps)["hit_rate"],
+                        "what": "decode_token per step: copies, graph launch, routed ids back, cache step"},
+               "roofline": {**rep["roofline"], "expert_bytes_per_step": expert_bytes,
+                            "expert_gbs": round(expert_bytes / (us * 1e-6) / 1e9, 1),
+                            "expert_frac": round(expert_bytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}}
+        out["roofline"]["size_matched"] = size_matched(out["roofline"])
+        cache.close()
+        if not args.no_check:
+            out["check"] = wl.check(ids_log, kept, frames, s1, dict(admit="window"), every=True, steer=False,
+                                    heat=hp)
+        os.unlink(hp)
+        return out
+    finally:
+        wl.close()
 
 
 def run_wide(args, wl):
@@ -826,7 +1109,7 @@ def main():
     ap.add_argument("--steps", type=int, default=None, help="timed batch-1 tokens (448; wide40: 960)")
     ap.add_argument("--warmup", type=int, default=64)
     ap.add_argument("--workload", default="stacked48",
-                    choices=["stacked48", "prior48", "prefill48", "wide40", "residual48"])
+                    choices=["stacked48", "prior48", "prefill48", "wide40", "residual48", "single1"])
     ap.add_argument("--batch", type=int, default=None, help="tokens per chunk (prefill48: 512) or per batched "
                                                             "decode step (wide40: 16)")
     ap.add_argument("--batch-tokens", type=int, default=128, help="wide40: tokens decoded in batches")
@@ -834,9 +1117,10 @@ def main():
     ap.add_argument("--slots", type=int, default=None, help="56; wide40: 96")
     ap.add_argument("--admit", default="window")
     ap.add_argument("--seed", type=int, default=42)
-    ap.add_argument("--cpu-seconds", type=float, default=10.0, help="bounded CPU-baseline sample")
+    ap.add_argument("--cpu-seconds", type=float, default=16.0, help="bounded CPU-baseline sample")
     ap.add_argument("--kernel-steps", type=int, default=64, help="eager tokens timed per kernel")
-    ap.add_argument("--path", type=int, default=0, help="0 fused, 1 fork/join, 2 serial expert launches")
+    ap.add_argument("--path", type=int, default=0,
+                    help="0 fused layer launch, 1 fork/join, 2 serial expert launches, 3 unfused launches")
     ap.add_argument("--sidecar", type=int, default=-1,
                     help="host threads serving absent experts (0: GPU only; default: 14 on a 16-CPU host)")
     ap.add_argument("--share", default="1/1", help="num/den: absent experts of rank r with r %% den < num go to "
@@ -846,7 +1130,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-gpu-only", action="store_true", help="skip the GPU-only decode beside the default one")
     ap.add_argument("--no-check", action="store_true")
-    ap.add_argument("--no-lookahead", action="store_true", help="skip the residual48 streaming comparison")
+    ap.add_argument("--no-extra", action="store_true", help="stacked48: only configuration 2 (no config1/3/4/5)")
+    ap.add_argument("--no-lookahead", action="store_true", help="residual48: skip the streaming-off comparison")
     ap.add_argument("--stream-per-layer", type=int, default=4)
     ap.add_argument("--stream-reserve", type=int, default=2)
     ap.add_argument("--stream-gbps", type=float, default=45.7)
@@ -870,11 +1155,20 @@ def main():
         args.slots = 96 if wide else 56
     if args.batch is None:
         args.batch = 16 if wide else 512
-    if args.workload == "prefill48":
-        print(json.dumps(run_prefill(args)), flush=True)
-        return
     import torch
-    if wide:
+    wl = None
+    if args.workload == "stacked48":
+        result = run_default(args)
+    elif args.workload == "prefill48":
+        result = run_prefill(args)
+    elif args.workload == "single1":
+        r = run_single(args)
+        result = {"metric": "MoE layer steps/s (1 layer, 128 experts resident, batch 1) + achieved HBM GB/s",
+                  "value": r["value"], "unit": r["unit"], "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+                  "ms_per_step": round(r["step"]["us_wall"] / 1e3, 5), "higher_is_better": True, "scaling": "weak",
+                  "vs_baseline": None, "dtype": "q4_k x q8_k int8-dot, fp32 scale (router fp32)",
+                  "data": "synthetic (seeded N(0,0.02) experts quantized to Q4_K, N(0,1) activations)", **r}
+    elif wide:
         if args.batch_tokens % args.batch:
             sys.exit("--batch-tokens must be a multiple of --batch")
         wl = Workload(args, steer=True, n_experts=256, inter=512, shared=True, zipf_s=1.0, reuse=0.5,
@@ -884,13 +1178,14 @@ def main():
         wl = Workload(args, steer=False)
         result = run_residual(args, wl)
     else:
-        wl = Workload(args, steer=args.workload == "stacked48")
-        result = run_stacked(args, wl) if args.workload == "stacked48" else run_prior(args, wl)
-    if not args.no_cpu:
-        result["cpu_baseline"] = wl.cpu_baseline()
-    wl.close()
+        wl = Workload(args, steer=False)
+        result = run_prior(args, wl)
+    if wl is not None:
+        if not args.no_cpu:
+            result["cpu_baseline"] = wl.cpu_baseline(args.cpu_seconds)
+        wl.close()
     if args.calibrate_copy:
-        src = torch.ones(256 << 20, dtype=torch.uint8, device=wl.dev)
+        src = torch.ones(256 << 20, dtype=torch.uint8, device="cuda:0")
         for _ in range(3):
             dst = src.clone()
         torch.cuda.synchronize()

@@ -165,7 +165,9 @@ int moe_experts(const moe_experts_desc *d, void *stream);
  * experts at host addresses experts[k] ([up][gate][down] bytes), given the
  * Q8_K of x (host, [H/256][292]).  n_threads workers (the caller included);
  * AVX-512 VNNI integer dots when the CPU has them, or the portable path
- * (portable != 0 forces it).  Results equal the device kernels' bit for bit. */
+ * (portable != 0 forces it).  Results equal the device kernels' bit for bit.
+ * The worker threads of each n_threads are started by the first call and kept;
+ * calls from several threads run one at a time. */
 int moe_cpu_experts(const void *const *experts, int n, const uint8_t *q8x, int H, int I, int down_type, float *rows,
                     int n_threads, int portable);
 int moe_cpu_has_vnni(void);
@@ -211,6 +213,7 @@ typedef struct {
     double sidecar_wait_us, sidecar_cpu_us;      /* host time waiting for the GPU's posts / computing */
     double host_boundary_us;                     /* batch-1 decode: host time after the token's GPU work
                                                     (observe, step, table flush) before it returns */
+    uint64_t n_evicted;                          /* resident experts evicted by the steps for uploads */
 } moe_cache_stats;
 
 typedef struct {

@@ -29,6 +29,7 @@
 #include <cstring>
 #include <deque>
 #include <memory>
+#include <map>
 #include <mutex>
 #include <string>
 #include <thread>
@@ -212,6 +213,7 @@ struct moe_cache {
     std::vector<float> sc_log;                  // per served layer: wait us, cpu us, experts (last 64K)
     uint64_t clock = 0, n_steps = 0, n_uploads = 0, n_scheduled = 0, n_copied = 0, n_published = 0;
     uint64_t n_admit_ok = 0, n_admit_denied = 0, n_table_flushes = 0, bytes_uploaded = 0;
+    uint64_t n_evicted = 0;            // resident experts the step evicted for an upload
     double wait_us = 0.0;
     double boundary_us = 0.0;          // batch-1 decode: host time from the token's sync to the return
     FILE *route = nullptr, *map = nullptr;
@@ -911,6 +913,7 @@ int cache_step(moe_cache *c) {
                     ls.expert_slot[victim] = -1;
                     ls.slot_expert[slot] = -1;
                     set_table_entry(c, ls, victim, ls.S);
+                    c->n_evicted++;
                 }
                 ls.slot_in_flight[slot] = 1;
                 const int r = start_upload(c, (int)li, id, slot);
@@ -936,6 +939,7 @@ int cache_step(moe_cache *c) {
             ls.slot_expert[slot] = -1;
             set_table_entry(c, ls, victim, ls.S);
             ls.free_slots.push_back(slot);
+            c->n_evicted++;
         }
     }
 
@@ -1355,11 +1359,16 @@ int moe_cpu_experts(const void *const *experts, int n, const uint8_t *q8x, int H
     }
     std::vector<float> h((size_t)n * I);
     std::vector<uint8_t> q8h((size_t)n * (I / 256) * mp::Q8K_BYTES);
-    mpc::Team *t = mpc::team_create(n_threads < 1 ? 1 : n_threads);
+    // one team per thread count, kept for later calls (a team's threads start
+    // once, not per call); calls run one at a time
+    static std::mutex m;
+    static std::map<int, mpc::Team *> teams;
+    std::lock_guard<std::mutex> lk(m);
+    mpc::Team *&t = teams[n_threads < 1 ? 1 : n_threads];
+    if (!t) t = mpc::team_create(n_threads < 1 ? 1 : n_threads);
     mpc::set_portable(portable != 0);
     mpc::experts(t, e.data(), n, H, I, down_type, h.data(), q8h.data());
     mpc::set_portable(false);
-    mpc::team_destroy(t);
     return MOE_OK;
 }
 
@@ -2103,6 +2112,7 @@ int moe_cache_stats_get(moe_cache *c, moe_cache_stats *s) {
     s->bytes_uploaded = c->bytes_uploaded;
     s->publication_wait_us = c->wait_us;
     s->host_boundary_us = c->boundary_us;
+    s->n_evicted = c->n_evicted;
     return MOE_OK;
 }
 

@@ -67,7 +67,8 @@ class CacheStats(ctypes.Structure):
                                    "n_table_flushes", "bytes_uploaded")] + \
                [("publication_wait_us", ctypes.c_double), ("n_staged", ctypes.c_uint64),
                 ("n_cpu_served", ctypes.c_uint64), ("sidecar_wait_us", ctypes.c_double),
-                ("sidecar_cpu_us", ctypes.c_double), ("host_boundary_us", ctypes.c_double)]
+                ("sidecar_cpu_us", ctypes.c_double), ("host_boundary_us", ctypes.c_double),
+                ("n_evicted", ctypes.c_uint64)]
 
 
 class LayerView(ctypes.Structure):

@@ -313,6 +313,7 @@ def test_decode_48_layers_past_cache_fill(tmp_path):
         assert st[k] == ost[k], (k, st[k], ost[k])
     print("evicted", rig.n_evicted, "denied", st["n_admit_denied"], "hit", st["n_hit"] / (st["n_hit"] + st["n_miss"]))
     assert rig.n_evicted > 100 and st["n_admit_denied"] > 100
+    assert st["n_evicted"] == rig.n_evicted          # the step's count equals the evictions the frames show
 
 
 def test_sidecar_host_abort_then_next_token_exact(tmp_path):
