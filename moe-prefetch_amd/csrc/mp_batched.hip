@@ -277,9 +277,8 @@ __device__ inline void q6_frag(const uint8_t *blk, int h, half8_t bh[8], half8_t
 #pragma unroll
     for (int hh = 0; hh < 2; ++hh) {
         const uint8_t *pa = blk + 64 * hh + 8 * h;
-        const uint32_t a0 = lds_u32_at2(pa), a1 = lds_u32_at2(pa + 4);
-        const uint32_t b0 = lds_u32_at2(pa + 32), b1 = lds_u32_at2(pa + 36);
-        const uint32_t q0 = lds_u32_at2(blk + 128 + 32 * hh + 8 * h), q1 = lds_u32_at2(blk + 132 + 32 * hh + 8 * h);
+        const uint2 va = lds_u64_at2(pa), vb = lds_u64_at2(pa + 32), vq = lds_u64_at2(blk + 128 + 32 * hh + 8 * h);
+        const uint32_t a0 = va.x, a1 = va.y, b0 = vb.x, b1 = vb.y, q0 = vq.x, q1 = vq.y;
         const uint32_t w[4][2] = {{(a0 & M) | ((q0 << 4) & HM), (a1 & M) | ((q1 << 4) & HM)},
                                   {(b0 & M) | ((q0 << 2) & HM), (b1 & M) | ((q1 << 2) & HM)},
                                   {((a0 >> 4) & M) | (q0 & HM), ((a1 >> 4) & M) | (q1 & HM)},

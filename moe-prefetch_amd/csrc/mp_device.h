@@ -211,9 +211,11 @@ __device__ inline void q4k_sm(const uint4 &hdr, int j, int &sc, int &m) {
     }
 }
 
-__device__ inline uint32_t lds_u32_at2(const uint8_t *p) {   // 2-byte aligned
-    const uint16_t *q = (const uint16_t *)p;
-    return (uint32_t)q[0] | ((uint32_t)q[1] << 16);
+// 8 bytes of LDS at a 2-byte boundary, one unaligned read
+__device__ inline uint2 lds_u64_at2(const uint8_t *p) {
+    uint2 v;
+    __builtin_memcpy(&v, p, 8);
+    return v;
 }
 
 }  // namespace mp

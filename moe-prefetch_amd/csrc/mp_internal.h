@@ -163,14 +163,16 @@ struct FusedArgs {
                               // no combine; else combine workgroups write x.out
     uint64_t *xlog;           // [256] tagged logits (bias added)
     uint64_t *rec;            // [FUSED_COPIES][FUSED_REC] tagged routing words
-    uint64_t *hx;             // [K + 1][I] tagged SwiGLU activations
+    uint64_t *hflag;          // [K + 1][I / FUSED_GU_TILE] tagged: gate/up tile t of expert k has stored its h
+    float *h;                 // [K + 1][I] SwiGLU activations (agent-scope stores, read after the tile's flag)
     uint64_t *yx;             // [K + 1][H] tagged down rows
     uint32_t *err;            // a bounded wait ran out: the token's sequence number is written here
     uint64_t wait_ticks;      // bound of every wait, 100 MHz wall clock
 };
 // exchange words per layer of the fused decode
 inline size_t fused_words(int K, int I, int H) {
-    return 256 + (size_t)FUSED_COPIES * FUSED_REC + (size_t)(K + 1) * I + (size_t)(K + 1) * H;
+    return 256 + (size_t)FUSED_COPIES * FUSED_REC + (size_t)(K + 1) * (I / FUSED_GU_TILE) + (size_t)(K + 1) * I / 2 +
+           (size_t)(K + 1) * H;
 }
 
 constexpr int MAX_E = 256;   // experts per layer the kernels support

@@ -567,15 +567,19 @@ __device__ inline float down_rows_dot(const uint8_t *s_wt, const uint8_t *s_q8h,
             d = h2f_dev((uint16_t)(hdr.x & 0xffff)) * dx;
             dm = h2f_dev((uint16_t)(hdr.x >> 16)) * dx;
         } else {
+            // a Q6_K block (210 bytes) is only 2-byte aligned: 8-byte LDS
+            // reads at any 2-byte boundary (gfx950 reads LDS unaligned)
             const uint8_t *blk = s_wt + g * rowb + b * Q6K_BYTES;
             const int hh = u >> 2, up4 = u & 3;
-            const uint8_t *pa = blk + 64 * hh + 8 * up4;
-            const uint8_t *pb = pa + 32;
-            const uint8_t *ph = blk + 128 + 32 * hh + 8 * up4;
-            const uint32_t a0 = lds_u32_at2(pa), a1 = lds_u32_at2(pa + 4);
-            const uint32_t b0 = lds_u32_at2(pb), b1 = lds_u32_at2(pb + 4);
-            const uint32_t h0 = lds_u32_at2(ph), h1 = lds_u32_at2(ph + 4);
-            const int8_t *sc = (const int8_t *)(blk + 192 + 8 * hh + (up4 >> 1));
+            const uint2 va = lds_u64_at2(blk + 64 * hh + 8 * up4);
+            const uint2 vb = lds_u64_at2(blk + 64 * hh + 8 * up4 + 32);
+            const uint2 vh = lds_u64_at2(blk + 128 + 32 * hh + 8 * up4);
+            const uint2 vs = lds_u64_at2(blk + 192 + 8 * hh);             // the half's 8 scales
+            const uint32_t a0 = va.x, a1 = va.y, b0 = vb.x, b1 = vb.y, h0 = vh.x, h1 = vh.y;
+            // scale of sub-block (up4 >> 1) + 2 q, q = 0..3: bytes (up4 >> 1) + 2 q of the 8
+            const uint32_t sw = (up4 >> 1) ? ((vs.x >> 8) & 0x00ff00ffu) | (((vs.y >> 8) & 0x00ff00ffu) << 8)
+                                           : (vs.x & 0x00ff00ffu) | ((vs.y & 0x00ff00ffu) << 8);
+            const int8_t sc[8] = {(int8_t)sw, 0, (int8_t)(sw >> 16), 0, (int8_t)(sw >> 8), 0, (int8_t)(sw >> 24), 0};
             const uint32_t L = 0x0F0F0F0Fu, Hm = 0x30303030u;
             const uint32_t qv[4][2] = {
                 {(a0 & L) | ((h0 << 4) & Hm), (a1 & L) | ((h1 << 4) & Hm)},
@@ -1030,8 +1034,14 @@ __device__ void fused_gateup(const FusedArgs &a, int g, uint32_t seq, uint8_t *s
     const float upv = __shfl(acc, lane + 32, 64);                  // row i's up sum, for the gate lanes
     if (is_gate && b == 7) {
         const float gv = acc;
-        store_tagged(a.hx + (size_t)k * x.I + row, tagged(seq, gv / (1.0f + canon_expf(-gv)) * upv));
+        __hip_atomic_store(a.h + (size_t)k * x.I + row, gv / (1.0f + canon_expf(-gv)) * upv, __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
     }
+    // the tile's flag once every wave's h stores have completed (written
+    // through at agent scope: no cache write-back needed)
+    __builtin_amdgcn_s_waitcnt(0x0f70);                            // vmcnt(0)
+    __syncthreads();
+    if (threadIdx.x == 0) store_tagged(a.hflag + (size_t)k * (x.I / FUSED_GU_TILE) + tile, tagged(seq, 0.0f));
 }
 
 // FUSED_DN_TILE down rows of expert k, 8 per wave: the weights into LDS as
@@ -1061,17 +1071,26 @@ __device__ void fused_down(const FusedArgs &a, int g, uint32_t seq, uint8_t *sme
     const size_t dn_off = 2ull * x.I * (x.H / QK) * Q4K_BYTES + (size_t)r0 * rowb;
     const uint4 *wsrc = src.base ? (const uint4 *)(src.base + dn_off) : nullptr;
     uint8_t *sb = src.absent && x.stage ? x.stage + (size_t)k * x.stage_stride + dn_off : nullptr;
-    // the weights first: straight into LDS (16 bytes a lane, lane-contiguous),
-    // or through registers when they are also staged
+    // The weights first, straight into LDS (16 bytes a lane, lane-contiguous)
+    // and all by the last wave: a wave's loads return in the order they were
+    // issued, so the waves that poll for h must not have weights queued ahead
+    // of their polls.  Rows that are also staged pass through registers, each
+    // wave its own 8.
     uint4 buf[5];
     if (wsrc && !sb) {
+        if (wave == 3) {
+            const uint4 *w0 = (const uint4 *)(src.base + 2ull * x.I * (x.H / QK) * Q4K_BYTES +
+                                              (size_t)tile * FUSED_DN_TILE * rowb);
 #pragma unroll
-        for (int j = 0; j < 5; ++j) {
-            const int i = lane + 64 * j;
-            if (i < nvec)
-                __builtin_amdgcn_global_load_lds((const void *)(wsrc + i),
-                                                 (__attribute__((address_space(3))) void *)(s_wt + 1024 * j), 16, 0,
-                                                 0);
+            for (int ww = 0; ww < 4; ++ww)
+#pragma unroll
+                for (int j = 0; j < 5; ++j) {
+                    const int i = lane + 64 * j;
+                    if (i < nvec)
+                        __builtin_amdgcn_global_load_lds(
+                            (const void *)(w0 + (size_t)ww * nvec + i),
+                            (__attribute__((address_space(3))) void *)(smem + ww * DN_LDS_ROWS + 1024 * j), 16, 0, 0);
+                }
         }
     } else if (wsrc) {
 #pragma unroll
@@ -1080,21 +1099,17 @@ __device__ void fused_down(const FusedArgs &a, int g, uint32_t seq, uint8_t *sme
             buf[j] = i < nvec ? wsrc[i] : make_uint4(0, 0, 0, 0);
         }
     }
-    // h of expert k, block `wave`, as the gate/up workgroups post it
+    // h of expert k, block `wave`: once the flags of all the expert's gate/up
+    // tiles carry seq, the block's values (four a lane)
     if (wave < nb) {
-        const uint64_t *hp = a.hx + (size_t)k * x.I + QK * wave + 4 * lane;
-        uint64_t hv[4] = {0, 0, 0, 0};
-        bool ok[4] = {false, false, false, false};
+        const int nt = x.I / FUSED_GU_TILE;            // <= 48 tiles
+        const uint64_t *fp = a.hflag + (size_t)k * nt;
+        bool ok = lane >= nt;
         int late = 0;
         const uint64_t t0 = wall_clock64();
         for (;;) {
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-                if (!ok[i]) {
-                    hv[i] = load_tagged(hp + i);
-                    ok[i] = (uint32_t)(hv[i] >> 32) == seq;
-                }
-            if (__all(ok[0] && ok[1] && ok[2] && ok[3])) break;
+            if (!ok) ok = (uint32_t)(load_tagged(fp + lane) >> 32) == seq;
+            if (__all(ok)) break;
             if (wall_clock64() - t0 > a.wait_ticks) {
                 late = 1;
                 break;
@@ -1102,15 +1117,17 @@ __device__ void fused_down(const FusedArgs &a, int g, uint32_t seq, uint8_t *sme
             __builtin_amdgcn_s_sleep(1);
         }
         if (late && lane == 0) fused_late(a, seq);
-        const float xv[4] = {__uint_as_float((uint32_t)hv[0]), __uint_as_float((uint32_t)hv[1]),
-                             __uint_as_float((uint32_t)hv[2]), __uint_as_float((uint32_t)hv[3])};
+        const uint64_t *hp = (const uint64_t *)(a.h + (size_t)k * x.I + QK * wave + 4 * lane);
+        const uint64_t h01 = load_tagged(hp), h23 = load_tagged(hp + 1);   // two values per word
+        const float xv[4] = {__uint_as_float((uint32_t)h01), __uint_as_float((uint32_t)(h01 >> 32)),
+                             __uint_as_float((uint32_t)h23), __uint_as_float((uint32_t)(h23 >> 32))};
         int q[4];
         float d;
         q8k_wave_vals(xv, lane, q, d);
         q8k_store(q, d, s_q8h + wave * Q8K_BYTES, lane);
     }
     if (wsrc && !sb) {
-        __builtin_amdgcn_s_waitcnt(0x0f70);             // vmcnt(0): the direct-to-LDS weights have landed
+        if (wave == 3) __builtin_amdgcn_s_waitcnt(0x0f70);      // vmcnt(0): the weights have landed in LDS
     } else if (wsrc) {
         uint4 *dst = (uint4 *)s_wt;
 #pragma unroll
