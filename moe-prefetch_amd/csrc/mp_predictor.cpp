@@ -1,257 +1,309 @@
-// mp_predictor.cpp -- the MOEP expert predictor / evictor (see mp_predictor.h).
+// mp_predictor.cpp -- the MOEP expert predictor / evictor (behaviour of the
+// reference's cpp/moe-predictor.cpp: load() 21-155, score() 165-222,
+// top_k_ids() 224-238, update() 241-309, save() 318-362).
 //
-// File format MOEP v3, as the reference's loader reads it (cpp/moe-predictor.cpp
-// load(), 21-151) and its saver writes it (save(), 318-362):
-//   "MOEP", u32 version 3, d_model, n_comp, n_expert, n_layers, top_k, feat_dim,
-//   n_present, n_blocks, pca_flag, reserved;
-//   n_blocks x (u32 kind, offset, size): contiguous from column 0, covering
-//   feat_dim; size n_comp for the PCA block, n_expert for the id blocks;
-//   [pca_flag] f32 mean[d_model], comp[d_model * n_comp], scale[n_comp];
+// MOEP v3, little-endian, as the reference's loader and saver define it:
+//   "MOEP", then eleven u32: version (3), d_model, n_comp, n_expert, n_layers,
+//   top_k, feat_dim, n_present, n_blocks, pca_flag, reserved;
+//   n_blocks x (u32 group, first column, width), the groups laid end to end
+//   from column 0 up to feat_dim, width n_comp for the PCA group and n_expert
+//   for the id groups (a group named twice keeps its last entry);
+//   when pca_flag is set: f32 mean[d_model], comp[d_model][n_comp], scale[n_comp];
 //   i32 layer[n_present], f32 prior[n_present], f32 bias[n_present][n_expert],
-//   f32 w[n_present][feat_dim][n_expert]; nothing after it.
+//   f32 w[n_present][feat_dim][n_expert], and nothing after it.
+//
+// The loader reads the file whole, checks the header and the block table,
+// derives from them the size the file must have and compares it with the size
+// it has (a short or an over-long file is refused by that one test), then
+// splits the sections. Every refusal names the byte offset it concerns.
 #include "mp_predictor.h"
 
 #include <algorithm>
 #include <cmath>
 #include <cstdio>
 #include <cstring>
-#include <memory>
-#include <numeric>
 
 namespace mpp {
 
 namespace {
 
-struct File {
-    FILE *f;
-    explicit File(FILE *p) : f(p) {}
-    ~File() {
-        if (f) fclose(f);
-    }
-    bool get(void *p, size_t n) { return fread(p, 1, n, f) == n; }
-    bool u32(uint32_t &v) { return get(&v, 4); }
+const char *const kGroupName[N_GROUPS] = {"PCA", "prev", "cur", "below", "self_prev"};
+constexpr uint32_t kVersion = 3;
+
+struct Refused {
+    std::string why;
 };
+
+std::string at_byte(size_t off) { return "byte " + std::to_string(off) + ": "; }
+
+// The file's bytes and a read position; a read past the end is a refusal
+// that names what was being read.
+class Image {
+public:
+    bool open(const std::string &path) {
+        FILE *f = fopen(path.c_str(), "rb");
+        if (!f) return false;
+        uint8_t chunk[1 << 16];
+        size_t got;
+        while ((got = fread(chunk, 1, sizeof chunk, f)) > 0) bytes_.insert(bytes_.end(), chunk, chunk + got);
+        const bool ok = !ferror(f);
+        fclose(f);
+        return ok;
+    }
+    size_t size() const { return bytes_.size(); }
+    size_t at() const { return at_; }
+    const uint8_t *take(size_t n, const char *what) {
+        if (bytes_.size() - at_ < n)
+            throw Refused{at_byte(bytes_.size()) + "the file ends inside the " + what};
+        const uint8_t *p = bytes_.data() + at_;
+        at_ += n;
+        return p;
+    }
+    uint32_t u32(const char *what) {
+        uint32_t v;
+        memcpy(&v, take(4, what), 4);
+        return v;
+    }
+    template <class T>
+    void fill(std::vector<T> &dst, size_t n, const char *what) {
+        dst.resize(n);
+        if (n) memcpy(dst.data(), take(n * sizeof(T), what), n * sizeof(T));
+    }
+
+private:
+    std::vector<uint8_t> bytes_;
+    size_t at_ = 0;
+};
+
+// Byte counts the header implies, refused when they do not fit a size_t.
+size_t mul(size_t a, size_t b) {
+    if (a != 0 && b > SIZE_MAX / a) throw Refused{"the header describes more data than can be addressed"};
+    return a * b;
+}
+size_t add(size_t a, size_t b) {
+    if (b > SIZE_MAX - a) throw Refused{"the header describes more data than can be addressed"};
+    return a + b;
+}
+
+// Order-preserving 32-bit image of a score: a larger score has a larger key,
+// -0 and +0 are equal, and a NaN is equal to -inf.
+uint32_t order_bits(float s) {
+    if (s != s) s = -INFINITY;
+    if (s == 0.0f) s = 0.0f;
+    uint32_t b;
+    memcpy(&b, &s, 4);
+    return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+}
 
 }  // namespace
 
 bool Predictor::load(const std::string &path, std::string &err) {
-    File in(fopen(path.c_str(), "rb"));
-    if (!in.f) {
-        err = "cannot open " + path;
+    Image im;
+    if (!im.open(path)) {
+        err = "cannot read " + path;
         return false;
     }
-    Predictor p;                 // filled completely before it replaces *this
-    char magic[4];
-    if (!in.get(magic, 4) || memcmp(magic, "MOEP", 4) != 0) {
-        err = path + ": not a MOEP file";
-        return false;
-    }
-    uint32_t version, n_present, n_blocks, pca_flag, reserved;
-    if (!in.u32(version) || !in.u32(p.d_model) || !in.u32(p.n_comp) || !in.u32(p.n_expert) ||
-        !in.u32(p.n_layers) || !in.u32(p.top_k) || !in.u32(p.feat_dim) || !in.u32(n_present) ||
-        !in.u32(n_blocks) || !in.u32(pca_flag) || !in.u32(reserved)) {
-        err = path + ": truncated header";
-        return false;
-    }
-    if (version != 3) {
-        err = path + ": version " + std::to_string(version) + ", expected 3";
-        return false;
-    }
-    p.has_pca = pca_flag != 0;
-    // the block table says which columns mean what: it must tile [0, feat_dim)
-    uint32_t next = 0;
-    for (uint32_t i = 0; i < n_blocks; ++i) {
-        uint32_t kind, offset, size;
-        if (!in.u32(kind) || !in.u32(offset) || !in.u32(size)) {
-            err = path + ": truncated block table";
-            return false;
+    Predictor p;
+    try {
+        if (memcmp(im.take(4, "magic"), "MOEP", 4) != 0) throw Refused{at_byte(0) + "the magic is not MOEP"};
+        uint32_t h[11];
+        for (uint32_t &v : h) v = im.u32("header");
+        const uint32_t version = h[0], n_present = h[7], n_blocks = h[8], pca_flag = h[9];
+        if (version != kVersion)
+            throw Refused{at_byte(4) + "format version " + std::to_string(version) + ", this loader reads " +
+                          std::to_string(kVersion)};
+        p.shape = Shape{h[1], h[2], h[3], h[4], h[5], h[6]};
+
+        // the block table: which feature columns hold which group
+        uint64_t column = 0;
+        for (uint32_t i = 0; i < n_blocks; ++i) {
+            const size_t entry = im.at();
+            const uint32_t group = im.u32("block table"), first = im.u32("block table"),
+                           width = im.u32("block table");
+            if (first != column)
+                throw Refused{at_byte(entry) + "block " + std::to_string(i) + " begins at column " +
+                              std::to_string(first) + " where the previous blocks end at " + std::to_string(column)};
+            if (group >= N_GROUPS)
+                throw Refused{at_byte(entry) + "block " + std::to_string(i) + " names group " +
+                              std::to_string(group) + ", known groups are 0.." + std::to_string(N_GROUPS - 1)};
+            const uint32_t want = group == GROUP_PCA ? p.shape.n_comp : p.shape.n_expert;
+            if (width != want)
+                throw Refused{at_byte(entry) + "the " + kGroupName[group] + " block is " + std::to_string(width) +
+                              " columns wide, the header implies " + std::to_string(want)};
+            p.group_col[group] = (int32_t)first;
+            column = (uint32_t)(column + width);     // the 32-bit sum the format's own offsets use
         }
-        if (offset != next) {
-            err = path + ": block " + std::to_string(i) + " starts at " + std::to_string(offset) + ", expected " +
-                  std::to_string(next);
-            return false;
+        if (column != p.shape.feat_dim)
+            throw Refused{at_byte(im.at()) + "the blocks cover " + std::to_string(column) +
+                          " columns, the header's feat_dim is " + std::to_string(p.shape.feat_dim)};
+        if ((pca_flag != 0) != p.has_pca())
+            throw Refused{at_byte(40) + "pca_flag " + std::to_string(pca_flag) +
+                          (p.has_pca() ? " but the block table has a PCA block"
+                                       : " but the block table has no PCA block")};
+
+        // the size every later section fixes, checked before any is split off
+        const size_t E = p.shape.n_expert;
+        const size_t pca_floats =
+            pca_flag ? add(add(p.shape.d_model, mul(p.shape.d_model, p.shape.n_comp)), p.shape.n_comp) : 0;
+        const size_t per_layer = add(add(2, E), mul(p.shape.feat_dim, E));    // layer id, prior, bias, rows
+        const size_t want = add(im.at(), mul(4, add(pca_floats, mul(n_present, per_layer))));
+        if (im.size() != want)
+            throw Refused{at_byte(std::min(im.size(), want)) + "the file is " + std::to_string(im.size()) +
+                          " bytes, its header and block table describe " + std::to_string(want)};
+
+        if (pca_flag) {
+            im.fill(p.pca_mean, p.shape.d_model, "PCA mean");
+            im.fill(p.pca_comp, (size_t)p.shape.d_model * p.shape.n_comp, "PCA components");
+            im.fill(p.pca_scale, p.shape.n_comp, "PCA scale");
         }
-        if (kind > BLOCK_SELF_PREV) {
-            err = path + ": unknown feature block kind " + std::to_string(kind);
-            return false;
+        const size_t tables = im.at();
+        std::vector<int32_t> layer;
+        std::vector<float> prior;
+        im.fill(layer, n_present, "layer list");
+        im.fill(prior, n_present, "prior list");
+        p.present.resize(n_present);
+        p.slot.assign(p.shape.n_layers, -1);
+        for (uint32_t i = 0; i < n_present; ++i) {
+            LayerWeights &lw = p.present[i];
+            lw.layer = layer[i];
+            lw.prior = prior[i];
+            if (lw.layer < 0 || lw.layer >= (int64_t)p.shape.n_layers)
+                throw Refused{at_byte(tables + 4 * (size_t)i) + "layer " + std::to_string(lw.layer) +
+                              " is outside the model's " + std::to_string(p.shape.n_layers) + " layers"};
+            p.slot[(size_t)lw.layer] = (int32_t)i;     // a layer listed twice scores with its last entry
         }
-        const uint32_t want = kind == BLOCK_PCA ? p.n_comp : p.n_expert;
-        if (size != want) {
-            static const char *names[] = {"PCA", "prev", "cur", "below", "self_prev"};
-            err = path + ": " + names[kind] + " block size " + std::to_string(size) + " != " + std::to_string(want);
-            return false;
-        }
-        p.off[kind] = (int32_t)offset;
-        next += size;
-    }
-    if (next != p.feat_dim) {
-        err = path + ": blocks cover " + std::to_string(next) + " columns, feat_dim is " + std::to_string(p.feat_dim);
+        for (LayerWeights &lw : p.present) im.fill(lw.bias, E, "biases");
+        for (LayerWeights &lw : p.present) im.fill(lw.rows, (size_t)p.shape.feat_dim * E, "weights");
+    } catch (const Refused &r) {
+        err = "MOEP " + path + ", " + r.why;
         return false;
-    }
-    if (p.has_pca != (p.off[BLOCK_PCA] >= 0)) {
-        err = path + ": the PCA flag disagrees with the block table";
-        return false;
-    }
-    if (p.has_pca) {
-        p.pca_mean.resize(p.d_model);
-        p.pca_comp.resize((size_t)p.d_model * p.n_comp);
-        p.pca_scale.resize(p.n_comp);
-        if (!in.get(p.pca_mean.data(), p.pca_mean.size() * 4) || !in.get(p.pca_comp.data(), p.pca_comp.size() * 4) ||
-            !in.get(p.pca_scale.data(), p.pca_scale.size() * 4)) {
-            err = path + ": truncated PCA block";
-            return false;
-        }
-    }
-    p.layers.resize(n_present);
-    p.prior.resize(n_present);
-    p.bias.resize((size_t)n_present * p.n_expert);
-    if (!in.get(p.layers.data(), (size_t)n_present * 4) || !in.get(p.prior.data(), (size_t)n_present * 4) ||
-        !in.get(p.bias.data(), p.bias.size() * 4)) {
-        err = path + ": truncated layer table";
-        return false;
-    }
-    p.w.resize((size_t)n_present * p.feat_dim * p.n_expert);
-    if (!in.get(p.w.data(), p.w.size() * 4)) {
-        err = path + ": truncated weights (wanted " + std::to_string(p.w.size() * 4) + " bytes)";
-        return false;
-    }
-    char extra;
-    if (fread(&extra, 1, 1, in.f) != 0) {
-        err = path + ": trailing bytes after the weights";
-        return false;
-    }
-    p.slot_of.assign(p.n_layers, -1);
-    for (uint32_t i = 0; i < n_present; ++i) {
-        const int32_t il = p.layers[i];
-        if (il < 0 || il >= (int32_t)p.n_layers) {
-            err = path + ": layer index " + std::to_string(il) + " out of range";
-            return false;
-        }
-        p.slot_of[(size_t)il] = (int32_t)i;
     }
     *this = std::move(p);
     return true;
 }
 
-void Predictor::score(int il, const Lists &in, float *out) const {
-    const int32_t slot = slot_of[(size_t)il];
-    const uint32_t E = n_expert;
-    const float *W = w.data() + (size_t)slot * feat_dim * E;
-    memcpy(out, bias.data() + (size_t)slot * E, (size_t)E * sizeof(float));
-    // x is multi-hot: x . W adds the rows its ids select, block by block
-    static const int kinds[4] = {BLOCK_PREV, BLOCK_CUR, BLOCK_BELOW, BLOCK_SELF_PREV};
+void Predictor::pick(const Lists &in, std::vector<uint32_t> &rows) const {
+    static const Group kOrder[4] = {GROUP_PREV, GROUP_CUR, GROUP_BELOW, GROUP_SELF_PREV};
+    const int32_t E = (int32_t)shape.n_expert;
+    rows.clear();
     for (int b = 0; b < 4; ++b) {
-        const int32_t o = off[kinds[b]];
-        if (o < 0) continue;
+        const int32_t col = group_col[kOrder[b]];
+        if (col < 0) continue;
         for (size_t i = 0; i < in.n[b]; ++i) {
             const int32_t e = in.ids[b][i];
-            if (e < 0 || e >= (int32_t)E) continue;
-            const float *row = W + (size_t)(o + e) * E;
-            for (uint32_t j = 0; j < E; ++j) out[j] += row[j];
+            if (e >= 0 && e < E) rows.push_back((uint32_t)(col + e));
         }
     }
-    // z-score the row, then the repeat prior on the prev ids (the order the
-    // prior's weight was fitted in)
-    float sum = 0.0f;
-    for (uint32_t j = 0; j < E; ++j) sum += out[j];
-    const float mean = sum / (float)E;
+}
+
+void Predictor::score(int il, const Lists &in, float *out) const {
+    const LayerWeights &lw = present[(size_t)slot[(size_t)il]];
+    const size_t E = shape.n_expert;
+    std::vector<uint32_t> rows;
+    pick(in, rows);
+    // x . W for a multi-hot x: per column, the bias plus the picked rows
+    for (size_t j = 0; j < E; ++j) {
+        float acc = lw.bias[j];
+        for (uint32_t r : rows) acc += lw.rows[(size_t)r * E + j];
+        out[j] = acc;
+    }
+    // z-score over the row, then the repeat prior (the prior's weight was
+    // fitted on z-scored scores)
+    float total = 0.0f;
+    for (size_t j = 0; j < E; ++j) total += out[j];
+    const float mean = total / (float)E;
     float ss = 0.0f;
-    for (uint32_t j = 0; j < E; ++j) {
-        const float dv = out[j] - mean;
-        const float sq = dv * dv;
-        ss += sq;
-    }
+    for (size_t j = 0; j < E; ++j) ss += (out[j] - mean) * (out[j] - mean);
     const float sd = std::sqrt(ss / (float)E) + 1e-9f;
-    for (uint32_t j = 0; j < E; ++j) out[j] = (out[j] - mean) / sd;
-    const float pw = prior[(size_t)slot];
-    if (pw != 0.0f)
-        for (size_t i = 0; i < in.n[0]; ++i) {
-            const int32_t e = in.ids[0][i];
-            if (e >= 0 && e < (int32_t)E) out[e] += pw;
-        }
+    for (size_t j = 0; j < E; ++j) out[j] = (out[j] - mean) / sd;
+    if (lw.prior == 0.0f) return;          // adding +0 would turn a -0 score into +0
+    const int32_t *prev = in.ids[0];
+    for (size_t i = 0; i < in.n[0]; ++i)
+        if (prev[i] >= 0 && prev[i] < (int32_t)E) out[prev[i]] += lw.prior;
 }
 
 size_t Predictor::top(const float *scores, size_t k, int32_t *out) const {
-    const size_t E = n_expert;
-    if (k > E) k = E;
-    std::vector<int32_t> order(E);
-    std::iota(order.begin(), order.end(), 0);
-    std::partial_sort(order.begin(), order.begin() + (ptrdiff_t)k, order.end(), [scores](int32_t a, int32_t b) {
-        return scores[a] != scores[b] ? scores[a] > scores[b] : a < b;
-    });
-    std::copy(order.begin(), order.begin() + (ptrdiff_t)k, out);
+    const size_t E = shape.n_expert;
+    k = std::min(k, E);
+    // one 64-bit key per column, score bits above the complemented id, so that
+    // a descending sort puts the larger score first and, on equal scores, the
+    // lower id first
+    std::vector<uint64_t> key(E);
+    for (size_t e = 0; e < E; ++e) key[e] = (uint64_t)order_bits(scores[e]) << 32 | (0xffffffffu - (uint32_t)e);
+    std::partial_sort(key.begin(), key.begin() + (ptrdiff_t)k, key.end(), [](uint64_t a, uint64_t b) { return a > b; });
+    for (size_t i = 0; i < k; ++i) out[i] = (int32_t)(0xffffffffu - (uint32_t)key[i]);
     return k;
 }
 
 float Predictor::update(int il, const Lists &in, const int32_t *truth, size_t n_truth, float lr) {
     if (!has_layer(il) || n_truth == 0) return 0.0f;
-    const int32_t slot = slot_of[(size_t)il];
-    const uint32_t E = n_expert;
-    std::vector<float> s(E), g(E);
+    LayerWeights &lw = present[(size_t)slot[(size_t)il]];
+    const size_t E = shape.n_expert;
+    std::vector<float> s(E);
     score(il, in, s.data());
-    std::vector<uint8_t> y(E, 0);
+    std::vector<char> hit(E, 0);
     for (size_t i = 0; i < n_truth; ++i)
-        if (truth[i] >= 0 && truth[i] < (int32_t)E) y[(size_t)truth[i]] = 1;
+        if (truth[i] >= 0 && (size_t)truth[i] < E) hit[(size_t)truth[i]] = 1;
+    // recall@8 of the prediction the step corrects, over every truth entry given
     int32_t best[8];
-    const size_t nt = top(s.data(), 8, best);
-    float hits = 0.0f;
-    for (size_t i = 0; i < nt; ++i) hits += y[(size_t)best[i]] ? 1.0f : 0.0f;
-    const float recall = hits / (float)n_truth;
-    // logistic loss on the z-scored scores: d/ds = sigmoid(s) - y
-    for (uint32_t j = 0; j < E; ++j) {
-        const float p = 1.0f / (1.0f + std::exp(-s[j]));
-        g[j] = (p - (y[j] ? 1.0f : 0.0f)) * lr;
+    float found = 0.0f;
+    for (size_t i = 0, n = top(s.data(), 8, best); i < n; ++i) found += hit[(size_t)best[i]] ? 1.0f : 0.0f;
+    // logistic loss on the z-scored scores: the step is lr * (sigmoid(s) - y)
+    std::vector<float> step(E);
+    for (size_t j = 0; j < E; ++j) step[j] = (1.0f / (1.0f + std::exp(-s[j])) - (hit[j] ? 1.0f : 0.0f)) * lr;
+    std::vector<uint32_t> rows;
+    pick(in, rows);
+    for (uint32_t r : rows) {
+        float *row = lw.rows.data() + (size_t)r * E;
+        for (size_t j = 0; j < E; ++j) row[j] -= step[j];
     }
-    float *W = w.data() + (size_t)slot * feat_dim * E;
-    static const int kinds[4] = {BLOCK_PREV, BLOCK_CUR, BLOCK_BELOW, BLOCK_SELF_PREV};
-    for (int b = 0; b < 4; ++b) {
-        const int32_t o = off[kinds[b]];
-        if (o < 0) continue;
-        for (size_t i = 0; i < in.n[b]; ++i) {
-            const int32_t e = in.ids[b][i];
-            if (e < 0 || e >= (int32_t)E) continue;
-            float *row = W + (size_t)(o + e) * E;
-            for (uint32_t j = 0; j < E; ++j) row[j] -= g[j];
-        }
-    }
-    float *bb = bias.data() + (size_t)slot * E;
-    for (uint32_t j = 0; j < E; ++j) bb[j] -= g[j];
-    return recall;
+    for (size_t j = 0; j < E; ++j) lw.bias[j] -= step[j];
+    return found / (float)n_truth;
 }
 
 bool Predictor::save(const std::string &path, std::string &err) const {
-    if (has_pca) {
-        err = "a predictor with a PCA block is not saved (the cache never uses one)";
+    if (has_pca()) {
+        err = "MOEP " + path + ": not written, the model has a PCA block (scoring never uses it, so a "
+              "written copy could not be checked against the model that wrote it)";
         return false;
     }
+    // the id groups in column order
+    std::vector<uint32_t> groups;
+    for (uint32_t g = GROUP_PREV; g < N_GROUPS; ++g)
+        if (group_col[g] >= 0) groups.push_back(g);
+    std::sort(groups.begin(), groups.end(), [this](uint32_t a, uint32_t b) { return group_col[a] < group_col[b]; });
+
+    std::vector<uint8_t> buf;
+    auto put = [&buf](const void *p, size_t n) {
+        const uint8_t *b = (const uint8_t *)p;
+        buf.insert(buf.end(), b, b + n);
+    };
+    auto word = [&put](uint32_t v) { put(&v, 4); };
+    put("MOEP", 4);
+    for (uint32_t v : {kVersion, shape.d_model, shape.n_comp, shape.n_expert, shape.n_layers, shape.top_k,
+                       shape.feat_dim, (uint32_t)present.size(), (uint32_t)groups.size(), 0u, 0u})
+        word(v);
+    for (uint32_t g : groups) {
+        word(g);
+        word((uint32_t)group_col[g]);
+        word(shape.n_expert);
+    }
+    for (const LayerWeights &lw : present) put(&lw.layer, 4);
+    for (const LayerWeights &lw : present) put(&lw.prior, 4);
+    for (const LayerWeights &lw : present) put(lw.bias.data(), lw.bias.size() * 4);
+    for (const LayerWeights &lw : present) put(lw.rows.data(), lw.rows.size() * 4);
+
     FILE *f = fopen(path.c_str(), "wb");
     if (!f) {
-        err = "cannot open " + path + " for writing";
+        err = "MOEP " + path + ": cannot open for writing";
         return false;
     }
-    bool ok = true;
-    auto put = [&](const void *p, size_t n) { ok = ok && fwrite(p, 1, n, f) == n; };
-    auto u32 = [&](uint32_t v) { put(&v, 4); };
-    std::vector<std::pair<int32_t, uint32_t>> blocks;      // (offset, kind), in column order
-    for (uint32_t kind = BLOCK_PREV; kind <= BLOCK_SELF_PREV; ++kind)
-        if (off[kind] >= 0) blocks.push_back({off[kind], kind});
-    std::sort(blocks.begin(), blocks.end());
-    put("MOEP", 4);
-    for (uint32_t v : {3u, d_model, n_comp, n_expert, n_layers, top_k, feat_dim, (uint32_t)layers.size(),
-                       (uint32_t)blocks.size(), 0u, 0u})
-        u32(v);
-    for (const auto &b : blocks) {
-        u32(b.second);
-        u32((uint32_t)b.first);
-        u32(n_expert);
+    const bool wrote = fwrite(buf.data(), 1, buf.size(), f) == buf.size();
+    if (fclose(f) != 0 || !wrote) {
+        err = "MOEP " + path + ": short write";
+        return false;
     }
-    put(layers.data(), layers.size() * 4);
-    put(prior.data(), prior.size() * 4);
-    put(bias.data(), bias.size() * 4);
-    put(w.data(), w.size() * 4);
-    if (fclose(f) != 0) ok = false;
-    if (!ok) err = "short write to " + path;
-    return ok;
+    return true;
 }
 
 }  // namespace mpp

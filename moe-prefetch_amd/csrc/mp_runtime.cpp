@@ -2037,10 +2037,11 @@ void moe_predictor_free(moe_predictor *p) { delete p; }
 int moe_predictor_info_get(const moe_predictor *p, moe_predictor_info *out) {
     if (!p || !out) return fail(MOE_ERR_ARG, "null argument");
     const mpp::Predictor &q = p->p;
-    *out = moe_predictor_info{q.n_expert, q.n_layers, q.feat_dim, q.top_k, q.d_model, q.n_comp,
-                              (uint32_t)q.layers.size(), q.has_pca ? 1 : 0, q.off[mpp::BLOCK_PCA],
-                              q.off[mpp::BLOCK_PREV], q.off[mpp::BLOCK_CUR], q.off[mpp::BLOCK_BELOW],
-                              q.off[mpp::BLOCK_SELF_PREV]};
+    *out = moe_predictor_info{q.shape.n_expert, q.shape.n_layers, q.shape.feat_dim, q.shape.top_k,
+                              q.shape.d_model, q.shape.n_comp, (uint32_t)q.present.size(), q.has_pca() ? 1 : 0,
+                              q.group_col[mpp::GROUP_PCA], q.group_col[mpp::GROUP_PREV],
+                              q.group_col[mpp::GROUP_CUR], q.group_col[mpp::GROUP_BELOW],
+                              q.group_col[mpp::GROUP_SELF_PREV]};
     return MOE_OK;
 }
 
