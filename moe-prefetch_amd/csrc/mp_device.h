@@ -164,6 +164,21 @@ __device__ inline uint64_t sel_key(float v, int id) {
     return ((uint64_t)o << 32) | (uint64_t)(0xffffffffu - (uint32_t)id);
 }
 
+// the score half of sel_key: an order-preserving image of v, every real
+// value above 0 (a NaN equal to -inf, -0 equal to +0)
+__device__ inline uint32_t sel_bits(float v) { return (uint32_t)(sel_key(v, 0) >> 32); }
+
+// unsigned maximum over the wave, on every lane (a uniform value)
+__device__ inline uint32_t wave_max_u32(uint32_t v) {
+    v = max(v, (uint32_t)dpp_i<DPP_XOR1>((int)v));
+    v = max(v, (uint32_t)dpp_i<DPP_XOR2>((int)v));
+    v = max(v, (uint32_t)dpp_i<DPP_HALF_MIRROR>((int)v));
+    v = max(v, (uint32_t)dpp_i<DPP_MIRROR>((int)v));
+    const uint32_t a = __builtin_amdgcn_readlane(v, 0), b = __builtin_amdgcn_readlane(v, 16);
+    const uint32_t c = __builtin_amdgcn_readlane(v, 32), d = __builtin_amdgcn_readlane(v, 48);
+    return max(max(a, b), max(c, d));
+}
+
 // rank of `key` among n keys in LDS (the count of keys above it)
 __device__ inline int key_rank(const uint64_t *s_key, int n, uint64_t key) {
     int rank = 0;

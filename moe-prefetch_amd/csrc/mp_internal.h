@@ -150,7 +150,11 @@ struct JoinArgs {
 // is valid once its tag is the token's number, so nothing is reset between
 // tokens.  Workgroups in index order: [0, E) router rows, the selection,
 // gate/up row tiles, down row tiles, combine tiles; a workgroup waits only
-// for words of workgroups with a lower index.
+// for words of workgroups with a lower index.  The gate/up workgroups route
+// the token themselves from the posted logits (the selection's code, so the
+// same ids), which spares them the wait for the selection's record; the
+// down and combine workgroups read the record.
+constexpr int FUSED_LOG_COPIES = 8; // copies of the posted logits (fewer readers per line)
 constexpr int FUSED_COPIES = 16;    // copies of the routing record (fewer readers per line)
 constexpr int FUSED_REC = 32;       // words per copy: [k] sc_tag(seq, slot, id) of routed expert k,
                                     // [16 + k] (seq << 32) | bits of its gate weight
@@ -161,17 +165,16 @@ struct FusedArgs {
     ExpertArgs x;             // the experts; x.ids/slots/w receive the selection.  x.ypart set: the down
                               // rows go there for the join kernel (CPU-assisted serving) and there is
                               // no combine; else combine workgroups write x.out
-    uint64_t *xlog;           // [256] tagged logits (bias added)
+    uint64_t *xlog;           // [FUSED_LOG_COPIES][256] tagged logits (bias added)
     uint64_t *rec;            // [FUSED_COPIES][FUSED_REC] tagged routing words
-    uint64_t *hflag;          // [K + 1][I / FUSED_GU_TILE] tagged: gate/up tile t of expert k has stored its h
-    float *h;                 // [K + 1][I] SwiGLU activations (agent-scope stores, read after the tile's flag)
+    uint64_t *hx;             // [K + 1][I] tagged SwiGLU activations
     uint64_t *yx;             // [K + 1][H] tagged down rows
     uint32_t *err;            // a bounded wait ran out: the token's sequence number is written here
     uint64_t wait_ticks;      // bound of every wait, 100 MHz wall clock
 };
 // exchange words per layer of the fused decode
 inline size_t fused_words(int K, int I, int H) {
-    return 256 + (size_t)FUSED_COPIES * FUSED_REC + (size_t)(K + 1) * (I / FUSED_GU_TILE) + (size_t)(K + 1) * I / 2 +
+    return (size_t)FUSED_LOG_COPIES * 256 + (size_t)FUSED_COPIES * FUSED_REC + (size_t)(K + 1) * I +
            (size_t)(K + 1) * H;
 }
 

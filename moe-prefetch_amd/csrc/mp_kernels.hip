@@ -536,11 +536,56 @@ __device__ inline void wave_lds_sync() {
 // down + combine.  Workgroup = 8 waves, 8 output rows; wave w owns expert
 // kb + w of each group of 8 experts.
 constexpr int DN_ROWS = 8;
-constexpr int DN_LDS_ROWS = 5040;           // 8 Q6_K rows at I = 768
+constexpr int Q6K_PAD = 224;                // a Q6_K block's stride in LDS (16-byte aligned)
+constexpr int DN_LDS_ROWS = 8 * 3 * Q6K_PAD;   // 8 padded Q6_K rows at I = 768
 constexpr int DN_LDS_Q8 = 3 * Q8K_BYTES;    // I <= 768
 
-// One wave's 8 down rows (LDS, lane-contiguous as loaded: row g of the tile
-// at g * rowb) against the Q8_K blocks of h (LDS): lane (g, u) works on row g,
+// Q6_K rows into LDS with every 210-byte block at a 224-byte stride, so that
+// the dot's 8-byte LDS reads are aligned (at the blocks' own 2-byte
+// alignment they run about four times slower under load).  One wave moves
+// n_blocks blocks (<= 24: 8 rows at I = 768) from `src` (the rows
+// contiguous, so block n at n * 210): chunk c of the padded layout, 16
+// bytes, is block c / 14 from byte 16 (c % 14) -- except the 14th chunk of a
+// block, which only carries the block's last two bytes (its fp16 scale) and
+// is read as the block's last 16 bytes, so no read passes the block's end.
+// q6k_rows_load issues the loads; q6k_rows_store writes LDS and, with
+// `stage`, the same bytes to the staging copy at their own offsets.
+struct Q6Rows {
+    uint4 v[6];
+};
+__device__ inline void q6k_rows_load(Q6Rows &r, const uint8_t *src, int n_blocks, int lane) {
+#pragma unroll
+    for (int i = 0; i < 6; ++i) {
+        const int c = lane + 64 * i;
+        r.v[i] = make_uint4(0, 0, 0, 0);
+        if (src && c < 14 * n_blocks) {
+            const int n = c / 14, j = c - 14 * n;
+            const uint8_t *p = src + (size_t)n * Q6K_BYTES + (j < 13 ? 16 * j : Q6K_BYTES - 16);
+            __builtin_memcpy(&r.v[i], __builtin_assume_aligned(p, 2), 16);
+        }
+    }
+}
+__device__ inline void q6k_rows_store(const Q6Rows &r, uint8_t *s_dst, uint8_t *stage, int n_blocks, int lane) {
+#pragma unroll
+    for (int i = 0; i < 6; ++i) {
+        const int c = lane + 64 * i;
+        if (c < 14 * n_blocks) {
+            const int n = c / 14, j = c - 14 * n;
+            if (j < 13) {
+                *(uint4 *)(s_dst + 16 * c) = r.v[i];
+                if (stage) __builtin_memcpy(__builtin_assume_aligned(stage + (size_t)n * Q6K_BYTES + 16 * j, 2), &r.v[i], 16);
+            } else {
+                const uint16_t d = (uint16_t)(r.v[i].w >> 16);
+                *(uint16_t *)(s_dst + 16 * c) = d;
+                if (stage) *(uint16_t *)(stage + (size_t)n * Q6K_BYTES + Q6K_BYTES - 2) = d;
+            }
+        }
+    }
+}
+
+// One wave's 8 down rows (LDS: row g of the tile at g * rowb; Q4_K rows
+// lane-contiguous as loaded, Q6_K blocks at the padded stride) against the
+// Q8_K blocks of h (LDS): lane (g, u) works on row g,
 // part u of each super-block; the row's value is complete on lanes with
 // u == 0.  Super-blocks in order, scale term then min term (the CPU vec_dot
 // order).
@@ -567,18 +612,17 @@ __device__ inline float down_rows_dot(const uint8_t *s_wt, const uint8_t *s_q8h,
             d = h2f_dev((uint16_t)(hdr.x & 0xffff)) * dx;
             dm = h2f_dev((uint16_t)(hdr.x >> 16)) * dx;
         } else {
-            // a Q6_K block (210 bytes) is only 2-byte aligned: 8-byte LDS
-            // reads at any 2-byte boundary (gfx950 reads LDS unaligned)
-            const uint8_t *blk = s_wt + g * rowb + b * Q6K_BYTES;
+            // Q6_K blocks at the padded stride (q6k_rows_store): aligned reads
+            const uint8_t *blk = s_wt + g * rowb + b * Q6K_PAD;
             const int hh = u >> 2, up4 = u & 3;
-            const uint2 va = lds_u64_at2(blk + 64 * hh + 8 * up4);
-            const uint2 vb = lds_u64_at2(blk + 64 * hh + 8 * up4 + 32);
-            const uint2 vh = lds_u64_at2(blk + 128 + 32 * hh + 8 * up4);
-            const uint2 vs = lds_u64_at2(blk + 192 + 8 * hh);             // the half's 8 scales
+            const uint2 va = *(const uint2 *)(blk + 64 * hh + 8 * up4);
+            const uint2 vb = *(const uint2 *)(blk + 64 * hh + 8 * up4 + 32);
+            const uint2 vh = *(const uint2 *)(blk + 128 + 32 * hh + 8 * up4);
+            const uint2 vs = *(const uint2 *)(blk + 192 + 8 * hh);        // the half's 8 scales
             const uint32_t a0 = va.x, a1 = va.y, b0 = vb.x, b1 = vb.y, h0 = vh.x, h1 = vh.y;
             // scale of sub-block (up4 >> 1) + 2 q, q = 0..3: bytes (up4 >> 1) + 2 q of the 8
-            const uint32_t sw = (up4 >> 1) ? ((vs.x >> 8) & 0x00ff00ffu) | (((vs.y >> 8) & 0x00ff00ffu) << 8)
-                                           : (vs.x & 0x00ff00ffu) | ((vs.y & 0x00ff00ffu) << 8);
+            const uint32_t sh = (uint32_t)(up4 >> 1) * 8;
+            const uint32_t sw = ((vs.x >> sh) & 0x00ff00ffu) | (((vs.y >> sh) & 0x00ff00ffu) << 8);
             const int8_t sc[8] = {(int8_t)sw, 0, (int8_t)(sw >> 16), 0, (int8_t)(sw >> 8), 0, (int8_t)(sw >> 24), 0};
             const uint32_t L = 0x0F0F0F0Fu, Hm = 0x30303030u;
             const uint32_t qv[4][2] = {
@@ -671,8 +715,15 @@ __global__ __launch_bounds__(512) void down_kernel(ExpertArgs a) {
             // The others pass through registers on their way to the staging
             // area too.  Each branch quantizes h after issuing its loads.
             uint8_t *sb = SRC != SRC_HBM ? stage_base(a, k) : nullptr;
-            direct = src && !sb;
-            if (direct) {
+            direct = DT == TYPE_Q4K && src && !sb;
+            if (DT == TYPE_Q6K) {
+                Q6Rows rows;
+                q6k_rows_load(rows, (const uint8_t *)src, DN_ROWS * nb, lane);
+                quantize_h();
+                q6k_rows_store(rows, s_w[wave],
+                               sb ? sb + 2ull * a.I * (a.H / QK) * Q4K_BYTES + (size_t)r0 * rowb : nullptr,
+                               DN_ROWS * nb, lane);
+            } else if (direct) {
 #pragma unroll
                 for (int j = 0; j < 5; ++j) {
                     const int i = lane + 64 * j;
@@ -712,7 +763,7 @@ __global__ __launch_bounds__(512) void down_kernel(ExpertArgs a) {
         if (direct) __builtin_amdgcn_s_waitcnt(0x0f70);       // vmcnt(0)
         wave_lds_sync();
         if (mine) {
-            const float y = down_rows_dot<DT>(s_w[wave], s_q8[wave], nb, rowb, lane);
+            const float y = down_rows_dot<DT>(s_w[wave], s_q8[wave], nb, nb * (DT == TYPE_Q6K ? Q6K_PAD : Q4K_BYTES), lane);
             if (u == 0) {
                 s_y[k][g] = y;
                 if (a.ypart && !a.join) a.ypart[(size_t)k * a.H + r0 + g] = y;
@@ -737,8 +788,9 @@ __global__ __launch_bounds__(512) void down_kernel(ExpertArgs a) {
 // tagged words written and read at agent scope (coherent across the XCDs'
 // L2s without a cache write-back or invalidation); every wait is for
 // workgroups of a lower index, which the dispatcher starts first, and is
-// bounded by the wall clock.  The down rows' weights are requested as soon as
-// the routing is known, while the gate/up rows are still being read.
+// bounded by the wall clock.  The gate/up workgroups route the token
+// themselves; the down rows' weights are requested once the selection's
+// record is seen, while the gate/up rows are still being read.
 
 __device__ inline void store_tagged(uint64_t *p, uint64_t v) {
     __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -754,18 +806,19 @@ __device__ inline void fused_late(const FusedArgs &a, uint32_t seq) {
 // LDS of one fused workgroup, shared by the roles (each uses its own part)
 constexpr int FUSED_LDS_W = 4 * DN_LDS_ROWS;                  // down: each wave's 8 weight rows
 constexpr int FUSED_LDS_Q8 = 3 * Q8K_BYTES + 4;               // down: the Q8_K of h (I <= 768)
-constexpr int FUSED_LDS = FUSED_LDS_W + FUSED_LDS_Q8 + 8 * FUSED_REC + 16;
+constexpr int FUSED_LDS_RS = FUSED_LDS_W + FUSED_LDS_Q8 + 8 * FUSED_REC + 16;   // the routing
+constexpr int FUSED_LDS = FUSED_LDS_RS + 2 * 4 * 256 + 16 * 4 + 16;
 
 // The routing record (copy `copy`): wave 0 polls until the words the
-// workgroup needs carry seq -- the K routing words, and with need_w the K gate
-// weights too -- and leaves them in s_rec for the workgroup.  false: the wait
+// workgroup needs carry seq -- the K routing words, or with need_w the K gate
+// weights -- and leaves them in s_rec for the workgroup.  false: the wait
 // ran out (reported through a.err).
 __device__ bool fused_record(const FusedArgs &a, int copy, uint32_t seq, bool need_w, uint64_t *s_rec, int *s_flag) {
     const int K = a.x.K;
     if (threadIdx.x < 64) {
         const int lane = threadIdx.x;
         const uint64_t *src = a.rec + (size_t)copy * FUSED_REC;
-        const bool want = lane < K || (need_w && lane >= 16 && lane < 16 + K);
+        const bool want = need_w ? lane >= 16 && lane < 16 + K : lane < K;
         bool ok = !want;
         uint64_t v = 0;
         int late = 0;
@@ -791,7 +844,7 @@ __device__ bool fused_record(const FusedArgs &a, int copy, uint32_t seq, bool ne
     return !late;
 }
 
-// where routed expert k's bytes are, from the record: an HBM slot, the pinned
+// where routed expert k's bytes are, from the routing words: an HBM slot, the pinned
 // store (absent), or nothing (an id outside the store contributes zero); cpu:
 // the host computes it (absent, rank r among the absent experts in k order
 // with r % den < num)
@@ -799,12 +852,13 @@ struct ExpertSrc {
     const uint8_t *base;
     bool absent, cpu;
 };
-__device__ inline ExpertSrc fused_src(const ExpertArgs &x, const uint64_t *s_rec, int k) {
+template <class Word>          // Word(kk): the routing word of rank kk (sc_tag layout)
+__device__ inline ExpertSrc expert_src(const ExpertArgs &x, int k, Word word) {
     if (k >= x.K) return {x.shared, false, false};
     int rank = 0;
     ExpertSrc r{nullptr, false, false};
     for (int kk = 0; kk <= k; ++kk) {
-        const uint64_t w = s_rec[kk];
+        const uint64_t w = word(kk);
         const int id = (int)(w & 0xffffu), slot = (int)((w >> 16) & 0xffffu);
         const bool res = x.slot_pool && slot < x.n_slots;
         const bool absent = !res && x.host_store && id < x.n_experts;
@@ -821,42 +875,148 @@ __device__ inline ExpertSrc fused_src(const ExpertArgs &x, const uint64_t *s_rec
 }
 
 // router row e: the canonical four-quarter dot, + the steering bias, posted
-// as a tagged word
+// as a tagged word in every copy of the logits
 __device__ void fused_router(const FusedArgs &a, int e, uint32_t seq, uint8_t *smem) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     float *s_q = (float *)smem;
     const float part = router_quarter(a.r.W + (size_t)e * a.r.H, a.r.x, nullptr, a.r.H, wave, lane);
     if (lane == 0) s_q[wave] = part;
     __syncthreads();
-    if (threadIdx.x == 0) {
+    if (threadIdx.x < FUSED_LOG_COPIES) {
         float acc = s_q[0];
 #pragma unroll
         for (int q = 1; q < RL_WAVES; ++q) acc = acc + s_q[q];
         if (a.r.bias) acc = acc + a.r.bias[e];
-        store_tagged(a.xlog + e, tagged(seq, acc));
+        store_tagged(a.xlog + (size_t)threadIdx.x * MAX_E + e, tagged(seq, acc));
     }
 }
 
-// the selection: softmax, prior, top-k and gate weights as route_select_kernel
-// computes them (the same order, so the same bits), from the posted logits;
-// then the outputs, the host's post and the routing record
+// LDS of the in-workgroup routing
+struct RouteScratch {
+    float p[MAX_E];           // the probabilities (kept when asked for)
+    int32_t tbl[MAX_E];       // the layer's id -> slot table
+    int ids[16];              // the ids in rank order
+    int late;
+};
+static_assert(FUSED_LDS_RS + sizeof(RouteScratch) <= FUSED_LDS, "routing LDS");
+static_assert((2048 / QK) * Q8K_BYTES <= FUSED_LDS_W, "gate/up: the Q8_K of x (H = 2048)");
+
+// The routing of the token, as every workgroup that needs it computes it:
+// the same code on the same posted logits (copy `copy`), so the same bits as
+// route_select_kernel -- softmax over 64-expert chunks (each chunk's sum in
+// the canonical order, the chunks added in order), the prior, the score of
+// each expert -- and the n_top best experts, best first, by n_top rounds of
+// a wave-wide maximum of the scores (on a tie the lowest id, as the 64-bit
+// keys order them), each round removing its expert.  Wave 0 polls for the
+// logits and routes while wave 1 reads the table into LDS; one barrier
+// hands the ids (s->ids), the table (s->tbl) and, with want_p, the
+// probabilities (s->p) to the workgroup.  false: the wait for the logits
+// ran out (the caller reports it).
+template <int NC>
+__device__ void route_wave(const FusedArgs &a, uint32_t seq, int copy, RouteScratch *s, bool want_p, int n_top) {
+    const RouteLaunch &r = a.r;
+    const int lane = threadIdx.x & 63;
+    float pr[NC];
+#pragma unroll
+    for (int c = 0; c < NC; ++c) pr[c] = r.prior ? r.prior[64 * c + lane] : 0.0f;
+    const uint64_t *src = a.xlog + (size_t)copy * MAX_E;
+    uint64_t v[NC];
+    bool ok[NC];
+#pragma unroll
+    for (int c = 0; c < NC; ++c) ok[c] = false;
+    int late = 0;
+    const uint64_t t0 = wall_clock64();
+    // one lane polls the last router row's word first (a thousand workgroups
+    // poll these words while the router rows are still being read)
+    bool seen = lane != 0;
+    for (;;) {
+        if (!seen) seen = (uint32_t)(load_tagged(src + r.E - 1) >> 32) == seq;
+        if (__all(seen)) break;
+        if (wall_clock64() - t0 > a.wait_ticks) break;
+        __builtin_amdgcn_s_sleep(1);
+    }
+    for (;;) {
+        bool all = true;
+#pragma unroll
+        for (int c = 0; c < NC; ++c)
+            if (!ok[c]) v[c] = load_tagged(src + 64 * c + lane);
+#pragma unroll
+        for (int c = 0; c < NC; ++c) {
+            if (!ok[c]) ok[c] = (uint32_t)(v[c] >> 32) == seq;
+            all = all && ok[c];
+        }
+        if (__all(all)) break;
+        if (wall_clock64() - t0 > a.wait_ticks) {
+            late = 1;
+            break;
+        }
+        __builtin_amdgcn_s_sleep(1);
+    }
+    if (lane == 0) s->late = late;
+    if (late) return;
+    float l[NC], ex[NC];
+    float m = 0.0f;
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+        l[c] = __uint_as_float((uint32_t)v[c]);
+        const float mc = wave_max(l[c]);
+        m = c == 0 ? mc : fmaxf(m, mc);
+    }
+    float sum = 0.0f;
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+        ex[c] = canon_expf(l[c] - m);
+        const float cs = wave_sum_canon(ex[c]);
+        sum = c == 0 ? cs : sum + cs;
+    }
+    uint32_t u[NC];
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+        const float p = ex[c] / sum;
+        if (want_p) s->p[64 * c + lane] = p;
+        u[c] = sel_bits(!r.prior ? p : (r.prior_on_logits ? l[c] + pr[c] : p + pr[c]));
+    }
+    for (int k = 0; k < n_top; ++k) {
+        uint32_t mx = u[0];
+#pragma unroll
+        for (int c = 1; c < NC; ++c) mx = max(mx, u[c]);
+        mx = wave_max_u32(mx);
+        int id = -1;
+#pragma unroll
+        for (int c = 0; c < NC; ++c) {
+            const uint64_t b = __ballot(u[c] == mx);
+            if (id < 0 && b) id = 64 * c + (int)__builtin_ctzll(b);
+        }
+#pragma unroll
+        for (int c = 0; c < NC; ++c)
+            if (64 * c + lane == id) u[c] = 0;                // below every score
+        if (lane == 0) s->ids[k] = id;
+    }
+}
+__device__ bool fused_route(const FusedArgs &a, uint32_t seq, int copy, RouteScratch *s, bool want_p, int n_top) {
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    if (wave == 1)
+        for (int e = lane; e < a.r.E; e += 64) s->tbl[e] = a.r.table[e];
+    if (wave == 0) {
+        switch (a.r.E >> 6) {
+        case 1: route_wave<1>(a, seq, copy, s, want_p, n_top); break;
+        case 2: route_wave<2>(a, seq, copy, s, want_p, n_top); break;
+        case 3: route_wave<3>(a, seq, copy, s, want_p, n_top); break;
+        default: route_wave<4>(a, seq, copy, s, want_p, n_top); break;
+        }
+    }
+    __syncthreads();
+    return !s->late;
+}
+
+// the selection's outputs: ids, gate weights, slots, the host's post and the
+// routing record the down and combine workgroups read
 __device__ void fused_select(const FusedArgs &a, uint32_t seq, uint8_t *smem) {
     const RouteLaunch &r = a.r;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int nc = r.E / 64;
-    uint64_t *s_key = (uint64_t *)smem;             // 16-byte aligned: read two keys at a time
-    float *s_p = (float *)(s_key + 256);
-    int32_t *s_tbl = (int32_t *)(s_p + 256);
-    float *s_m = (float *)(s_tbl + 256);
-    float *s_cs = s_m + 4;
-    int *s_ids = (int *)(s_cs + 4);
-    int *s_slot = s_ids + 16;
+    RouteScratch *s = (RouteScratch *)(smem + FUSED_LDS_RS);
+    int *s_slot = (int *)smem;
     float *s_w = (float *)(s_slot + 16);
-    int *s_late = (int *)(s_w + 16);
-    int *s_part = s_late + 4;                       // [256] partial ranks
-    if (tid == 0) *s_late = 0;
-    const int32_t tword = tid < r.E ? r.table[tid] : 0;
-    const float pr = (r.prior && tid < r.E) ? r.prior[tid] : 0.0f;
     // Q8_K of x for the host's share of absent experts, written through to
     // host memory (each wave waits for its stores) before the post's words
     if (r.post)
@@ -868,65 +1028,18 @@ __device__ void fused_select(const FusedArgs &a, uint32_t seq, uint8_t *smem) {
             q8k_wave_vals(xv, lane, q, d);
             q8k_store_sys(q, d, (uint32_t *)(r.post->q8x + (size_t)b * Q8K_BYTES), lane);
         }
-    __syncthreads();                            // *s_late cleared before any lane may raise it
-    float l = 0.0f;
-    if (tid < r.E) {
-        const uint64_t t0 = wall_clock64();
-        uint64_t v = 0;
-        for (;;) {
-            v = load_tagged(a.xlog + tid);
-            if ((uint32_t)(v >> 32) == seq) break;
-            if (wall_clock64() - t0 > a.wait_ticks) {
-                *s_late = 1;
-                break;
-            }
-            __builtin_amdgcn_s_sleep(1);
-        }
-        l = __uint_as_float((uint32_t)v);
-        s_tbl[tid] = tword;
+    if (!fused_route(a, seq, 0, s, true, r.K)) {
+        if (tid == 0) fused_late(a, seq);
+        return;
     }
-    if (wave < nc) {
-        const float m = wave_max(l);
-        if (lane == 0) s_m[wave] = m;
-    }
-    __syncthreads();
-    float ex = 0.0f;
-    if (wave < nc) {
-        float m = s_m[0];
-        for (int c = 1; c < nc; ++c) m = fmaxf(m, s_m[c]);
-        ex = canon_expf(l - m);
-        const float cs = wave_sum_canon(ex);
-        if (lane == 0) s_cs[wave] = cs;
-    }
-    __syncthreads();
-    if (wave < nc) {
-        float sum = s_cs[0];
-        for (int c = 1; c < nc; ++c) sum = sum + s_cs[c];
-        const float p = ex / sum;
-        s_p[tid] = p;
-        const float sel = !r.prior ? p : (r.prior_on_logits ? l + pr : p + pr);
-        s_key[tid] = sel_key(sel, tid);                 // a NaN sorts last
-    }
-    __syncthreads();
-    // rank of expert e: experts ahead of it (larger, or equal with a lower
-    // id), counted by all 256 threads, 256 / E parts of the keys each
-    const int parts = 256 / r.E, span = r.E / parts;
-    const int e = tid % r.E, part = tid / r.E;
-    if (part < parts) s_part[tid] = key_rank(s_key + part * span, span, s_key[e]);
-    __syncthreads();
-    if (tid < r.E) {
-        int rank = 0;
-        for (int q = 0; q < parts; ++q) rank += s_part[tid + q * r.E];
-        if (rank < r.K) s_ids[rank] = tid;
-    }
-    __syncthreads();
     if (wave == 0) {
+        const int *ids = s->ids;
         float ws = 0.0f;
-        for (int k = 0; k < r.K; ++k) ws = ws + s_p[s_ids[k]];
+        for (int k = 0; k < r.K; ++k) ws = ws + s->p[ids[k]];
         if (lane < r.K) {
-            const int id = s_ids[lane];
-            const int slot = s_tbl[id];
-            const float w = s_p[id] / ws;
+            const int id = ids[lane];
+            const int slot = s->tbl[id];
+            const float w = s->p[id] / ws;
             r.ids[lane] = id;
             r.w[lane] = w;
             r.slots[lane] = slot;
@@ -938,12 +1051,12 @@ __device__ void fused_select(const FusedArgs &a, uint32_t seq, uint8_t *smem) {
         }
     }
     __syncthreads();
+    const int *ids = s->ids;
     for (int i = tid; i < FUSED_COPIES * FUSED_REC; i += 256) {
         const int k = i % FUSED_REC;
-        if (k < r.K) store_tagged(a.rec + i, sc_tag(seq, s_slot[k], s_ids[k]));
+        if (k < r.K) store_tagged(a.rec + i, sc_tag(seq, s_slot[k], ids[k]));
         else if (k >= 16 && k - 16 < r.K) store_tagged(a.rec + i, tagged(seq, s_w[k - 16]));
     }
-    if (tid == 0 && *s_late) fused_late(a, seq);
 }
 
 // Gate/up rows of routed expert k (or of the shared expert, which needs no
@@ -960,8 +1073,7 @@ __device__ void fused_gateup(const FusedArgs &a, int g, uint32_t seq, uint8_t *s
     const int per = x.I / FUSED_GU_TILE;
     const int k = g / per, tile = g - k * per;
     uint8_t *s_q8x = smem;                                          // [H / 256][292]
-    uint64_t *s_rec = (uint64_t *)(smem + FUSED_LDS_W + FUSED_LDS_Q8);
-    int *s_flag = (int *)(s_rec + FUSED_REC);
+    RouteScratch *rs = (RouteScratch *)(smem + FUSED_LDS_RS);
     for (int b = wave; b < x.H / QK; b += 4) {         // the bytes route_logits_kernel writes
         const float4 v = *(const float4 *)(a.r.x + QK * b + 4 * lane);
         const float xv[4] = {v.x, v.y, v.z, v.w};
@@ -971,9 +1083,14 @@ __device__ void fused_gateup(const FusedArgs &a, int g, uint32_t seq, uint8_t *s
         q8k_store(q, d, s_q8x + b * Q8K_BYTES, lane);
     }
     ExpertSrc src{x.shared, false, false};
-    if (k < x.K) {                                     // (fused_record's barrier orders the LDS writes)
-        if (!fused_record(a, g % FUSED_COPIES, seq, false, s_rec, s_flag)) return;
-        src = fused_src(x, s_rec, k);
+    if (k < x.K) {                                     // (fused_route's barrier orders the LDS writes)
+        if (!fused_route(a, seq, g % FUSED_LOG_COPIES, rs, false, k + 1)) {
+            if (threadIdx.x == 0) fused_late(a, seq);
+            return;
+        }
+        const int *ids = rs->ids;
+        const int32_t *tbl = rs->tbl;
+        src = expert_src(x, k, [ids, tbl](int kk) { return sc_tag(0, tbl[ids[kk]], ids[kk]); });
         if (src.cpu) return;
     } else {
         __syncthreads();
@@ -1032,16 +1149,8 @@ __device__ void fused_gateup(const FusedArgs &a, int g, uint32_t seq, uint8_t *s
         if (b == sb) acc = (prev + t) - m;                         // row_shr:1 -- the lane below
     }
     const float upv = __shfl(acc, lane + 32, 64);                  // row i's up sum, for the gate lanes
-    if (is_gate && b == 7) {
-        const float gv = acc;
-        __hip_atomic_store(a.h + (size_t)k * x.I + row, gv / (1.0f + canon_expf(-gv)) * upv, __ATOMIC_RELAXED,
-                           __HIP_MEMORY_SCOPE_AGENT);
-    }
-    // the tile's flag once every wave's h stores have completed (written
-    // through at agent scope: no cache write-back needed)
-    __builtin_amdgcn_s_waitcnt(0x0f70);                            // vmcnt(0)
-    __syncthreads();
-    if (threadIdx.x == 0) store_tagged(a.hflag + (size_t)k * (x.I / FUSED_GU_TILE) + tile, tagged(seq, 0.0f));
+    if (is_gate && b == 7)
+        store_tagged(a.hx + (size_t)k * x.I + row, tagged(seq, acc / (1.0f + canon_expf(-acc)) * upv));
 }
 
 // FUSED_DN_TILE down rows of expert k, 8 per wave: the weights into LDS as
@@ -1060,8 +1169,11 @@ __device__ void fused_down(const FusedArgs &a, int g, uint32_t seq, uint8_t *sme
     int *s_flag = (int *)(s_rec + FUSED_REC);
     ExpertSrc src{x.shared, false, false};
     if (k < x.K) {
+        // the selection's record (the down rows' weights are not needed
+        // before h, and requested later they leave the memory system to the
+        // gate/up rows first)
         if (!fused_record(a, g % FUSED_COPIES, seq, false, s_rec, s_flag)) return;
-        src = fused_src(x, s_rec, k);
+        src = expert_src(x, k, [s_rec](int kk) { return s_rec[kk]; });
         if (src.cpu) return;
     }
     const int nb = x.I / QK;
@@ -1071,13 +1183,18 @@ __device__ void fused_down(const FusedArgs &a, int g, uint32_t seq, uint8_t *sme
     const size_t dn_off = 2ull * x.I * (x.H / QK) * Q4K_BYTES + (size_t)r0 * rowb;
     const uint4 *wsrc = src.base ? (const uint4 *)(src.base + dn_off) : nullptr;
     uint8_t *sb = src.absent && x.stage ? x.stage + (size_t)k * x.stage_stride + dn_off : nullptr;
-    // The weights first, straight into LDS (16 bytes a lane, lane-contiguous)
-    // and all by the last wave: a wave's loads return in the order they were
-    // issued, so the waves that poll for h must not have weights queued ahead
-    // of their polls.  Rows that are also staged pass through registers, each
-    // wave its own 8.
+    // The weights first.  Q4_K rows go straight into LDS (16 bytes a lane,
+    // lane-contiguous), all by the last wave: a wave's loads return in the
+    // order they were issued, so the waves that poll for h must not have
+    // weights queued ahead of their polls.  Rows that are also staged pass
+    // through registers, each wave its own 8; so do Q6_K rows, which LDS
+    // holds at the padded block stride (q6k_rows_load).
     uint4 buf[5];
-    if (wsrc && !sb) {
+    Q6Rows q6;
+    if (DT == TYPE_Q6K) {
+        // each wave its own 8 rows, through registers into the padded layout
+        q6k_rows_load(q6, (const uint8_t *)wsrc, 8 * nb, lane);
+    } else if (wsrc && !sb) {
         if (wave == 3) {
             const uint4 *w0 = (const uint4 *)(src.base + 2ull * x.I * (x.H / QK) * Q4K_BYTES +
                                               (size_t)tile * FUSED_DN_TILE * rowb);
@@ -1099,17 +1216,32 @@ __device__ void fused_down(const FusedArgs &a, int g, uint32_t seq, uint8_t *sme
             buf[j] = i < nvec ? wsrc[i] : make_uint4(0, 0, 0, 0);
         }
     }
-    // h of expert k, block `wave`: once the flags of all the expert's gate/up
-    // tiles carry seq, the block's values (four a lane)
+    // h of expert k, block `wave`: its four words a lane, once each carries
+    // seq.  Until then the wave polls only the last row of each of the
+    // block's 16 gate/up tiles (16 words, not 256: thousands of waves poll
+    // at once, and their reads share the memory system with the weights)
     if (wave < nb) {
-        const int nt = x.I / FUSED_GU_TILE;            // <= 48 tiles
-        const uint64_t *fp = a.hflag + (size_t)k * nt;
-        bool ok = lane >= nt;
+        const uint64_t *hb = a.hx + (size_t)k * x.I + QK * wave;
+        const uint64_t *hp = hb + 4 * lane;
+        uint64_t hv[4] = {0, 0, 0, 0};
+        uint32_t pending = 0xfu;
         int late = 0;
         const uint64_t t0 = wall_clock64();
+        bool seen = lane >= QK / FUSED_GU_TILE;
         for (;;) {
-            if (!ok) ok = (uint32_t)(load_tagged(fp + lane) >> 32) == seq;
-            if (__all(ok)) break;
+            if (!seen) seen = (uint32_t)(load_tagged(hb + FUSED_GU_TILE * lane + FUSED_GU_TILE - 1) >> 32) == seq;
+            if (__all(seen)) break;
+            if (wall_clock64() - t0 > a.wait_ticks) break;
+            __builtin_amdgcn_s_sleep(1);
+        }
+        for (;;) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                if (pending >> j & 1u) hv[j] = load_tagged(hp + j);
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                if ((pending >> j & 1u) && (uint32_t)(hv[j] >> 32) == seq) pending &= ~(1u << j);
+            if (__all(pending == 0)) break;
             if (wall_clock64() - t0 > a.wait_ticks) {
                 late = 1;
                 break;
@@ -1117,16 +1249,16 @@ __device__ void fused_down(const FusedArgs &a, int g, uint32_t seq, uint8_t *sme
             __builtin_amdgcn_s_sleep(1);
         }
         if (late && lane == 0) fused_late(a, seq);
-        const uint64_t *hp = (const uint64_t *)(a.h + (size_t)k * x.I + QK * wave + 4 * lane);
-        const uint64_t h01 = load_tagged(hp), h23 = load_tagged(hp + 1);   // two values per word
-        const float xv[4] = {__uint_as_float((uint32_t)h01), __uint_as_float((uint32_t)(h01 >> 32)),
-                             __uint_as_float((uint32_t)h23), __uint_as_float((uint32_t)(h23 >> 32))};
+        const float xv[4] = {__uint_as_float((uint32_t)hv[0]), __uint_as_float((uint32_t)hv[1]),
+                             __uint_as_float((uint32_t)hv[2]), __uint_as_float((uint32_t)hv[3])};
         int q[4];
         float d;
         q8k_wave_vals(xv, lane, q, d);
         q8k_store(q, d, s_q8h + wave * Q8K_BYTES, lane);
     }
-    if (wsrc && !sb) {
+    if (DT == TYPE_Q6K) {
+        if (wsrc) q6k_rows_store(q6, s_wt, sb, 8 * nb, lane);
+    } else if (wsrc && !sb) {
         if (wave == 3) __builtin_amdgcn_s_waitcnt(0x0f70);      // vmcnt(0): the weights have landed in LDS
     } else if (wsrc) {
         uint4 *dst = (uint4 *)s_wt;
@@ -1143,7 +1275,7 @@ __device__ void fused_down(const FusedArgs &a, int g, uint32_t seq, uint8_t *sme
         }
     }
     __syncthreads();                // the Q8_K blocks of h and every wave's weights
-    const float y = wsrc ? down_rows_dot<DT>(s_wt, s_q8h, nb, rowb, lane) : 0.0f;
+    const float y = wsrc ? down_rows_dot<DT>(s_wt, s_q8h, nb, nb * (DT == TYPE_Q6K ? Q6K_PAD : Q4K_BYTES), lane) : 0.0f;
     if ((lane & 7) == 0) {
         const int row = r0 + (lane >> 3);
         if (x.ypart) x.ypart[(size_t)k * x.H + row] = y;

@@ -2376,10 +2376,9 @@ static int decode_layer_impl(moe_cache *c, int layer, const float *x, const floa
         f.x = a;
         f.x.ypart = sidecar ? c->ypart : nullptr;       // the join kernel combines with the host's rows
         f.xlog = c->fx + (size_t)layer * c->fx_words;
-        f.rec = f.xlog + 256;
-        f.hflag = f.rec + (size_t)mp::FUSED_COPIES * mp::FUSED_REC;
-        f.h = (float *)(f.hflag + (size_t)(c->K + 1) * (c->I / mp::FUSED_GU_TILE));
-        f.yx = (uint64_t *)(f.h + (size_t)(c->K + 1) * c->I);
+        f.rec = f.xlog + (size_t)mp::FUSED_LOG_COPIES * 256;
+        f.hx = f.rec + (size_t)mp::FUSED_COPIES * mp::FUSED_REC;
+        f.yx = f.hx + (size_t)(c->K + 1) * c->I;
         f.err = (uint32_t *)(c->d_ids + c->L.size() * (size_t)c->K);
         f.wait_ticks = (uint64_t)(c->fused_wait_s * 1e8);
         HIPCHK(mp::launch_fused(f, st, E_(0), E_(1)));
