@@ -807,7 +807,7 @@ __device__ inline void fused_late(const FusedArgs &a, uint32_t seq) {
 constexpr int FUSED_LDS_W = 4 * DN_LDS_ROWS;                  // down: each wave's 8 weight rows
 constexpr int FUSED_LDS_Q8 = 3 * Q8K_BYTES + 4;               // down: the Q8_K of h (I <= 768)
 constexpr int FUSED_LDS_RS = FUSED_LDS_W + FUSED_LDS_Q8 + 8 * FUSED_REC + 16;   // the routing
-constexpr int FUSED_LDS = FUSED_LDS_RS + 2 * 4 * 256 + 16 * 4 + 16;
+constexpr int FUSED_LDS = FUSED_LDS_RS + 256;
 
 // The routing record (copy `copy`): wave 0 polls until the words the
 // workgroup needs carry seq -- the K routing words, or with need_w the K gate
@@ -852,24 +852,29 @@ struct ExpertSrc {
     const uint8_t *base;
     bool absent, cpu;
 };
+// one routed expert in rank order (id, its table word as 16 bits): the
+// source if it is rank k, else its count among the absent ranks before k
+__device__ inline void expert_src_step(const ExpertArgs &x, int id, int slot16, bool is_k, int &absent_before,
+                                       ExpertSrc &r) {
+    const bool res = x.slot_pool && slot16 < x.n_slots;
+    const bool absent = !res && x.host_store && id < x.n_experts;
+    if (!is_k) {
+        absent_before += absent;
+        return;
+    }
+    r.absent = absent;
+    r.cpu = x.cpu_den > 0 && absent && absent_before % x.cpu_den < x.cpu_num;
+    r.base = res ? x.slot_pool + (size_t)slot16 * x.slot_bytes
+                 : absent ? x.host_store + (size_t)id * x.expert_bytes : nullptr;
+}
 template <class Word>          // Word(kk): the routing word of rank kk (sc_tag layout)
 __device__ inline ExpertSrc expert_src(const ExpertArgs &x, int k, Word word) {
     if (k >= x.K) return {x.shared, false, false};
-    int rank = 0;
+    int absent_before = 0;
     ExpertSrc r{nullptr, false, false};
     for (int kk = 0; kk <= k; ++kk) {
         const uint64_t w = word(kk);
-        const int id = (int)(w & 0xffffu), slot = (int)((w >> 16) & 0xffffu);
-        const bool res = x.slot_pool && slot < x.n_slots;
-        const bool absent = !res && x.host_store && id < x.n_experts;
-        if (kk < k) {
-            rank += absent;
-        } else {
-            r.absent = absent;
-            r.cpu = x.cpu_den > 0 && absent && rank % x.cpu_den < x.cpu_num;
-            if (res) r.base = x.slot_pool + (size_t)slot * x.slot_bytes;
-            else if (absent) r.base = x.host_store + (size_t)id * x.expert_bytes;
-        }
+        expert_src_step(x, (int)(w & 0xffffu), (int)((w >> 16) & 0xffffu), kk == k, absent_before, r);
     }
     return r;
 }
@@ -891,11 +896,13 @@ __device__ void fused_router(const FusedArgs &a, int e, uint32_t seq, uint8_t *s
     }
 }
 
-// LDS of the in-workgroup routing
+// LDS of the in-workgroup routing (written by wave 0)
 struct RouteScratch {
-    float p[MAX_E];           // the probabilities (kept when asked for)
-    int32_t tbl[MAX_E];       // the layer's id -> slot table
+    ExpertSrc src;            // the workgroup's expert (rank want_k)
     int ids[16];              // the ids in rank order
+    int slots[16];            // their table words
+    float psel[16];           // their probabilities
+    float ws;                 // the sum of those, in rank order
     int late;
 };
 static_assert(FUSED_LDS_RS + sizeof(RouteScratch) <= FUSED_LDS, "routing LDS");
@@ -907,18 +914,24 @@ static_assert((2048 / QK) * Q8K_BYTES <= FUSED_LDS_W, "gate/up: the Q8_K of x (H
 // the canonical order, the chunks added in order), the prior, the score of
 // each expert -- and the n_top best experts, best first, by n_top rounds of
 // a wave-wide maximum of the scores (on a tie the lowest id, as the 64-bit
-// keys order them), each round removing its expert.  Wave 0 polls for the
-// logits and routes while wave 1 reads the table into LDS; one barrier
-// hands the ids (s->ids), the table (s->tbl) and, with want_p, the
-// probabilities (s->p) to the workgroup.  false: the wait for the logits
-// ran out (the caller reports it).
+// keys order them), each round removing its expert.  Wave 0 alone polls
+// and routes; every round's expert is a uniform value, so its table word,
+// its probability and (want_k >= 0) the source of rank want_k follow from
+// lane reads of registers, with no LDS round trip.  One barrier hands s to
+// the workgroup.  false: the wait for the logits ran out (the caller
+// reports it).
 template <int NC>
-__device__ void route_wave(const FusedArgs &a, uint32_t seq, int copy, RouteScratch *s, bool want_p, int n_top) {
+__device__ void route_wave(const FusedArgs &a, uint32_t seq, int copy, RouteScratch *s, int n_top, int want_k) {
     const RouteLaunch &r = a.r;
+    const ExpertArgs &x = a.x;
     const int lane = threadIdx.x & 63;
     float pr[NC];
+    int32_t tbl[NC];
 #pragma unroll
-    for (int c = 0; c < NC; ++c) pr[c] = r.prior ? r.prior[64 * c + lane] : 0.0f;
+    for (int c = 0; c < NC; ++c) {
+        pr[c] = r.prior ? r.prior[64 * c + lane] : 0.0f;
+        tbl[c] = r.table[64 * c + lane];
+    }
     const uint64_t *src = a.xlog + (size_t)copy * MAX_E;
     uint64_t v[NC];
     bool ok[NC];
@@ -926,15 +939,6 @@ __device__ void route_wave(const FusedArgs &a, uint32_t seq, int copy, RouteScra
     for (int c = 0; c < NC; ++c) ok[c] = false;
     int late = 0;
     const uint64_t t0 = wall_clock64();
-    // one lane polls the last router row's word first (a thousand workgroups
-    // poll these words while the router rows are still being read)
-    bool seen = lane != 0;
-    for (;;) {
-        if (!seen) seen = (uint32_t)(load_tagged(src + r.E - 1) >> 32) == seq;
-        if (__all(seen)) break;
-        if (wall_clock64() - t0 > a.wait_ticks) break;
-        __builtin_amdgcn_s_sleep(1);
-    }
     for (;;) {
         bool all = true;
 #pragma unroll
@@ -954,7 +958,7 @@ __device__ void route_wave(const FusedArgs &a, uint32_t seq, int copy, RouteScra
     }
     if (lane == 0) s->late = late;
     if (late) return;
-    float l[NC], ex[NC];
+    float l[NC], ex[NC], p[NC];
     float m = 0.0f;
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
@@ -972,10 +976,12 @@ __device__ void route_wave(const FusedArgs &a, uint32_t seq, int copy, RouteScra
     uint32_t u[NC];
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
-        const float p = ex[c] / sum;
-        if (want_p) s->p[64 * c + lane] = p;
-        u[c] = sel_bits(!r.prior ? p : (r.prior_on_logits ? l[c] + pr[c] : p + pr[c]));
+        p[c] = ex[c] / sum;
+        u[c] = sel_bits(!r.prior ? p[c] : (r.prior_on_logits ? l[c] + pr[c] : p[c] + pr[c]));
     }
+    float ws = 0.0f;
+    int absent_before = 0;
+    ExpertSrc mine{nullptr, false, false};
     for (int k = 0; k < n_top; ++k) {
         uint32_t mx = u[0];
 #pragma unroll
@@ -990,19 +996,34 @@ __device__ void route_wave(const FusedArgs &a, uint32_t seq, int copy, RouteScra
 #pragma unroll
         for (int c = 0; c < NC; ++c)
             if (64 * c + lane == id) u[c] = 0;                // below every score
-        if (lane == 0) s->ids[k] = id;
+        int32_t slot = 0;
+        float pk = 0.0f;
+#pragma unroll
+        for (int c = 0; c < NC; ++c)
+            if ((id >> 6) == c) {
+                slot = __builtin_amdgcn_readlane(tbl[c], id & 63);
+                pk = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(p[c]), id & 63));
+            }
+        if (want_k >= 0) expert_src_step(x, id, (int)(uint16_t)slot, k == want_k, absent_before, mine);
+        ws = ws + pk;
+        if (lane == 0) {
+            s->ids[k] = id;
+            s->slots[k] = slot;
+            s->psel[k] = pk;
+        }
+    }
+    if (lane == 0) {
+        s->ws = ws;
+        s->src = mine;
     }
 }
-__device__ bool fused_route(const FusedArgs &a, uint32_t seq, int copy, RouteScratch *s, bool want_p, int n_top) {
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    if (wave == 1)
-        for (int e = lane; e < a.r.E; e += 64) s->tbl[e] = a.r.table[e];
-    if (wave == 0) {
+__device__ bool fused_route(const FusedArgs &a, uint32_t seq, int copy, RouteScratch *s, int n_top, int want_k) {
+    if ((threadIdx.x >> 6) == 0) {
         switch (a.r.E >> 6) {
-        case 1: route_wave<1>(a, seq, copy, s, want_p, n_top); break;
-        case 2: route_wave<2>(a, seq, copy, s, want_p, n_top); break;
-        case 3: route_wave<3>(a, seq, copy, s, want_p, n_top); break;
-        default: route_wave<4>(a, seq, copy, s, want_p, n_top); break;
+        case 1: route_wave<1>(a, seq, copy, s, n_top, want_k); break;
+        case 2: route_wave<2>(a, seq, copy, s, n_top, want_k); break;
+        case 3: route_wave<3>(a, seq, copy, s, n_top, want_k); break;
+        default: route_wave<4>(a, seq, copy, s, n_top, want_k); break;
         }
     }
     __syncthreads();
@@ -1028,18 +1049,15 @@ __device__ void fused_select(const FusedArgs &a, uint32_t seq, uint8_t *smem) {
             q8k_wave_vals(xv, lane, q, d);
             q8k_store_sys(q, d, (uint32_t *)(r.post->q8x + (size_t)b * Q8K_BYTES), lane);
         }
-    if (!fused_route(a, seq, 0, s, true, r.K)) {
+    if (!fused_route(a, seq, 0, s, r.K, -1)) {
         if (tid == 0) fused_late(a, seq);
         return;
     }
     if (wave == 0) {
-        const int *ids = s->ids;
-        float ws = 0.0f;
-        for (int k = 0; k < r.K; ++k) ws = ws + s->p[ids[k]];
         if (lane < r.K) {
-            const int id = ids[lane];
-            const int slot = s->tbl[id];
-            const float w = s->p[id] / ws;
+            const int id = s->ids[lane];
+            const int slot = s->slots[lane];
+            const float w = s->psel[lane] / s->ws;
             r.ids[lane] = id;
             r.w[lane] = w;
             r.slots[lane] = slot;
@@ -1084,13 +1102,11 @@ __device__ void fused_gateup(const FusedArgs &a, int g, uint32_t seq, uint8_t *s
     }
     ExpertSrc src{x.shared, false, false};
     if (k < x.K) {                                     // (fused_route's barrier orders the LDS writes)
-        if (!fused_route(a, seq, g % FUSED_LOG_COPIES, rs, false, k + 1)) {
+        if (!fused_route(a, seq, g % FUSED_LOG_COPIES, rs, k + 1, k)) {
             if (threadIdx.x == 0) fused_late(a, seq);
             return;
         }
-        const int *ids = rs->ids;
-        const int32_t *tbl = rs->tbl;
-        src = expert_src(x, k, [ids, tbl](int kk) { return sc_tag(0, tbl[ids[kk]], ids[kk]); });
+        src = rs->src;
         if (src.cpu) return;
     } else {
         __syncthreads();
