@@ -265,11 +265,12 @@ __device__ inline void q4_scales(const uint4 &hdr, int h, Q4Scales &o) {
     }
 }
 
-// Q6_K B operands of one super-block for the lane's row (bytes in LDS, rows
-// only 2-byte aligned): MFMA 4*hh + g covers elements 128*hh + 32*g + 8*h .. +7
-// with sc = scales[8*hh + (h >> 1) + 2*g].  (q - 32) * sc reaches 4096, past
-// fp16's exact integers, so sc = 16*sh + sl splits it into two exact operands
-// (|(q-32)*sh| <= 256, (q-32)*sl <= 480): sumi = 16*acc_h + acc_l.
+// Q6_K B operands of one super-block for the lane's row (bytes in LDS at the
+// padded block stride, q6k_rows_store: aligned reads): MFMA 4*hh + g covers
+// elements 128*hh + 32*g + 8*h .. +7 with sc = scales[8*hh + (h >> 1) + 2*g].
+// (q - 32) * sc reaches 4096, past fp16's exact integers, so sc = 16*sh + sl
+// splits it into two exact operands (|(q-32)*sh| <= 256, (q-32)*sl <= 480):
+// sumi = 16*acc_h + acc_l.
 __device__ inline void q6_frag(const uint8_t *blk, int h, half8_t bh[8], half8_t bl[8], float &d) {
     d = h2f_dev(*(const uint16_t *)(blk + 208));
     const uint32_t M = 0x0F0F0F0Fu, HM = 0x30303030u;
@@ -277,7 +278,9 @@ __device__ inline void q6_frag(const uint8_t *blk, int h, half8_t bh[8], half8_t
 #pragma unroll
     for (int hh = 0; hh < 2; ++hh) {
         const uint8_t *pa = blk + 64 * hh + 8 * h;
-        const uint2 va = lds_u64_at2(pa), vb = lds_u64_at2(pa + 32), vq = lds_u64_at2(blk + 128 + 32 * hh + 8 * h);
+        const uint2 va = *(const uint2 *)pa, vb = *(const uint2 *)(pa + 32);
+        const uint2 vq = *(const uint2 *)(blk + 128 + 32 * hh + 8 * h);
+        const uint2 vs = *(const uint2 *)(blk + 192 + 8 * hh);          // the half's 8 scales
         const uint32_t a0 = va.x, a1 = va.y, b0 = vb.x, b1 = vb.y, q0 = vq.x, q1 = vq.y;
         const uint32_t w[4][2] = {{(a0 & M) | ((q0 << 4) & HM), (a1 & M) | ((q1 << 4) & HM)},
                                   {(b0 & M) | ((q0 << 2) & HM), (b1 & M) | ((q1 << 2) & HM)},
@@ -285,7 +288,8 @@ __device__ inline void q6_frag(const uint8_t *blk, int h, half8_t bh[8], half8_t
                                   {((b0 >> 4) & M) | ((q0 >> 2) & HM), ((b1 >> 4) & M) | ((q1 >> 2) & HM)}};
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
-            const int sc = (int)(int8_t)blk[192 + 8 * hh + (h >> 1) + 2 * g];
+            const int j = (h >> 1) + 2 * g;                                   // byte j of the 8
+            const int sc = (int)(int8_t)(uint8_t)((j < 4 ? vs.x : vs.y) >> (8 * (j & 3)));
             const half8_t q = pack_1024(w[g][0], w[g][1]) - c1056;          // q - 32, exact
             bh[4 * hh + g] = q * splat8((_Float16)(float)(sc >> 4));        // arithmetic shift: -8 .. 7
             bl[4 * hh + g] = q * splat8((_Float16)(float)(sc & 15));
@@ -331,7 +335,7 @@ __device__ inline half8_t stage_frag(const AStage &st, int r, int off) {
     return *(const half8_t *)&st.a[r][8 * c];
 }
 
-constexpr int G6_LDS = 64 * 3 * Q6K_BYTES;   // 64 Q6_K rows at K <= 768
+constexpr int G6_LDS = 64 * 3 * Q6K_PAD;     // 64 padded Q6_K rows at K <= 768
 
 // Workgroup -> (row tile, expert).  Workgroups go to the 8 XCDs round-robin
 // (workgroup L on XCD L % 8); with E a multiple of 8, every row tile of
@@ -392,14 +396,17 @@ __global__ __launch_bounds__(256, 4) void grouped_gemm_kernel(GroupedArgs a) {
     __shared__ __attribute__((aligned(16))) uint8_t s_w6[DT == TYPE_Q6K ? G6_LDS : 16];
 
     const uint8_t *wrow = mat + (size_t)row * ROWB;   // the lane's Q4_K row
+    constexpr int LROWB = NB * Q6K_PAD;               // a padded Q6_K row in LDS
     if (DT == TYPE_Q6K) {
-        // 64 rows * ROWB bytes from a 16-byte aligned start (64 * 210 = 840 * 16)
-        const uint8_t *src = mat + (size_t)r0 * ROWB;
-        constexpr int NV = 64 * ROWB / 16;
-        for (int c0 = 64 * wave; c0 < NV; c0 += 256) {
-            if (c0 + lane < NV)
-                __builtin_amdgcn_global_load_lds((gptr_t *)(src + 16 * (c0 + lane)), (lptr_t *)(s_w6 + 16 * c0), 16,
-                                                 0, 0);
+        // the wave's 16 rows into LDS at the padded block stride, 24 blocks
+        // (16 * NB <= 48) at a time through registers
+        const uint8_t *src = mat + (size_t)(r0 + 16 * wave) * ROWB;
+        uint8_t *dst = s_w6 + (size_t)(16 * wave) * LROWB;
+        for (int b0 = 0; b0 < 16 * NB; b0 += 24) {
+            const int nbk = min(24, 16 * NB - b0);
+            Q6Rows rows;
+            q6k_rows_load(rows, src + (size_t)b0 * Q6K_BYTES, nbk, lane);
+            q6k_rows_store(rows, dst + (size_t)b0 * Q6K_PAD, nullptr, nbk, lane);
         }
     }
 
@@ -457,7 +464,7 @@ __global__ __launch_bounds__(256, 4) void grouped_gemm_kernel(GroupedArgs a) {
                 }
             } else {
                 half8_t bh[8], bl[8];
-                q6_frag(s_w6 + (size_t)(wave * 16 + n) * ROWB + (size_t)s * Q6K_BYTES, h, bh, bl, d);
+                q6_frag(s_w6 + (size_t)(wave * 16 + n) * LROWB + (size_t)s * Q6K_PAD, h, bh, bl, d);
                 float4_t accl[2] = {{0, 0, 0, 0}, {0, 0, 0, 0}};
 #pragma unroll
                 for (int i = 0; i < 8; ++i) {

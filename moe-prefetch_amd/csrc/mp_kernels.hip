@@ -536,52 +536,8 @@ __device__ inline void wave_lds_sync() {
 // down + combine.  Workgroup = 8 waves, 8 output rows; wave w owns expert
 // kb + w of each group of 8 experts.
 constexpr int DN_ROWS = 8;
-constexpr int Q6K_PAD = 224;                // a Q6_K block's stride in LDS (16-byte aligned)
 constexpr int DN_LDS_ROWS = 8 * 3 * Q6K_PAD;   // 8 padded Q6_K rows at I = 768
 constexpr int DN_LDS_Q8 = 3 * Q8K_BYTES;    // I <= 768
-
-// Q6_K rows into LDS with every 210-byte block at a 224-byte stride, so that
-// the dot's 8-byte LDS reads are aligned (at the blocks' own 2-byte
-// alignment they run about four times slower under load).  One wave moves
-// n_blocks blocks (<= 24: 8 rows at I = 768) from `src` (the rows
-// contiguous, so block n at n * 210): chunk c of the padded layout, 16
-// bytes, is block c / 14 from byte 16 (c % 14) -- except the 14th chunk of a
-// block, which only carries the block's last two bytes (its fp16 scale) and
-// is read as the block's last 16 bytes, so no read passes the block's end.
-// q6k_rows_load issues the loads; q6k_rows_store writes LDS and, with
-// `stage`, the same bytes to the staging copy at their own offsets.
-struct Q6Rows {
-    uint4 v[6];
-};
-__device__ inline void q6k_rows_load(Q6Rows &r, const uint8_t *src, int n_blocks, int lane) {
-#pragma unroll
-    for (int i = 0; i < 6; ++i) {
-        const int c = lane + 64 * i;
-        r.v[i] = make_uint4(0, 0, 0, 0);
-        if (src && c < 14 * n_blocks) {
-            const int n = c / 14, j = c - 14 * n;
-            const uint8_t *p = src + (size_t)n * Q6K_BYTES + (j < 13 ? 16 * j : Q6K_BYTES - 16);
-            __builtin_memcpy(&r.v[i], __builtin_assume_aligned(p, 2), 16);
-        }
-    }
-}
-__device__ inline void q6k_rows_store(const Q6Rows &r, uint8_t *s_dst, uint8_t *stage, int n_blocks, int lane) {
-#pragma unroll
-    for (int i = 0; i < 6; ++i) {
-        const int c = lane + 64 * i;
-        if (c < 14 * n_blocks) {
-            const int n = c / 14, j = c - 14 * n;
-            if (j < 13) {
-                *(uint4 *)(s_dst + 16 * c) = r.v[i];
-                if (stage) __builtin_memcpy(__builtin_assume_aligned(stage + (size_t)n * Q6K_BYTES + 16 * j, 2), &r.v[i], 16);
-            } else {
-                const uint16_t d = (uint16_t)(r.v[i].w >> 16);
-                *(uint16_t *)(s_dst + 16 * c) = d;
-                if (stage) *(uint16_t *)(stage + (size_t)n * Q6K_BYTES + Q6K_BYTES - 2) = d;
-            }
-        }
-    }
-}
 
 // One wave's 8 down rows (LDS: row g of the tile at g * rowb; Q4_K rows
 // lane-contiguous as loaded, Q6_K blocks at the padded stride) against the
