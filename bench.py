@@ -475,7 +475,8 @@ def fused_report(kt, n_tok):
                 tr["algorithmic_bytes_per_launch"]
             traffic = round(ratio * hb / n)
             tsrc = ("this run's bytes per launch x the (FETCH_SIZE + WRITE_SIZE) / algorithmic ratio of the "
-                    "committed rocprofv3 PMC run (profiles/traffic.json), not counters of this run")
+                    "committed rocprofv3 PMC run on the one-layer all-resident workload (profiles/traffic.json, "
+                    "profiles/fused_layer_traffic.md), not counters of this run")
     return {
         "kernels_ms_per_token": {"fused_layer": round(ms / max(n_tok, 1), 4)},
         "kernel_timing": f"HIP events stamped by each dispatch (hipExtLaunchKernelGGL) on its stream, {n_tok} "
@@ -835,7 +836,8 @@ def run_single(args):
     1 MiB of router per step over its dispatch-stamped duration."""
     import tempfile
     import numpy as np
-    a = _sub(args, layers=1, slots=E, sidecar=0)
+    # one layer: the timing pass affords as many launches as the timed steps
+    a = _sub(args, layers=1, slots=E, sidecar=0, kernel_steps=max(args.kernel_steps, args.steps))
     wl = Workload(a, steer=False)
     try:
         cache = wl.cache(admit="window")
