@@ -842,9 +842,15 @@ def run_single(args):
     try:
         cache = wl.cache(admit="window")
         # every expert with a count (halved on load, so >= 2), hottest first
+        # the cache saves its counts back to its heat file (on close, and every
+        # 512 steps), so the oracle's check warm-starts from a copy of it
+        heat_text = f"moe-heat 1 1 {E}\n" + "".join(f"0 {e} {2 * (E - e)}\n" for e in range(E))
         with tempfile.NamedTemporaryFile("w", suffix=".heat", delete=False) as f:
-            f.write(f"moe-heat 1 1 {E}\n" + "".join(f"0 {e} {2 * (E - e)}\n" for e in range(E)))
+            f.write(heat_text)
             hp = f.name
+        with tempfile.NamedTemporaryFile("w", suffix=".heat", delete=False) as f:
+            f.write(heat_text)
+            hp_check = f.name
         n_rec, n_placed = cache.heat_file(hp)
         if n_placed != E:
             raise RuntimeError(f"warm start placed {n_placed} of {E} experts")
@@ -874,8 +880,9 @@ def run_single(args):
         cache.close()
         if not args.no_check:
             out["check"] = wl.check(ids_log, kept, frames, s1, dict(admit="window"), every=True, steer=False,
-                                    heat=hp)
+                                    heat=hp_check)
         os.unlink(hp)
+        os.unlink(hp_check)
         return out
     finally:
         wl.close()
@@ -1105,7 +1112,7 @@ def run_prefill(args):
     return result
 
 
-def main():
+def parse_args(argv=None):
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=None, help="timed batch-1 tokens (448; wide40: 960)")
@@ -1138,13 +1145,7 @@ def main():
     ap.add_argument("--stream-reserve", type=int, default=2)
     ap.add_argument("--stream-gbps", type=float, default=45.7)
     ap.add_argument("--stream-chunk-kib", type=int, default=0, help="0: a whole expert per copy")
-    args = ap.parse_args()
-
-    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
-        print("bench.py measures one GPU: this path has no multi-GPU mode in this build "
-              "(the expert-sharded design is described in DESIGN.md); run with --gpus 1", file=sys.stderr)
-        sys.exit(2)
-
+    args = ap.parse_args(argv)
     if args.sidecar < 0:
         n_cpu = len(os.sched_getaffinity(0))
         args.sidecar = 14 if n_cpu >= 16 else (n_cpu - 2 if n_cpu >= 8 else 0)
@@ -1157,6 +1158,16 @@ def main():
         args.slots = 96 if wide else 56
     if args.batch is None:
         args.batch = 16 if wide else 512
+    return args
+
+
+def main():
+    args = parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU: this path has no multi-GPU mode in this build "
+              "(the expert-sharded design is described in DESIGN.md); run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+    wide = args.workload == "wide40"
     import torch
     wl = None
     if args.workload == "stacked48":
