@@ -87,6 +87,20 @@ def test_decode_4_layers_window_admission(tmp_path, split, graph):
         rig.close()
 
 
+@pytest.mark.parametrize("E,I,graph", [(64, 256, 1), (192, 512, 0)], ids=["e64_i256_graph", "e192_i512_eager"])
+def test_decode_fused_chunk_counts(tmp_path, E, I, graph):
+    # the fused layer routes in registers per 64-expert chunk (1 to 4 chunks:
+    # one instantiation each); E = 64 and E = 192, with the cache prior on so
+    # the routing reads the published tables every token
+    rig = Rig([24, 40], [Q4, Q6], T=32, I=I, E=E, admit="window", batch_tables=True, cache_prior=0.01)
+    rig.cache.set_decode_path(split=0, graph=bool(graph))
+    try:
+        worst = check_run(rig, tmp_path)
+        print("worst rel-L2", worst)
+    finally:
+        rig.close()
+
+
 def test_decode_256_experts_shared_expert(tmp_path):
     # the wide variant: 256 routed experts (top-8) plus an always-on shared
     # expert, I = 512, cache prior 0.01, Zipf(1.0) popularity with reuse 0.5
