@@ -400,6 +400,37 @@ int moe_predictor_update(moe_predictor *p, int layer, const moe_predictor_lists 
                          int n_truth, float lr, float *recall);
 int moe_predictor_save(const moe_predictor *p, const char *path);
 
+/* The cache's use of the models (patches/0006:295-427 and 765-922,
+ * patches/0007:149-168, 232-242, 330-355, 655-724; the reference's knobs
+ * LLAMA_MOE_PREDICTOR, LLAMA_MOE_PREDICT_TOP, LLAMA_MOE_ONLINE_LR,
+ * LLAMA_MOE_PREDICTOR_SAVE, LLAMA_MOE_EVICTOR, LLAMA_MOE_SPEC_PROBATION).
+ * Models are borrowed: keep them alive until the cache is destroyed or the
+ * hook is cleared (NULL).  Call between tokens.
+ *
+ * moe_cache_set_predictor: after each layer is observed, its model scores
+ * the next layer from (the next layer's ids of the previous token, this
+ * layer's ids); up to predict_top of the best absent experts are copied into
+ * the next layer's spare slots (speculative uploads, never below max_inserts
+ * spare slots; in heat admission each must be hotter than the expert it would
+ * displace).  The spare pool kept at each step grows by predict_top.  Turns
+ * early issue on.  online_lr > 0: each prediction is resolved against the ids
+ * the layer then routes to with one SGD step on the model (updated in place);
+ * save_path (or NULL): the model is written there every 200000 updates.
+ * predict_top <= 0 or p NULL removes the predictor.
+ * moe_cache_set_evictor: eviction victims are the lowest score of the model
+ * (features: the next layer's previous ids, this layer's ids, the layer
+ * below's, this layer's previous ones; recency breaks ties), in the step's
+ * scheduling and in the early path's pool top-up; LRU for layers the model
+ * lacks.  NULL restores LRU.
+ * moe_cache_set_spec_probation: speculative uploads are published with the
+ * oldest recency and cannot be evicted at their first step.
+ * Errors: MOE_ERR_ARG for a model with a PCA block or a different expert count. */
+int moe_cache_set_predictor(moe_cache *c, moe_predictor *p, int predict_top, float online_lr, const char *save_path);
+int moe_cache_set_evictor(moe_cache *c, moe_predictor *p);
+int moe_cache_set_spec_probation(moe_cache *c, int on);
+/* resolved predictions, the sum of their recall@8, speculative uploads issued */
+int moe_cache_predictor_stats(const moe_cache *c, uint64_t *n_updates, double *recall_sum, uint64_t *n_spec);
+
 /* Kernel time of the decode, from HIP events stamped by each launch's
  * dispatch on the stream it runs on (off by default; set before decoding;
  * the token's launches then run eagerly).  With the fused layer (split 0)

@@ -83,11 +83,17 @@ struct Layer {
     std::vector<float> heat;
     bool tbl_dirty = false;
     uint64_t n_hit = 0, n_miss = 0;
+    // MOEP predictor / evictor (patches/0006:139-154): the ids this layer routed
+    // to this token and the token before, and the features of the last
+    // prediction made for this layer (resolved when the layer routes)
+    std::vector<int32_t> cur_ids, prev_ids, pend_prev, pend_cur;
+    bool pend_valid = false;
 };
 
 struct Job {
     int li, expert, slot;
     hipEvent_t ev;     // live mode only
+    bool spec;         // issued from a prediction, not a miss (patches/0007:168)
 };
 
 // Just-in-time streaming (LLAMA_MOE_STREAM; state as in patches/0010:957-1021).
@@ -147,6 +153,10 @@ struct Streamer {
 };
 
 }  // namespace
+
+struct moe_predictor {
+    mpp::Predictor p;
+};
 
 struct moe_cache {
     moe_cache_config cfg{};
@@ -247,6 +257,15 @@ struct moe_cache {
     std::vector<uint8_t> has_norm;             // [layer]
     int32_t *h_slots = nullptr;                // pinned [layer][K]: the slots the GPU read this token
     std::atomic<int> sc_computing{-1};         // layer whose absent experts the host team is computing
+    // MOEP predictor and evictor (LLAMA_MOE_PREDICTOR / _EVICTOR, patches/0006:186-212),
+    // borrowed from the caller; the predictor is updated in place when online_lr > 0
+    moe_predictor *pred = nullptr, *evict = nullptr;
+    int predict_top = 0;
+    float online_lr = 0.0f;
+    std::string pred_save;                     // checkpoint path (LLAMA_MOE_PREDICTOR_SAVE), or empty
+    uint64_t online_n = 0, n_spec = 0;
+    double online_recall = 0.0;
+    bool spec_probation = false;               // LLAMA_MOE_SPEC_PROBATION (patches/0007:149-153)
 };
 
 struct moe_pool {
@@ -273,7 +292,7 @@ void set_table_entry(moe_cache *c, Layer &ls, int expert, int v) {
 // streaming reserve (patches/0010:1135-1142)
 int pool_target_of(const moe_cache *c) {
     if (c->freeze) return 0;
-    return c->cfg.max_inserts + (c->st ? c->st->reserve : 0);
+    return c->cfg.max_inserts + (c->pred ? c->predict_top : 0) + (c->st ? c->st->reserve : 0);
 }
 
 // expert `id` of layer `li` is being streamed in this token
@@ -325,9 +344,9 @@ hipEvent_t take_event(moe_cache *c) {
 }
 
 // hand one expert copy to the upload stream
-int start_upload(moe_cache *c, int li, int expert, int slot) {
+int start_upload(moe_cache *c, int li, int expert, int slot, bool spec = false) {
     Layer &ls = c->L[li];
-    Job j{li, expert, slot, nullptr};
+    Job j{li, expert, slot, nullptr, spec};
     if (c->host_only) {
         c->jobs.push_back(j);
         c->bytes_uploaded += ls.expert_bytes;
@@ -358,7 +377,8 @@ int start_upload(moe_cache *c, int li, int expert, int slot) {
     return MOE_OK;
 }
 
-int issue_uploads(moe_cache *c, int li, const int32_t *ids, int n, int budget, int min_keep) {
+// spec: the ids are a prediction (patches/0007:232-242)
+int issue_uploads(moe_cache *c, int li, const int32_t *ids, int n, int budget, int min_keep, bool spec = false) {
     Layer &ls = c->L[li];
     int issued = 0;
     if (c->freeze) return 0;
@@ -375,10 +395,11 @@ int issue_uploads(moe_cache *c, int li, const int32_t *ids, int n, int budget, i
         const int slot = ls.free_slots.back();
         ls.free_slots.pop_back();
         ls.slot_in_flight[slot] = 1;
-        int r = start_upload(c, li, id, slot);
+        int r = start_upload(c, li, id, slot, spec);
         if (r != MOE_OK) return r;
         c->n_uploads++;
         c->n_scheduled++;
+        c->n_spec += spec;
         issued++;
     }
     return issued;
@@ -519,7 +540,15 @@ void publish(moe_cache *c, const Job &j) {
     Layer &ls = c->L[j.li];
     ls.slot_expert[j.slot] = j.expert;
     ls.expert_slot[j.expert] = j.slot;
-    ls.slot_last_use[j.slot] = ++c->clock;
+    if (j.spec && c->spec_probation) {
+        // a guess is not evidence of reuse: oldest recency, and no eviction
+        // through this step's top-up and the next token (n_steps goes up after
+        // publication; patches/0007:655-668)
+        ls.slot_last_use[j.slot] = 1;
+        ls.slot_protect[j.slot] = c->n_steps + 1;
+    } else {
+        ls.slot_last_use[j.slot] = ++c->clock;
+    }
     ls.slot_in_flight[j.slot] = 0;
     set_table_entry(c, ls, j.expert, j.slot);
     c->n_published++;
@@ -845,6 +874,49 @@ void stream_free(moe_cache *c) {
     c->st = nullptr;
 }
 
+// the evictor's scores of layer li's experts, once per step (patches/0006:404-427);
+// false when it has no model for the layer
+bool evict_scores(const moe_cache *c, size_t li, std::vector<float> &out) {
+    const Layer &ls = c->L[li];
+    if (!c->evict || !c->evict->p.has_layer(ls.il)) return false;
+    mpp::Lists in;
+    auto set = [&in](int g, const std::vector<int32_t> &v) {
+        in.ids[g] = v.data();
+        in.n[g] = v.size();
+    };
+    set(1, ls.cur_ids);
+    set(3, ls.prev_ids);
+    if (li + 1 < c->L.size()) set(0, c->L[li + 1].prev_ids);
+    if (li > 0) set(2, c->L[li - 1].cur_ids);
+    out.resize((size_t)c->E);
+    c->evict->p.score(ls.il, in, out.data());
+    return true;
+}
+
+// victim among the slots that may go: with the evictor the lowest score
+// (recency breaks ties: many cold experts share a near-zero score), else the
+// least recently used (patches/0006:802-824)
+struct VictimPick {
+    bool use_model;
+    const std::vector<float> &esc;
+    int slot = -1;
+    uint64_t best = U64MAX;
+    float best_score = 3.4e38f;
+    void offer(const Layer &ls, int s) {
+        if (use_model) {
+            const float sc = esc[(size_t)ls.slot_expert[s]];
+            if (sc < best_score || (sc == best_score && ls.slot_last_use[s] < best)) {
+                best_score = sc;
+                best = ls.slot_last_use[s];
+                slot = s;
+            }
+        } else if (ls.slot_last_use[s] < best) {
+            best = ls.slot_last_use[s];
+            slot = s;
+        }
+    }
+};
+
 int cache_step(moe_cache *c) {
     // 1) publish finished uploads (no kernel of the cache is running)
     if (!c->jobs.empty()) {
@@ -886,11 +958,13 @@ int cache_step(moe_cache *c) {
     c->n_steps++;
 
     // 2) per layer
+    std::vector<float> esc;
     for (size_t li = 0; li < c->L.size(); ++li) {
         Layer &ls = c->L[li];
         if (!c->cfg.early_issue) {
             if (ls.pending.empty()) continue;
             int budget = c->cfg.max_inserts;
+            const bool use_model = evict_scores(c, li, esc);
             for (auto it = ls.pending.rbegin(); it != ls.pending.rend() && budget > 0; ++it) {
                 const int id = *it;
                 if (ls.expert_slot[id] >= 0) {
@@ -898,13 +972,14 @@ int cache_step(moe_cache *c) {
                     continue;
                 }
                 int slot = -1;
-                uint64_t best = U64MAX;
+                VictimPick vp{use_model, esc};
                 for (int s = 0; s < ls.S; ++s) {
                     if (ls.slot_in_flight[s]) continue;
                     if (ls.slot_expert[s] < 0) { slot = s; break; }
                     if (ls.slot_protect[s] >= c->n_steps) continue;
-                    if (ls.slot_last_use[s] < best) { best = ls.slot_last_use[s]; slot = s; }
+                    vp.offer(ls, s);
                 }
+                if (slot < 0) slot = vp.slot;
                 if (slot < 0) break;
                 const int victim = ls.slot_expert[slot];
                 if (!admit_ok(c, ls, id, victim)) continue;
@@ -925,14 +1000,15 @@ int cache_step(moe_cache *c) {
         }
         ls.pending.clear();
         const int pool_target = pool_target_of(c);
+        const bool use_model = evict_scores(c, li, esc);
         while ((int)ls.free_slots.size() < pool_target) {
-            int slot = -1;
-            uint64_t best = U64MAX;
+            VictimPick vp{use_model, esc};
             for (int s = 0; s < ls.S; ++s) {
                 if (ls.slot_in_flight[s] || ls.slot_expert[s] < 0) continue;
                 if (ls.slot_protect[s] >= c->n_steps) continue;
-                if (ls.slot_last_use[s] < best) { best = ls.slot_last_use[s]; slot = s; }
+                vp.offer(ls, s);
             }
+            const int slot = vp.slot;
             if (slot < 0) break;
             const int victim = ls.slot_expert[slot];
             ls.expert_slot[victim] = -1;
@@ -942,6 +1018,10 @@ int cache_step(moe_cache *c) {
             c->n_evicted++;
         }
     }
+
+    // after every eviction decision: this token's ids become the previous ones (patches/0006:915-922)
+    if (c->evict)
+        for (Layer &ls : c->L) ls.prev_ids = ls.cur_ids;
 
     // 3) heat decays on a clock
     if (c->cfg.admit_mode == MOE_ADMIT_HEAT && c->cfg.admit_half > 0 && c->n_steps % (uint64_t)c->cfg.admit_half == 0)
@@ -972,10 +1052,13 @@ int cache_observe(moe_cache *c, int li, const int32_t *ids, int n_ids, int n_tok
         }
         fputc('\n', c->route);
     }
+    std::vector<int32_t> observed;
+    observed.reserve((size_t)n_ids * n_tok);
     for (int t = 0; t < n_tok; ++t) {
         for (int i = 0; i < n_ids; ++i) {
             const int id = ids[t * n_ids + i];
             if (id < 0 || id >= ls.E) continue;
+            observed.push_back(id);
             if (!ls.heat.empty()) ls.heat[id] += 1.0f;
             if (!ls.use_count.empty()) ls.use_count[id]++;
             const int slot = ls.expert_slot[id];
@@ -994,6 +1077,24 @@ int cache_observe(moe_cache *c, int li, const int32_t *ids, int n_ids, int n_tok
             }
         }
     }
+    // the prediction made for this layer resolves against what it routed to
+    // (patches/0006:323-363): one SGD step, a checkpoint every 200000
+    if (c->pred && c->online_lr > 0.0f && ls.pend_valid && c->pred->p.has_layer(ls.il)) {
+        mpp::Lists in;
+        in.ids[0] = ls.pend_prev.data();
+        in.n[0] = ls.pend_prev.size();
+        in.ids[1] = ls.pend_cur.data();
+        in.n[1] = ls.pend_cur.size();
+        c->online_recall += c->pred->p.update(ls.il, in, observed.data(), observed.size(), c->online_lr);
+        ls.pend_valid = false;
+        c->online_n++;
+        if (!c->pred_save.empty() && c->online_n % 200000 == 0) {
+            std::string err;
+            const std::string tmp = c->pred_save + ".tmp";
+            if (!c->pred->p.save(tmp, err) || rename(tmp.c_str(), c->pred_save.c_str()) != 0)
+                fprintf(stderr, "moe-cache: predictor checkpoint FAILED: %s\n", err.c_str());
+        }
+    }
     if (c->cfg.early_issue) {
         const int pool_target = pool_target_of(c);
         const int next_victim = c->cfg.admit_mode == MOE_ADMIT_OFF ? -1
@@ -1008,7 +1109,41 @@ int cache_observe(moe_cache *c, int li, const int32_t *ids, int n_ids, int n_tok
             r = issue_uploads(c, li, adm.data(), (int)adm.size(), c->cfg.max_inserts, 0);
         }
         if (r < 0) return r;
+        // the next layer's experts, predicted from its previous ids and this
+        // layer's, copied into its spare slots; the demand path keeps
+        // max_inserts of them (patches/0006:367-396, 0007:424-452)
+        if (c->pred && c->pred->p.has_layer(ls.il) && (size_t)li + 1 < c->L.size()) {
+            Layer &nls = c->L[(size_t)li + 1];
+            mpp::Lists in;
+            in.ids[0] = nls.cur_ids.data();
+            in.n[0] = nls.cur_ids.size();
+            in.ids[1] = observed.data();
+            in.n[1] = observed.size();
+            std::vector<float> sc((size_t)c->E);
+            std::vector<int32_t> top((size_t)c->predict_top);
+            c->pred->p.score(ls.il, in, sc.data());
+            const int n_top = (int)c->pred->p.top(sc.data(), (size_t)c->predict_top, top.data());
+            if (c->online_lr > 0.0f) {
+                nls.pend_prev = nls.cur_ids;
+                nls.pend_cur = observed;
+                nls.pend_valid = true;
+            }
+            int n_issue = n_top;
+            if (c->cfg.admit_mode == MOE_ADMIT_HEAT) {
+                // a guess may only displace something colder than itself
+                const int nv = (int)nls.free_slots.size() > pool_target ? -1 : lru_resident(nls);
+                n_issue = 0;
+                for (int k = 0; k < n_top; ++k) {
+                    const int id = top[(size_t)k];
+                    if (id >= 0 && id < nls.E && nls.expert_slot[id] < 0 && admit_ok(c, nls, id, nv))
+                        top[(size_t)n_issue++] = id;
+                }
+            }
+            r = issue_uploads(c, li + 1, top.data(), n_issue, c->predict_top, c->cfg.max_inserts, true);
+            if (r < 0) return r;
+        }
     }
+    ls.cur_ids.swap(observed);
     if (gslots && c->st) stream_account(c, li, ids, gslots, n_ids);
     return MOE_OK;
 }
@@ -1668,7 +1803,7 @@ int moe_cache_heat_file(moe_cache *c, const char *path, int64_t *n_records, int6
     // for early issue; the hottest is the most recent use, so LRU evicts the
     // coldest of the warm set first
     if (n_rec > 0) {
-        const int reserve = c->cfg.early_issue ? c->cfg.max_inserts : 0;
+        const int reserve = c->cfg.early_issue ? c->cfg.max_inserts + (c->pred ? c->predict_top : 0) : 0;
         for (Layer &ls : c->L) {
             std::vector<int32_t> order(ls.E);
             for (int e = 0; e < ls.E; ++e) order[e] = e;
@@ -2008,9 +2143,6 @@ void moe_planner_counters(const moe_planner *p, uint64_t out[4]) {
 }
 
 // ---- MOEP expert predictor ---------------------------------------------------------
-struct moe_predictor {
-    mpp::Predictor p;
-};
 
 static mpp::Lists to_lists(const moe_predictor_lists *in) {
     mpp::Lists l;
@@ -2071,6 +2203,58 @@ int moe_predictor_save(const moe_predictor *p, const char *path) {
     if (!p || !path) return fail(MOE_ERR_ARG, "null argument");
     std::string err;
     if (!p->p.save(path, err)) return fail(MOE_ERR_IO, "%s", err.c_str());
+    return MOE_OK;
+}
+
+// a model the cache can score for its layers: E columns, no PCA block
+static int check_cache_model(const moe_cache *c, const moe_predictor *p, const char *who) {
+    if (p->p.has_pca())
+        return fail(MOE_ERR_ARG, "%s: the model has a PCA block over the hidden state, which the cache "
+                    "cannot score (the reference disables such a predictor)", who);
+    if ((int)p->p.shape.n_expert != c->E)
+        return fail(MOE_ERR_ARG, "%s: the model scores %u experts, the cache has %d", who, p->p.shape.n_expert,
+                    c->E);
+    return MOE_OK;
+}
+
+int moe_cache_set_predictor(moe_cache *c, moe_predictor *p, int predict_top, float online_lr,
+                            const char *save_path) {
+    if (!c) return fail(MOE_ERR_ARG, "null cache");
+    if (p && predict_top > 0) {
+        const int r = check_cache_model(c, p, "moe_cache_set_predictor");
+        if (r != MOE_OK) return r;
+        if (!(online_lr >= 0.0f)) return fail(MOE_ERR_ARG, "moe_cache_set_predictor: online_lr %g < 0", online_lr);
+        c->cfg.early_issue = 1;        // a predictor issues from the observation (patches/0006:558-562)
+    }
+    c->pred = p && predict_top > 0 ? p : nullptr;
+    c->predict_top = predict_top > 0 ? predict_top : 0;
+    c->online_lr = c->pred ? online_lr : 0.0f;
+    c->pred_save = c->pred && save_path ? save_path : "";
+    for (Layer &ls : c->L) ls.pend_valid = false;
+    return MOE_OK;
+}
+
+int moe_cache_set_evictor(moe_cache *c, moe_predictor *p) {
+    if (!c) return fail(MOE_ERR_ARG, "null cache");
+    if (p) {
+        const int r = check_cache_model(c, p, "moe_cache_set_evictor");
+        if (r != MOE_OK) return r;
+    }
+    c->evict = p;
+    return MOE_OK;
+}
+
+int moe_cache_set_spec_probation(moe_cache *c, int on) {
+    if (!c) return fail(MOE_ERR_ARG, "null cache");
+    c->spec_probation = on != 0;
+    return MOE_OK;
+}
+
+int moe_cache_predictor_stats(const moe_cache *c, uint64_t *n_updates, double *recall_sum, uint64_t *n_spec) {
+    if (!c) return fail(MOE_ERR_ARG, "null cache");
+    if (n_updates) *n_updates = c->online_n;
+    if (recall_sum) *recall_sum = c->online_recall;
+    if (n_spec) *n_spec = c->n_spec;
     return MOE_OK;
 }
 

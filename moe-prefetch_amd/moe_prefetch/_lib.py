@@ -192,6 +192,11 @@ SIGNATURES = {
     "moe_predictor_update": (ctypes.c_int, [P, ctypes.c_int, ctypes.POINTER(PredictorLists), P, ctypes.c_int, F32,
                                             ctypes.POINTER(F32)]),
     "moe_predictor_save": (ctypes.c_int, [P, ctypes.c_char_p]),
+    "moe_cache_set_predictor": (ctypes.c_int, [P, P, ctypes.c_int, ctypes.c_float, ctypes.c_char_p]),
+    "moe_cache_set_evictor": (ctypes.c_int, [P, P]),
+    "moe_cache_set_spec_probation": (ctypes.c_int, [P, ctypes.c_int]),
+    "moe_cache_predictor_stats": (ctypes.c_int, [P, ctypes.POINTER(ctypes.c_uint64), ctypes.POINTER(ctypes.c_double),
+                                                 ctypes.POINTER(ctypes.c_uint64)]),
     "moe_planner_create": (P, [U64]),
     "moe_planner_destroy": (None, [P]),
     "moe_planner_reset": (None, [P]),

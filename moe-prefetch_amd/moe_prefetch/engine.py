@@ -99,6 +99,15 @@ class MoeCache:
                    early_issue=int(g("LLAMA_MOE_EARLY_ISSUE", "0")) != 0,
                    cache_prior=max(0.0, float(g("LLAMA_MOE_CACHE_PRIOR", "0"))),
                    deterministic=int(g("LLAMA_MOE_DETERMINISTIC", "0")) != 0, **shape)
+        if g("LLAMA_MOE_EVICTOR"):
+            from .moep import MoePredictor
+            c.set_evictor(MoePredictor(g("LLAMA_MOE_EVICTOR")))
+        if g("LLAMA_MOE_PREDICTOR"):
+            from .moep import MoePredictor
+            c.set_predictor(MoePredictor(g("LLAMA_MOE_PREDICTOR")), predict_top=int(g("LLAMA_MOE_PREDICT_TOP", "3")),
+                            online_lr=float(g("LLAMA_MOE_ONLINE_LR", "0")), save_path=g("LLAMA_MOE_PREDICTOR_SAVE"))
+        if int(g("LLAMA_MOE_SPEC_PROBATION", "0") or "0") != 0:
+            c.set_spec_probation(True)
         if int(g("LLAMA_MOE_CACHE_FREEZE", "0") or "0") != 0:
             c.freeze()
         if int(g("LLAMA_MOE_SIDECAR", "0") or "0") != 0:
@@ -120,6 +129,30 @@ class MoeCache:
 
     def __del__(self):
         self.close()
+
+    # -- MOEP predictor / evictor (borrowed models: kept referenced here) ----
+    def set_predictor(self, model, predict_top=3, online_lr=0.0, save_path=None):
+        """LLAMA_MOE_PREDICTOR / _PREDICT_TOP / _ONLINE_LR / _PREDICTOR_SAVE (patches/0006:501-562):
+        speculative next-layer uploads from a MoePredictor; turns early issue on."""
+        self._pred = model
+        check(lib().moe_cache_set_predictor(self.h, model.h if model is not None else None, predict_top,
+                                            float(online_lr), save_path.encode() if save_path else None),
+              "set_predictor")
+
+    def set_evictor(self, model):
+        """LLAMA_MOE_EVICTOR (patches/0006:521-537): victims by the model's lowest score."""
+        self._evict = model
+        check(lib().moe_cache_set_evictor(self.h, model.h if model is not None else None), "set_evictor")
+
+    def set_spec_probation(self, on=True):
+        """LLAMA_MOE_SPEC_PROBATION (patches/0007:503)."""
+        check(lib().moe_cache_set_spec_probation(self.h, int(on)), "set_spec_probation")
+
+    def predictor_stats(self):
+        n, r, sp = ctypes.c_uint64(), ctypes.c_double(), ctypes.c_uint64()
+        check(lib().moe_cache_predictor_stats(self.h, ctypes.byref(n), ctypes.byref(r), ctypes.byref(sp)),
+              "predictor_stats")
+        return {"n_updates": n.value, "recall_sum": r.value, "n_spec": sp.value}
 
     # -- weights -----------------------------------------------------------
     def expert_bytes(self, layer):

@@ -15,9 +15,13 @@
  *   streaming 0010:1096-1129 (map frame one step late), 0010:1183-1210 (account),
  *             0010:1466-1530 (take), 0010:1722-1760 (adopt), 0010:1138-1175 (pool target,
  *             issue skip, observe skip)
- * The predictor/evictor and speculative probation are not restated (out of
- * scope); slot_protect is kept at 0, which is what it is when no speculative
- * upload exists.
+ *   predictor 0006:295-400 (online resolution, next-layer prediction), 0007:330-355
+ *             (admission guard on speculative uploads, spec jobs), 0006:501-560 (knobs)
+ *   evictor   0006:404-427 (scores), 0006:790-900 and 0007:676-724 (victims), 0006:918-922
+ *   probation 0007:149-153, 0007:655-668 (speculative jobs published oldest and protected)
+ * The hooks are pinned only where they reduce to the recorded traces (a flat
+ * evictor is LRU); beyond that they are parity unpinned: no reference trace
+ * ran with a predictor.
  *
  * Upload completion: every job is published at the step after the one that
  * scheduled (or, early path, issued) it.  With `deterministic` the order is
@@ -51,12 +55,17 @@ typedef struct {
     float *prior_mirror;
     int tbl_dirty;
     uint64_t n_hit, n_miss;
+    /* predictor / evictor: this token's ids, the previous token's, and the
+     * features of the last prediction made for this layer */
+    int32_t *cur_ids, *prev_ids, *pend_prev, *pend_cur;
+    int n_cur, n_prev_ids, n_pend_prev, n_pend_cur, cap_ids;
+    int pend_valid;
 } layer_t;
 
 typedef struct {
     int li, expert, slot;
     uint64_t sched_step;
-    int hold;
+    int hold, spec;
 } job_t;
 
 typedef struct {
@@ -98,14 +107,30 @@ struct or_cache {
     int rec_have;
     int32_t *rec_used;              /* (layer, slot, expert) triples used in time this step */
     int n_rec_used;
+    /* MOEP predictor (borrowed; updated in place when online_lr > 0) and evictor */
+    or_moep *pred, *evict;
+    int predict_top, spec_probation;
+    float online_lr;
+    uint64_t online_n, n_spec;
+    double online_recall;
 };
 
-static void push_job(or_cache *c, int li, int e, int slot) {
+/* room for n ids in each of a layer's id lists */
+static void ids_room(layer_t *ls, int n) {
+    if (n <= ls->cap_ids) return;
+    ls->cap_ids = n;
+    ls->cur_ids = (int32_t *)realloc(ls->cur_ids, sizeof(int32_t) * (size_t)n);
+    ls->prev_ids = (int32_t *)realloc(ls->prev_ids, sizeof(int32_t) * (size_t)n);
+    ls->pend_prev = (int32_t *)realloc(ls->pend_prev, sizeof(int32_t) * (size_t)n);
+    ls->pend_cur = (int32_t *)realloc(ls->pend_cur, sizeof(int32_t) * (size_t)n);
+}
+
+static void push_job(or_cache *c, int li, int e, int slot, int spec) {
     if (c->n_jobs == c->cap_jobs) {
         c->cap_jobs = c->cap_jobs ? 2 * c->cap_jobs : 256;
         c->jobs = (job_t *)realloc(c->jobs, sizeof(job_t) * (size_t)c->cap_jobs);
     }
-    job_t j = {li, e, slot, c->n_steps, 0};
+    job_t j = {li, e, slot, c->n_steps, 0, spec};
     for (int h = 0; h < c->n_holds; ++h) {
         const job_t *q = &c->holds[h];
         if (q->li == li && q->expert == e && q->slot == slot && q->sched_step == c->n_steps) j.hold = 1;
@@ -209,6 +234,7 @@ void or_cache_destroy(or_cache *c) {
         free(ls->slot_protect); free(ls->slot_in_flight); free(ls->free_slots);
         free(ls->pending); free(ls->tbl_mirror); free(ls->prior_mirror);
         free(ls->heat); free(ls->miss_last); free(ls->miss_prev); free(ls->use_count);
+        free(ls->cur_ids); free(ls->prev_ids); free(ls->pend_prev); free(ls->pend_cur);
     }
     if (c->map && c->rec_have) write_frame(c, c->rec_step, c->rec_frame);   /* the last boundary */
     if (c->route) fclose(c->route);
@@ -299,8 +325,9 @@ int or_cache_trace_open(or_cache *c, const char *route_path, const char *map_pat
     return 0;
 }
 
-/* 0006:241-293: early issue out of pre-freed slots; caller-side admission */
-static int issue_uploads(or_cache *c, int li, const int32_t *ids, int n, int budget, int min_keep) {
+/* 0006:241-293: early issue out of pre-freed slots; caller-side admission;
+ * spec: issued from a prediction (0007:232-242) */
+static int issue_uploads(or_cache *c, int li, const int32_t *ids, int n, int budget, int min_keep, int spec) {
     layer_t *ls = &c->L[li];
     int issued = 0;
     if (c->freeze) return 0;
@@ -316,9 +343,10 @@ static int issue_uploads(or_cache *c, int li, const int32_t *ids, int n, int bud
         if (dup) continue;
         const int slot = ls->free_slots[--ls->n_free];
         ls->slot_in_flight[slot] = 1;
-        push_job(c, li, id, slot);
+        push_job(c, li, id, slot, spec);
         c->n_uploads++;
         c->n_scheduled++;
+        c->n_spec += spec != 0;
         issued++;
     }
     return issued;
@@ -326,7 +354,7 @@ static int issue_uploads(or_cache *c, int li, const int32_t *ids, int n, int bud
 
 static int pool_target_of(const or_cache *c) {
     if (c->freeze) return 0;
-    return c->k.max_inserts + (c->st_on ? c->st_reserve : 0);
+    return c->k.max_inserts + (c->pred ? c->predict_top : 0) + (c->st_on ? c->st_reserve : 0);
 }
 
 /* gslots (batch 1 with streaming): the slots the GPU used, n_slots = absent */
@@ -341,10 +369,14 @@ static void observe_body(or_cache *c, int li, const int32_t *ids, int n_ids, int
         }
         fputc('\n', c->route);
     }
+    ids_room(ls, n_ids * n_tok);
+    int32_t *observed = (int32_t *)malloc(sizeof(int32_t) * (size_t)(n_ids * n_tok + 1));
+    int n_obs = 0;
     for (int t = 0; t < n_tok; ++t) {
         for (int i = 0; i < n_ids; ++i) {
             const int id = ids[t * n_ids + i];
             if (id < 0 || id >= ls->E) continue;
+            observed[n_obs++] = id;
             if (ls->heat) ls->heat[id] += 1.0f;
             if (ls->use_count) ls->use_count[id]++;
             const int slot = ls->expert_slot[id];
@@ -364,12 +396,20 @@ static void observe_body(or_cache *c, int li, const int32_t *ids, int n_ids, int
             }
         }
     }
+    /* 0006:323-363: the prediction made for this layer resolves against what it routed */
+    if (c->pred && c->online_lr > 0.0f && ls->pend_valid && or_moep_has_layer(c->pred, ls->il)) {
+        or_moep_lists in = {{ls->pend_prev, ls->pend_cur, NULL, NULL}, {ls->n_pend_prev, ls->n_pend_cur, 0, 0}};
+        const float hit = or_moep_update(c->pred, ls->il, &in, observed, n_obs, c->online_lr);
+        ls->pend_valid = 0;
+        c->online_recall += hit;
+        c->online_n++;
+    }
     if (c->k.early_issue) {
         const int pool_target = pool_target_of(c);
         const int next_victim = c->k.admit_mode == 0 ? -1 :
             (ls->n_free > pool_target ? -1 : lru_resident(ls));
         if (c->k.admit_mode == 0) {
-            issue_uploads(c, li, ls->pending, ls->n_pending, c->k.max_inserts, 0);
+            issue_uploads(c, li, ls->pending, ls->n_pending, c->k.max_inserts, 0, 0);
         } else {
             int32_t adm[1024];
             int n = 0;
@@ -377,9 +417,80 @@ static void observe_body(or_cache *c, int li, const int32_t *ids, int n_ids, int
                 const int id = ls->pending[p];
                 if (ls->expert_slot[id] < 0 && admit_ok(c, ls, id, next_victim)) adm[n++] = id;
             }
-            issue_uploads(c, li, adm, n, c->k.max_inserts, 0);
+            issue_uploads(c, li, adm, n, c->k.max_inserts, 0, 0);
+        }
+        /* 0006:367-396, 0007:424-452: the next layer's experts, predicted from
+         * its previous ids and this layer's, copied into its spare slots */
+        if (c->pred && or_moep_has_layer(c->pred, ls->il) && li + 1 < c->n_layers) {
+            layer_t *nls = &c->L[li + 1];
+            const int E = or_moep_n_expert(c->pred);
+            float *sc = (float *)malloc(sizeof(float) * (size_t)E);
+            int32_t *top = (int32_t *)malloc(sizeof(int32_t) * (size_t)(c->predict_top + 1));
+            or_moep_lists in = {{nls->cur_ids, observed, NULL, NULL}, {nls->n_cur, n_obs, 0, 0}};
+            or_moep_score(c->pred, ls->il, &in, sc);
+            const int n_top = or_moep_top(c->pred, sc, c->predict_top, top);
+            if (c->online_lr > 0.0f) {
+                ids_room(nls, n_obs > nls->n_cur ? n_obs : nls->n_cur);
+                memcpy(nls->pend_prev, nls->cur_ids, sizeof(int32_t) * (size_t)nls->n_cur);
+                nls->n_pend_prev = nls->n_cur;
+                memcpy(nls->pend_cur, observed, sizeof(int32_t) * (size_t)n_obs);
+                nls->n_pend_cur = n_obs;
+                nls->pend_valid = 1;
+            }
+            int n_issue = n_top;
+            if (c->k.admit_mode == 1) {
+                /* a guess may only displace something colder than itself */
+                const int nv = nls->n_free > pool_target ? -1 : lru_resident(nls);
+                n_issue = 0;
+                for (int k = 0; k < n_top; ++k) {
+                    const int id = top[k];
+                    if (id >= 0 && id < nls->E && nls->expert_slot[id] < 0 && admit_ok(c, nls, id, nv))
+                        top[n_issue++] = id;
+                }
+            }
+            issue_uploads(c, li + 1, top, n_issue, c->predict_top, c->k.max_inserts, 1);
+            free(sc);
+            free(top);
         }
     }
+    memcpy(ls->cur_ids, observed, sizeof(int32_t) * (size_t)n_obs);
+    ls->n_cur = n_obs;
+    free(observed);
+}
+
+/* 0006:404-427: the evictor's scores of a layer's experts, once per step
+ * (0 when there is no model for the layer) */
+static int evict_scores(const or_cache *c, int li, float *out) {
+    const layer_t *ls = &c->L[li];
+    if (!c->evict || !or_moep_has_layer(c->evict, ls->il)) return 0;
+    or_moep_lists in = {{NULL, ls->cur_ids, NULL, ls->prev_ids}, {0, ls->n_cur, 0, ls->n_prev_ids}};
+    if (li + 1 < c->n_layers) {
+        in.ids[0] = c->L[li + 1].prev_ids;
+        in.n[0] = c->L[li + 1].n_prev_ids;
+    }
+    if (li > 0) {
+        in.ids[2] = c->L[li - 1].cur_ids;
+        in.n[2] = c->L[li - 1].n_cur;
+    }
+    or_moep_score(c->evict, ls->il, &in, out);
+    return 1;
+}
+
+void or_cache_set_predictor(or_cache *c, or_moep *m, int predict_top, float online_lr) {
+    c->pred = m && predict_top > 0 ? m : NULL;
+    c->predict_top = predict_top;
+    c->online_lr = online_lr;
+    if (c->pred) c->k.early_issue = 1;      /* 0006:558-562: a predictor needs early issue */
+}
+
+void or_cache_set_evictor(or_cache *c, or_moep *m) { c->evict = m; }
+
+void or_cache_set_spec_probation(or_cache *c, int on) { c->spec_probation = on != 0; }
+
+void or_cache_predictor_stats(const or_cache *c, uint64_t *n_updates, double *recall_sum, uint64_t *n_spec) {
+    if (n_updates) *n_updates = c->online_n;
+    if (recall_sum) *recall_sum = c->online_recall;
+    if (n_spec) *n_spec = c->n_spec;
 }
 
 void or_cache_observe(or_cache *c, int li, const int32_t *ids, int n_ids, int n_tok) {
@@ -579,7 +690,13 @@ void or_cache_step(or_cache *c) {
         layer_t *ls = &c->L[done[j].li];
         ls->slot_expert[done[j].slot] = done[j].expert;
         ls->expert_slot[done[j].expert] = done[j].slot;
-        ls->slot_last_use[done[j].slot] = ++c->clock;
+        if (done[j].spec && c->spec_probation) {
+            /* oldest recency, protected through this step's top-up and the next token */
+            ls->slot_last_use[done[j].slot] = 1;
+            ls->slot_protect[done[j].slot] = c->n_steps + 1;
+        } else {
+            ls->slot_last_use[done[j].slot] = ++c->clock;
+        }
         ls->slot_in_flight[done[j].slot] = 0;
         set_table_entry(c, ls, done[j].expert, done[j].slot);
         c->n_published++;
@@ -589,22 +706,36 @@ void or_cache_step(or_cache *c) {
 
     c->n_steps++;
 
-    /* 2) per layer: schedule (non-early) or top the free pool up (early) */
+    /* 2) per layer: schedule (non-early) or top the free pool up (early);
+     * victims by the evictor's score where it has a model, else LRU */
+    float *esc = (float *)malloc(sizeof(float) * (size_t)c->E);
     for (int li = 0; li < c->n_layers; ++li) {
         layer_t *ls = &c->L[li];
         if (!c->k.early_issue) {
             if (ls->n_pending == 0) continue;
             int budget = c->k.max_inserts;
+            const int use_model = evict_scores(c, li, esc);
             for (int p = ls->n_pending - 1; p >= 0 && budget > 0; --p) {
                 const int id = ls->pending[p];
                 if (ls->expert_slot[id] >= 0) { --budget; continue; }
                 int slot = -1;
                 uint64_t best = U64MAX;
+                float best_score = 3.4e38f;
                 for (int s = 0; s < ls->S; ++s) {
                     if (ls->slot_in_flight[s]) continue;
                     if (ls->slot_expert[s] < 0) { slot = s; break; }
                     if (ls->slot_protect[s] >= c->n_steps) continue;
-                    if (ls->slot_last_use[s] < best) { best = ls->slot_last_use[s]; slot = s; }
+                    if (use_model) {
+                        const float sc = esc[ls->slot_expert[s]];
+                        if (sc < best_score || (sc == best_score && ls->slot_last_use[s] < best)) {
+                            best_score = sc;
+                            best = ls->slot_last_use[s];
+                            slot = s;
+                        }
+                    } else if (ls->slot_last_use[s] < best) {
+                        best = ls->slot_last_use[s];
+                        slot = s;
+                    }
                 }
                 if (slot < 0) break;
                 const int victim = ls->slot_expert[slot];
@@ -616,7 +747,7 @@ void or_cache_step(or_cache *c) {
                     set_table_entry(c, ls, victim, ls->S);
                 }
                 ls->slot_in_flight[slot] = 1;
-                push_job(c, li, id, slot);
+                push_job(c, li, id, slot, 0);
                 c->n_scheduled++;
             }
             ls->n_pending = 0;
@@ -624,13 +755,25 @@ void or_cache_step(or_cache *c) {
         }
         ls->n_pending = 0;
         const int pool_target = pool_target_of(c);
+        const int use_model = evict_scores(c, li, esc);
         while (ls->n_free < pool_target) {
             int slot = -1;
             uint64_t best = U64MAX;
+            float best_score = 3.4e38f;
             for (int s = 0; s < ls->S; ++s) {
                 if (ls->slot_in_flight[s] || ls->slot_expert[s] < 0) continue;
                 if (ls->slot_protect[s] >= c->n_steps) continue;
-                if (ls->slot_last_use[s] < best) { best = ls->slot_last_use[s]; slot = s; }
+                if (use_model) {
+                    const float sc = esc[ls->slot_expert[s]];
+                    if (sc < best_score || (sc == best_score && ls->slot_last_use[s] < best)) {
+                        best_score = sc;
+                        best = ls->slot_last_use[s];
+                        slot = s;
+                    }
+                } else if (ls->slot_last_use[s] < best) {
+                    best = ls->slot_last_use[s];
+                    slot = s;
+                }
             }
             if (slot < 0) break;
             const int victim = ls->slot_expert[slot];
@@ -640,6 +783,14 @@ void or_cache_step(or_cache *c) {
             ls->free_slots[ls->n_free++] = slot;
         }
     }
+    free(esc);
+    /* 0006:915-922: after every eviction decision, this token's ids become the previous ones */
+    if (c->evict)
+        for (int li = 0; li < c->n_layers; ++li) {
+            layer_t *ls = &c->L[li];
+            memcpy(ls->prev_ids, ls->cur_ids, sizeof(int32_t) * (size_t)ls->n_cur);
+            ls->n_prev_ids = ls->n_cur;
+        }
 
     /* 3) heat decay on a clock */
     if (c->k.admit_mode == 1 && c->k.admit_half > 0 && c->n_steps % (uint64_t)c->k.admit_half == 0) {
@@ -714,7 +865,7 @@ int or_cache_heat_file(or_cache *c, const char *path, long long *n_records, long
     }
     /* 0007:576-611: hottest first into slots 0.., a reserve left for early issue */
     if (n_rec > 0) {
-        const int reserve = c->k.early_issue ? (c->freeze ? 0 : c->k.max_inserts) : 0;
+        const int reserve = c->k.early_issue ? (c->freeze ? 0 : c->k.max_inserts + (c->pred ? c->predict_top : 0)) : 0;
         int32_t *order = (int32_t *)malloc(sizeof(int32_t) * (size_t)c->E);
         for (int l = 0; l < c->n_layers; ++l) {
             layer_t *ls = &c->L[l];
@@ -774,7 +925,7 @@ int or_cache_replay_error(const or_cache *c) { return c->replay_err; }
 
 void or_cache_hold_job(or_cache *c, int layer, int expert, int slot, uint64_t sched_step) {
     c->holds = (job_t *)realloc(c->holds, sizeof(job_t) * (size_t)(c->n_holds + 1));
-    job_t j = {layer, expert, slot, sched_step, 1};
+    job_t j = {layer, expert, slot, sched_step, 1, 0};
     c->holds[c->n_holds++] = j;
 }
 

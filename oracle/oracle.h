@@ -250,6 +250,41 @@ int  or_cache_stream_job(const or_cache *c, int job, int32_t *layer, int32_t *ex
 void or_cache_observe_gpu(or_cache *c, int layer, const int32_t *ids, const int32_t *gslots, int n_ids);
 void or_cache_stream_stats(const or_cache *c, uint64_t out[11]);
 
+
+/* ---- the MOEP predictor / evictor (moep.c; cpp/moe-predictor.cpp) ---------
+ * Lists in block order prev, cur, below, self_prev (n = 0: absent).  load
+ * returns NULL for a file it cannot use (PCA models included). */
+typedef struct or_moep or_moep;
+typedef struct {
+    const int32_t *ids[4];
+    int n[4];
+} or_moep_lists;
+or_moep *or_moep_load(const char *path);
+void  or_moep_free(or_moep *m);
+int   or_moep_n_expert(const or_moep *m);
+int   or_moep_has_layer(const or_moep *m, int il);
+void  or_moep_score(const or_moep *m, int il, const or_moep_lists *in, float *out);
+int   or_moep_top(const or_moep *m, const float *scores, int k, int32_t *out);
+float or_moep_update(or_moep *m, int il, const or_moep_lists *in, const int32_t *truth, int n_truth, float lr);
+
+/* ---- the predictor's and evictor's hooks in the state machine (0006:295-427,
+ * 0006:765-900, 0007:149-318, 0007:655-724) ------------------------------------
+ * set_predictor: with early issue, after each layer is observed the
+ * predictor scores the next layer from (its previous ids, this layer's ids)
+ * and issues up to predict_top speculative uploads there, keeping max_inserts
+ * free slots for the demand path; online_lr > 0 resolves each prediction
+ * against the ids the target layer then routes to (one SGD step; the model is
+ * the caller's and is updated in place).  A predictor turns early issue on.
+ * set_evictor: victims are the lowest score of the evictor (recency breaks
+ * ties) in both the scheduling and the pool top-up.  set_spec_probation:
+ * speculative uploads are published with the oldest recency and protected
+ * from eviction for one step.  Borrowed models: keep them alive while set. */
+void or_cache_set_predictor(or_cache *c, or_moep *m, int predict_top, float online_lr);
+void or_cache_set_evictor(or_cache *c, or_moep *m);
+void or_cache_set_spec_probation(or_cache *c, int on);
+/* resolved predictions, the sum of their recall@8, speculative uploads issued */
+void or_cache_predictor_stats(const or_cache *c, uint64_t *n_updates, double *recall_sum, uint64_t *n_spec);
+
 #ifdef __cplusplus
 }
 #endif

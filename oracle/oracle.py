@@ -60,6 +60,10 @@ class PlannerJob(ctypes.Structure):
                 ("drop", ctypes.c_int)]
 
 
+class MoepLists(ctypes.Structure):
+    _fields_ = [("ids", ctypes.c_void_p * 4), ("n", ctypes.c_int * 4)]
+
+
 STREAM_STATS = ("records", "offered", "landed", "in_time", "late", "unused", "dropped_late", "dropped_posted",
                 "not_sent", "gpu_miss", "bytes")
 DROP_NONE, DROP_LATE, DROP_POSTED = 0, 1, 2
@@ -129,6 +133,18 @@ def _declare(L):
     d("or_cache_stream_job", ctypes.c_int, P, ctypes.c_int, P, P)
     d("or_cache_observe_gpu", None, P, ctypes.c_int, P, P, ctypes.c_int)
     d("or_cache_stream_stats", None, P, P)
+    d("or_moep_load", P, ctypes.c_char_p)
+    d("or_moep_free", None, P)
+    d("or_moep_n_expert", ctypes.c_int, P)
+    d("or_moep_has_layer", ctypes.c_int, P, ctypes.c_int)
+    d("or_moep_score", None, P, ctypes.c_int, ctypes.POINTER(MoepLists), P)
+    d("or_moep_top", ctypes.c_int, P, P, ctypes.c_int, P)
+    d("or_moep_update", F32, P, ctypes.c_int, ctypes.POINTER(MoepLists), P, ctypes.c_int, F32)
+    d("or_cache_set_predictor", None, P, P, ctypes.c_int, F32)
+    d("or_cache_set_evictor", None, P, P)
+    d("or_cache_set_spec_probation", None, P, ctypes.c_int)
+    d("or_cache_predictor_stats", None, P, ctypes.POINTER(ctypes.c_uint64), ctypes.POINTER(ctypes.c_double),
+      ctypes.POINTER(ctypes.c_uint64))
 
 
 def _p(a):
@@ -396,6 +412,23 @@ class Cache:
         lib().or_cache_stats(self.h, ctypes.byref(s))
         return {n: getattr(s, n) for n, _ in Stats._fields_}
 
+    # ---- MOEP predictor / evictor hooks (Moep models, borrowed) ----
+    def set_predictor(self, model, predict_top=3, online_lr=0.0):
+        self._pred = model
+        lib().or_cache_set_predictor(self.h, model.h if model else None, predict_top, online_lr)
+
+    def set_evictor(self, model):
+        self._evict = model
+        lib().or_cache_set_evictor(self.h, model.h if model else None)
+
+    def set_spec_probation(self, on=True):
+        lib().or_cache_set_spec_probation(self.h, int(on))
+
+    def predictor_stats(self):
+        n, r, sp = ctypes.c_uint64(), ctypes.c_double(), ctypes.c_uint64()
+        lib().or_cache_predictor_stats(self.h, ctypes.byref(n), ctypes.byref(r), ctypes.byref(sp))
+        return {"n_updates": n.value, "recall_sum": r.value, "n_spec": sp.value}
+
     # ---- just-in-time streaming ----
     def stream_enable(self, per_layer=4, reserve=2, gbps=45.7, chunk_bytes=512 * 1024):
         if lib().or_cache_stream_enable(self.h, per_layer, reserve, gbps, chunk_bytes) != 0:
@@ -434,6 +467,60 @@ class Cache:
         out = np.zeros(11, np.uint64)
         lib().or_cache_stream_stats(self.h, _p(out))
         return dict(zip(STREAM_STATS, (int(v) for v in out)))
+
+
+# ---- the MOEP predictor / evictor, restated (moep.c) ----
+class Moep:
+    """The oracle's MOEP model (cpp/moe-predictor.cpp restated)."""
+
+    def __init__(self, path):
+        self.h = lib().or_moep_load(str(path).encode())
+        if not self.h:
+            raise ValueError(f"oracle cannot load MOEP file {path}")
+        self.n_expert = lib().or_moep_n_expert(self.h)
+
+    def close(self):
+        if getattr(self, "h", None):
+            lib().or_moep_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        self.close()
+
+    @staticmethod
+    def _lists(keep, ids):
+        l = MoepLists()
+        for b, name in enumerate(("prev", "cur", "below", "self_prev")):
+            v = ids.get(name)
+            if v is None or len(v) == 0:
+                l.ids[b], l.n[b] = None, 0
+                continue
+            a = np.ascontiguousarray(v, np.int32)
+            keep.append(a)
+            l.ids[b], l.n[b] = a.ctypes.data, a.size
+        return l
+
+    def has_layer(self, layer):
+        return bool(lib().or_moep_has_layer(self.h, layer))
+
+    def score(self, layer, **ids):
+        keep = []
+        l = self._lists(keep, ids)
+        out = np.empty(self.n_expert, np.float32)
+        lib().or_moep_score(self.h, layer, ctypes.byref(l), out.ctypes.data)
+        return out
+
+    def top_k(self, scores, k=8):
+        s = np.ascontiguousarray(scores, np.float32)
+        out = np.empty(max(k, 0), np.int32)
+        n = lib().or_moep_top(self.h, s.ctypes.data, k, out.ctypes.data)
+        return out[:n]
+
+    def update(self, layer, truth, lr, **ids):
+        keep = []
+        l = self._lists(keep, ids)
+        t = np.ascontiguousarray(truth, np.int32)
+        return lib().or_moep_update(self.h, layer, ctypes.byref(l), t.ctypes.data, t.size, lr)
 
 
 # ---- the reference's own MOEP predictor (oracle/_ref, built where the reference is) ----

@@ -58,6 +58,7 @@ def check_run(rig, tmp_path, out_every=1, tol=1e-3, oc=None, record_map=True, to
             rig.n_evicted += int(np.sum((prev[l] >= 0) & (f != prev[l])))
             prev[l] = f
     rig.stats, rig.ostats = rig.cache.stats(), oc.stats()
+    rig.pstats, rig.opstats = rig.cache.predictor_stats(), oc.predictor_stats()
     rig.cache.close()
     oc.close()
     assert open(rp).read() == open(orp).read()
@@ -352,6 +353,38 @@ def test_sidecar_host_abort_then_next_token_exact(tmp_path):
     finally:
         rig.close()
     assert rig.stats["n_cpu_served"] > 0
+
+
+def test_decode_with_predictor_and_evictor(tmp_path):
+    """The MOEP hooks on the GPU decode (patches/0006:295-427, 765-922;
+    0007:149-168, 330-355, 655-724): an online-learning predictor issuing
+    speculative next-layer uploads on probation, and an evictor choosing the
+    victims; ids, frames, traces and outputs equal the oracle's token by token,
+    and so do the predictor's resolved predictions, recall and speculative
+    uploads."""
+    from moep_models import write_moep
+    from moe_prefetch.moep import MoePredictor
+    pp, ep = str(tmp_path / "pred.bin"), str(tmp_path / "evict.bin")
+    write_moep(pp, 128, 4, [0, 1, 2], blocks=(1, 2), seed=5)
+    write_moep(ep, 128, 4, [0, 1, 2, 3], blocks=(1, 2, 3, 4), seed=6, prior=0.0)
+    rig = Rig([16, 24, 12, 40], [Q4, Q6, Q4, Q6], T=48, admit="window", batch_tables=True)
+    models = [MoePredictor(pp), MoePredictor(ep), O.Moep(pp), O.Moep(ep)]
+    try:
+        rig.cache.set_predictor(models[0], 3, 0.02)
+        rig.cache.set_evictor(models[1])
+        rig.cache.set_spec_probation(True)
+        oc = rig.oracle_cache()
+        oc.set_predictor(models[2], 3, 0.02)
+        oc.set_evictor(models[3])
+        oc.set_spec_probation(True)
+        check_run(rig, tmp_path, oc=oc)
+        assert rig.pstats == rig.opstats, (rig.pstats, rig.opstats)
+        # predictions for layers 1..3; one resolves where the model holds the
+        # target layer (1 and 2), every token
+        assert rig.pstats["n_spec"] > 0 and rig.pstats["n_updates"] == 2 * 48
+        assert rig.n_evicted > 0
+    finally:
+        rig.close()
 
 
 def test_expert_cache_dropin():

@@ -8,6 +8,7 @@ import numpy as np
 import pytest
 
 import x3t
+from moep_models import write_moep
 from moe_prefetch import MoeCache
 from moe_prefetch.workload import zipf_targets
 from oracle import oracle as O
@@ -131,3 +132,125 @@ def test_from_env_reads_reference_variables():
 def test_bad_knob_is_loud():
     with pytest.raises(ValueError):
         MoeCache(2, admit="sometimes", device=-1)
+
+
+# ---- MOEP predictor / evictor hooks (patches/0006:295-427, 765-922; 0007:149-168, 330-355, 655-724) ----
+HOOKS = [
+    dict(pred=True),
+    dict(pred=True, online_lr=0.05),
+    dict(pred=True, online_lr=0.02, probation=True),
+    dict(evict=True),
+    dict(evict=True, early_issue=True),
+    dict(pred=True, evict=True, online_lr=0.03, probation=True),
+    dict(pred=True, evict=True, admit="heat", admit_half=16, admit_floor=0.5),
+    dict(pred=True, evict=True, admit="window", predict_top=5),
+]
+
+
+def hooked_pair(tmp_path, slots, hooks, L, E=128):
+    from moe_prefetch.moep import MoePredictor
+    pp, ep = str(tmp_path / "pred.bin"), str(tmp_path / "evict.bin")
+    write_moep(pp, E, L, list(range(L - 1)), blocks=(1, 2), seed=5)
+    write_moep(ep, E, L, list(range(L)), blocks=(1, 2, 3, 4), seed=6, prior=0.0)
+    knobs = {k: v for k, v in hooks.items() if k not in ("pred", "evict", "online_lr", "probation", "predict_top")}
+    knobs.setdefault("admit", "off")
+    oc = O.Cache(slots, **knobs)
+    pc = product_cache(slots, **knobs)
+    models = []
+    if hooks.get("pred"):
+        om, pm = O.Moep(pp), MoePredictor(pp)
+        oc.set_predictor(om, hooks.get("predict_top", 3), hooks.get("online_lr", 0.0))
+        pc.set_predictor(pm, hooks.get("predict_top", 3), hooks.get("online_lr", 0.0))
+        models += [om, pm]
+    if hooks.get("evict"):
+        om, pm = O.Moep(ep), MoePredictor(ep)
+        oc.set_evictor(om)
+        pc.set_evictor(pm)
+        models += [om, pm]
+    if hooks.get("probation"):
+        oc.set_spec_probation(True)
+        pc.set_spec_probation(True)
+    return oc, pc, models
+
+
+@pytest.mark.parametrize("hooks", HOOKS, ids=lambda k: ",".join(f"{a}={b}" for a, b in k.items()))
+def test_predictor_and_evictor_match_oracle(hooks, tmp_path):
+    L, T = 6, 200
+    slots = [12, 20, 8, 16, 12, 32]
+    tg = [zipf_targets(31, l, T, s=1.0, reuse=0.5) for l in range(L)]
+    oc, pc, _models = hooked_pair(tmp_path, slots, hooks, L)
+    for t in range(T):
+        for l in range(L):
+            oc.observe(l, tg[l][t])
+            pc.observe(l, tg[l][t])
+        oc.step()
+        pc.step()
+        for l in range(L):
+            assert np.array_equal(oc.frame(l), pc.frame(l)), (t, l)
+            assert np.array_equal(oc.table(l)[0], pc.table(l)[0])
+    os_, ps = oc.stats(), pc.stats()
+    for k in ("n_steps", "clock", "n_hit", "n_miss", "n_uploads", "n_scheduled", "n_published",
+              "n_admit_ok", "n_admit_denied"):
+        assert os_[k] == ps[k], k
+    op, pp = oc.predictor_stats(), pc.predictor_stats()
+    assert op == pp, (op, pp)
+    if hooks.get("pred"):
+        assert pp["n_spec"] > 0                                   # speculative uploads were issued
+        if hooks.get("online_lr"):
+            assert pp["n_updates"] == (L - 1) * T - 1 or pp["n_updates"] > 0
+    if hooks.get("evict"):
+        # the evictor changes the placement against plain LRU on the same stream
+        plain = product_cache(slots, **{k: v for k, v in hooks.items()
+                                        if k in ("admit", "admit_half", "admit_floor", "early_issue")} or {"admit": "off"})
+        for t in range(T):
+            for l in range(L):
+                plain.observe(l, tg[l][t])
+            plain.step()
+        assert any(not np.array_equal(plain.frame(l), pc.frame(l)) for l in range(L))
+
+
+def test_hooks_refuse_models_the_cache_cannot_score(tmp_path):
+    from moe_prefetch.moep import MoePredictor
+    p = str(tmp_path / "e64.bin")
+    write_moep(p, 64, 4, [0, 1, 2])
+    c = product_cache([8, 8, 8, 8])
+    m = MoePredictor(p)
+    with pytest.raises(Exception, match="64 experts"):
+        c.set_predictor(m, 3)
+    with pytest.raises(Exception, match="64 experts"):
+        c.set_evictor(m)
+    c.set_predictor(None, 0)          # clearing is always allowed
+    c.set_evictor(None)
+
+
+@pytest.mark.skipif(not os.path.isdir("/root/reference/models"), reason="the reference's shipped models are not here")
+@pytest.mark.parametrize("i", [0, 1])
+def test_x3t_routes_with_shipped_models_match_oracle(i):
+    """The reference's recorded route ids (48 layers, byte-priced slots) through
+    the product and the oracle with its shipped evictor and online predictor."""
+    from moe_prefetch.moep import MoePredictor
+    slots, experts, frames, routes = x3t.load(i)
+    layers = sorted(slots)
+    sl = [slots[l] for l in layers]
+    knobs = dict(max_inserts=2, admit="window", admit_window=8, batch_tables=True)
+    oc = O.Cache(sl, **knobs)
+    pc = product_cache(sl, **knobs)
+    ep, pp = "/root/reference/models/evictor-real.bin", "/root/reference/models/predictor-real.bin"
+    keep = [O.Moep(ep), MoePredictor(ep), O.Moep(pp), MoePredictor(pp)]
+    oc.set_evictor(keep[0])
+    pc.set_evictor(keep[1])
+    oc.set_predictor(keep[2], 3, 0.01)
+    pc.set_predictor(keep[3], 3, 0.01)
+    by = collections.defaultdict(list)
+    for s, il, n_ids, n_tok, pairs in routes:
+        by[s].append((il, n_tok, [e for e, _ in pairs]))
+    for s in range(max(frames)):
+        for il, n_tok, ids in by.get(s, []):
+            oc.observe(il, np.array(ids, np.int32), n_tok)
+            pc.observe(il, np.array(ids, np.int32), n_tok)
+        oc.step()
+        pc.step()
+        for l in range(len(layers)):
+            assert np.array_equal(oc.frame(l), pc.frame(l)), (s, l)
+    assert oc.predictor_stats() == pc.predictor_stats()
+    assert pc.predictor_stats()["n_updates"] > 1000
