@@ -62,6 +62,37 @@ static inline float canon_expf(float x) {
     return p * mp::bits_f32(e << 23);
 }
 
+// the order-preserving unsigned image of a selection value, then the lower id first
+static inline uint64_t sel_key(float v, int id) {
+    v = v != v ? -INFINITY : v + 0.0f;
+    uint32_t b;
+    memcpy(&b, &v, 4);
+    const uint32_t o = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+    return ((uint64_t)o << 32) | (uint64_t)(0xffffffffu - (uint32_t)id);
+}
+
+void route_topk(const float *logits, int E, const float *prior, bool prior_on_logits, int K, int32_t *ids) {
+    float m = logits[0];
+    for (int e = 1; e < E; ++e) m = fmaxf(m, logits[e]);
+    float ex[256], p[256];
+    float sum = 0.0f;
+    for (int c = 0; c < E / 64; ++c) {
+        float t[64];
+        for (int i = 0; i < 64; ++i) t[i] = ex[64 * c + i] = canon_expf(logits[64 * c + i] - m);
+        for (int w = 1; w < 64; w *= 2)
+            for (int i = 0; i < 64; i += 2 * w) t[i] = t[i] + t[i + w];
+        sum = c == 0 ? t[0] : sum + t[0];
+    }
+    uint64_t key[256];
+    for (int e = 0; e < E; ++e) {
+        p[e] = ex[e] / sum;
+        const float v = !prior ? p[e] : (prior_on_logits ? logits[e] + prior[e] : p[e] + prior[e]);
+        key[e] = sel_key(v, e);
+    }
+    std::partial_sort(key, key + K, key + E, [](uint64_t a, uint64_t b) { return a > b; });
+    for (int k = 0; k < K; ++k) ids[k] = (int32_t)(0xffffffffu - (uint32_t)key[k]);
+}
+
 void quant_q8k(const float *x, int n, uint8_t *out) {
     for (int b = 0; b < n / QK; ++b) {
         const float *v = x + (size_t)b * QK;

@@ -39,6 +39,15 @@ void experts(Team *t, const CpuExpert *e, int n, int H, int I, int down_type, fl
 // reads would fault page by page, ~1 ms per expert, in the middle of a decode)
 void prefault(Team *t, const void *p, size_t n);
 
+// The token's K routed experts from its logits (bias added), as the batch-1
+// decode kernels select them: the softmax in their canonical order (the
+// maximum; canonical exp; per 64-expert chunk a balanced pairwise sum in
+// expert order, the chunks added in order; IEEE division), plus the cache
+// prior (on the probabilities, or on the logits), then the K best by the
+// selection value with the lower id first on a tie (a NaN as -inf, -0 as +0).
+// ids in rank order.  E a multiple of 64, at most 256; K <= E.
+void route_topk(const float *logits, int E, const float *prior, bool prior_on_logits, int K, int32_t *ids);
+
 // building blocks (exposed for the tests of this file's arithmetic)
 void quant_q8k(const float *x, int n, uint8_t *out);
 float dot_q4k(const uint8_t *row, const uint8_t *q8, int nb);

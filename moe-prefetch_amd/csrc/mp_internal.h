@@ -19,10 +19,17 @@ constexpr int SC_Q8X_BYTES = 8 * 292;          // Q8_K of x at H = 2048
 // load), so the host takes the layer once every word of it carries the token's
 // number: no word has to land before another.  q8x (the Q8_K of x) is
 // written, and waited for, by an earlier kernel of the layer.
+constexpr int SC_MAX_E = 256;
 struct alignas(256) SidecarPost {
     uint64_t tag[16];
     uint8_t pad0[128];
     uint8_t q8x[SC_Q8X_BYTES];
+    // the fused layer also posts what the host needs to route the token
+    // itself, as soon as it exists: (seq << 32) once Q8_K(x) is written, and
+    // every logit (bias added) as (seq << 32) | its bits
+    uint64_t q8x_tag;
+    uint8_t pad1[120];
+    uint64_t logit[SC_MAX_E];
 };
 __host__ __device__ inline uint64_t sc_tag(uint32_t seq, int32_t slot, int32_t id) {
     return ((uint64_t)seq << 32) | ((uint64_t)(uint16_t)slot << 16) | (uint64_t)(uint16_t)id;
@@ -179,6 +186,7 @@ inline size_t fused_words(int K, int I, int H) {
 }
 
 constexpr int MAX_E = 256;   // experts per layer the kernels support
+static_assert(MAX_E == SC_MAX_E, "the post holds every logit");
 
 // batched layer: pairs dispatched expert-major, experts from slots or a store
 struct GroupedArgs {

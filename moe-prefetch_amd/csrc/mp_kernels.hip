@@ -843,12 +843,15 @@ __device__ void fused_router(const FusedArgs &a, int e, uint32_t seq, uint8_t *s
     const float part = router_quarter(a.r.W + (size_t)e * a.r.H, a.r.x, nullptr, a.r.H, wave, lane);
     if (lane == 0) s_q[wave] = part;
     __syncthreads();
-    if (threadIdx.x < FUSED_LOG_COPIES) {
+    if (threadIdx.x <= FUSED_LOG_COPIES) {
         float acc = s_q[0];
 #pragma unroll
         for (int q = 1; q < RL_WAVES; ++q) acc = acc + s_q[q];
         if (a.r.bias) acc = acc + a.r.bias[e];
-        store_tagged(a.xlog + (size_t)threadIdx.x * MAX_E + e, tagged(seq, acc));
+        if (threadIdx.x < FUSED_LOG_COPIES)
+            store_tagged(a.xlog + (size_t)threadIdx.x * MAX_E + e, tagged(seq, acc));
+        else if (a.r.post)          // the host routes the token from these (CPU-assisted serving)
+            __hip_atomic_store(&a.r.post->logit[e], tagged(seq, acc), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
     }
 }
 
@@ -1005,6 +1008,10 @@ __device__ void fused_select(const FusedArgs &a, uint32_t seq, uint8_t *smem) {
             q8k_wave_vals(xv, lane, q, d);
             q8k_store_sys(q, d, (uint32_t *)(r.post->q8x + (size_t)b * Q8K_BYTES), lane);
         }
+    if (r.post) {
+        __syncthreads();            // every wave's Q8_K words have reached host memory
+        if (tid == 0) __hip_atomic_store(&r.post->q8x_tag, (uint64_t)seq << 32, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    }
     if (!fused_route(a, seq, 0, s, r.K, -1)) {
         if (tid == 0) fused_late(a, seq);
         return;

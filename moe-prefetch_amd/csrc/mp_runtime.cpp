@@ -213,6 +213,7 @@ struct moe_cache {
     double sc_timeout_s = 2.0;
     std::vector<float> sc_h, sc_y;         // host scratch: h, and the rows before they are published
     std::vector<uint8_t> sc_q8h, sc_q8x;
+    std::vector<int32_t> sc_ids;           // [L][K]: the ids each layer was served with this token
     uint64_t n_cpu_served = 0;
     double sc_wait_us = 0.0, sc_cpu_us = 0.0;   // host time waiting for posts / computing experts
     // heat file (LLAMA_MOE_HEAT_FILE), freeze (LLAMA_MOE_CACHE_FREEZE) and
@@ -2353,6 +2354,7 @@ int moe_cache_set_sidecar(moe_cache *c, int n_threads, int num, int den) {
     c->sc_y.resize((size_t)c->K * c->H);
     c->sc_q8h.resize((size_t)c->K * (c->I / 256) * mp::Q8K_BYTES);
     c->sc_q8x.resize((size_t)(c->H / 256) * mp::Q8K_BYTES);
+    c->sc_ids.assign((size_t)c->cfg.n_layers * c->K, -1);
     // the CPU reads the stores from now on: fault their pages in here, not
     // expert by expert in the middle of a token
     for (const Layer &ls : c->L)
@@ -2371,10 +2373,22 @@ static bool post_ready(const mp::SidecarPost &p, int K, uint32_t seq) {
     return true;
 }
 
-static int sidecar_serve(moe_cache *c, int l, uint32_t seq) {
+// the fused layer's early post: Q8_K(x) written, and every logit
+static bool logits_ready(const mp::SidecarPost &p, int E, uint32_t seq) {
+    if ((uint32_t)(__atomic_load_n(&p.q8x_tag, __ATOMIC_ACQUIRE) >> 32) != seq) return false;
+    for (int e = 0; e < E; ++e)
+        if ((uint32_t)(__atomic_load_n(&p.logit[e], __ATOMIC_ACQUIRE) >> 32) != seq) return false;
+    return true;
+}
+
+// by_logits (the fused layer): the host routes the token itself from the
+// posted logits, with the published tables' host mirrors, as soon as the
+// router rows are done, instead of waiting for the selection's post
+static int sidecar_serve(moe_cache *c, int l, uint32_t seq, bool by_logits) {
     const auto t0 = std::chrono::steady_clock::now();
     unsigned spins = 0;
-    while (!post_ready(c->sc_post[l], c->K, seq)) {
+    const mp::SidecarPost &p = c->sc_post[l];
+    while (by_logits ? !logits_ready(p, c->E, seq) : !post_ready(p, c->K, seq)) {
         _mm_pause();
         if ((++spins & 1023u) == 0 &&
             std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count() > c->sc_timeout_s)
@@ -2384,7 +2398,18 @@ static int sidecar_serve(moe_cache *c, int l, uint32_t seq) {
     const auto t1 = std::chrono::steady_clock::now();
     c->sc_wait_us += std::chrono::duration<double, std::micro>(t1 - t0).count();
     const Layer &ls = c->L[l];
-    const mp::SidecarPost &p = c->sc_post[l];
+    int32_t *rid = c->sc_ids.data() + (size_t)l * c->K;       // the ids the host served with, checked after the token
+    if (by_logits) {
+        float lg[mp::SC_MAX_E];
+        for (int e = 0; e < c->E; ++e) {
+            const uint32_t b = (uint32_t)p.logit[e];
+            memcpy(&lg[e], &b, 4);
+        }
+        mpc::route_topk(lg, c->E, c->d_prior ? c->h_prior + (size_t)l * c->E : nullptr, c->cfg.prior_on_logits != 0,
+                        c->K, rid);
+    } else {
+        for (int k = 0; k < c->K; ++k) rid[k] = (int)(p.tag[k] & 0xffff);
+    }
     // the exchange block is memory the GPU reads and writes over PCIe: copy
     // x's Q8_K out of it once, compute into host scratch, publish the rows once
     memcpy(c->sc_q8x.data(), p.q8x, c->sc_q8x.size());
@@ -2392,8 +2417,8 @@ static int sidecar_serve(moe_cache *c, int l, uint32_t seq) {
     int kk[16];
     int n = 0, r = 0;
     for (int k = 0; k < c->K; ++k) {
-        const uint64_t tg = p.tag[k];
-        const int id = (int)(tg & 0xffff), slot = (int)((tg >> 16) & 0xffff);
+        const int id = rid[k];
+        const int slot = by_logits ? c->h_tbl[(size_t)l * c->E + id] : (int)((p.tag[k] >> 16) & 0xffff);
         if (id < 0 || id >= ls.E || (slot >= 0 && slot < ls.S)) continue;  // outside the store, or read from a slot
         if (r++ % c->sc_den < c->sc_num) {
             kk[n] = k;
@@ -2734,7 +2759,7 @@ int moe_decode_token(moe_cache *c, const float *x, const float *bias, float *out
     int serve_err = MOE_OK;
     if (sc) {               // serve the layers as the GPU reaches them
         mpc::team_hot(c->team, true);
-        for (int l = 0; l < NL && serve_err == MOE_OK; ++l) serve_err = sidecar_serve(c, l, seq);
+        for (int l = 0; l < NL && serve_err == MOE_OK; ++l) serve_err = sidecar_serve(c, l, seq, fused);
         mpc::team_hot(c->team, false);
         if (serve_err != MOE_OK) abort_joins();
     }
@@ -2757,6 +2782,9 @@ int moe_decode_token(moe_cache *c, const float *x, const float *bias, float *out
         }
         if (serve_err != MOE_OK) return serve_err;
         if (late) return fail(MOE_ERR_HIP, "a join kernel gave up waiting for the host (%.1f s)", c->sc_timeout_s);
+        // the host's routing must have been the GPU's (it chose which experts it computed)
+        if (memcmp(c->sc_ids.data(), c->h_ids, (size_t)NL * c->K * 4) != 0)
+            return fail(MOE_ERR_STATE, "the host's routing of a layer differs from the GPU's");
     }
     if (c->timing) {
         const uint64_t gu_b = 2ull * c->I * (c->H / 256) * mp::Q4K_BYTES;
