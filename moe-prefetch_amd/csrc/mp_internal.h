@@ -24,12 +24,12 @@ struct alignas(256) SidecarPost {
     uint64_t tag[16];
     uint8_t pad0[128];
     uint8_t q8x[SC_Q8X_BYTES];
-    // the fused layer also posts what the host needs to route the token
-    // itself, as soon as it exists: (seq << 32) once Q8_K(x) is written, and
-    // every logit (bias added) as (seq << 32) | its bits
-    uint64_t q8x_tag;
-    uint8_t pad1[120];
+    // the fused layer also posts what the host needs to route the token and
+    // compute its experts as soon as each part exists, as tagged words
+    // (seq << 32) | payload: every logit (bias added) and the 32-bit words
+    // of Q8_K(x) (q8x's bytes, word by word)
     uint64_t logit[SC_MAX_E];
+    uint64_t q8x_words[SC_Q8X_BYTES / 4];
 };
 __host__ __device__ inline uint64_t sc_tag(uint32_t seq, int32_t slot, int32_t id) {
     return ((uint64_t)seq << 32) | ((uint64_t)(uint16_t)slot << 16) | (uint64_t)(uint16_t)id;
@@ -155,8 +155,10 @@ struct JoinArgs {
 // Inside the launch the phases pass tagged 8-byte words, (token sequence
 // number << 32) | payload, each written and read whole at agent scope; a word
 // is valid once its tag is the token's number, so nothing is reset between
-// tokens.  Workgroups in index order: [0, E) router rows, the selection,
-// gate/up row tiles, down row tiles, combine tiles; a workgroup waits only
+// tokens.  Workgroups in index order: with CPU-assisted serving first H/256
+// that post x's Q8_K blocks to the host, then [0, E) router rows (each also
+// posting its logit to the host when serving), the selection, gate/up row
+// tiles, down row tiles, combine tiles; a workgroup waits only
 // for words of workgroups with a lower index.  The gate/up workgroups route
 // the token themselves from the posted logits (the selection's code, so the
 // same ids), which spares them the wait for the selection's record; the

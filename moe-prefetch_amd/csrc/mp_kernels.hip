@@ -76,6 +76,21 @@ __device__ void q8k_store_sys(const int q[4], float d, uint32_t *out, int lane) 
     __builtin_amdgcn_s_waitcnt(0x0f70);
 }
 
+// The same words as q8k_store_sys, each as (seq << 32) | word, without the
+// wait: a reader takes a word once its tag is seq.
+__device__ void q8k_store_tagged_sys(const int q[4], float d, uint64_t *out, uint32_t seq, int lane) {
+    const int gs = q8k_group_sum(q);
+    const int gs_odd = __shfl_down(gs, 4, 64);
+    const uint32_t packed = (uint32_t)(q[0] & 0xff) | ((uint32_t)(q[1] & 0xff) << 8) |
+                            ((uint32_t)(q[2] & 0xff) << 16) | ((uint32_t)(q[3] & 0xff) << 24);
+    const uint64_t tag = (uint64_t)seq << 32;
+    __hip_atomic_store(out + 1 + lane, tag | packed, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    if ((lane & 7) == 0)
+        __hip_atomic_store(out + 1 + QK / 4 + (lane >> 3), tag | (((uint32_t)gs & 0xffffu) | ((uint32_t)gs_odd << 16)),
+                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    if (lane == 0) __hip_atomic_store(out, tag | __float_as_uint(d), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+
 // ---------------------------------------------------------------------------
 // router
 struct RouteArgs {
@@ -855,6 +870,20 @@ __device__ void fused_router(const FusedArgs &a, int e, uint32_t seq, uint8_t *s
     }
 }
 
+// CPU-assisted serving: Q8_K block b of x for the host, as tagged words (no
+// wait for the stores: every word validates itself).  These workgroups come
+// first in the launch, so x's codes reach the host before the logits.
+__device__ void fused_post_q8x(const FusedArgs &a, int b, uint32_t seq) {
+    if (threadIdx.x >= 64) return;
+    const int lane = threadIdx.x;
+    const float4 v = *(const float4 *)(a.r.x + QK * b + 4 * lane);
+    const float xv[4] = {v.x, v.y, v.z, v.w};
+    int q[4];
+    float d;
+    q8k_wave_vals(xv, lane, q, d);
+    q8k_store_tagged_sys(q, d, a.r.post->q8x_words + (size_t)b * (Q8K_BYTES / 4), seq, lane);
+}
+
 // LDS of the in-workgroup routing (written by wave 0)
 struct RouteScratch {
     ExpertSrc src;            // the workgroup's expert (rank want_k)
@@ -997,21 +1026,6 @@ __device__ void fused_select(const FusedArgs &a, uint32_t seq, uint8_t *smem) {
     RouteScratch *s = (RouteScratch *)(smem + FUSED_LDS_RS);
     int *s_slot = (int *)smem;
     float *s_w = (float *)(s_slot + 16);
-    // Q8_K of x for the host's share of absent experts, written through to
-    // host memory (each wave waits for its stores) before the post's words
-    if (r.post)
-        for (int b = wave; b < r.H / QK; b += 4) {
-            const float4 v = *(const float4 *)(r.x + QK * b + 4 * lane);
-            const float xv[4] = {v.x, v.y, v.z, v.w};
-            int q[4];
-            float d;
-            q8k_wave_vals(xv, lane, q, d);
-            q8k_store_sys(q, d, (uint32_t *)(r.post->q8x + (size_t)b * Q8K_BYTES), lane);
-        }
-    if (r.post) {
-        __syncthreads();            // every wave's Q8_K words have reached host memory
-        if (tid == 0) __hip_atomic_store(&r.post->q8x_tag, (uint64_t)seq << 32, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-    }
     if (!fused_route(a, seq, 0, s, r.K, -1)) {
         if (tid == 0) fused_late(a, seq);
         return;
@@ -1311,6 +1325,13 @@ __global__ __launch_bounds__(256) void fused_kernel(FusedArgs a) {
     const int kt = a.x.K + a.x.n_shared;
     const int nG = kt * (a.x.I / FUSED_GU_TILE), nD = kt * (a.x.H / FUSED_DN_TILE);
     int g = (int)blockIdx.x;
+    if (a.r.post) {
+        if (g < a.r.H / QK) {
+            fused_post_q8x(a, g, seq);
+            return;
+        }
+        g -= a.r.H / QK;
+    }
     if (g < E) {
         fused_router(a, g, seq, smem);
     } else if (g == E) {
@@ -1479,8 +1500,8 @@ hipError_t launch_join(const JoinArgs &a, hipStream_t st) {
 
 hipError_t launch_fused(const FusedArgs &a, hipStream_t st, hipEvent_t e0, hipEvent_t e1) {
     const int kt = a.x.K + a.x.n_shared;
-    const unsigned n = (unsigned)(a.r.E + 1 + kt * (a.x.I / FUSED_GU_TILE) + kt * (a.x.H / FUSED_DN_TILE) +
-                                  (a.x.ypart ? 0 : a.x.H / 256));
+    const unsigned n = (unsigned)((a.r.post ? a.r.H / QK : 0) + a.r.E + 1 + kt * (a.x.I / FUSED_GU_TILE) +
+                                  kt * (a.x.H / FUSED_DN_TILE) + (a.x.ypart ? 0 : a.x.H / 256));
     if (a.x.down_type == TYPE_Q6K) return launch(fused_kernel<TYPE_Q6K>, dim3(n), dim3(256), st, e0, e1, a);
     return launch(fused_kernel<TYPE_Q4K>, dim3(n), dim3(256), st, e0, e1, a);
 }

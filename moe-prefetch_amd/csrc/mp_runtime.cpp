@@ -2373,11 +2373,12 @@ static bool post_ready(const mp::SidecarPost &p, int K, uint32_t seq) {
     return true;
 }
 
-// the fused layer's early post: Q8_K(x) written, and every logit
-static bool logits_ready(const mp::SidecarPost &p, int E, uint32_t seq) {
-    if ((uint32_t)(__atomic_load_n(&p.q8x_tag, __ATOMIC_ACQUIRE) >> 32) != seq) return false;
+// the fused layer's early post: every logit and every word of Q8_K(x)
+static bool logits_ready(const mp::SidecarPost &p, int E, int n_q8_words, uint32_t seq) {
     for (int e = 0; e < E; ++e)
         if ((uint32_t)(__atomic_load_n(&p.logit[e], __ATOMIC_ACQUIRE) >> 32) != seq) return false;
+    for (int i = 0; i < n_q8_words; ++i)
+        if ((uint32_t)(__atomic_load_n(&p.q8x_words[i], __ATOMIC_ACQUIRE) >> 32) != seq) return false;
     return true;
 }
 
@@ -2388,7 +2389,8 @@ static int sidecar_serve(moe_cache *c, int l, uint32_t seq, bool by_logits) {
     const auto t0 = std::chrono::steady_clock::now();
     unsigned spins = 0;
     const mp::SidecarPost &p = c->sc_post[l];
-    while (by_logits ? !logits_ready(p, c->E, seq) : !post_ready(p, c->K, seq)) {
+    const int n_q8_words = (int)(c->sc_q8x.size() / 4);
+    while (by_logits ? !logits_ready(p, c->E, n_q8_words, seq) : !post_ready(p, c->K, seq)) {
         _mm_pause();
         if ((++spins & 1023u) == 0 &&
             std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count() > c->sc_timeout_s)
@@ -2412,7 +2414,12 @@ static int sidecar_serve(moe_cache *c, int l, uint32_t seq, bool by_logits) {
     }
     // the exchange block is memory the GPU reads and writes over PCIe: copy
     // x's Q8_K out of it once, compute into host scratch, publish the rows once
-    memcpy(c->sc_q8x.data(), p.q8x, c->sc_q8x.size());
+    if (by_logits) {
+        uint32_t *q8 = (uint32_t *)c->sc_q8x.data();
+        for (int i = 0; i < n_q8_words; ++i) q8[i] = (uint32_t)p.q8x_words[i];
+    } else {
+        memcpy(c->sc_q8x.data(), p.q8x, c->sc_q8x.size());
+    }
     mpc::CpuExpert e[16];
     int kk[16];
     int n = 0, r = 0;
