@@ -1437,6 +1437,26 @@ hipError_t launch_down(const ExpertArgs &a, int src, hipStream_t st, hipEvent_t 
 __global__ __launch_bounds__(256) void join_kernel(JoinArgs a) {
     __shared__ int s_ok;
     __shared__ int s_cpu[16];
+    if (threadIdx.x < 16)
+        s_cpu[threadIdx.x] = cpu_served(a.slots, a.ids, a.slot_pool, a.n_slots, a.host_store, a.n_experts, a.cpu_num,
+                                        a.cpu_den, a.K, (int)threadIdx.x);
+    __syncthreads();
+    const int r = blockIdx.x * 256 + threadIdx.x;
+    // the gate weights and the GPU's rows (an earlier kernel's: in memory)
+    // are requested before the wait for the host, so that after it only the
+    // host's rows cross PCIe
+    constexpr int MK = 16;
+    float y[MK], wk[MK];
+    float ys = 0.0f;
+    if (r < a.H) {
+#pragma unroll
+        for (int k = 0; k < MK; ++k)
+            if (k < a.K) {
+                wk[k] = a.w[k];
+                y[k] = s_cpu[k] ? 0.0f : a.ypart[(size_t)k * a.H + r];
+            }
+        if (a.n_shared) ys = a.ypart[(size_t)a.K * a.H + r];
+    }
     if (threadIdx.x == 0) {
         const uint32_t want = *a.seq;
         const uint64_t t0 = wall_clock64();
@@ -1462,34 +1482,23 @@ __global__ __launch_bounds__(256) void join_kernel(JoinArgs a) {
         }
         s_ok = ok;
     }
-    if (threadIdx.x < 16)
-        s_cpu[threadIdx.x] = cpu_served(a.slots, a.ids, a.slot_pool, a.n_slots, a.host_store, a.n_experts, a.cpu_num,
-                                        a.cpu_den, a.K, (int)threadIdx.x);
     __syncthreads();
-    const int r = blockIdx.x * 256 + threadIdx.x;
     if (r >= a.H) return;
     if (!s_ok) {
         a.out[r] = 0.0f;
         return;
     }
-    // every row's load issued before the first is used: one round trip over
-    // PCIe for the host's rows, not one per expert.  One kind of load for
-    // both sources (system scope: the host's rows bypass the caches; the
-    // GPU's partials, from an earlier kernel, are in memory too).
-    constexpr int MK = 16;
-    float y[MK], wk[MK];
+    // every host row's load issued before the first is used: one round trip
+    // over PCIe (system scope: the host's rows bypass the caches)
 #pragma unroll
     for (int k = 0; k < MK; ++k)
-        if (k < a.K) {
-            const float *src = s_cpu[k] ? a.hrows + (size_t)k * a.H + r : a.ypart + (size_t)k * a.H + r;
-            y[k] = __hip_atomic_load(src, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-            wk[k] = a.w[k];
-        }
+        if (k < a.K && s_cpu[k]) y[k] = __hip_atomic_load(a.hrows + (size_t)k * a.H + r, __ATOMIC_RELAXED,
+                                                          __HIP_MEMORY_SCOPE_SYSTEM);
     float acc = wk[0] * y[0];
 #pragma unroll
     for (int k = 1; k < MK; ++k)
         if (k < a.K) acc = acc + wk[k] * y[k];
-    if (a.n_shared) acc = acc + a.ypart[(size_t)a.K * a.H + r];   // weight 1, after the routed experts
+    if (a.n_shared) acc = acc + ys;     // weight 1, after the routed experts
     a.out[r] = acc;
 }
 
