@@ -2373,13 +2373,14 @@ static bool post_ready(const mp::SidecarPost &p, int K, uint32_t seq) {
     return true;
 }
 
-// the fused layer's early post: every logit and every word of Q8_K(x)
-static bool logits_ready(const mp::SidecarPost &p, int E, int n_q8_words, uint32_t seq) {
-    for (int e = 0; e < E; ++e)
-        if ((uint32_t)(__atomic_load_n(&p.logit[e], __ATOMIC_ACQUIRE) >> 32) != seq) return false;
-    for (int i = 0; i < n_q8_words; ++i)
-        if ((uint32_t)(__atomic_load_n(&p.q8x_words[i], __ATOMIC_ACQUIRE) >> 32) != seq) return false;
-    return true;
+// the fused layer's early post: every logit and every word of Q8_K(x).  The
+// words already seen valid are not read again (n_lg, n_q8 carry over between
+// calls): the device's writes invalidate those lines in the host's caches, so
+// each is fetched once, as it arrives, not all again at the end.
+static bool logits_ready(const mp::SidecarPost &p, int E, int n_q8_words, uint32_t seq, int &n_lg, int &n_q8) {
+    while (n_q8 < n_q8_words && (uint32_t)(__atomic_load_n(&p.q8x_words[n_q8], __ATOMIC_ACQUIRE) >> 32) == seq) ++n_q8;
+    while (n_lg < E && (uint32_t)(__atomic_load_n(&p.logit[n_lg], __ATOMIC_ACQUIRE) >> 32) == seq) ++n_lg;
+    return n_lg == E && n_q8 == n_q8_words;
 }
 
 // by_logits (the fused layer): the host routes the token itself from the
@@ -2390,7 +2391,8 @@ static int sidecar_serve(moe_cache *c, int l, uint32_t seq, bool by_logits) {
     unsigned spins = 0;
     const mp::SidecarPost &p = c->sc_post[l];
     const int n_q8_words = (int)(c->sc_q8x.size() / 4);
-    while (by_logits ? !logits_ready(p, c->E, n_q8_words, seq) : !post_ready(p, c->K, seq)) {
+    int n_lg = 0, n_q8 = 0;
+    while (by_logits ? !logits_ready(p, c->E, n_q8_words, seq, n_lg, n_q8) : !post_ready(p, c->K, seq)) {
         _mm_pause();
         if ((++spins & 1023u) == 0 &&
             std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count() > c->sc_timeout_s)
