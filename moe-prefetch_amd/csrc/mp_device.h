@@ -179,6 +179,21 @@ __device__ inline uint32_t wave_max_u32(uint32_t v) {
     return max(max(a, b), max(c, d));
 }
 
+// unsigned maximum over the wave as a uniform value: the row maxima by lane
+// moves inside each row of 16 lanes, then row_bcast:15 and row_bcast:31
+// carry them across the rows (0 is the identity of the maximum, so the lanes
+// those moves leave out keep their value), and lane 63 holds the maximum of
+// all -- one read of a lane, not four
+__device__ inline uint32_t wave_max_u32_bcast(uint32_t v) {
+    v = max(v, (uint32_t)dpp_i<DPP_XOR1>((int)v));
+    v = max(v, (uint32_t)dpp_i<DPP_XOR2>((int)v));
+    v = max(v, (uint32_t)dpp_i<DPP_HALF_MIRROR>((int)v));
+    v = max(v, (uint32_t)dpp_i<DPP_MIRROR>((int)v));
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x142, 0xA, 0xF, false));     // row_bcast:15
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x143, 0xC, 0xF, false));     // row_bcast:31
+    return __builtin_amdgcn_readlane(v, 63);
+}
+
 // rank of `key` among n keys in LDS (the count of keys above it)
 __device__ inline int key_rank(const uint64_t *s_key, int n, uint64_t key) {
     int rank = 0;

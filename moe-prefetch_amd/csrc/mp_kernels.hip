@@ -884,34 +884,32 @@ __device__ void fused_post_q8x(const FusedArgs &a, int b, uint32_t seq) {
     q8k_store_tagged_sys(q, d, a.r.post->q8x_words + (size_t)b * (Q8K_BYTES / 4), seq, lane);
 }
 
-// LDS of the in-workgroup routing (written by wave 0)
+// LDS of the in-workgroup routing
 struct RouteScratch {
-    ExpertSrc src;            // the workgroup's expert (rank want_k)
     int ids[16];              // the ids in rank order
     int slots[16];            // their table words
     float psel[16];           // their probabilities
-    float ws;                 // the sum of those, in rank order
     int late;
 };
 static_assert(FUSED_LDS_RS + sizeof(RouteScratch) <= FUSED_LDS, "routing LDS");
 static_assert((2048 / QK) * Q8K_BYTES <= FUSED_LDS_W, "gate/up: the Q8_K of x (H = 2048)");
 
-// The routing of the token, as every workgroup that needs it computes it:
-// the same code on the same posted logits (copy `copy`), so the same bits as
-// route_select_kernel -- softmax over 64-expert chunks (each chunk's sum in
-// the canonical order, the chunks added in order), the prior, the score of
-// each expert -- and the n_top best experts, best first, by n_top rounds of
-// a wave-wide maximum of the scores (on a tie the lowest id, as the 64-bit
-// keys order them), each round removing its expert.  Wave 0 alone polls
-// and routes; every round's expert is a uniform value, so its table word,
-// its probability and (want_k >= 0) the source of rank want_k follow from
-// lane reads of registers, with no LDS round trip.  One barrier hands s to
-// the workgroup.  false: the wait for the logits ran out (the caller
-// reports it).
+// The token's routing as every wave that needs it computes it: poll the
+// posted logits (copy `copy`), then the softmax over 64-expert chunks (each
+// chunk's sum in the canonical order, the chunks added in order), the prior,
+// the score of each expert -- the same code on the same bits as
+// route_select_kernel -- and the n_top best experts, best first, by n_top
+// rounds of a wave-wide maximum of the scores (on a tie the lowest id, as
+// the 64-bit keys order them), each round removing its expert.  Each round's
+// expert is a uniform value: with want_k >= 0 its table word follows by a
+// lane read and the source of rank want_k accumulates in scalars (src).
+// With s, lane k keeps the id of rank k, and the ids, table words and
+// probabilities go to s in one lane exchange after the last round.  false:
+// the wait for the logits ran out.
 template <int NC>
-__device__ void route_wave(const FusedArgs &a, uint32_t seq, int copy, RouteScratch *s, int n_top, int want_k) {
+__device__ bool route_wave(const FusedArgs &a, uint32_t seq, int copy, int n_top, int want_k, RouteScratch *s,
+                           ExpertSrc &src) {
     const RouteLaunch &r = a.r;
-    const ExpertArgs &x = a.x;
     const int lane = threadIdx.x & 63;
     float pr[NC];
     int32_t tbl[NC];
@@ -920,32 +918,29 @@ __device__ void route_wave(const FusedArgs &a, uint32_t seq, int copy, RouteScra
         pr[c] = r.prior ? r.prior[64 * c + lane] : 0.0f;
         tbl[c] = r.table[64 * c + lane];
     }
-    const uint64_t *src = a.xlog + (size_t)copy * MAX_E;
+    const uint64_t *lsrc = a.xlog + (size_t)copy * MAX_E;
     uint64_t v[NC];
     bool ok[NC];
 #pragma unroll
     for (int c = 0; c < NC; ++c) ok[c] = false;
-    int late = 0;
     const uint64_t t0 = wall_clock64();
     for (;;) {
         bool all = true;
 #pragma unroll
         for (int c = 0; c < NC; ++c)
-            if (!ok[c]) v[c] = load_tagged(src + 64 * c + lane);
+            if (!ok[c]) v[c] = load_tagged(lsrc + 64 * c + lane);
 #pragma unroll
         for (int c = 0; c < NC; ++c) {
             if (!ok[c]) ok[c] = (uint32_t)(v[c] >> 32) == seq;
             all = all && ok[c];
         }
         if (__all(all)) break;
-        if (wall_clock64() - t0 > a.wait_ticks) {
-            late = 1;
-            break;
-        }
+        if (wall_clock64() - t0 > a.wait_ticks) return false;
         __builtin_amdgcn_s_sleep(1);
     }
-    if (lane == 0) s->late = late;
-    if (late) return;
+    // a chain of dependent cross-lane steps on which the workgroup waits:
+    // ahead of the other workgroups' dot products on this SIMD
+    __builtin_amdgcn_s_setprio(3);
     float l[NC], ex[NC], p[NC];
     float m = 0.0f;
 #pragma unroll
@@ -967,14 +962,13 @@ __device__ void route_wave(const FusedArgs &a, uint32_t seq, int copy, RouteScra
         p[c] = ex[c] / sum;
         u[c] = sel_bits(!r.prior ? p[c] : (r.prior_on_logits ? l[c] + pr[c] : p[c] + pr[c]));
     }
-    float ws = 0.0f;
+    int my_id = 0;                          // lane k < n_top: the id of rank k
     int absent_before = 0;
-    ExpertSrc mine{nullptr, false, false};
     for (int k = 0; k < n_top; ++k) {
         uint32_t mx = u[0];
 #pragma unroll
         for (int c = 1; c < NC; ++c) mx = max(mx, u[c]);
-        mx = wave_max_u32(mx);
+        mx = wave_max_u32_bcast(mx);
         int id = -1;
 #pragma unroll
         for (int c = 0; c < NC; ++c) {
@@ -984,35 +978,63 @@ __device__ void route_wave(const FusedArgs &a, uint32_t seq, int copy, RouteScra
 #pragma unroll
         for (int c = 0; c < NC; ++c)
             if (64 * c + lane == id) u[c] = 0;                // below every score
+        if (s) my_id = lane == k ? id : my_id;
+        if (want_k >= 0) {
+            int32_t slot = 0;
+#pragma unroll
+            for (int c = 0; c < NC; ++c)
+                if ((id >> 6) == c) slot = __builtin_amdgcn_readlane(tbl[c], id & 63);
+            expert_src_step(a.x, id, (int)(uint16_t)slot, k == want_k, absent_before, src);
+        }
+    }
+    if (s) {
         int32_t slot = 0;
         float pk = 0.0f;
 #pragma unroll
-        for (int c = 0; c < NC; ++c)
-            if ((id >> 6) == c) {
-                slot = __builtin_amdgcn_readlane(tbl[c], id & 63);
-                pk = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(p[c]), id & 63));
+        for (int c = 0; c < NC; ++c) {
+            const int32_t t = __shfl(tbl[c], my_id & 63);
+            const float q = __shfl(p[c], my_id & 63);
+            if ((my_id >> 6) == c) {
+                slot = t;
+                pk = q;
             }
-        if (want_k >= 0) expert_src_step(x, id, (int)(uint16_t)slot, k == want_k, absent_before, mine);
-        ws = ws + pk;
-        if (lane == 0) {
-            s->ids[k] = id;
-            s->slots[k] = slot;
-            s->psel[k] = pk;
+        }
+        if (lane < n_top) {
+            s->ids[lane] = my_id;
+            s->slots[lane] = slot;
+            s->psel[lane] = pk;
         }
     }
-    if (lane == 0) {
-        s->ws = ws;
-        s->src = mine;
+    __builtin_amdgcn_s_setprio(0);
+    return true;
+}
+template <int NC>
+__device__ bool route_wave(const FusedArgs &a, uint32_t seq, int copy, int n_top, int want_k, RouteScratch *s) {
+    ExpertSrc unused{nullptr, false, false};
+    return route_wave<NC>(a, seq, copy, n_top, want_k, s, unused);
+}
+// every wave routes the token itself (same code, same bits): no hand-over
+// of the routing between waves
+__device__ bool route_in_wave(const FusedArgs &a, uint32_t seq, int copy, int n_top, int want_k, ExpertSrc &src) {
+    switch (a.r.E >> 6) {
+    case 1: return route_wave<1>(a, seq, copy, n_top, want_k, nullptr, src);
+    case 2: return route_wave<2>(a, seq, copy, n_top, want_k, nullptr, src);
+    case 3: return route_wave<3>(a, seq, copy, n_top, want_k, nullptr, src);
+    default: return route_wave<4>(a, seq, copy, n_top, want_k, nullptr, src);
     }
 }
-__device__ bool fused_route(const FusedArgs &a, uint32_t seq, int copy, RouteScratch *s, int n_top, int want_k) {
+// wave 0 routes into s, one barrier hands it to the workgroup; false: the
+// wait for the logits ran out (the caller reports it)
+__device__ bool fused_route(const FusedArgs &a, uint32_t seq, int copy, RouteScratch *s, int n_top) {
     if ((threadIdx.x >> 6) == 0) {
+        bool ok;
         switch (a.r.E >> 6) {
-        case 1: route_wave<1>(a, seq, copy, s, n_top, want_k); break;
-        case 2: route_wave<2>(a, seq, copy, s, n_top, want_k); break;
-        case 3: route_wave<3>(a, seq, copy, s, n_top, want_k); break;
-        default: route_wave<4>(a, seq, copy, s, n_top, want_k); break;
+        case 1: ok = route_wave<1>(a, seq, copy, n_top, -1, s); break;
+        case 2: ok = route_wave<2>(a, seq, copy, n_top, -1, s); break;
+        case 3: ok = route_wave<3>(a, seq, copy, n_top, -1, s); break;
+        default: ok = route_wave<4>(a, seq, copy, n_top, -1, s); break;
         }
+        if ((threadIdx.x & 63) == 0) s->late = !ok;
     }
     __syncthreads();
     return !s->late;
@@ -1026,15 +1048,17 @@ __device__ void fused_select(const FusedArgs &a, uint32_t seq, uint8_t *smem) {
     RouteScratch *s = (RouteScratch *)(smem + FUSED_LDS_RS);
     int *s_slot = (int *)smem;
     float *s_w = (float *)(s_slot + 16);
-    if (!fused_route(a, seq, 0, s, r.K, -1)) {
+    if (!fused_route(a, seq, 0, s, r.K)) {
         if (tid == 0) fused_late(a, seq);
         return;
     }
     if (wave == 0) {
+        float ws = 0.0f;                // the routed probabilities' sum, in rank order
+        for (int k = 0; k < r.K; ++k) ws = ws + s->psel[k];
         if (lane < r.K) {
             const int id = s->ids[lane];
             const int slot = s->slots[lane];
-            const float w = s->psel[lane] / s->ws;
+            const float w = s->psel[lane] / ws;
             r.ids[lane] = id;
             r.w[lane] = w;
             r.slots[lane] = slot;
@@ -1068,7 +1092,6 @@ __device__ void fused_gateup(const FusedArgs &a, int g, uint32_t seq, uint8_t *s
     const int per = x.I / FUSED_GU_TILE;
     const int k = g / per, tile = g - k * per;
     uint8_t *s_q8x = smem;                                          // [H / 256][292]
-    RouteScratch *rs = (RouteScratch *)(smem + FUSED_LDS_RS);
     for (int b = wave; b < x.H / QK; b += 4) {         // the bytes route_logits_kernel writes
         const float4 v = *(const float4 *)(a.r.x + QK * b + 4 * lane);
         const float xv[4] = {v.x, v.y, v.z, v.w};
@@ -1077,16 +1100,14 @@ __device__ void fused_gateup(const FusedArgs &a, int g, uint32_t seq, uint8_t *s
         q8k_wave_vals(xv, lane, q, d);
         q8k_store(q, d, s_q8x + b * Q8K_BYTES, lane);
     }
+    __syncthreads();                                   // the Q8_K of x, for every wave
     ExpertSrc src{x.shared, false, false};
-    if (k < x.K) {                                     // (fused_route's barrier orders the LDS writes)
-        if (!fused_route(a, seq, g % FUSED_LOG_COPIES, rs, k + 1, k)) {
-            if (threadIdx.x == 0) fused_late(a, seq);
+    if (k < x.K) {
+        if (!route_in_wave(a, seq, g % FUSED_LOG_COPIES, k + 1, k, src)) {
+            if (lane == 0) fused_late(a, seq);
             return;
         }
-        src = rs->src;
         if (src.cpu) return;
-    } else {
-        __syncthreads();
     }
     const int b = lane & 7, i = (lane >> 3) & 3;
     const bool is_gate = lane < 32;
