@@ -900,6 +900,8 @@ def run_wide(args, wl):
     cache = wl.cache(**knobs)
     cache.set_decode_path(split=args.path, graph=True)
     sidecar_setup(args, cache)
+    if args.sidecar > 0 and args.batch_share:
+        cache.set_sidecar_batch(tuple(int(v) for v in args.batch_share.split("/")))
     T1, n_b = wl.T1, wl.T - wl.T1
     el1, s0, s1, ids_log, kept, _ = wl.decode(cache, keep={args.warmup, T1 - 1})
     el2, per, s2, s3, ids_b, kept_b = wl.decode_batches(cache, B, keep={T1, wl.T - 1})
@@ -926,9 +928,19 @@ def run_wide(args, wl):
         f"batch{B}": {"tok_s": round(n_b / el2, 2), "tokens": n_b, "ms_per_batch": per,
                       "cache": cache_summary(s2, s3, n_b),
                       "path": "moe_decode_batch: route, dispatch, grouped up/gate + SwiGLU and down on the matrix "
-                              "cores from slots or the pinned store, shared expert, combine; ids back, one cache "
-                              "step per batch (batch buffers allocated in the first call)"},
+                              "cores from slots" + (
+                                  "; the pairs of experts absent from the slots computed by the host CPU team from "
+                                  "the pinned store while the GPU runs the rest, their rows combined in k order"
+                                  if args.sidecar > 0 else " or the pinned store") +
+                              ", shared expert, combine; ids back, one cache step per batch (batch buffers "
+                              "allocated in the first call)"},
     }
+    if args.sidecar > 0:
+        nb_ = max(n_b // B, 1)
+        result[f"batch{B}"]["sidecar"] = {"share": args.batch_share or args.share,
+            "cpu_pairs_per_token": round((s3["n_cpu_served"] - s2["n_cpu_served"]) / n_b, 2),
+            "host_wait_ms_per_batch": round((s3["sidecar_wait_us"] - s2["sidecar_wait_us"]) / 1e3 / nb_, 3),
+            "host_cpu_ms_per_batch": round((s3["sidecar_cpu_us"] - s2["sidecar_cpu_us"]) / 1e3 / nb_, 3)}
     result.update(kernel_report(*wl.kernel_pass(cache), args.steps, s0, s1))
     result["roofline"]["size_matched"] = size_matched(result["roofline"])
     if not args.no_check:
@@ -1134,6 +1146,8 @@ def parse_args(argv=None):
                     help="0 fused layer launch, 1 fork/join, 2 serial expert launches, 3 unfused launches")
     ap.add_argument("--sidecar", type=int, default=-1,
                     help="host threads serving absent experts (0: GPU only; default: 14 on a 16-CPU host)")
+    ap.add_argument("--batch-share", default="2/3", help="num/den: the host's share of absent experts in batched "
+                                                          "decode (wide40's batch phase; empty: --share)")
     ap.add_argument("--share", default="1/1", help="num/den: absent experts of rank r with r %% den < num go to "
                                                    "the CPU")
     ap.add_argument("--calibrate-copy", action="store_true",

@@ -170,6 +170,14 @@ int moe_experts(const moe_experts_desc *d, void *stream);
  * calls from several threads run one at a time. */
 int moe_cpu_experts(const void *const *experts, int n, const uint8_t *q8x, int H, int I, int down_type, float *rows,
                     int n_threads, int portable);
+/* No counterpart in the reference (its sidecar serves one token).  The same
+ * chain for groups of tokens that share an expert, as CPU-assisted batched
+ * decode runs it: group k applies experts[k] to the next count[k] tokens of
+ * q8x ([tokens][H/256][292]); rows [tokens][H].  Each block of an expert's
+ * rows is read from memory once for all of its tokens; results equal
+ * moe_cpu_experts token by token. */
+int moe_cpu_experts_tokens(const void *const *experts, int n_groups, const int32_t *count, const uint8_t *q8x,
+                           int H, int I, int down_type, float *rows, int n_threads);
 int moe_cpu_has_vnni(void);
 
 /* ---- cache runtime --------------------------------------------------------- */
@@ -478,6 +486,16 @@ int moe_cache_set_staging(moe_cache *c, int on);
  * order.  Outputs, ids and cache traces are identical to the GPU-only path.
  * Needs split 0.  n_threads <= 0 turns it off. */
 int moe_cache_set_sidecar(moe_cache *c, int n_threads, int num, int den);
+/* CPU-assisted serving in moe_decode_batch (no counterpart in the reference,
+ * whose sidecar serves one token, P9:841-912): per layer the routing comes
+ * back to the host, which computes the pairs of the absent experts whose rank
+ * r among the layer's absent experts (ascending id) has r % den < num -- each
+ * expert's rows read once for all its tokens -- while the GPU's grouped
+ * products skip them and read the other absent experts from the pinned store;
+ * the combine then takes the host's weighted rows in k order.  The same
+ * outputs, ids and traces.  num = den = 0 (the default): the share set by
+ * moe_cache_set_sidecar.  Active while moe_cache_set_sidecar is on. */
+int moe_cache_set_sidecar_batch(moe_cache *c, int num, int den);
 /* Per served layer since the last call: (host wait us, host compute us,
  * experts computed), up to max_rows rows into out [rows][3]; returns rows. */
 int moe_cache_sidecar_log(moe_cache *c, float *out, int max_rows);

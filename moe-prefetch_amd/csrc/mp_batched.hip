@@ -190,6 +190,7 @@ __global__ __launch_bounds__(256) void swiglu_quant_kernel(const float *y2, int 
 // grouped expert products
 
 __device__ inline const uint8_t *grouped_expert(const GroupedArgs &a, int e) {
+    if (a.host_mask && a.host_mask[e]) return nullptr;          // computed by the host
     if (a.table) {
         const int s = a.table[e];
         if (a.slot_pool && s >= 0 && s < a.n_slots) return a.slot_pool + (size_t)s * a.slot_bytes;
@@ -561,6 +562,31 @@ __global__ __launch_bounds__(256) void combine_kernel(const float *ypair, int n_
     *o = s;
 }
 
+// the same with the host's rows: pair i's row from hrows when hflag[i] (mapped
+// host memory, read over PCIe), else from ypair; k ascending either way
+__global__ __launch_bounds__(256) void combine_host_kernel(const float *ypair, const float *hrows, const uint8_t *hflag,
+                                                           int n_tok, int K, int H, float *out, int accumulate) {
+    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+    const size_t h4 = (size_t)H / 4;
+    if (i >= (size_t)n_tok * h4) return;
+    const size_t t = i / h4, c = i % h4;
+    auto row = [&](int k) {
+        const size_t pr = (size_t)t * K + k;
+        return hflag[pr] ? ((const float4 *)hrows)[pr * h4 + c] : ((const float4 *)ypair)[pr * h4 + c];
+    };
+    float4 s = row(0);
+    for (int k = 1; k < K; ++k) {
+        const float4 v = row(k);
+        s.x = s.x + v.x; s.y = s.y + v.y; s.z = s.z + v.z; s.w = s.w + v.w;
+    }
+    float4 *o = (float4 *)out + i;
+    if (accumulate) {
+        const float4 p = *o;
+        s.x = p.x + s.x; s.y = p.y + s.y; s.z = p.z + s.z; s.w = p.w + s.w;
+    }
+    *o = s;
+}
+
 // ---------------------------------------------------------------------------
 // launchers (shapes checked by the caller)
 template <typename F, typename... A>
@@ -788,6 +814,13 @@ hipError_t launch_combine(const float *ypair, int n_tok, int K, int H, float *ou
     if (n4 == 0) return hipSuccess;
     return launch_b(combine_kernel, dim3((unsigned)((n4 + 255) / 256)), dim3(256), st, nullptr, nullptr, ypair, n_tok,
                     K, H, out, accumulate);
+}
+
+hipError_t launch_combine_host(const float *ypair, const float *hrows, const uint8_t *hflag, int n_tok, int K, int H,
+                               float *out, int accumulate, hipStream_t st) {
+    const size_t n4 = (size_t)n_tok * (H / 4);
+    return launch_b(combine_host_kernel, dim3((unsigned)((n4 + 255) / 256)), dim3(256), st, nullptr, nullptr, ypair,
+                    hrows, hflag, n_tok, K, H, out, accumulate);
 }
 
 // ---------------------------------------------------------------------------

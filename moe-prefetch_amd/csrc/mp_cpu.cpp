@@ -581,7 +581,78 @@ void chain_item(void *p, int item) {
     else
         down_item(c, item - c.n_up);
 }
+// groups of tokens sharing an expert: the same items, each token of the
+// group in turn against rows that are already in the cache after the first
+struct GChain {
+    const CpuGroup *g;
+    const uint8_t *const *q8x;
+    float *const *y;
+    int n, H, I, down_type;
+    int n_up;
+    float *h;                    // [token][I], tokens numbered as in q8x / y
+    uint8_t *q8h;
+    alignas(64) std::atomic<int> left[16];
+    alignas(64) std::atomic<int> ready[16];
+};
+
+void gup_item(GChain &c, int item) {
+    const int per = c.I / UP_ROWS;
+    const int k = item / per, r0 = (item % per) * UP_ROWS;
+    const CpuGroup &g = c.g[k];
+    const size_t rb = (size_t)(c.H / QK) * Q4K_BYTES;
+    const uint8_t *up = g.w, *gate = g.w + (size_t)c.I * rb;
+    prefetch_rows(mp::TYPE_Q4K, up + r0 * rb, rb, 4, c.H / QK);
+    prefetch_rows(mp::TYPE_Q4K, gate + r0 * rb, rb, 4, c.H / QK);
+    for (int j = g.first; j < g.first + g.n; ++j) {
+        float u[UP_ROWS], gg[UP_ROWS];
+        dot_rows(mp::TYPE_Q4K, up + r0 * rb, rb, UP_ROWS, c.q8x[j], c.H / QK, u);
+        dot_rows(mp::TYPE_Q4K, gate + r0 * rb, rb, UP_ROWS, c.q8x[j], c.H / QK, gg);
+        float *h = c.h + (size_t)j * c.I;
+        for (int r = 0; r < UP_ROWS; ++r) h[r0 + r] = gg[r] / (1.0f + canon_expf(-gg[r])) * u[r];
+    }
+    if (c.left[k].fetch_sub(1, std::memory_order_acq_rel) == 1) {
+        for (int j = g.first; j < g.first + g.n; ++j)
+            quant_q8k(c.h + (size_t)j * c.I, c.I, c.q8h + (size_t)j * (c.I / QK) * Q8K_BYTES);
+        c.ready[k].store(1, std::memory_order_release);
+    }
+}
+
+void gdown_item(const GChain &c, int item) {
+    const int per = c.H / DN_ROWS;
+    const int k = item / per, r0 = (item % per) * DN_ROWS;
+    const CpuGroup &g = c.g[k];
+    const size_t rb_in = (size_t)(c.H / QK) * Q4K_BYTES;
+    const size_t rb = (size_t)(c.I / QK) * (c.down_type == mp::TYPE_Q6K ? Q6K_BYTES : Q4K_BYTES);
+    const uint8_t *down = g.w + 2 * (size_t)c.I * rb_in;
+    while (!c.ready[k].load(std::memory_order_acquire)) _mm_pause();
+    for (int j = g.first; j < g.first + g.n; ++j)
+        dot_rows(c.down_type, down + r0 * rb, rb, DN_ROWS, c.q8h + (size_t)j * (c.I / QK) * Q8K_BYTES, c.I / QK,
+                 c.y[j] + r0);
+}
+
+void gchain_item(void *p, int item) {
+    GChain &c = *(GChain *)p;
+    if (item < c.n_up)
+        gup_item(c, item);
+    else
+        gdown_item(c, item - c.n_up);
+}
 }  // namespace
+
+void experts_grouped(Team *t, const CpuGroup *g, int n_groups, const uint8_t *const *q8x, float *const *y, int H,
+                     int I, int down_type, float *h_scratch, uint8_t *q8h_scratch) {
+    for (int b = 0; b < n_groups; b += 16) {  // at most 16 experts per pass
+        GChain c;
+        c.g = g + b; c.n = std::min(16, n_groups - b); c.H = H; c.I = I; c.down_type = down_type;
+        c.q8x = q8x; c.y = y; c.h = h_scratch; c.q8h = q8h_scratch;
+        c.n_up = c.n * (I / UP_ROWS);
+        for (int k = 0; k < c.n; ++k) {
+            c.left[k].store(I / UP_ROWS, std::memory_order_relaxed);
+            c.ready[k].store(0, std::memory_order_relaxed);
+        }
+        t->run(c.n_up + c.n * (H / DN_ROWS), gchain_item, &c);
+    }
+}
 
 // One team job per pass: up/gate of every expert, then down expert by expert;
 // a down item waits only for its own expert's h, so the down rows of the first

@@ -34,6 +34,18 @@ void team_hot(Team *t, bool on);
 void experts(Team *t, const CpuExpert *e, int n, int H, int I, int down_type, float *h_scratch,
              uint8_t *q8h_scratch);
 
+// The same chain for groups of tokens that share an expert: group g applies
+// expert g.w to tokens first .. first + n - 1 (q8x[j], y[j]), reading each
+// block of the expert's rows from memory once for all of them.  h_scratch
+// holds (total tokens) * I floats and q8h_scratch (total tokens) * (I/256) *
+// 292 bytes.  Results equal experts() token by token.
+struct CpuGroup {
+    const uint8_t *w;
+    int first, n;
+};
+void experts_grouped(Team *t, const CpuGroup *g, int n_groups, const uint8_t *const *q8x, float *const *y, int H,
+                     int I, int down_type, float *h_scratch, uint8_t *q8h_scratch);
+
 // Map every page of [p, p + n) into this process's page tables for reading
 // (memory another device filled has never been touched by the CPU: its first
 // reads would fault page by page, ~1 ms per expert, in the middle of a decode)

@@ -212,6 +212,7 @@ struct GroupedArgs {
     const float *hdx;           // [P][I/256]
     const uint16_t *hbs;        // [P][I/16]
     float *ypair;               // [P][H] weighted rows, pair (t*K + k) order
+    const uint8_t *host_mask;   // [E] or null: experts the host computes (their rows read as zeros)
 };
 
 hipError_t launch_dispatch(const int32_t *ids, int P, int E, int32_t *counts, int32_t *offsets, int32_t *perm,
@@ -221,6 +222,10 @@ hipError_t launch_quant_rows(const void *src, int bf16, int n_rows, int n, uint1
 hipError_t launch_gateup_grouped(const GroupedArgs &a, hipStream_t st, hipEvent_t e0, hipEvent_t e1);
 hipError_t launch_down_grouped(const GroupedArgs &a, hipStream_t st, hipEvent_t e0, hipEvent_t e1);
 hipError_t launch_combine(const float *ypair, int n_tok, int K, int H, float *out, int accumulate, hipStream_t st);
+// the same sum with the rows of pairs flagged in hflag [n_tok*K] taken from hrows [n_tok*K][H]
+// (the host's, in mapped memory) instead of ypair
+hipError_t launch_combine_host(const float *ypair, const float *hrows, const uint8_t *hflag, int n_tok, int K, int H,
+                               float *out, int accumulate, hipStream_t st);
 hipError_t launch_iota(int n, int32_t *offsets, int32_t *perm, float *ones, hipStream_t st);
 // the allocation-free grouped entry point's workspace: this device's address
 // of a static device array of STATIC_SCRATCH_BYTES

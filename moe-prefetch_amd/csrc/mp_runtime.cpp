@@ -252,6 +252,19 @@ struct moe_cache {
     float *b_w = nullptr;
     uint8_t *b_q8x = nullptr;
     void *b_route_ws = nullptr, *b_ws = nullptr;
+    // CPU-assisted batched decode: pinned copies of a layer's gate weights and
+    // Q8_K(x); mapped [2][...] (by layer parity) host-expert flags per expert
+    // and per pair, and the host's weighted rows
+    int bs_cap = 0;
+    int sb_num = 0, sb_den = 0;            // the host's share in batches (0/0: the batch-1 share)
+    float *bs_w = nullptr;
+    uint8_t *bs_q8 = nullptr;
+    uint8_t *bs_mask = nullptr, *bs_mask_d = nullptr;
+    uint8_t *bs_flag = nullptr, *bs_flag_d = nullptr;
+    float *bs_rows = nullptr, *bs_rows_d = nullptr;
+    hipEvent_t bs_ev = nullptr;
+    std::vector<float> bs_h, bs_y;
+    std::vector<uint8_t> bs_q8h;
     // router lookahead and just-in-time streaming
     Streamer *st = nullptr;
     std::vector<float> norm;                   // [layer][H] RMS-norm weights of the router inputs
@@ -1286,6 +1299,9 @@ void free_cache(moe_cache *c) {
                     (void *)c->b_w, (void *)c->b_q8x, c->b_route_ws, c->b_ws})
         hipFree(p);
     if (c->bh_ids) hipHostFree(c->bh_ids);
+    for (void *p : {(void *)c->bs_w, (void *)c->bs_q8, (void *)c->bs_mask, (void *)c->bs_flag, (void *)c->bs_rows})
+        if (p) hipHostFree(p);
+    if (c->bs_ev) hipEventDestroy(c->bs_ev);
     hipFree(c->d_tbl);
     hipFree(c->d_prior);
     hipFree(c->route_ws);
@@ -1505,6 +1521,39 @@ int moe_cpu_experts(const void *const *experts, int n, const uint8_t *q8x, int H
     mpc::set_portable(portable != 0);
     mpc::experts(t, e.data(), n, H, I, down_type, h.data(), q8h.data());
     mpc::set_portable(false);
+    return MOE_OK;
+}
+
+int moe_cpu_experts_tokens(const void *const *experts, int n_groups, const int32_t *count, const uint8_t *q8x,
+                           int H, int I, int down_type, float *rows, int n_threads) {
+    if (!experts || !count || !q8x || !rows || n_groups < 0) return fail(MOE_ERR_ARG, "moe_cpu_experts_tokens: bad arguments");
+    int r = check_shape(64, H, I, 1);
+    if (r != MOE_OK) return r;
+    if (I == 0) return fail(MOE_ERR_ARG, "intermediate size 0");
+    if (down_type != MOE_TYPE_Q4K && down_type != MOE_TYPE_Q6K)
+        return fail(MOE_ERR_ARG, "down type %d unsupported", down_type);
+    std::vector<mpc::CpuGroup> g((size_t)n_groups);
+    int n = 0;
+    for (int k = 0; k < n_groups; ++k) {
+        if (!experts[k] || count[k] < 1) return fail(MOE_ERR_ARG, "moe_cpu_experts_tokens: group %d is empty", k);
+        g[(size_t)k] = {(const uint8_t *)experts[k], n, count[k]};
+        n += count[k];
+    }
+    const size_t q8row = (size_t)(H / 256) * mp::Q8K_BYTES;
+    std::vector<const uint8_t *> q8p((size_t)n);
+    std::vector<float *> yp((size_t)n);
+    for (int j = 0; j < n; ++j) {
+        q8p[(size_t)j] = q8x + (size_t)j * q8row;
+        yp[(size_t)j] = rows + (size_t)j * H;
+    }
+    std::vector<float> h((size_t)n * I);
+    std::vector<uint8_t> q8h((size_t)n * (I / 256) * mp::Q8K_BYTES);
+    static std::mutex m;
+    static std::map<int, mpc::Team *> teams;
+    std::lock_guard<std::mutex> lk(m);
+    mpc::Team *&t = teams[n_threads < 1 ? 1 : n_threads];
+    if (!t) t = mpc::team_create(n_threads < 1 ? 1 : n_threads);
+    mpc::experts_grouped(t, g.data(), n_groups, q8p.data(), yp.data(), H, I, down_type, h.data(), q8h.data());
     return MOE_OK;
 }
 
@@ -2453,6 +2502,18 @@ static int sidecar_serve(moe_cache *c, int l, uint32_t seq, bool by_logits) {
     return MOE_OK;
 }
 
+int moe_cache_set_sidecar_batch(moe_cache *c, int num, int den) {
+    if (!c) return fail(MOE_ERR_ARG, "null cache");
+    if (num == 0 && den == 0) {
+        c->sb_num = c->sb_den = 0;
+        return MOE_OK;
+    }
+    if (den < 1 || num < 0 || num > den) return fail(MOE_ERR_ARG, "share %d/%d: need 0 <= num <= den, den >= 1", num, den);
+    c->sb_num = num;
+    c->sb_den = den;
+    return MOE_OK;
+}
+
 int moe_cache_sidecar_log(moe_cache *c, float *out, int max_rows) {
     if (!c) return -1;
     const int rows = (int)std::min<size_t>(c->sc_log.size() / 3, (size_t)std::max(0, max_rows));
@@ -2930,8 +2991,15 @@ static int grouped_check(const moe_grouped_desc *d) {
     return MOE_OK;
 }
 
-// the grouped expert chain over a checked descriptor, with ws as its workspace
-static int grouped_run(const moe_grouped_desc *d, uint8_t *ws, hipStream_t st) {
+// the grouped expert chain over a checked descriptor, with ws as its workspace.
+// CPU-assisted batched decode runs it in two parts: the expert products with
+// the host's experts masked out (host_mask, device view of [E] flags), then,
+// once the host's rows are written, the combine taking flagged pairs' rows
+// from hrows (hflag [P]) and the shared expert.
+constexpr int GR_EXPERTS = 1, GR_COMBINE = 2;
+static int grouped_run(const moe_grouped_desc *d, uint8_t *ws, hipStream_t st, int parts = GR_EXPERTS | GR_COMBINE,
+                       const uint8_t *host_mask = nullptr, const float *hrows = nullptr,
+                       const uint8_t *hflag = nullptr) {
     const GroupedWs w = grouped_ws(d->n_tok, d->K, d->H, d->I);
     mp::GroupedArgs a{};
     a.offsets = d->offsets; a.perm = d->perm; a.w = d->w;
@@ -2942,6 +3010,7 @@ static int grouped_run(const moe_grouped_desc *d, uint8_t *ws, hipStream_t st) {
     a.y2 = (float *)(ws + w.h);
     a.ha = (const uint16_t *)(ws + w.ha); a.hdx = (const float *)(ws + w.hdx); a.hbs = (const uint16_t *)(ws + w.hbs);
     a.ypair = d->pair_out ? d->pair_out : (float *)(ws + w.ypair);
+    a.host_mask = host_mask;
     const int P = d->n_tok * d->K;
     a.P = P;
     hipEvent_t ev[4] = {};
@@ -2949,16 +3018,23 @@ static int grouped_run(const moe_grouped_desc *d, uint8_t *ws, hipStream_t st) {
     if (timed)
         for (auto &e : ev) HIPCHK(hipEventCreate(&e));
     auto run = [&]() -> int {
-        HIPCHK(mp::launch_quant_rows(d->x, d->x_type == MOE_DTYPE_BF16, d->n_tok, d->H, (uint16_t *)a.xa,
-                                     (float *)a.xdx, (uint16_t *)a.xbs, st));
-        HIPCHK(mp::launch_gateup_grouped(a, st, ev[0], ev[1]));
-        HIPCHK(mp::launch_swiglu_quant(a.y2, P, d->I, d->h_out, (uint16_t *)a.ha, (float *)a.hdx, (uint16_t *)a.hbs,
-                                       st));
-        HIPCHK(mp::launch_down_grouped(a, st, ev[2], ev[3]));
-        HIPCHK(mp::launch_combine(a.ypair, d->n_tok, d->K, d->H, d->out, d->accumulate, st));
+        if (parts & GR_EXPERTS) {
+            HIPCHK(mp::launch_quant_rows(d->x, d->x_type == MOE_DTYPE_BF16, d->n_tok, d->H, (uint16_t *)a.xa,
+                                         (float *)a.xdx, (uint16_t *)a.xbs, st));
+            HIPCHK(mp::launch_gateup_grouped(a, st, ev[0], ev[1]));
+            HIPCHK(mp::launch_swiglu_quant(a.y2, P, d->I, d->h_out, (uint16_t *)a.ha, (float *)a.hdx,
+                                           (uint16_t *)a.hbs, st));
+            HIPCHK(mp::launch_down_grouped(a, st, ev[2], ev[3]));
+        }
+        if (!(parts & GR_COMBINE)) return MOE_OK;
+        if (hflag)
+            HIPCHK(mp::launch_combine_host(a.ypair, hrows, hflag, d->n_tok, d->K, d->H, d->out, d->accumulate, st));
+        else
+            HIPCHK(mp::launch_combine(a.ypair, d->n_tok, d->K, d->H, d->out, d->accumulate, st));
         if (d->shared) {
             // the shared expert as a one-expert dispatch of every token, added after the routed sum
             mp::GroupedArgs sa = a;
+            sa.host_mask = nullptr;
             sa.offsets = (const int32_t *)(ws + w.sh_offs);
             sa.perm = (const int32_t *)(ws + w.sh_perm);
             sa.w = (const float *)(ws + w.sh_ones);
@@ -2975,7 +3051,7 @@ static int grouped_run(const moe_grouped_desc *d, uint8_t *ws, hipStream_t st) {
     };
     int rc = run();
     if (timed) {
-        if (rc == MOE_OK && hipEventSynchronize(ev[3]) == hipSuccess) {
+        if (rc == MOE_OK && (parts & GR_EXPERTS) && hipEventSynchronize(ev[3]) == hipSuccess) {
             float ms = 0.0f;
             hipEventElapsedTime(&ms, ev[0], ev[1]);
             d->kernel_ms[0] = ms;
@@ -3035,6 +3111,111 @@ static int batch_buffers(moe_cache *c, int n_tok) {
     return MOE_OK;
 }
 
+// exchange buffers of CPU-assisted batched decode for up to n_tok tokens
+static int batch_sidecar_buffers(moe_cache *c, int n_tok) {
+    if (n_tok <= c->bs_cap) return MOE_OK;
+    for (void *p : {(void *)c->bs_w, (void *)c->bs_q8, (void *)c->bs_mask, (void *)c->bs_flag, (void *)c->bs_rows})
+        if (p) hipHostFree(p);
+    c->bs_w = nullptr;
+    c->bs_q8 = c->bs_mask = c->bs_flag = nullptr;
+    c->bs_rows = nullptr;
+    c->bs_cap = 0;
+    const size_t TK = (size_t)n_tok * c->K;
+    const unsigned fl = hipHostMallocMapped | hipHostMallocCoherent;
+    bool ok = hipHostMalloc((void **)&c->bs_w, TK * 4, hipHostMallocDefault) == hipSuccess &&
+              hipHostMalloc((void **)&c->bs_q8, (size_t)n_tok * (c->H / 256) * mp::Q8K_BYTES, hipHostMallocDefault) ==
+                  hipSuccess &&
+              hipHostMalloc((void **)&c->bs_mask, 2 * (size_t)c->E, fl) == hipSuccess &&
+              hipHostMalloc((void **)&c->bs_flag, 2 * TK, fl) == hipSuccess &&
+              hipHostMalloc((void **)&c->bs_rows, 2 * TK * c->H * 4, fl) == hipSuccess;
+    if (!ok) return fail(MOE_ERR_NOMEM, "CPU-assisted batch buffers for %d tokens", n_tok);
+    HIPCHK(hipHostGetDevicePointer((void **)&c->bs_mask_d, c->bs_mask, 0));
+    HIPCHK(hipHostGetDevicePointer((void **)&c->bs_flag_d, c->bs_flag, 0));
+    HIPCHK(hipHostGetDevicePointer((void **)&c->bs_rows_d, c->bs_rows, 0));
+    if (!c->bs_ev) HIPCHK(hipEventCreateWithFlags(&c->bs_ev, hipEventDisableTiming));
+    c->bs_cap = n_tok;
+    return MOE_OK;
+}
+
+// CPU-assisted serving of one layer of a batch, after its routing was copied
+// back: the host takes the absent experts whose rank r among the layer's
+// absent experts (ascending id) has r % den < num, masks them out of the
+// grouped products it then enqueues, computes their pairs from the pinned
+// store while the GPU runs the rest, and writes each pair's weighted row
+// (w * y, the kernels' one multiplication) for the combine.
+static int batch_sidecar_layer(moe_cache *c, int l, int n_tok, const moe_grouped_desc *gd, hipStream_t st) {
+    const Layer &ls = c->L[l];
+    const int TK = n_tok * c->K, par = l & 1;
+    const auto t0 = std::chrono::steady_clock::now();
+    HIPCHK(hipEventSynchronize(c->bs_ev));
+    const auto t1 = std::chrono::steady_clock::now();
+    c->sc_wait_us += std::chrono::duration<double, std::micro>(t1 - t0).count();
+    uint8_t *mask = c->bs_mask + (size_t)par * c->E, *flag = c->bs_flag + (size_t)par * TK;
+    float *rows = c->bs_rows + (size_t)par * TK * c->H;
+    const int32_t *ids = c->bh_ids + (size_t)l * TK;
+    std::vector<uint8_t> absent((size_t)c->E, 0);
+    for (int i = 0; i < TK; ++i) {
+        const int id = ids[i];
+        if (id < 0 || id >= ls.E) continue;
+        const int slot = c->h_tbl[(size_t)l * c->E + id];
+        if (!(slot >= 0 && slot < ls.S)) absent[id] = 1;
+    }
+    const int num = c->sb_den ? c->sb_num : c->sc_num, den = c->sb_den ? c->sb_den : c->sc_den;
+    for (int e = 0, r = 0; e < c->E; ++e) {
+        mask[e] = absent[e] && r % den < num;
+        r += absent[e];
+    }
+    // the host's pairs grouped by expert (ascending id, pairs in order): each
+    // expert's rows are read from memory once for all of its tokens
+    std::vector<int> first((size_t)c->E + 1, 0);
+    for (int i = 0; i < TK; ++i) {
+        const int id = ids[i];
+        flag[i] = id >= 0 && id < ls.E && mask[id];
+        if (flag[i]) ++first[(size_t)id + 1];
+    }
+    for (int e = 0; e < c->E; ++e) first[(size_t)e + 1] += first[e];
+    const int n = first[c->E];
+    std::vector<int> pair((size_t)n), fill(first.begin(), first.end() - 1);
+    for (int i = 0; i < TK; ++i)
+        if (flag[i]) pair[(size_t)fill[ids[i]]++] = i;
+    std::vector<mpc::CpuGroup> grp;
+    for (int e = 0; e < c->E; ++e)
+        if (first[(size_t)e + 1] > first[e])
+            grp.push_back({ls.store_host + (size_t)e * ls.expert_bytes, first[e], first[(size_t)e + 1] - first[e]});
+    const size_t q8row = (size_t)(c->H / 256) * mp::Q8K_BYTES;
+    if (c->bs_y.size() < (size_t)TK * c->H) {
+        c->bs_y.resize((size_t)TK * c->H);
+        c->bs_h.resize((size_t)TK * c->I);
+        c->bs_q8h.resize((size_t)TK * (c->I / 256) * mp::Q8K_BYTES);
+    }
+    std::vector<const uint8_t *> q8p((size_t)n);
+    std::vector<float *> yp((size_t)n);
+    for (int j = 0; j < n; ++j) {
+        q8p[(size_t)j] = c->bs_q8 + (size_t)(pair[(size_t)j] / c->K) * q8row;
+        yp[(size_t)j] = c->bs_y.data() + (size_t)j * c->H;
+    }
+    std::atomic_thread_fence(std::memory_order_release);
+    int r = grouped_run(gd, (uint8_t *)c->b_ws, st, GR_EXPERTS, c->bs_mask_d + (size_t)par * c->E);
+    if (r != MOE_OK) return r;
+    if (n) {
+        c->sc_computing.store(l, std::memory_order_relaxed);
+        mpc::experts_grouped(c->team, grp.data(), (int)grp.size(), q8p.data(), yp.data(), c->H, c->I, ls.down_type,
+                             c->bs_h.data(), c->bs_q8h.data());
+        c->sc_computing.store(-1, std::memory_order_relaxed);
+        for (int j = 0; j < n; ++j) {
+            const float w = c->bs_w[pair[j]];
+            const float *y = c->bs_y.data() + (size_t)j * c->H;
+            float *o = rows + (size_t)pair[j] * c->H;
+            for (int h = 0; h < c->H; ++h) o[h] = w * y[h];
+        }
+    }
+    c->n_cpu_served += n;
+    c->sc_cpu_us += std::chrono::duration<double, std::micro>(std::chrono::steady_clock::now() - t1).count();
+    std::atomic_thread_fence(std::memory_order_release);
+    return grouped_run(gd, (uint8_t *)c->b_ws, st, GR_COMBINE, nullptr, c->bs_rows_d + (size_t)par * TK * c->H,
+                       c->bs_flag_d + (size_t)par * TK);
+}
+
 int moe_decode_batch(moe_cache *c, const float *x, const float *bias, float *out, int n_tok, int32_t *ids_host,
                      void *stream) {
     if (!c || !x || !out) return fail(MOE_ERR_ARG, "bad arguments");
@@ -3046,6 +3227,14 @@ int moe_decode_batch(moe_cache *c, const float *x, const float *bias, float *out
     if (r != MOE_OK) return r;
     const hipStream_t st = (hipStream_t)stream;
     const int NL = (int)c->L.size(), TK = n_tok * c->K;
+    const bool sc = c->sc_den > 0;
+    if (sc && (r = batch_sidecar_buffers(c, n_tok)) != MOE_OK) return r;
+    if (sc) mpc::team_hot(c->team, true);
+    struct Cold {
+        moe_cache *c;
+        bool on;
+        ~Cold() { if (on) mpc::team_hot(c->team, false); }
+    } cold{c, sc};
     // (the last step published only finished copies: its tables are safe to read)
     for (int l = 0; l < NL; ++l) {
         const Layer &ls = c->L[l];
@@ -3062,6 +3251,13 @@ int moe_decode_batch(moe_cache *c, const float *x, const float *bias, float *out
         rd.ids = c->b_ids + (size_t)l * TK; rd.w = c->b_w; rd.slots = c->b_slots; rd.q8x = c->b_q8x;
         rd.workspace = c->b_route_ws;
         if ((r = run_route(&rd, st)) != MOE_OK) return r;
+        if (sc) {                       // the routing back to the host for its share
+            HIPCHK(hipMemcpyAsync(c->bh_ids + (size_t)l * TK, rd.ids, (size_t)TK * 4, hipMemcpyDeviceToHost, st));
+            HIPCHK(hipMemcpyAsync(c->bs_w, c->b_w, (size_t)TK * 4, hipMemcpyDeviceToHost, st));
+            HIPCHK(hipMemcpyAsync(c->bs_q8, c->b_q8x, (size_t)n_tok * (c->H / 256) * mp::Q8K_BYTES,
+                                  hipMemcpyDeviceToHost, st));
+            HIPCHK(hipEventRecord(c->bs_ev, st));
+        }
         HIPCHK(mp::launch_dispatch(rd.ids, TK, c->E, c->b_counts, c->b_offs, c->b_perm, st));
         moe_grouped_desc gd{};
         gd.offsets = c->b_offs; gd.perm = c->b_perm; gd.w = c->b_w;
@@ -3072,7 +3268,13 @@ int moe_decode_batch(moe_cache *c, const float *x, const float *bias, float *out
         gd.store = ls.store_dev; gd.expert_bytes = ls.expert_bytes; gd.n_store = c->E;
         gd.out = out + (size_t)l * n_tok * c->H; gd.accumulate = 0;
         gd.workspace = c->b_ws; gd.shared = ls.shared;
-        if ((r = moe_grouped_experts(&gd, stream)) != MOE_OK) return r;
+        if (!sc) {
+            if ((r = moe_grouped_experts(&gd, stream)) != MOE_OK) return r;
+        } else {
+            if ((r = grouped_check(&gd)) != MOE_OK) return r;
+            if (!ls.store_host) return fail(MOE_ERR_STATE, "layer %d: CPU-assisted serving needs the host store", l);
+            if ((r = batch_sidecar_layer(c, l, n_tok, &gd, st)) != MOE_OK) return r;
+        }
     }
     HIPCHK(hipMemcpyAsync(c->bh_ids, c->b_ids, (size_t)NL * TK * 4, hipMemcpyDeviceToHost, st));
     HIPCHK(hipStreamSynchronize(st));

@@ -144,6 +144,8 @@ SIGNATURES = {
     "moe_expert_bytes": (SZ, [ctypes.c_int, ctypes.c_int, ctypes.c_int]),
     "moe_route_workspace_bytes": (SZ, [ctypes.c_int, ctypes.c_int]),
     "moe_experts_workspace_bytes": (SZ, [ctypes.c_int, ctypes.c_int]),
+    "moe_cpu_experts_tokens": (ctypes.c_int, [P, ctypes.c_int, P, P, ctypes.c_int, ctypes.c_int, ctypes.c_int, P,
+                                               ctypes.c_int]),
     "moe_cpu_experts": (ctypes.c_int, [P, ctypes.c_int, P, ctypes.c_int, ctypes.c_int, ctypes.c_int, P,
                                        ctypes.c_int, ctypes.c_int]),
     "moe_cpu_has_vnni": (ctypes.c_int, []),
@@ -167,6 +169,7 @@ SIGNATURES = {
     "moe_cache_set_decode_path": (ctypes.c_int, [P, ctypes.c_int, ctypes.c_int]),
     "moe_cache_set_staging": (ctypes.c_int, [P, ctypes.c_int]),
     "moe_cache_set_sidecar": (ctypes.c_int, [P, ctypes.c_int, ctypes.c_int, ctypes.c_int]),
+    "moe_cache_set_sidecar_batch": (ctypes.c_int, [P, ctypes.c_int, ctypes.c_int]),
     "moe_cache_sidecar_log": (ctypes.c_int, [P, P, ctypes.c_int]),
     "moe_cache_heat_file": (ctypes.c_int, [P, ctypes.c_char_p, ctypes.POINTER(ctypes.c_int64),
                                            ctypes.POINTER(ctypes.c_int64)]),

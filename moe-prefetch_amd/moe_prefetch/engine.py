@@ -231,6 +231,12 @@ class MoeCache:
         num, den = share
         check(lib().moe_cache_set_sidecar(self.h, int(n_threads), int(num), int(den)), "set_sidecar")
 
+    def set_sidecar_batch(self, share=None):
+        """The host's share (num, den) of the absent experts in decode_batch
+        (None: the share given to set_sidecar)."""
+        num, den = share if share else (0, 0)
+        check(lib().moe_cache_set_sidecar_batch(self.h, int(num), int(den)), "set_sidecar_batch")
+
     def heat_file(self, path):
         """LLAMA_MOE_HEAT_FILE: count observations, save every 512 steps, and
         warm-start from `path` if it holds this cache's dimensions.  Returns

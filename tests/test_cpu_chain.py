@@ -93,3 +93,30 @@ def test_cpu_chain_rejects_bad_shapes():
                                rows.ctypes.data, 1, 0) != 0
     assert L().moe_cpu_experts(ctypes.cast(ptrs, ctypes.c_void_p), 1, q8x.ctypes.data, H, 512, 13,
                                rows.ctypes.data, 1, 0) != 0
+
+
+@pytest.mark.parametrize("dt", [Q4, Q6], ids=["q4k_down", "q6k_down"])
+def test_grouped_tokens_chain_matches_oracle(dt):
+    """Groups of tokens sharing an expert (CPU-assisted batched decode): each
+    group's rows are read once for all of its tokens; every token's rows equal
+    the oracle's chain for that expert and token, bit for bit."""
+    I = 512
+    buf, eb = synth(5, I, dt, seed=31 + dt)
+    groups = [(3, 4), (0, 1), (4, 3), (1, 2), (2, 1)]       # (expert, tokens)
+    n = sum(c for _, c in groups)
+    rng = np.random.default_rng(17)
+    xs = rng.standard_normal((n, H)).astype(np.float32)
+    xs[2] *= 40.0                                          # a wide token among them
+    q8 = np.stack([O.quant_q8k(x) for x in xs])
+    ptrs = (ctypes.c_void_p * len(groups))(*[buf.ctypes.data + e * eb for e, _ in groups])
+    count = np.asarray([c for _, c in groups], np.int32)
+    for threads in (1, 5):
+        rows = np.full((n, H), np.nan, np.float32)
+        _lib.check(L().moe_cpu_experts_tokens(ctypes.cast(ptrs, ctypes.c_void_p), len(groups), count.ctypes.data,
+                                              q8.ctypes.data, H, I, dt, rows.ctypes.data, threads), "tokens")
+        j = 0
+        for e, c in groups:
+            for _ in range(c):
+                want = O.expert_chain(H, I, dt, buf[e * eb:(e + 1) * eb], xs[j])[0]
+                assert np.array_equal(rows[j], want), (threads, e, j)
+                j += 1

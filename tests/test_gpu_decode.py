@@ -114,13 +114,17 @@ def test_decode_256_experts_shared_expert(tmp_path):
         rig.close()
 
 
-@pytest.mark.parametrize("shape", ["e256_shared_i512", "e128_i768", "e128_unsteered_prior"])
+@pytest.mark.parametrize("shape", ["e256_shared_i512", "e128_i768", "e128_unsteered_prior", "e256_shared_i512_cpu",
+                                   "e128_i768_cpu_2of3"])
 def test_decode_batch_matches_oracle(shape):
     # moe_decode_batch: batches of 16 tokens through every layer (route -- the
     # cache prior biases single-token selection only, so it is off here --,
     # dispatch, grouped experts from slots or the pinned store, the shared
     # expert), observed token-major and stepped: ids, frames and counters equal
-    # to the oracle's, outputs bit for bit
+    # to the oracle's, outputs bit for bit.  *_cpu: CPU-assisted serving, the
+    # host computing the pairs of (a share of) the absent experts
+    share = {"e256_shared_i512_cpu": (1, 1), "e128_i768_cpu_2of3": (2, 3)}.get(shape)
+    shape = shape.replace("_cpu_2of3", "").replace("_cpu", "")
     if shape == "e256_shared_i512":
         rig = Rig([48, 32], [Q4, Q6], T=64, I=512, E=256, shared=True, zipf_s=1.0, reuse=0.5, admit="window",
                   batch_tables=True, cache_prior=0.01)
@@ -130,6 +134,8 @@ def test_decode_batch_matches_oracle(shape):
         rig = Rig([24, 24], [Q4, Q6], T=64, steer=False, admit="window", batch_tables=True, cache_prior=0.01)
     nb, B = 4, 16
     oc = rig.oracle_cache()
+    if share:
+        rig.cache.set_sidecar(4, share)
     try:
         out = torch.empty((rig.nl, B, 2048), dtype=torch.float32, device=rig.dev)
         for b in range(nb):
@@ -156,6 +162,8 @@ def test_decode_batch_matches_oracle(shape):
         st, ost = rig.cache.stats(), oc.stats()
         for k in ("n_hit", "n_miss", "n_scheduled", "n_published", "n_admit_ok", "n_admit_denied"):
             assert st[k] == ost[k], (k, st[k], ost[k])
+        if share:
+            assert st["n_cpu_served"] > 0                      # the host computed pairs
     finally:
         oc.close()
         rig.close()
