@@ -1309,13 +1309,11 @@ void free_cache(moe_cache *c) {
     hipFree(c->ypart);
     hipFree(c->d_ids);
     hipFree(c->fx);
-    hipFree(c->d_slots);
     hipFree(c->d_w);
     hipFree(c->d_q8x);
     if (c->h_tbl) hipHostFree(c->h_tbl);
     if (c->h_prior) hipHostFree(c->h_prior);
     if (c->h_ids) hipHostFree(c->h_ids);
-    if (c->h_slots) hipHostFree(c->h_slots);
     if (c->route) fclose(c->route);
     if (c->map) fclose(c->map);
     if (c->replay) fclose(c->replay);
@@ -1664,16 +1662,17 @@ int moe_cache_create(const moe_cache_config *cfg, moe_cache **out) {
     const size_t rws = route_ws_bytes(E, 1), ews = exp_ws_bytes(c->I, c->K);
     if (hipMalloc(&c->route_ws, rws) != hipSuccess || hipMalloc(&c->exp_ws, ews) != hipSuccess ||
         hipMalloc(&c->ypart, ((size_t)c->K + 1) * c->H * 4) != hipSuccess ||
-        hipMalloc(&c->d_ids, ((size_t)NL * c->K + 64) * 4) != hipSuccess ||
-        hipMalloc(&c->d_slots, (size_t)NL * c->K * 4) != hipSuccess ||
+        hipMalloc(&c->d_ids, (2 * (size_t)NL * c->K + 64) * 4) != hipSuccess ||
         hipMalloc(&c->d_w, (size_t)NL * c->K * 4) != hipSuccess ||
         hipMalloc(&c->d_q8x, (size_t)(c->H / 256) * mp::Q8K_BYTES + 256) != hipSuccess ||
-        hipHostMalloc(&c->h_ids, ((size_t)NL * c->K + 64) * 4, 0) != hipSuccess ||
-        hipHostMalloc(&c->h_slots, (size_t)NL * c->K * 4, 0) != hipSuccess ||
+        hipHostMalloc(&c->h_ids, (2 * (size_t)NL * c->K + 64) * 4, 0) != hipSuccess ||
         hipMalloc(&c->fx, (size_t)NL * mp::fused_words(c->K, c->I, c->H) * 8) != hipSuccess ||
         hipHostMalloc((void **)&c->h_seq, 64, hipHostMallocDefault) != hipSuccess ||
         hipMalloc(&c->d_seq, 64) != hipSuccess)
         return bail(fail(MOE_ERR_NOMEM, "decode scratch"));
+    // ids [L][K], the late-wait word and padding, then slots [L][K]: one copy back per token
+    c->d_slots = c->d_ids + (size_t)NL * c->K + 64;
+    c->h_slots = c->h_ids + (size_t)NL * c->K + 64;
     // tag 0 is never a token's sequence number: zeroed exchange words are stale
     if (hipMemset(c->route_ws, 0, rws) != hipSuccess || hipMemset(c->exp_ws, 0, ews) != hipSuccess ||
         hipMemset(c->fx, 0, (size_t)NL * mp::fused_words(c->K, c->I, c->H) * 8) != hipSuccess ||
@@ -2834,8 +2833,7 @@ int moe_decode_token(moe_cache *c, const float *x, const float *bias, float *out
         if (serve_err != MOE_OK) abort_joins();
     }
     // the routed ids and, after them, the fused layers' late-wait word
-    HIPCHK(hipMemcpyAsync(c->h_ids, c->d_ids, ((size_t)NL * c->K + 1) * 4, hipMemcpyDeviceToHost, st));
-    HIPCHK(hipMemcpyAsync(c->h_slots, c->d_slots, (size_t)NL * c->K * 4, hipMemcpyDeviceToHost, st));
+    HIPCHK(hipMemcpyAsync(c->h_ids, c->d_ids, (2 * (size_t)NL * c->K + 64) * 4, hipMemcpyDeviceToHost, st));
     const hipError_t sync_err = hipStreamSynchronize(st);
     const auto t_sync = std::chrono::steady_clock::now();
     const int drain_err = mover_drain();
