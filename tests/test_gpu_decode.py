@@ -115,7 +115,7 @@ def test_decode_256_experts_shared_expert(tmp_path):
 
 
 @pytest.mark.parametrize("shape", ["e256_shared_i512", "e128_i768", "e128_unsteered_prior", "e256_shared_i512_cpu",
-                                   "e128_i768_cpu_2of3"])
+                                   "e128_i768_cpu_2of3", "e128_i768_cpu_1of2_b5", "e128_i768_cpu_0of1"])
 def test_decode_batch_matches_oracle(shape):
     # moe_decode_batch: batches of 16 tokens through every layer (route -- the
     # cache prior biases single-token selection only, so it is off here --,
@@ -123,8 +123,11 @@ def test_decode_batch_matches_oracle(shape):
     # expert), observed token-major and stepped: ids, frames and counters equal
     # to the oracle's, outputs bit for bit.  *_cpu: CPU-assisted serving, the
     # host computing the pairs of (a share of) the absent experts
-    share = {"e256_shared_i512_cpu": (1, 1), "e128_i768_cpu_2of3": (2, 3)}.get(shape)
-    shape = shape.replace("_cpu_2of3", "").replace("_cpu", "")
+    # (b5: batches of 5 tokens; 0of1: CPU-assisted serving on, the host's share empty)
+    share = {"e256_shared_i512_cpu": (1, 1), "e128_i768_cpu_2of3": (2, 3), "e128_i768_cpu_1of2_b5": (1, 2),
+             "e128_i768_cpu_0of1": (0, 1)}.get(shape)
+    B = 5 if shape.endswith("_b5") else 16
+    shape = shape.split("_cpu")[0]
     if shape == "e256_shared_i512":
         rig = Rig([48, 32], [Q4, Q6], T=64, I=512, E=256, shared=True, zipf_s=1.0, reuse=0.5, admit="window",
                   batch_tables=True, cache_prior=0.01)
@@ -132,7 +135,7 @@ def test_decode_batch_matches_oracle(shape):
         rig = Rig([20, 28], [Q6, Q4], T=64, I=768, admit="window", batch_tables=True)
     else:   # W x alone: a 0.01 prior on probabilities near 1/128 would change the ids
         rig = Rig([24, 24], [Q4, Q6], T=64, steer=False, admit="window", batch_tables=True, cache_prior=0.01)
-    nb, B = 4, 16
+    nb = 4
     oc = rig.oracle_cache()
     if share:
         rig.cache.set_sidecar(4, share)
@@ -163,7 +166,7 @@ def test_decode_batch_matches_oracle(shape):
         for k in ("n_hit", "n_miss", "n_scheduled", "n_published", "n_admit_ok", "n_admit_denied"):
             assert st[k] == ost[k], (k, st[k], ost[k])
         if share:
-            assert st["n_cpu_served"] > 0                      # the host computed pairs
+            assert (st["n_cpu_served"] > 0) == (share[0] > 0)   # the host computed pairs (none at 0/1)
     finally:
         oc.close()
         rig.close()
