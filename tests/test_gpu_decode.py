@@ -232,15 +232,22 @@ def test_staged_uploads_fill_slots(knobs):
         assert on[3][k] == off[3][k], k
 
 
-@pytest.mark.parametrize("case", ["all-graph", "two-thirds-graph", "all-eager", "e256-shared"])
+@pytest.mark.parametrize("case", ["all-graph", "two-thirds-graph", "all-eager", "e256-shared", "e64-prior",
+                                  "e192-prior"])
 def test_sidecar_decode_matches_oracle(tmp_path, case):
-    # CPU-assisted serving: the router kernel posts ids and Q8_K(x) to mapped
-    # host memory, the host computes the absent experts assigned to it, the
-    # join kernel combines in k order -- ids, frames, traces and outputs bit
-    # for bit as the oracle's
+    # CPU-assisted serving: the fused launch posts each logit and Q8_K(x) to
+    # mapped host memory, the host routes the token from them and computes the
+    # absent experts assigned to it, the join kernel combines in k order --
+    # ids, frames, traces and outputs bit for bit as the oracle's.  e64 / e192:
+    # one and three 64-expert chunks in the host's routing, with the cache
+    # prior on the probabilities
     if case == "e256-shared":
         rig = Rig([40, 24], [Q4, Q6], T=32, I=512, E=256, shared=True, zipf_s=1.0, reuse=0.5, admit="window",
                   batch_tables=True, cache_prior=0.01)
+    elif case == "e64-prior":
+        rig = Rig([16, 24], [Q4, Q6], T=32, I=256, E=64, admit="window", batch_tables=True, cache_prior=0.01)
+    elif case == "e192-prior":
+        rig = Rig([24, 40], [Q6, Q4], T=32, I=512, E=192, admit="window", batch_tables=True, cache_prior=0.01)
     else:
         rig = Rig([16, 24, 12, 40], [Q4, Q6, Q4, Q6], T=40, admit="window", batch_tables=True)
     share = (2, 3) if case == "two-thirds-graph" else (1, 1)
