@@ -1180,8 +1180,8 @@ def parse_args(argv=None):
 def main():
     args = parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
-        print("bench.py measures one GPU: this path has no multi-GPU mode in this build "
-              "(the expert-sharded design is described in DESIGN.md); run with --gpus 1", file=sys.stderr)
+        print("bench.py measures one GPU: this path has no multi-GPU mode (the expert-sharded "
+              "design is documented, not built); run with --gpus 1", file=sys.stderr)
         sys.exit(2)
     wide = args.workload == "wide40"
     import torch

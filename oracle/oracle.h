@@ -3,8 +3,8 @@
  *
  * TEST INFRASTRUCTURE ONLY.  Nothing in the product links, loads or calls this
  * code.  Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg
- * use it, and only as the checker (or, for the CPU baseline, as the thing timed
- * beside the GPU).
+ * use it, and only to check the product's results (or, for the CPU baseline, as
+ * the thing timed beside the GPU).
  *
  * What each part restates, and what pins it:
  *
@@ -42,8 +42,8 @@
  *       requiring every placement frame of {0..3}.map.txt.
  *   _ref/libref_predictor.so (ref_predictor_shim.cpp + the reference's own
  *       cpp/moe-predictor.cpp, built from where it lies by `make ref`)
- *       the MOEP predictor itself, not restated: the checker of the product's
- *       moe_predictor_* (tests/test_moep.py, tests/golden/make_moep_golden.py).
+ *       the MOEP predictor itself, not restated: what the product's
+ *       moe_predictor_* is compared with (tests/test_moep.py, tests/golden/make_moep_golden.py).
  *   or_ahead, or_planner_*
  *       router lookahead (k_moe_ahead_scores/post, patches/0010-team-and-streaming.patch:382-474)
  *       and the just-in-time copy planner (moe_planner, 0010:777-909).  or_ahead is

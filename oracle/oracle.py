@@ -1,8 +1,8 @@
 """ctypes view of liboracle.so -- the CPU restatement of the MoE decode path.
 
 TEST INFRASTRUCTURE ONLY.  Imported by tests/, __graft_entry__.smoke() and the
-cpu_baseline leg of bench.py, always as the checker (or the CPU baseline timed
-beside the GPU), never as a product path.  See oracle.h for what each function
+cpu_baseline leg of bench.py, always to check the product's results (or as the
+CPU baseline timed beside the GPU), never as a product path.  See oracle.h for what each function
 restates and what pins it.
 """
 import ctypes

@@ -1,7 +1,7 @@
 // ref_predictor_shim.cpp -- a C entry point onto the reference's own MOEP
 // predictor (cpp/moe-predictor.cpp, compiled from where it lies by the Makefile
 // in this directory into _ref/, only where the reference tree is present).
-// TEST INFRASTRUCTURE ONLY: the checker of moe_predictor_* in the product.
+// TEST INFRASTRUCTURE ONLY: what the tests compare moe_predictor_* in the product with.
 #include "moe-predictor.h"
 
 #include <cstdint>

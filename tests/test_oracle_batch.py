@@ -1,4 +1,4 @@
-"""The batch oracle (or_moe_tokens, the checker of the batched GPU path) against
+"""The batch oracle (or_moe_tokens, which the batched GPU path is compared with) against
 the per-token oracle it restates: same expert chain, same k-order combine, so
 the two agree bit for bit; an id outside the store contributes zero."""
 import numpy as np
