@@ -254,3 +254,15 @@ def test_x3t_routes_with_shipped_models_match_oracle(i):
             assert np.array_equal(oc.frame(l), pc.frame(l)), (s, l)
     assert oc.predictor_stats() == pc.predictor_stats()
     assert pc.predictor_stats()["n_updates"] > 1000
+
+
+def test_sidecar_batch_share_arguments():
+    # the batched decode's host share: 0/0 falls back to the single-token
+    # share, anything else needs 0 <= num <= den, den >= 1
+    c = product_cache([8, 8])
+    c.set_sidecar_batch((2, 3))
+    c.set_sidecar_batch(None)
+    c.set_sidecar_batch((0, 1))
+    for bad in ((3, 2), (1, 0), (-1, 2)):
+        with pytest.raises(Exception):
+            c.set_sidecar_batch(bad)
