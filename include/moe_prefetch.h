@@ -460,8 +460,8 @@ typedef struct {
 int moe_cache_set_timing(moe_cache *c, int on);
 /* split: 0 (default) the fused layer -- router GEMV, selection, every routed
  * expert's gate/up and down rows and the weighted combine in one launch,
- * resident and absent experts alike (moe_decode_token without streaming;
- * moe_decode_layer and streaming use split 3's launches);
+ * resident and absent experts alike (moe_decode_token without streaming, and
+ * moe_decode_layer; streaming uses split 3's launches);
  * 3 router GEMV, selection, gate/up and down as four launches; 1 resident and
  * absent experts as separate launches on two streams, forked and joined per
  * layer; 2 the same launches one after the other on one stream.
@@ -477,14 +477,15 @@ int moe_cache_set_decode_path(moe_cache *c, int split, int graph);
 int moe_cache_set_staging(moe_cache *c, int on);
 /* CPU-assisted serving of absent experts (the reference's sidecar,
  * patches/0009: MOE_POST P9:277-320, MOE_JOIN P9:322-359, sidecar_serve
- * P9:841-912).  With n_threads > 0, moe_decode_token's router kernel posts
- * each layer's ids and Q8_K(x) to mapped host memory; the calling thread and
+ * P9:841-912).  With n_threads > 0, the decode launches of moe_decode_token
+ * and moe_decode_layer post each layer's logits (or ids) and Q8_K(x) to mapped
+ * host memory; the calling thread and
  * n_threads - 1 workers compute the absent experts whose rank r among the
  * layer's absent experts (k order) has r % den < num, from the pinned store,
  * while the GPU runs the others; a join kernel waits (at most 2 s, bounded
  * by the GPU wall clock) for the host's rows and combines sum_k w_k y_k in k
  * order.  Outputs, ids and cache traces are identical to the GPU-only path.
- * Needs split 0.  n_threads <= 0 turns it off. */
+ * Needs split 0 or 3.  n_threads <= 0 turns it off. */
 int moe_cache_set_sidecar(moe_cache *c, int n_threads, int num, int den);
 /* CPU-assisted serving in moe_decode_batch (no counterpart in the reference,
  * whose sidecar serves one token, P9:841-912): per layer the routing comes
@@ -501,8 +502,22 @@ int moe_cache_set_sidecar_batch(moe_cache *c, int num, int den);
 int moe_cache_sidecar_log(moe_cache *c, float *out, int max_rows);
 int moe_cache_kernel_times(moe_cache *c, moe_kernel_times *out);
 
-/* One layer at batch 1: route x (+bias), run the K experts, out = sum_k w_k y_k.
- * ids_dev/w_dev receive this layer's routing (dev [K]) when not NULL. */
+/* One layer at batch 1, the per-layer graph op (the cached chain and, with
+ * CPU-assisted serving, its post and join, patches/0009:659-705): route x
+ * (+bias), run the K experts, out = sum_k w_k y_k.  ids_dev/w_dev receive the
+ * layer's routing (dev [K]) when not NULL.  Split 0 (the default) runs the
+ * fused launch, split 3 the four launches.  Each call carries a sequence
+ * number of its own, so a layer's input may be computed from the layer below
+ * (x_{l+1} = x_l + out_l) between calls.  With CPU-assisted serving the
+ * calling thread waits for the layer's post, computes the host's share of its
+ * absent experts and answers before it returns; the GPU's join does the rest.
+ * Drive a token as the reference does: every layer in order, the ids observed
+ * (moe_cache_observe, after each layer or at the end; the call compares them
+ * with the host's routing and stages the experts the kernels read from the
+ * pinned store for the uploads), then moe_cache_step, which also checks the
+ * launches' bounded waits (MOE_ERR_HIP if one ran out).  Calls of one cache
+ * run one at a time on one stream; not with just-in-time streaming
+ * (MOE_ERR_STATE: streaming decodes whole tokens). */
 int moe_decode_layer(moe_cache *c, int layer, const float *x, const float *bias, float *out,
                      int32_t *ids_dev, float *w_dev, void *stream);
 /* One decode token over every layer: x dev [L][H], bias dev [L][E] or NULL,

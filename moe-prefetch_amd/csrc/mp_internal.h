@@ -83,7 +83,8 @@ struct RouteLaunch {
     float *probs;          // out [n_tok][E] or null
     uint8_t *q8x;          // out [n_tok][H/256][292]
     SidecarPost *post;     // batch-1 decode with CPU-assisted serving: post ids + Q8_K(x), or null
-    const uint32_t *seq;   // device: the token's sequence number
+    const uint32_t *seq;   // device: the token's sequence number, or null: seq_val (one layer decoded on
+    uint32_t seq_val;      // its own carries the call's number by value; 0 reads as 1)
     // router lookahead (batch 1, router GEMV path): an > 0 target layers
     int an, ak;            // targets (0..2), candidates kept per target (<= AHEAD_K)
     const float *aW[2];    // [E][H] f32 routers of the targets
@@ -145,7 +146,8 @@ struct JoinArgs {
     const float *ypart;       // dev [K + n_shared][H]
     const float *hrows;       // mapped host [K][H]
     SidecarResp *resp;        // mapped host
-    const uint32_t *seq;      // dev
+    const uint32_t *seq;      // dev, or null: seq_val is the call's sequence number
+    uint32_t seq_val;
     uint64_t timeout_ticks;   // of the 100 MHz wall clock
     float *out;               // dev [H]
 };

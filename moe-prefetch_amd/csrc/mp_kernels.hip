@@ -111,7 +111,8 @@ struct RouteArgs {
     float *probs;          // [n_tok][E] or null
     uint8_t *q8x;          // [n_tok][H/256 * 292]
     SidecarPost *post;     // batch 1 with CPU-assisted serving, or null
-    const uint32_t *seq;
+    const uint32_t *seq;   // or null: seq_val
+    uint32_t seq_val;
     int an, ak;            // router lookahead: target layers (0..2), candidates per target
     const float *aW[2];
     const float *ar[2];
@@ -290,7 +291,7 @@ __global__ __launch_bounds__(256) void route_select_kernel(RouteArgs a) {
         }
         if (a.prior) pr = a.prior[ee];
     }
-    const uint32_t seqv = a.seq ? *a.seq : 1u;
+    const uint32_t seqv = a.seq ? *a.seq : a.seq_val;
     if (a.table && tid < a.E) s_tbl[tid] = tword;
     if (look)
         for (int j = 0; j < 2; ++j) {
@@ -1341,7 +1342,7 @@ __device__ void fused_combine(const FusedArgs &a, int c, uint32_t seq, uint8_t *
 template <int DT>
 __global__ __launch_bounds__(256) void fused_kernel(FusedArgs a) {
     __shared__ __attribute__((aligned(16))) uint8_t smem[FUSED_LDS];
-    const uint32_t seq = *a.r.seq;
+    const uint32_t seq = a.r.seq ? *a.r.seq : a.r.seq_val;
     const int E = a.r.E;
     const int kt = a.x.K + a.x.n_shared;
     const int nG = kt * (a.x.I / FUSED_GU_TILE), nD = kt * (a.x.H / FUSED_DN_TILE);
@@ -1408,7 +1409,7 @@ hipError_t launch_route(const RouteLaunch &l, hipStream_t st, hipEvent_t *ev) {
     a.E = l.E; a.H = l.H; a.K = l.K;
     a.logits = l.logits; a.counter = l.counter; a.ids = l.ids; a.w = l.w; a.slots = l.slots;
     a.probs = l.probs; a.q8x = l.q8x; a.logits_in = l.logits_in;
-    a.post = l.post; a.seq = l.seq;
+    a.post = l.post; a.seq = l.seq; a.seq_val = l.seq_val ? l.seq_val : 1u;
     a.an = l.an; a.ak = l.ak;
     for (int t = 0; t < 2; ++t) {
         a.aW[t] = l.aW[t]; a.ar[t] = l.ar[t]; a.atbl[t] = l.atbl[t];
@@ -1479,7 +1480,7 @@ __global__ __launch_bounds__(256) void join_kernel(JoinArgs a) {
         if (a.n_shared) ys = a.ypart[(size_t)a.K * a.H + r];
     }
     if (threadIdx.x == 0) {
-        const uint32_t want = *a.seq;
+        const uint32_t want = a.seq ? *a.seq : a.seq_val;
         const uint64_t t0 = wall_clock64();
         int ok = 0;
         // relaxed polls (system-scope loads bypass the caches), one acquire

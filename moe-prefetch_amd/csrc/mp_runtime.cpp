@@ -222,6 +222,16 @@ struct moe_cache {
     bool freeze = false;
     FILE *replay = nullptr;
     std::vector<float> sc_log;                  // per served layer: wait us, cpu us, experts (last 64K)
+    // layers decoded one call at a time (moe_decode_layer), since the last
+    // step: each call carries its own sequence number; what the token path
+    // settles after its sync (the late-wait word, the host's routing against
+    // the GPU's, which experts were staged, kernel times) is settled at the
+    // layer's observe and at the step
+    std::vector<uint8_t> pl_flags;              // [L]: PL_* bits
+    std::vector<uint32_t> pl_seq;               // [L]: the call's sequence number
+    std::vector<hipStream_t> pl_streams;        // streams the calls ran on
+    bool pl_synced = false;                     // those streams were synchronised since the last call
+    bool pl_hot = false;                        // the host team spins between layers
     uint64_t clock = 0, n_steps = 0, n_uploads = 0, n_scheduled = 0, n_copied = 0, n_published = 0;
     uint64_t n_admit_ok = 0, n_admit_denied = 0, n_table_flushes = 0, bytes_uploaded = 0;
     uint64_t n_evicted = 0;            // resident experts the step evicted for an upload
@@ -1178,8 +1188,9 @@ size_t exp_ws_bytes(int I, int K) {
     return align_up(k1 * I * 4, 256) + align_up(k1 * (I / 256) * mp::Q8K_BYTES, 256) + align_up(k1 * 4, 256);
 }
 
+// seq: the token's sequence number on the device, or null and seq_val
 int run_route(const moe_route_desc *d, hipStream_t st, hipEvent_t *ev = nullptr, mp::SidecarPost *post = nullptr,
-              const uint32_t *seq = nullptr, const mp::RouteLaunch *ahead = nullptr) {
+              const uint32_t *seq = nullptr, const mp::RouteLaunch *ahead = nullptr, uint32_t seq_val = 0) {
     mp::RouteLaunch l{};
     if (ahead) l = *ahead;          // lookahead and table-freshness fields; the rest is set below
     l.W = d->W; l.x = d->x; l.bias = d->bias; l.prior = d->prior; l.table = d->table; l.dummy = d->dummy;
@@ -1192,6 +1203,7 @@ int run_route(const moe_route_desc *d, hipStream_t st, hipEvent_t *ev = nullptr,
     l.logits_in = d->logits;
     l.post = post;
     l.seq = seq;
+    l.seq_val = seq_val;
     HIPCHK(mp::launch_route(l, st, ev));
     return MOE_OK;
 }
@@ -1797,14 +1809,38 @@ int moe_cache_trace_open(moe_cache *c, const char *route_path, const char *map_p
     return MOE_OK;
 }
 
+// the state of a layer decoded by moe_decode_layer since the last step
+enum : uint8_t {
+    PL_DECODED = 1,     // decoded since the last step
+    PL_FUSED = 2,       // by the fused launch
+    PL_SIDECAR = 4,     // the host served its share of the absent experts
+    PL_STAGE = 8,       // the kernels staged the experts they read from the pinned store
+    PL_AGAIN = 16,      // decoded more than once: nothing of it is staged, its routing is not compared
+    PL_OBSERVED = 32,   // its ids were observed
+};
+
+static int pl_observe(moe_cache *c, int l, const int32_t *ids);
+static int pl_step(moe_cache *c);
+
 int moe_cache_observe(moe_cache *c, int layer, const int32_t *ids, int n_ids, int n_tok) {
     if (!c || !ids || layer < 0 || layer >= (int)c->L.size() || n_ids <= 0 || n_tok <= 0)
         return fail(MOE_ERR_ARG, "bad arguments");
-    return cache_observe(c, layer, ids, n_ids, n_tok);
+    // a layer moe_decode_layer decoded: its record first (early issue may
+    // upload from the staging area inside the observe)
+    const bool pl = !c->pl_flags.empty() && (c->pl_flags[(size_t)layer] & PL_DECODED) && n_tok == 1 && n_ids == c->K;
+    if (pl) {
+        const int r = pl_observe(c, layer, ids);
+        if (r != MOE_OK) return r;
+    }
+    c->stage_valid = pl;
+    const int r = cache_observe(c, layer, ids, n_ids, n_tok);
+    c->stage_valid = false;
+    return r;
 }
 
 int moe_cache_step(moe_cache *c) {
     if (!c) return fail(MOE_ERR_ARG, "null cache");
+    if (!c->pl_streams.empty()) return pl_step(c);
     return cache_step(c);
 }
 
@@ -2550,21 +2586,12 @@ int moe_cache_sync(moe_cache *c) {
     return MOE_OK;
 }
 
-static int decode_layer_impl(moe_cache *c, int layer, const float *x, const float *bias, float *out,
-                             int32_t *ids_dev, float *w_dev, hipStream_t st, hipEvent_t *ev, bool stage = false,
-                             bool sidecar = false, bool fused = false);
-
-
-int moe_decode_layer(moe_cache *c, int layer, const float *x, const float *bias, float *out, int32_t *ids_dev,
-                     float *w_dev, void *stream) {
-    return decode_layer_impl(c, layer, x, bias, out, ids_dev, w_dev, (hipStream_t)stream, nullptr);
-}
-
-// fused: the token's sequence number is in d_seq (moe_decode_token), split is
-// 0 and streaming is off; the router, selection and gate/up run as one launch
+// fused: split is 0 and streaming is off; the router, selection, experts and
+// combine run as one launch.  seq_val: 0, the token's sequence number is in
+// d_seq (moe_decode_token); else the call's own number, passed by value
 static int decode_layer_impl(moe_cache *c, int layer, const float *x, const float *bias, float *out,
                              int32_t *ids_dev, float *w_dev, hipStream_t st, hipEvent_t *ev, bool stage,
-                             bool sidecar, bool fused) {
+                             bool sidecar, bool fused, uint32_t seq_val) {
     if (!c || !x || !out || layer < 0 || layer >= (int)c->L.size()) return fail(MOE_ERR_ARG, "bad arguments");
     if (c->host_only) return fail(MOE_ERR_STATE, "host-only cache (device < 0) cannot decode");
     const Layer &ls = c->L[layer];
@@ -2650,7 +2677,8 @@ static int decode_layer_impl(moe_cache *c, int layer, const float *x, const floa
         rl.E = rd.E; rl.H = rd.H; rl.K = rd.K; rl.n_tok = 1;
         rl.ids = ids; rl.w = w; rl.slots = slots;
         rl.post = sidecar ? c->sc_post_d + layer : nullptr;
-        rl.seq = c->d_seq;
+        rl.seq = seq_val ? nullptr : c->d_seq;
+        rl.seq_val = seq_val;
         f.x = a;
         f.x.ypart = sidecar ? c->ypart : nullptr;       // the join kernel combines with the host's rows
         f.xlog = c->fx + (size_t)layer * c->fx_words;
@@ -2661,7 +2689,8 @@ static int decode_layer_impl(moe_cache *c, int layer, const float *x, const floa
         f.wait_ticks = (uint64_t)(c->fused_wait_s * 1e8);
         HIPCHK(mp::launch_fused(f, st, E_(0), E_(1)));
     } else {
-        const int r = run_route(&rd, st, ev, sidecar ? c->sc_post_d + layer : nullptr, c->d_seq, stm ? &look : nullptr);
+        const int r = run_route(&rd, st, ev, sidecar ? c->sc_post_d + layer : nullptr, seq_val ? nullptr : c->d_seq,
+                                stm ? &look : nullptr, seq_val);
         if (r != MOE_OK) return r;
     }
     if (c->split == 0 || c->split == 3) {
@@ -2678,7 +2707,8 @@ static int decode_layer_impl(moe_cache *c, int layer, const float *x, const floa
             j.ypart = c->ypart;
             j.hrows = c->sc_rows_d + (size_t)layer * c->K * c->H;
             j.resp = c->sc_resp_d + layer;
-            j.seq = c->d_seq;
+            j.seq = seq_val ? nullptr : c->d_seq;
+            j.seq_val = seq_val;
             j.timeout_ticks = (uint64_t)(c->sc_timeout_s * 1e8);     // 100 MHz wall clock
             j.out = a.out;
             HIPCHK(mp::launch_join(j, st));
@@ -2708,25 +2738,250 @@ static int decode_layer_impl(moe_cache *c, int layer, const float *x, const floa
     return MOE_OK;
 }
 
+// a fresh sequence number for a token or a layer call (never 0 nor SC_ABORT)
+static uint32_t next_seq(moe_cache *c) {
+    uint32_t seq = ++c->sc_seq;
+    if (seq == 0 || seq == mp::SC_ABORT) seq = c->sc_seq = 1;
+    return seq;
+}
+
+// timing mode: 12 events per layer, stamped by the launches' dispatches
+static int ensure_tev(moe_cache *c) {
+    const size_t n = c->L.size() * 12;
+    if (!c->timing || c->tev.size() == n) return MOE_OK;
+    for (hipEvent_t e : c->tev) hipEventDestroy(e);
+    c->tev.assign(n, nullptr);
+    for (auto &e : c->tev) HIPCHK(hipEventCreate(&e));
+    return MOE_OK;
+}
+
+// the staging area, [L][K] experts of the largest slot size, at first use
+static int ensure_stage(moe_cache *c) {
+    if (!c->staging || c->stage) return MOE_OK;
+    size_t sb = 0;
+    for (const Layer &ls : c->L) sb = std::max(sb, (size_t)ls.slot_bytes);
+    const size_t n = c->L.size() * (size_t)c->K * sb;
+    if (hipMalloc(&c->stage, n) != hipSuccess) {
+        c->stage = nullptr;
+        return fail(MOE_ERR_NOMEM, "staging area of %zu bytes", n);
+    }
+    c->stage_stride = sb;
+    drop_graphs(c);             // captured launches carry the staging pointers
+    return MOE_OK;
+}
+
+// layer l's routed experts the kernels read from the pinned store (and so
+// staged), from the token's ids and the slots the GPU read (h_ids, h_slots):
+// absent experts the host served were not read by the kernels
+static void set_staged(moe_cache *c, int l, bool sc, bool stage) {
+    Layer &ls = c->L[l];
+    int r = 0;
+    for (int k = 0; k < c->K; ++k) {
+        const int id = c->h_ids[(size_t)l * c->K + k], gs = c->h_slots[(size_t)l * c->K + k];
+        const bool absent = id >= 0 && id < ls.E && !(gs >= 0 && gs < ls.S);
+        const bool cpu = absent && sc && r % c->sc_den < c->sc_num;
+        r += absent;
+        ls.staged[k] = stage && absent && !cpu ? id : -1;
+    }
+}
+
+// timing mode: layer l's kernel times (its events) and the expert bytes its
+// launches read by source, from h_ids / h_slots when have_ids
+static int account_times(moe_cache *c, int l, bool fused, bool sc, bool have_ids) {
+    const uint64_t gu_b = 2ull * c->I * (c->H / 256) * mp::Q4K_BYTES;
+    float t[6] = {0, 0, 0, 0, 0, 0};
+    hipEvent_t *e = c->tev.data() + (size_t)l * 12;
+    const Layer &ls = c->L[l];
+    if (fused) {            // [0,1] the fused layer
+        HIPCHK(hipEventElapsedTime(&t[0], e[0], e[1]));
+        c->kt.layer_ms += t[0];
+        c->kt.layer_hbm_bytes += (uint64_t)c->E * c->H * 4;       // the router rows
+    } else {
+        for (int i = 0; i < 6; ++i) {
+            if ((c->split == 0 || c->split == 3) && i >= 4) break;   // no separate absent-expert launches
+            HIPCHK(hipEventElapsedTime(&t[i], e[2 * i], e[2 * i + 1]));
+        }
+        c->kt.route_ms += t[0] + t[1];
+        c->kt.gateup_hbm_ms += t[2];
+        c->kt.down_hbm_ms += t[3];
+        c->kt.gateup_host_ms += t[4];
+        c->kt.down_host_ms += t[5];
+    }
+    c->kt.n_layers++;
+    if (!have_ids) return MOE_OK;
+    int r_abs = 0;          // rank among the absent experts: the host's share is not read by the GPU
+    for (int k = 0; k < c->K; ++k) {
+        const int gs = c->h_slots[(size_t)l * c->K + k];
+        const int id = c->h_ids[(size_t)l * c->K + k];
+        const bool res = gs >= 0 && gs < ls.S;
+        const bool absent = !res && id >= 0 && id < ls.E;
+        const bool cpu = absent && sc && r_abs % c->sc_den < c->sc_num;
+        r_abs += absent;
+        if (cpu) continue;
+        (res ? c->kt.gateup_hbm_bytes : c->kt.gateup_host_bytes) += gu_b;
+        (res ? c->kt.down_hbm_bytes : c->kt.down_host_bytes) += ls.expert_bytes - gu_b;
+        if (fused) (res ? c->kt.layer_hbm_bytes : c->kt.layer_host_bytes) += ls.expert_bytes;
+    }
+    if (ls.shared) {
+        c->kt.gateup_hbm_bytes += gu_b;
+        c->kt.down_hbm_bytes += ls.expert_bytes - gu_b;
+        if (fused) c->kt.layer_hbm_bytes += ls.expert_bytes;
+    }
+    return MOE_OK;
+}
+
+// ---- one layer per call ---------------------------------------------------------
+static int pl_sync(moe_cache *c) {
+    if (c->pl_synced) return MOE_OK;
+    for (hipStream_t s : c->pl_streams) HIPCHK(hipStreamSynchronize(s));
+    c->pl_synced = true;
+    return MOE_OK;
+}
+
+static void pl_clear(moe_cache *c) {
+    std::fill(c->pl_flags.begin(), c->pl_flags.end(), (uint8_t)0);
+    c->pl_streams.clear();
+    c->pl_synced = false;
+    if (c->pl_hot && c->team) mpc::team_hot(c->team, false);
+    c->pl_hot = false;
+}
+
+// observe of a layer decoded by moe_decode_layer: its ids and the slots the
+// GPU read (the published table, which changes only at the step) become the
+// token's record; with CPU-assisted serving the host's routing must equal
+// the ids observed; with staging, the experts the kernels read from the
+// store are staged for the uploads observe (early issue) or the step start
+static int pl_observe(moe_cache *c, int l, const int32_t *ids) {
+    const int r = pl_sync(c);
+    if (r != MOE_OK) return r;
+    const uint8_t f = c->pl_flags[(size_t)l];
+    const Layer &ls = c->L[(size_t)l];
+    for (int k = 0; k < c->K; ++k) {
+        const int id = ids[k];
+        c->h_ids[(size_t)l * c->K + k] = id;
+        c->h_slots[(size_t)l * c->K + k] = id >= 0 && id < ls.E ? c->h_tbl[(size_t)l * c->E + id] : ls.S;
+    }
+    const bool once = !(f & PL_AGAIN);
+    if ((f & PL_SIDECAR) && once && memcmp(c->sc_ids.data() + (size_t)l * c->K, ids, (size_t)c->K * 4) != 0)
+        return fail(MOE_ERR_STATE, "layer %d: the host's routing differs from the ids observed", l);
+    set_staged(c, l, (f & PL_SIDECAR) != 0, (f & PL_STAGE) && once);
+    c->pl_flags[(size_t)l] |= PL_OBSERVED;
+    return MOE_OK;
+}
+
+// the step after per-layer calls: their kernels have finished; a bounded
+// wait that ran out (fused late word, a join's error word) fails the token
+static int pl_step(moe_cache *c) {
+    int r = pl_sync(c);
+    uint32_t late_seq = 0;
+    const size_t NL = c->L.size();
+    if (r == MOE_OK && hipMemcpy(&late_seq, c->d_ids + NL * c->K, 4, hipMemcpyDeviceToHost) != hipSuccess)
+        r = fail(MOE_ERR_HIP, "late-wait word read back");
+    bool late = false, late_join = false, staged = false;
+    for (size_t l = 0; l < NL && r == MOE_OK; ++l) {
+        const uint8_t f = c->pl_flags[l];
+        if (!(f & PL_DECODED)) continue;
+        late |= (f & PL_FUSED) && late_seq == c->pl_seq[l];
+        if (f & PL_SIDECAR) {
+            late_join |= c->sc_resp[l].err != 0;
+            c->sc_resp[l].err = 0;
+        }
+        staged |= (f & PL_STAGE) && (f & PL_OBSERVED) && !(f & PL_AGAIN);
+        if (c->timing) r = account_times(c, (int)l, (f & PL_FUSED) != 0, (f & PL_SIDECAR) != 0, (f & PL_OBSERVED) != 0);
+    }
+    pl_clear(c);
+    if (r != MOE_OK) return r;
+    if (late) return fail(MOE_ERR_HIP, "a fused layer's workgroup gave up waiting for another (%.1f s)", c->fused_wait_s);
+    if (late_join) return fail(MOE_ERR_HIP, "a join kernel gave up waiting for the host (%.1f s)", c->sc_timeout_s);
+    c->stage_valid = staged;
+    r = cache_step(c);
+    c->stage_valid = false;
+    if (c->stg_pending) HIPCHK(hipEventRecord(c->ev_stg, c->stg_stream));
+    return r;
+}
+
+// One decode layer at batch 1 on its own: the reference's per-layer graph op
+// (the cached chain, and with the sidecar its post and join, P9:659-705).
+// The fused launch by default (split 0); split 3's launches otherwise.  With
+// CPU-assisted serving the calling thread serves the host's share of the
+// layer's absent experts before it returns, and the GPU's join waits for it.
+int moe_decode_layer(moe_cache *c, int layer, const float *x, const float *bias, float *out, int32_t *ids_dev,
+                     float *w_dev, void *stream) {
+    if (!c || !x || !out || layer < 0 || layer >= (int)c->L.size()) return fail(MOE_ERR_ARG, "bad arguments");
+    if (c->host_only) return fail(MOE_ERR_STATE, "host-only cache (device < 0) cannot decode");
+    if (c->st && c->st->live) return fail(MOE_ERR_STATE, "just-in-time streaming decodes whole tokens (moe_decode_token)");
+    const hipStream_t st = (hipStream_t)stream;
+    const size_t NL = c->L.size();
+    int r = ensure_stage(c);
+    if (r == MOE_OK) r = ensure_tev(c);
+    if (r != MOE_OK) return r;
+    if (c->pl_flags.size() != NL) {
+        c->pl_flags.assign(NL, 0);
+        c->pl_seq.assign(NL, 0);
+    }
+    if (c->pl_streams.empty())          // the first call since the step: nothing is staged yet
+        for (Layer &ls : c->L) std::fill(ls.staged.begin(), ls.staged.end(), -1);
+    std::fill(c->L[(size_t)layer].staged.begin(), c->L[(size_t)layer].staged.end(), -1);
+    // uploads copied from the staging area so far must be done before this
+    // layer's kernels overwrite it
+    if (c->stg_pending) {
+        HIPCHK(hipEventRecord(c->ev_stg, c->stg_stream));
+        HIPCHK(hipStreamWaitEvent(st, c->ev_stg, 0));
+        c->stg_pending = false;
+    }
+    const bool stage = c->staging && c->stage;
+    const bool sc = c->sc_den > 0;
+    const bool fused = c->split == 0;
+    // a failed token may have left SC_ABORT in this layer's answer word; every
+    // kernel of that token has finished (the failure synchronised its stream)
+    if (sc && c->sc_resp[layer].seq == mp::SC_ABORT) {
+        *(volatile uint32_t *)&c->sc_resp[layer].seq = 0;
+        *(volatile uint32_t *)&c->sc_resp[layer].err = 0;
+    }
+    const uint32_t seq = next_seq(c);
+    r = decode_layer_impl(c, layer, x, bias, out, ids_dev, w_dev, st,
+                          c->timing ? c->tev.data() + (size_t)layer * 12 : nullptr, stage, sc, fused, seq);
+    if (r != MOE_OK) {
+        hipStreamSynchronize(st);
+        return r;
+    }
+    if (sc) {
+        if (!c->pl_hot) {
+            mpc::team_hot(c->team, true);
+            c->pl_hot = true;
+        }
+        r = sidecar_serve(c, layer, seq, fused);
+        if (r != MOE_OK) {              // end the join's wait, and let every kernel finish
+            *(volatile uint32_t *)&c->sc_resp[layer].seq = mp::SC_ABORT;
+            hipStreamSynchronize(st);
+            *(volatile uint32_t *)&c->sc_resp[layer].seq = 0;
+            *(volatile uint32_t *)&c->sc_resp[layer].err = 0;
+            return r;
+        }
+    }
+    uint8_t &f = c->pl_flags[(size_t)layer];
+    f = (uint8_t)((f & PL_DECODED ? PL_AGAIN : 0) | PL_DECODED | (fused ? PL_FUSED : 0) | (sc ? PL_SIDECAR : 0) |
+                  (stage ? PL_STAGE : 0));
+    c->pl_seq[(size_t)layer] = seq;
+    if (std::find(c->pl_streams.begin(), c->pl_streams.end(), st) == c->pl_streams.end()) c->pl_streams.push_back(st);
+    c->pl_synced = false;
+    return MOE_OK;
+}
+
 int moe_decode_token(moe_cache *c, const float *x, const float *bias, float *out, int32_t *ids_host, void *stream) {
     if (!c || !x || !out) return fail(MOE_ERR_ARG, "bad arguments");
     if (c->host_only) return fail(MOE_ERR_STATE, "host-only cache (device < 0) cannot decode");
     hipStream_t st = (hipStream_t)stream;
     const int NL = (int)c->L.size();
-    if (c->timing && c->tev.size() != (size_t)NL * 12) {
-        for (hipEvent_t e : c->tev) hipEventDestroy(e);
-        c->tev.assign((size_t)NL * 12, nullptr);
-        for (auto &e : c->tev) HIPCHK(hipEventCreate(&e));
-    }
-    if (c->staging && !c->stage) {
-        size_t sb = 0;
-        for (const Layer &ls : c->L) sb = std::max(sb, (size_t)ls.slot_bytes);
-        if (hipMalloc(&c->stage, (size_t)NL * c->K * sb) != hipSuccess) {
-            c->stage = nullptr;
-            return fail(MOE_ERR_NOMEM, "staging area of %zu bytes", (size_t)NL * c->K * sb);
-        }
-        c->stage_stride = sb;
-        drop_graphs(c);
+    int er = ensure_tev(c);
+    if (er == MOE_OK) er = ensure_stage(c);
+    if (er != MOE_OK) return er;
+    // layers decoded one by one and not stepped: their kernels finish first,
+    // and this token's record replaces theirs
+    if (!c->pl_streams.empty()) {
+        er = pl_sync(c);
+        pl_clear(c);
+        if (er != MOE_OK) return er;
     }
     const bool stage = c->staging && c->stage;
     // the last step's device-to-device uploads read the staging area this
@@ -2742,8 +2997,7 @@ int moe_decode_token(moe_cache *c, const float *x, const float *bias, float *out
     // (the fused layers' exchange words are tagged with it too).  The copy
     // reads h_seq when the stream reaches it; the previous token synchronised
     // the stream before returning, so no copy of an older number is pending.
-    uint32_t seq = ++c->sc_seq;
-    if (seq == 0 || seq == mp::SC_ABORT) seq = c->sc_seq = 1;
+    const uint32_t seq = next_seq(c);
     *c->h_seq = seq;
     HIPCHK(hipMemcpyAsync(c->d_seq, c->h_seq, 4, hipMemcpyHostToDevice, st));
     const bool fused = c->split == 0 && !stm;
@@ -2788,7 +3042,8 @@ int moe_decode_token(moe_cache *c, const float *x, const float *bias, float *out
         for (int l = 0; l < NL; ++l) {
             const int r = decode_layer_impl(c, l, x + (size_t)l * c->H, bias ? bias + (size_t)l * c->E : nullptr,
                                             out + (size_t)l * c->H, nullptr, nullptr, st,
-                                            c->timing ? c->tev.data() + (size_t)l * 12 : nullptr, stage, sc, fused);
+                                            c->timing ? c->tev.data() + (size_t)l * 12 : nullptr, stage, sc, fused,
+                                            0);
             if (r != MOE_OK) {
                 abort_joins();
                 hipStreamSynchronize(st);
@@ -2807,7 +3062,7 @@ int moe_decode_token(moe_cache *c, const float *x, const float *bias, float *out
             for (int l = 0; l < NL && r == MOE_OK; ++l)
                 r = decode_layer_impl(c, l, c->x_buf + (size_t)l * c->H, key ? c->bias_buf + (size_t)l * c->E : nullptr,
                                       c->out_buf + (size_t)l * c->H, nullptr, nullptr, c->cap_stream, nullptr, stage,
-                                      sc, fused);
+                                      sc, fused, 0);
 
             hipGraph_t g = nullptr;
             const hipError_t ec = hipStreamEndCapture(c->cap_stream, &g);
@@ -2854,63 +3109,15 @@ int moe_decode_token(moe_cache *c, const float *x, const float *bias, float *out
         if (memcmp(c->sc_ids.data(), c->h_ids, (size_t)NL * c->K * 4) != 0)
             return fail(MOE_ERR_STATE, "the host's routing of a layer differs from the GPU's");
     }
-    if (c->timing) {
-        const uint64_t gu_b = 2ull * c->I * (c->H / 256) * mp::Q4K_BYTES;
+    if (c->timing)
         for (int l = 0; l < NL; ++l) {
-            float t[6] = {0, 0, 0, 0, 0, 0};
-            hipEvent_t *e = c->tev.data() + (size_t)l * 12;
-            const Layer &ls = c->L[l];
-            if (fused) {            // [0,1] the fused layer
-                HIPCHK(hipEventElapsedTime(&t[0], e[0], e[1]));
-                c->kt.layer_ms += t[0];
-                c->kt.layer_hbm_bytes += (uint64_t)c->E * c->H * 4;       // the router rows
-            } else {
-                for (int i = 0; i < 6; ++i) {
-                    if ((c->split == 0 || c->split == 3) && i >= 4) break;   // no separate absent-expert launches
-                    HIPCHK(hipEventElapsedTime(&t[i], e[2 * i], e[2 * i + 1]));
-                }
-                c->kt.route_ms += t[0] + t[1];
-                c->kt.gateup_hbm_ms += t[2];
-                c->kt.down_hbm_ms += t[3];
-                c->kt.gateup_host_ms += t[4];
-                c->kt.down_host_ms += t[5];
-            }
-            c->kt.n_layers++;
-            int r_abs = 0;          // rank among the absent experts: the host's share is not read by the GPU
-            for (int k = 0; k < c->K; ++k) {
-                const int gs = c->h_slots[(size_t)l * c->K + k];
-                const int id = c->h_ids[(size_t)l * c->K + k];
-                const bool res = gs >= 0 && gs < ls.S;
-                const bool absent = !res && id >= 0 && id < ls.E;
-                const bool cpu = absent && sc && r_abs % c->sc_den < c->sc_num;
-                r_abs += absent;
-                if (cpu) continue;
-                (res ? c->kt.gateup_hbm_bytes : c->kt.gateup_host_bytes) += gu_b;
-                (res ? c->kt.down_hbm_bytes : c->kt.down_host_bytes) += ls.expert_bytes - gu_b;
-                if (fused) (res ? c->kt.layer_hbm_bytes : c->kt.layer_host_bytes) += ls.expert_bytes;
-            }
-            if (ls.shared) {
-                c->kt.gateup_hbm_bytes += gu_b;
-                c->kt.down_hbm_bytes += ls.expert_bytes - gu_b;
-                if (fused) c->kt.layer_hbm_bytes += ls.expert_bytes;
-            }
+            const int tr = account_times(c, l, fused, sc, true);
+            if (tr != MOE_OK) return tr;
         }
-    }
     // which routed experts the kernels read from the store (and staged): the
     // slots the GPU read say which were absent
-    if (stage) {
-        for (int l = 0; l < NL; ++l) {
-            Layer &ls = c->L[l];
-            int r = 0;         // (absent experts the CPU served were not read by the kernels)
-            for (int k = 0; k < c->K; ++k) {
-                const int id = c->h_ids[(size_t)l * c->K + k], gs = c->h_slots[(size_t)l * c->K + k];
-                const bool absent = id >= 0 && id < ls.E && !(gs >= 0 && gs < ls.S);
-                const bool cpu = absent && sc && r % c->sc_den < c->sc_num;
-                r += absent;
-                ls.staged[k] = absent && !cpu ? id : -1;
-            }
-        }
-    }
+    if (stage)
+        for (int l = 0; l < NL; ++l) set_staged(c, l, sc, true);
     // (early issue starts uploads inside observe: staged copies apply there too)
     c->stage_valid = stage;
     int r = MOE_OK;

@@ -109,6 +109,7 @@ class Rig:
 
     def oracle_cache(self):
         kn = dict(self.knobs)
+        kn.pop("prior_space", None)         # the space only changes the routing (O.route's prior_on_logits)
         kn.setdefault("admit", "off")
         return O.Cache(self.slots, n_experts=self.E, **kn)
 
@@ -122,6 +123,9 @@ class Rig:
             w.append(1.0)
         return O.moe_layer(H, self.I, self.down_types[l], experts, np.asarray(w, np.float32),
                            self.xh[t, l] if x is None else x)
+
+    def prior_on_logits(self):
+        return self.knobs.get("prior_space") == "logits"
 
     def close(self):
         self.cache.close()

@@ -167,6 +167,11 @@ class Store:
 def routing(rng, T, K, E, kind):
     if kind == "uniform":
         ids = np.stack([rng.choice(E, size=K, replace=False) for _ in range(T)])
+    elif kind == "repeat":  # pair i = t*K + k routed to expert i % 2, as the reference's repeated-ids mode
+        ids = (np.arange(T * K) % 2).reshape(T, K)   # (cpp/test-moe-rows.cpp:60-67, mode 3)
+    elif kind == "dups":    # ids drawn with replacement from 5 experts: repeats inside a token, uneven
+        hot = rng.choice(E, size=5, replace=False)
+        ids = np.stack([rng.choice(hot, size=K, replace=True) for _ in range(T)])
     else:   # crowd: most tokens share a handful of experts (several passes of 64 pairs)
         hot = rng.choice(E, size=K + 2, replace=False)
         ids = np.stack([rng.choice(hot, size=K, replace=False) if rng.random() < 0.8 else
@@ -206,6 +211,8 @@ GROUPED_CASES = {
     "q4k_i768_t512": (_lib.TYPE_Q4K, 768, 512, 128, "uniform", "bf16"),
     "q6k_i768_t200_crowded": (_lib.TYPE_Q6K, 768, 200, 128, "crowd", "bf16"),
     "q4k_i256_t150_e64_crowded": (_lib.TYPE_Q4K, 256, 150, 64, "crowd", "f32"),
+    "q4k_i768_t24_repeated_ids": (_lib.TYPE_Q4K, 768, 24, 128, "repeat", "bf16"),
+    "q6k_i512_t40_ids_with_replacement": (_lib.TYPE_Q6K, 512, 40, 128, "dups", "f32"),
 }
 
 

@@ -42,7 +42,8 @@ def check_run(rig, tmp_path, out_every=1, tol=1e-3, oc=None, record_map=True, to
             tbl, prior = oc.table(l)
             use_prior = prior if rig.knobs.get("cache_prior", 0.0) > 0 else None
             bias = None if rig.bh is None else rig.bh[t, l]
-            rids, rw, _, _ = O.route(rig.Wh[l], rig.xh[t, l], 8, bias=bias, prior=use_prior, table=tbl)
+            rids, rw, _, _ = O.route(rig.Wh[l], rig.xh[t, l], 8, bias=bias, prior=use_prior, table=tbl,
+                                     prior_on_logits=rig.prior_on_logits())
             assert np.array_equal(ids_all[t][l], rids), (t, l, ids_all[t][l], rids)
             if t in keep:
                 want = rig.oracle_layer(t, l, rids, rw)
@@ -176,6 +177,21 @@ def test_decode_cache_prior_delta(tmp_path):
     # no steering: routing is W x alone, and the 0.01 prior on resident
     # experts' probabilities changes the selection
     rig = Rig([24, 24], [Q4, Q6], T=48, steer=False, admit="window", cache_prior=0.01)
+    try:
+        check_run(rig, tmp_path)
+    finally:
+        rig.close()
+
+
+@pytest.mark.parametrize("graph", [1, 0], ids=["graph", "eager"])
+def test_decode_cache_prior_on_logits_fused(tmp_path, graph):
+    # the logits-space variant of the cache prior (delta added to resident
+    # experts' logits before the top-k, gate weights from the unbiased
+    # softmax) on the default fused launch, which routes the token inside
+    # every gate/up wave; no steering, so the prior changes the selection
+    rig = Rig([24, 24, 16], [Q4, Q6, Q4], T=48, steer=False, admit="window", batch_tables=True, cache_prior=0.01,
+              prior_space="logits")
+    rig.cache.set_decode_path(split=0, graph=bool(graph))
     try:
         check_run(rig, tmp_path)
     finally:
@@ -430,3 +446,110 @@ def test_expert_cache_dropin():
     assert L().moe_memcpy(back.ctypes.data, c.slot_ptr(0, slot), nb) == 0
     assert np.array_equal(back, c.staging[10])
     c.close()
+
+
+@pytest.mark.parametrize("case", ["fused", "fused-sidecar", "fused-sidecar-2of3-each-early", "fused-timing-each",
+                                  "unfused-sidecar", "fused-prior-logits-sidecar"])
+def test_decode_layer_by_layer(tmp_path, case):
+    """The per-layer op (moe_decode_layer: the reference's cached-MoE graph op,
+    patches/0009:659-705) driving a real decode: layer l + 1's input is
+    x_l + out_l (fp32, the same bits on the host), so no layer's input exists
+    before the layer below has run.  Per token: every layer through
+    moe_decode_layer (the fused launch, or split 3's launches; with the
+    sidecar the call serves the host's share before it returns), the ids
+    observed -- after the token, or after each layer as the reference's
+    callback does (`each`, with early issue: uploads start mid-token) -- and
+    one step.  Ids, frames, route and map traces and outputs equal the
+    oracle's bit for bit, 40 tokens x 4 layers."""
+    knobs = dict(admit="window", batch_tables=True)
+    if "early" in case:
+        knobs = dict(admit="off", early_issue=True)
+    if "prior-logits" in case:
+        knobs.update(cache_prior=0.01, prior_space="logits")
+    rig = Rig([16, 24, 12, 40], [Q4, Q6, Q4, Q6], T=40, steer="prior" not in case, **knobs)
+    rig.cache.set_decode_path(split=3 if case.startswith("unfused") else 0, graph=False)
+    if "sidecar" in case:
+        rig.cache.set_sidecar(6, (2, 3) if "2of3" in case else (1, 1))
+    if "timing" in case:
+        rig.cache.set_timing(True)
+    each = "each" in case
+    rp, mp = str(tmp_path / "gpu.routes"), str(tmp_path / "gpu.map")
+    orp, omp = str(tmp_path / "ora.routes"), str(tmp_path / "ora.map")
+    rig.cache.trace_open(rp, mp)
+    oc = rig.oracle_cache()
+    oc.trace_open(orp, omp)
+    nl, dev, st = rig.nl, rig.dev, torch.cuda.current_stream().cuda_stream
+    ids_dev = torch.empty((nl, 8), dtype=torch.int32, device=dev)
+    outs = torch.empty((nl, 2048), dtype=torch.float32, device=dev)
+    try:
+        for t in range(rig.T):
+            x = rig.x[t, 0].clone()
+            for l in range(nl):
+                b = None if rig.bias is None else rig.bias[t, l]
+                rig.cache.decode_layer(l, x, outs[l], bias=b, ids=ids_dev[l], stream=st)
+                if each:
+                    rig.cache.observe(l, ids_dev[l].cpu().numpy())
+                x = x + outs[l]
+            got_ids = ids_dev.cpu().numpy()
+            got = outs.cpu().numpy()
+            if not each:
+                for l in range(nl):
+                    rig.cache.observe(l, got_ids[l])
+            rig.cache.step()
+            xh = rig.xh[t, 0].copy()
+            for l in range(nl):
+                tbl, prior = oc.table(l)
+                use_prior = prior if rig.knobs.get("cache_prior", 0.0) > 0 else None
+                bias = None if rig.bh is None else rig.bh[t, l]
+                rids, rw, _, _ = O.route(rig.Wh[l], xh, 8, bias=bias, prior=use_prior, table=tbl,
+                                         prior_on_logits=rig.prior_on_logits())
+                assert np.array_equal(got_ids[l], rids), (t, l, got_ids[l], rids)
+                want = rig.oracle_layer(t, l, rids, rw, x=xh)
+                assert np.array_equal(got[l], want), (t, l, float(np.abs(got[l] - want).max()))
+                oc.observe(l, rids)
+                xh = (xh + want).astype(np.float32)
+            oc.step()
+            for l in range(nl):
+                assert np.array_equal(rig.cache.frame(l), oc.frame(l)), (t, l)
+        st_, ost = rig.cache.stats(), oc.stats()
+        for k in ("n_hit", "n_miss", "n_scheduled", "n_published", "n_admit_ok", "n_admit_denied"):
+            assert st_[k] == ost[k], (k, st_[k], ost[k])
+        assert st_["n_scheduled"] > 0
+        if "sidecar" in case:
+            assert st_["n_cpu_served"] > 0
+        else:
+            assert st_["n_staged"] > 0          # uploads copied from what the layer kernels staged
+        if "timing" in case:
+            kt = rig.cache.kernel_times()
+            assert kt["n_layers"] == rig.T * nl and kt["layer_ms"] > 0 and kt["layer_hbm_bytes"] > 0
+    finally:
+        rig.cache.close()
+        oc.close()
+        rig.close()
+    assert open(rp).read() == open(orp).read()
+    assert open(mp).read() == open(omp).read()
+
+
+@pytest.mark.parametrize("graph", [1, 0], ids=["graph", "eager"])
+def test_decode_one_layer_all_resident_fused(tmp_path, graph):
+    """The one-layer workload: a layer of 128 experts, all resident (placed
+    by a heat file naming each of them, patches/0007:431-485), an N(0,0.02)
+    router with no steering, 40 tokens through the default fused launch:
+    every id, frame, trace line and output bit-exact, every routed expert a
+    hit, no upload."""
+    E = 128
+    heat = tmp_path / "all.heat"
+    # (counts are halved at load, patches/0007:461: every count here stays above 0)
+    heat.write_text("\n".join([f"moe-heat 1 1 {E}"] + [f"0 {e} {2 * (E - e)}" for e in range(E)]) + "\n")
+    rig = Rig([E], [Q4], T=40, steer=False, admit="window", batch_tables=True)
+    rig.cache.set_decode_path(split=0, graph=bool(graph))
+    try:
+        assert rig.cache.heat_file(str(heat)) == (E, E)
+        assert sorted(rig.cache.frame(0).tolist()) == list(range(E))
+        oc = rig.oracle_cache()
+        assert oc.heat_file(str(heat)) == (E, E)
+        check_run(rig, tmp_path, oc=oc)
+    finally:
+        rig.close()
+    st = rig.stats
+    assert st["n_miss"] == 0 and st["n_hit"] == 40 * 8 and st["n_scheduled"] == 0

@@ -200,6 +200,31 @@ def test_experts_within_tolerance(dt, I):
         store.free()
 
 
+@pytest.mark.parametrize("dt", [_lib.TYPE_Q4K, _lib.TYPE_Q6K])
+def test_experts_repeated_ids(dt):
+    # the reference's repeated-ids mode (cpp/test-moe-rows.cpp:60-67, mode 3):
+    # routed slot k takes expert k % 2, expert 0 resident and expert 1 read
+    # from the pinned store; then one expert in every slot, and ids drawn with
+    # replacement over mixed sources -- bit for bit as the oracle
+    I, n = 768, 16
+    pool, store, eb = make_experts(n, I, dt, seed=7 + dt)
+    rng = np.random.default_rng(31 + dt)
+    try:
+        cases = [(np.arange(8) % 2, np.where(np.arange(8) % 2 == 0, 0, n)),
+                 (np.full(8, 5), np.full(8, 5)), (np.full(8, 9), np.full(8, n))]
+        ids = rng.choice(4, 8, replace=True)
+        cases.append((ids, np.where(ids % 2 == 0, ids, n)))
+        for ids, slots in cases:
+            w = rng.random(8).astype(np.float32)
+            w /= w.sum()
+            x = rng.standard_normal(H).astype(np.float32)
+            got = run_experts(pool, store, eb, n, I, dt, ids, slots, w, x)
+            want = O.moe_layer(H, I, dt, [store.arr[e * eb:(e + 1) * eb] for e in ids], w, x)
+            assert np.array_equal(got, want), (ids, slots, rel_l2(got, want))
+    finally:
+        store.free()
+
+
 def test_experts_accumulate_and_zero_input():
     I, dt, n = 768, _lib.TYPE_Q4K, 8
     pool, store, eb = make_experts(n, I, dt)
