@@ -204,6 +204,34 @@ class Workload:
         torch.cuda.synchronize()
         return time.perf_counter() - tic
 
+    def tokens_per_layer(self, cache, t0, t1, ids_log, xin, outs):
+        """Decode tokens [t0, t1) as a model drives the per-layer op: layer l's
+        input is x_l = x_{l-1} + out_{l-1} (x_0 the token's first activation;
+        one add on the stream per layer, the caller's residual), every layer
+        one moe_decode_layer call (the fused launch; the host's share of the
+        absent experts served inside the call), the ids copied back once, each
+        layer observed, one step.  xin [T][L][H] and outs [T][L][H] keep every
+        layer's input and output for the check.  Returns the elapsed seconds,
+        synchronised on both sides."""
+        torch = self.torch
+        ids_dev = torch.empty((self.NL, K), dtype=torch.int32, device=self.dev)
+        bias = self.bias
+        torch.cuda.synchronize()
+        tic = time.perf_counter()
+        for t in range(t0, t1):
+            xin[t, 0].copy_(self.x[t, 0])
+            for l in range(self.NL):
+                cache.decode_layer(l, xin[t, l], outs[t, l], bias=None if bias is None else bias[t, l],
+                                   ids=ids_dev[l], stream=self.stream)
+                if l + 1 < self.NL:
+                    torch.add(xin[t, l], outs[t, l], out=xin[t, l + 1])
+            ids_log[t] = ids_dev.cpu().numpy()
+            for l in range(self.NL):
+                cache.observe(l, ids_log[t, l])
+            cache.step()
+        torch.cuda.synchronize()
+        return time.perf_counter() - tic
+
     def kernel_pass(self, cache, split=2, keep_serving=False):
         """Per-kernel durations: the same cache continues for --kernel-steps more
         tokens launched eagerly (HIP events cannot be read from graph nodes).
@@ -225,13 +253,42 @@ class Workload:
                    for l in range(self.NL)]
             b2 = torch.from_numpy(self.steering_bias(tg2, n_experts=self.E)).to(self.dev)
         out = torch.empty((self.NL, H), dtype=torch.float32, device=self.dev)
+        cache.set_upload_stats(True)            # each upload's copy timed on its stream as well
+        u0 = cache.stats()
         for t in range(n):
             cache.decode_token(xs[t], out, bias=None if b2 is None else b2[t], stream=self.stream)
         torch.cuda.synchronize()
+        u1 = cache.stats()
+        cache.set_upload_stats(False)
+        self.upload_in_decode = {}
+        for kind in ("h2d", "d2d"):
+            nu = u1[f"n_upload_{kind}"] - u0[f"n_upload_{kind}"]
+            us = u1[f"upload_{kind}_us"] - u0[f"upload_{kind}_us"]
+            self.upload_in_decode[kind] = {"n": nu, "us_per_upload": round(us / nu, 1) if nu else None}
         kt = cache.kernel_times()
         cache.set_timing(False)
         log(f"[bench] per-kernel timing pass: {n} tokens")
         return kt, n
+
+    def batch_kernel_pass(self, cache, B, n_batches=4):
+        """Per-kernel durations of the batched decode: the batched tokens'
+        first n_batches batches decoded again on the same cache with timing on
+        (each layer's grouped launches waited for)."""
+        torch = self.torch
+        cache.set_timing(True)
+        out = torch.empty((self.NL, B, H), dtype=torch.float32, device=self.dev)
+        for i in range(n_batches):
+            t0 = self.T1 + B * i
+            if t0 + B > self.T:
+                break
+            xb = self.x[t0:t0 + B].transpose(0, 1).contiguous()
+            bb = None if self.bias is None else self.bias[t0:t0 + B].transpose(0, 1).contiguous()
+            cache.decode_batch(xb, out, bias=bb, stream=self.stream)
+        torch.cuda.synchronize()
+        kt = cache.kernel_times()
+        cache.set_timing(False)
+        log(f"[bench] batched per-kernel timing pass: {n_batches} batches of {B}")
+        return kt
 
     def decode_batches(self, cache, B, keep=()):
         """Tokens T1.. decoded B at a time with moe_decode_batch.  Returns
@@ -264,12 +321,14 @@ class Workload:
         log(f"[bench] timed {n} batched tokens in {elapsed:.3f}s")
         return elapsed, per, s0, s1, ids.transpose(0, 2, 1, 3).reshape(n, self.NL, K), kept
 
-    def check(self, ids_log, kept, frames, s1, knobs, every=False, batch=1, steer=True, T=None, heat=None):
+    def check(self, ids_log, kept, frames, s1, knobs, every=False, batch=1, steer=True, T=None, heat=None,
+              x_host=None):
         """Full-size properties against the oracle, outside every timed region:
         routed ids (every token and layer when `every` or a prior is on, else
         one layer per token), frames, counters, and the kept outputs.  Tokens
         from T1 on were decoded `batch` at a time: observed together, one step
-        per batch, no prior (it biases single-token selection only)."""
+        per batch, no prior (it biases single-token selection only).  x_host:
+        the layers' inputs [T][L][H] when they are not the workload's own."""
         import ctypes
         import numpy as np
         from oracle import oracle as O
@@ -279,7 +338,7 @@ class Workload:
                      cache_prior=knobs.get("cache_prior", 0.0))
         if heat:
             oc.heat_file(heat)
-        Wh, xh = self.W.cpu().numpy(), self.x.cpu().numpy()
+        Wh, xh = self.W.cpu().numpy(), self.x.cpu().numpy() if x_host is None else x_host
         bh = None if (self.bias is None or not steer) else self.bias.cpu().numpy()
         stores = [np.ctypeslib.as_array((ctypes.c_uint8 * (self.E * self.eb[l])).from_address(self.stores[l]))
                   for l in range(self.NL)]
@@ -377,6 +436,39 @@ class Workload:
         for p in self.stores:
             self.L.moe_host_free(p)
         self.stores = []
+
+
+def upload_cost(expert_bytes, n=300):
+    """One expert's upload, measured as experiments/e1_upload_cost.py measures
+    it ('pinned, dedicated stream': a pinned host buffer copied to HBM on a
+    stream of its own, synchronised per expert, n times), and the staged
+    device-to-device copy of the same bytes.  Host wall time per expert and the
+    copy's own duration from events on the stream."""
+    import torch
+    dev = torch.device("cuda:0")
+    src = torch.empty(expert_bytes, dtype=torch.uint8, pin_memory=True)
+    src.fill_(3)
+    dst = torch.empty(expert_bytes, dtype=torch.uint8, device=dev)
+    dst2 = torch.empty(expert_bytes, dtype=torch.uint8, device=dev)
+    s = torch.cuda.Stream()
+    out = {"expert_bytes": expert_bytes, "n": n}
+    for name, a, b in (("pinned_h2d", dst, src), ("staged_d2d", dst2, dst)):
+        evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(n)]
+        with torch.cuda.stream(s):
+            for _ in range(10):
+                a.copy_(b, non_blocking=True)
+            s.synchronize()
+            t0 = time.perf_counter()
+            for e0, e1 in evs:
+                e0.record(s)
+                a.copy_(b, non_blocking=True)
+                e1.record(s)
+                s.synchronize()
+            wall = (time.perf_counter() - t0) / n * 1e6
+        dev_us = sum(e0.elapsed_time(e1) for e0, e1 in evs) / n * 1e3
+        out[name] = {"us_wall": round(wall, 2), "us_copy": round(dev_us, 2),
+                     "gbs_copy": round(expert_bytes / (dev_us * 1e-6) / 1e9, 1)}
+    return out
 
 
 def size_matched(roof, iters=50):
@@ -591,6 +683,12 @@ def run_default(args):
                               "ids_equal": bool((ids2 == ids_log).all()),
                               "path": "absent experts read by the fused launch from the pinned store over PCIe "
                                       "(and staged, so their uploads are HBM copies)"}
+    up = upload_cost(max(wl.eb))
+    up["in_decode"] = wl.upload_in_decode
+    up["context"] = "reference: 85.8 us per 3.06 MB expert pinned on a dedicated stream, RTX 5070 PCIe"
+    result["uploads"] = up
+    if not args.no_per_layer:
+        result["per_layer"] = run_per_layer(args, wl, knobs, W, Kt, s_lo, T, ids_log)
     if not args.no_cpu:
         result["cpu_baseline"] = wl.cpu_baseline(args.cpu_seconds)
     if not args.no_extra:
@@ -602,6 +700,67 @@ def run_default(args):
         result["config4"] = config4(args)
         result["config5"] = config5(args)
     return result
+
+
+def run_per_layer(args, wl, knobs, W, Kt, s_lo, T, ids_tok):
+    """Configuration 2 decoded as a model drives the per-layer op
+    (moe_decode_layer per layer, x_{l+1} = x_l + out_l, observe, step): the
+    same windows as the token figures, the fused launch's time per layer from
+    a timing pass after the sequence, and the oracle's check of the whole
+    sequence (every layer's routing against the inputs the chain produced)."""
+    import numpy as np
+    torch = wl.torch
+    c = wl.cache(**knobs)
+    c.set_decode_path(split=args.path, graph=False)
+    sidecar_setup(args, c)
+    xin = torch.empty((T, wl.NL, H), dtype=torch.float32, device=wl.dev)
+    outs = torch.empty((T, wl.NL, H), dtype=torch.float32, device=wl.dev)
+    ids = np.empty((T, wl.NL, K), np.int32)
+    log("[bench] per-layer decode (moe_decode_layer, residual inputs)")
+    wl.tokens_per_layer(c, 0, W, ids, xin, outs)
+    a0 = c.stats()
+    el = wl.tokens_per_layer(c, W, W + Kt, ids, xin, outs)
+    a1 = c.stats()
+    if s_lo > W + Kt:
+        wl.tokens_per_layer(c, W + Kt, s_lo, ids, xin, outs)
+    b0 = c.stats()
+    el_s = wl.tokens_per_layer(c, s_lo, T, ids, xin, outs) if T > s_lo else 0.0
+    b1 = c.stats()
+    frames = [c.frame(l) for l in range(wl.NL)]
+    res = {"value": round(Kt / el, 2), "unit": "tok/s", "tokens": f"{W}..{W + Kt - 1}",
+           "hit_rate": window(a0, a1, Kt)["hit_rate"]}
+    if T > s_lo:
+        res["steady"] = {"tokens": f"{s_lo}..{T - 1}", "value": round((T - s_lo) / el_s, 2),
+                         "hit_rate": window(b0, b1, T - s_lo)["hit_rate"]}
+    if not args.no_check:
+        keep = {W, T - 1}
+        kept = {t: outs[t].cpu().numpy() for t in keep}
+        log("[bench] per-layer: checking every routed id and two tokens' outputs against the oracle")
+        chk = wl.check(ids, kept, frames, b1, knobs, every=True, x_host=xin.cpu().numpy())
+        res["check"] = compact_check(chk)
+    del xin, outs
+    # the fused launch's time per layer, a timing pass over the sequence's first tokens again
+    n = min(args.kernel_steps, 64)
+    c.set_timing(True)
+    xin = torch.empty((n, wl.NL, H), dtype=torch.float32, device=wl.dev)
+    outs = torch.empty((n, wl.NL, H), dtype=torch.float32, device=wl.dev)
+    wl.tokens_per_layer(c, 0, n, np.empty((n, wl.NL, K), np.int32), xin, outs)
+    kt = c.kernel_times()
+    c.close()
+    res["fused_us"] = round(kt["layer_ms"] / max(kt["n_layers"], 1) * 1e3, 2)
+    res["fused_gbs"] = round(kt["layer_hbm_bytes"] / max(kt["layer_ms"] * 1e-3, 1e-12) / 1e9, 1)
+    log(f"[bench] per-layer: {res}")
+    return res
+
+
+def compact_check(c):
+    """A check result in a few characters: ids checked/mismatched, frames and
+    counters equal, outputs checked and the worst relative L2."""
+    out = {"ids": f"{c.get('ids_checked', 0)}/{c.get('ids_mismatched', 0)}",
+           "outputs": f"{c.get('outputs_checked', 0)}, worst rel-L2 {c.get('worst_rel_l2', 0.0):.2g}"}
+    if "frames_equal" in c:
+        out["frames_counters_equal"] = bool(c["frames_equal"] and c.get("counters_equal", True))
+    return out
 
 
 def _sub(args, **kw):
@@ -941,7 +1100,11 @@ def run_wide(args, wl):
             "cpu_pairs_per_token": round((s3["n_cpu_served"] - s2["n_cpu_served"]) / n_b, 2),
             "host_wait_ms_per_batch": round((s3["sidecar_wait_us"] - s2["sidecar_wait_us"]) / 1e3 / nb_, 3),
             "host_cpu_ms_per_batch": round((s3["sidecar_cpu_us"] - s2["sidecar_cpu_us"]) / 1e3 / nb_, 3)}
-    result.update(kernel_report(*wl.kernel_pass(cache), args.steps, s0, s1))
+    result[f"batch{B}"]["kernels"] = grouped_report(wl.batch_kernel_pass(cache, B), wl.I)
+    # the batch-1 launches as the timed decode ran them (the fused launch, the
+    # host serving its share of the absent experts)
+    kt, n_kt = wl.kernel_pass(cache, split=args.path, keep_serving=args.sidecar > 0)
+    result.update(fused_report(kt, n_kt) if args.path == 0 else kernel_report(kt, n_kt, args.steps, s0, s1))
     result["roofline"]["size_matched"] = size_matched(result["roofline"])
     if not args.no_check:
         log("[bench] replaying every routed id of both phases through the oracle (outside the timed region)")
@@ -952,6 +1115,25 @@ def run_wide(args, wl):
 
 
 MFMA_PEAK_TFLOPS = 2500.0   # dense fp16/bf16
+
+
+def grouped_report(kt, inter):
+    """GB/s and matrix-core utilisation of the batched decode's grouped
+    launches: weights read once per expert with pairs on the GPU (slots in HBM,
+    or the pinned store over PCIe), useful FLOPs 2 x pairs x (2 I H) up/gate and
+    2 x pairs x I H down."""
+    n = max(kt["grouped_launches"], 1)
+    out = {"launches": kt["grouped_launches"], "pairs_per_launch": round(kt["grouped_pairs"] / n, 1)}
+    for part, ms, hb, pb, fl in (("gateup", kt["grouped_gateup_ms"], kt["grouped_gateup_hbm_bytes"],
+                                  kt["grouped_gateup_host_bytes"], 4 * inter * H),
+                                 ("down", kt["grouped_down_ms"], kt["grouped_down_hbm_bytes"],
+                                  kt["grouped_down_host_bytes"], 2 * inter * H)):
+        sec = max(ms * 1e-3, 1e-12)
+        tfl = fl * kt["grouped_pairs"] / sec / 1e12
+        out[part] = {"us": round(ms / n * 1e3, 2), "hbm_mb": round(hb / n / 1e6, 2), "pcie_mb": round(pb / n / 1e6, 2),
+                     "gbs": round((hb + pb) / sec / 1e9, 1), "hbm_frac": round((hb + pb) / sec / 1e9 / HBM_PEAK_GBS, 4),
+                     "tflops": round(tfl, 2), "mfma_util": round(tfl / MFMA_PEAK_TFLOPS, 4)}
+    return out
 
 
 def run_prefill(args):
@@ -1154,6 +1336,7 @@ def parse_args(argv=None):
                     help="end with a plain 256 MiB device copy (scale for rocprofv3 FETCH_SIZE/WRITE_SIZE)")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-gpu-only", action="store_true", help="skip the GPU-only decode beside the default one")
+    ap.add_argument("--no-per-layer", action="store_true", help="skip the decode through the per-layer op")
     ap.add_argument("--no-check", action="store_true")
     ap.add_argument("--no-extra", action="store_true", help="stacked48: only configuration 2 (no config1/3/4/5)")
     ap.add_argument("--no-lookahead", action="store_true", help="residual48: skip the streaming-off comparison")
@@ -1175,6 +1358,38 @@ def parse_args(argv=None):
     if args.batch is None:
         args.batch = 16 if wide else 512
     return args
+
+
+# long descriptions go to stderr; the one stdout line keeps every figure and
+# stays short enough for a log tail of ~10 KB
+_DROP = {"what", "path", "engine", "kernel_timing", "flops", "ms_per_batch", "sweep"}
+
+
+def compact(v, key=None):
+    """The result without its long descriptive strings: checks as short
+    summaries, the CPU sweep as [threads, experts per call, p50 us] rows,
+    workload texts cut at 160 characters."""
+    if isinstance(v, dict):
+        if "ids_checked" in v:
+            return compact_check(v)
+        out = {}
+        for k, x in v.items():
+            if k in _DROP:
+                continue
+            if k == "bytes" and isinstance(x, str):
+                continue
+            if k == "traffic_source" and isinstance(x, str):
+                out[k] = "pmc" if x.startswith("pmc") else "PMC ratio of profiles/traffic.json x bytes"
+                continue
+            out[k] = compact(x, k)
+        if key == "cpu_baseline" and "sweep" in v:
+            out["sweep_thr_experts_p50us"] = [[r["threads"], r["experts_per_call"], r["us_p50"]] for r in v["sweep"]]
+        return out
+    if isinstance(v, str) and key in ("workload", "sample") and len(v) > 160:
+        return v[:157] + "..."
+    if isinstance(v, list):
+        return [compact(x) for x in v]
+    return v
 
 
 def main():
@@ -1219,7 +1434,8 @@ def main():
             dst = src.clone()
         torch.cuda.synchronize()
         del src, dst
-    print(json.dumps(result), flush=True)
+    log("[bench] full result: " + json.dumps(result))
+    print(json.dumps(compact(result)), flush=True)
 
 
 if __name__ == "__main__":

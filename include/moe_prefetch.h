@@ -222,6 +222,12 @@ typedef struct {
     double host_boundary_us;                     /* batch-1 decode: host time after the token's GPU work
                                                     (observe, step, table flush) before it returns */
     uint64_t n_evicted;                          /* resident experts evicted by the steps for uploads */
+    /* with moe_cache_set_upload_stats: finished uploads from the pinned store
+     * (host to device) and from the staging area (device to device), and the
+     * sum of their copies' durations on the upload streams (events recorded
+     * around each copy) */
+    uint64_t n_upload_h2d, n_upload_d2d;
+    double upload_h2d_us, upload_d2d_us;
 } moe_cache_stats;
 
 typedef struct {
@@ -253,6 +259,10 @@ int moe_cache_requires_sync(const moe_cache *c);
 int moe_cache_frame(moe_cache *c, int layer, int32_t *out);   /* out[slot] = expert or -1 */
 int moe_cache_table(moe_cache *c, int layer, int32_t *tbl, float *prior);  /* host mirrors */
 int moe_cache_stats_get(moe_cache *c, moe_cache_stats *out);
+/* Per-upload timing (LLAMA_MOE_UPLOAD_STATS, patches/0006:689-703), off by
+ * default: each upload's copy is bracketed by two events on its stream, read
+ * when the step publishes it (the n_upload_* / upload_*_us statistics). */
+int moe_cache_set_upload_stats(moe_cache *c, int on);
 int moe_cache_sync(moe_cache *c);  /* wait for every upload in flight */
 /* Heat file, LLAMA_MOE_HEAT_FILE (patches/0007:431-485 load/save, 568-621 warm
  * start, 745-752 periodic save): from now on every observed id is counted and
@@ -456,6 +466,13 @@ typedef struct {
     double layer_ms;                       /* split 0: the fused layer launch */
     uint64_t layer_hbm_bytes;              /* its router rows + resident (and shared) experts' bytes */
     uint64_t layer_host_bytes;             /* its absent experts' bytes read from the pinned store */
+    /* moe_decode_batch: the grouped up/gate and down launches of the routed
+     * experts (each layer's launches waited for: timing mode serialises the
+     * host's share behind them); weights by source, one read per expert with
+     * pairs on the GPU; pairs the GPU computed */
+    double grouped_gateup_ms, grouped_down_ms;
+    uint64_t grouped_launches, grouped_pairs;
+    uint64_t grouped_gateup_hbm_bytes, grouped_down_hbm_bytes, grouped_gateup_host_bytes, grouped_down_host_bytes;
 } moe_kernel_times;
 int moe_cache_set_timing(moe_cache *c, int on);
 /* split: 0 (default) the fused layer -- router GEMV, selection, every routed
@@ -487,6 +504,17 @@ int moe_cache_set_staging(moe_cache *c, int on);
  * order.  Outputs, ids and cache traces are identical to the GPU-only path.
  * Needs split 0 or 3.  n_threads <= 0 turns it off. */
 int moe_cache_set_sidecar(moe_cache *c, int n_threads, int num, int den);
+/* The serving channel's self-test (the reference's sidecar self-test before it
+ * enables the sidecar, patches/0009:436-472, 914-925), over the exchange the
+ * decode uses: in each of n_rounds a kernel posts a seeded pattern as tagged
+ * words, the calling thread checks them and writes a row pattern back and
+ * answers, the kernel checks the rows.  Every wait on either side is bounded by
+ * timeout_s.  withhold_from >= 0: the host stops answering from that round on
+ * (the kernel's bounded wait then ends it; for tests).  *n_bad receives the
+ * failed exchanges; MOE_ERR_HIP when any failed.  moe_cache_set_sidecar runs
+ * 10000 rounds the first time it is turned on and refuses, loudly, on a
+ * failure (serving stays GPU-only). */
+int moe_cache_sidecar_selftest(moe_cache *c, int n_rounds, int withhold_from, double timeout_s, int *n_bad);
 /* CPU-assisted serving in moe_decode_batch (no counterpart in the reference,
  * whose sidecar serves one token, P9:841-912): per layer the routing comes
  * back to the host, which computes the pairs of the absent experts whose rank
@@ -589,11 +617,15 @@ int moe_grouped_experts_static(const moe_grouped_desc *d, void *stream);
 int moe_combine(const float *pair_rows, int n_tok, int K, int H, float *out, int accumulate, void *stream);
 
 /* One decode step of n_tok tokens (batch > 1) over every layer: x dev [L][n_tok][H],
- * bias dev [L][n_tok][E] or NULL, out dev [L][n_tok][H].  Per layer: route (with the
- * cache prior), dispatch, the grouped experts from HBM slots or the pinned store,
- * and the shared expert; then the routed ids come back in one copy, each layer
- * observes them token-major and the cache steps.  ids_host [L][n_tok][K] receives
- * them when not NULL.  n_tok <= 4096. */
+ * bias dev [L][n_tok][E] or NULL, out dev [L][n_tok][H].  Per layer: route (the
+ * cache prior biases single-token selection only, so it applies when n_tok is 1,
+ * patches/0007:114), dispatch, the grouped experts from HBM slots or the pinned
+ * store, and the shared expert; then the routed ids come back in one copy, each
+ * layer observes them token-major and the cache steps.  ids_host [L][n_tok][K]
+ * receives them when not NULL.  n_tok <= 4096.  With CPU-assisted serving on, the
+ * host computes its share of the absent experts when the share is not empty and
+ * n_tok <= MOE_BATCH_HOST_MAX_TOKENS; larger batches run on the GPU alone. */
+#define MOE_BATCH_HOST_MAX_TOKENS 64
 int moe_decode_batch(moe_cache *c, const float *x, const float *bias, float *out, int n_tok, int32_t *ids_host,
                      void *stream);
 

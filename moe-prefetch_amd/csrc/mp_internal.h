@@ -152,6 +152,30 @@ struct JoinArgs {
     float *out;               // dev [H]
 };
 
+// Self-test of the CPU-assisted serving channel, over the words the decode
+// uses (one layer's post, answer and rows): in round r the kernel posts every
+// logit word and every Q8_K(x) word of the post as (seq0 + r) << 32 | a seeded
+// pattern, waits (bounded by the 100 MHz wall clock) for the host's answer,
+// then checks the H rows the host wrote.  A timeout ends the kernel: the
+// rounds left count as failed.
+struct ScSelfTestArgs {
+    SidecarPost *post;        // mapped host
+    const SidecarResp *resp;  // mapped host
+    const float *rows;        // mapped host [H]
+    int n_rounds, E, n_q8_words, H;
+    uint32_t seq0;
+    uint64_t timeout_ticks;
+    uint32_t *bad;            // dev: failed exchanges (zeroed by the caller)
+};
+// the seeded words of round r (splitmix64 finaliser of (round, index, stream))
+__host__ __device__ inline uint32_t sc_test_word(uint32_t r, uint32_t i, uint32_t stream) {
+    uint64_t z = ((uint64_t)r << 32 | i) + 0x9e3779b97f4a7c15ull * (stream + 1);
+    z = (z ^ (z >> 30)) * 0xbf58476d1ce4e5b9ull;
+    z = (z ^ (z >> 27)) * 0x94d049bb133111ebull;
+    return (uint32_t)(z ^ (z >> 31));
+}
+hipError_t launch_sc_selftest(const ScSelfTestArgs &a, hipStream_t st);
+
 // A batch-1 decode layer in one launch: the router GEMV, the selection, every
 // routed expert's gate/up rows, its down rows and the weighted combine.
 // Inside the launch the phases pass tagged 8-byte words, (token sequence

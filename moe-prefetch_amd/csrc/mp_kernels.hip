@@ -1524,6 +1524,52 @@ __global__ __launch_bounds__(256) void join_kernel(JoinArgs a) {
     a.out[r] = acc;
 }
 
+// the serving channel's self-test: one workgroup, rounds in order
+__global__ __launch_bounds__(256) void sc_selftest_kernel(ScSelfTestArgs a) {
+    __shared__ int s_ok;
+    for (int r = 0; r < a.n_rounds; ++r) {
+        const uint32_t seq = a.seq0 + (uint32_t)r;
+        const uint64_t tag = (uint64_t)seq << 32;
+        for (int i = threadIdx.x; i < a.E; i += blockDim.x)
+            __hip_atomic_store(&a.post->logit[i], tag | sc_test_word(seq, i, 0), __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_SYSTEM);
+        for (int i = threadIdx.x; i < a.n_q8_words; i += blockDim.x)
+            __hip_atomic_store(&a.post->q8x_words[i], tag | sc_test_word(seq, i, 1), __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_SYSTEM);
+        if (threadIdx.x == 0) {
+            const uint64_t t0 = wall_clock64();
+            int ok = 1;
+            while (__hip_atomic_load(&a.resp->seq, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM) != seq) {
+                if (wall_clock64() - t0 > a.timeout_ticks) {
+                    ok = 0;
+                    break;
+                }
+                __builtin_amdgcn_s_sleep(2);
+            }
+            if (ok) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "");     // system scope
+            s_ok = ok;
+        }
+        __syncthreads();
+        if (!s_ok) {
+            if (threadIdx.x == 0)
+                __hip_atomic_fetch_add(a.bad, (uint32_t)(a.n_rounds - r), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            return;
+        }
+        int wrong = 0;
+        for (int i = threadIdx.x; i < a.H; i += blockDim.x) {
+            const float v = __hip_atomic_load(a.rows + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+            wrong |= __float_as_uint(v) != (sc_test_word(seq, i, 2) & 0x3fffffffu);
+        }
+        wrong = __syncthreads_or(wrong);
+        if (wrong && threadIdx.x == 0) __hip_atomic_fetch_add(a.bad, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+}
+
+hipError_t launch_sc_selftest(const ScSelfTestArgs &a, hipStream_t st) {
+    hipLaunchKernelGGL(sc_selftest_kernel, dim3(1), dim3(256), 0, st, a);
+    return hipGetLastError();
+}
+
 hipError_t launch_join(const JoinArgs &a, hipStream_t st) {
     hipLaunchKernelGGL(join_kernel, dim3((unsigned)((a.H + 255) / 256)), dim3(256), 0, st, a);
     return hipGetLastError();

@@ -94,6 +94,8 @@ struct Job {
     int li, expert, slot;
     hipEvent_t ev;     // live mode only
     bool spec;         // issued from a prediction, not a miss (patches/0007:168)
+    hipEvent_t t0 = nullptr, t1 = nullptr;   // upload statistics: around the copy on its stream
+    bool staged = false;                     // a device-to-device copy from the staging area
 };
 
 // Just-in-time streaming (LLAMA_MOE_STREAM; state as in patches/0010:957-1021).
@@ -232,9 +234,16 @@ struct moe_cache {
     std::vector<hipStream_t> pl_streams;        // streams the calls ran on
     bool pl_synced = false;                     // those streams were synchronised since the last call
     bool pl_hot = false;                        // the host team spins between layers
+    bool sc_tested = false;                     // the serving channel passed its self-test
     uint64_t clock = 0, n_steps = 0, n_uploads = 0, n_scheduled = 0, n_copied = 0, n_published = 0;
     uint64_t n_admit_ok = 0, n_admit_denied = 0, n_table_flushes = 0, bytes_uploaded = 0;
     uint64_t n_evicted = 0;            // resident experts the step evicted for an upload
+    // upload statistics (LLAMA_MOE_UPLOAD_STATS, patches/0006:689-703): each
+    // copy's own duration on its stream, from events recorded around it
+    bool up_stats = false;
+    std::vector<hipEvent_t> tfree;     // timing events, reused
+    uint64_t n_up_h2d = 0, n_up_d2d = 0;
+    double up_h2d_us = 0.0, up_d2d_us = 0.0;
     double wait_us = 0.0;
     double boundary_us = 0.0;          // batch-1 decode: host time from the token's sync to the return
     FILE *route = nullptr, *map = nullptr;
@@ -383,6 +392,18 @@ int start_upload(moe_cache *c, int li, int expert, int slot, bool spec = false) 
             if (ls.staged[k] == expert) staged = c->stage + ((size_t)li * c->K + k) * c->stage_stride;
     uint8_t *dst = ls.pool + (size_t)slot * ls.slot_bytes;
     hipStream_t s = staged ? c->stg_stream : c->up_stream;
+    j.staged = staged != nullptr;
+    if (c->up_stats) {
+        for (hipEvent_t *e : {&j.t0, &j.t1}) {
+            if (!c->tfree.empty()) {
+                *e = c->tfree.back();
+                c->tfree.pop_back();
+            } else if (hipEventCreate(e) != hipSuccess) {
+                return fail(MOE_ERR_HIP, "event creation failed");
+            }
+        }
+        HIPCHK(hipEventRecord(j.t0, s));
+    }
     if (staged) {
         HIPCHK(hipMemcpyAsync(dst, staged, ls.expert_bytes, hipMemcpyDeviceToDevice, s));
         c->stg_pending = true;
@@ -391,6 +412,7 @@ int start_upload(moe_cache *c, int li, int expert, int slot, bool spec = false) 
         HIPCHK(hipMemcpyAsync(dst, ls.store_host + (size_t)expert * ls.expert_bytes, ls.expert_bytes,
                               hipMemcpyHostToDevice, s));
     }
+    if (j.t1) HIPCHK(hipEventRecord(j.t1, s));
     if (c->cfg.publish == MOE_PUBLISH_LIVE) {
         j.ev = take_event(c);
         if (!j.ev) return fail(MOE_ERR_HIP, "event creation failed");
@@ -975,7 +997,18 @@ int cache_step(moe_cache *c) {
                 });
         }
         c->n_copied += done.size();
-        for (const Job &j : done) publish(c, j);
+        for (Job &j : done) {
+            if (j.t0) {             // the copy is done: its events have completed
+                float ms = 0.0f;
+                HIPCHK(hipEventElapsedTime(&ms, j.t0, j.t1));
+                (j.staged ? c->n_up_d2d : c->n_up_h2d)++;
+                (j.staged ? c->up_d2d_us : c->up_h2d_us) += 1e3 * ms;
+                c->tfree.push_back(j.t0);
+                c->tfree.push_back(j.t1);
+                j.t0 = j.t1 = nullptr;
+            }
+            publish(c, j);
+        }
     }
     if (c->st) stream_adopt(c);         // after the uploads: an expert both copied is kept once
 
@@ -1282,8 +1315,10 @@ void free_cache(moe_cache *c) {
     if (c->up_stream) hipStreamSynchronize(c->up_stream);
     if (c->stg_stream) hipStreamSynchronize(c->stg_stream);
     for (Job &j : c->jobs)
-        if (j.ev) hipEventDestroy(j.ev);
+        for (hipEvent_t e : {j.ev, j.t0, j.t1})
+            if (e) hipEventDestroy(e);
     for (hipEvent_t e : c->free_events) hipEventDestroy(e);
+    for (hipEvent_t e : c->tfree) hipEventDestroy(e);
     if (c->up_mark) hipEventDestroy(c->up_mark);
     for (hipEvent_t e : {c->ev_route, c->ev_hbm, c->ev_host, c->ev_user, c->ev_done})
         if (e) hipEventDestroy(e);
@@ -2383,6 +2418,16 @@ int moe_cache_stats_get(moe_cache *c, moe_cache_stats *s) {
     s->publication_wait_us = c->wait_us;
     s->host_boundary_us = c->boundary_us;
     s->n_evicted = c->n_evicted;
+    s->n_upload_h2d = c->n_up_h2d;
+    s->n_upload_d2d = c->n_up_d2d;
+    s->upload_h2d_us = c->up_h2d_us;
+    s->upload_d2d_us = c->up_d2d_us;
+    return MOE_OK;
+}
+
+int moe_cache_set_upload_stats(moe_cache *c, int on) {
+    if (!c) return fail(MOE_ERR_ARG, "null cache");
+    c->up_stats = on != 0 && !c->host_only;
     return MOE_OK;
 }
 
@@ -2395,6 +2440,9 @@ int moe_cache_set_decode_path(moe_cache *c, int split, int graph) {
     c->graph = graph != 0;
     return MOE_OK;
 }
+
+static int sc_buffers(moe_cache *c);
+static bool logits_ready(const mp::SidecarPost &p, int E, int n_q8_words, uint32_t seq, int &n_lg, int &n_q8);
 
 int moe_cache_set_sidecar(moe_cache *c, int n_threads, int num, int den) {
     if (!c) return fail(MOE_ERR_ARG, "null cache");
@@ -2409,6 +2457,43 @@ int moe_cache_set_sidecar(moe_cache *c, int n_threads, int num, int den) {
         return fail(MOE_ERR_STATE, "CPU-assisted serving runs with one expert launch (split 0 or 3)");
     if (c->K > 16 || (c->H / 256) * mp::Q8K_BYTES > mp::SC_Q8X_BYTES) return fail(MOE_ERR_ARG, "shape too large");
     HIPCHK(hipSetDevice(c->cfg.device));
+    int r = sc_buffers(c);
+    if (r != MOE_OK) return r;
+    // the channel is tested before it serves (patches/0009:914-925): 10000
+    // bounded round trips of a seeded pattern; a failure leaves GPU-only serving
+    if (!c->sc_tested) {
+        int bad = 0;
+        r = moe_cache_sidecar_selftest(c, 10000, -1, c->sc_timeout_s, &bad);
+        if (r != MOE_OK) {
+            fprintf(stderr, "moe-cache: CPU-assisted serving DISABLED (channel self-test: %d of 10000 exchanges "
+                            "failed)\n", bad);
+            c->sc_den = c->sc_num = 0;
+            return fail(MOE_ERR_HIP, "CPU-assisted serving disabled: channel self-test failed (%d of 10000)", bad);
+        }
+        c->sc_tested = true;
+    }
+    if (c->team && mpc::team_size(c->team) != n_threads) {
+        mpc::team_destroy(c->team);
+        c->team = nullptr;
+    }
+    if (!c->team) c->team = mpc::team_create(n_threads);
+    c->sc_h.resize((size_t)c->K * c->I);
+    c->sc_y.resize((size_t)c->K * c->H);
+    c->sc_q8h.resize((size_t)c->K * (c->I / 256) * mp::Q8K_BYTES);
+    c->sc_q8x.resize((size_t)(c->H / 256) * mp::Q8K_BYTES);
+    c->sc_ids.assign((size_t)c->cfg.n_layers * c->K, -1);
+    // the CPU reads the stores from now on: fault their pages in here, not
+    // expert by expert in the middle of a token
+    for (const Layer &ls : c->L)
+        if (ls.store_host) mpc::prefault(c->team, ls.store_host, (size_t)ls.E * ls.expert_bytes);
+    c->sc_num = num;
+    c->sc_den = den;
+    drop_graphs(c);
+    return MOE_OK;
+}
+
+// the exchange blocks of CPU-assisted serving (mapped, coherent host memory)
+static int sc_buffers(moe_cache *c) {
     const size_t NL = c->L.size();
     const unsigned fl = hipHostMallocMapped | hipHostMallocCoherent;
     if (!c->sc_post) {
@@ -2429,23 +2514,89 @@ int moe_cache_set_sidecar(moe_cache *c, int n_threads, int num, int den) {
         HIPCHK(hipHostGetDevicePointer((void **)&c->sc_resp_d, c->sc_resp, 0));
         HIPCHK(hipHostGetDevicePointer((void **)&c->sc_rows_d, c->sc_rows, 0));
     }
-    if (c->team && mpc::team_size(c->team) != n_threads) {
-        mpc::team_destroy(c->team);
-        c->team = nullptr;
+    return MOE_OK;
+}
+
+int moe_cache_sidecar_selftest(moe_cache *c, int n_rounds, int withhold_from, double timeout_s, int *n_bad) {
+    if (n_bad) *n_bad = 0;
+    if (!c || n_rounds < 1 || timeout_s <= 0.0) return fail(MOE_ERR_ARG, "bad arguments");
+    if (c->host_only) return fail(MOE_ERR_STATE, "host-only cache has no GPU to exchange with");
+    HIPCHK(hipSetDevice(c->cfg.device));
+    int r = sc_buffers(c);
+    if (r != MOE_OK) return r;
+    // layer 0's post, answer and rows; the sequence numbers continue the
+    // decode's, so no later token can mistake a test word for its own
+    mp::SidecarPost &post = c->sc_post[0];
+    mp::SidecarResp &resp = c->sc_resp[0];
+    const int E = mp::SC_MAX_E, nq = mp::SC_Q8X_BYTES / 4, H = c->H;
+    uint32_t seq0 = c->sc_seq + 1;
+    if (seq0 == 0 || seq0 == mp::SC_ABORT || seq0 + (uint32_t)n_rounds < seq0 ||
+        seq0 + (uint32_t)n_rounds >= mp::SC_ABORT)
+        seq0 = 1;
+    c->sc_seq = seq0 + (uint32_t)n_rounds - 1;
+    *(volatile uint32_t *)&resp.seq = 0;
+    uint32_t *bad_d = nullptr;
+    uint32_t bad_h = 0;
+    HIPCHK(hipMalloc((void **)&bad_d, 4));
+    hipStream_t st = c->host_stream;
+    mp::ScSelfTestArgs a{};
+    a.post = c->sc_post_d;
+    a.resp = c->sc_resp_d;
+    a.rows = c->sc_rows_d;
+    a.n_rounds = n_rounds;
+    a.E = E;
+    a.n_q8_words = nq;
+    a.H = H;
+    a.seq0 = seq0;
+    a.timeout_ticks = (uint64_t)(timeout_s * 1e8);
+    a.bad = bad_d;
+    int host_bad = 0;
+    hipError_t e = hipMemsetAsync(bad_d, 0, 4, st);
+    if (e == hipSuccess) e = mp::launch_sc_selftest(a, st);
+    if (e == hipSuccess) {
+        for (int k = 0; k < n_rounds; ++k) {
+            if (withhold_from >= 0 && k >= withhold_from) {     // the kernel's own bound ends the rest
+                host_bad += n_rounds - k;
+                break;
+            }
+            const uint32_t seq = seq0 + (uint32_t)k;
+            const auto t0 = std::chrono::steady_clock::now();
+            int n_lg = 0, n_q8 = 0;
+            bool late = false;
+            unsigned spins = 0;
+            while (!logits_ready(post, E, nq, seq, n_lg, n_q8)) {
+                _mm_pause();
+                if ((++spins & 1023u) == 0 &&
+                    std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count() > timeout_s) {
+                    late = true;
+                    break;
+                }
+            }
+            if (late) {         // no answer: the kernel's bounded wait ends it
+                host_bad += n_rounds - k;
+                break;
+            }
+            std::atomic_thread_fence(std::memory_order_acquire);
+            bool wrong = false;
+            for (int i = 0; i < E; ++i) wrong |= (uint32_t)post.logit[i] != mp::sc_test_word(seq, i, 0);
+            for (int i = 0; i < nq; ++i) wrong |= (uint32_t)post.q8x_words[i] != mp::sc_test_word(seq, i, 1);
+            host_bad += wrong;
+            for (int i = 0; i < H; ++i) {
+                const uint32_t b = mp::sc_test_word(seq, i, 2) & 0x3fffffffu;
+                memcpy(&c->sc_rows[i], &b, 4);
+            }
+            std::atomic_thread_fence(std::memory_order_release);
+            *(volatile uint32_t *)&resp.seq = seq;
+        }
+        e = hipStreamSynchronize(st);
     }
-    if (!c->team) c->team = mpc::team_create(n_threads);
-    c->sc_h.resize((size_t)c->K * c->I);
-    c->sc_y.resize((size_t)c->K * c->H);
-    c->sc_q8h.resize((size_t)c->K * (c->I / 256) * mp::Q8K_BYTES);
-    c->sc_q8x.resize((size_t)(c->H / 256) * mp::Q8K_BYTES);
-    c->sc_ids.assign((size_t)c->cfg.n_layers * c->K, -1);
-    // the CPU reads the stores from now on: fault their pages in here, not
-    // expert by expert in the middle of a token
-    for (const Layer &ls : c->L)
-        if (ls.store_host) mpc::prefault(c->team, ls.store_host, (size_t)ls.E * ls.expert_bytes);
-    c->sc_num = num;
-    c->sc_den = den;
-    drop_graphs(c);
+    if (e == hipSuccess) e = hipMemcpy(&bad_h, bad_d, 4, hipMemcpyDeviceToHost);
+    hipFree(bad_d);
+    *(volatile uint32_t *)&resp.seq = 0;
+    if (e != hipSuccess) return fail(MOE_ERR_HIP, "channel self-test: %s", hipGetErrorString(e));
+    const int bad = std::max(host_bad, (int)bad_h);
+    if (n_bad) *n_bad = bad;
+    if (bad) return fail(MOE_ERR_HIP, "channel self-test: %d of %d exchanges failed", bad, n_rounds);
     return MOE_OK;
 }
 
@@ -3432,8 +3583,12 @@ int moe_decode_batch(moe_cache *c, const float *x, const float *bias, float *out
     if (r != MOE_OK) return r;
     const hipStream_t st = (hipStream_t)stream;
     const int NL = (int)c->L.size(), TK = n_tok * c->K;
-    const bool sc = c->sc_den > 0;
+    // the host's share applies to decode-sized batches; a prefill-sized batch
+    // would serialise every layer on the CPU and pin 2 n_tok K H floats
+    const int sh_num = c->sb_den ? c->sb_num : c->sc_num, sh_den = c->sb_den ? c->sb_den : c->sc_den;
+    const bool sc = c->sc_den > 0 && sh_num > 0 && n_tok <= MOE_BATCH_HOST_MAX_TOKENS;
     if (sc && (r = batch_sidecar_buffers(c, n_tok)) != MOE_OK) return r;
+    float gms[2] = {0.0f, 0.0f};
     if (sc) mpc::team_hot(c->team, true);
     struct Cold {
         moe_cache *c;
@@ -3473,6 +3628,7 @@ int moe_decode_batch(moe_cache *c, const float *x, const float *bias, float *out
         gd.store = ls.store_dev; gd.expert_bytes = ls.expert_bytes; gd.n_store = c->E;
         gd.out = out + (size_t)l * n_tok * c->H; gd.accumulate = 0;
         gd.workspace = c->b_ws; gd.shared = ls.shared;
+        gd.kernel_ms = c->timing ? gms : nullptr;
         if (!sc) {
             if ((r = moe_grouped_experts(&gd, stream)) != MOE_OK) return r;
         } else {
@@ -3480,9 +3636,35 @@ int moe_decode_batch(moe_cache *c, const float *x, const float *bias, float *out
             if (!ls.store_host) return fail(MOE_ERR_STATE, "layer %d: CPU-assisted serving needs the host store", l);
             if ((r = batch_sidecar_layer(c, l, n_tok, &gd, st)) != MOE_OK) return r;
         }
+        if (c->timing) {
+            c->kt.grouped_gateup_ms += gms[0];
+            c->kt.grouped_down_ms += gms[1];
+            c->kt.grouped_launches++;
+        }
     }
     HIPCHK(hipMemcpyAsync(c->bh_ids, c->b_ids, (size_t)NL * TK * 4, hipMemcpyDeviceToHost, st));
     HIPCHK(hipStreamSynchronize(st));
+    if (c->timing)          // the weights the grouped launches read: each GPU expert's once, by source
+        for (int l = 0; l < NL; ++l) {
+            const Layer &ls = c->L[l];
+            const int32_t *ids = c->bh_ids + (size_t)l * TK;
+            std::vector<uint8_t> used((size_t)c->E, 0);
+            for (int i = 0; i < TK; ++i)
+                if (ids[i] >= 0 && ids[i] < ls.E) used[(size_t)ids[i]] = 1;
+            const uint64_t gu_b = 2ull * c->I * (c->H / 256) * mp::Q4K_BYTES, dn_b = ls.expert_bytes - gu_b;
+            std::vector<uint8_t> host((size_t)c->E, 0);
+            for (int e = 0, rk = 0; e < c->E; ++e) {        // the host's experts: batch_sidecar_layer's rule
+                const int slot = c->h_tbl[(size_t)l * c->E + e];
+                const bool absent = used[(size_t)e] && !(slot >= 0 && slot < ls.S);
+                host[(size_t)e] = sc && absent && rk % sh_den < sh_num;
+                rk += absent;
+                if (!used[(size_t)e] || host[(size_t)e]) continue;
+                const bool res = slot >= 0 && slot < ls.S;
+                (res ? c->kt.grouped_gateup_hbm_bytes : c->kt.grouped_gateup_host_bytes) += gu_b;
+                (res ? c->kt.grouped_down_hbm_bytes : c->kt.grouped_down_host_bytes) += dn_b;
+            }
+            for (int i = 0; i < TK; ++i) c->kt.grouped_pairs += ids[i] >= 0 && ids[i] < ls.E && !host[(size_t)ids[i]];
+        }
     for (int l = 0; l < NL; ++l) {
         if ((r = cache_observe(c, l, c->bh_ids + (size_t)l * TK, c->K, n_tok)) != MOE_OK) return r;
     }

@@ -10,6 +10,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libmoeprefetch.so")
 
 MOE_OK = 0
+MOE_ERR_ARG, MOE_ERR_HIP, MOE_ERR_NOMEM, MOE_ERR_STATE = -1, -2, -3, -4
 TYPE_Q4K, TYPE_Q6K = 12, 14
 DTYPE_F32, DTYPE_BF16 = 0, 1
 # the static workspace of moe_grouped_experts_static (MOE_GROUPED_STATIC_SCRATCH_BYTES)
@@ -68,7 +69,8 @@ class CacheStats(ctypes.Structure):
                [("publication_wait_us", ctypes.c_double), ("n_staged", ctypes.c_uint64),
                 ("n_cpu_served", ctypes.c_uint64), ("sidecar_wait_us", ctypes.c_double),
                 ("sidecar_cpu_us", ctypes.c_double), ("host_boundary_us", ctypes.c_double),
-                ("n_evicted", ctypes.c_uint64)]
+                ("n_evicted", ctypes.c_uint64), ("n_upload_h2d", ctypes.c_uint64), ("n_upload_d2d", ctypes.c_uint64),
+                ("upload_h2d_us", ctypes.c_double), ("upload_d2d_us", ctypes.c_double)]
 
 
 class LayerView(ctypes.Structure):
@@ -82,7 +84,10 @@ class KernelTimes(ctypes.Structure):
                                                "down_host_ms")] + \
                [(n, U64) for n in ("n_layers", "gateup_hbm_bytes", "down_hbm_bytes", "gateup_host_bytes",
                                    "down_host_bytes")] + \
-               [("layer_ms", ctypes.c_double), ("layer_hbm_bytes", U64), ("layer_host_bytes", U64)]
+               [("layer_ms", ctypes.c_double), ("layer_hbm_bytes", U64), ("layer_host_bytes", U64)] + \
+               [(n, ctypes.c_double) for n in ("grouped_gateup_ms", "grouped_down_ms")] + \
+               [(n, U64) for n in ("grouped_launches", "grouped_pairs", "grouped_gateup_hbm_bytes",
+                                   "grouped_down_hbm_bytes", "grouped_gateup_host_bytes", "grouped_down_host_bytes")]
 
 
 class StreamConfig(ctypes.Structure):
@@ -165,6 +170,9 @@ SIGNATURES = {
     "moe_cache_table": (ctypes.c_int, [P, ctypes.c_int, P, P]),
     "moe_cache_stats_get": (ctypes.c_int, [P, ctypes.POINTER(CacheStats)]),
     "moe_cache_sync": (ctypes.c_int, [P]),
+    "moe_cache_set_upload_stats": (ctypes.c_int, [P, ctypes.c_int]),
+    "moe_cache_sidecar_selftest": (ctypes.c_int, [P, ctypes.c_int, ctypes.c_int, ctypes.c_double,
+                                                  ctypes.POINTER(ctypes.c_int)]),
     "moe_cache_set_timing": (ctypes.c_int, [P, ctypes.c_int]),
     "moe_cache_set_decode_path": (ctypes.c_int, [P, ctypes.c_int, ctypes.c_int]),
     "moe_cache_set_staging": (ctypes.c_int, [P, ctypes.c_int]),

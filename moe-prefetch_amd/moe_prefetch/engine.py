@@ -108,6 +108,8 @@ class MoeCache:
                             online_lr=float(g("LLAMA_MOE_ONLINE_LR", "0")), save_path=g("LLAMA_MOE_PREDICTOR_SAVE"))
         if int(g("LLAMA_MOE_SPEC_PROBATION", "0") or "0") != 0:
             c.set_spec_probation(True)
+        if int(g("LLAMA_MOE_UPLOAD_STATS", "0") or "0") != 0:
+            c.set_upload_stats(True)
         if int(g("LLAMA_MOE_CACHE_FREEZE", "0") or "0") != 0:
             c.freeze()
         if int(g("LLAMA_MOE_SIDECAR", "0") or "0") != 0:
@@ -214,6 +216,11 @@ class MoeCache:
 
     def sync(self):
         check(lib().moe_cache_sync(self.h), "sync")
+
+    def set_upload_stats(self, on=True):
+        """LLAMA_MOE_UPLOAD_STATS (patches/0006:689-703): time every upload's copy on
+        its stream (stats n_upload_h2d / n_upload_d2d, upload_h2d_us / upload_d2d_us)."""
+        check(lib().moe_cache_set_upload_stats(self.h, int(on)), "set_upload_stats")
 
     def set_decode_path(self, split=0, graph=True):
         """split: 0 one launch for all routed experts, 1 resident/absent experts on

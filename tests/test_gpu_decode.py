@@ -116,7 +116,8 @@ def test_decode_256_experts_shared_expert(tmp_path):
 
 
 @pytest.mark.parametrize("shape", ["e256_shared_i512", "e128_i768", "e128_unsteered_prior", "e256_shared_i512_cpu",
-                                   "e128_i768_cpu_2of3", "e128_i768_cpu_1of2_b5", "e128_i768_cpu_0of1"])
+                                   "e128_i768_cpu_2of3", "e128_i768_cpu_1of2_b5", "e128_i768_cpu_0of1",
+                                   "e128_i768_cpu_1of1_b80_timed"])
 def test_decode_batch_matches_oracle(shape):
     # moe_decode_batch: batches of 16 tokens through every layer (route -- the
     # cache prior biases single-token selection only, so it is off here --,
@@ -124,22 +125,27 @@ def test_decode_batch_matches_oracle(shape):
     # expert), observed token-major and stepped: ids, frames and counters equal
     # to the oracle's, outputs bit for bit.  *_cpu: CPU-assisted serving, the
     # host computing the pairs of (a share of) the absent experts
-    # (b5: batches of 5 tokens; 0of1: CPU-assisted serving on, the host's share empty)
+    # (b5: batches of 5 tokens; 0of1: CPU-assisted serving on, the host's share empty;
+    # b80: batches above 64 tokens run on the GPU alone with serving on, timed per kernel)
     share = {"e256_shared_i512_cpu": (1, 1), "e128_i768_cpu_2of3": (2, 3), "e128_i768_cpu_1of2_b5": (1, 2),
-             "e128_i768_cpu_0of1": (0, 1)}.get(shape)
-    B = 5 if shape.endswith("_b5") else 16
+             "e128_i768_cpu_0of1": (0, 1), "e128_i768_cpu_1of1_b80_timed": (1, 1)}.get(shape)
+    B = 5 if shape.endswith("_b5") else 80 if "_b80" in shape else 16
+    timed = shape.endswith("_timed")
     shape = shape.split("_cpu")[0]
+    nb = 2 if B > 16 else 4
+    T = max(64, B * nb)
     if shape == "e256_shared_i512":
-        rig = Rig([48, 32], [Q4, Q6], T=64, I=512, E=256, shared=True, zipf_s=1.0, reuse=0.5, admit="window",
+        rig = Rig([48, 32], [Q4, Q6], T=T, I=512, E=256, shared=True, zipf_s=1.0, reuse=0.5, admit="window",
                   batch_tables=True, cache_prior=0.01)
     elif shape == "e128_i768":
-        rig = Rig([20, 28], [Q6, Q4], T=64, I=768, admit="window", batch_tables=True)
+        rig = Rig([20, 28], [Q6, Q4], T=T, I=768, admit="window", batch_tables=True)
     else:   # W x alone: a 0.01 prior on probabilities near 1/128 would change the ids
-        rig = Rig([24, 24], [Q4, Q6], T=64, steer=False, admit="window", batch_tables=True, cache_prior=0.01)
-    nb = 4
+        rig = Rig([24, 24], [Q4, Q6], T=T, steer=False, admit="window", batch_tables=True, cache_prior=0.01)
     oc = rig.oracle_cache()
     if share:
         rig.cache.set_sidecar(4, share)
+    if timed:
+        rig.cache.set_timing(True)
     try:
         out = torch.empty((rig.nl, B, 2048), dtype=torch.float32, device=rig.dev)
         for b in range(nb):
@@ -167,7 +173,13 @@ def test_decode_batch_matches_oracle(shape):
         for k in ("n_hit", "n_miss", "n_scheduled", "n_published", "n_admit_ok", "n_admit_denied"):
             assert st[k] == ost[k], (k, st[k], ost[k])
         if share:
-            assert (st["n_cpu_served"] > 0) == (share[0] > 0)   # the host computed pairs (none at 0/1)
+            # the host computed pairs (none at 0/1, nor in batches above 64 tokens)
+            assert (st["n_cpu_served"] > 0) == (share[0] > 0 and B <= 64)
+        if timed:
+            kt = rig.cache.kernel_times()
+            assert kt["grouped_launches"] == nb * rig.nl and kt["grouped_gateup_ms"] > 0 and kt["grouped_down_ms"] > 0
+            assert kt["grouped_pairs"] == nb * B * 8 * rig.nl          # every pair on the GPU
+            assert kt["grouped_gateup_hbm_bytes"] + kt["grouped_gateup_host_bytes"] > 0
     finally:
         oc.close()
         rig.close()
@@ -220,10 +232,17 @@ def test_staged_uploads_fill_slots(knobs):
     for staging in (True, False):
         rig = Rig([12, 20, 16], [Q4, Q6, Q4], T=T, **knobs)
         rig.cache.set_staging(staging)
+        rig.cache.set_upload_stats(True)
         try:
             ids, outs, frames = rig.run()
             rig.cache.sync()
             st = rig.cache.stats()
+            # every finished upload timed on its stream, by source (LLAMA_MOE_UPLOAD_STATS)
+            assert st["n_upload_h2d"] + st["n_upload_d2d"] == st["n_copied"] > 0
+            assert st["n_upload_d2d"] <= st["n_staged"] and (st["n_upload_d2d"] > 0) == staging
+            assert st["upload_d2d_us"] > 0 if staging else st["upload_d2d_us"] == 0
+            if st["n_upload_h2d"]:
+                assert st["upload_h2d_us"] > 0
             for l in range(rig.nl):
                 v = rig.cache.lookup(l)
                 eb = rig.eb[l]
@@ -553,3 +572,27 @@ def test_decode_one_layer_all_resident_fused(tmp_path, graph):
         rig.close()
     st = rig.stats
     assert st["n_miss"] == 0 and st["n_hit"] == 40 * 8 and st["n_scheduled"] == 0
+
+
+def test_sidecar_channel_selftest(tmp_path):
+    """The serving channel's self-test (patches/0009:436-472, 914-925) over the
+    decode's own exchange words: 2000 bounded round trips pass; with the host
+    withholding its answer from round 10 on, the kernel's own 50 ms bound ends
+    its wait, the call reports the 40 failed exchanges and every kernel has
+    exited; the decode with CPU-assisted serving that follows is bit-exact."""
+    import ctypes
+    rig = Rig([16, 24], [Q4, Q6], T=16, admit="window", batch_tables=True)
+    try:
+        bad = ctypes.c_int(-1)
+        assert L().moe_cache_sidecar_selftest(rig.cache.h, 2000, -1, 2.0, ctypes.byref(bad)) == 0, \
+            L().moe_last_error()
+        assert bad.value == 0
+        assert L().moe_cache_sidecar_selftest(rig.cache.h, 50, 10, 0.05, ctypes.byref(bad)) == _lib.MOE_ERR_HIP
+        assert bad.value == 40 and b"40 of 50" in L().moe_last_error()
+        torch.cuda.synchronize()
+        rig.cache.set_sidecar(4)            # its own 10000-round test passes
+        rig.cache.set_decode_path(split=0, graph=True)
+        check_run(rig, tmp_path)
+    finally:
+        rig.close()
+    assert rig.stats["n_cpu_served"] > 0
