@@ -17,6 +17,7 @@ completes at once) -- the CPU-testable core.
 """
 import ctypes
 import os
+import sys
 
 import numpy as np
 
@@ -99,13 +100,23 @@ class MoeCache:
                    early_issue=int(g("LLAMA_MOE_EARLY_ISSUE", "0")) != 0,
                    cache_prior=max(0.0, float(g("LLAMA_MOE_CACHE_PRIOR", "0"))),
                    deterministic=int(g("LLAMA_MOE_DETERMINISTIC", "0")) != 0, **shape)
+        # a model that fails to load (or that the cache refuses: a PCA block,
+        # another expert count) is reported loudly and serving goes on without
+        # it (patches/0006:521-556)
         if g("LLAMA_MOE_EVICTOR"):
             from .moep import MoePredictor
-            c.set_evictor(MoePredictor(g("LLAMA_MOE_EVICTOR")))
+            try:
+                c.set_evictor(MoePredictor(g("LLAMA_MOE_EVICTOR")))
+            except (_lib.MoeError, OSError) as e:
+                print(f"moe-cache: EVICTOR NOT LOADED: {e}", file=sys.stderr, flush=True)
         if g("LLAMA_MOE_PREDICTOR"):
             from .moep import MoePredictor
-            c.set_predictor(MoePredictor(g("LLAMA_MOE_PREDICTOR")), predict_top=int(g("LLAMA_MOE_PREDICT_TOP", "3")),
-                            online_lr=float(g("LLAMA_MOE_ONLINE_LR", "0")), save_path=g("LLAMA_MOE_PREDICTOR_SAVE"))
+            try:
+                c.set_predictor(MoePredictor(g("LLAMA_MOE_PREDICTOR")),
+                                predict_top=int(g("LLAMA_MOE_PREDICT_TOP", "3")),
+                                online_lr=float(g("LLAMA_MOE_ONLINE_LR", "0")), save_path=g("LLAMA_MOE_PREDICTOR_SAVE"))
+            except (_lib.MoeError, OSError) as e:
+                print(f"moe-cache: PREDICTOR NOT LOADED: {e}", file=sys.stderr, flush=True)
         if int(g("LLAMA_MOE_SPEC_PROBATION", "0") or "0") != 0:
             c.set_spec_probation(True)
         if int(g("LLAMA_MOE_UPLOAD_STATS", "0") or "0") != 0:

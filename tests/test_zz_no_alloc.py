@@ -1,8 +1,9 @@
 """moe_grouped_experts_static -- the grouped expert chain with its workspace in
 a static device array, for callers that cannot allocate -- against
-moe_grouped_experts with a caller workspace: outputs, pair rows and h bit for
-bit on two calls in a row, the second smaller (the array keeps the first
-call's contents), and the host-side refusals."""
+moe_grouped_experts with a caller workspace: captured into a HIP graph and
+replayed, outputs, pair rows and h bit for bit on two calls in a row, the
+second smaller (the array keeps the first call's contents), and the host-side
+refusals."""
 import ctypes
 import zlib
 
@@ -56,6 +57,51 @@ def _call(n_tok, seed, dt, I, shared, rows_out):
         assert np.isfinite(a).all()
         assert np.array_equal(a, b)
     return bm, x, store, eb, w
+
+
+def test_static_scratch_under_graph_capture():
+    # first in this file: in a fresh process the capture is the first static
+    # call on the device, so its scratch-address lookup runs inside the
+    # capture.  The captured call is replayed three times, with eager work and
+    # synchronisation between the replays; every replay equals the workspace
+    # path's result bit for bit
+    E, K, I, dt, n_tok = 128, 8, 768, _lib.TYPE_Q4K, 32
+    seed = zlib.crc32(b"capture")
+    rng = np.random.default_rng(seed)
+    eb = L().moe_expert_bytes(H, I, dt)
+    store = torch.empty(E * eb, dtype=torch.uint8, device=DEV)
+    synth_experts_dev(seed, 4, 0, E, I, dt, store.data_ptr(), eb)
+    xf = torch.empty((n_tok, H), dtype=torch.float32, device=DEV)
+    _lib.check(L().moe_synth_vec(seed, 1, 0, n_tok, 5, 1, H, 1.0, xf.data_ptr(), stream()), "x")
+    x = xf.to(torch.bfloat16)
+    ids = np.stack([rng.choice(E, size=K, replace=False) for _ in range(n_tok)]).astype(np.int32)
+    w = rng.random((n_tok, K)).astype(np.float32) + 0.05
+    w = torch.from_numpy(w / w.sum(1, keepdims=True)).to(DEV)
+    bm = BatchedMoe(n_tok, n_experts=E, n_expert_used=K, intermediate=I)
+    bm.dispatch(n_tok, ids=torch.from_numpy(ids).to(DEV), stream=stream())
+    want = torch.empty((n_tok, H), dtype=torch.float32, device=DEV)
+    d = _desc(bm, x, want, n_tok, store.data_ptr(), eb, E, dt, w, None, None, bm.ws.data_ptr())
+    _lib.check(L().moe_grouped_experts(ctypes.byref(d), stream()), "workspace")
+    torch.cuda.synchronize()
+    want_h = want.cpu().numpy()
+    out = torch.empty((n_tok, H), dtype=torch.float32, device=DEV)
+    ds = _desc(bm, x, out, n_tok, store.data_ptr(), eb, E, dt, w, None, None, None)
+    g = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream()
+    rc = []
+    with torch.cuda.graph(g, stream=side, capture_error_mode="thread_local"):
+        rc.append(L().moe_grouped_experts_static(ctypes.byref(ds), torch.cuda.current_stream().cuda_stream))
+    assert rc == [0], L().moe_last_error()
+    for _ in range(3):
+        out.fill_(float("nan"))
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert np.array_equal(out.cpu().numpy(), want_h)
+        # eager work between replays: the workspace path again
+        _lib.check(L().moe_grouped_experts(ctypes.byref(d), stream()), "workspace")
+        torch.cuda.synchronize()
+    del g
 
 
 def test_static_scratch_matches_workspace_two_calls():
