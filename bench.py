@@ -551,24 +551,33 @@ def kernel_report(kt, n_tok, steps, s0, s1):
     }
 
 
-def fused_report(kt, n_tok):
+# the rocprofv3 PMC runs behind roofline.traffic, per workload (profiles/traffic.json)
+TRAFFIC_KEYS = {"single1": ("fused_layer", "profiles/fused_layer_traffic.md"),
+                "stacked48": ("fused_layer_stacked48", "profiles/fused_layer_stacked48_traffic.md")}
+
+
+def fused_report(kt, n_tok, workload="stacked48"):
     """Roofline of the fused layer launch (router rows + the resident experts'
-    bytes it reads, over its dispatch-stamped duration)."""
+    bytes it reads, over its dispatch-stamped duration).  traffic: this run's
+    bytes per launch times the (FETCH_SIZE + WRITE_SIZE) / algorithmic ratio
+    of the committed PMC run on the same workload (on the 48-layer decode for a
+    workload without one of its own)."""
     n = max(kt["n_layers"], 1)
     ms, hb, pb = kt["layer_ms"], kt["layer_hbm_bytes"], kt["layer_host_bytes"]
     achieved = hb / (ms * 1e-3) / 1e9 if ms > 0 else 0.0
     traffic, tsrc = None, None
+    key, doc = TRAFFIC_KEYS.get(workload, TRAFFIC_KEYS["stacked48"])
     tpath = os.path.join(ROOT, "profiles", "traffic.json")
     if os.path.exists(tpath):
         with open(tpath) as f:
-            tr = json.load(f).get("fused_layer")
+            tr = json.load(f).get(key)
         if tr:
             ratio = (tr["hbm_read_bytes_per_launch"] + tr["hbm_write_bytes_per_launch"]) / \
                 tr["algorithmic_bytes_per_launch"]
             traffic = round(ratio * hb / n)
-            tsrc = ("this run's bytes per launch x the (FETCH_SIZE + WRITE_SIZE) / algorithmic ratio of the "
-                    "committed rocprofv3 PMC run on the one-layer all-resident workload (profiles/traffic.json, "
-                    "profiles/fused_layer_traffic.md), not counters of this run")
+            tsrc = (f"pmc: this run's bytes per launch x {ratio:.3f}, the (FETCH_SIZE + WRITE_SIZE) / algorithmic "
+                    f"ratio of the committed rocprofv3 run on the {key.replace('fused_layer_', '').replace('fused_layer', 'single1')} "
+                    f"workload ({doc})")
     return {
         "kernels_ms_per_token": {"fused_layer": round(ms / max(n_tok, 1), 4)},
         "kernel_timing": f"HIP events stamped by each dispatch (hipExtLaunchKernelGGL) on its stream, {n_tok} "
@@ -1025,7 +1034,7 @@ def run_single(args):
         s1 = cache.stats()
         frames = [cache.frame(0)]
         kt, n_kt = wl.kernel_pass(cache, split=0)
-        rep = fused_report(kt, n_kt)
+        rep = fused_report(kt, n_kt, "single1")
         n = max(kt["n_layers"], 1)
         us = kt["layer_ms"] / n * 1e3
         expert_bytes = K * wl.eb[0]
@@ -1379,7 +1388,7 @@ def compact(v, key=None):
             if k == "bytes" and isinstance(x, str):
                 continue
             if k == "traffic_source" and isinstance(x, str):
-                out[k] = "pmc" if x.startswith("pmc") else "PMC ratio of profiles/traffic.json x bytes"
+                out[k] = x if x.startswith("pmc") else "PMC ratio of profiles/traffic.json x bytes"
                 continue
             out[k] = compact(x, k)
         if key == "cpu_baseline" and "sweep" in v:
