@@ -42,7 +42,7 @@ struct PlanJob {
 struct Chunk {
     int job;
     size_t offset, len;
-    int last;          // the job's final chunk: its table word goes right after it
+    int last;          // 1 on the chunk that completes the expert: the mover writes the table word after it
 };
 
 class Planner {
