@@ -596,3 +596,33 @@ def test_sidecar_channel_selftest(tmp_path):
     finally:
         rig.close()
     assert rig.stats["n_cpu_served"] > 0
+
+
+def test_decode_config3_full_shape(tmp_path):
+    """Cache-aware routing at full size: the single-layer shape (N(0,0.02)
+    router, no steering) stacked 48 deep over 56 slots, δ = 0.01 on the
+    probabilities of resident experts (patches/0007:109-124); every id is
+    routed against the published tables of its step, so ids, frames and
+    traces agreeing token after token checks the prior end to end."""
+    rig = Rig([56] * 48, [Q6 if l % 2 else Q4 for l in range(48)], T=16, steer=False, admit="window",
+              batch_tables=True, cache_prior=0.01)
+    try:
+        check_run(rig, tmp_path, out_every=8)
+    finally:
+        rig.close()
+    assert rig.stats["n_hit"] > 0
+
+
+def test_decode_config5_full_shape(tmp_path):
+    """The wide variant at full size: 40 layers x 256 routed experts (top-8)
+    + 1 always-on shared expert, I = 512, 96 slots per layer, Q6_K down in odd
+    layers, Zipf(1.0) popularity with reuse 0.5, δ = 0.01, window admission,
+    with CPU-assisted serving as the bench runs it."""
+    rig = Rig([96] * 40, [Q6 if l % 2 else Q4 for l in range(40)], T=16, I=512, E=256, shared=True, zipf_s=1.0,
+              reuse=0.5, admit="window", batch_tables=True, cache_prior=0.01)
+    rig.cache.set_sidecar(8)
+    try:
+        check_run(rig, tmp_path, out_every=8)
+    finally:
+        rig.close()
+    assert rig.stats["n_cpu_served"] > 0
