@@ -657,7 +657,7 @@ __global__ __launch_bounds__(256, CH == 1 ? 4 : 3) void grouped_q4_kernel(Groupe
 
     __shared__ AStage st[2];
     __shared__ int s_rows[CH * GT];
-    __shared__ float s_dx[CH * GT][NB];
+    __shared__ __attribute__((aligned(16))) float s_dx[NB][CH * GT];   // [block][pair]: a lane's 4 rows in one read
     const uint8_t *wrow = mat + (size_t)row * ROWB;
     const int gm = (h >> 1) + 2 * (h & 1);
 
@@ -669,7 +669,7 @@ __global__ __launch_bounds__(256, CH == 1 ? 4 : 3) void grouped_q4_kernel(Groupe
             s_rows[tid] = DOWN ? pos : a.perm[pos] / a.K;
         }
         __syncthreads();
-        for (int i = tid; i < CH * GT * NB; i += 256) s_dx[i / NB][i % NB] = adx[(size_t)s_rows[i / NB] * NB + (i % NB)];
+        for (int i = tid; i < CH * GT * NB; i += 256) s_dx[i % NB][i / NB] = adx[(size_t)s_rows[i / NB] * NB + (i % NB)];
         stage_a(st[0], s_rows, min(GT, npc), act, abs16, K, 0, wave, lane);
         uint4 cw[3], nw[3];
         cw[0] = *(const uint4 *)wrow;
@@ -713,9 +713,17 @@ __global__ __launch_bounds__(256, CH == 1 ? 4 : 3) void grouped_q4_kernel(Groupe
                         stage_a(st[jn & 1], s_rows + p2 * GT, min(GT, npc - p2 * GT), act, abs16, K, s2, wave, lane);
                     }
                     float4_t acc[2] = {{0, 0, 0, 0}, {0, 0, 0, 0}};
+                    // the fragments of K chunk i+1 are read before chunk i's products
+                    half8_t fa[2][2];
+#pragma unroll
+                    for (int t = 0; t < 2; ++t) fa[0][t] = stage_frag(S, 16 * t + n, q4_a_offset(h, 0));
 #pragma unroll
                     for (int i = 0; i < 8; ++i) {
-                        const int off = q4_a_offset(h, i);
+                        if (i + 1 < 8) {
+#pragma unroll
+                            for (int t = 0; t < 2; ++t)
+                                fa[(i + 1) & 1][t] = stage_frag(S, 16 * t + n, q4_a_offset(h, i + 1 < 8 ? i + 1 : 0));
+                        }
                         half8_t bi;
                         if constexpr (CH > 1) {
                             bi = b[i];
@@ -724,8 +732,11 @@ __global__ __launch_bounds__(256, CH == 1 ? 4 : 3) void grouped_q4_kernel(Groupe
                             bi = q4_b(L ? cw[2] : cw[1], i, sc.sc[L][nib]);
                         }
 #pragma unroll
-                        for (int t = 0; t < 2; ++t) acc[t] = mfma32(stage_frag(S, 16 * t + n, off), bi, acc[t]);
+                        for (int t = 0; t < 2; ++t) acc[t] = mfma32(fa[i & 1][t], bi, acc[t]);
                     }
+                    float4 dxv[2];
+#pragma unroll
+                    for (int t = 0; t < 2; ++t) dxv[t] = *(const float4 *)&s_dx[s][p * GT + 16 * t + 4 * h];
 #pragma unroll
                     for (int t = 0; t < 2; ++t) {
                         const half4_t am = *(const half4_t *)&S.bs[16 * t + n][4 * gm];
@@ -734,7 +745,7 @@ __global__ __launch_bounds__(256, CH == 1 ? 4 : 3) void grouped_q4_kernel(Groupe
 #pragma unroll
                         for (int i = 0; i < 4; ++i) {
                             // ggml's order: acc += (d*dx)*sumi; acc -= (dmin*dx)*summ
-                            const float dx = s_dx[p * GT + 16 * t + 4 * h + i][s];
+                            const float dx = i == 0 ? dxv[t].x : i == 1 ? dxv[t].y : i == 2 ? dxv[t].z : dxv[t].w;
                             y[p][t][i] = y[p][t][i] + (sc.d * dx) * acc[t][i];
                             y[p][t][i] = y[p][t][i] - (sc.dmin * dx) * z[i];
                         }
