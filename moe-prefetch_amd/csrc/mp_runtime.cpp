@@ -3119,6 +3119,9 @@ int moe_decode_layer(moe_cache *c, int layer, const float *x, const float *bias,
     return MOE_OK;
 }
 
+// tokens of at most this many layers launch directly in graph mode (see below)
+constexpr int DIRECT_MAX_LAYERS = 8;
+
 int moe_decode_token(moe_cache *c, const float *x, const float *bias, float *out, int32_t *ids_host, void *stream) {
     if (!c || !x || !out) return fail(MOE_ERR_ARG, "bad arguments");
     if (c->host_only) return fail(MOE_ERR_STATE, "host-only cache (device < 0) cannot decode");
@@ -3149,8 +3152,20 @@ int moe_decode_token(moe_cache *c, const float *x, const float *bias, float *out
     // reads h_seq when the stream reaches it; the previous token synchronised
     // the stream before returning, so no copy of an older number is pending.
     const uint32_t seq = next_seq(c);
-    *c->h_seq = seq;
-    HIPCHK(hipMemcpyAsync(c->d_seq, c->h_seq, 4, hipMemcpyHostToDevice, st));
+    // A captured graph's launch costs ~30 us of latency here (ROCm 7 on
+    // MI355X) against ~11 us for a kernel launch, and launching ~15 us layers
+    // one by one measured faster at every layer count (1 layer: 26 against
+    // 35 us a step; 48 layers within 1 %).  The graph frees the host sooner,
+    // which CPU-assisted serving and streaming need (the host serves a layer
+    // while the GPU runs the next), and it costs less host time for many
+    // layers.  So a token of at most DIRECT_MAX_LAYERS layers without them
+    // launches its layers directly, with the sequence number by value and the
+    // caller's x and out: no copies.
+    const bool use_graph = c->graph && !c->timing && (NL > DIRECT_MAX_LAYERS || sc || stm);
+    if (use_graph) {
+        *c->h_seq = seq;
+        HIPCHK(hipMemcpyAsync(c->d_seq, c->h_seq, 4, hipMemcpyHostToDevice, st));
+    }
     const bool fused = c->split == 0 && !stm;
     // An earlier token that failed may have left SC_ABORT in the answers; a
     // join of this token must wait for this token's answer, not end on that.
@@ -3189,12 +3204,12 @@ int moe_decode_token(moe_cache *c, const float *x, const float *bias, float *out
     };
     // per-kernel HIP-event timing needs eager launches: hipEventElapsedTime
     // does not accept events recorded as nodes of a graph
-    if (!c->graph || c->timing) {
+    if (!use_graph) {
         for (int l = 0; l < NL; ++l) {
             const int r = decode_layer_impl(c, l, x + (size_t)l * c->H, bias ? bias + (size_t)l * c->E : nullptr,
                                             out + (size_t)l * c->H, nullptr, nullptr, st,
                                             c->timing ? c->tev.data() + (size_t)l * 12 : nullptr, stage, sc, fused,
-                                            0);
+                                            seq);
             if (r != MOE_OK) {
                 abort_joins();
                 hipStreamSynchronize(st);
