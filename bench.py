@@ -1042,7 +1042,7 @@ def run_single(args):
                "config": {"workload": f"one layer x {E} experts all resident, H {H}, I {I}, top-{K}, Q4_K gate/up/down, "
                                       f"router N(0,0.02), x N(0,1); {a.steps} independent steps timed ({W} warmup)"},
                "step": {"us_wall": round(1e6 * el / a.steps, 2), "hit_rate": window(s0, s1, a.steps)["hit_rate"],
-                        "what": "decode_token per step: copies, graph launch, routed ids back, cache step"},
+                        "what": "decode_token per step: the layer launched directly (graph mode launches tokens of at most 8 layers directly), routed ids back, cache step"},
                "roofline": {**rep["roofline"], "expert_bytes_per_step": expert_bytes,
                             "expert_gbs": round(expert_bytes / (us * 1e-6) / 1e9, 1),
                             "expert_frac": round(expert_bytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}}
