@@ -482,12 +482,14 @@ int moe_cache_set_timing(moe_cache *c, int on);
  * 3 router GEMV, selection, gate/up and down as four launches; 1 resident and
  * absent experts as separate launches on two streams, forked and joined per
  * layer; 2 the same launches one after the other on one stream.
- * graph: replay each token's launches as one captured HIP graph (default 1;
- * timing mode launches eagerly).  A token of at most 8 layers without
- * CPU-assisted serving or streaming launches its layers directly even so: a
- * graph launch costs ~30 us of latency against ~11 us for a kernel launch
- * (ROCm 7, MI355X), and the direct launches need no copies of x, out or the
- * sequence number.  Every path gives the same bits. */
+ * graph: 1 (default) replay each token's launches as one captured HIP graph,
+ * except that a token of at most 8 layers without CPU-assisted serving or
+ * streaming launches its layers directly: a graph launch costs ~30 us of
+ * latency against ~11 us for a kernel launch (ROCm 7, MI355X), and direct
+ * launches need no copies of x, out or the sequence number; 2 always the
+ * graph; 0 always direct launches.  Timing mode launches directly.  Every
+ * path gives the same bits.  MOE_ERR_ARG for split outside 0..3 or graph
+ * outside 0..2. */
 int moe_cache_set_decode_path(moe_cache *c, int split, int graph);
 /* Staged uploads (default on; no counterpart in the reference, which uploads
  * from the host store, P6:428-440): moe_decode_token's kernels also write each

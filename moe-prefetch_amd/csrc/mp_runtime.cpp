@@ -257,7 +257,7 @@ struct moe_cache {
     // device buffers (x_buf, bias_buf, out_buf)
     int split = 0;                     // 0 fused layer launch, 1 fork/join over two streams,
                                        // 2 serial on one stream, 3 router, selection and experts unfused
-    bool graph = true;
+    int graph = 1;                 // 0 direct launches, 1 a graph where it is faster, 2 always a graph
     hipStream_t cap_stream = nullptr;
     hipEvent_t ev_user = nullptr, ev_done = nullptr;
     float *x_buf = nullptr, *bias_buf = nullptr, *out_buf = nullptr;
@@ -2436,8 +2436,9 @@ int moe_cache_set_decode_path(moe_cache *c, int split, int graph) {
     if (split < 0 || split > 3) return fail(MOE_ERR_ARG, "split must be 0, 1, 2 or 3");
     if ((split == 1 || split == 2) && c->sc_den > 0)
         return fail(MOE_ERR_STATE, "CPU-assisted serving runs with one expert launch (split 0 or 3); turn it off first");
+    if (graph < 0 || graph > 2) return fail(MOE_ERR_ARG, "graph must be 0, 1 or 2");
     c->split = split;
-    c->graph = graph != 0;
+    c->graph = graph;
     return MOE_OK;
 }
 
@@ -3160,8 +3161,8 @@ int moe_decode_token(moe_cache *c, const float *x, const float *bias, float *out
     // while the GPU runs the next), and it costs less host time for many
     // layers.  So a token of at most DIRECT_MAX_LAYERS layers without them
     // launches its layers directly, with the sequence number by value and the
-    // caller's x and out: no copies.
-    const bool use_graph = c->graph && !c->timing && (NL > DIRECT_MAX_LAYERS || sc || stm);
+    // caller's x and out: no copies.  (graph 2 keeps the graph for any token.)
+    const bool use_graph = c->graph && !c->timing && (c->graph == 2 || NL > DIRECT_MAX_LAYERS || sc || stm);
     if (use_graph) {
         *c->h_seq = seq;
         HIPCHK(hipMemcpyAsync(c->d_seq, c->h_seq, 4, hipMemcpyHostToDevice, st));

@@ -235,7 +235,11 @@ class MoeCache:
 
     def set_decode_path(self, split=0, graph=True):
         """split: 0 one launch for all routed experts, 1 resident/absent experts on
-        two forked streams, 2 resident then absent on one stream."""
+        two forked streams, 2 resident then absent on one stream, 3 router,
+        selection, gate/up and down as four launches.  graph: True/1 a captured
+        graph per token (tokens of at most 8 layers without CPU-assisted serving
+        or streaming launch directly, which is faster), 2 always the graph,
+        False/0 direct launches."""
         check(lib().moe_cache_set_decode_path(self.h, int(split), int(graph)), "set_decode_path")
 
     def set_timing(self, on=True):

@@ -68,18 +68,19 @@ def check_run(rig, tmp_path, out_every=1, tol=1e-3, oc=None, record_map=True, to
     return worst
 
 
-@pytest.mark.parametrize("split,graph", [(1, 1), (0, 1), (2, 1), (3, 1), (1, 0), (0, 0), (2, 0), (3, 0)],
+@pytest.mark.parametrize("split,graph", [(1, 2), (0, 2), (2, 2), (3, 2), (1, 0), (0, 0), (2, 0), (3, 0), (0, 1)],
                          ids=["fork-graph", "fused-graph", "serial-graph", "unfused-graph", "fork-eager",
-                              "fused-eager", "serial-eager", "unfused-eager"])
+                              "fused-eager", "serial-eager", "unfused-eager", "fused-direct"])
 def test_decode_4_layers_window_admission(tmp_path, split, graph):
     # every decode path (the fused front with one expert launch; router,
     # selection and experts as four launches; resident/absent experts split
     # over two streams or one after the other; captured graph replayed per
-    # token or eager launches) must give
-    # the oracle's ids, frames and outputs; the graph is replayed 40 times
-    # with eager copies, host work and synchronisation between replays
+    # token (graph 2: kept for 4 layers) or eager launches; graph 1 launches
+    # a token this short directly) must give the oracle's ids, frames and
+    # outputs; the graph is replayed 40 times with eager copies, host work and
+    # synchronisation between replays
     rig = Rig([16, 24, 12, 40], [Q4, Q6, Q4, Q6], T=40, admit="window", batch_tables=True)
-    rig.cache.set_decode_path(split=split, graph=bool(graph))
+    rig.cache.set_decode_path(split=split, graph=graph)
     if split and not graph:
         rig.cache.set_timing(True)          # per-kernel events around every launch
     try:
@@ -89,13 +90,13 @@ def test_decode_4_layers_window_admission(tmp_path, split, graph):
         rig.close()
 
 
-@pytest.mark.parametrize("E,I,graph", [(64, 256, 1), (192, 512, 0)], ids=["e64_i256_graph", "e192_i512_eager"])
+@pytest.mark.parametrize("E,I,graph", [(64, 256, 2), (192, 512, 0)], ids=["e64_i256_graph", "e192_i512_eager"])
 def test_decode_fused_chunk_counts(tmp_path, E, I, graph):
     # the fused layer routes in registers per 64-expert chunk (1 to 4 chunks:
     # one instantiation each); E = 64 and E = 192, with the cache prior on so
     # the routing reads the published tables every token
     rig = Rig([24, 40], [Q4, Q6], T=32, I=I, E=E, admit="window", batch_tables=True, cache_prior=0.01)
-    rig.cache.set_decode_path(split=0, graph=bool(graph))
+    rig.cache.set_decode_path(split=0, graph=graph)
     try:
         worst = check_run(rig, tmp_path)
         print("worst rel-L2", worst)
@@ -195,7 +196,7 @@ def test_decode_cache_prior_delta(tmp_path):
         rig.close()
 
 
-@pytest.mark.parametrize("graph", [1, 0], ids=["graph", "eager"])
+@pytest.mark.parametrize("graph", [2, 0], ids=["graph", "eager"])
 def test_decode_cache_prior_on_logits_fused(tmp_path, graph):
     # the logits-space variant of the cache prior (delta added to resident
     # experts' logits before the top-k, gate weights from the unbiased
@@ -203,7 +204,7 @@ def test_decode_cache_prior_on_logits_fused(tmp_path, graph):
     # every gate/up wave; no steering, so the prior changes the selection
     rig = Rig([24, 24, 16], [Q4, Q6, Q4], T=48, steer=False, admit="window", batch_tables=True, cache_prior=0.01,
               prior_space="logits")
-    rig.cache.set_decode_path(split=0, graph=bool(graph))
+    rig.cache.set_decode_path(split=0, graph=graph)
     try:
         check_run(rig, tmp_path)
     finally:
@@ -549,7 +550,7 @@ def test_decode_layer_by_layer(tmp_path, case):
     assert open(mp).read() == open(omp).read()
 
 
-@pytest.mark.parametrize("graph", [1, 0], ids=["graph", "eager"])
+@pytest.mark.parametrize("graph", [2, 0], ids=["graph", "eager"])
 def test_decode_one_layer_all_resident_fused(tmp_path, graph):
     """The one-layer workload: a layer of 128 experts, all resident (placed
     by a heat file naming each of them, patches/0007:431-485), an N(0,0.02)
@@ -561,7 +562,7 @@ def test_decode_one_layer_all_resident_fused(tmp_path, graph):
     # (counts are halved at load, patches/0007:461: every count here stays above 0)
     heat.write_text("\n".join([f"moe-heat 1 1 {E}"] + [f"0 {e} {2 * (E - e)}" for e in range(E)]) + "\n")
     rig = Rig([E], [Q4], T=40, steer=False, admit="window", batch_tables=True)
-    rig.cache.set_decode_path(split=0, graph=bool(graph))
+    rig.cache.set_decode_path(split=0, graph=graph)
     try:
         assert rig.cache.heat_file(str(heat)) == (E, E)
         assert sorted(rig.cache.frame(0).tolist()) == list(range(E))

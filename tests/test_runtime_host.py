@@ -153,6 +153,19 @@ def test_bad_knob_is_loud():
         MoeCache(2, admit="sometimes", device=-1)
 
 
+def test_decode_path_arguments():
+    # split 0..3 and graph 0 (direct launches), 1 (a graph where it is faster)
+    # or 2 (always a graph); anything else is MOE_ERR_ARG and changes nothing
+    from moe_prefetch import _lib
+    c = product_cache([8, 8])
+    for split, graph in ((0, 0), (0, 1), (0, 2), (3, 2), (1, 1), (2, 0)):
+        c.set_decode_path(split=split, graph=graph)
+    for split, graph in ((0, 3), (0, -1), (4, 1), (-1, 0)):
+        with pytest.raises(_lib.MoeError, match="must be"):
+            c.set_decode_path(split=split, graph=graph)
+    c.close()
+
+
 # ---- MOEP predictor / evictor hooks (patches/0006:295-427, 765-922; 0007:149-168, 330-355, 655-724) ----
 HOOKS = [
     dict(pred=True),
