@@ -29,7 +29,7 @@
  *                           llama_moe_cache_step (0008:362-369)
  *   moe_decode_batch        the same for a batch of tokens: the observe callback sees ids [n_tok][K]
  *                           token-major (0006:295-400); the reference's cached graph handles one token
- *                           (0007:114), this build serves batches from the same slots
+ *                           (0007:114); here batches are served from the same slots
  *   moe_pool_*              the slab/slot store behind src/prefetch_engine.py ExpertCache (:45-168)
  *   moe_dispatch            ggml mul_mat_id's batch row mapping (per-expert counts + mmid_row_mapping,
  *                           visible in 0008:157-167): histogram, exclusive scan, stable (token, k) order
@@ -303,7 +303,7 @@ typedef struct {
     int32_t reserve;           /* LLAMA_MOE_STREAM_RESERVE, default 2: extra free slots kept per layer */
     int32_t top_k;             /* LLAMA_MOE_STREAM_TOPK, default 8 (<= 8): candidates scored per target */
     double gbps;               /* LLAMA_MOE_STREAM_GBPS, default 45.7: the copy engine's rate for deadlines */
-    int32_t chunk_kib;         /* LLAMA_MOE_STREAM_CHUNK_KIB (this build's): largest copy per push; 0 (default):
+    int32_t chunk_kib;         /* LLAMA_MOE_STREAM_CHUNK_KIB (no counterpart in the reference): largest copy per push; 0 (default):
                                   a whole expert per push (the reference used 512 KiB) */
 } moe_stream_config;
 
@@ -542,9 +542,13 @@ int moe_cache_kernel_times(moe_cache *c, moe_kernel_times *out);
  * layer's routing (dev [K]) when not NULL.  Split 0 (the default) runs the
  * fused launch, split 3 the four launches.  Each call carries a sequence
  * number of its own, so a layer's input may be computed from the layer below
- * (x_{l+1} = x_l + out_l) between calls.  With CPU-assisted serving the
- * calling thread waits for the layer's post, computes the host's share of its
- * absent experts and answers before it returns; the GPU's join does the rest.
+ * (x_{l+1} = x_l + out_l) between calls.  With CPU-assisted serving a call
+ * returns once its layer is launched: the cache's server thread waits for the
+ * layer's post, computes the host's share of its absent experts and answers,
+ * layer after layer in call order, while the caller launches the next layers
+ * (they queue behind the layer's join on the GPU, as a token's graph does).
+ * A serving failure ends the joins of the layers still queued and is reported
+ * by the next call, moe_cache_observe or moe_cache_step.
  * Drive a token as the reference does: every layer in order, the ids observed
  * (moe_cache_observe, after each layer or at the end; the call compares them
  * with the host's routing and stages the experts the kernels read from the

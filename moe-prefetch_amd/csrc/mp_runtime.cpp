@@ -13,7 +13,7 @@
 //             heat decay, one batched table write
 //   publish   0008:613-627 deterministic (sorted) variant
 //   admission 0007:398-429; tables 0007:327-396; map trace 0008:417-489
-// The data path is this build's own: one contiguous copy per expert
+// The data path is the library's own: one contiguous copy per expert
 // ([up|gate|down] in the store and in the slot) on a dedicated stream,
 // completion by hipEvent, tables in one pinned mirror flushed with one copy.
 #include <hip/hip_runtime.h>
@@ -160,6 +160,26 @@ struct moe_predictor {
     mpp::Predictor p;
 };
 
+// The server of layers decoded one by one with CPU-assisted serving: each
+// call queues its layer, and this thread serves the host's share of the
+// layers in call order, so a call returns once its layer is launched and the
+// caller's next launches queue behind it on the GPU, as a token's graph does.
+struct PlServer {
+    struct Job {
+        int layer;
+        uint32_t seq;
+        bool fused;
+    };
+    std::thread th;
+    std::mutex m;
+    std::condition_variable cv, cv_idle;
+    std::deque<Job> q;
+    int busy = 0;                      // queued and being served
+    bool quit = false;
+    int err = 0;                       // the first failure (MOE_OK = 0: none), reported at the next sync point
+    std::string msg;
+};
+
 struct moe_cache {
     moe_cache_config cfg{};
     bool host_only = false;            // device < 0: state machine only, no HIP calls
@@ -234,6 +254,7 @@ struct moe_cache {
     std::vector<hipStream_t> pl_streams;        // streams the calls ran on
     bool pl_synced = false;                     // those streams were synchronised since the last call
     bool pl_hot = false;                        // the host team spins between layers
+    std::unique_ptr<PlServer> pls;              // serves the host's share of those layers
     bool sc_tested = false;                     // the serving channel passed its self-test
     uint64_t clock = 0, n_steps = 0, n_uploads = 0, n_scheduled = 0, n_copied = 0, n_published = 0;
     uint64_t n_admit_ok = 0, n_admit_denied = 0, n_table_flushes = 0, bytes_uploaded = 0;
@@ -300,6 +321,8 @@ struct moe_cache {
     double online_recall = 0.0;
     bool spec_probation = false;               // LLAMA_MOE_SPEC_PROBATION (patches/0007:149-153)
 };
+
+static void pl_server_stop(moe_cache *c);
 
 struct moe_pool {
     int n_layers = 0, capacity = 0, device = 0;
@@ -1333,6 +1356,7 @@ void free_cache(moe_cache *c) {
     hipFree(c->out_buf);
     if (c->up_stream) hipStreamDestroy(c->up_stream);
     if (c->stg_stream) hipStreamDestroy(c->stg_stream);
+    pl_server_stop(c);
     if (c->team) mpc::team_destroy(c->team);
     for (void *p : {(void *)c->sc_post, (void *)c->sc_resp, (void *)c->sc_rows, (void *)c->h_seq})
         if (p) hipHostFree(p);
@@ -2443,11 +2467,16 @@ int moe_cache_set_decode_path(moe_cache *c, int split, int graph) {
 }
 
 static int sc_buffers(moe_cache *c);
+static int pl_server_drain(moe_cache *c);
 static bool logits_ready(const mp::SidecarPost &p, int E, int n_q8_words, uint32_t seq, int &n_lg, int &n_q8);
 
 int moe_cache_set_sidecar(moe_cache *c, int n_threads, int num, int den) {
     if (!c) return fail(MOE_ERR_ARG, "null cache");
     if (c->host_only) return fail(MOE_ERR_STATE, "host-only cache (device < 0) cannot decode");
+    if (c->pls) {                       // layers queued by per-layer calls are served first
+        const int r = pl_server_drain(c);
+        if (r != MOE_OK) return r;
+    }
     if (n_threads <= 0) {
         if (c->sc_den) drop_graphs(c);
         c->sc_den = c->sc_num = 0;
@@ -2687,6 +2716,73 @@ static int sidecar_serve(moe_cache *c, int l, uint32_t seq, bool by_logits) {
     std::atomic_thread_fence(std::memory_order_release);
     *(volatile uint32_t *)&c->sc_resp[l].seq = seq;
     return MOE_OK;
+}
+
+// ---- the per-layer server (see PlServer) ------------------------------------
+static void pl_server_main(moe_cache *c) {
+    PlServer &sv = *c->pls;
+    for (;;) {
+        PlServer::Job j;
+        bool failed;
+        {
+            std::unique_lock<std::mutex> lk(sv.m);
+            sv.cv.wait(lk, [&] { return sv.quit || !sv.q.empty(); });
+            if (sv.q.empty()) return;
+            j = sv.q.front();
+            sv.q.pop_front();
+            failed = sv.err != MOE_OK || sv.quit;
+        }
+        const int r = failed ? MOE_OK : sidecar_serve(c, j.layer, j.seq, j.fused);
+        // after a failure no later layer is served: end each one's join at once
+        if (failed || r != MOE_OK) *(volatile uint32_t *)&c->sc_resp[j.layer].seq = mp::SC_ABORT;
+        std::lock_guard<std::mutex> lk(sv.m);
+        if (r != MOE_OK && sv.err == MOE_OK) {
+            sv.err = r;
+            sv.msg = g_err;             // (the message was this thread's)
+        }
+        if (--sv.busy == 0) sv.cv_idle.notify_all();
+    }
+}
+
+static void pl_server_push(moe_cache *c, int layer, uint32_t seq, bool fused) {
+    if (!c->pls) {
+        c->pls.reset(new PlServer);
+        c->pls->th = std::thread(pl_server_main, c);
+    }
+    PlServer &sv = *c->pls;
+    std::lock_guard<std::mutex> lk(sv.m);
+    sv.q.push_back({layer, seq, fused});
+    ++sv.busy;
+    sv.cv.notify_one();
+}
+
+// Wait until every queued layer is served (each serve is bounded by its wait
+// for the GPU's post, sc_timeout_s); the first failure, with its message.
+static int pl_server_drain(moe_cache *c) {
+    if (!c->pls) return MOE_OK;
+    PlServer &sv = *c->pls;
+    std::unique_lock<std::mutex> lk(sv.m);
+    const double limit = (c->sc_timeout_s + 1.0) * std::max(1, sv.busy);
+    if (!sv.cv_idle.wait_for(lk, std::chrono::duration<double>(limit), [&] { return sv.busy == 0; }))
+        return fail(MOE_ERR_HIP, "the host's share of the queued layers was not served within %.1f s", limit);
+    if (sv.err == MOE_OK) return MOE_OK;
+    const int e = sv.err;
+    const std::string msg = sv.msg;
+    sv.err = MOE_OK;
+    sv.msg.clear();
+    return fail(e, "%s", msg.c_str());
+}
+
+static void pl_server_stop(moe_cache *c) {
+    if (!c->pls) return;
+    pl_server_drain(c);
+    {
+        std::lock_guard<std::mutex> lk(c->pls->m);
+        c->pls->quit = true;
+    }
+    c->pls->cv.notify_all();
+    if (c->pls->th.joinable()) c->pls->th.join();
+    c->pls.reset();
 }
 
 int moe_cache_set_sidecar_batch(moe_cache *c, int num, int den) {
@@ -2985,7 +3081,9 @@ static int account_times(moe_cache *c, int l, bool fused, bool sc, bool have_ids
 // ---- one layer per call ---------------------------------------------------------
 static int pl_sync(moe_cache *c) {
     if (c->pl_synced) return MOE_OK;
+    const int r = pl_server_drain(c);          // the host's share of every queued layer
     for (hipStream_t s : c->pl_streams) HIPCHK(hipStreamSynchronize(s));
+    if (r != MOE_OK) return r;
     c->pl_synced = true;
     return MOE_OK;
 }
@@ -3090,6 +3188,19 @@ int moe_decode_layer(moe_cache *c, int layer, const float *x, const float *bias,
         *(volatile uint32_t *)&c->sc_resp[layer].seq = 0;
         *(volatile uint32_t *)&c->sc_resp[layer].err = 0;
     }
+    // an earlier layer's serving failed: report it before launching more
+    if (c->pls) {
+        bool failed;
+        {
+            std::lock_guard<std::mutex> lk(c->pls->m);
+            failed = c->pls->err != MOE_OK;
+        }
+        if (failed) {
+            r = pl_server_drain(c);
+            for (hipStream_t s : c->pl_streams) hipStreamSynchronize(s);
+            return r;
+        }
+    }
     const uint32_t seq = next_seq(c);
     r = decode_layer_impl(c, layer, x, bias, out, ids_dev, w_dev, st,
                           c->timing ? c->tev.data() + (size_t)layer * 12 : nullptr, stage, sc, fused, seq);
@@ -3097,19 +3208,12 @@ int moe_decode_layer(moe_cache *c, int layer, const float *x, const float *bias,
         hipStreamSynchronize(st);
         return r;
     }
-    if (sc) {
+    if (sc) {                           // the host's share: served by the server thread, in call order
         if (!c->pl_hot) {
             mpc::team_hot(c->team, true);
             c->pl_hot = true;
         }
-        r = sidecar_serve(c, layer, seq, fused);
-        if (r != MOE_OK) {              // end the join's wait, and let every kernel finish
-            *(volatile uint32_t *)&c->sc_resp[layer].seq = mp::SC_ABORT;
-            hipStreamSynchronize(st);
-            *(volatile uint32_t *)&c->sc_resp[layer].seq = 0;
-            *(volatile uint32_t *)&c->sc_resp[layer].err = 0;
-            return r;
-        }
+        pl_server_push(c, layer, seq, fused);
     }
     uint8_t &f = c->pl_flags[(size_t)layer];
     f = (uint8_t)((f & PL_DECODED ? PL_AGAIN : 0) | PL_DECODED | (fused ? PL_FUSED : 0) | (sc ? PL_SIDECAR : 0) |
@@ -3603,6 +3707,7 @@ int moe_decode_batch(moe_cache *c, const float *x, const float *bias, float *out
     // would serialise every layer on the CPU and pin 2 n_tok K H floats
     const int sh_num = c->sb_den ? c->sb_num : c->sc_num, sh_den = c->sb_den ? c->sb_den : c->sc_den;
     const bool sc = c->sc_den > 0 && sh_num > 0 && n_tok <= MOE_BATCH_HOST_MAX_TOKENS;
+    if (c->pls && (r = pl_server_drain(c)) != MOE_OK) return r;     // the team is the server's until then
     if (sc && (r = batch_sidecar_buffers(c, n_tok)) != MOE_OK) return r;
     float gms[2] = {0.0f, 0.0f};
     if (sc) mpc::team_hot(c->team, true);

@@ -11,7 +11,7 @@
  * out = sum_k w_k * y_k accumulated in k order (patches/0009-moe-sidecar.patch:
  * 697-703: experts = host_rows + cached_rows, times the weights, summed).
  *
- * Expert byte layout (this build's host store and slot pool): one expert is
+ * Expert byte layout (the library's host store and slot pool): one expert is
  * [up: I rows x H/256 Q4_K blocks][gate: same][down: H rows x I/256 blocks].
  */
 #include "oracle.h"

@@ -476,7 +476,8 @@ def test_decode_layer_by_layer(tmp_path, case):
     x_l + out_l (fp32, the same bits on the host), so no layer's input exists
     before the layer below has run.  Per token: every layer through
     moe_decode_layer (the fused launch, or split 3's launches; with the
-    sidecar the call serves the host's share before it returns), the ids
+    sidecar the call returns once its layer is launched and the cache's
+    server thread serves the host's share in call order), the ids
     observed -- after the token, or after each layer as the reference's
     callback does (`each`, with early issue: uploads start mid-token) -- and
     one step.  Ids, frames, route and map traces and outputs equal the
