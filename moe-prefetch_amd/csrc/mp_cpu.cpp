@@ -527,8 +527,13 @@ void team_hot(Team *t, bool on) { t->hot(on); }
 
 // ---- the chain -----------------------------------------------------------------
 namespace {
-constexpr int UP_ROWS = 16;     // up/gate rows per work item
-constexpr int DN_ROWS = 32;     // down rows per work item
+// Rows per work item.  Measured on the 48-layer decode with 14 threads (the
+// host's compute per layer is the critical path there): 8/16, 8/32, 16/16 ran
+// 321-350 tok/s; 16/32 393-415; 32/64 451-479; 64/128 484-488; 64/64 475-495;
+// 128/128 452-458 (6 up/gate items an expert leave threads idle).  Long runs
+// of contiguous rows per thread read DRAM better than many short ones.
+constexpr int UP_ROWS = 64;     // up/gate rows per work item
+constexpr int DN_ROWS = 64;     // down rows per work item
 
 struct Chain {
     const CpuExpert *e;
