@@ -604,7 +604,8 @@ def window(s0, s1, steps, t0_s=None):
             "admit_denied_per_token": round((s1["n_admit_denied"] - s0["n_admit_denied"]) / steps, 2),
             "cpu_served_per_token": round((s1["n_cpu_served"] - s0["n_cpu_served"]) / steps, 2),
             "publication_wait_ms_per_token": round((s1["publication_wait_us"] - s0["publication_wait_us"])
-                                                   / 1e3 / steps, 4)}
+                                                   / 1e3 / steps, 4),
+            "host_boundary_ms_per_token": round((s1["host_boundary_us"] - s0["host_boundary_us"]) / 1e3 / steps, 4)}
 
 
 def run_default(args):
