@@ -574,7 +574,12 @@ void down_item(const Chain &c, int item) {
     const size_t rb_in = (size_t)(c.H / QK) * Q4K_BYTES;
     const size_t rb = (size_t)(c.I / QK) * (c.down_type == mp::TYPE_Q6K ? Q6K_BYTES : Q4K_BYTES);
     const uint8_t *down = c.e[k].w + 2 * (size_t)c.I * rb_in;
-    while (!c.ready[k].load(std::memory_order_acquire)) _mm_pause();
+    if (!c.ready[k].load(std::memory_order_acquire)) {
+        // h is not ready yet: fetch this item's rows meanwhile (one expert a
+        // layer leaves DRAM headroom while its up/gate items run)
+        prefetch_rows(c.down_type, down + r0 * rb, rb, DN_ROWS, c.I / QK);
+        while (!c.ready[k].load(std::memory_order_acquire)) _mm_pause();
+    }
     const uint8_t *q = c.q8h + (size_t)k * (c.I / QK) * Q8K_BYTES;
     dot_rows(c.down_type, down + r0 * rb, rb, DN_ROWS, q, c.I / QK, c.e[k].y + r0);
 }
