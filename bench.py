@@ -1338,7 +1338,7 @@ def parse_args(argv=None):
                     help="0 fused layer launch, 1 fork/join, 2 serial expert launches, 3 unfused launches")
     ap.add_argument("--sidecar", type=int, default=-1,
                     help="host threads serving absent experts (0: GPU only; default: 14 on a 16-CPU host)")
-    ap.add_argument("--batch-share", default="2/3", help="num/den: the host's share of absent experts in batched "
+    ap.add_argument("--batch-share", default="3/4", help="num/den: the host's share of absent experts in batched "
                                                           "decode (wide40's batch phase; empty: --share)")
     ap.add_argument("--share", default="1/1", help="num/den: absent experts of rank r with r %% den < num go to "
                                                    "the CPU")
