@@ -224,9 +224,11 @@ static inline void q4k_scales8(const uint8_t *s, uint64_t &sc, uint64_t &mn) {
     mn = (uint64_t)mn_lo | ((uint64_t)mn_hi << 32);
 }
 
-// Prefetch: the same super-block of the next group of four rows (a row is only
-// 6-18 lines, too short for the hardware's stream detection to run ahead),
-// when the caller says a next group follows.
+// Prefetch: the same super-block of the group of four rows two groups ahead
+// (a row is only 6-18 lines, too short for the hardware's stream detection to
+// run ahead), when the caller says such a group follows.  Two groups ahead
+// measured ~4 % faster than one on the 48-layer decode (494-501 against
+// 470-482 tok/s); a non-temporal hint was no better.
 void prefetch_rows(int type, const uint8_t *row0, size_t stride, int nrows, int nb) {
     const size_t bytes = (size_t)nb * (type == mp::TYPE_Q6K ? Q6K_BYTES : Q4K_BYTES);
     for (int r = 0; r < nrows; ++r)
@@ -267,7 +269,7 @@ MPC_AVX512 static void rows_q4k_vnni(const uint8_t *row0, size_t stride, const u
                 a = _mm512_dpwssd_epi32(a, _mm512_maddubs_epi16(w[g], xv[g]), _mm512_permutexvar_epi16(gidx[g], sc16));
             si[r] = a;
             if (more) {
-                const char *pf = (const char *)(b + 4 * stride);
+                const char *pf = (const char *)(b + 8 * stride);
                 _mm_prefetch(pf, _MM_HINT_T0);
                 _mm_prefetch(pf + 64, _MM_HINT_T0);
                 _mm_prefetch(pf + 128, _MM_HINT_T0);
@@ -339,7 +341,7 @@ MPC_AVX512 static void rows_q6k_vnni(const uint8_t *row0, size_t stride, const u
             so[r] = _mm512_zextsi256_si512(_mm256_madd_epi16(sc16, bs));      // sum_c scale_c * bsum_c
             dh[r] = u16_at(b + 208);
             if (more)
-                for (int l = 0; l < 4; ++l) _mm_prefetch((const char *)(b + 4 * stride + 64 * l), _MM_HINT_T0);
+                for (int l = 0; l < 4; ++l) _mm_prefetch((const char *)(b + 8 * stride + 64 * l), _MM_HINT_T0);
         }
         for (int r = NR; r < 4; ++r) si[r] = so[r] = _mm512_setzero_si512();
         const __m128i sum_dot = hsum4(si[0], si[1], si[2], si[3]);
@@ -355,11 +357,11 @@ MPC_AVX512 static void rows_q6k_vnni(const uint8_t *row0, size_t stride, const u
 
 MPC_AVX512 static void rows_vnni(int type, const uint8_t *row0, size_t stride, int nrows, const uint8_t *q8, int nb,
                                  float *out) {
-    prefetch_rows(type, row0, stride, std::min(nrows, 4), nb);     // the first group; each group fetches the next
+    prefetch_rows(type, row0, stride, std::min(nrows, 8), nb);     // the first two groups; each group fetches the one two ahead
     int r = 0;
     for (; r + 4 <= nrows; r += 4)
         (type == mp::TYPE_Q6K ? rows_q6k_vnni<4> : rows_q4k_vnni<4>)(row0 + (size_t)r * stride, stride, q8, nb, out + r,
-                                                                      r + 8 <= nrows);
+                                                                      r + 12 <= nrows);
     for (; r < nrows; ++r)
         (type == mp::TYPE_Q6K ? rows_q6k_vnni<1> : rows_q4k_vnni<1>)(row0 + (size_t)r * stride, stride, q8, nb, out + r,
                                                                       false);
@@ -554,8 +556,8 @@ void up_item(Chain &c, int item) {
     const uint8_t *up = c.e[k].w, *gate = c.e[k].w + (size_t)c.I * rb;
     float *h = c.h + (size_t)k * c.I;
     float u[UP_ROWS], g[UP_ROWS];
-    prefetch_rows(mp::TYPE_Q4K, up + r0 * rb, rb, 4, c.H / QK);       // both first groups at once
-    prefetch_rows(mp::TYPE_Q4K, gate + r0 * rb, rb, 4, c.H / QK);
+    prefetch_rows(mp::TYPE_Q4K, up + r0 * rb, rb, 8, c.H / QK);       // the first two groups of both at once
+    prefetch_rows(mp::TYPE_Q4K, gate + r0 * rb, rb, 8, c.H / QK);
     dot_rows(mp::TYPE_Q4K, up + r0 * rb, rb, UP_ROWS, c.e[k].q8x, c.H / QK, u);
     dot_rows(mp::TYPE_Q4K, gate + r0 * rb, rb, UP_ROWS, c.e[k].q8x, c.H / QK, g);
     for (int r = 0; r < UP_ROWS; ++r) h[r0 + r] = g[r] / (1.0f + canon_expf(-g[r])) * u[r];
@@ -611,8 +613,8 @@ void gup_item(GChain &c, int item) {
     const CpuGroup &g = c.g[k];
     const size_t rb = (size_t)(c.H / QK) * Q4K_BYTES;
     const uint8_t *up = g.w, *gate = g.w + (size_t)c.I * rb;
-    prefetch_rows(mp::TYPE_Q4K, up + r0 * rb, rb, 4, c.H / QK);
-    prefetch_rows(mp::TYPE_Q4K, gate + r0 * rb, rb, 4, c.H / QK);
+    prefetch_rows(mp::TYPE_Q4K, up + r0 * rb, rb, 8, c.H / QK);
+    prefetch_rows(mp::TYPE_Q4K, gate + r0 * rb, rb, 8, c.H / QK);
     for (int j = g.first; j < g.first + g.n; ++j) {
         float u[UP_ROWS], gg[UP_ROWS];
         dot_rows(mp::TYPE_Q4K, up + r0 * rb, rb, UP_ROWS, c.q8x[j], c.H / QK, u);
