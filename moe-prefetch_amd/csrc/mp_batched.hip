@@ -304,20 +304,24 @@ __device__ inline void q6_frag(const uint8_t *blk, int h, half8_t bh[8], half8_t
 // fragment read touches fall in distinct banks.
 constexpr int GT = 32;   // pairs per pass (2 M tiles of 16)
 
-struct __attribute__((aligned(16))) AStage {
-    _Float16 a[GT][QK];
-    _Float16 bs[GT][16];
+// R activation rows (32, or 16 for one M tile) and the group sums of up to 32
+template <int R>
+struct __attribute__((aligned(16))) AStageR {
+    _Float16 a[R][QK];
+    _Float16 bs[32][16];
 };
+using AStage = AStageR<GT>;
 
 // Direct global -> LDS loads: lane l of an instruction writes base + 16*l.
 // rows[r]: activation row of pair r of the pass (r < np); rows are K values
-// long.  Wave w stages rows 8w .. 8w+7 (two per instruction), wave 0 also the
-// group sums.  Rows past np are not loaded.
-__device__ inline void stage_a(AStage &st, const int *rows, int np, const uint16_t *xa, const uint16_t *xbs, int K,
-                               int s, int wave, int lane) {
+// long.  Wave w stages rows (R/4)w .. (R/4)w + R/4 - 1 (two per instruction),
+// wave 0 also the group sums.  Rows past np are not loaded.
+template <int R>
+__device__ inline void stage_a(AStageR<R> &st, const int *rows, int np, const uint16_t *xa, const uint16_t *xbs,
+                               int K, int s, int wave, int lane) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const int r0 = 8 * wave + 2 * j;
+    for (int j = 0; j < R / 8; ++j) {
+        const int r0 = (R / 4) * wave + 2 * j;
         if (r0 >= np) break;
         const int r = min(r0 + (lane >> 5), np - 1);
         const int c = (lane & 31) ^ ((r0 + (lane >> 5)) & 15);
@@ -331,7 +335,8 @@ __device__ inline void stage_a(AStage &st, const int *rows, int np, const uint16
     }
 }
 
-__device__ inline half8_t stage_frag(const AStage &st, int r, int off) {
+template <int R>
+__device__ inline half8_t stage_frag(const AStageR<R> &st, int r, int off) {
     const int c = (off >> 3) ^ (r & 15);
     return *(const half8_t *)&st.a[r][8 * c];
 }
@@ -619,16 +624,21 @@ hipError_t launch_swiglu_quant(const float *y2, int P, int I, float *h_out, uint
 
 // ---------------------------------------------------------------------------
 // The Q4_K grouped product with the weights read and decoded once per chunk
-// of up to CH passes (CH * 32 pairs): for each super-block s, the lane's
+// of up to CH passes (CH * 16 * MT pairs): for each super-block s, the lane's
 // weights are loaded once (block s+1 in flight meanwhile) and turned into the
 // eight MFMA B operands once, then every pass of the chunk multiplies its
 // staged activation rows by them.  Each pair still accumulates its
 // super-blocks in order 0, 1, ..., so the arithmetic is the one-pass kernel's.
 // CH = 2 for large batches, (256, 3): up to 168 registers, which the eight
 // operands of two passes need; CH = 1 when experts rarely get more than 32
-// pairs, (256, 4): four waves per SIMD.
-template <int NB, bool DOWN, int CH>
+// pairs, (256, 4): four waves per SIMD.  MT = 1 (one 16-row M tile a pass)
+// when experts average at most 8 pairs: half the staged rows and products,
+// which would be empty anyway (batch 64 at 128 experts: up/gate 67.0 -> 63.4
+// us a launch, batch 16: 53.1 -> 51.1).  The (256, 5) bound that MT = 1
+// nearly fits spills and was no faster.
+template <int NB, bool DOWN, int CH, int MT>
 __global__ __launch_bounds__(256, CH == 1 ? 4 : 3) void grouped_q4_kernel(GroupedArgs a) {
+    constexpr int GK = 16 * MT;           // pairs per pass: MT M tiles of 16
     int e, tile;
     tile_expert(blockIdx.x, (DOWN ? a.H : 2 * a.I) / 64, a.E, tile, e);
     const int n0 = a.offsets[e], ne = a.offsets[e + 1] - n0;
@@ -655,33 +665,33 @@ __global__ __launch_bounds__(256, CH == 1 ? 4 : 3) void grouped_q4_kernel(Groupe
     const uint16_t *abs16 = DOWN ? a.hbs : a.xbs;
     const float *adx = DOWN ? a.hdx : a.xdx;
 
-    __shared__ AStage st[2];
-    __shared__ int s_rows[CH * GT];
-    __shared__ __attribute__((aligned(16))) float s_dx[NB][CH * GT];   // [block][pair]: a lane's 4 rows in one read
+    __shared__ AStageR<GK> st[2];
+    __shared__ int s_rows[CH * GK];
+    __shared__ __attribute__((aligned(16))) float s_dx[NB][CH * GK];   // [block][pair]: a lane's 4 rows in one read
     const uint8_t *wrow = mat + (size_t)row * ROWB;
     const int gm = (h >> 1) + 2 * (h & 1);
 
-    for (int cb = 0; cb < ne; cb += CH * GT) {
-        const int npc = min(CH * GT, ne - cb);
-        const int nps = (npc + GT - 1) / GT;
-        if (tid < CH * GT) {
+    for (int cb = 0; cb < ne; cb += CH * GK) {
+        const int npc = min(CH * GK, ne - cb);
+        const int nps = (npc + GK - 1) / GK;
+        if (tid < CH * GK) {
             const int pos = n0 + cb + min(tid, npc - 1);
             s_rows[tid] = DOWN ? pos : a.perm[pos] / a.K;
         }
         __syncthreads();
-        for (int i = tid; i < CH * GT * NB; i += 256) s_dx[i % NB][i / NB] = adx[(size_t)s_rows[i / NB] * NB + (i % NB)];
-        stage_a(st[0], s_rows, min(GT, npc), act, abs16, K, 0, wave, lane);
+        for (int i = tid; i < CH * GK * NB; i += 256) s_dx[i % NB][i / NB] = adx[(size_t)s_rows[i / NB] * NB + (i % NB)];
+        stage_a(st[0], s_rows, min(GK, npc), act, abs16, K, 0, wave, lane);
         uint4 cw[3], nw[3];
         cw[0] = *(const uint4 *)wrow;
         cw[1] = *(const uint4 *)(wrow + 16 + 16 * h);
         cw[2] = *(const uint4 *)(wrow + 80 + 16 * h);
         __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
-        float y[CH][2][4];
+        float y[CH][MT][4];
 #pragma unroll
         for (int p = 0; p < CH; ++p)
 #pragma unroll
-            for (int t = 0; t < 2; ++t)
+            for (int t = 0; t < MT; ++t)
 #pragma unroll
                 for (int i = 0; i < 4; ++i) y[p][t][i] = 0.0f;
         int j = 0;                       // step j = s * nps + p
@@ -706,22 +716,24 @@ __global__ __launch_bounds__(256, CH == 1 ? 4 : 3) void grouped_q4_kernel(Groupe
 #pragma unroll
             for (int p = 0; p < CH; ++p) {
                 if (p < nps) {
-                    const AStage &S = st[j & 1];
+                    const AStageR<GK> &S = st[j & 1];
                     const int jn = j + 1;
                     if (jn < NB * nps) {
                         const int s2 = jn / nps, p2 = jn - s2 * nps;
-                        stage_a(st[jn & 1], s_rows + p2 * GT, min(GT, npc - p2 * GT), act, abs16, K, s2, wave, lane);
+                        stage_a(st[jn & 1], s_rows + p2 * GK, min(GK, npc - p2 * GK), act, abs16, K, s2, wave, lane);
                     }
-                    float4_t acc[2] = {{0, 0, 0, 0}, {0, 0, 0, 0}};
-                    // the fragments of K chunk i+1 are read before chunk i's products
-                    half8_t fa[2][2];
+                    float4_t acc[MT];
 #pragma unroll
-                    for (int t = 0; t < 2; ++t) fa[0][t] = stage_frag(S, 16 * t + n, q4_a_offset(h, 0));
+                    for (int t = 0; t < MT; ++t) acc[t] = float4_t{0, 0, 0, 0};
+                    // the fragments of K chunk i+1 are read before chunk i's products
+                    half8_t fa[2][MT];
+#pragma unroll
+                    for (int t = 0; t < MT; ++t) fa[0][t] = stage_frag(S, 16 * t + n, q4_a_offset(h, 0));
 #pragma unroll
                     for (int i = 0; i < 8; ++i) {
                         if (i + 1 < 8) {
 #pragma unroll
-                            for (int t = 0; t < 2; ++t)
+                            for (int t = 0; t < MT; ++t)
                                 fa[(i + 1) & 1][t] = stage_frag(S, 16 * t + n, q4_a_offset(h, i + 1 < 8 ? i + 1 : 0));
                         }
                         half8_t bi;
@@ -732,13 +744,13 @@ __global__ __launch_bounds__(256, CH == 1 ? 4 : 3) void grouped_q4_kernel(Groupe
                             bi = q4_b(L ? cw[2] : cw[1], i, sc.sc[L][nib]);
                         }
 #pragma unroll
-                        for (int t = 0; t < 2; ++t) acc[t] = mfma32(fa[i & 1][t], bi, acc[t]);
+                        for (int t = 0; t < MT; ++t) acc[t] = mfma32(fa[i & 1][t], bi, acc[t]);
                     }
-                    float4 dxv[2];
+                    float4 dxv[MT];
 #pragma unroll
-                    for (int t = 0; t < 2; ++t) dxv[t] = *(const float4 *)&s_dx[s][p * GT + 16 * t + 4 * h];
+                    for (int t = 0; t < MT; ++t) dxv[t] = *(const float4 *)&s_dx[s][p * GK + 16 * t + 4 * h];
 #pragma unroll
-                    for (int t = 0; t < 2; ++t) {
+                    for (int t = 0; t < MT; ++t) {
                         const half4_t am = *(const half4_t *)&S.bs[16 * t + n][4 * gm];
                         float4_t z = {0, 0, 0, 0};
                         z = __builtin_amdgcn_mfma_f32_16x16x16f16(am, sc.bm, z, 0, 0, 0);
@@ -762,10 +774,10 @@ __global__ __launch_bounds__(256, CH == 1 ? 4 : 3) void grouped_q4_kernel(Groupe
 #pragma unroll
         for (int p = 0; p < CH; ++p) {
 #pragma unroll
-            for (int t = 0; t < 2; ++t) {
+            for (int t = 0; t < MT; ++t) {
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
-                    const int r = p * GT + 16 * t + 4 * h + i;
+                    const int r = p * GK + 16 * t + 4 * h + i;
                     if (r < npc) {
                         const int pos = n0 + cb + r;
                         if (DOWN) {
@@ -788,6 +800,7 @@ static hipError_t launch_gg(const GroupedArgs &a, hipStream_t st, hipEvent_t e0,
     const int nb = (DOWN ? a.I : a.H) / QK;
     const dim3 grid((unsigned)(rows / 64 * a.E)), blk(256);     // (row tile, expert) from the linear id
     const bool two = a.P > 16 * a.E;                            // many experts above 32 pairs
+    const bool one = a.P <= 8 * a.E;                            // few pairs: one 16-row M tile a pass
     if (DOWN) {
         if (a.down_type == TYPE_Q6K) {
             if (nb == 3) return launch_b(grouped_gemm_kernel<3, TYPE_Q6K, true>, grid, blk, st, e0, e1, a);
@@ -795,16 +808,22 @@ static hipError_t launch_gg(const GroupedArgs &a, hipStream_t st, hipEvent_t e0,
             return launch_b(grouped_gemm_kernel<1, TYPE_Q6K, true>, grid, blk, st, e0, e1, a);
         }
         if (two) {
-            if (nb == 3) return launch_b(grouped_q4_kernel<3, true, 2>, grid, blk, st, e0, e1, a);
-            if (nb == 2) return launch_b(grouped_q4_kernel<2, true, 2>, grid, blk, st, e0, e1, a);
-            return launch_b(grouped_q4_kernel<1, true, 2>, grid, blk, st, e0, e1, a);
+            if (nb == 3) return launch_b(grouped_q4_kernel<3, true, 2, 2>, grid, blk, st, e0, e1, a);
+            if (nb == 2) return launch_b(grouped_q4_kernel<2, true, 2, 2>, grid, blk, st, e0, e1, a);
+            return launch_b(grouped_q4_kernel<1, true, 2, 2>, grid, blk, st, e0, e1, a);
         }
-        if (nb == 3) return launch_b(grouped_q4_kernel<3, true, 1>, grid, blk, st, e0, e1, a);
-        if (nb == 2) return launch_b(grouped_q4_kernel<2, true, 1>, grid, blk, st, e0, e1, a);
-        return launch_b(grouped_q4_kernel<1, true, 1>, grid, blk, st, e0, e1, a);
+        if (one) {
+            if (nb == 3) return launch_b(grouped_q4_kernel<3, true, 1, 1>, grid, blk, st, e0, e1, a);
+            if (nb == 2) return launch_b(grouped_q4_kernel<2, true, 1, 1>, grid, blk, st, e0, e1, a);
+            return launch_b(grouped_q4_kernel<1, true, 1, 1>, grid, blk, st, e0, e1, a);
+        }
+        if (nb == 3) return launch_b(grouped_q4_kernel<3, true, 1, 2>, grid, blk, st, e0, e1, a);
+        if (nb == 2) return launch_b(grouped_q4_kernel<2, true, 1, 2>, grid, blk, st, e0, e1, a);
+        return launch_b(grouped_q4_kernel<1, true, 1, 2>, grid, blk, st, e0, e1, a);
     }
-    return two ? launch_b(grouped_q4_kernel<8, false, 2>, grid, blk, st, e0, e1, a)
-               : launch_b(grouped_q4_kernel<8, false, 1>, grid, blk, st, e0, e1, a);
+    if (two) return launch_b(grouped_q4_kernel<8, false, 2, 2>, grid, blk, st, e0, e1, a);
+    if (one) return launch_b(grouped_q4_kernel<8, false, 1, 1>, grid, blk, st, e0, e1, a);
+    return launch_b(grouped_q4_kernel<8, false, 1, 2>, grid, blk, st, e0, e1, a);
 }
 
 hipError_t launch_gateup_grouped(const GroupedArgs &a, hipStream_t st, hipEvent_t e0, hipEvent_t e1) {

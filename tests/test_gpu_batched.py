@@ -213,6 +213,9 @@ GROUPED_CASES = {
     "q4k_i256_t150_e64_crowded": (_lib.TYPE_Q4K, 256, 150, 64, "crowd", "f32"),
     "q4k_i768_t24_repeated_ids": (_lib.TYPE_Q4K, 768, 24, 128, "repeat", "bf16"),
     "q6k_i512_t40_ids_with_replacement": (_lib.TYPE_Q6K, 512, 40, 128, "dups", "f32"),
+    # at most 8 pairs per expert on average: one 16-row M tile a pass
+    "q4k_i256_t20_one_tile": (_lib.TYPE_Q4K, 256, 20, 128, "uniform", "bf16"),
+    "q4k_i512_t100_crowded_one_tile": (_lib.TYPE_Q4K, 512, 100, 128, "crowd", "f32"),
 }
 
 
