@@ -358,18 +358,18 @@ __device__ inline void tile_expert(int L, int T, int E, int &tile, int &e) {
     }
 }
 
-// The grouped product of one (64-row tile, expert): rows of the expert's
-// matrix (up and gate as one 2I-row matrix, or down) against the activation
-// rows of every pair dispatched to the expert, K = NB*256.  Workgroup = 4
-// waves of 16 rows.  Each pass covers up to 32 pairs: block s+1 of their
-// activations is staged in LDS, and block s+1 of the lane's Q4_K row loaded
-// into registers, while block s is decoded and multiplied; a Q6_K tile (rows
-// only 2-byte aligned) is copied into LDS once with direct loads.  up/gate: y2[pair position][row]; down: the pair's
-// gate weight times y, to the pair's (t*K + k) row.
-// (256, 4): at most 128 registers, so four waves share each SIMD and one wave's
-// loads hide behind another's dequantization
+// The grouped product of one (64-row tile, expert) for a Q6_K matrix (down in
+// the mixed layers): the tile's rows against the activation rows of every pair
+// dispatched to the expert, K = NB*256.  Workgroup = 4 waves of 16 rows.  The
+// tile (rows only 2-byte aligned) is copied into LDS once, at the padded block
+// stride; each pass covers up to 32 pairs, block s+1 of their activations
+// staged in LDS while block s is decoded and multiplied.  up/gate (DOWN false):
+// y2[pair position][row]; down: the pair's gate weight times y, to the pair's
+// (t*K + k) row.  (256, 4): at most 128 registers.  Q4_K matrices take
+// grouped_q4_kernel.
 template <int NB, int DT, bool DOWN>
 __global__ __launch_bounds__(256, 4) void grouped_gemm_kernel(GroupedArgs a) {
+    static_assert(DT == TYPE_Q6K, "Q4_K matrices take grouped_q4_kernel");
     int e, tile;
     tile_expert(blockIdx.x, (DOWN ? a.H : 2 * a.I) / 64, a.E, tile, e);
     const int n0 = a.offsets[e], ne = a.offsets[e + 1] - n0;
@@ -380,7 +380,7 @@ __global__ __launch_bounds__(256, 4) void grouped_gemm_kernel(GroupedArgs a) {
     const int r0 = tile * 64;
     const int row = r0 + wave * 16 + n;
     constexpr int K = NB * QK;
-    constexpr int ROWB = NB * (DT == TYPE_Q6K ? Q6K_BYTES : Q4K_BYTES);
+    constexpr int ROWB = NB * Q6K_BYTES;
     const int out_n = DOWN ? a.H : 2 * a.I;   // columns of the output rows
     const uint8_t *base = grouped_expert(a, e);
     if (!base) {
@@ -399,11 +399,10 @@ __global__ __launch_bounds__(256, 4) void grouped_gemm_kernel(GroupedArgs a) {
     __shared__ AStage st[2];
     __shared__ int s_rows[GT];
     __shared__ float s_dx[GT][NB];
-    __shared__ __attribute__((aligned(16))) uint8_t s_w6[DT == TYPE_Q6K ? G6_LDS : 16];
+    __shared__ __attribute__((aligned(16))) uint8_t s_w6[G6_LDS];
 
-    const uint8_t *wrow = mat + (size_t)row * ROWB;   // the lane's Q4_K row
     constexpr int LROWB = NB * Q6K_PAD;               // a padded Q6_K row in LDS
-    if (DT == TYPE_Q6K) {
+    {
         // the wave's 16 rows into LDS at the padded block stride, 24 blocks
         // (16 * NB <= 48) at a time through registers
         const uint8_t *src = mat + (size_t)(r0 + 16 * wave) * ROWB;
@@ -425,92 +424,48 @@ __global__ __launch_bounds__(256, 4) void grouped_gemm_kernel(GroupedArgs a) {
         }
         __syncthreads();
         if (tid < GT * NB) s_dx[tid / NB][tid % NB] = adx[(size_t)s_rows[tid / NB] * NB + (tid % NB)];
-        // block 0: activations staged, the lane's weights in registers; then
-        // block s+1 is in flight (weights to registers, activations to LDS)
-        // while block s is multiplied
-        uint4 cw[3], nw[3];
+        // block 0's activations staged; then block s+1's are in flight while
+        // block s is multiplied
         stage_a(st[0], s_rows, np, act, abs16, K, 0, wave, lane);
-        if (DT == TYPE_Q4K) {
-            cw[0] = *(const uint4 *)wrow;
-            cw[1] = *(const uint4 *)(wrow + 16 + 16 * h);
-            cw[2] = *(const uint4 *)(wrow + 80 + 16 * h);
-        }
         __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
         float y[2][4] = {{0, 0, 0, 0}, {0, 0, 0, 0}};
-        const int gm = (h >> 1) + 2 * (h & 1);
 #pragma unroll 1
         for (int s = 0; s < NB; ++s) {
             const AStage &S = st[s & 1];
-            if (s + 1 < NB) {
-                stage_a(st[(s + 1) & 1], s_rows, np, act, abs16, K, s + 1, wave, lane);
-                if (DT == TYPE_Q4K) {
-                    const uint8_t *p = wrow + (s + 1) * Q4K_BYTES;
-                    nw[0] = *(const uint4 *)p;
-                    nw[1] = *(const uint4 *)(p + 16 + 16 * h);
-                    nw[2] = *(const uint4 *)(p + 80 + 16 * h);
-                }
-            }
+            if (s + 1 < NB) stage_a(st[(s + 1) & 1], s_rows, np, act, abs16, K, s + 1, wave, lane);
             float4_t acc[2] = {{0, 0, 0, 0}, {0, 0, 0, 0}};
-            float d, dmin = 0.0f;
-            half4_t bm;
-            if (DT == TYPE_Q4K) {
-                Q4Scales sc;
-                q4_scales(cw[0], h, sc);
-                d = sc.d;
-                dmin = sc.dmin;
-                bm = sc.bm;
+            float d;
+            half8_t bh[8], bl[8];
+            q6_frag(s_w6 + (size_t)(wave * 16 + n) * LROWB + (size_t)s * Q6K_PAD, h, bh, bl, d);
+            float4_t accl[2] = {{0, 0, 0, 0}, {0, 0, 0, 0}};
 #pragma unroll
-                for (int i = 0; i < 8; ++i) {
-                    const int L = i >> 2, nib = (i >> 1) & 1;
-                    const half8_t b = q4_b(L ? cw[2] : cw[1], i, sc.sc[L][nib]);
-                    const int off = q4_a_offset(h, i);
+            for (int i = 0; i < 8; ++i) {
+                const int off = 128 * (i >> 2) + 32 * (i & 3) + 8 * h;
 #pragma unroll
-                    for (int t = 0; t < 2; ++t) acc[t] = mfma32(stage_frag(S, 16 * t + n, off), b, acc[t]);
+                for (int t = 0; t < 2; ++t) {
+                    const half8_t av = stage_frag(S, 16 * t + n, off);
+                    acc[t] = mfma32(av, bh[i], acc[t]);
+                    accl[t] = mfma32(av, bl[i], accl[t]);
                 }
-            } else {
-                half8_t bh[8], bl[8];
-                q6_frag(s_w6 + (size_t)(wave * 16 + n) * LROWB + (size_t)s * Q6K_PAD, h, bh, bl, d);
-                float4_t accl[2] = {{0, 0, 0, 0}, {0, 0, 0, 0}};
-#pragma unroll
-                for (int i = 0; i < 8; ++i) {
-                    const int off = 128 * (i >> 2) + 32 * (i & 3) + 8 * h;
-#pragma unroll
-                    for (int t = 0; t < 2; ++t) {
-                        const half8_t av = stage_frag(S, 16 * t + n, off);
-                        acc[t] = mfma32(av, bh[i], acc[t]);
-                        accl[t] = mfma32(av, bl[i], accl[t]);
-                    }
-                }
-#pragma unroll
-                for (int t = 0; t < 2; ++t)
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) acc[t][i] = 16.0f * acc[t][i] + accl[t][i];   // exact integers
             }
             // both M tiles every time (no branch merges around the accumulators);
             // rows past the pass's pairs compute on stale LDS and are never written
 #pragma unroll
             for (int t = 0; t < 2; ++t) {
-                float4_t z = {0, 0, 0, 0};
-                if (DT == TYPE_Q4K) {
-                    const half4_t am = *(const half4_t *)&S.bs[16 * t + n][4 * gm];
-                    z = __builtin_amdgcn_mfma_f32_16x16x16f16(am, bm, z, 0, 0, 0);
-                }
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
-                    // ggml's order: acc += (d*dx)*sumi; acc -= (dmin*dx)*summ
+                    // the block's integer sum: |acc| <= 256 * 32 * 8 * 127 and
+                    // |accl| <= 256 * 32 * 15 * 127, both below 2^24, so exact,
+                    // and 16*acc + accl rounds once, as ggml's (float)sumi
+                    const float sumi = 16.0f * acc[t][i] + accl[t][i];
+                    // ggml's order: acc += (d*dx)*sumi
                     const float dx = s_dx[16 * t + 4 * h + i][s];
-                    y[t][i] = y[t][i] + (d * dx) * acc[t][i];
-                    if (DT == TYPE_Q4K) y[t][i] = y[t][i] - (dmin * dx) * z[i];
+                    y[t][i] = y[t][i] + (d * dx) * sumi;
                 }
             }
             __builtin_amdgcn_s_waitcnt(0);
             __syncthreads();
-            if (DT == TYPE_Q4K) {
-                cw[0] = nw[0];
-                cw[1] = nw[1];
-                cw[2] = nw[2];
-            }
         }
 #pragma unroll
         for (int t = 0; t < 2; ++t) {
@@ -722,7 +677,11 @@ __global__ __launch_bounds__(256, CH == 1 ? 4 : 3) void grouped_q4_kernel(Groupe
                         const int s2 = jn / nps, p2 = jn - s2 * nps;
                         stage_a(st[jn & 1], s_rows + p2 * GK, min(GK, npc - p2 * GK), act, abs16, K, s2, wave, lane);
                     }
-                    float4_t acc[MT];
+                    // each 128-value half of the super-block in its own accumulator:
+                    // a half's products sum to at most 128 * 63 * 15 * 127 < 2^24, so
+                    // it is exact in fp32, and one add gives ggml's (float)sumi (a
+                    // whole block's sum can pass 2^24, where a running fp32 sum rounds)
+                    float4_t acc[MT], acc0[MT];
 #pragma unroll
                     for (int t = 0; t < MT; ++t) acc[t] = float4_t{0, 0, 0, 0};
                     // the fragments of K chunk i+1 are read before chunk i's products
@@ -743,9 +702,18 @@ __global__ __launch_bounds__(256, CH == 1 ? 4 : 3) void grouped_q4_kernel(Groupe
                             const int L = i >> 2, nib = (i >> 1) & 1;
                             bi = q4_b(L ? cw[2] : cw[1], i, sc.sc[L][nib]);
                         }
+                        if (i == 4) {
+#pragma unroll
+                            for (int t = 0; t < MT; ++t) {
+                                acc0[t] = acc[t];
+                                acc[t] = float4_t{0, 0, 0, 0};
+                            }
+                        }
 #pragma unroll
                         for (int t = 0; t < MT; ++t) acc[t] = mfma32(fa[i & 1][t], bi, acc[t]);
                     }
+#pragma unroll
+                    for (int t = 0; t < MT; ++t) acc[t] = acc0[t] + acc[t];
                     float4 dxv[MT];
 #pragma unroll
                     for (int t = 0; t < MT; ++t) dxv[t] = *(const float4 *)&s_dx[s][p * GK + 16 * t + 4 * h];

@@ -14,7 +14,8 @@ the C ABI against the oracle on the same seeded inputs.
                        oracle, and in fact bit-exact (Q4_K and Q6_K down,
                        intermediate 768/512/256, batch 1..512, tokens crowding
                        a few experts into several passes, experts in HBM slots
-                       / a pinned host store / nowhere)
+                       / a pinned host store / nowhere, super-block sums past
+                       2**24)
 """
 import zlib
 
@@ -185,9 +186,12 @@ def rel_l2(a, b):
 
 
 def run_grouped(store, T, K, E, ids, w, x_dtype, table=None, slot_pool=None, slot_bytes=0, n_slots=0,
-                store_ptr=None, n_store=None, seed=0):
-    xf = torch.empty((T, H), dtype=torch.float32, device=DEV)
-    _lib.check(L().moe_synth_vec(seed, 1, 0, T, 7, 1, H, 1.0, xf.data_ptr(), stream()), "x")
+                store_ptr=None, n_store=None, seed=0, x_host=None):
+    if x_host is None:
+        xf = torch.empty((T, H), dtype=torch.float32, device=DEV)
+        _lib.check(L().moe_synth_vec(seed, 1, 0, T, 7, 1, H, 1.0, xf.data_ptr(), stream()), "x")
+    else:
+        xf = t_(x_host.astype(np.float32))
     x = xf.to(torch.bfloat16) if x_dtype == "bf16" else xf
     bm = BatchedMoe(T, n_experts=E, n_expert_used=K, intermediate=store.I)
     d_ids, d_w = t_(ids), t_(w)
@@ -249,6 +253,69 @@ def test_grouped_experts_vs_oracle(case):
     for k in range(1, K):
         acc = acc + s[:, k]
     assert np.array_equal(acc, out)
+
+
+class LargeSumStore:
+    """Experts whose Q4_K super-block sums pass 2**24 against near-uniform
+    activations: every six-bit scale and min 63 (scale bytes 0xFF), nibbles
+    8..15, d = 2**-14, dmin = 0.  A Q6_K down matrix gets scales of the
+    largest magnitude (-128..-120, 120..127) and quants 0..3 (q - 32 near -32)."""
+
+    def __init__(self, n, I, dt, seed=5):
+        rng = np.random.default_rng(seed)
+        self.n, self.I, self.dt = n, I, dt
+        self.eb = L().moe_expert_bytes(H, I, dt)
+        n_up, n_dn = 2 * I * (H // 256), H * (I // 256)
+        d = np.frombuffer(np.float16(2.0 ** -14).tobytes(), np.uint8)
+        experts = []
+        for _ in range(n):
+            q4 = np.zeros((n_up + (n_dn if dt == _lib.TYPE_Q4K else 0), 144), np.uint8)
+            q4[:, 0:2] = d
+            q4[:, 4:16] = 0xFF
+            q4[:, 16:] = rng.integers(8, 16, size=(len(q4), 128)) | (rng.integers(8, 16, size=(len(q4), 128)) << 4)
+            parts = [q4.reshape(-1)]
+            if dt == _lib.TYPE_Q6K:
+                q6 = np.zeros((n_dn, 210), np.uint8)
+                q6[:, :128] = rng.integers(0, 4, size=(n_dn, 128)) | (rng.integers(0, 4, size=(n_dn, 128)) << 4)
+                sc = rng.integers(120, 129, size=(n_dn, 16)) * rng.choice([-1, 1], size=(n_dn, 16))
+                q6[:, 192:208] = np.clip(sc, -128, 127).astype(np.int8).view(np.uint8)
+                q6[:, 208:210] = d
+                parts.append(q6.reshape(-1))
+            e = np.concatenate(parts)
+            assert e.size == self.eb
+            experts.append(e)
+        self.host = np.concatenate(experts)
+        self.t = t_(self.host)
+
+
+@pytest.mark.parametrize("dt,T", [(_lib.TYPE_Q4K, 8), (_lib.TYPE_Q4K, 24), (_lib.TYPE_Q4K, 48),
+                                  (_lib.TYPE_Q6K, 48)], ids=["q4k_t8", "q4k_t24", "q4k_t48", "q6k_t48"])
+def test_grouped_experts_sums_past_2_24(dt, T):
+    """Super-block integer sums beyond fp32's exact integers (2**24): the
+    grouped kernels still equal ggml's (float)sumi bit for bit.  16 experts,
+    top-8: 4, 12 and 24 pairs per expert (one-tile, one-pass and two-pass
+    chunks)."""
+    E, K, I = 16, 8, 768
+    rng = np.random.default_rng(77 + T)
+    store = LargeSumStore(E, I, dt)
+    x = (1.0 - 0.06 * rng.random((T, H))).astype(np.float32)      # Q8_K codes -127 .. -119
+    ids, w = routing(rng, T, K, E, "uniform")
+    # the sums really pass 2**24: gate row 0 of expert ids[0, 0] against token 0
+    q8 = O.quant_q8k(x[0]).reshape(H // 256, 292)[:, 4:260].view(np.int8).astype(np.int64)
+    row = store.host[ids[0, 0] * store.eb:][:(H // 256) * 144].reshape(H // 256, 144)
+    nib = np.stack([row[:, 16:] & 15, row[:, 16:] >> 4], 1)            # [block][lo/hi][128]
+    q = np.concatenate([np.concatenate([nib[:, 0, 32 * j:32 * j + 32], nib[:, 1, 32 * j:32 * j + 32]], 1)
+                        for j in range(4)], 1).astype(np.int64)        # element order of ggml's Q4_K
+    sums = (63 * q * q8).sum(1)
+    assert np.abs(sums).max() > 2 ** 24, np.abs(sums).max()
+    out, h_out, pair, perm, xh = run_grouped(store, T, K, E, ids, w, "f32", x_host=x)
+    want, want_h = O.moe_tokens(H, I, dt, store.host, store.eb, E, ids, w, xh, n_threads=16, want_h=True)
+    hw = want_h.reshape(T * K, I)[perm]
+    assert np.isfinite(want).all() and np.abs(hw).min() > 0
+    n_h = sum(np.array_equal(h_out[j], hw[j]) for j in range(T * K))
+    n_out = sum(np.array_equal(out[t], want[t]) for t in range(T))
+    print(f"max |super-block sum| {np.abs(sums).max()}; bit-exact pairs {n_h}/{T * K}, tokens {n_out}/{T}")
+    assert n_h == T * K and n_out == T
 
 
 def test_grouped_experts_slots_pinned_and_absent():
