@@ -7,11 +7,13 @@
 //                        cores consume: the int8 values as fp16 codes, the
 //                        block scale, and the 16-value group sums as fp16 --
 //                        all exact
-//   grouped_gemm_kernel  per (64-row tile, expert): the expert's rows against
-//                        the activations of every pair dispatched to it, on
-//                        MFMA 16x16x32 f16; up and gate as one 2I-row matrix
-//                        (the expert's [up | gate] layout), then down with the
-//                        pair's gate weight, scattered to the pair's row
+//   grouped_q4_kernel    per (64-row tile, expert): the expert's Q4_K rows
+//                        against the activations of every pair dispatched to
+//                        it, on MFMA 16x16x32 f16; up and gate as one 2I-row
+//                        matrix (the expert's [up | gate] layout), and Q4_K
+//                        down with the pair's gate weight, scattered to the
+//                        pair's row
+//   grouped_q6_kernel    the same for a Q6_K down matrix
 //   swiglu_quant_kernel  h = silu(gate) * up, and its Q8_K
 //   combine_kernel       out[t] = sum over k of the weighted rows, k in order
 //
@@ -19,8 +21,10 @@
 // d*sc*q - dmin*m with q a nibble and sc, m six-bit.  The B operand holds sc*q
 // (<= 945, an integer fp16 represents exactly: 11-bit significand; bf16's 8 bits
 // cannot), the A operand the Q8_K integers of the activation (|q8| <= 127,
-// exact), so the fp32 accumulation over a 256-value super-block is the exact
-// integer sum_j sc_j * sum_i q_i q8_i of ggml's vec_dot_q4_K_q8_K.  The min
+// exact).  Each 128-value half of a 256-value super-block accumulates in fp32
+// exactly (below 2^24), and the halves add once: the block's integer sum
+// sum_j sc_j * sum_i q_i q8_i of ggml's vec_dot_q4_K_q8_K rounded once, as its
+// (float)sumi.  The min
 // term sum_j m_j * bsum_j is a second, 16-deep MFMA of the six-bit mins
 // against the Q8_K group sums (|bsum16| <= 2032, exact).  fp32 appears only
 // where ggml has it, in ggml's order: y += (d*dx)*sumi; y -= (dmin*dx)*summ per
@@ -266,38 +270,6 @@ __device__ inline void q4_scales(const uint4 &hdr, int h, Q4Scales &o) {
     }
 }
 
-// Q6_K B operands of one super-block for the lane's row (bytes in LDS at the
-// padded block stride, q6k_rows_store: aligned reads): MFMA 4*hh + g covers
-// elements 128*hh + 32*g + 8*h .. +7 with sc = scales[8*hh + (h >> 1) + 2*g].
-// (q - 32) * sc reaches 4096, past fp16's exact integers, so sc = 16*sh + sl
-// splits it into two exact operands (|(q-32)*sh| <= 256, (q-32)*sl <= 480):
-// sumi = 16*acc_h + acc_l.
-__device__ inline void q6_frag(const uint8_t *blk, int h, half8_t bh[8], half8_t bl[8], float &d) {
-    d = h2f_dev(*(const uint16_t *)(blk + 208));
-    const uint32_t M = 0x0F0F0F0Fu, HM = 0x30303030u;
-    const half8_t c1056 = splat8((_Float16)1056.0f);
-#pragma unroll
-    for (int hh = 0; hh < 2; ++hh) {
-        const uint8_t *pa = blk + 64 * hh + 8 * h;
-        const uint2 va = *(const uint2 *)pa, vb = *(const uint2 *)(pa + 32);
-        const uint2 vq = *(const uint2 *)(blk + 128 + 32 * hh + 8 * h);
-        const uint2 vs = *(const uint2 *)(blk + 192 + 8 * hh);          // the half's 8 scales
-        const uint32_t a0 = va.x, a1 = va.y, b0 = vb.x, b1 = vb.y, q0 = vq.x, q1 = vq.y;
-        const uint32_t w[4][2] = {{(a0 & M) | ((q0 << 4) & HM), (a1 & M) | ((q1 << 4) & HM)},
-                                  {(b0 & M) | ((q0 << 2) & HM), (b1 & M) | ((q1 << 2) & HM)},
-                                  {((a0 >> 4) & M) | (q0 & HM), ((a1 >> 4) & M) | (q1 & HM)},
-                                  {((b0 >> 4) & M) | ((q0 >> 2) & HM), ((b1 >> 4) & M) | ((q1 >> 2) & HM)}};
-#pragma unroll
-        for (int g = 0; g < 4; ++g) {
-            const int j = (h >> 1) + 2 * g;                                   // byte j of the 8
-            const int sc = (int)(int8_t)(uint8_t)((j < 4 ? vs.x : vs.y) >> (8 * (j & 3)));
-            const half8_t q = pack_1024(w[g][0], w[g][1]) - c1056;          // q - 32, exact
-            bh[4 * hh + g] = q * splat8((_Float16)(float)(sc >> 4));        // arithmetic shift: -8 .. 7
-            bl[4 * hh + g] = q * splat8((_Float16)(float)(sc & 15));
-        }
-    }
-}
-
 // ---- activation staging ------------------------------------------------------
 // One 256-value block of the activation rows of a pass's pairs, in LDS.  The
 // 16-byte chunk c of row r sits at position c ^ (r & 15), so the 16 rows one
@@ -316,7 +288,7 @@ using AStage = AStageR<GT>;
 // rows[r]: activation row of pair r of the pass (r < np); rows are K values
 // long.  Wave w stages rows (R/4)w .. (R/4)w + R/4 - 1 (two per instruction),
 // wave 0 also the group sums.  Rows past np are not loaded.
-template <int R>
+template <int R, bool SUMS = true>
 __device__ inline void stage_a(AStageR<R> &st, const int *rows, int np, const uint16_t *xa, const uint16_t *xbs,
                                int K, int s, int wave, int lane) {
 #pragma unroll
@@ -328,7 +300,7 @@ __device__ inline void stage_a(AStageR<R> &st, const int *rows, int np, const ui
         const uint16_t *src = xa + (size_t)rows[r] * K + (size_t)s * QK + 8 * c;
         __builtin_amdgcn_global_load_lds((gptr_t *)src, (lptr_t *)&st.a[r0][0], 16, 0, 0);
     }
-    if (wave == 0) {
+    if (SUMS && wave == 0) {
         const int r = min(lane >> 1, np - 1);
         const uint16_t *src = xbs + (size_t)rows[r] * (K / 16) + (size_t)s * 16 + 8 * (lane & 1);
         __builtin_amdgcn_global_load_lds((gptr_t *)src, (lptr_t *)&st.bs[0][0], 16, 0, 0);
@@ -340,8 +312,6 @@ __device__ inline half8_t stage_frag(const AStageR<R> &st, int r, int off) {
     const int c = (off >> 3) ^ (r & 15);
     return *(const half8_t *)&st.a[r][8 * c];
 }
-
-constexpr int G6_LDS = 64 * 3 * Q6K_PAD;     // 64 padded Q6_K rows at K <= 768
 
 // Workgroup -> (row tile, expert).  Workgroups go to the 8 XCDs round-robin
 // (workgroup L on XCD L % 8); with E a multiple of 8, every row tile of
@@ -358,20 +328,73 @@ __device__ inline void tile_expert(int L, int T, int E, int &tile, int &e) {
     }
 }
 
-// The grouped product of one (64-row tile, expert) for a Q6_K matrix (down in
-// the mixed layers): the tile's rows against the activation rows of every pair
-// dispatched to the expert, K = NB*256.  Workgroup = 4 waves of 16 rows.  The
-// tile (rows only 2-byte aligned) is copied into LDS once, at the padded block
-// stride; each pass covers up to 32 pairs, block s+1 of their activations
-// staged in LDS while block s is decoded and multiplied.  up/gate (DOWN false):
-// y2[pair position][row]; down: the pair's gate weight times y, to the pair's
-// (t*K + k) row.  (256, 4): at most 128 registers.  Q4_K matrices take
-// grouped_q4_kernel.
-template <int NB, int DT, bool DOWN>
-__global__ __launch_bounds__(256, 4) void grouped_gemm_kernel(GroupedArgs a) {
-    static_assert(DT == TYPE_Q6K, "Q4_K matrices take grouped_q4_kernel");
+// ---------------------------------------------------------------------------
+// Q6_K lane layout of the streamed kernel.  Lane (n = row, h) takes, of the
+// 128-value half hh = h >> 1, the 16 positions l = 16*(h & 1) .. +15 of each
+// of its four 32-value groups g: ql bytes 64hh + l (g = 0 low nibbles, g = 2
+// high) and 64hh + 32 + l (g = 1, 3), qh bytes 32hh + l (two bits a group),
+// so each group's 16 values share one scale, 8hh + 2g + (h & 1).  MFMA
+// i = 2g + half multiplies positions l = 16*(h & 1) + 8*half .. +7 of group g;
+// the activation values at those positions sit at this offset of the block:
+__device__ inline int q6_a_offset(int h, int i) {
+    return 128 * (h >> 1) + 32 * (i >> 1) + 16 * (h & 1) + 8 * (i & 1);
+}
+
+struct Q6Lane {
+    uint4 qa, qb, qh;      // ql bytes 64hh + l, 64hh + 32 + l, qh bytes 32hh + l
+    uint2 sc;              // scales 8hh .. 8hh + 7
+    uint32_t d;            // the block's fp16 scale in the low half
+};
+
+// a Q6_K block starts 2-byte aligned (210-byte blocks); the loads are unaligned
+__device__ inline void q6_lane_load(Q6Lane &w, const uint8_t *blk, int h) {
+    const int hh = h >> 1, l0 = 16 * (h & 1);
+    __builtin_memcpy(&w.qa, __builtin_assume_aligned(blk + 64 * hh + l0, 2), 16);
+    __builtin_memcpy(&w.qb, __builtin_assume_aligned(blk + 64 * hh + 32 + l0, 2), 16);
+    __builtin_memcpy(&w.qh, __builtin_assume_aligned(blk + 128 + 32 * hh + l0, 2), 16);
+    __builtin_memcpy(&w.sc, __builtin_assume_aligned(blk + 192 + 8 * hh, 2), 8);
+    w.d = *(const uint16_t *)(blk + 208);
+}
+
+// The B operands of MFMA i: (q - 32) * sc in two exact halves, sc = 16*sh + sl
+// (|(q - 32) * sh| <= 256, |(q - 32) * sl| <= 480); (1024 + q)*s - 1056*s is
+// one rounding of an exact integer.
+__device__ inline void q6_lane_b(const Q6Lane &w, int i, int h, half8_t &bh, half8_t &bl) {
+    const uint32_t M = 0x0F0F0F0Fu, HM = 0x30303030u;
+    const int g = i >> 1, half = i & 1;
+    const uint4 &ql = (g & 1) ? w.qb : w.qa;
+    uint32_t l0 = half ? ql.z : ql.x, l1 = half ? ql.w : ql.y;
+    uint32_t q0 = half ? w.qh.z : w.qh.x, q1 = half ? w.qh.w : w.qh.y;
+    if (g >= 2) {
+        l0 >>= 4;
+        l1 >>= 4;
+    }
+    // group g's two high bits (qh bits 2g, 2g+1) to bits 4, 5 of each byte
+    if (g == 0) { q0 <<= 4; q1 <<= 4; }
+    if (g == 1) { q0 <<= 2; q1 <<= 2; }
+    if (g == 3) { q0 >>= 2; q1 >>= 2; }
+    const half8_t q = pack_1024((l0 & M) | (q0 & HM), (l1 & M) | (q1 & HM));
+    const int j = 2 * g + (h & 1);
+    const int sc = (int)(int8_t)(uint8_t)((j < 4 ? w.sc.x : w.sc.y) >> (8 * (j & 3)));
+    const _Float16 sh = (_Float16)(float)(sc >> 4), sl = (_Float16)(float)(sc & 15);   // arithmetic shift
+    bh = __builtin_elementwise_fma(q, splat8(sh), splat8((_Float16)(float)(-1056 * (sc >> 4))));
+    bl = __builtin_elementwise_fma(q, splat8(sl), splat8((_Float16)(float)(-1056 * (sc & 15))));
+}
+
+// The grouped down product for a Q6_K matrix, the lane's weights streamed from
+// HBM into registers as in grouped_q4_kernel (block s+1 in flight while block
+// s is multiplied, no LDS tile), in chunks of up to CH passes of MT M tiles of
+// 16 pairs: each block's weights are loaded once for the chunk and decoded per
+// pass.  CH = 1, (256, 4): four workgroups a CU; CH = 2 for large batches,
+// (256, 3).  A block's two integer sums stay below 2^24 (256 * 32 * 8 * 127
+// and 256 * 32 * 15 * 127), so each is exact and 16*acc_h + acc_l rounds once,
+// as ggml's (float)sumi.  y = the pair's gate weight times the row value, to
+// the pair's (t*K + k) row.
+template <int NB, int CH, int MT>
+__global__ __launch_bounds__(256, CH == 1 ? 4 : 3) void grouped_q6_kernel(GroupedArgs a) {
+    constexpr int GK = 16 * MT;
     int e, tile;
-    tile_expert(blockIdx.x, (DOWN ? a.H : 2 * a.I) / 64, a.E, tile, e);
+    tile_expert(blockIdx.x, a.H / 64, a.E, tile, e);
     const int n0 = a.offsets[e], ne = a.offsets[e + 1] - n0;
     if (ne <= 0) return;
     const int tid = threadIdx.x, lane = tid & 63;
@@ -380,105 +403,102 @@ __global__ __launch_bounds__(256, 4) void grouped_gemm_kernel(GroupedArgs a) {
     const int r0 = tile * 64;
     const int row = r0 + wave * 16 + n;
     constexpr int K = NB * QK;
-    constexpr int ROWB = NB * Q6K_BYTES;
-    const int out_n = DOWN ? a.H : 2 * a.I;   // columns of the output rows
     const uint8_t *base = grouped_expert(a, e);
     if (!base) {
         for (int i = tid; i < ne * 64; i += 256) {
             const int pos = n0 + i / 64, c = r0 + (i % 64);
-            if (DOWN) a.ypair[(size_t)a.perm[pos] * a.H + c] = 0.0f;
-            else a.y2[(size_t)pos * out_n + c] = 0.0f;
+            a.ypair[(size_t)a.perm[pos] * a.H + c] = 0.0f;
         }
         return;
     }
-    const uint8_t *mat = DOWN ? base + 2ull * a.I * (a.H / QK) * Q4K_BYTES : base;
-    const uint16_t *act = DOWN ? a.ha : a.xa;
-    const uint16_t *abs16 = DOWN ? a.hbs : a.xbs;
-    const float *adx = DOWN ? a.hdx : a.xdx;
+    const uint8_t *wrow = base + 2ull * a.I * (a.H / QK) * Q4K_BYTES + (size_t)row * (NB * Q6K_BYTES);
 
-    __shared__ AStage st[2];
-    __shared__ int s_rows[GT];
-    __shared__ float s_dx[GT][NB];
-    __shared__ __attribute__((aligned(16))) uint8_t s_w6[G6_LDS];
+    __shared__ AStageR<GK> st[2];
+    __shared__ int s_rows[CH * GK];
+    __shared__ __attribute__((aligned(16))) float s_dx[NB][CH * GK];
 
-    constexpr int LROWB = NB * Q6K_PAD;               // a padded Q6_K row in LDS
-    {
-        // the wave's 16 rows into LDS at the padded block stride, 24 blocks
-        // (16 * NB <= 48) at a time through registers
-        const uint8_t *src = mat + (size_t)(r0 + 16 * wave) * ROWB;
-        uint8_t *dst = s_w6 + (size_t)(16 * wave) * LROWB;
-        for (int b0 = 0; b0 < 16 * NB; b0 += 24) {
-            const int nbk = min(24, 16 * NB - b0);
-            Q6Rows rows;
-            q6k_rows_load(rows, src + (size_t)b0 * Q6K_BYTES, nbk, lane);
-            q6k_rows_store(rows, dst + (size_t)b0 * Q6K_PAD, nullptr, nbk, lane);
-        }
-    }
-
-    for (int pb = 0; pb < ne; pb += GT) {
-        const int np = min(GT, ne - pb);
-        const int nt = (np + 15) / 16;
-        if (tid < GT) {
-            const int pos = n0 + pb + min(tid, np - 1);
-            s_rows[tid] = DOWN ? pos : a.perm[pos] / a.K;
-        }
+    for (int cb = 0; cb < ne; cb += CH * GK) {
+        const int npc = min(CH * GK, ne - cb);
+        const int nps = (npc + GK - 1) / GK;
+        if (tid < CH * GK) s_rows[tid] = n0 + cb + min(tid, npc - 1);   // h rows are in dispatch order
         __syncthreads();
-        if (tid < GT * NB) s_dx[tid / NB][tid % NB] = adx[(size_t)s_rows[tid / NB] * NB + (tid % NB)];
-        // block 0's activations staged; then block s+1's are in flight while
-        // block s is multiplied
-        stage_a(st[0], s_rows, np, act, abs16, K, 0, wave, lane);
+        for (int i = tid; i < CH * GK * NB; i += 256)
+            s_dx[i % NB][i / NB] = a.hdx[(size_t)s_rows[i / NB] * NB + (i % NB)];
+        stage_a<GK, false>(st[0], s_rows, min(GK, npc), a.ha, a.hbs, K, 0, wave, lane);
+        Q6Lane cw, nw;
+        q6_lane_load(cw, wrow, h);
         __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
-        float y[2][4] = {{0, 0, 0, 0}, {0, 0, 0, 0}};
+        float y[CH][MT][4];
+#pragma unroll
+        for (int p = 0; p < CH; ++p)
+#pragma unroll
+            for (int t = 0; t < MT; ++t)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) y[p][t][i] = 0.0f;
+        int j = 0;                       // step j = s * nps + p
 #pragma unroll 1
         for (int s = 0; s < NB; ++s) {
-            const AStage &S = st[s & 1];
-            if (s + 1 < NB) stage_a(st[(s + 1) & 1], s_rows, np, act, abs16, K, s + 1, wave, lane);
-            float4_t acc[2] = {{0, 0, 0, 0}, {0, 0, 0, 0}};
-            float d;
-            half8_t bh[8], bl[8];
-            q6_frag(s_w6 + (size_t)(wave * 16 + n) * LROWB + (size_t)s * Q6K_PAD, h, bh, bl, d);
-            float4_t accl[2] = {{0, 0, 0, 0}, {0, 0, 0, 0}};
+            if (s + 1 < NB) q6_lane_load(nw, wrow + (s + 1) * Q6K_BYTES, h);
+            const float d = h2f_dev((uint16_t)cw.d);
 #pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                const int off = 128 * (i >> 2) + 32 * (i & 3) + 8 * h;
+            for (int p = 0; p < CH; ++p) {
+                if (p < nps) {
+                    const AStageR<GK> &S = st[j & 1];
+                    const int jn = j + 1;
+                    if (jn < NB * nps) {
+                        const int s2 = jn / nps, p2 = jn - s2 * nps;
+                        stage_a<GK, false>(st[jn & 1], s_rows + p2 * GK, min(GK, npc - p2 * GK), a.ha, a.hbs, K, s2,
+                                           wave, lane);
+                    }
+                    float4_t acc[MT], accl[MT];
 #pragma unroll
-                for (int t = 0; t < 2; ++t) {
-                    const half8_t av = stage_frag(S, 16 * t + n, off);
-                    acc[t] = mfma32(av, bh[i], acc[t]);
-                    accl[t] = mfma32(av, bl[i], accl[t]);
+                    for (int t = 0; t < MT; ++t) acc[t] = accl[t] = float4_t{0, 0, 0, 0};
+                    half8_t fa[2][MT];
+#pragma unroll
+                    for (int t = 0; t < MT; ++t) fa[0][t] = stage_frag(S, 16 * t + n, q6_a_offset(h, 0));
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) {
+                        if (i + 1 < 8) {
+#pragma unroll
+                            for (int t = 0; t < MT; ++t)
+                                fa[(i + 1) & 1][t] = stage_frag(S, 16 * t + n, q6_a_offset(h, i + 1 < 8 ? i + 1 : 0));
+                        }
+                        half8_t bh, bl;
+                        q6_lane_b(cw, i, h, bh, bl);
+#pragma unroll
+                        for (int t = 0; t < MT; ++t) {
+                            acc[t] = mfma32(fa[i & 1][t], bh, acc[t]);
+                            accl[t] = mfma32(fa[i & 1][t], bl, accl[t]);
+                        }
+                    }
+#pragma unroll
+                    for (int t = 0; t < MT; ++t) {
+                        const float4 dxv = *(const float4 *)&s_dx[s][p * GK + 16 * t + 4 * h];
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) {
+                            const float dx = i == 0 ? dxv.x : i == 1 ? dxv.y : i == 2 ? dxv.z : dxv.w;
+                            const float sumi = 16.0f * acc[t][i] + accl[t][i];
+                            y[p][t][i] = y[p][t][i] + (d * dx) * sumi;   // ggml's order: acc += (d*dx)*sumi
+                        }
+                    }
+                    __builtin_amdgcn_s_waitcnt(0);
+                    __syncthreads();
+                    ++j;
                 }
             }
-            // both M tiles every time (no branch merges around the accumulators);
-            // rows past the pass's pairs compute on stale LDS and are never written
-#pragma unroll
-            for (int t = 0; t < 2; ++t) {
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    // the block's integer sum: |acc| <= 256 * 32 * 8 * 127 and
-                    // |accl| <= 256 * 32 * 15 * 127, both below 2^24, so exact,
-                    // and 16*acc + accl rounds once, as ggml's (float)sumi
-                    const float sumi = 16.0f * acc[t][i] + accl[t][i];
-                    // ggml's order: acc += (d*dx)*sumi
-                    const float dx = s_dx[16 * t + 4 * h + i][s];
-                    y[t][i] = y[t][i] + (d * dx) * sumi;
-                }
-            }
-            __builtin_amdgcn_s_waitcnt(0);
-            __syncthreads();
+            cw = nw;
         }
 #pragma unroll
-        for (int t = 0; t < 2; ++t) {
+        for (int p = 0; p < CH; ++p) {
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int r = 16 * t + 4 * h + i;
-                if (t < nt && r < np) {
-                    const int pos = n0 + pb + r;
-                    if (DOWN) {
-                        const int p = a.perm[pos];
-                        a.ypair[(size_t)p * a.H + row] = a.w[p] * y[t][i];
-                    } else {
-                        a.y2[(size_t)pos * out_n + row] = y[t][i];
+            for (int t = 0; t < MT; ++t) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int r = p * GK + 16 * t + 4 * h + i;
+                    if (r < npc) {
+                        const int q = a.perm[n0 + cb + r];
+                        a.ypair[(size_t)q * a.H + row] = a.w[q] * y[p][t][i];
                     }
                 }
             }
@@ -771,9 +791,19 @@ static hipError_t launch_gg(const GroupedArgs &a, hipStream_t st, hipEvent_t e0,
     const bool one = a.P <= 8 * a.E;                            // few pairs: one 16-row M tile a pass
     if (DOWN) {
         if (a.down_type == TYPE_Q6K) {
-            if (nb == 3) return launch_b(grouped_gemm_kernel<3, TYPE_Q6K, true>, grid, blk, st, e0, e1, a);
-            if (nb == 2) return launch_b(grouped_gemm_kernel<2, TYPE_Q6K, true>, grid, blk, st, e0, e1, a);
-            return launch_b(grouped_gemm_kernel<1, TYPE_Q6K, true>, grid, blk, st, e0, e1, a);
+            if (two) {
+                if (nb == 3) return launch_b(grouped_q6_kernel<3, 2, 2>, grid, blk, st, e0, e1, a);
+                if (nb == 2) return launch_b(grouped_q6_kernel<2, 2, 2>, grid, blk, st, e0, e1, a);
+                return launch_b(grouped_q6_kernel<1, 2, 2>, grid, blk, st, e0, e1, a);
+            }
+            if (one) {
+                if (nb == 3) return launch_b(grouped_q6_kernel<3, 1, 1>, grid, blk, st, e0, e1, a);
+                if (nb == 2) return launch_b(grouped_q6_kernel<2, 1, 1>, grid, blk, st, e0, e1, a);
+                return launch_b(grouped_q6_kernel<1, 1, 1>, grid, blk, st, e0, e1, a);
+            }
+            if (nb == 3) return launch_b(grouped_q6_kernel<3, 1, 2>, grid, blk, st, e0, e1, a);
+            if (nb == 2) return launch_b(grouped_q6_kernel<2, 1, 2>, grid, blk, st, e0, e1, a);
+            return launch_b(grouped_q6_kernel<1, 1, 2>, grid, blk, st, e0, e1, a);
         }
         if (two) {
             if (nb == 3) return launch_b(grouped_q4_kernel<3, true, 2, 2>, grid, blk, st, e0, e1, a);

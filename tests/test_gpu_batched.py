@@ -220,6 +220,10 @@ GROUPED_CASES = {
     # at most 8 pairs per expert on average: one 16-row M tile a pass
     "q4k_i256_t20_one_tile": (_lib.TYPE_Q4K, 256, 20, 128, "uniform", "bf16"),
     "q4k_i512_t100_crowded_one_tile": (_lib.TYPE_Q4K, 512, 100, 128, "crowd", "f32"),
+    # more than 16 pairs per expert: Q6_K down in chunks of two passes
+    "q6k_i768_t512": (_lib.TYPE_Q6K, 768, 512, 128, "uniform", "bf16"),
+    "q6k_i512_t300_crowded": (_lib.TYPE_Q6K, 512, 300, 128, "crowd", "f32"),
+    "q6k_i256_t300_e64": (_lib.TYPE_Q6K, 256, 300, 64, "uniform", "bf16"),
 }
 
 
