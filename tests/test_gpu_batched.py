@@ -220,10 +220,13 @@ GROUPED_CASES = {
     # at most 8 pairs per expert on average: one 16-row M tile a pass
     "q4k_i256_t20_one_tile": (_lib.TYPE_Q4K, 256, 20, 128, "uniform", "bf16"),
     "q4k_i512_t100_crowded_one_tile": (_lib.TYPE_Q4K, 512, 100, 128, "crowd", "f32"),
-    # more than 16 pairs per expert: Q6_K down in chunks of two passes
+    # more than 16 pairs per expert on average: chunks of two 32-pair passes
     "q6k_i768_t512": (_lib.TYPE_Q6K, 768, 512, 128, "uniform", "bf16"),
     "q6k_i512_t300_crowded": (_lib.TYPE_Q6K, 512, 300, 128, "crowd", "f32"),
     "q6k_i256_t300_e64": (_lib.TYPE_Q6K, 256, 300, 64, "uniform", "bf16"),
+    "q4k_i768_t200_e32": (_lib.TYPE_Q4K, 768, 200, 32, "uniform", "bf16"),
+    "q6k_i512_t200_e32": (_lib.TYPE_Q6K, 512, 200, 32, "uniform", "f32"),
+    "q6k_i256_t400_e32_crowded": (_lib.TYPE_Q6K, 256, 400, 32, "crowd", "bf16"),
 }
 
 
@@ -293,12 +296,13 @@ class LargeSumStore:
 
 
 @pytest.mark.parametrize("dt,T", [(_lib.TYPE_Q4K, 8), (_lib.TYPE_Q4K, 24), (_lib.TYPE_Q4K, 48),
-                                  (_lib.TYPE_Q6K, 48)], ids=["q4k_t8", "q4k_t24", "q4k_t48", "q6k_t48"])
+                                  (_lib.TYPE_Q4K, 96), (_lib.TYPE_Q6K, 48), (_lib.TYPE_Q6K, 96)],
+                         ids=["q4k_t8", "q4k_t24", "q4k_t48", "q4k_t96", "q6k_t48", "q6k_t96"])
 def test_grouped_experts_sums_past_2_24(dt, T):
     """Super-block integer sums beyond fp32's exact integers (2**24): the
     grouped kernels still equal ggml's (float)sumi bit for bit.  16 experts,
-    top-8: 4, 12 and 24 pairs per expert (one-tile, one-pass and two-pass
-    chunks)."""
+    top-8: 4, 12, 24 and 48 pairs per expert (one-tile passes, one-pass and
+    two-pass chunks)."""
     E, K, I = 16, 8, 768
     rng = np.random.default_rng(77 + T)
     store = LargeSumStore(E, I, dt)
