@@ -55,11 +55,24 @@ typedef __attribute__((address_space(3))) void lptr_t;
 // ---------------------------------------------------------------------------
 // dispatch: ids [P] (P = n_tok * K, pair i = t*K + k) -> counts[E], offsets[E+1],
 // perm[offsets[e] + r] = i of the r-th pair routed to e in pair order.
-// Pass 1 counts with LDS atomics (order-free); pass 2 places 64-pair chunks:
-// lanes holding the same id find each other with 8 ballots (one per id bit),
-// their rank inside the chunk is a popcount, and a per-expert scan over the
-// chunks of the pass (continuing a running count) gives each chunk's base.
+// Pass 1 counts with LDS atomics (order-free) and one wave turns the counts
+// into offsets with a prefix sum (lane l holds experts 4l .. 4l+3); pass 2
+// places 64-pair chunks: lanes holding the same id find each other with 8
+// ballots (one per id bit), their rank inside the chunk is a popcount, and a
+// per-expert scan over the chunks of the pass (continuing a running count)
+// gives each chunk's base.
 constexpr int DSP_CHUNKS = 64;
+static_assert(MAX_E <= 256, "4 experts a lane in the offsets' prefix sum");
+
+// inclusive prefix sum over the 64 lanes of a wave
+__device__ inline int wave_incl_sum(int v, int lane) {
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+        const int t = __shfl_up(v, d, 64);
+        if (lane >= d) v += t;
+    }
+    return v;
+}
 
 __global__ __launch_bounds__(1024) void dispatch_kernel(const int32_t *ids, int P, int E, int32_t *counts,
                                                         int32_t *offsets, int32_t *perm) {
@@ -74,16 +87,27 @@ __global__ __launch_bounds__(1024) void dispatch_kernel(const int32_t *ids, int 
         if (e >= 0 && e < E) atomicAdd(&s_off[e], 1);
     }
     __syncthreads();
-    if (tid == 0) {
-        int acc = 0;
-        for (int e = 0; e < E; ++e) {
-            const int c = s_off[e];
-            counts[e] = c;
-            offsets[e] = acc;
-            s_off[e] = acc;
-            acc += c;
+    if (wave == 0) {
+        int c[4], sum = 0;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int e = 4 * lane + j;
+            c[j] = e < E ? s_off[e] : 0;
+            sum += c[j];
         }
-        offsets[E] = acc;
+        const int incl = wave_incl_sum(sum, lane);
+        int acc = incl - sum;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int e = 4 * lane + j;
+            if (e < E) {
+                counts[e] = c[j];
+                offsets[e] = acc;
+                s_off[e] = acc;
+            }
+            acc += c[j];
+        }
+        if (lane == 63) offsets[E] = incl;
     }
     __syncthreads();
     const int nwaves = blockDim.x >> 6;
