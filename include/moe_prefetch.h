@@ -491,6 +491,14 @@ int moe_cache_set_timing(moe_cache *c, int on);
  * path gives the same bits.  MOE_ERR_ARG for split outside 0..3 or graph
  * outside 0..2. */
 int moe_cache_set_decode_path(moe_cache *c, int split, int graph);
+/* Bound of every wait inside the fused decode launch (default 0.5 s): a
+ * workgroup that waits longer for another gives up and exits, and the token
+ * fails with MOE_ERR_HIP (moe_decode_token, or moe_cache_step after per-layer
+ * calls).  No counterpart in the reference, whose layer runs as separate
+ * launches with no waits between workgroups; for callers that want failures
+ * reported sooner, and for tests that force the give-up from the host.
+ * MOE_ERR_ARG outside (0, 60]. */
+int moe_cache_set_wait_bound(moe_cache *c, double seconds);
 /* Staged uploads (default on; no counterpart in the reference, which uploads
  * from the host store, P6:428-440): moe_decode_token's kernels also write each
  * expert they read from the pinned store into an HBM staging area ([L][K]
@@ -560,7 +568,13 @@ int moe_decode_layer(moe_cache *c, int layer, const float *x, const float *bias,
                      int32_t *ids_dev, float *w_dev, void *stream);
 /* One decode token over every layer: x dev [L][H], bias dev [L][E] or NULL,
  * out dev [L][H]; then the routed ids come back (one copy), are observed in
- * layer order and the cache steps.  ids_host [L][K] receives them when not NULL. */
+ * layer order and the cache steps.  ids_host [L][K] receives them when not NULL.
+ * The call returns with out complete in device memory.  When the layers are
+ * launched directly without CPU-assisted serving or streaming (at most 8
+ * layers, graph mode 0 or 1, no timing), the fused launches publish the ids
+ * into mapped memory and the call returns on their done word, without
+ * synchronising the stream: the last launch may still be retiring, and work
+ * enqueued later on the stream orders after it as usual. */
 int moe_decode_token(moe_cache *c, const float *x, const float *bias, float *out, int32_t *ids_host,
                      void *stream);
 

@@ -206,6 +206,15 @@ struct FusedArgs {
     uint64_t *yx;             // [K + 1][H] tagged down rows
     uint32_t *err;            // a bounded wait ran out: the token's sequence number is written here
     uint64_t wait_ticks;      // bound of every wait, 100 MHz wall clock
+    // Publishing to the host (or pub null): the device view of the host's mapped
+    // copy of the ids buffer -- ids [L][K], the late word, the done word, padding,
+    // slots [L][K] from word L*K + 64.  The layer's last combine workgroup writes
+    // the layer's ids and slots there, and with pub_done the late word and then the
+    // token's sequence number in the done word: the token's outputs are complete.
+    uint32_t *pub;
+    uint64_t *pub_ctr;        // (seq << 32) | the layer's combine workgroups finished
+    int pub_layer, pub_L;
+    int pub_done;
 };
 // exchange words per layer of the fused decode
 inline size_t fused_words(int K, int I, int H) {

@@ -782,15 +782,16 @@ constexpr int FUSED_LDS_RS = FUSED_LDS_W + FUSED_LDS_Q8 + 8 * FUSED_REC + 16;   
 constexpr int FUSED_LDS = FUSED_LDS_RS + 256;
 
 // The routing record (copy `copy`): wave 0 polls until the words the
-// workgroup needs carry seq -- the K routing words, or with need_w the K gate
-// weights -- and leaves them in s_rec for the workgroup.  false: the wait
-// ran out (reported through a.err).
-__device__ bool fused_record(const FusedArgs &a, int copy, uint32_t seq, bool need_w, uint64_t *s_rec, int *s_flag) {
+// workgroup needs carry seq -- with need_ids the K routing words, with need_w
+// the K gate weights -- and leaves them in s_rec for the workgroup (the words
+// not polled are 0).  false: the wait ran out (reported through a.err).
+__device__ bool fused_record(const FusedArgs &a, int copy, uint32_t seq, bool need_ids, bool need_w, uint64_t *s_rec,
+                             int *s_flag) {
     const int K = a.x.K;
     if (threadIdx.x < 64) {
         const int lane = threadIdx.x;
         const uint64_t *src = a.rec + (size_t)copy * FUSED_REC;
-        const bool want = need_w ? lane >= 16 && lane < 16 + K : lane < K;
+        const bool want = (need_ids && lane < K) || (need_w && lane >= 16 && lane < 16 + K);
         bool ok = !want;
         uint64_t v = 0;
         int late = 0;
@@ -1187,7 +1188,7 @@ __device__ void fused_down(const FusedArgs &a, int g, uint32_t seq, uint8_t *sme
         // the selection's record (the down rows' weights are not needed
         // before h, and requested later they leave the memory system to the
         // gate/up rows first)
-        if (!fused_record(a, g % FUSED_COPIES, seq, false, s_rec, s_flag)) return;
+        if (!fused_record(a, g % FUSED_COPIES, seq, true, false, s_rec, s_flag)) return;
         src = expert_src(x, k, [s_rec](int kk) { return s_rec[kk]; });
         if (src.cpu) return;
     }
@@ -1298,15 +1299,10 @@ __device__ void fused_down(const FusedArgs &a, int g, uint32_t seq, uint8_t *sme
     }
 }
 
-// 256 output rows: out = sum_k w_k y_k in k order, then the shared expert
+// one output row: out = sum_k w_k y_k in k order, then the shared expert
 // (weight 1), as down_kernel's combine adds them
-__device__ void fused_combine(const FusedArgs &a, int c, uint32_t seq, uint8_t *smem) {
+__device__ void fused_combine_row(const FusedArgs &a, int row, uint32_t seq, const uint64_t *s_rec) {
     const ExpertArgs &x = a.x;
-    uint64_t *s_rec = (uint64_t *)(smem + FUSED_LDS_W + FUSED_LDS_Q8);
-    int *s_flag = (int *)(s_rec + FUSED_REC);
-    if (!fused_record(a, c % FUSED_COPIES, seq, true, s_rec, s_flag)) return;
-    const int row = c * 256 + (int)threadIdx.x;
-    if (row >= x.H) return;
     const int kt = x.K + x.n_shared;
     // every row word requested in each round (one round trip, not one per
     // expert); a round re-reads only the words not yet valid
@@ -1336,7 +1332,56 @@ __device__ void fused_combine(const FusedArgs &a, int c, uint32_t seq, uint8_t *
     float acc = __uint_as_float((uint32_t)s_rec[16]) * y[0];
     for (int k = 1; k < x.K; ++k) acc = acc + __uint_as_float((uint32_t)s_rec[16 + k]) * y[k];
     if (x.n_shared) acc = acc + y[x.K];
-    x.out[row] = acc;
+    // publishing: written through to memory (performed before the workgroup
+    // counts itself done), so a reader on another stream or engine sees the
+    // row once the host has the done word, before the launch has retired
+    if (a.pub) __hip_atomic_store(x.out + row, acc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    else x.out[row] = acc;
+}
+
+// The layer's last combine workgroup publishes the routed ids and slots (from
+// the routing record) into the host's mapped ids buffer; in the token's last
+// layer it then writes the late word and the sequence number in the done
+// word, release at system scope: the host reads the token's results without a
+// copy back or a stream synchronisation.  The slots keep the record's 16 bits
+// (a table word below 2^16: a slot, or the slot count for an absent expert).
+__device__ void fused_publish(const FusedArgs &a, uint32_t seq, const uint64_t *s_rec) {
+    __syncthreads();                        // this workgroup's output rows are written
+    if (threadIdx.x != 0) return;
+    const int n_comb = (a.x.H + 255) / 256;
+    uint64_t old = __hip_atomic_load(a.pub_ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT), nv;
+    do {
+        nv = (uint32_t)(old >> 32) == seq ? old + 1 : ((uint64_t)seq << 32) | 1u;
+    } while (!__hip_atomic_compare_exchange_strong(a.pub_ctr, &old, nv, __ATOMIC_ACQ_REL, __ATOMIC_RELAXED,
+                                                   __HIP_MEMORY_SCOPE_AGENT));
+    if ((uint32_t)nv != (uint32_t)n_comb) return;
+    const int K = a.x.K, L = a.pub_L, l = a.pub_layer;
+    for (int k = 0; k < K; ++k) {
+        const uint64_t t = s_rec[k];
+        __hip_atomic_store(a.pub + (size_t)l * K + k, (uint32_t)(t & 0xffffu), __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_SYSTEM);
+        __hip_atomic_store(a.pub + (size_t)L * K + 64 + (size_t)l * K + k, (uint32_t)((t >> 16) & 0xffffu),
+                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    }
+    // performed before this workgroup goes on, so a later layer's done word
+    // (another workgroup, maybe another XCD) cannot reach the host first
+    __threadfence_system();
+    if (a.pub_done) {
+        const uint32_t late = __hip_atomic_load(a.err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(a.pub + (size_t)L * K, late, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+        __hip_atomic_store(a.pub + (size_t)L * K + 1, seq, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
+    }
+}
+
+// 256 output rows of the combine, then (publishing) the count of finished
+// combine workgroups
+__device__ void fused_combine(const FusedArgs &a, int c, uint32_t seq, uint8_t *smem) {
+    uint64_t *s_rec = (uint64_t *)(smem + FUSED_LDS_W + FUSED_LDS_Q8);
+    int *s_flag = (int *)(s_rec + FUSED_REC);
+    if (!fused_record(a, c % FUSED_COPIES, seq, a.pub != nullptr, true, s_rec, s_flag)) return;
+    const int row = c * 256 + (int)threadIdx.x;
+    if (row < a.x.H) fused_combine_row(a, row, seq, s_rec);
+    if (a.pub) fused_publish(a, seq, s_rec);
 }
 
 template <int DT>

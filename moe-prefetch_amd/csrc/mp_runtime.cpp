@@ -192,6 +192,9 @@ struct moe_cache {
     void *route_ws = nullptr, *exp_ws = nullptr;
     float *ypart = nullptr;            // [K + 1][H]: per-expert down rows between the two launches of a split
     int32_t *d_ids = nullptr, *d_slots = nullptr, *h_ids = nullptr;
+    uint32_t *h_ids_d = nullptr;        // h_ids (mapped, coherent) as the device sees it
+    uint64_t *d_pub_ctr = nullptr;      // [L]: the fused combine's count of finished workgroups
+    bool pub_on = false;                // this token's fused launches publish ids and completion
     float *d_w = nullptr;
     uint8_t *d_q8x = nullptr;
     uint8_t *pool_base = nullptr;
@@ -1379,6 +1382,7 @@ void free_cache(moe_cache *c) {
     hipFree(c->exp_ws);
     hipFree(c->ypart);
     hipFree(c->d_ids);
+    hipFree(c->d_pub_ctr);
     hipFree(c->fx);
     hipFree(c->d_w);
     hipFree(c->d_q8x);
@@ -1736,18 +1740,23 @@ int moe_cache_create(const moe_cache_config *cfg, moe_cache **out) {
         hipMalloc(&c->d_ids, (2 * (size_t)NL * c->K + 64) * 4) != hipSuccess ||
         hipMalloc(&c->d_w, (size_t)NL * c->K * 4) != hipSuccess ||
         hipMalloc(&c->d_q8x, (size_t)(c->H / 256) * mp::Q8K_BYTES + 256) != hipSuccess ||
-        hipHostMalloc(&c->h_ids, (2 * (size_t)NL * c->K + 64) * 4, 0) != hipSuccess ||
+        hipHostMalloc(&c->h_ids, (2 * (size_t)NL * c->K + 64) * 4, hipHostMallocMapped | hipHostMallocCoherent) !=
+            hipSuccess ||
+        hipHostGetDevicePointer((void **)&c->h_ids_d, c->h_ids, 0) != hipSuccess ||
+        hipMalloc(&c->d_pub_ctr, (size_t)NL * 8) != hipSuccess ||
         hipMalloc(&c->fx, (size_t)NL * mp::fused_words(c->K, c->I, c->H) * 8) != hipSuccess ||
         hipHostMalloc((void **)&c->h_seq, 64, hipHostMallocDefault) != hipSuccess ||
         hipMalloc(&c->d_seq, 64) != hipSuccess)
         return bail(fail(MOE_ERR_NOMEM, "decode scratch"));
-    // ids [L][K], the late-wait word and padding, then slots [L][K]: one copy back per token
+    // ids [L][K], the late-wait word, the done word and padding, then slots [L][K]:
+    // one copy back per token, or published into h_ids by the fused launches
     c->d_slots = c->d_ids + (size_t)NL * c->K + 64;
     c->h_slots = c->h_ids + (size_t)NL * c->K + 64;
     // tag 0 is never a token's sequence number: zeroed exchange words are stale
     if (hipMemset(c->route_ws, 0, rws) != hipSuccess || hipMemset(c->exp_ws, 0, ews) != hipSuccess ||
         hipMemset(c->fx, 0, (size_t)NL * mp::fused_words(c->K, c->I, c->H) * 8) != hipSuccess ||
-        hipMemset(c->d_ids, 0, ((size_t)NL * c->K + 64) * 4) != hipSuccess || hipMemset(c->d_seq, 0, 64) != hipSuccess)
+        hipMemset(c->d_ids, 0, ((size_t)NL * c->K + 64) * 4) != hipSuccess || hipMemset(c->d_seq, 0, 64) != hipSuccess ||
+        hipMemset(c->d_pub_ctr, 0, (size_t)NL * 8) != hipSuccess)
         return bail(fail(MOE_ERR_HIP, "scratch clear"));
     c->fx_words = mp::fused_words(c->K, c->I, c->H);
     if (hipStreamCreateWithFlags(&c->up_stream, hipStreamNonBlocking) != hipSuccess ||
@@ -2466,8 +2475,21 @@ int moe_cache_set_decode_path(moe_cache *c, int split, int graph) {
     return MOE_OK;
 }
 
-static int sc_buffers(moe_cache *c);
 static int pl_server_drain(moe_cache *c);
+
+int moe_cache_set_wait_bound(moe_cache *c, double seconds) {
+    if (!c) return fail(MOE_ERR_ARG, "null cache");
+    if (!(seconds > 0.0) || seconds > 60.0) return fail(MOE_ERR_ARG, "wait bound %g s must be in (0, 60]", seconds);
+    if (c->pls) {                       // layers queued by per-layer calls run with the old bound
+        const int r = pl_server_drain(c);
+        if (r != MOE_OK) return r;
+    }
+    if (seconds != c->fused_wait_s) drop_graphs(c);     // captured launches carry the bound
+    c->fused_wait_s = seconds;
+    return MOE_OK;
+}
+
+static int sc_buffers(moe_cache *c);
 static bool logits_ready(const mp::SidecarPost &p, int E, int n_q8_words, uint32_t seq, int &n_lg, int &n_q8);
 
 int moe_cache_set_sidecar(moe_cache *c, int n_threads, int num, int den) {
@@ -2935,6 +2957,13 @@ static int decode_layer_impl(moe_cache *c, int layer, const float *x, const floa
         f.yx = f.hx + (size_t)(c->K + 1) * c->I;
         f.err = (uint32_t *)(c->d_ids + c->L.size() * (size_t)c->K);
         f.wait_ticks = (uint64_t)(c->fused_wait_s * 1e8);
+        if (c->pub_on && !sidecar) {
+            f.pub = c->h_ids_d;
+            f.pub_ctr = c->d_pub_ctr + layer;
+            f.pub_layer = layer;
+            f.pub_L = (int)c->L.size();
+            f.pub_done = layer + 1 == (int)c->L.size();
+        }
         HIPCHK(mp::launch_fused(f, st, E_(0), E_(1)));
     } else {
         const int r = run_route(&rd, st, ev, sidecar ? c->sc_post_d + layer : nullptr, seq_val ? nullptr : c->d_seq,
@@ -3227,6 +3256,22 @@ int moe_decode_layer(moe_cache *c, int layer, const float *x, const float *bias,
 // tokens of at most this many layers launch directly in graph mode (see below)
 constexpr int DIRECT_MAX_LAYERS = 8;
 
+// the fused launches' done word in h_ids carries this token's number: bounded
+// spin (a legitimate token takes microseconds; past the bound the caller
+// copies back and synchronises, which also reports a failed launch)
+static bool wait_published(moe_cache *c, int NL, uint32_t seq) {
+    const uint32_t *done = (const uint32_t *)(c->h_ids + (size_t)NL * c->K + 1);
+    const auto t0 = std::chrono::steady_clock::now();
+    const auto bound = std::chrono::duration<double>(4 * c->fused_wait_s + 0.5);
+    for (uint64_t i = 0;; ++i) {
+        if (__atomic_load_n(done, __ATOMIC_ACQUIRE) == seq) return true;
+        if ((i & 255) == 0 && std::chrono::steady_clock::now() - t0 > bound) return false;
+#if defined(__x86_64__)
+        __builtin_ia32_pause();
+#endif
+    }
+}
+
 int moe_decode_token(moe_cache *c, const float *x, const float *bias, float *out, int32_t *ids_host, void *stream) {
     if (!c || !x || !out) return fail(MOE_ERR_ARG, "bad arguments");
     if (c->host_only) return fail(MOE_ERR_STATE, "host-only cache (device < 0) cannot decode");
@@ -3307,6 +3352,15 @@ int moe_decode_token(moe_cache *c, const float *x, const float *bias, float *out
         if (sc)
             for (int l = 0; l < NL; ++l) *(volatile uint32_t *)&c->sc_resp[l].seq = mp::SC_ABORT;
     };
+    // Launched directly, GPU only, the fused layers publish the token's ids,
+    // slots and late word into h_ids themselves and then a done word: the host
+    // spins on that word instead of a copy back and a stream synchronisation
+    // (a kernel's completion reaches a waiting host ~4.7 us later than a word
+    // it writes; the copy costs 1.7 us more).  The wait is bounded; past it
+    // (a workgroup gave up, no done word) the copy and the synchronisation
+    // run as on the other paths.
+    const bool publish = !use_graph && fused && !sc && !stm && !c->timing;
+    c->pub_on = publish;
     // per-kernel HIP-event timing needs eager launches: hipEventElapsedTime
     // does not accept events recorded as nodes of a graph
     if (!use_graph) {
@@ -3316,12 +3370,14 @@ int moe_decode_token(moe_cache *c, const float *x, const float *bias, float *out
                                             c->timing ? c->tev.data() + (size_t)l * 12 : nullptr, stage, sc, fused,
                                             seq);
             if (r != MOE_OK) {
+                c->pub_on = false;
                 abort_joins();
                 hipStreamSynchronize(st);
                 mover_drain();
                 return r;
             }
         }
+        c->pub_on = false;
 
     } else {
         const int key = bias ? 1 : 0;        const int mode = c->split + (fused ? 10 : 0);
@@ -3359,8 +3415,11 @@ int moe_decode_token(moe_cache *c, const float *x, const float *bias, float *out
         if (serve_err != MOE_OK) abort_joins();
     }
     // the routed ids and, after them, the fused layers' late-wait word
-    HIPCHK(hipMemcpyAsync(c->h_ids, c->d_ids, (2 * (size_t)NL * c->K + 64) * 4, hipMemcpyDeviceToHost, st));
-    const hipError_t sync_err = hipStreamSynchronize(st);
+    hipError_t sync_err = hipSuccess;
+    if (!(publish && wait_published(c, NL, seq))) {
+        HIPCHK(hipMemcpyAsync(c->h_ids, c->d_ids, (2 * (size_t)NL * c->K + 64) * 4, hipMemcpyDeviceToHost, st));
+        sync_err = hipStreamSynchronize(st);
+    }
     const auto t_sync = std::chrono::steady_clock::now();
     const int drain_err = mover_drain();
     if (sync_err != hipSuccess) return fail(MOE_ERR_HIP, "decode: %s", hipGetErrorString(sync_err));

@@ -175,6 +175,7 @@ SIGNATURES = {
                                                   ctypes.POINTER(ctypes.c_int)]),
     "moe_cache_set_timing": (ctypes.c_int, [P, ctypes.c_int]),
     "moe_cache_set_decode_path": (ctypes.c_int, [P, ctypes.c_int, ctypes.c_int]),
+    "moe_cache_set_wait_bound": (ctypes.c_int, [P, ctypes.c_double]),
     "moe_cache_set_staging": (ctypes.c_int, [P, ctypes.c_int]),
     "moe_cache_set_sidecar": (ctypes.c_int, [P, ctypes.c_int, ctypes.c_int, ctypes.c_int]),
     "moe_cache_set_sidecar_batch": (ctypes.c_int, [P, ctypes.c_int, ctypes.c_int]),

@@ -242,6 +242,11 @@ class MoeCache:
         False/0 direct launches."""
         check(lib().moe_cache_set_decode_path(self.h, int(split), int(graph)), "set_decode_path")
 
+    def set_wait_bound(self, seconds):
+        """Bound of every wait inside the fused decode launch (default 0.5 s):
+        past it a workgroup gives up and the token fails (MoeError)."""
+        check(lib().moe_cache_set_wait_bound(self.h, float(seconds)), "set_wait_bound")
+
     def set_timing(self, on=True):
         check(lib().moe_cache_set_timing(self.h, int(on)), "set_timing")
 

@@ -13,7 +13,7 @@ import numpy as np
 import pytest
 import torch
 
-from gpu_rig import L, Rig
+from gpu_rig import L, Rig, stream
 from moe_prefetch import ExpertCache, _lib
 from oracle import oracle as O
 
@@ -87,6 +87,42 @@ def test_decode_4_layers_window_admission(tmp_path, split, graph):
         worst = check_run(rig, tmp_path)
         print("worst rel-L2", worst)
     finally:
+        rig.close()
+
+
+@pytest.mark.parametrize("graph", [0, 2], ids=["direct", "graph"])
+def test_fused_wait_bound_reports_and_recovers(graph):
+    """The fused launch's bounded waits, forced from the host: with the bound
+    at 0.1 us the workgroups that wait give up and exit (every kernel ends
+    normally), and the token fails with MOE_ERR_HIP naming the wait -- launched
+    directly (the published late word, or no done word and the bounded spin's
+    fallback to the copy back and synchronisation) and as a graph.  The failed
+    token observed and stepped nothing; with the bound restored the next tokens
+    decode as the oracle's (ids and outputs bit for bit)."""
+    rig = Rig([16, 24], [Q4, Q6], T=4, admit="window", batch_tables=True)
+    rig.cache.set_decode_path(split=0, graph=graph)
+    oc = rig.oracle_cache()
+    out = torch.empty((rig.nl, rig.x.shape[-1]), dtype=torch.float32, device=rig.dev)
+    bias = lambda t: None if rig.bias is None else rig.bias[t]
+    try:
+        rig.cache.set_wait_bound(1e-7)
+        with pytest.raises(_lib.MoeError, match="gave up waiting"):
+            rig.cache.decode_token(rig.x[0], out, bias=bias(0), stream=stream())
+        rig.cache.set_wait_bound(0.5)
+        for t in (1, 2, 3):
+            ids = rig.cache.decode_token(rig.x[t], out, bias=bias(t), stream=stream())
+            torch.cuda.synchronize()
+            got = out.cpu().numpy()
+            for l in range(rig.nl):
+                tbl, _ = oc.table(l)
+                b = None if rig.bh is None else rig.bh[t, l]
+                rids, rw, _, _ = O.route(rig.Wh[l], rig.xh[t, l], 8, bias=b, table=tbl)
+                assert np.array_equal(ids[l], rids), (t, l, ids[l], rids)
+                assert np.array_equal(got[l], rig.oracle_layer(t, l, rids, rw)), (t, l)
+                oc.observe(l, rids)
+            oc.step()
+    finally:
+        oc.close()
         rig.close()
 
 

@@ -163,6 +163,12 @@ def test_decode_path_arguments():
     for split, graph in ((0, 3), (0, -1), (4, 1), (-1, 0)):
         with pytest.raises(_lib.MoeError, match="must be"):
             c.set_decode_path(split=split, graph=graph)
+    # the fused launch's wait bound: (0, 60] seconds
+    for sec in (1e-7, 0.5, 60.0):
+        c.set_wait_bound(sec)
+    for sec in (0.0, -1.0, 61.0, float("nan")):
+        with pytest.raises(_lib.MoeError, match="must be in"):
+            c.set_wait_bound(sec)
     c.close()
 
 
