@@ -572,9 +572,10 @@ int moe_decode_layer(moe_cache *c, int layer, const float *x, const float *bias,
  * The call returns with out complete in device memory.  When the layers are
  * launched directly without CPU-assisted serving or streaming (at most 8
  * layers, graph mode 0 or 1, no timing), the fused launches publish the ids
- * into mapped memory and the call returns on their done word, without
- * synchronising the stream: the last launch may still be retiring, and work
- * enqueued later on the stream orders after it as usual. */
+ * into mapped memory as tagged words and the call returns once all of them
+ * carry the token's number, without synchronising the stream: the last launch
+ * may still be retiring, and work enqueued later on the stream orders after it
+ * as usual. */
 int moe_decode_token(moe_cache *c, const float *x, const float *bias, float *out, int32_t *ids_host,
                      void *stream);
 

@@ -206,12 +206,13 @@ struct FusedArgs {
     uint64_t *yx;             // [K + 1][H] tagged down rows
     uint32_t *err;            // a bounded wait ran out: the token's sequence number is written here
     uint64_t wait_ticks;      // bound of every wait, 100 MHz wall clock
-    // Publishing to the host (or pub null): the device view of the host's mapped
-    // copy of the ids buffer -- ids [L][K], the late word, the done word, padding,
-    // slots [L][K] from word L*K + 64.  The layer's last combine workgroup writes
-    // the layer's ids and slots there, and with pub_done the late word and then the
-    // token's sequence number in the done word: the token's outputs are complete.
-    uint32_t *pub;
+    // Publishing to the host (or pub null): tagged words in mapped host memory,
+    // [l * K + k] = (seq << 32) | (slot & 0xffff) << 16 | id of layer l's routed
+    // expert k, [L * K] = (seq << 32) | the late word.  The layer's last combine
+    // workgroup writes the layer's words after every combine workgroup has
+    // written its output rows (through to memory), and with pub_done the late
+    // word: when every word carries the token's number its outputs are complete.
+    uint64_t *pub;
     uint64_t *pub_ctr;        // (seq << 32) | the layer's combine workgroups finished
     int pub_layer, pub_L;
     int pub_done;

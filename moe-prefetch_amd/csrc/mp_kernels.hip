@@ -1339,12 +1339,12 @@ __device__ void fused_combine_row(const FusedArgs &a, int row, uint32_t seq, con
     else x.out[row] = acc;
 }
 
-// The layer's last combine workgroup publishes the routed ids and slots (from
-// the routing record) into the host's mapped ids buffer; in the token's last
-// layer it then writes the late word and the sequence number in the done
-// word, release at system scope: the host reads the token's results without a
-// copy back or a stream synchronisation.  The slots keep the record's 16 bits
-// (a table word below 2^16: a slot, or the slot count for an absent expert).
+// The layer's last combine workgroup publishes the routed experts (the routing
+// record's words, (seq << 32) | slot << 16 | id) as tagged words in mapped host
+// memory, and in the token's last layer the late word, tagged too: each word
+// carries the token's number, so the host needs no ordering between them and
+// no fence is spent here.  The slots keep the record's 16 bits (a table word
+// below 2^16: a slot, or the slot count for an absent expert).
 __device__ void fused_publish(const FusedArgs &a, uint32_t seq, const uint64_t *s_rec) {
     __syncthreads();                        // this workgroup's output rows are written
     if (threadIdx.x != 0) return;
@@ -1355,21 +1355,14 @@ __device__ void fused_publish(const FusedArgs &a, uint32_t seq, const uint64_t *
     } while (!__hip_atomic_compare_exchange_strong(a.pub_ctr, &old, nv, __ATOMIC_ACQ_REL, __ATOMIC_RELAXED,
                                                    __HIP_MEMORY_SCOPE_AGENT));
     if ((uint32_t)nv != (uint32_t)n_comb) return;
-    const int K = a.x.K, L = a.pub_L, l = a.pub_layer;
-    for (int k = 0; k < K; ++k) {
-        const uint64_t t = s_rec[k];
-        __hip_atomic_store(a.pub + (size_t)l * K + k, (uint32_t)(t & 0xffffu), __ATOMIC_RELAXED,
+    const int K = a.x.K;
+    for (int k = 0; k < K; ++k)
+        __hip_atomic_store(a.pub + (size_t)a.pub_layer * K + k, s_rec[k], __ATOMIC_RELAXED,
                            __HIP_MEMORY_SCOPE_SYSTEM);
-        __hip_atomic_store(a.pub + (size_t)L * K + 64 + (size_t)l * K + k, (uint32_t)((t >> 16) & 0xffffu),
-                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-    }
-    // performed before this workgroup goes on, so a later layer's done word
-    // (another workgroup, maybe another XCD) cannot reach the host first
-    __threadfence_system();
     if (a.pub_done) {
         const uint32_t late = __hip_atomic_load(a.err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        __hip_atomic_store(a.pub + (size_t)L * K, late, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-        __hip_atomic_store(a.pub + (size_t)L * K + 1, seq, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
+        __hip_atomic_store(a.pub + (size_t)a.pub_L * K, ((uint64_t)seq << 32) | late, __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_SYSTEM);
     }
 }
 

@@ -192,7 +192,7 @@ struct moe_cache {
     void *route_ws = nullptr, *exp_ws = nullptr;
     float *ypart = nullptr;            // [K + 1][H]: per-expert down rows between the two launches of a split
     int32_t *d_ids = nullptr, *d_slots = nullptr, *h_ids = nullptr;
-    uint32_t *h_ids_d = nullptr;        // h_ids (mapped, coherent) as the device sees it
+    uint64_t *h_pub = nullptr, *h_pub_d = nullptr;  // [L * K + 1] tagged words the fused launches publish
     uint64_t *d_pub_ctr = nullptr;      // [L]: the fused combine's count of finished workgroups
     bool pub_on = false;                // this token's fused launches publish ids and completion
     float *d_w = nullptr;
@@ -1389,6 +1389,7 @@ void free_cache(moe_cache *c) {
     if (c->h_tbl) hipHostFree(c->h_tbl);
     if (c->h_prior) hipHostFree(c->h_prior);
     if (c->h_ids) hipHostFree(c->h_ids);
+    if (c->h_pub) hipHostFree(c->h_pub);
     if (c->route) fclose(c->route);
     if (c->map) fclose(c->map);
     if (c->replay) fclose(c->replay);
@@ -1740,16 +1741,18 @@ int moe_cache_create(const moe_cache_config *cfg, moe_cache **out) {
         hipMalloc(&c->d_ids, (2 * (size_t)NL * c->K + 64) * 4) != hipSuccess ||
         hipMalloc(&c->d_w, (size_t)NL * c->K * 4) != hipSuccess ||
         hipMalloc(&c->d_q8x, (size_t)(c->H / 256) * mp::Q8K_BYTES + 256) != hipSuccess ||
-        hipHostMalloc(&c->h_ids, (2 * (size_t)NL * c->K + 64) * 4, hipHostMallocMapped | hipHostMallocCoherent) !=
+        hipHostMalloc(&c->h_ids, (2 * (size_t)NL * c->K + 64) * 4, 0) != hipSuccess ||
+        hipHostMalloc((void **)&c->h_pub, ((size_t)NL * c->K + 1) * 8, hipHostMallocMapped | hipHostMallocCoherent) !=
             hipSuccess ||
-        hipHostGetDevicePointer((void **)&c->h_ids_d, c->h_ids, 0) != hipSuccess ||
+        hipHostGetDevicePointer((void **)&c->h_pub_d, c->h_pub, 0) != hipSuccess ||
         hipMalloc(&c->d_pub_ctr, (size_t)NL * 8) != hipSuccess ||
         hipMalloc(&c->fx, (size_t)NL * mp::fused_words(c->K, c->I, c->H) * 8) != hipSuccess ||
         hipHostMalloc((void **)&c->h_seq, 64, hipHostMallocDefault) != hipSuccess ||
         hipMalloc(&c->d_seq, 64) != hipSuccess)
         return bail(fail(MOE_ERR_NOMEM, "decode scratch"));
-    // ids [L][K], the late-wait word, the done word and padding, then slots [L][K]:
-    // one copy back per token, or published into h_ids by the fused launches
+    // ids [L][K], the late-wait word and padding, then slots [L][K]: one copy back
+    // per token, or unpacked from the words the fused launches publish (h_pub)
+    memset(c->h_pub, 0, ((size_t)NL * c->K + 1) * 8);
     c->d_slots = c->d_ids + (size_t)NL * c->K + 64;
     c->h_slots = c->h_ids + (size_t)NL * c->K + 64;
     // tag 0 is never a token's sequence number: zeroed exchange words are stale
@@ -2958,7 +2961,7 @@ static int decode_layer_impl(moe_cache *c, int layer, const float *x, const floa
         f.err = (uint32_t *)(c->d_ids + c->L.size() * (size_t)c->K);
         f.wait_ticks = (uint64_t)(c->fused_wait_s * 1e8);
         if (c->pub_on && !sidecar) {
-            f.pub = c->h_ids_d;
+            f.pub = c->h_pub_d;
             f.pub_ctr = c->d_pub_ctr + layer;
             f.pub_layer = layer;
             f.pub_L = (int)c->L.size();
@@ -3256,20 +3259,30 @@ int moe_decode_layer(moe_cache *c, int layer, const float *x, const float *bias,
 // tokens of at most this many layers launch directly in graph mode (see below)
 constexpr int DIRECT_MAX_LAYERS = 8;
 
-// the fused launches' done word in h_ids carries this token's number: bounded
-// spin (a legitimate token takes microseconds; past the bound the caller
-// copies back and synchronises, which also reports a failed launch)
+// every word the fused launches publish (h_pub) carries this token's number:
+// bounded spin (a legitimate token takes microseconds; past the bound the
+// caller copies back and synchronises, which also reports a failed launch),
+// then the ids, slots and late word go where the copy back would put them
 static bool wait_published(moe_cache *c, int NL, uint32_t seq) {
-    const uint32_t *done = (const uint32_t *)(c->h_ids + (size_t)NL * c->K + 1);
+    const size_t n = (size_t)NL * c->K + 1;
     const auto t0 = std::chrono::steady_clock::now();
     const auto bound = std::chrono::duration<double>(4 * c->fused_wait_s + 0.5);
-    for (uint64_t i = 0;; ++i) {
-        if (__atomic_load_n(done, __ATOMIC_ACQUIRE) == seq) return true;
-        if ((i & 255) == 0 && std::chrono::steady_clock::now() - t0 > bound) return false;
+    size_t i = 0;                       // words before i carry seq
+    for (uint64_t spin = 0; i < n; ++spin) {
+        while (i < n && (uint32_t)(__atomic_load_n(c->h_pub + i, __ATOMIC_ACQUIRE) >> 32) == seq) ++i;
+        if (i == n) break;
+        if ((spin & 255) == 0 && std::chrono::steady_clock::now() - t0 > bound) return false;
 #if defined(__x86_64__)
         __builtin_ia32_pause();
 #endif
     }
+    for (size_t j = 0; j + 1 < n; ++j) {
+        const uint64_t w = c->h_pub[j];
+        c->h_ids[j] = (int32_t)(w & 0xffffu);
+        c->h_slots[j] = (int32_t)((w >> 16) & 0xffffu);
+    }
+    c->h_ids[n - 1] = (int32_t)(uint32_t)c->h_pub[n - 1];     // the late word
+    return true;
 }
 
 int moe_decode_token(moe_cache *c, const float *x, const float *bias, float *out, int32_t *ids_host, void *stream) {
