@@ -215,6 +215,11 @@ struct moe_cache {
     bool stage_valid = false, stg_pending = false;
     hipStream_t stg_stream = nullptr;
     hipEvent_t ev_stg = nullptr;
+    // a token that returned on its published words without synchronising: its
+    // launches may still be retiring (their staging writes not yet written back),
+    // so the step's first staged copy orders stg_stream behind them (ev_dec)
+    hipStream_t dec_open = nullptr;
+    hipEvent_t ev_dec = nullptr;
     uint64_t n_staged = 0;
     // CPU-assisted serving of absent experts (off while sc_den == 0): the
     // decode kernels post each layer's ids and Q8_K(x) to sc_post; the host
@@ -431,6 +436,11 @@ int start_upload(moe_cache *c, int li, int expert, int slot, bool spec = false) 
         HIPCHK(hipEventRecord(j.t0, s));
     }
     if (staged) {
+        if (c->dec_open) {
+            HIPCHK(hipEventRecord(c->ev_dec, c->dec_open));
+            HIPCHK(hipStreamWaitEvent(c->stg_stream, c->ev_dec, 0));
+            c->dec_open = nullptr;
+        }
         HIPCHK(hipMemcpyAsync(dst, staged, ls.expert_bytes, hipMemcpyDeviceToDevice, s));
         c->stg_pending = true;
         c->n_staged++;
@@ -1365,6 +1375,7 @@ void free_cache(moe_cache *c) {
         if (p) hipHostFree(p);
     hipFree(c->d_seq);
     if (c->ev_stg) hipEventDestroy(c->ev_stg);
+    if (c->ev_dec) hipEventDestroy(c->ev_dec);
     hipFree(c->stage);
     if (c->tbl_stream) hipStreamDestroy(c->tbl_stream);
     hipFree(c->pool_base);
@@ -1768,6 +1779,7 @@ int moe_cache_create(const moe_cache_config *cfg, moe_cache **out) {
         hipEventCreateWithFlags(&c->up_mark, hipEventDisableTiming) != hipSuccess ||
         hipStreamCreateWithFlags(&c->stg_stream, hipStreamNonBlocking) != hipSuccess ||
         hipEventCreateWithFlags(&c->ev_stg, hipEventDisableTiming) != hipSuccess ||
+        hipEventCreateWithFlags(&c->ev_dec, hipEventDisableTiming) != hipSuccess ||
         hipEventCreateWithFlags(&c->ev_route, hipEventDisableTiming) != hipSuccess ||
         hipEventCreateWithFlags(&c->ev_hbm, hipEventDisableTiming) != hipSuccess ||
         hipEventCreateWithFlags(&c->ev_host, hipEventDisableTiming) != hipSuccess ||
@@ -3429,7 +3441,15 @@ int moe_decode_token(moe_cache *c, const float *x, const float *bias, float *out
     }
     // the routed ids and, after them, the fused layers' late-wait word
     hipError_t sync_err = hipSuccess;
-    if (!(publish && wait_published(c, NL, seq))) {
+    // (the token's staged copies, issued by observe or the step below, are the
+    // only readers of what the launches wrote that run on another stream)
+    struct DecClose {
+        moe_cache *c;
+        ~DecClose() { c->dec_open = nullptr; }
+    } dec_close{c};
+    if (publish && wait_published(c, NL, seq)) {
+        c->dec_open = st;
+    } else {
         HIPCHK(hipMemcpyAsync(c->h_ids, c->d_ids, (2 * (size_t)NL * c->K + 64) * 4, hipMemcpyDeviceToHost, st));
         sync_err = hipStreamSynchronize(st);
     }
