@@ -112,10 +112,12 @@ __global__ __launch_bounds__(1024) void dispatch_kernel(const int32_t *ids, int 
     __syncthreads();
     const int nwaves = blockDim.x >> 6;
     for (int base = 0; base < P; base += DSP_CHUNKS * 64) {
-        for (int i = tid; i < DSP_CHUNKS * E; i += blockDim.x) s_c[i / E][i % E] = 0;
+        const int nc = min(DSP_CHUNKS, (P - base + 63) / 64);      // chunks holding pairs
+        for (int i = tid; i < nc * E; i += blockDim.x) s_c[i / E][i % E] = 0;
         __syncthreads();
         int my_e[DSP_CHUNKS / 16], my_r[DSP_CHUNKS / 16];
         for (int j = 0, c = wave; c < DSP_CHUNKS; ++j, c += nwaves) {
+            if (c >= nc) break;
             const int i = base + 64 * c + lane;
             const int e = i < P ? ids[i] : -1;
             const bool valid = e >= 0 && e < E;
@@ -134,7 +136,8 @@ __global__ __launch_bounds__(1024) void dispatch_kernel(const int32_t *ids, int 
         __syncthreads();
         for (int e = tid; e < E; e += blockDim.x) {
             int run = s_run[e];
-            for (int c = 0; c < DSP_CHUNKS; ++c) {
+#pragma unroll 16
+            for (int c = 0; c < nc; ++c) {
                 const int v = s_c[c][e];
                 s_c[c][e] = (uint16_t)run;
                 run += v;
@@ -143,6 +146,7 @@ __global__ __launch_bounds__(1024) void dispatch_kernel(const int32_t *ids, int 
         }
         __syncthreads();
         for (int j = 0, c = wave; c < DSP_CHUNKS; ++j, c += nwaves) {
+            if (c >= nc) break;
             const int e = my_e[j];
             if (e >= 0) perm[s_off[e] + s_c[c][e] + my_r[j]] = base + 64 * c + lane;
         }
