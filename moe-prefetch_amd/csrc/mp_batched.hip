@@ -302,15 +302,14 @@ __device__ inline void q4_scales(const uint4 &hdr, int h, Q4Scales &o) {
 // One 256-value block of the activation rows of a pass's pairs, in LDS.  The
 // 16-byte chunk c of row r sits at position c ^ (r & 15), so the 16 rows one
 // fragment read touches fall in distinct banks.
-constexpr int GT = 32;   // pairs per pass (2 M tiles of 16)
 
-// R activation rows (32, or 16 for one M tile) and the group sums of up to 32
+// R activation rows (32 for two M tiles of 16 pairs, 16 for one) and the group
+// sums of up to 32
 template <int R>
 struct __attribute__((aligned(16))) AStageR {
     _Float16 a[R][QK];
     _Float16 bs[32][16];
 };
-using AStage = AStageR<GT>;
 
 // Direct global -> LDS loads: lane l of an instruction writes base + 16*l.
 // rows[r]: activation row of pair r of the pass (r < np); rows are K values
