@@ -126,6 +126,47 @@ def test_fused_wait_bound_reports_and_recovers(graph):
         rig.close()
 
 
+def test_layer_op_wait_bound_reports_and_recovers():
+    """The per-layer op with the fused launch's waits forced to give up (the
+    bound at 0.1 us, set from the host; every kernel exits normally): the step
+    after the token's layers reports MOE_ERR_HIP naming the wait.  With the bound
+    restored the next tokens decode layer by layer with ids and outputs equal
+    to the oracle's (no cache prior, so the routing does not depend on what
+    the failed token observed)."""
+    rig = Rig([16, 24], [Q4, Q6], T=3, admit="window", batch_tables=True)
+    c = rig.cache
+    c.set_decode_path(split=0, graph=0)
+    ids_dev = torch.empty((rig.nl, 8), dtype=torch.int32, device=rig.dev)
+    outs = torch.empty((rig.nl, rig.x.shape[-1]), dtype=torch.float32, device=rig.dev)
+
+    def token(t):
+        for l in range(rig.nl):
+            c.decode_layer(l, rig.x[t, l], outs[l], bias=None if rig.bias is None else rig.bias[t, l],
+                           ids=ids_dev[l], stream=stream())
+        ids = ids_dev.cpu().numpy()
+        for l in range(rig.nl):
+            c.observe(l, ids[l])
+        c.step()
+        return ids
+
+    try:
+        c.set_wait_bound(1e-7)
+        with pytest.raises(_lib.MoeError, match="gave up waiting"):
+            token(0)
+        c.set_wait_bound(0.5)
+        for t in (1, 2):
+            ids = token(t)
+            torch.cuda.synchronize()
+            got = outs.cpu().numpy()
+            for l in range(rig.nl):
+                b = None if rig.bh is None else rig.bh[t, l]
+                rids, rw, _, _ = O.route(rig.Wh[l], rig.xh[t, l], 8, bias=b)
+                assert np.array_equal(ids[l], rids), (t, l, ids[l], rids)
+                assert np.array_equal(got[l], rig.oracle_layer(t, l, rids, rw)), (t, l)
+    finally:
+        rig.close()
+
+
 @pytest.mark.parametrize("E,I,graph", [(64, 256, 2), (192, 512, 0)], ids=["e64_i256_graph", "e192_i512_eager"])
 def test_decode_fused_chunk_counts(tmp_path, E, I, graph):
     # the fused layer routes in registers per 64-expert chunk (1 to 4 chunks:
