@@ -49,7 +49,6 @@ namespace mp {
 typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
 typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
 typedef float float4_t __attribute__((ext_vector_type(4)));
-typedef __attribute__((address_space(1))) void gptr_t;
 typedef __attribute__((address_space(3))) void lptr_t;
 
 // ---------------------------------------------------------------------------
@@ -311,33 +310,67 @@ struct __attribute__((aligned(16))) AStageR {
     _Float16 bs[32][16];
 };
 
-// Direct global -> LDS loads: lane l of an instruction writes base + 16*l.
-// rows[r]: activation row of pair r of the pass (r < np); rows are K values
-// long.  Wave w stages rows (R/4)w .. (R/4)w + R/4 - 1 (two per instruction),
-// wave 0 also the group sums.  Rows past np are not loaded.
-template <int R, bool SUMS = true>
-__device__ inline void stage_a(AStageR<R> &st, const int *rows, int np, const uint16_t *xa, const uint16_t *xbs,
-                               int K, int s, int wave, int lane) {
-#pragma unroll
-    for (int j = 0; j < R / 8; ++j) {
-        const int r0 = (R / 4) * wave + 2 * j;
-        if (r0 >= np) break;
-        const int r = min(r0 + (lane >> 5), np - 1);
-        const int c = (lane & 31) ^ ((r0 + (lane >> 5)) & 15);
-        const uint16_t *src = xa + (size_t)rows[r] * K + (size_t)s * QK + 8 * c;
-        __builtin_amdgcn_global_load_lds((gptr_t *)src, (lptr_t *)&st.a[r0][0], 16, 0, 0);
-    }
-    if (SUMS && wave == 0) {
-        const int r = min(lane >> 1, np - 1);
-        const uint16_t *src = xbs + (size_t)rows[r] * (K / 16) + (size_t)s * 16 + 8 * (lane & 1);
-        __builtin_amdgcn_global_load_lds((gptr_t *)src, (lptr_t *)&st.bs[0][0], 16, 0, 0);
-    }
-}
-
 template <int R>
 __device__ inline half8_t stage_frag(const AStageR<R> &st, int r, int off) {
     const int c = (off >> 3) ^ (r & 15);
     return *(const half8_t *)&st.a[r][8 * c];
+}
+
+// Staging by direct buffer -> LDS loads: lane l of an instruction writes
+// base + 16*l.  rows[r]: activation row of pair r of the pass (r < np); rows
+// are K values long.  Wave w stages rows (R/4)w .. (R/4)w + R/4 - 1 (two per
+// instruction), wave 0 also the group sums; rows past np are not loaded.  The
+// activation codes and the group sums are raw buffers, the lane's byte offsets
+// are computed once per pass of a chunk and block s's offset s*QK*2 is a
+// scalar: a step's staging costs no per-lane address arithmetic (up/gate at
+// 512 tokens 104.0 -> 97.8 us a launch against 64-bit pointers per load).
+constexpr int BUF_WORD3 = 0x00020000;    // raw buffer, 32-bit elements (gfx9)
+typedef int i32x4_t __attribute__((ext_vector_type(4)));
+__device__ void buffer_load_lds(i32x4_t rsrc, lptr_t *lds, int size, int voffset, int soffset, int offset,
+                                int aux) __asm("llvm.amdgcn.raw.buffer.load.lds");
+__device__ i32x4_t buffer_load_v4(i32x4_t rsrc, int voffset, int soffset, int aux) __asm("llvm.amdgcn.raw.buffer.load.v4i32");
+// a buffer resource over [p, p + bytes): base address, no stride, the size, raw
+// (the words are the same in every lane: scalar registers)
+__device__ inline i32x4_t raw_buffer(const void *p, uint32_t bytes) {
+    const uint64_t a = (uint64_t)p;
+    i32x4_t r;
+    r.x = __builtin_amdgcn_readfirstlane((int)(uint32_t)a);
+    r.y = __builtin_amdgcn_readfirstlane((int)((uint32_t)(a >> 32) & 0xffffu));
+    r.z = __builtin_amdgcn_readfirstlane((int)bytes);
+    r.w = BUF_WORD3;
+    return r;
+}
+template <int R>
+struct StageOff {
+    int a[R / 8];       // instruction j: the lane's row and swizzled chunk, bytes
+    int bs;             // the lane's group-sum chunk (wave 0), bytes
+};
+template <int R>
+__device__ inline void stage_offsets(StageOff<R> &o, const int *rows, int np, int K, int wave, int lane) {
+#pragma unroll
+    for (int j = 0; j < R / 8; ++j) {
+        const int r0 = (R / 4) * wave + 2 * j;
+        const int r = min(r0 + (lane >> 5), np - 1);
+        const int c = (lane & 31) ^ ((r0 + (lane >> 5)) & 15);
+        o.a[j] = 2 * (rows[max(r, 0)] * K + 8 * c);
+    }
+    const int r = min(lane >> 1, np - 1);
+    o.bs = 2 * (rows[max(r, 0)] * (K / 16) + 8 * (lane & 1));
+}
+template <int R, bool SUMS = true>
+__device__ inline void stage_a_buf(AStageR<R> &st, const StageOff<R> &o, int np, i32x4_t ra, i32x4_t rbs, int s,
+                                   int wave) {
+#pragma unroll
+    for (int j = 0; j < R / 8; ++j) {
+        const int r0 = (R / 4) * wave + 2 * j;
+        if (r0 >= np) break;
+        buffer_load_lds(ra, (lptr_t *)&st.a[r0][0], 16, o.a[j], s * QK * 2, 0, 0);
+    }
+    if (SUMS && wave == 0) buffer_load_lds(rbs, (lptr_t *)&st.bs[0][0], 16, o.bs, s * 32, 0, 0);
+}
+__device__ inline uint4 buf_load16(i32x4_t r, int voff, int soff) {
+    const i32x4_t v = buffer_load_v4(r, voff, soff, 0);
+    return make_uint4((uint32_t)v.x, (uint32_t)v.y, (uint32_t)v.z, (uint32_t)v.w);
 }
 
 // Workgroup -> (row tile, expert).  Workgroups go to the 8 XCDs round-robin
@@ -439,6 +472,7 @@ __global__ __launch_bounds__(256, CH == 1 ? 4 : 3) void grouped_q6_kernel(Groupe
         return;
     }
     const uint8_t *wrow = base + 2ull * a.I * (a.H / QK) * Q4K_BYTES + (size_t)row * (NB * Q6K_BYTES);
+    const i32x4_t ra = raw_buffer(a.ha, 0xffffffffu);         // Q8_K codes of h: staged by buffer loads
 
     __shared__ AStageR<GK> st[2];
     __shared__ int s_rows[CH * GK];
@@ -451,7 +485,11 @@ __global__ __launch_bounds__(256, CH == 1 ? 4 : 3) void grouped_q6_kernel(Groupe
         __syncthreads();
         for (int i = tid; i < CH * GK * NB; i += 256)
             s_dx[i % NB][i / NB] = a.hdx[(size_t)s_rows[i / NB] * NB + (i % NB)];
-        stage_a<GK, false>(st[0], s_rows, min(GK, npc), a.ha, a.hbs, K, 0, wave, lane);
+        StageOff<GK> so[CH];
+#pragma unroll
+        for (int p = 0; p < CH; ++p)
+            if (p < nps) stage_offsets(so[p], s_rows + p * GK, min(GK, npc - p * GK), K, wave, lane);
+        stage_a_buf<GK, false>(st[0], so[0], min(GK, npc), ra, ra, 0, wave);
         Q6Lane cw, nw;
         q6_lane_load(cw, wrow, h);
         __builtin_amdgcn_s_waitcnt(0);
@@ -475,8 +513,12 @@ __global__ __launch_bounds__(256, CH == 1 ? 4 : 3) void grouped_q6_kernel(Groupe
                     const int jn = j + 1;
                     if (jn < NB * nps) {
                         const int s2 = jn / nps, p2 = jn - s2 * nps;
-                        stage_a<GK, false>(st[jn & 1], s_rows + p2 * GK, min(GK, npc - p2 * GK), a.ha, a.hbs, K, s2,
-                                           wave, lane);
+                        StageOff<GK> sp = so[0];
+                        if constexpr (CH > 1) {
+#pragma unroll
+                            for (int q = 0; q < GK / 8; ++q) sp.a[q] = p2 ? so[1].a[q] : so[0].a[q];
+                        }
+                        stage_a_buf<GK, false>(st[jn & 1], sp, min(GK, npc - p2 * GK), ra, ra, s2, wave);
                     }
                     float4_t acc[MT], accl[MT];
 #pragma unroll
@@ -670,8 +712,12 @@ __global__ __launch_bounds__(256, CH == 1 ? 4 : 3) void grouped_q4_kernel(Groupe
     __shared__ AStageR<GK> st[2];
     __shared__ int s_rows[CH * GK];
     __shared__ __attribute__((aligned(16))) float s_dx[NB][CH * GK];   // [block][pair]: a lane's 4 rows in one read
-    const uint8_t *wrow = mat + (size_t)row * ROWB;
     const int gm = (h >> 1) + 2 * (h & 1);
+    // the expert's matrix, the activation codes and their group sums as raw
+    // buffers; the lane's weight offsets (header, the two qs loads) fixed
+    const i32x4_t rw = raw_buffer(mat, (uint32_t)((DOWN ? a.H : 2 * a.I) * ROWB));
+    const i32x4_t ra = raw_buffer(act, 0xffffffffu), rbs = raw_buffer(abs16, 0xffffffffu);
+    const int wo0 = row * ROWB, wo1 = wo0 + 16 + 16 * h, wo2 = wo0 + 80 + 16 * h;
 
     for (int cb = 0; cb < ne; cb += CH * GK) {
         const int npc = min(CH * GK, ne - cb);
@@ -682,11 +728,15 @@ __global__ __launch_bounds__(256, CH == 1 ? 4 : 3) void grouped_q4_kernel(Groupe
         }
         __syncthreads();
         for (int i = tid; i < CH * GK * NB; i += 256) s_dx[i % NB][i / NB] = adx[(size_t)s_rows[i / NB] * NB + (i % NB)];
-        stage_a(st[0], s_rows, min(GK, npc), act, abs16, K, 0, wave, lane);
+        StageOff<GK> so[CH];
+#pragma unroll
+        for (int p = 0; p < CH; ++p)
+            if (p < nps) stage_offsets(so[p], s_rows + p * GK, min(GK, npc - p * GK), K, wave, lane);
+        stage_a_buf(st[0], so[0], min(GK, npc), ra, rbs, 0, wave);
         uint4 cw[3], nw[3];
-        cw[0] = *(const uint4 *)wrow;
-        cw[1] = *(const uint4 *)(wrow + 16 + 16 * h);
-        cw[2] = *(const uint4 *)(wrow + 80 + 16 * h);
+        cw[0] = buf_load16(rw, wo0, 0);
+        cw[1] = buf_load16(rw, wo1, 0);
+        cw[2] = buf_load16(rw, wo2, 0);
         __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
         float y[CH][MT][4];
@@ -700,10 +750,9 @@ __global__ __launch_bounds__(256, CH == 1 ? 4 : 3) void grouped_q4_kernel(Groupe
 #pragma unroll 1
         for (int s = 0; s < NB; ++s) {
             if (s + 1 < NB) {
-                const uint8_t *q = wrow + (s + 1) * Q4K_BYTES;
-                nw[0] = *(const uint4 *)q;
-                nw[1] = *(const uint4 *)(q + 16 + 16 * h);
-                nw[2] = *(const uint4 *)(q + 80 + 16 * h);
+                nw[0] = buf_load16(rw, wo0, (s + 1) * Q4K_BYTES);
+                nw[1] = buf_load16(rw, wo1, (s + 1) * Q4K_BYTES);
+                nw[2] = buf_load16(rw, wo2, (s + 1) * Q4K_BYTES);
             }
             Q4Scales sc;
             q4_scales(cw[0], h, sc);
@@ -722,7 +771,14 @@ __global__ __launch_bounds__(256, CH == 1 ? 4 : 3) void grouped_q4_kernel(Groupe
                     const int jn = j + 1;
                     if (jn < NB * nps) {
                         const int s2 = jn / nps, p2 = jn - s2 * nps;
-                        stage_a(st[jn & 1], s_rows + p2 * GK, min(GK, npc - p2 * GK), act, abs16, K, s2, wave, lane);
+                        // the pass's offsets by selects (a runtime index would put so in scratch)
+                        StageOff<GK> sp = so[0];
+                        if constexpr (CH > 1) {
+#pragma unroll
+                            for (int q = 0; q < GK / 8; ++q) sp.a[q] = p2 ? so[1].a[q] : so[0].a[q];
+                            sp.bs = p2 ? so[1].bs : so[0].bs;
+                        }
+                        stage_a_buf(st[jn & 1], sp, min(GK, npc - p2 * GK), ra, rbs, s2, wave);
                     }
                     // each 128-value half of the super-block in its own accumulator:
                     // a half's products sum to at most 128 * 63 * 15 * 127 < 2^24, so
