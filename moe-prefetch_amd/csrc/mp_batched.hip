@@ -329,6 +329,9 @@ typedef int i32x4_t __attribute__((ext_vector_type(4)));
 __device__ void buffer_load_lds(i32x4_t rsrc, lptr_t *lds, int size, int voffset, int soffset, int offset,
                                 int aux) __asm("llvm.amdgcn.raw.buffer.load.lds");
 __device__ i32x4_t buffer_load_v4(i32x4_t rsrc, int voffset, int soffset, int aux) __asm("llvm.amdgcn.raw.buffer.load.v4i32");
+typedef int i32x2_t __attribute__((ext_vector_type(2)));
+__device__ i32x2_t buffer_load_v2(i32x4_t rsrc, int voffset, int soffset, int aux) __asm("llvm.amdgcn.raw.buffer.load.v2i32");
+__device__ short buffer_load_i16(i32x4_t rsrc, int voffset, int soffset, int aux) __asm("llvm.amdgcn.raw.buffer.load.i16");
 // a buffer resource over [p, p + bytes): base address, no stride, the size, raw
 // (the words are the same in every lane: scalar registers)
 __device__ inline i32x4_t raw_buffer(const void *p, uint32_t bytes) {
@@ -406,14 +409,26 @@ struct Q6Lane {
     uint32_t d;            // the block's fp16 scale in the low half
 };
 
-// a Q6_K block starts 2-byte aligned (210-byte blocks); the loads are unaligned
-__device__ inline void q6_lane_load(Q6Lane &w, const uint8_t *blk, int h) {
+// The lane's offsets into its row's blocks, and one block's pieces by buffer
+// loads at the block's offset (a scalar).  A Q6_K block starts 2-byte aligned
+// (210-byte blocks); the loads are unaligned.
+struct Q6Off {
+    int qa, qb, qh, sc, d;
+};
+__device__ inline Q6Off q6_lane_offsets(int row_off, int h) {
     const int hh = h >> 1, l0 = 16 * (h & 1);
-    __builtin_memcpy(&w.qa, __builtin_assume_aligned(blk + 64 * hh + l0, 2), 16);
-    __builtin_memcpy(&w.qb, __builtin_assume_aligned(blk + 64 * hh + 32 + l0, 2), 16);
-    __builtin_memcpy(&w.qh, __builtin_assume_aligned(blk + 128 + 32 * hh + l0, 2), 16);
-    __builtin_memcpy(&w.sc, __builtin_assume_aligned(blk + 192 + 8 * hh, 2), 8);
-    w.d = *(const uint16_t *)(blk + 208);
+    return Q6Off{row_off + 64 * hh + l0, row_off + 64 * hh + 32 + l0, row_off + 128 + 32 * hh + l0,
+                 row_off + 192 + 8 * hh, row_off + 208};
+}
+__device__ inline void q6_lane_load(Q6Lane &w, i32x4_t rw, const Q6Off &o, int blk_off) {
+    const i32x4_t a = buffer_load_v4(rw, o.qa, blk_off, 0), b = buffer_load_v4(rw, o.qb, blk_off, 0);
+    const i32x4_t q = buffer_load_v4(rw, o.qh, blk_off, 0);
+    const i32x2_t sc = buffer_load_v2(rw, o.sc, blk_off, 0);
+    w.qa = make_uint4((uint32_t)a.x, (uint32_t)a.y, (uint32_t)a.z, (uint32_t)a.w);
+    w.qb = make_uint4((uint32_t)b.x, (uint32_t)b.y, (uint32_t)b.z, (uint32_t)b.w);
+    w.qh = make_uint4((uint32_t)q.x, (uint32_t)q.y, (uint32_t)q.z, (uint32_t)q.w);
+    w.sc = make_uint2((uint32_t)sc.x, (uint32_t)sc.y);
+    w.d = (uint16_t)buffer_load_i16(rw, o.d, blk_off, 0);
 }
 
 // The B operands of MFMA i: (q - 32) * sc in two exact halves, sc = 16*sh + sl
@@ -471,8 +486,10 @@ __global__ __launch_bounds__(256, CH == 1 ? 4 : 3) void grouped_q6_kernel(Groupe
         }
         return;
     }
-    const uint8_t *wrow = base + 2ull * a.I * (a.H / QK) * Q4K_BYTES + (size_t)row * (NB * Q6K_BYTES);
-    const i32x4_t ra = raw_buffer(a.ha, 0xffffffffu);         // Q8_K codes of h: staged by buffer loads
+    // the expert's down matrix and the Q8_K codes of h as raw buffers
+    const i32x4_t rw = raw_buffer(base + 2ull * a.I * (a.H / QK) * Q4K_BYTES, (uint32_t)(a.H * NB * Q6K_BYTES));
+    const i32x4_t ra = raw_buffer(a.ha, 0xffffffffu);
+    const Q6Off wo = q6_lane_offsets(row * (NB * Q6K_BYTES), h);
 
     __shared__ AStageR<GK> st[2];
     __shared__ int s_rows[CH * GK];
@@ -491,7 +508,7 @@ __global__ __launch_bounds__(256, CH == 1 ? 4 : 3) void grouped_q6_kernel(Groupe
             if (p < nps) stage_offsets(so[p], s_rows + p * GK, min(GK, npc - p * GK), K, wave, lane);
         stage_a_buf<GK, false>(st[0], so[0], min(GK, npc), ra, ra, 0, wave);
         Q6Lane cw, nw;
-        q6_lane_load(cw, wrow, h);
+        q6_lane_load(cw, rw, wo, 0);
         __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
         float y[CH][MT][4];
@@ -504,7 +521,7 @@ __global__ __launch_bounds__(256, CH == 1 ? 4 : 3) void grouped_q6_kernel(Groupe
         int j = 0;                       // step j = s * nps + p
 #pragma unroll 1
         for (int s = 0; s < NB; ++s) {
-            if (s + 1 < NB) q6_lane_load(nw, wrow + (s + 1) * Q6K_BYTES, h);
+            if (s + 1 < NB) q6_lane_load(nw, rw, wo, (s + 1) * Q6K_BYTES);
             const float d = h2f_dev((uint16_t)cw.d);
 #pragma unroll
             for (int p = 0; p < CH; ++p) {
