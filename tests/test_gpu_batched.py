@@ -225,6 +225,7 @@ GROUPED_CASES = {
     "q6k_i512_t300_crowded": (_lib.TYPE_Q6K, 512, 300, 128, "crowd", "f32"),
     "q6k_i256_t300_e64": (_lib.TYPE_Q6K, 256, 300, 64, "uniform", "bf16"),
     "q4k_i768_t200_e32": (_lib.TYPE_Q4K, 768, 200, 32, "uniform", "bf16"),
+    "q4k_i512_t300": (_lib.TYPE_Q4K, 512, 300, 128, "uniform", "f32"),
     "q6k_i512_t200_e32": (_lib.TYPE_Q6K, 512, 200, 32, "uniform", "f32"),
     "q6k_i256_t400_e32_crowded": (_lib.TYPE_Q6K, 256, 400, 32, "crowd", "bf16"),
 }
