@@ -1267,6 +1267,19 @@ def run_prefill(args):
         "hbm": {"gateup_gbs": round(gu_gbs, 1), "down_gbs": round(dn_gbs, 1),
                 "experts_touched_per_layer": round(touched / NL, 1), "pairs_per_layer": pairs // NL},
     }
+    # HBM bytes per launch: the (read + write) / algorithmic ratio of the rocprofv3
+    # PMC runs on this chunk size (profiles/traffic.json) times this run's bytes
+    tpath = os.path.join(ROOT, "profiles", "traffic.json")
+    if os.path.exists(tpath):
+        with open(tpath) as f:
+            tr = json.load(f).get(f"{dom}_t{T}")
+        if tr:
+            ratio = (tr["hbm_read_bytes_per_launch"] + tr["hbm_write_bytes_per_launch"]) / \
+                tr["algorithmic_bytes_per_launch"]
+            result["roofline"]["traffic"] = round(ratio * d_bytes / NL)
+            result["roofline"]["traffic_source"] = (f"pmc: this run's bytes per launch x {ratio:.3f}, the "
+                                                    f"(FETCH_SIZE + WRITE_SIZE) / algorithmic ratio of the committed "
+                                                    f"rocprofv3 runs at {T} tokens ({tr['source']})")
     result["roofline"]["size_matched"] = size_matched(result["roofline"], iters=10)
     if not args.no_check:
         from oracle import oracle as O

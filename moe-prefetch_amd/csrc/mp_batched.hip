@@ -695,8 +695,9 @@ hipError_t launch_swiglu_quant(const float *y2, int P, int I, float *h_out, uint
 // pairs, (256, 4): four waves per SIMD.  MT = 1 (one 16-row M tile a pass)
 // when experts average at most 8 pairs: half the staged rows and products,
 // which would be empty anyway (batch 64 at 128 experts: up/gate 67.0 -> 63.4
-// us a launch, batch 16: 53.1 -> 51.1).  The (256, 5) bound that MT = 1
-// nearly fits spills and was no faster.
+// us a launch, batch 16: 53.1 -> 51.1).  The (256, 5) bound, which the MT = 1
+// kernels fit without spills (73-94 registers), was no faster (batch 64:
+// 10,629 -> 10,633 tok/s).
 template <int NB, bool DOWN, int CH, int MT>
 __global__ __launch_bounds__(256, CH == 1 ? 4 : 3) void grouped_q4_kernel(GroupedArgs a) {
     constexpr int GK = 16 * MT;           // pairs per pass: MT M tiles of 16
