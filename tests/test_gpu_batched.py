@@ -173,6 +173,14 @@ def routing(rng, T, K, E, kind):
     elif kind == "dups":    # ids drawn with replacement from 5 experts: repeats inside a token, uneven
         hot = rng.choice(E, size=5, replace=False)
         ids = np.stack([rng.choice(hot, size=K, replace=True) for _ in range(T)])
+    elif kind == "edges":   # exact counts at the edges of the two-pass chunks' M tiles: 48 pairs (a
+        # second pass of 16, its second tile empty), 49 (17), 33, 64, 65 (a second chunk of 1), 32, 17
+        # and 16; the other experts share the rest (ids repeat inside tokens)
+        fixed = [48, 49, 33, 64, 65, 32, 17, 16]
+        flat = np.concatenate([np.full(c, e) for e, c in enumerate(fixed)] +
+                              [rng.choice(np.arange(len(fixed), E), size=T * K - sum(fixed))])
+        ids = rng.permutation(flat).reshape(T, K)
+        assert [int((ids == e).sum()) for e in range(len(fixed))] == fixed
     else:   # crowd: most tokens share a handful of experts (several passes of 64 pairs)
         hot = rng.choice(E, size=K + 2, replace=False)
         ids = np.stack([rng.choice(hot, size=K, replace=False) if rng.random() < 0.8 else
@@ -226,6 +234,8 @@ GROUPED_CASES = {
     "q6k_i256_t300_e64": (_lib.TYPE_Q6K, 256, 300, 64, "uniform", "bf16"),
     "q4k_i768_t200_e32": (_lib.TYPE_Q4K, 768, 200, 32, "uniform", "bf16"),
     "q4k_i512_t300": (_lib.TYPE_Q4K, 512, 300, 128, "uniform", "f32"),
+    "q4k_i768_t300_tile_edges": (_lib.TYPE_Q4K, 768, 300, 128, "edges", "bf16"),
+    "q6k_i512_t300_tile_edges": (_lib.TYPE_Q6K, 512, 300, 128, "edges", "f32"),
     "q6k_i512_t200_e32": (_lib.TYPE_Q6K, 512, 200, 32, "uniform", "f32"),
     "q6k_i256_t400_e32_crowded": (_lib.TYPE_Q6K, 256, 400, 32, "crowd", "bf16"),
 }
